@@ -1,0 +1,109 @@
+/* nemoasr-mi355x kernel-level C ABI: the launchers of the streaming hot path.
+ *
+ * Every pointer argument is a device address (from gpu_buf_dptr); sizes are element counts.
+ * Launches are ordered on the library's one stream and must sit between gpu_begin / gpu_end
+ * (or inside a capture).  Return 0, or -1 with the message in gpu_last_error().
+ *
+ * These replace the reference's launchers and dispatch sites:
+ *   nk_gemm             k_gemm                       src/model.c:148-177 (policy + dispatch)
+ *   nk_layernorm        k_layernorm                  src/model.c:184-189
+ *   nk_layernorm2       k_layernorm2                 src/model.c:178-183
+ *   nk_copy / nk_fill   k_copy / k_fill              src/model.c:190-200
+ *   nk_attention_rel    attention_rel dispatch       src/encoder.c:189-194
+ *   nk_dwconv_ln_silu   dwconv_ln_silu dispatch      src/encoder.c:201-203
+ *   nk_conv2d_c1_s2_relu, nk_dwconv2d_s2, nk_flatten_cf   subsampling dispatches src/encoder.c:150-171
+ *   nk_compact          compact_caches               src/encoder.c:230-240 (one launch for all layers)
+ *   nk_lstm_cell        lstm_cell dispatch           src/decoder.c:383-385
+ *   nk_joint_argmax     joint_partial + argmax_reduce src/decoder.c:393-402
+ * and the GPU runtime of src/gpu.h:54-75 (gpu_* below).
+ */
+#ifndef NEMO_KERNELS_H
+#define NEMO_KERNELS_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct gpu gpu_t;
+typedef struct gpu_buf gpu_buf_t;
+
+/* ---- runtime (src/gpu.h:54-75) ---------------------------------------------------------------- */
+gpu_t *gpu_create(char *err, size_t errlen);
+void gpu_destroy(gpu_t *g);
+const char *gpu_device_name(gpu_t *g);
+gpu_buf_t *gpu_buf_alloc(gpu_t *g, size_t bytes);
+void gpu_buf_free(gpu_buf_t *b);
+void *gpu_buf_dptr(gpu_buf_t *b);
+size_t gpu_buf_len(gpu_buf_t *b);
+int gpu_upload(gpu_t *g, void *dst_dev, const void *src, size_t n);
+int gpu_download(gpu_t *g, void *dst, const void *src_dev, size_t n);
+int gpu_begin(gpu_t *g);
+int gpu_end(gpu_t *g, char *err, size_t errlen);
+double gpu_last_ms(gpu_t *g);
+const char *gpu_last_error(gpu_t *g);
+int gpu_timing_set(gpu_t *g, const char *kernel, int max_launches);
+/* mean duration (ms), launch count and summed algorithmic bytes of the timed launches */
+int gpu_timing_collect(gpu_t *g, double *mean_ms, int *count, double *bytes);
+uint64_t gpu_launch_count(const gpu_t *g);
+
+/* ---- GEMM ------------------------------------------------------------------------------------
+ * C[m][n] (= or +=) alpha * act(sum_k A[m][k] W[n][k] + bias[n]); W bf16 [N][ldw]; act 0 none,
+ * 1 SiLU, 2 ReLU, 3 GLU (output N/2 columns, a_j * sigmoid(b_{j+N/2})).  bias may be NULL.
+ * Requirements: K % 32 == 0 (M > 4) or K % 8 == 0 (M <= 4); A, W 16-byte aligned; lda % 4 == 0;
+ * ldw % 8 == 0. */
+int nk_gemm(gpu_t *g, const float *A, uint32_t lda, const uint16_t *W, uint32_t ldw, const float *bias,
+            float *C, uint32_t ldc, uint32_t M, uint32_t N, uint32_t K, int act, int accumulate, float alpha);
+/* Same, with output row m written to row crow[m] of C (crow: device int array of M entries). */
+int nk_gemm_rows(gpu_t *g, const float *A, uint32_t lda, const uint16_t *W, uint32_t ldw, const float *bias,
+                 float *C, uint32_t ldc, const int *crow, uint32_t M, uint32_t N, uint32_t K, int act, int accumulate,
+                 float alpha);
+/* Kernel selection: 0 automatic (by row count), 1 VALU weight streaming (M <= 4),
+ * 2 few-row MFMA (M <= 16), 3 many-row MFMA.  Returns the previous setting. */
+int nk_gemm_force(int kind);
+/* Name of the kernel nk_gemm would launch for these shapes (for profiling and tests). */
+const char *nk_gemm_kernel_name(uint32_t M, uint32_t N, uint32_t K, int act);
+
+/* ---- norms, attention, convolution ----------------------------------------------------------- */
+int nk_layernorm(gpu_t *g, const float *X, const float *gamma, const float *beta, float *Y, uint32_t M, uint32_t D,
+                 float eps);
+int nk_layernorm2(gpu_t *g, const float *X, const float *g1, const float *b1, const float *g2, const float *b2,
+                  float *Y1, float *Y2, uint32_t M, uint32_t D, float eps);
+int nk_attention_rel(gpu_t *g, const float *Q, uint32_t ldq, const float *K, const float *V, uint32_t ldk,
+                     const float *P, const float *bias_u, const float *bias_v, float *O, uint32_t c, uint32_t L,
+                     uint32_t Lmax, uint32_t H, uint32_t dh, uint32_t D, float scale);
+int nk_dwconv_ln_silu(gpu_t *g, const float *din, const float *W, const float *gamma, const float *beta, float *Y,
+                      uint32_t c, uint32_t D, uint32_t taps, float eps);
+/* Variants that take the cache position from a device chunk descriptor (int[4 + 16]:
+ * pos, cache_len, L, c, then pos + i per row) so a captured graph replays at any position.
+ * kv: K/V cache base with rows of `ld` floats (q | k | v); din_base: conv cache base. */
+int nk_attention_rel_desc(gpu_t *g, const float *kv, uint32_t ld, const int *desc, const float *P, const float *bias_u,
+                          const float *bias_v, float *O, uint32_t c, uint32_t Lmax, uint32_t H, uint32_t dh, uint32_t D,
+                          float scale);
+int nk_dwconv_ln_silu_desc(gpu_t *g, const float *din_base, const int *desc, const float *W, const float *gamma,
+                           const float *beta, float *Y, uint32_t c, uint32_t D, uint32_t taps, float eps);
+int nk_conv2d_c1_s2_relu(gpu_t *g, const float *X, const float *W, const float *bias, float *Y, uint32_t T,
+                         uint32_t F, uint32_t T1, uint32_t F1, uint32_t C);
+int nk_dwconv2d_s2(gpu_t *g, const float *X, const float *W, const float *bias, float *Y, uint32_t T, uint32_t F,
+                   uint32_t T1, uint32_t F1, uint32_t C);
+int nk_flatten_cf(gpu_t *g, const float *X, float *Y, uint32_t T, uint32_t F, uint32_t C);
+int nk_copy(gpu_t *g, const float *src, float *dst, uint32_t n);
+int nk_copy2d(gpu_t *g, const float *src, uint32_t src_ld, float *dst, uint32_t dst_ld, uint32_t rows, uint32_t cols);
+int nk_fill(gpu_t *g, float *dst, uint32_t n, float value);
+int nk_compact(gpu_t *g, float *base, uint64_t stride, uint32_t nbuf, uint32_t rows, uint32_t cols,
+               uint32_t src_row, uint32_t dst_row);
+
+/* ---- RNNT decoder ------------------------------------------------------------------------------ */
+int nk_lstm_cell(gpu_t *g, const float *gates, const float *c_in, float *c_out, float *h_out, uint32_t H);
+/* argmax over V classes of W . relu(enc[enc_row + r] + pred) + bias for r < rows (<= 16);
+ * out[2r] = index (lowest on ties), out[2r+1] = value bits.  part_v/part_i: scratch of
+ * rows * 256 entries. */
+int nk_joint_argmax(gpu_t *g, const float *enc, uint32_t enc_row, uint32_t enc_ld, uint32_t rows, const float *pred,
+                    const uint16_t *W, const float *bias, uint32_t V, uint32_t H, float *part_v, int *part_i,
+                    int *out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,45 @@
+/* Cache-aware streaming FastConformer encoder + language prompt + joint encoder projection.
+ * Same interface and bookkeeping as the reference (src/encoder.h:1-29, src/encoder.c). */
+#ifndef NEMO_ENCODER_H
+#define NEMO_ENCODER_H
+#include "model.h"
+
+typedef struct encoder encoder_t;
+
+typedef struct {
+    int frames;              /* encoder frames produced by this step (may be 0) */
+    const float *prompted;   /* device [frames][d_model] post-prompt encoder output */
+    const float *joint_enc;  /* device [frames][joint_hidden] joint.enc projection */
+    double gpu_ms, wall_ms;
+} enc_out_t;
+
+encoder_t *encoder_create(model_t *m, int right_context);
+void encoder_destroy(encoder_t *e);
+void encoder_reset(encoder_t *e);
+int encoder_right(const encoder_t *e);
+int encoder_chunk_frames(const encoder_t *e);
+int encoder_chunk_mel(const encoder_t *e);
+void encoder_push(encoder_t *e, const float *mel, size_t nframes);
+/* 1: a piece was consumed (out->frames may be 0); 0: nothing to do; -1: error in err */
+int encoder_step(encoder_t *e, int final, enc_out_t *out, char *err, size_t errlen);
+
+/* Replay each chunk shape as a captured hipGraph (default on). */
+void encoder_use_graphs(encoder_t *e, int on);
+/* Keep per-layer block outputs of every chunk (test hook). */
+void encoder_set_dump(encoder_t *e, int on);
+size_t encoder_dump_frames(const encoder_t *e);
+const float *encoder_dump_layers(const encoder_t *e);   /* frames x n_layers x d_model */
+const float *encoder_dump_prompted(const encoder_t *e); /* frames x d_model */
+const float *encoder_dump_joint(const encoder_t *e);    /* frames x joint_hidden */
+
+/* Bookkeeping of one step (src/encoder.c:242-280), exposed for host-side tests. */
+typedef struct {
+    size_t pending_n, consumed, emitted;
+    int mel_cache_n, closed;
+} enc_book_t;
+typedef struct {
+    int ran, take, nwin, lo, hi, c, include_boundary, T3;
+} enc_plan_t;
+enc_plan_t enc_plan_step(enc_book_t *b, int final, int chunk_mel, int subsampling, int mel_cache);
+
+#endif

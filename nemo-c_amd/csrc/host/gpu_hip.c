@@ -1,0 +1,330 @@
+/* HIP runtime layer for one gfx950 GPU (see gpu.h).  Plain C over the HIP runtime API. */
+#include "gpu.h"
+#include <hip/hip_runtime_api.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* gfx950 code object linked into the library (co_blob.S) */
+extern const unsigned char nk_code_object_start[];
+extern const unsigned char nk_code_object_end[];
+
+#define GPU_MAX_FN 96
+#define GPU_MAX_TIMED 4096
+
+struct gpu {
+    int dev;
+    hipModule_t mod;
+    hipStream_t stream;
+    hipEvent_t ev0, ev1;
+    double last_ms;
+    int in_batch, capturing, failed;
+    char name[256];
+    char err[512];
+    struct { char name[48]; hipFunction_t f; } fn[GPU_MAX_FN];
+    int nfn;
+    float *ws;
+    size_t ws_floats;
+    uint32_t *counters;
+    size_t ncounters;
+    uint64_t launches;
+    /* per-kernel timing */
+    char timed[48];
+    hipEvent_t *tev;
+    double *tbytes, next_bytes;
+    int tmax, tn;
+};
+struct gpu_buf {
+    void *d;
+    size_t len;
+};
+struct gpu_graph {
+    hipGraph_t graph;
+    hipGraphExec_t exec;
+};
+
+static int fail(gpu_t *g, const char *what, hipError_t e) {
+    if (!g->failed) snprintf(g->err, sizeof g->err, "%s: %s", what, hipGetErrorString(e));
+    g->failed = 1;
+    return -1;
+}
+
+int gpu_fail(gpu_t *g, const char *msg) {
+    if (!g->failed) snprintf(g->err, sizeof g->err, "%s", msg);
+    g->failed = 1;
+    return -1;
+}
+
+gpu_t *gpu_create(char *err, size_t errlen) {
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess || n <= 0) {
+        snprintf(err, errlen, "no HIP device (%s)", hipGetErrorString(e));
+        return NULL;
+    }
+    hipDeviceProp_t prop;
+    if ((e = hipSetDevice(0)) != hipSuccess || (e = hipGetDeviceProperties(&prop, 0)) != hipSuccess) {
+        snprintf(err, errlen, "hip device 0: %s", hipGetErrorString(e));
+        return NULL;
+    }
+    if (strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
+        snprintf(err, errlen, "device is %s; this build carries gfx950 code only", prop.gcnArchName);
+        return NULL;
+    }
+    gpu_t *g = calloc(1, sizeof *g);
+    g->dev = 0;
+    snprintf(g->name, sizeof g->name, "%s (%s, %d CUs)", prop.name, prop.gcnArchName, prop.multiProcessorCount);
+    if ((e = hipModuleLoadData(&g->mod, nk_code_object_start)) != hipSuccess) {
+        snprintf(err, errlen, "load gfx950 code object: %s", hipGetErrorString(e));
+        free(g);
+        return NULL;
+    }
+    if ((e = hipStreamCreateWithFlags(&g->stream, hipStreamNonBlocking)) != hipSuccess ||
+        (e = hipEventCreate(&g->ev0)) != hipSuccess || (e = hipEventCreate(&g->ev1)) != hipSuccess) {
+        snprintf(err, errlen, "stream/event: %s", hipGetErrorString(e));
+        hipModuleUnload(g->mod);
+        free(g);
+        return NULL;
+    }
+    return g;
+}
+
+void gpu_destroy(gpu_t *g) {
+    if (!g) return;
+    hipStreamSynchronize(g->stream);
+    if (g->tev) {
+        for (int i = 0; i < 2 * g->tmax; ++i) hipEventDestroy(g->tev[i]);
+        free(g->tev);
+        free(g->tbytes);
+    }
+    if (g->ws) hipFree(g->ws);
+    if (g->counters) hipFree(g->counters);
+    hipEventDestroy(g->ev0);
+    hipEventDestroy(g->ev1);
+    hipStreamDestroy(g->stream);
+    hipModuleUnload(g->mod);
+    free(g);
+}
+
+const char *gpu_device_name(gpu_t *g) { return g->name; }
+const char *gpu_last_error(gpu_t *g) { return g->err; }
+double gpu_last_ms(gpu_t *g) { return g->last_ms; }
+uint64_t gpu_launch_count(const gpu_t *g) { return g->launches; }
+int gpu_capturing(const gpu_t *g) { return g->capturing; }
+
+gpu_buf_t *gpu_buf_alloc(gpu_t *g, size_t bytes) {
+    gpu_buf_t *b = calloc(1, sizeof *b);
+    b->len = bytes ? bytes : 256;
+    if (hipMalloc(&b->d, b->len) != hipSuccess) { free(b); return NULL; }
+    if (hipMemset(b->d, 0, b->len) != hipSuccess) { hipFree(b->d); free(b); return NULL; }
+    (void)g;
+    return b;
+}
+void gpu_buf_free(gpu_buf_t *b) {
+    if (!b) return;
+    hipFree(b->d);
+    free(b);
+}
+void *gpu_buf_dptr(gpu_buf_t *b) { return b ? b->d : NULL; }
+size_t gpu_buf_len(gpu_buf_t *b) { return b->len; }
+
+void *gpu_host_alloc(gpu_t *g, size_t bytes) {
+    void *p = NULL;
+    (void)g;
+    if (hipHostMalloc(&p, bytes ? bytes : 64, hipHostMallocDefault) != hipSuccess) return NULL;
+    memset(p, 0, bytes ? bytes : 64);
+    return p;
+}
+void gpu_host_free(void *p) { if (p) hipHostFree(p); }
+
+int gpu_upload(gpu_t *g, void *dst, const void *src, size_t n) {
+    if (!n) return 0;
+    hipError_t e = hipMemcpy(dst, src, n, hipMemcpyHostToDevice);
+    return e == hipSuccess ? 0 : fail(g, "upload", e);
+}
+int gpu_download(gpu_t *g, void *dst, const void *src, size_t n) {
+    if (!n) return 0;
+    hipError_t e = hipStreamSynchronize(g->stream);
+    if (e != hipSuccess) return fail(g, "download sync", e);
+    e = hipMemcpy(dst, src, n, hipMemcpyDeviceToHost);
+    return e == hipSuccess ? 0 : fail(g, "download", e);
+}
+int gpu_upload_async(gpu_t *g, void *dst, const void *src, size_t n) {
+    if (!n) return 0;
+    hipError_t e = hipMemcpyAsync(dst, src, n, hipMemcpyHostToDevice, g->stream);
+    return e == hipSuccess ? 0 : fail(g, "upload_async", e);
+}
+int gpu_download_async(gpu_t *g, void *dst, const void *src, size_t n) {
+    if (!n) return 0;
+    hipError_t e = hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToHost, g->stream);
+    return e == hipSuccess ? 0 : fail(g, "download_async", e);
+}
+
+static hipFunction_t lookup(gpu_t *g, const char *kernel) {
+    for (int i = 0; i < g->nfn; ++i)
+        if (!strcmp(g->fn[i].name, kernel)) return g->fn[i].f;
+    hipFunction_t f = NULL;
+    hipError_t e = hipModuleGetFunction(&f, g->mod, kernel);
+    if (e != hipSuccess) {
+        char what[96];
+        snprintf(what, sizeof what, "kernel %s", kernel);
+        fail(g, what, e);
+        return NULL;
+    }
+    if (g->nfn < GPU_MAX_FN) {
+        snprintf(g->fn[g->nfn].name, sizeof g->fn[g->nfn].name, "%s", kernel);
+        g->fn[g->nfn].f = f;
+        g->nfn++;
+    }
+    return f;
+}
+
+int gpu_begin(gpu_t *g) {
+    g->failed = 0;
+    g->err[0] = 0;
+    g->in_batch = 1;
+    hipError_t e = hipEventRecord(g->ev0, g->stream);
+    return e == hipSuccess ? 0 : fail(g, "begin", e);
+}
+
+int gpu_launch(gpu_t *g, const char *kernel, const void *args, size_t args_size,
+               uint32_t gx, uint32_t gy, uint32_t gz, uint32_t bx, uint32_t by, uint32_t bz) {
+    if (!gx || !gy || !gz) return 0;
+    hipFunction_t f = lookup(g, kernel);
+    if (!f) return -1;
+    size_t sz = args_size;
+    void *config[] = { HIP_LAUNCH_PARAM_BUFFER_POINTER, (void *)args, HIP_LAUNCH_PARAM_BUFFER_SIZE, &sz,
+                       HIP_LAUNCH_PARAM_END };
+    const int timed = !g->capturing && g->tev && g->tn < g->tmax && !strcmp(kernel, g->timed);
+    if (timed) hipEventRecord(g->tev[2 * g->tn], g->stream);
+    hipError_t e = hipModuleLaunchKernel(f, gx, gy, gz, bx, by, bz, 0, g->stream, NULL, config);
+    if (timed) {
+        hipEventRecord(g->tev[2 * g->tn + 1], g->stream);
+        g->tbytes[g->tn] = g->next_bytes;
+        g->tn++;
+    }
+    g->next_bytes = 0.0;
+    g->launches++;
+    if (e != hipSuccess) {
+        char what[96];
+        snprintf(what, sizeof what, "launch %s", kernel);
+        return fail(g, what, e);
+    }
+    return 0;
+}
+
+int gpu_sync(gpu_t *g) {
+    hipError_t e = hipStreamSynchronize(g->stream);
+    return e == hipSuccess ? 0 : fail(g, "sync", e);
+}
+
+int gpu_end(gpu_t *g, char *err, size_t errlen) {
+    hipError_t e = hipEventRecord(g->ev1, g->stream);
+    if (e == hipSuccess) e = hipEventSynchronize(g->ev1);
+    if (e != hipSuccess) fail(g, "end", e);
+    float ms = 0.0f;
+    if (!g->failed && hipEventElapsedTime(&ms, g->ev0, g->ev1) == hipSuccess) g->last_ms = ms;
+    g->in_batch = 0;
+    if (g->failed) {
+        if (errlen) snprintf(err, errlen, "gpu: %s", g->err);
+        return -1;
+    }
+    return 0;
+}
+
+int gpu_capture_begin(gpu_t *g) {
+    hipError_t e = hipStreamBeginCapture(g->stream, hipStreamCaptureModeThreadLocal);
+    if (e != hipSuccess) return fail(g, "capture begin", e);
+    g->capturing = 1;
+    return 0;
+}
+
+gpu_graph_t *gpu_capture_end(gpu_t *g) {
+    gpu_graph_t *gr = calloc(1, sizeof *gr);
+    hipError_t e = hipStreamEndCapture(g->stream, &gr->graph);
+    g->capturing = 0;
+    if (e != hipSuccess) { fail(g, "capture end", e); free(gr); return NULL; }
+    if (g->failed) { hipGraphDestroy(gr->graph); free(gr); return NULL; }
+    e = hipGraphInstantiate(&gr->exec, gr->graph, NULL, NULL, 0);
+    if (e != hipSuccess) { fail(g, "graph instantiate", e); hipGraphDestroy(gr->graph); free(gr); return NULL; }
+    return gr;
+}
+
+int gpu_graph_launch(gpu_t *g, gpu_graph_t *gr) {
+    hipError_t e = hipGraphLaunch(gr->exec, g->stream);
+    return e == hipSuccess ? 0 : fail(g, "graph launch", e);
+}
+
+void gpu_graph_free(gpu_graph_t *gr) {
+    if (!gr) return;
+    hipGraphExecDestroy(gr->exec);
+    hipGraphDestroy(gr->graph);
+    free(gr);
+}
+
+float *gpu_splitk_ws(gpu_t *g, size_t floats) {
+    if (floats > g->ws_floats) {
+        if (g->capturing) { fail(g, "split-K scratch grown during capture", hipErrorInvalidValue); return NULL; }
+        hipStreamSynchronize(g->stream);
+        if (g->ws) hipFree(g->ws);
+        size_t n = floats < (1u << 20) ? (1u << 20) : floats;
+        if (hipMalloc((void **)&g->ws, n * sizeof(float)) != hipSuccess) { g->ws = NULL; g->ws_floats = 0; return NULL; }
+        g->ws_floats = n;
+    }
+    return g->ws;
+}
+
+uint32_t *gpu_splitk_counters(gpu_t *g, size_t n) {
+    if (n > g->ncounters) {
+        if (g->capturing) { fail(g, "split-K counters grown during capture", hipErrorInvalidValue); return NULL; }
+        hipStreamSynchronize(g->stream);
+        if (g->counters) hipFree(g->counters);
+        size_t m = n < 4096 ? 4096 : n;
+        if (hipMalloc((void **)&g->counters, m * sizeof(uint32_t)) != hipSuccess) { g->counters = NULL; g->ncounters = 0; return NULL; }
+        if (hipMemset(g->counters, 0, m * sizeof(uint32_t)) != hipSuccess) return NULL;
+        g->ncounters = m;
+    }
+    return g->counters;
+}
+
+int gpu_timing_set(gpu_t *g, const char *kernel, int max_launches) {
+    if (g->tev) {
+        for (int i = 0; i < 2 * g->tmax; ++i) hipEventDestroy(g->tev[i]);
+        free(g->tev);
+        free(g->tbytes);
+        g->tev = NULL;
+        g->tbytes = NULL;
+    }
+    g->tn = g->tmax = 0;
+    g->timed[0] = 0;
+    if (!kernel || max_launches <= 0) return 0;
+    if (max_launches > GPU_MAX_TIMED) max_launches = GPU_MAX_TIMED;
+    g->tev = calloc((size_t)max_launches * 2, sizeof(hipEvent_t));
+    g->tbytes = calloc((size_t)max_launches, sizeof(double));
+    for (int i = 0; i < 2 * max_launches; ++i)
+        if (hipEventCreate(&g->tev[i]) != hipSuccess) return fail(g, "timing events", hipErrorOutOfMemory);
+    g->tmax = max_launches;
+    snprintf(g->timed, sizeof g->timed, "%s", kernel);
+    return 0;
+}
+
+void gpu_next_bytes(gpu_t *g, double bytes) { g->next_bytes = bytes; }
+
+int gpu_timing_collect(gpu_t *g, double *mean_ms, int *count, double *bytes) {
+    *mean_ms = 0.0;
+    *count = 0;
+    if (bytes) *bytes = 0.0;
+    if (!g->tev) return 0;
+    hipStreamSynchronize(g->stream);
+    double sum = 0.0;
+    for (int i = 0; i < g->tn; ++i) {
+        float ms = 0.0f;
+        if (hipEventElapsedTime(&ms, g->tev[2 * i], g->tev[2 * i + 1]) != hipSuccess) return fail(g, "timing", hipErrorInvalidValue);
+        sum += ms;
+        if (bytes) *bytes += g->tbytes[i];
+    }
+    *count = g->tn;
+    *mean_ms = g->tn ? sum / g->tn : 0.0;
+    g->tn = 0;
+    return 0;
+}

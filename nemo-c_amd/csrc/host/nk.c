@@ -1,0 +1,202 @@
+/* Kernel launchers and the GEMM kernel policy (see include/nemo_kernels.h).
+ * Host-side shape and alignment checks turn unsupported arguments into errors before any
+ * launch, so a kernel never sees a shape its grid or indexing does not cover. */
+#include "nemo_kernels.h"
+#include "gpu.h"
+#include "../kernel_params.h"
+#include <stdio.h>
+#include <string.h>
+
+static int g_force = 0;
+
+int nk_gemm_force(int kind) {
+    int prev = g_force;
+    g_force = kind;
+    return prev;
+}
+
+/* argument errors are recorded like launch failures: gpu_end then reports them */
+static int bad(gpu_t *g, const char *what) { return gpu_fail(g, what); }
+
+static int aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
+
+enum { K_GEMV = 1, K_FR = 2, K_MR = 3 };
+
+static int pick(uint32_t M, uint32_t K, int act) {
+    if (g_force == K_GEMV && M <= 4) return K_GEMV;
+    if (g_force == K_FR && M <= NK_FEW_ROWS && K % 32 == 0) return K_FR;
+    if (g_force == K_MR && act != NK_ACT_GLU && K % 32 == 0) return K_MR;
+    if (M <= 4) return K_GEMV;
+    if (M <= NK_FEW_ROWS) return K_FR;
+    return K_MR;
+}
+
+const char *nk_gemm_kernel_name(uint32_t M, uint32_t N, uint32_t K, int act) {
+    static char buf[32];
+    (void)N;
+    switch (pick(M, K, act)) {
+    case K_GEMV:
+        snprintf(buf, sizeof buf, "gemv_r%u_c%u", M, (act == NK_ACT_GLU || K <= 2048) ? 2u : 1u);
+        return buf;
+    case K_FR: return "gemm_fr";
+    default: return "gemm_mr";
+    }
+}
+
+int nk_gemm_rows(gpu_t *g, const float *A, uint32_t lda, const uint16_t *W, uint32_t ldw, const float *bias,
+                 float *C, uint32_t ldc, const int *crow, uint32_t M, uint32_t N, uint32_t K, int act, int accumulate,
+                 float alpha) {
+    if (!M) return 0;
+    if (!N || !K || (act == NK_ACT_GLU && (N & 1))) return bad(g, "gemm: bad shape");
+    if (!aligned16(A) || !aligned16(W) || lda % 4 || ldw % 8 || K % 8 || K > lda || K > ldw)
+        return bad(g, "gemm: A/W must be 16-byte aligned with lda % 4 == 0, ldw % 8 == 0, K % 8 == 0");
+    const uint32_t nout = act == NK_ACT_GLU ? N / 2 : N;
+    if (ldc < nout) return bad(g, "gemm: ldc < output width");
+    NkGemmArgs a;
+    memset(&a, 0, sizeof a);
+    a.A = A; a.W = W; a.bias = bias; a.C = C; a.crow = crow;
+    a.M = M; a.N = N; a.K = K; a.lda = lda; a.ldw = ldw; a.ldc = ldc;
+    a.act = (uint32_t)act; a.accumulate = (uint32_t)(accumulate != 0); a.alpha = alpha; a.splits = 1;
+    const int kind = pick(M, K, act);
+    /* algorithmic HBM bytes: every weight once, A once, C written (and read when accumulating) */
+    gpu_next_bytes(g, 2.0 * N * K + 4.0 * M * K + 4.0 * M * nout * (accumulate ? 2 : 1) + (bias ? 4.0 * N : 0.0));
+    if (kind == K_GEMV) {
+        const uint32_t nc = (act == NK_ACT_GLU || K <= 2048) ? 2u : 1u;
+        const uint32_t per_wave = act == NK_ACT_GLU ? 1u : nc;
+        const uint32_t waves = (nout + per_wave - 1) / per_wave;
+        char name[24];
+        snprintf(name, sizeof name, "gemv_r%u_c%u", M, nc);
+        return gpu_launch(g, name, &a, sizeof a, (waves + 3) / 4, 1, 1, 256, 1, 1);
+    }
+    if (K % 32) return bad(g, "gemm: K % 32 != 0 for the MFMA kernels");
+    if (kind == K_FR) {
+        const uint32_t tiles = (nout + 15) / 16;
+        const uint32_t KS = K / 32, maxsteps = NK_FR_MAX_KC / 32;
+        uint32_t S = (KS + maxsteps - 1) / maxsteps;
+        const uint32_t want = (256 + tiles - 1) / tiles;
+        if (S < want) S = want;
+        if (S > KS) S = KS;
+        a.splits = S;
+        if (S > 1) {
+            a.ws = gpu_splitk_ws(g, (size_t)tiles * S * 512);
+            a.counters = gpu_splitk_counters(g, tiles);
+            if (!a.ws || !a.counters) return bad(g, "gemm: split-K scratch");
+        }
+        return gpu_launch(g, "gemm_fr", &a, sizeof a, tiles, S, 1, 256, 1, 1);
+    }
+    if (act == NK_ACT_GLU) return bad(g, "gemm: GLU needs M <= 16");
+    return gpu_launch(g, "gemm_mr", &a, sizeof a, (N + 63) / 64, (M + 63) / 64, 1, 256, 1, 1);
+}
+
+int nk_gemm(gpu_t *g, const float *A, uint32_t lda, const uint16_t *W, uint32_t ldw, const float *bias, float *C,
+            uint32_t ldc, uint32_t M, uint32_t N, uint32_t K, int act, int accumulate, float alpha) {
+    return nk_gemm_rows(g, A, lda, W, ldw, bias, C, ldc, NULL, M, N, K, act, accumulate, alpha);
+}
+
+int nk_layernorm2(gpu_t *g, const float *X, const float *g1, const float *b1, const float *g2, const float *b2,
+                  float *Y1, float *Y2, uint32_t M, uint32_t D, float eps) {
+    if (!M) return 0;
+    if (D > NK_LN_THREADS * NK_LN_MAX_PER) return bad(g, "layernorm: D too large");
+    NkLnArgs a = { X, g1, b1, g2, b2, Y1, Y2, M, D, eps, 0 };
+    return gpu_launch(g, "layernorm", &a, sizeof a, M, 1, 1, NK_LN_THREADS, 1, 1);
+}
+
+int nk_layernorm(gpu_t *g, const float *X, const float *gamma, const float *beta, float *Y, uint32_t M, uint32_t D,
+                 float eps) {
+    return nk_layernorm2(g, X, gamma, beta, NULL, NULL, Y, NULL, M, D, eps);
+}
+
+int nk_attention_rel(gpu_t *g, const float *Q, uint32_t ldq, const float *K, const float *V, uint32_t ldk,
+                     const float *P, const float *bias_u, const float *bias_v, float *O, uint32_t c, uint32_t L,
+                     uint32_t Lmax, uint32_t H, uint32_t dh, uint32_t D, float scale) {
+    if (!c) return 0;
+    if (dh != 128 || H * dh != D) return bad(g, "attention: head_dim must be 128");
+    if (L > NK_ATT_MAX_L || L > Lmax || c > L || c > Lmax) return bad(g, "attention: window exceeds the table");
+    if ((uintptr_t)K % 8 || (uintptr_t)P % 8 || ldk % 2) return bad(g, "attention: K/P must be 8-byte aligned");
+    NkAttnArgs a = { Q, K, V, P, bias_u, bias_v, O, NULL, c, L, Lmax, H, dh, D, ldq, ldk, scale, 0 };
+    return gpu_launch(g, "attention_rel", &a, sizeof a, H, c, 1, 128, 1, 1);
+}
+
+int nk_attention_rel_desc(gpu_t *g, const float *kv, uint32_t ld, const int *desc, const float *P, const float *bias_u,
+                          const float *bias_v, float *O, uint32_t c, uint32_t Lmax, uint32_t H, uint32_t dh, uint32_t D,
+                          float scale) {
+    if (!c) return 0;
+    if (dh != 128 || H * dh != D || c > Lmax) return bad(g, "attention: head_dim must be 128");
+    NkAttnArgs a = { kv, kv + D, kv + 2 * D, P, bias_u, bias_v, O, desc, c, 0, Lmax, H, dh, D, ld, ld, scale, 0 };
+    return gpu_launch(g, "attention_rel", &a, sizeof a, H, c, 1, 128, 1, 1);
+}
+
+int nk_dwconv_ln_silu(gpu_t *g, const float *din, const float *W, const float *gamma, const float *beta, float *Y,
+                      uint32_t c, uint32_t D, uint32_t taps, float eps) {
+    if (!c) return 0;
+    if (D > NK_LN_THREADS * NK_LN_MAX_PER) return bad(g, "dwconv: D too large");
+    NkDwArgs a = { din, W, gamma, beta, Y, NULL, c, D, taps, eps };
+    return gpu_launch(g, "dwconv_ln_silu", &a, sizeof a, c, 1, 1, NK_LN_THREADS, 1, 1);
+}
+
+int nk_dwconv_ln_silu_desc(gpu_t *g, const float *din_base, const int *desc, const float *W, const float *gamma,
+                           const float *beta, float *Y, uint32_t c, uint32_t D, uint32_t taps, float eps) {
+    if (!c) return 0;
+    if (D > NK_LN_THREADS * NK_LN_MAX_PER) return bad(g, "dwconv: D too large");
+    NkDwArgs a = { din_base, W, gamma, beta, Y, desc, c, D, taps, eps };
+    return gpu_launch(g, "dwconv_ln_silu", &a, sizeof a, c, 1, 1, NK_LN_THREADS, 1, 1);
+}
+
+static uint32_t blocks_for(uint64_t n) { return (uint32_t)((n + 255) / 256); }
+
+int nk_conv2d_c1_s2_relu(gpu_t *g, const float *X, const float *W, const float *bias, float *Y, uint32_t T,
+                         uint32_t F, uint32_t T1, uint32_t F1, uint32_t C) {
+    NkConvArgs a = { X, W, bias, Y, T, F, T1, F1, C, 0 };
+    return gpu_launch(g, "conv2d_c1_s2_relu", &a, sizeof a, blocks_for((uint64_t)T1 * F1 * C), 1, 1, 256, 1, 1);
+}
+
+int nk_dwconv2d_s2(gpu_t *g, const float *X, const float *W, const float *bias, float *Y, uint32_t T, uint32_t F,
+                   uint32_t T1, uint32_t F1, uint32_t C) {
+    NkConvArgs a = { X, W, bias, Y, T, F, T1, F1, C, 0 };
+    return gpu_launch(g, "dwconv2d_s2", &a, sizeof a, blocks_for((uint64_t)T1 * F1 * C), 1, 1, 256, 1, 1);
+}
+
+int nk_flatten_cf(gpu_t *g, const float *X, float *Y, uint32_t T, uint32_t F, uint32_t C) {
+    NkFlatArgs a = { X, Y, T, F, C, 0 };
+    return gpu_launch(g, "flatten_cf", &a, sizeof a, blocks_for((uint64_t)T * F * C), 1, 1, 256, 1, 1);
+}
+
+int nk_copy(gpu_t *g, const float *src, float *dst, uint32_t n) {
+    NkCopyArgs a = { src, dst, n, 0 };
+    return gpu_launch(g, "copy_f32", &a, sizeof a, blocks_for(n), 1, 1, 256, 1, 1);
+}
+
+int nk_copy2d(gpu_t *g, const float *src, uint32_t src_ld, float *dst, uint32_t dst_ld, uint32_t rows, uint32_t cols) {
+    NkCopy2dArgs a = { src, dst, rows, cols, src_ld, dst_ld };
+    return gpu_launch(g, "copy2d_f32", &a, sizeof a, blocks_for((uint64_t)rows * cols), 1, 1, 256, 1, 1);
+}
+
+int nk_fill(gpu_t *g, float *dst, uint32_t n, float value) {
+    NkFillArgs a = { dst, n, value };
+    return gpu_launch(g, "fill_f32", &a, sizeof a, blocks_for(n), 1, 1, 256, 1, 1);
+}
+
+int nk_compact(gpu_t *g, float *base, uint64_t stride, uint32_t nbuf, uint32_t rows, uint32_t cols, uint32_t src_row,
+               uint32_t dst_row) {
+    if (!rows || !nbuf) return 0;
+    if (src_row < dst_row + rows && dst_row < src_row + rows) return bad(g, "compact: overlapping rows");
+    NkCompactArgs a = { base, stride, nbuf, rows, cols, src_row, dst_row, 0 };
+    return gpu_launch(g, "compact_rows", &a, sizeof a, blocks_for((uint64_t)rows * cols), nbuf, 1, 256, 1, 1);
+}
+
+int nk_lstm_cell(gpu_t *g, const float *gates, const float *c_in, float *c_out, float *h_out, uint32_t H) {
+    NkLstmArgs a = { gates, c_in, c_out, h_out, H, 0 };
+    return gpu_launch(g, "lstm_cell", &a, sizeof a, blocks_for(H), 1, 1, 256, 1, 1);
+}
+
+int nk_joint_argmax(gpu_t *g, const float *enc, uint32_t enc_row, uint32_t enc_ld, uint32_t rows, const float *pred,
+                    const uint16_t *W, const float *bias, uint32_t V, uint32_t H, float *part_v, int *part_i,
+                    int *out) {
+    if (!rows) return 0;
+    if (rows > NK_DEC_MAX_BATCH || H > NK_JOINT_MAX_H || (H & 1) || ((uintptr_t)W & 3))
+        return bad(g, "joint: rows <= 16, even H <= 1024, 4-byte aligned W");
+    NkJointArgs j = { enc, pred, W, bias, part_v, part_i, V, H, enc_row, enc_ld };
+    if (gpu_launch(g, "joint_partial", &j, sizeof j, NK_JOINT_GROUPS, rows, 1, 256, 1, 1)) return -1;
+    NkArgmaxArgs r = { part_v, part_i, out, NK_JOINT_GROUPS * NK_JOINT_WAVES, 0 };
+    return gpu_launch(g, "argmax_reduce", &r, sizeof r, rows, 1, 1, 256, 1, 1);
+}

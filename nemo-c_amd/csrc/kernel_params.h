@@ -1,0 +1,164 @@
+/* Kernel argument blocks shared by the C host and the gfx950 HIP kernels.
+ *
+ * Every kernel takes exactly one of these structs by value; the host passes its bytes through
+ * hipModuleLaunchKernel's argument buffer, so the struct layout is the kernel ABI.  Pointers are
+ * device addresses.  This replaces the Metal parameter blocks of the reference
+ * (src/kernel_params.h:22-32) with the same meaning per field, plus the device pointers that
+ * Metal bound as separate buffer arguments.
+ */
+#ifndef NEMO_KERNEL_PARAMS_H
+#define NEMO_KERNEL_PARAMS_H
+#ifdef __HIPCC__
+#include <hip/hip_runtime.h>
+typedef unsigned int u32;
+typedef unsigned short u16;
+#else
+#include <stdint.h>
+typedef uint32_t u32;
+typedef uint16_t u16;
+#endif
+
+/* Row and chunk limits.  One wavefront is 64 lanes on CDNA4. */
+#define NK_WAVE 64
+#define NK_FEW_ROWS 16          /* GEMMs with M <= 16 use the weight-streaming kernels            */
+#define NK_ATT_MAX_L 128        /* attention window limit (reference ATT_MAX_L 80; 56 + 16 + 2)    */
+#define NK_DEC_MAX_BATCH 16     /* joint rows per decoder round trip (reference DEC_MAX_BATCH)    */
+#define NK_JOINT_GROUPS 64      /* workgroups of the joint scoring kernel                          */
+#define NK_JOINT_WAVES 4        /* waves per joint workgroup                                       */
+#define NK_JOINT_MAX_H 1024     /* joint hidden size limit (LDS staging)                           */
+#define NK_CACHE_EPOCH_CHUNKS 8 /* K/V and conv caches compacted once per this many chunks         */
+#define NK_LN_THREADS 256
+#define NK_LN_MAX_PER 8         /* values per thread held by the LayerNorm kernels: D <= 2048      */
+#define NK_FR_MAX_KC 1024       /* few-row MFMA GEMM: K columns of A staged per workgroup          */
+
+enum { NK_ACT_NONE = 0, NK_ACT_SILU = 1, NK_ACT_RELU = 2, NK_ACT_GLU = 3 };
+
+/* C[row(m)][n] (= or +=) alpha * act(sum_k A[m][k] * W[n][k] + bias[n]); act GLU: N is the
+ * weight height and the output has N/2 columns, column j = a_j * sigmoid(b_{j+N/2}).
+ * crow, when set, maps output row m to row crow[m] of C (scatter into a cache). */
+typedef struct {
+    const float *A;
+    const u16 *W;
+    const float *bias;
+    float *C;
+    const int *crow;
+    float *ws;      /* split-K partials (few-row MFMA kernel)          */
+    u32 *counters;  /* split-K arrival counters, self-resetting         */
+    u32 M, N, K, lda, ldw, ldc;
+    u32 act, accumulate, splits, pad0;
+    float alpha;
+    u32 pad1;
+} NkGemmArgs;
+
+typedef struct {
+    const float *X;
+    const float *g1, *b1, *g2, *b2;
+    float *Y1, *Y2; /* Y2 only for the paired LayerNorm */
+    u32 M, D;
+    float eps;
+    u32 pad;
+} NkLnArgs;
+
+/* Chunk descriptor in device memory, written by the host before each chunk so that a captured
+ * graph can replay a chunk at any cache position:
+ *   [0] pos        first cache row of this chunk in the per-layer K/V and conv buffers
+ *   [1] cache_len  cached attention rows in front of pos
+ *   [2] L          attention window = cache_len + c
+ *   [3] c          rows of the chunk
+ *   [4 + i]        pos + i, the cache row of chunk row i (GEMM output row map) */
+#define NK_DESC_POS 0
+#define NK_DESC_CACHE 1
+#define NK_DESC_L 2
+#define NK_DESC_C 3
+#define NK_DESC_ROWS 4
+#define NK_DESC_INTS (NK_DESC_ROWS + NK_FEW_ROWS)
+
+/* Relative-position attention for one chunk of one stream.
+ * Q: [c][ldq]; K, V: [L][ldk] (the window: cached rows then the chunk's rows);
+ * P: [2*Lmax-1][D]; O: [c][D].
+ * With desc set, Q/K/V are the cache bases (rows of ldq = ldk floats) and the window comes from
+ * the descriptor: Q row pos + i, K/V rows pos - cache_len .. pos + c - 1, L = cache_len + c. */
+typedef struct {
+    const float *Q, *K, *V, *P, *bu, *bv;
+    float *O;
+    const int *desc;
+    u32 c, L, Lmax, H, dh, D, ldq, ldk;
+    float scale;
+    u32 pad;
+} NkAttnArgs;
+
+/* Causal depthwise conv + LN + SiLU. din: [(taps-1) + c][D]; W: [D][taps].
+ * With desc set, din is the conv cache base and the rows start at pos - (taps-1). */
+typedef struct {
+    const float *din, *W, *g, *b;
+    float *Y;
+    const int *desc;
+    u32 c, D, taps;
+    float eps;
+} NkDwArgs;
+
+/* Subsampling convs. X [T][F] (conv 0) or [T][F][C]; Y [T1][F1][C]. */
+typedef struct {
+    const float *X, *W, *bias;
+    float *Y;
+    u32 T, F, T1, F1, C, pad;
+} NkConvArgs;
+
+typedef struct {
+    const float *X;
+    float *Y;
+    u32 T, F, C, pad;
+} NkFlatArgs;
+
+typedef struct {
+    const float *src;
+    float *dst;
+    u32 n, pad;
+} NkCopyArgs;
+
+typedef struct {
+    float *dst;
+    u32 n;
+    float value;
+} NkFillArgs;
+
+/* rows x cols floats from src (row stride src_ld) to dst (row stride dst_ld) */
+typedef struct {
+    const float *src;
+    float *dst;
+    u32 rows, cols, src_ld, dst_ld;
+} NkCopy2dArgs;
+
+/* Moves `rows` rows of `cols` floats from row src_row to row dst_row in each of `nbuf`
+ * buffers laid out `stride` floats apart (the per-layer caches). */
+typedef struct {
+    float *base;
+    unsigned long long stride;
+    u32 nbuf, rows, cols, src_row, dst_row, pad;
+} NkCompactArgs;
+
+typedef struct {
+    const float *gates, *c_in;
+    float *c_out, *h_out;
+    u32 H, pad;
+} NkLstmArgs;
+
+/* Joint scoring of `rows` encoder frames with one prediction vector.
+ * part_v / part_i: [rows][NK_JOINT_GROUPS * NK_JOINT_WAVES]. */
+typedef struct {
+    const float *enc, *pred;
+    const u16 *W;
+    const float *bias;
+    float *part_v;
+    int *part_i;
+    u32 V, H, enc_row, enc_ld;
+} NkJointArgs;
+
+typedef struct {
+    const float *part_v;
+    const int *part_i;
+    int *out; /* out[2*row] = index, out[2*row+1] = value bits */
+    u32 n, pad;
+} NkArgmaxArgs;
+
+#endif

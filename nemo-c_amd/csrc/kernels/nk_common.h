@@ -1,0 +1,96 @@
+/* Device helpers shared by the gfx950 kernels. */
+#ifndef NK_COMMON_H
+#define NK_COMMON_H
+#include <hip/hip_runtime.h>
+#include "../kernel_params.h"
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef unsigned long long u64;
+typedef u32 u32x4 __attribute__((ext_vector_type(4)));
+
+/* 16-byte weight load marked non-temporal: weights are read once per chunk, so they should not
+ * displace activations and caches from L2 / MALL. */
+__device__ __forceinline__ uint4 ld_nt16(const u16 *p) {
+    const u32x4 v = __builtin_nontemporal_load((const u32x4 *)p);
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+/* bf16 bits -> f32: the upper half of the f32 pattern (exact). */
+__device__ __forceinline__ float bf2f(u32 bits16) { return __uint_as_float(bits16 << 16); }
+__device__ __forceinline__ float bf_lo(u32 pair) { return __uint_as_float(pair << 16); }
+__device__ __forceinline__ float bf_hi(u32 pair) { return __uint_as_float(pair & 0xffff0000u); }
+
+/* f32 -> bf16 bits, round to nearest even (finite inputs). */
+__device__ __forceinline__ u32 f2bf(float f) {
+    u32 u = __float_as_uint(f);
+    return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+}
+
+/* The reference's activation forms (src/kernels.metal:6-7): a division, IEEE expf. */
+__device__ __forceinline__ float sigmoid_f(float v) { return 1.0f / (1.0f + expf(-v)); }
+__device__ __forceinline__ float silu_f(float v) { return v / (1.0f + expf(-v)); }
+
+/* Butterfly sum over the 64 lanes of a wavefront; every lane ends with the same total. */
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
+/* Dot of 8 f32 activations with 8 bf16 weights packed in a uint4, summed in index order. */
+__device__ __forceinline__ float dot8(const float *a, uint4 w, float acc) {
+    acc += a[0] * bf_lo(w.x);
+    acc += a[1] * bf_hi(w.x);
+    acc += a[2] * bf_lo(w.y);
+    acc += a[3] * bf_hi(w.y);
+    acc += a[4] * bf_lo(w.z);
+    acc += a[5] * bf_hi(w.z);
+    acc += a[6] * bf_lo(w.w);
+    acc += a[7] * bf_hi(w.w);
+    return acc;
+}
+
+/* GEMM epilogue of one output element (reference src/kernels.metal:106-116). */
+__device__ __forceinline__ void epi_store(const NkGemmArgs &a, u32 m, u32 n, float s) {
+    float v = s + (a.bias ? a.bias[n] : 0.0f);
+    if (a.act == NK_ACT_SILU) v = silu_f(v);
+    else if (a.act == NK_ACT_RELU) v = fmaxf(v, 0.0f);
+    v *= a.alpha;
+    const u32 row = a.crow ? (u32)a.crow[m] : m;
+    float *c = a.C + (u64)row * a.ldc + n;
+    *c = a.accumulate ? (*c + v) : v;
+}
+
+/* GLU epilogue: output column j pairs weight rows j and j + N/2 (src/kernels.metal:96-104). */
+__device__ __forceinline__ void epi_store_glu(const NkGemmArgs &a, u32 m, u32 j, float sa, float sb) {
+    const float va = sa + (a.bias ? a.bias[j] : 0.0f);
+    const float vb = sb + (a.bias ? a.bias[j + a.N / 2] : 0.0f);
+    const float v = va * sigmoid_f(vb) * a.alpha;
+    const u32 row = a.crow ? (u32)a.crow[m] : m;
+    float *c = a.C + (u64)row * a.ldc + j;
+    *c = a.accumulate ? (*c + v) : v;
+}
+
+/* Split one f32 into bf16 hi + bf16 lo so that hi + lo carries 16 significant bits. */
+__device__ __forceinline__ void split_bf16(float v, u32 &hi, u32 &lo) {
+    hi = f2bf(v);
+    lo = f2bf(v - __uint_as_float(hi << 16));
+}
+
+__device__ __forceinline__ bf16x8 as_bf16x8(uint4 v) {
+    union { uint4 u; bf16x8 b; } c;
+    c.u = v;
+    return c.b;
+}
+
+__device__ __forceinline__ floatx4 mfma_bf16(uint4 a, uint4 b, floatx4 acc) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a), as_bf16x8(b), acc, 0, 0, 0);
+}
+
+#endif

@@ -1,0 +1,303 @@
+"""ctypes binding of libnemoasr_hip.so for tests, the benchmark and smoke checks.
+
+Exposes the public API (include/nemoasr.h), the test hooks (include/nemoasr_debug.h), the
+kernel-level C ABI (include/nemo_kernels.h) and the exported host helpers
+(include/nemoasr_host.h).  Loading the library needs no GPU; creating a session or a device
+context does, and fails loudly without one — there is no CPU fallback.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libnemoasr_hip.so")
+
+_f32p = C.POINTER(C.c_float)
+_i32p = C.POINTER(C.c_int)
+_u16p = C.POINTER(C.c_uint16)
+_vp = C.c_void_p
+_u32 = C.c_uint32
+
+_lib = None
+
+# exported entry points: name -> (restype, argtypes)
+API = {
+    # include/nemoasr.h
+    "nemoasr_default_model_dir": (C.c_int, [C.c_char_p, C.c_size_t]),
+    "nemoasr_open": (_vp, [C.c_char_p, C.c_char_p, C.c_int, C.c_int, C.c_char_p, C.c_size_t]),
+    "nemoasr_close": (None, [_vp]),
+    "nemoasr_feed": (_vp, [_vp, _f32p, C.c_size_t, C.c_int, C.c_char_p, C.c_size_t]),
+    "nemoasr_free": (None, [_vp]),
+    "nemoasr_reset": (C.c_int, [_vp, C.c_char_p, C.c_int, C.c_char_p, C.c_size_t]),
+    "nemoasr_prepare_latency": (C.c_int, [_vp, C.c_int, C.c_char_p, C.c_size_t]),
+    "nemoasr_load_ms": (C.c_double, [_vp]),
+    "nemoasr_gpu_name": (C.c_char_p, [_vp]),
+    "nemoasr_latency_ms": (C.c_int, [_vp]),
+    "nemoasr_stats": (None, [_vp, _vp]),
+    # include/nemoasr_debug.h
+    "nemoasr_debug_feed_mel": (C.c_int, [_vp, _f32p, C.c_size_t, C.c_int, C.c_char_p, C.c_size_t]),
+    "nemoasr_debug_tokens": (_i32p, [_vp, C.POINTER(C.c_size_t)]),
+    "nemoasr_debug_set_dump": (None, [_vp, C.c_int]),
+    "nemoasr_debug_frames": (C.c_size_t, [_vp]),
+    "nemoasr_debug_dump_layers": (_f32p, [_vp]),
+    "nemoasr_debug_dump_prompted": (_f32p, [_vp]),
+    "nemoasr_debug_dump_joint_enc": (_f32p, [_vp]),
+    "nemoasr_debug_use_graphs": (None, [_vp, C.c_int]),
+    "nemoasr_debug_joint_steps": (C.c_size_t, [_vp]),
+    "nemoasr_debug_encoder_gpu_ms": (C.c_double, [_vp]),
+    "nemoasr_debug_chunk_ms": (C.POINTER(C.c_double), [_vp, C.POINTER(C.c_size_t)]),
+    "nemoasr_debug_time_kernel": (C.c_int, [_vp, C.c_char_p, C.c_int]),
+    "nemoasr_debug_kernel_ms": (C.c_int, [_vp, C.POINTER(C.c_double), C.POINTER(C.c_int), C.POINTER(C.c_double)]),
+    "nemoasr_debug_weight_bytes": (C.c_size_t, [_vp]),
+    "nemoasr_debug_launches": (C.c_uint64, [_vp]),
+    # include/nemo_kernels.h
+    "gpu_create": (_vp, [C.c_char_p, C.c_size_t]),
+    "gpu_destroy": (None, [_vp]),
+    "gpu_device_name": (C.c_char_p, [_vp]),
+    "gpu_buf_alloc": (_vp, [_vp, C.c_size_t]),
+    "gpu_buf_free": (None, [_vp]),
+    "gpu_buf_dptr": (_vp, [_vp]),
+    "gpu_buf_len": (C.c_size_t, [_vp]),
+    "gpu_upload": (C.c_int, [_vp, _vp, _vp, C.c_size_t]),
+    "gpu_download": (C.c_int, [_vp, _vp, _vp, C.c_size_t]),
+    "gpu_begin": (C.c_int, [_vp]),
+    "gpu_end": (C.c_int, [_vp, C.c_char_p, C.c_size_t]),
+    "gpu_last_ms": (C.c_double, [_vp]),
+    "gpu_last_error": (C.c_char_p, [_vp]),
+    "gpu_timing_set": (C.c_int, [_vp, C.c_char_p, C.c_int]),
+    "gpu_timing_collect": (C.c_int, [_vp, C.POINTER(C.c_double), C.POINTER(C.c_int), C.POINTER(C.c_double)]),
+    "gpu_launch_count": (C.c_uint64, [_vp]),
+    "nk_gemm": (C.c_int, [_vp, _vp, _u32, _vp, _u32, _vp, _vp, _u32, _u32, _u32, _u32, C.c_int, C.c_int, C.c_float]),
+    "nk_gemm_rows": (C.c_int, [_vp, _vp, _u32, _vp, _u32, _vp, _vp, _u32, _vp, _u32, _u32, _u32, C.c_int, C.c_int,
+                               C.c_float]),
+    "nk_gemm_force": (C.c_int, [C.c_int]),
+    "nk_gemm_kernel_name": (C.c_char_p, [_u32, _u32, _u32, C.c_int]),
+    "nk_layernorm": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _u32, _u32, C.c_float]),
+    "nk_layernorm2": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32, C.c_float]),
+    "nk_attention_rel": (C.c_int, [_vp, _vp, _u32, _vp, _vp, _u32, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32,
+                                   _u32, C.c_float]),
+    "nk_attention_rel_desc": (C.c_int, [_vp, _vp, _u32, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32,
+                                        C.c_float]),
+    "nk_dwconv_ln_silu": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, C.c_float]),
+    "nk_dwconv_ln_silu_desc": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, C.c_float]),
+    "nk_conv2d_c1_s2_relu": (C.c_int, [_vp, _vp, _vp, _vp, _vp] + [_u32] * 5),
+    "nk_dwconv2d_s2": (C.c_int, [_vp, _vp, _vp, _vp, _vp] + [_u32] * 5),
+    "nk_flatten_cf": (C.c_int, [_vp, _vp, _vp, _u32, _u32, _u32]),
+    "nk_copy": (C.c_int, [_vp, _vp, _vp, _u32]),
+    "nk_copy2d": (C.c_int, [_vp, _vp, _u32, _vp, _u32, _u32, _u32]),
+    "nk_fill": (C.c_int, [_vp, _vp, _u32, C.c_float]),
+    "nk_compact": (C.c_int, [_vp, _vp, C.c_uint64, _u32, _u32, _u32, _u32, _u32]),
+    "nk_lstm_cell": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _u32]),
+    "nk_joint_argmax": (C.c_int, [_vp, _vp, _u32, _u32, _u32, _vp, _vp, _vp, _u32, _u32, _vp, _vp, _vp]),
+    # include/nemoasr_host.h
+    "melfe_create": (_vp, []),
+    "melfe_destroy": (None, [_vp]),
+    "melfe_push": (None, [_vp, _f32p, C.c_size_t, C.c_int, C.POINTER(_f32p), C.POINTER(C.c_size_t)]),
+    "melfe_samples": (C.c_size_t, [_vp]),
+    "melfe_frames": (C.c_size_t, [_vp]),
+    "rsmp_create": (_vp, [C.c_int, C.c_int]),
+    "rsmp_destroy": (None, [_vp]),
+    "rsmp_process": (C.c_size_t, [_vp, _f32p, C.c_size_t, _f32p, C.c_size_t]),
+    "rsmp_flush": (C.c_size_t, [_vp, _f32p, C.c_size_t]),
+    "nemo_enc_plan": (C.c_int, [_i32p, C.c_size_t, C.c_size_t, C.c_size_t, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
+                                C.c_int, _i32p]),
+    "nemo_piece_text": (C.c_int, [C.c_char_p, C.c_size_t, C.c_char_p, C.c_size_t]),
+}
+
+
+def lib() -> C.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is missing: build it with __graft_entry__.build() or make -C nemo-c_amd")
+        L = C.CDLL(LIB_PATH)
+        for name, (res, args) in API.items():
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = L
+    return _lib
+
+
+def fp(a: np.ndarray):
+    return a.ctypes.data_as(_f32p)
+
+
+class Gpu:
+    """Device context of the kernel-level C ABI (one stream)."""
+
+    def __init__(self):
+        err = C.create_string_buffer(512)
+        self.h = lib().gpu_create(err, 512)
+        if not self.h:
+            raise RuntimeError("gpu_create: " + err.value.decode())
+        self._bufs = []
+
+    @property
+    def name(self) -> str:
+        return lib().gpu_device_name(self.h).decode()
+
+    def alloc(self, nbytes: int) -> "Buf":
+        b = lib().gpu_buf_alloc(self.h, max(int(nbytes), 1))
+        if not b:
+            raise MemoryError(nbytes)
+        buf = Buf(self, b, int(nbytes))
+        self._bufs.append(buf)
+        return buf
+
+    def put(self, a: np.ndarray) -> "Buf":
+        a = np.ascontiguousarray(a)
+        b = self.alloc(a.nbytes)
+        b.write(a)
+        return b
+
+    def begin(self):
+        if lib().gpu_begin(self.h):
+            raise RuntimeError(lib().gpu_last_error(self.h).decode())
+
+    def end(self) -> float:
+        err = C.create_string_buffer(512)
+        if lib().gpu_end(self.h, err, 512):
+            raise RuntimeError(err.value.decode())
+        return lib().gpu_last_ms(self.h)
+
+    def check(self, rc: int):
+        if rc:
+            raise RuntimeError(lib().gpu_last_error(self.h).decode())
+
+    def close(self):
+        for b in self._bufs:
+            b.free()
+        self._bufs = []
+        if self.h:
+            lib().gpu_destroy(self.h)
+            self.h = None
+
+
+class Buf:
+    def __init__(self, gpu: Gpu, h, nbytes: int):
+        self.gpu, self.h, self.nbytes = gpu, h, nbytes
+
+    @property
+    def ptr(self) -> int:
+        return lib().gpu_buf_dptr(self.h)
+
+    def at(self, byte_offset: int) -> int:
+        return self.ptr + int(byte_offset)
+
+    def write(self, a: np.ndarray, byte_offset: int = 0):
+        a = np.ascontiguousarray(a)
+        assert byte_offset + a.nbytes <= self.nbytes
+        self.gpu.check(lib().gpu_upload(self.gpu.h, self.at(byte_offset), a.ctypes.data, a.nbytes))
+
+    def read(self, shape, dtype=np.float32, byte_offset: int = 0) -> np.ndarray:
+        out = np.empty(shape, dtype=dtype)
+        assert byte_offset + out.nbytes <= self.nbytes
+        self.gpu.check(lib().gpu_download(self.gpu.h, out.ctypes.data, self.at(byte_offset), out.nbytes))
+        return out
+
+    def free(self):
+        if self.h:
+            lib().gpu_buf_free(self.h)
+            self.h = None
+
+
+class Session:
+    """One streaming session through the public C API (include/nemoasr.h)."""
+
+    def __init__(self, model_dir: str, language: str = "en-US", latency_ms: int = 560, input_rate: int = 16000):
+        err = C.create_string_buffer(1024)
+        self.h = lib().nemoasr_open(model_dir.encode(), language.encode(), latency_ms, input_rate, err, 1024)
+        if not self.h:
+            raise RuntimeError("nemoasr_open: " + err.value.decode())
+
+    def feed(self, audio: np.ndarray, final: bool = False) -> str:
+        a = np.ascontiguousarray(audio, dtype=np.float32)
+        err = C.create_string_buffer(1024)
+        p = lib().nemoasr_feed(self.h, fp(a), a.size, int(final), err, 1024)
+        if err.value:
+            raise RuntimeError("nemoasr_feed: " + err.value.decode())
+        if not p:
+            return ""
+        s = C.cast(p, C.c_char_p).value.decode("utf-8", "replace")
+        lib().nemoasr_free(p)
+        return s
+
+    def feed_mel(self, mel: np.ndarray, final: bool = False) -> int:
+        m = np.ascontiguousarray(mel, dtype=np.float32).reshape(-1, 128)
+        err = C.create_string_buffer(1024)
+        n = lib().nemoasr_debug_feed_mel(self.h, fp(m), m.shape[0], int(final), err, 1024)
+        if n < 0:
+            raise RuntimeError("feed_mel: " + err.value.decode())
+        return n
+
+    def reset(self, language: str | None, latency_ms: int):
+        err = C.create_string_buffer(1024)
+        if lib().nemoasr_reset(self.h, language.encode() if language else None, latency_ms, err, 1024):
+            raise RuntimeError("nemoasr_reset: " + err.value.decode())
+
+    def tokens(self) -> list[int]:
+        n = C.c_size_t()
+        p = lib().nemoasr_debug_tokens(self.h, C.byref(n))
+        return np.ctypeslib.as_array(p, shape=(n.value,)).tolist() if n.value else []
+
+    def set_dump(self, on: bool):
+        lib().nemoasr_debug_set_dump(self.h, int(on))
+
+    def use_graphs(self, on: bool):
+        lib().nemoasr_debug_use_graphs(self.h, int(on))
+
+    def dumps(self, n_layers: int, d_model: int, joint_hidden: int):
+        F = lib().nemoasr_debug_frames(self.h)
+        if F == 0:
+            return (np.zeros((0, n_layers, d_model), np.float32), np.zeros((0, d_model), np.float32),
+                    np.zeros((0, joint_hidden), np.float32))
+        lay = np.ctypeslib.as_array(lib().nemoasr_debug_dump_layers(self.h), shape=(F * n_layers * d_model,))
+        pr = np.ctypeslib.as_array(lib().nemoasr_debug_dump_prompted(self.h), shape=(F * d_model,))
+        je = np.ctypeslib.as_array(lib().nemoasr_debug_dump_joint_enc(self.h), shape=(F * joint_hidden,))
+        return (lay.reshape(F, n_layers, d_model).copy(), pr.reshape(F, d_model).copy(), je.reshape(F, joint_hidden).copy())
+
+    def stats(self) -> dict:
+        class St(C.Structure):
+            _fields_ = [("audio_seconds", C.c_double), ("chunks", C.c_size_t), ("tokens", C.c_size_t),
+                        ("encoder_ms", C.c_double), ("decoder_ms", C.c_double)]
+        st = St()
+        lib().nemoasr_stats(self.h, C.byref(st))
+        return {k: getattr(st, k) for k, _ in St._fields_}
+
+    def chunk_ms(self) -> np.ndarray:
+        n = C.c_size_t()
+        p = lib().nemoasr_debug_chunk_ms(self.h, C.byref(n))
+        return np.ctypeslib.as_array(p, shape=(n.value,)).copy() if n.value else np.zeros(0)
+
+    @property
+    def joint_steps(self) -> int:
+        return lib().nemoasr_debug_joint_steps(self.h)
+
+    @property
+    def gpu_name(self) -> str:
+        return lib().nemoasr_gpu_name(self.h).decode()
+
+    @property
+    def load_ms(self) -> float:
+        return lib().nemoasr_load_ms(self.h)
+
+    def time_kernel(self, name: str | None, max_launches: int = 4096):
+        lib().nemoasr_debug_time_kernel(self.h, name.encode() if name else None, max_launches)
+
+    def kernel_ms(self):
+        """(mean ms per launch, launches, summed algorithmic bytes) of the timed kernel."""
+        ms, n, by = C.c_double(), C.c_int(), C.c_double()
+        lib().nemoasr_debug_kernel_ms(self.h, C.byref(ms), C.byref(n), C.byref(by))
+        return ms.value, n.value, by.value
+
+    def close(self):
+        if self.h:
+            lib().nemoasr_close(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()

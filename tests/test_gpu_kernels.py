@@ -1,0 +1,306 @@
+"""Per-kernel parity of the gfx950 kernels against the oracle, at the model's real shapes.
+
+Each test uploads seeded inputs, launches through the kernel-level C ABI
+(include/nemo_kernels.h) and compares with the oracle's CPU restatement on the same inputs.
+Tolerances: relative to the largest reference magnitude (tools/compare.py:30-32 style); the GPU
+sums in a different order than the oracle (and the MFMA kernels split activations into bf16
+hi + lo), so results agree to f32 rounding, not bit for bit.  Index outputs (argmax) are exact.
+"""
+import numpy as np
+import pytest
+
+import oracle
+from conftest import rel_err
+
+pytestmark = pytest.mark.gpu
+
+GEMM_TOL = 2e-5
+
+
+def _w(rng, n, k, scale=None):
+    s = scale if scale is not None else 1.0 / np.sqrt(k)
+    return oracle.f32_to_bf16(rng.standard_normal((n, k)).astype(np.float32) * s)
+
+
+def run_gemm(gpu, A, W, bias, act, acc, alpha, C0=None, ldw=None, K=None, kind=0, rows=None, ldc=None):
+    import nemoasr
+
+    L = nemoasr.lib()
+    M = A.shape[0]
+    N = W.shape[0]
+    K = A.shape[1] if K is None else K
+    ldw = W.shape[1] if ldw is None else ldw
+    nout = N // 2 if act == 3 else N
+    ldc = nout if ldc is None else ldc
+    crows = M if rows is None else int(max(rows)) + 1
+    C0 = np.zeros((crows, ldc), np.float32) if C0 is None else C0
+    dA, dW, dC = gpu.put(A), gpu.put(W), gpu.put(C0)
+    dB = gpu.put(bias) if bias is not None else None
+    dR = gpu.put(np.asarray(rows, np.int32)) if rows is not None else None
+    prev = L.nk_gemm_force(kind)
+    try:
+        gpu.begin()
+        gpu.check(L.nk_gemm_rows(gpu.h, dA.ptr, A.shape[1], dW.ptr, ldw, dB.ptr if dB else None, dC.ptr, ldc,
+                                 dR.ptr if dR else None, M, N, K, act, int(acc), alpha))
+        gpu.end()
+    finally:
+        L.nk_gemm_force(prev)
+    out = dC.read((crows, ldc))
+    for b in (dA, dW, dC, dB, dR):
+        if b is not None:
+            b.free()
+    return out
+
+
+# (N, K, act, accumulate, alpha, bias, ldw) at the model's shapes (src/encoder.c:150-223, decoder.c:381-388)
+SHAPES = [
+    (4096, 1024, 1, 0, 1.0, False, None),   # FF up + SiLU
+    (1024, 4096, 0, 1, 0.5, False, None),   # FF down, half-step residual
+    (3072, 1024, 0, 0, 1.0, False, None),   # fused QKV
+    (2048, 1024, 3, 0, 1.0, False, None),   # pointwise conv 1 + GLU
+    (1024, 1024, 0, 1, 1.0, False, None),   # out proj / pointwise conv 2
+    (2048, 1024, 2, 0, 1.0, True, 1152),    # prompt W0 (ldw 1152) + ReLU
+    (1024, 2048, 0, 0, 1.0, True, None),    # prompt W2
+    (640, 1024, 0, 0, 1.0, True, None),     # joint.enc
+    (1024, 4352, 0, 0, 1.0, True, None),    # pre-encode out
+]
+
+
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 5, 7, 10, 14, 16])
+@pytest.mark.parametrize("shape", SHAPES, ids=lambda s: f"{s[0]}x{s[1]}a{s[2]}")
+def test_gemm_few_rows(gpu, M, shape):
+    N, K, act, acc, alpha, has_bias, ldw = shape
+    rng = np.random.default_rng([M, N, K, act])
+    ldw_ = ldw or K
+    W = _w(rng, N, ldw_)
+    A = rng.standard_normal((M, K)).astype(np.float32)
+    bias = (0.1 * rng.standard_normal(N)).astype(np.float32) if has_bias else None
+    nout = N // 2 if act == 3 else N
+    C0 = rng.standard_normal((M, nout)).astype(np.float32) if acc else None
+    got = run_gemm(gpu, A, W, bias, act, acc, alpha, C0=C0, ldw=ldw_, K=K)
+    ref = oracle.gemm(A, W, bias, act, acc, alpha, C0=C0, ldw=ldw_, K=K)
+    assert rel_err(got, ref) < GEMM_TOL, (M, shape)
+
+
+@pytest.mark.parametrize("M,N,K,act", [(231, 256, 256, 2), (627, 256, 256, 2), (1089, 256, 256, 2),
+                                       (68, 256, 256, 2), (170, 256, 256, 2), (289, 256, 256, 2),
+                                       (17, 1024, 4352, 0), (143, 1024, 1024, 0), (448, 4096, 1024, 1)])
+def test_gemm_many_rows(gpu, M, N, K, act):
+    rng = np.random.default_rng([M, N, K])
+    W = _w(rng, N, K)
+    A = np.abs(rng.standard_normal((M, K))).astype(np.float32)
+    bias = (0.1 * rng.standard_normal(N)).astype(np.float32)
+    got = run_gemm(gpu, A, W, bias, act, False, 1.0)
+    ref = oracle.gemm(A, W, bias, act, False, 1.0)
+    assert rel_err(got, ref) < GEMM_TOL
+
+
+@pytest.mark.parametrize("kind,M", [(1, 1), (1, 4), (2, 1), (2, 4), (2, 16), (3, 5), (3, 16)])
+def test_gemm_variants_agree(gpu, kind, M):
+    """Every kernel the policy can pick computes the same GEMM (the reference's kbench.c:196-230
+    cross-check, with a threshold)."""
+    rng = np.random.default_rng([kind, M])
+    N, K = 1024, 1024
+    W = _w(rng, N, K)
+    A = rng.standard_normal((M, K)).astype(np.float32)
+    bias = (0.1 * rng.standard_normal(N)).astype(np.float32)
+    got = run_gemm(gpu, A, W, bias, 1, False, 1.0, kind=kind)
+    ref = oracle.gemm(A, W, bias, 1, False, 1.0)
+    assert rel_err(got, ref) < GEMM_TOL
+
+
+@pytest.mark.parametrize("M", [1, 7, 14])
+def test_gemm_row_scatter(gpu, M):
+    """Output row m lands in row crow[m] (the QKV / GLU write into the cache at pos)."""
+    rng = np.random.default_rng(M)
+    W = _w(rng, 2048, 1024)
+    A = rng.standard_normal((M, 1024)).astype(np.float32)
+    rows = list(range(40, 40 + M))
+    C0 = rng.standard_normal((40 + M + 3, 1024)).astype(np.float32)
+    got = run_gemm(gpu, A, W, None, 3, False, 1.0, C0=C0.copy(), rows=rows, ldc=1024)
+    ref = oracle.gemm(A, W, None, 3, False, 1.0)
+    assert rel_err(got[40:40 + M], ref) < GEMM_TOL
+    np.testing.assert_array_equal(got[:40], C0[:40])
+    np.testing.assert_array_equal(got[40 + M:], C0[40 + M:])
+
+
+@pytest.mark.parametrize("M,D", [(1, 1024), (7, 1024), (16, 1024), (3, 256)])
+def test_layernorm_and_pair(gpu, M, D):
+    import nemoasr
+
+    L = nemoasr.lib()
+    rng = np.random.default_rng([M, D])
+    X = (3 * rng.standard_normal((M, D)) + 1).astype(np.float32)
+    g1, b1, g2, b2 = [(1 + 0.1 * rng.standard_normal(D)).astype(np.float32) if i % 2 == 0 else
+                      (0.1 * rng.standard_normal(D)).astype(np.float32) for i in range(4)]
+    dX, dY1, dY2 = gpu.put(X), gpu.alloc(X.nbytes), gpu.alloc(X.nbytes)
+    dg1, db1, dg2, db2 = gpu.put(g1), gpu.put(b1), gpu.put(g2), gpu.put(b2)
+    gpu.begin()
+    gpu.check(L.nk_layernorm2(gpu.h, dX.ptr, dg1.ptr, db1.ptr, dg2.ptr, db2.ptr, dY1.ptr, dY2.ptr, M, D, 1e-5))
+    gpu.end()
+    r1, r2 = oracle.layernorm2(X, g1, b1, g2, b2)
+    assert rel_err(dY1.read((M, D)), r1) < 1e-5
+    assert rel_err(dY2.read((M, D)), r2) < 1e-5
+    gpu.begin()
+    gpu.check(L.nk_layernorm(gpu.h, dX.ptr, dg2.ptr, db2.ptr, dY1.ptr, M, D, 1e-5))
+    gpu.end()
+    assert rel_err(dY1.read((M, D)), oracle.layernorm(X, g2, b2)) < 1e-5
+
+
+@pytest.mark.parametrize("c,cache", [(1, 0), (1, 56), (7, 0), (7, 56), (14, 56), (16, 56), (7, 23)])
+def test_attention_rel(gpu, c, cache):
+    import nemoasr
+
+    lib = nemoasr.lib()
+    H, dh, D, Lmax = 8, 128, 1024, 72
+    L = cache + c
+    rng = np.random.default_rng([c, cache])
+    pos = cache + 5
+    kv = rng.standard_normal((pos + c + 2, 3 * D)).astype(np.float32)
+    P = rng.standard_normal((2 * Lmax - 1, D)).astype(np.float32)
+    bu = (0.1 * rng.standard_normal(D)).astype(np.float32)
+    bv = (0.1 * rng.standard_normal(D)).astype(np.float32)
+    Q = kv[pos:pos + c, :]
+    K = kv[pos - cache:pos + c, D:2 * D]
+    V = kv[pos - cache:pos + c, 2 * D:]
+    ref = oracle.attention_rel(Q, K, V, P, bu, bv, c, L, Lmax, H, dh)
+    dkv, dP, dbu, dbv, dO = gpu.put(kv), gpu.put(P), gpu.put(bu), gpu.put(bv), gpu.alloc(c * D * 4)
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(dh)))
+    gpu.begin()
+    row = 3 * D * 4
+    gpu.check(lib.nk_attention_rel(gpu.h, dkv.at(pos * row), 3 * D, dkv.at((pos - cache) * row + D * 4),
+                                   dkv.at((pos - cache) * row + 2 * D * 4), 3 * D, dP.ptr, dbu.ptr, dbv.ptr, dO.ptr,
+                                   c, L, Lmax, H, dh, D, scale))
+    gpu.end()
+    assert rel_err(dO.read((c, D)), ref) < 1e-5
+    desc = np.zeros(20, np.int32)
+    desc[:4] = [pos, cache, L, c]
+    ddesc = gpu.put(desc)
+    gpu.begin()
+    gpu.check(lib.nk_attention_rel_desc(gpu.h, dkv.ptr, 3 * D, ddesc.ptr, dP.ptr, dbu.ptr, dbv.ptr, dO.ptr, c, Lmax,
+                                        H, dh, D, scale))
+    gpu.end()
+    assert rel_err(dO.read((c, D)), ref) < 1e-5
+
+
+@pytest.mark.parametrize("c", [1, 7, 14])
+def test_dwconv_ln_silu(gpu, c):
+    import nemoasr
+
+    lib = nemoasr.lib()
+    D, taps = 1024, 9
+    rng = np.random.default_rng(c)
+    din = rng.standard_normal((taps - 1 + c, D)).astype(np.float32)
+    W = (rng.standard_normal((D, taps)) / 3).astype(np.float32)
+    g = (1 + 0.1 * rng.standard_normal(D)).astype(np.float32)
+    b = (0.1 * rng.standard_normal(D)).astype(np.float32)
+    ref = oracle.dwconv_ln_silu(din, W, g, b, c)
+    ddin, dW, dg, db, dY = gpu.put(din), gpu.put(W), gpu.put(g), gpu.put(b), gpu.alloc(c * D * 4)
+    gpu.begin()
+    gpu.check(lib.nk_dwconv_ln_silu(gpu.h, ddin.ptr, dW.ptr, dg.ptr, db.ptr, dY.ptr, c, D, taps, 1e-5))
+    gpu.end()
+    assert rel_err(dY.read((c, D)), ref) < 1e-5
+
+
+@pytest.mark.parametrize("nwin", [8, 24, 72, 128, 33])
+def test_subsampling_convs(gpu, nwin):
+    import nemoasr
+
+    lib = nemoasr.lib()
+    rng = np.random.default_rng(nwin)
+    F, C = 128, 256
+    X = rng.standard_normal((nwin, F)).astype(np.float32)
+    W0 = (rng.standard_normal((C, 9)) / 3).astype(np.float32)
+    b0 = (0.1 * rng.standard_normal(C)).astype(np.float32)
+    W2 = (rng.standard_normal((C, 9)) / 3).astype(np.float32)
+    b2 = (0.1 * rng.standard_normal(C)).astype(np.float32)
+    y0 = oracle.conv2d_c1_s2_relu(X, W0, b0)
+    y1 = oracle.dwconv2d_s2(y0, W2, b2)
+    fl = oracle.flatten_cf(y1)
+    T1, F1 = y0.shape[:2]
+    T2, F2 = y1.shape[:2]
+    dX, dW0, db0, dW2, db2 = gpu.put(X), gpu.put(W0), gpu.put(b0), gpu.put(W2), gpu.put(b2)
+    dy0, dy1, dfl = gpu.alloc(y0.nbytes), gpu.alloc(y1.nbytes), gpu.alloc(fl.nbytes)
+    gpu.begin()
+    gpu.check(lib.nk_conv2d_c1_s2_relu(gpu.h, dX.ptr, dW0.ptr, db0.ptr, dy0.ptr, nwin, F, T1, F1, C))
+    gpu.check(lib.nk_dwconv2d_s2(gpu.h, dy0.ptr, dW2.ptr, db2.ptr, dy1.ptr, T1, F1, T2, F2, C))
+    gpu.check(lib.nk_flatten_cf(gpu.h, dy1.ptr, dfl.ptr, T2, F2, C))
+    gpu.end()
+    assert rel_err(dy0.read(y0.shape), y0) < 1e-6
+    assert rel_err(dy1.read(y1.shape), y1) < 1e-6
+    np.testing.assert_array_equal(dfl.read(fl.shape), oracle.flatten_cf(dy1.read(y1.shape)))
+
+
+def test_lstm_cell(gpu):
+    import nemoasr
+
+    lib = nemoasr.lib()
+    H = 640
+    rng = np.random.default_rng(7)
+    gates = (2 * rng.standard_normal(4 * H)).astype(np.float32)
+    c_in = rng.standard_normal(H).astype(np.float32)
+    rc, rh = oracle.lstm_cell(gates, c_in)
+    dg, dc, dco, dho = gpu.put(gates), gpu.put(c_in), gpu.alloc(H * 4), gpu.alloc(H * 4)
+    gpu.begin()
+    gpu.check(lib.nk_lstm_cell(gpu.h, dg.ptr, dc.ptr, dco.ptr, dho.ptr, H))
+    gpu.end()
+    assert rel_err(dco.read(H), rc) < 1e-6
+    assert rel_err(dho.read(H), rh) < 1e-6
+
+
+@pytest.mark.parametrize("rows", [1, 5, 16])
+def test_joint_argmax(gpu, rows):
+    import nemoasr
+
+    lib = nemoasr.lib()
+    V, H = 1025, 640
+    rng = np.random.default_rng(rows)
+    W = _w(rng, V, H)
+    bias = (0.1 * rng.standard_normal(V)).astype(np.float32)
+    enc = rng.standard_normal((rows + 3, H)).astype(np.float32)
+    pred = rng.standard_normal(H).astype(np.float32)
+    dW, db, de, dp = gpu.put(W), gpu.put(bias), gpu.put(enc), gpu.put(pred)
+    pv, pi, out = gpu.alloc(16 * 256 * 4), gpu.alloc(16 * 256 * 4), gpu.alloc(32 * 4)
+    gpu.begin()
+    gpu.check(lib.nk_joint_argmax(gpu.h, de.ptr, 2, H, rows, dp.ptr, dW.ptr, db.ptr, V, H, pv.ptr, pi.ptr, out.ptr))
+    gpu.end()
+    res = out.read(2 * rows, np.int32)
+    for r in range(rows):
+        i, v, logits = oracle.joint_argmax(enc[2 + r], pred, W, bias)
+        assert res[2 * r] == i
+        assert abs(res[2 * r + 1:2 * r + 2].view(np.float32)[0] - v) <= 1e-5 * max(1.0, abs(v))
+
+
+def test_joint_argmax_tie_lowest_index(gpu):
+    """Exact ties resolve to the lowest class index (src/kernels.metal:516, :545)."""
+    import nemoasr
+
+    lib = nemoasr.lib()
+    V, H = 1025, 640
+    W = np.zeros((V, H), np.uint16)
+    bias = np.zeros(V, np.float32)
+    bias[[17, 300, 999]] = 1.0
+    enc = np.ones((1, H), np.float32)
+    pred = np.zeros(H, np.float32)
+    dW, db, de, dp = gpu.put(W), gpu.put(bias), gpu.put(enc), gpu.put(pred)
+    pv, pi, out = gpu.alloc(16 * 256 * 4), gpu.alloc(16 * 256 * 4), gpu.alloc(32 * 4)
+    gpu.begin()
+    gpu.check(lib.nk_joint_argmax(gpu.h, de.ptr, 0, H, 1, dp.ptr, dW.ptr, db.ptr, V, H, pv.ptr, pi.ptr, out.ptr))
+    gpu.end()
+    assert out.read(2, np.int32)[0] == 17
+
+
+def test_compact_rows(gpu):
+    import nemoasr
+
+    lib = nemoasr.lib()
+    nbuf, rows_total, cols = 3, 40, 96
+    rng = np.random.default_rng(3)
+    X = rng.standard_normal((nbuf, rows_total, cols)).astype(np.float32)
+    d = gpu.put(X)
+    gpu.begin()
+    gpu.check(lib.nk_compact(gpu.h, d.ptr, rows_total * cols, nbuf, 10, cols, 25, 2))
+    gpu.end()
+    Y = X.copy()
+    Y[:, 2:12] = X[:, 25:35]
+    np.testing.assert_array_equal(d.read(X.shape), Y)
