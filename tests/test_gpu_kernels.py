@@ -34,6 +34,7 @@ def run_gemm(gpu, A, W, bias, act, acc, alpha, C0=None, ldw=None, K=None, kind=0
     ldc = nout if ldc is None else ldc
     crows = M if rows is None else int(max(rows)) + 1
     C0 = np.zeros((crows, ldc), np.float32) if C0 is None else C0
+    crows = C0.shape[0]
     dA, dW, dC = gpu.put(A), gpu.put(W), gpu.put(C0)
     dB = gpu.put(bias) if bias is not None else None
     dR = gpu.put(np.asarray(rows, np.int32)) if rows is not None else None
