@@ -62,7 +62,7 @@ static int parse_cfg(model_t *m, char *err, size_t errlen) {
     g->att_right_default = (int)jn_num(jn_at(jn_get(c, "default_att_context_size"), 1), 13);
     if (g->pred_layers != 2) { snprintf(err, errlen, "only 2 LSTM layers supported"); return -1; }
     if (g->head_dim != 128 || g->joint_hidden > NK_JOINT_MAX_H || g->conv_kernel != 9 || g->subsampling != 8 ||
-        g->d_model % 32 || g->d_model > NK_LN_THREADS * NK_LN_MAX_PER || g->prompt_hidden % 32 || g->sub_channels % 32 ||
+        g->d_model % 32 || g->d_model > NK_ROW_MAX || g->prompt_hidden % 32 || g->sub_channels % 32 ||
         g->pred_hidden % 8 || g->joint_hidden % 8 || g->num_classes > NK_JOINT_GROUPS * NK_JOINT_WAVES * 1024) {
         snprintf(err, errlen, "unexpected architecture dims");
         return -1;

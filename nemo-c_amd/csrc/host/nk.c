@@ -96,7 +96,7 @@ int nk_gemm(gpu_t *g, const float *A, uint32_t lda, const uint16_t *W, uint32_t 
 int nk_layernorm2(gpu_t *g, const float *X, const float *g1, const float *b1, const float *g2, const float *b2,
                   float *Y1, float *Y2, uint32_t M, uint32_t D, float eps) {
     if (!M) return 0;
-    if (D > NK_LN_THREADS * NK_LN_MAX_PER) return bad(g, "layernorm: D too large");
+    if (D > NK_ROW_MAX || D % 4) return bad(g, "layernorm: D must be a multiple of 4, at most 4096");
     NkLnArgs a = { X, g1, b1, g2, b2, Y1, Y2, M, D, eps, 0 };
     return gpu_launch(g, "layernorm", &a, sizeof a, M, 1, 1, NK_LN_THREADS, 1, 1);
 }
@@ -113,23 +113,26 @@ int nk_attention_rel(gpu_t *g, const float *Q, uint32_t ldq, const float *K, con
     if (dh != 128 || H * dh != D) return bad(g, "attention: head_dim must be 128");
     if (L > NK_ATT_MAX_L || L > Lmax || c > L || c > Lmax) return bad(g, "attention: window exceeds the table");
     if ((uintptr_t)K % 8 || (uintptr_t)P % 8 || ldk % 2) return bad(g, "attention: K/P must be 8-byte aligned");
+    if ((uintptr_t)Q % 16 || (uintptr_t)K % 16 || (uintptr_t)V % 16 || ldq % 4 || ldk % 4)
+        return bad(g, "attention: Q/K/V must be 16-byte aligned");
     NkAttnArgs a = { Q, K, V, P, bias_u, bias_v, O, NULL, c, L, Lmax, H, dh, D, ldq, ldk, scale, 0 };
-    return gpu_launch(g, "attention_rel", &a, sizeof a, H, c, 1, 128, 1, 1);
+    return gpu_launch(g, "attention_rel", &a, sizeof a, H, c, 1, 256, 1, 1);
 }
 
 int nk_attention_rel_desc(gpu_t *g, const float *kv, uint32_t ld, const int *desc, const float *P, const float *bias_u,
                           const float *bias_v, float *O, uint32_t c, uint32_t Lmax, uint32_t H, uint32_t dh, uint32_t D,
                           float scale) {
     if (!c) return 0;
-    if (dh != 128 || H * dh != D || c > Lmax) return bad(g, "attention: head_dim must be 128");
+    if (dh != 128 || H * dh != D || c > Lmax || Lmax > NK_ATT_MAX_L) return bad(g, "attention: head_dim must be 128");
+    if ((uintptr_t)kv % 16 || ld % 4) return bad(g, "attention: cache must be 16-byte aligned");
     NkAttnArgs a = { kv, kv + D, kv + 2 * D, P, bias_u, bias_v, O, desc, c, 0, Lmax, H, dh, D, ld, ld, scale, 0 };
-    return gpu_launch(g, "attention_rel", &a, sizeof a, H, c, 1, 128, 1, 1);
+    return gpu_launch(g, "attention_rel", &a, sizeof a, H, c, 1, 256, 1, 1);
 }
 
 int nk_dwconv_ln_silu(gpu_t *g, const float *din, const float *W, const float *gamma, const float *beta, float *Y,
                       uint32_t c, uint32_t D, uint32_t taps, float eps) {
     if (!c) return 0;
-    if (D > NK_LN_THREADS * NK_LN_MAX_PER) return bad(g, "dwconv: D too large");
+    if (D > NK_ROW_MAX || D % 4 || taps != NK_CONV_TAPS) return bad(g, "dwconv: 9 taps, D a multiple of 4, at most 4096");
     NkDwArgs a = { din, W, gamma, beta, Y, NULL, c, D, taps, eps };
     return gpu_launch(g, "dwconv_ln_silu", &a, sizeof a, c, 1, 1, NK_LN_THREADS, 1, 1);
 }
@@ -137,7 +140,7 @@ int nk_dwconv_ln_silu(gpu_t *g, const float *din, const float *W, const float *g
 int nk_dwconv_ln_silu_desc(gpu_t *g, const float *din_base, const int *desc, const float *W, const float *gamma,
                            const float *beta, float *Y, uint32_t c, uint32_t D, uint32_t taps, float eps) {
     if (!c) return 0;
-    if (D > NK_LN_THREADS * NK_LN_MAX_PER) return bad(g, "dwconv: D too large");
+    if (D > NK_ROW_MAX || D % 4 || taps != NK_CONV_TAPS) return bad(g, "dwconv: 9 taps, D a multiple of 4, at most 4096");
     NkDwArgs a = { din_base, W, gamma, beta, Y, desc, c, D, taps, eps };
     return gpu_launch(g, "dwconv_ln_silu", &a, sizeof a, c, 1, 1, NK_LN_THREADS, 1, 1);
 }

@@ -28,7 +28,8 @@ typedef uint16_t u16;
 #define NK_JOINT_MAX_H 1024     /* joint hidden size limit (LDS staging)                           */
 #define NK_CACHE_EPOCH_CHUNKS 8 /* K/V and conv caches compacted once per this many chunks         */
 #define NK_LN_THREADS 256
-#define NK_LN_MAX_PER 8         /* values per thread held by the LayerNorm kernels: D <= 2048      */
+#define NK_ROW_MAX 4096         /* row width limit of the per-row kernels (4 float4 per thread)    */
+#define NK_CONV_TAPS 9          /* causal depthwise conv kernel size                               */
 #define NK_FR_MAX_KC 1024       /* few-row MFMA GEMM: K columns of A staged per workgroup          */
 
 enum { NK_ACT_NONE = 0, NK_ACT_SILU = 1, NK_ACT_RELU = 2, NK_ACT_GLU = 3 };

@@ -1,3 +1,4 @@
 /* Single translation unit for the gfx950 code object loaded by the host (hipModuleLoadData). */
 #include "nk_gemm.hip"
+#include "nk_seq.hip"
 #include "nk_ops.hip"

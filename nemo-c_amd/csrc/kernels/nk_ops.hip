@@ -1,137 +1,7 @@
-/* Non-GEMM kernels of the streaming chunk for gfx950: LayerNorm (single and paired),
- * relative-position attention, causal depthwise conv + LN + SiLU, the subsampling convs, and the
+/* Streaming-chunk kernels for gfx950 besides the GEMMs and the per-row kernels of nk_seq.hip:
+ * the subsampling convs, copies, cache compaction, and the
  * RNNT decoder's LSTM cell and joint argmax.  Each states the reference kernel it replaces. */
 #include "nk_common.h"
-
-/* Block-wide sum over 256 threads (4 wavefronts), combined in wavefront order. */
-__device__ __forceinline__ float block_sum256(float v, float *red) {
-    v = wave_sum(v);
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    __syncthreads();
-    if (lane == 0) red[wave] = v;
-    __syncthreads();
-    return ((red[0] + red[1]) + red[2]) + red[3];
-}
-
-/* LayerNorm of one row held in registers (reference src/kernels.metal:257-288):
- * mean = sum/D, var = sum((x-mean)^2)/D, inv = 1/sqrt(var + eps), y = (x-mean)*inv*g + b. */
-__device__ __forceinline__ void ln_regs(float *v, int per, u32 D, float eps, const float *g, const float *b, float *red) {
-    const u32 tid = threadIdx.x;
-    float s = 0.0f;
-    for (int k = 0; k < per; ++k)
-        if (tid + k * NK_LN_THREADS < D) s += v[k];
-    const float mean = block_sum256(s, red) / (float)D;
-    float q = 0.0f;
-    for (int k = 0; k < per; ++k)
-        if (tid + k * NK_LN_THREADS < D) { const float d = v[k] - mean; q += d * d; }
-    const float var = block_sum256(q, red);
-    const float inv = 1.0f / sqrtf(var / (float)D + eps);
-    for (int k = 0; k < per; ++k) {
-        const u32 i = tid + k * NK_LN_THREADS;
-        if (i < D) v[k] = (v[k] - mean) * inv * g[i] + b[i];
-    }
-}
-
-/* One workgroup per row. Y1 = LN(X; g1,b1); with Y2 set, also Y2 = LN(Y1; g2,b2)
- * (the paired norm_out + next norm_feed_forward1 of reference src/kernels.metal:210-255). */
-extern "C" __global__ __launch_bounds__(256) void layernorm(const NkLnArgs a) {
-    __shared__ float red[4];
-    const u32 row = blockIdx.x, tid = threadIdx.x;
-    const int per = (int)((a.D + NK_LN_THREADS - 1) / NK_LN_THREADS);
-    const float *x = a.X + (u64)row * a.D;
-    float v[NK_LN_MAX_PER];
-    for (int k = 0; k < per; ++k) {
-        const u32 i = tid + k * NK_LN_THREADS;
-        v[k] = i < a.D ? x[i] : 0.0f;
-    }
-    ln_regs(v, per, a.D, a.eps, a.g1, a.b1, red);
-    for (int k = 0; k < per; ++k) {
-        const u32 i = tid + k * NK_LN_THREADS;
-        if (i < a.D) a.Y1[(u64)row * a.D + i] = v[k];
-    }
-    if (!a.Y2) return;
-    ln_regs(v, per, a.D, a.eps, a.g2, a.b2, red);
-    for (int k = 0; k < per; ++k) {
-        const u32 i = tid + k * NK_LN_THREADS;
-        if (i < a.D) a.Y2[(u64)row * a.D + i] = v[k];
-    }
-}
-
-/* Relative-position attention, one workgroup (2 wavefronts, dh = 128 threads) per (head, query):
- * reference src/kernels.metal:290-348.  Scores: each wavefront takes every other key and its 64
- * lanes cover two head dims each; softmax over the whole window (no mask inside the chunk);
- * output: thread d sums the softmax-weighted V column d. */
-extern "C" __global__ __launch_bounds__(128) void attention_rel(const NkAttnArgs a) {
-    __shared__ float qu[128], qv[128], s[NK_ATT_MAX_L], red[2];
-    const u32 h = blockIdx.x, i = blockIdx.y, tid = threadIdx.x;
-    const int lane = tid & 63, wave = tid >> 6;
-    const u32 off = h * a.dh;
-    const float *Q = a.Q, *Kp = a.K, *Vp = a.V;
-    u32 L = a.L;
-    if (a.desc) {
-        const u32 pos = (u32)a.desc[NK_DESC_POS], cl = (u32)a.desc[NK_DESC_CACHE];
-        Q += (u64)pos * a.ldq;
-        Kp += (u64)(pos - cl) * a.ldk;
-        Vp += (u64)(pos - cl) * a.ldk;
-        L = cl + a.c;
-    }
-    {
-        const float q = Q[(u64)i * a.ldq + off + tid];
-        qu[tid] = q + a.bu[off + tid];
-        qv[tid] = q + a.bv[off + tid];
-    }
-    __syncthreads();
-    const u32 d0 = 2 * lane;
-    const float2 u2 = make_float2(qu[d0], qu[d0 + 1]), v2 = make_float2(qv[d0], qv[d0 + 1]);
-    for (u32 j = wave; j < L; j += 2) {
-        const u32 prow = (a.Lmax - L) + (a.c - 1 - i + j); /* relative position (L-c+i) - j */
-        const float2 k2 = *(const float2 *)(Kp + (u64)j * a.ldk + off + d0);
-        const float2 p2 = *(const float2 *)(a.P + (u64)prow * a.D + off + d0);
-        float part = u2.x * k2.x + u2.y * k2.y + v2.x * p2.x + v2.y * p2.y;
-        part = wave_sum(part);
-        if (lane == 0) s[j] = part * a.scale;
-    }
-    __syncthreads();
-    const float sv = tid < L ? s[tid] : -INFINITY;
-    float mx = wave_max(sv);
-    if (lane == 0) red[wave] = mx;
-    __syncthreads();
-    mx = fmaxf(red[0], red[1]);
-    __syncthreads();
-    const float ev = tid < L ? expf(sv - mx) : 0.0f;
-    float sum = wave_sum(ev);
-    if (lane == 0) red[wave] = sum;
-    __syncthreads();
-    sum = red[0] + red[1];
-    if (tid < L) s[tid] = ev / sum;
-    __syncthreads();
-    float acc = 0.0f;
-    for (u32 j = 0; j < L; ++j) acc += s[j] * Vp[(u64)j * a.ldk + off + tid];
-    a.O[(u64)i * a.D + off + tid] = acc;
-}
-
-/* Causal depthwise conv (taps rows: taps-1 history rows + the row itself, no bias) + LN + SiLU,
- * one workgroup per output row: reference src/kernels.metal:359-409. */
-extern "C" __global__ __launch_bounds__(256) void dwconv_ln_silu(const NkDwArgs a) {
-    __shared__ float red[4];
-    const u32 t = blockIdx.x, tid = threadIdx.x;
-    const int per = (int)((a.D + NK_LN_THREADS - 1) / NK_LN_THREADS);
-    const float *din = a.din;
-    if (a.desc) din += (u64)((u32)a.desc[NK_DESC_POS] - (a.taps - 1)) * a.D;
-    float v[NK_LN_MAX_PER];
-    for (int k = 0; k < per; ++k) {
-        const u32 ch = tid + k * NK_LN_THREADS;
-        float acc = 0.0f;
-        if (ch < a.D)
-            for (u32 tap = 0; tap < a.taps; ++tap) acc += a.W[ch * a.taps + tap] * din[(u64)(t + tap) * a.D + ch];
-        v[k] = acc;
-    }
-    ln_regs(v, per, a.D, a.eps, a.g, a.b, red);
-    for (int k = 0; k < per; ++k) {
-        const u32 ch = tid + k * NK_LN_THREADS;
-        if (ch < a.D) a.Y[(u64)t * a.D + ch] = silu_f(v[k]);
-    }
-}
 
 /* Subsampling conv 0: 1 -> C channels, 3x3, stride 2, causal padding (2 before, 1 after) on
  * time and frequency, + bias, ReLU.  X [T][F] -> Y [T1][F1][C].  One thread per output, channel
