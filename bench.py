@@ -28,7 +28,7 @@ import numpy as np  # noqa: E402
 METRIC = "RTFx (audio-s/s) + p50 chunk ms at 1 and 64 streams; achieved HBM GB/s"
 HBM_PEAK_GBS = 8000.0
 LAT_RIGHT = {80: 0, 160: 1, 320: 3, 560: 6, 1120: 13}
-DOMINANT = {80: "gemv_r1_c2", 560: "gemm_fr", 1120: "gemm_fr"}
+DOMINANT = {80: "gemv_*", 160: "gemv_*", 320: "gemm_fr", 560: "gemm_fr", 1120: "gemm_fr"}
 
 
 def weight_bytes_per_chunk(cfg: dict) -> int:
@@ -111,7 +111,7 @@ def main():
     kname = a.kernel or DOMINANT.get(a.latency, "gemm_fr")
     s.reset("en-US", a.latency)
     s.use_graphs(False)
-    s.time_kernel(kname, 4096)
+    s.time_kernel(kname, 32768)
     for i in range(0, audio.size, piece):
         s.feed(audio[i:i + piece], final=i + piece >= audio.size)
     kms, kn, kbytes = s.kernel_ms()

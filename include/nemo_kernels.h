@@ -59,8 +59,16 @@ int nk_gemm(gpu_t *g, const float *A, uint32_t lda, const uint16_t *W, uint32_t 
 int nk_gemm_rows(gpu_t *g, const float *A, uint32_t lda, const uint16_t *W, uint32_t ldw, const float *bias,
                  float *C, uint32_t ldc, const int *crow, uint32_t M, uint32_t N, uint32_t K, int act, int accumulate,
                  float alpha);
-/* Kernel selection: 0 automatic (by row count), 1 VALU weight streaming (M <= 4),
- * 2 few-row MFMA (M <= 16), 3 many-row MFMA.  Returns the previous setting. */
+/* Same, with a LayerNorm prologue on A when K is the row width (ln_mode 1: A' = LN(A; g1,b1);
+ * 2: A' = LN(LN(A; g1,b1); g2,b2)).  ln_out (optional) receives LN(A; g1,b1).  For M <= 4 the
+ * LayerNorm runs inside the GEMV; otherwise it is launched separately into `tmp` (M*K floats). */
+int nk_gemm_ln(gpu_t *g, const float *A, uint32_t lda, const uint16_t *W, uint32_t ldw, const float *bias, float *C,
+               uint32_t ldc, const int *crow, uint32_t M, uint32_t N, uint32_t K, int act, int accumulate, float alpha,
+               int ln_mode, const float *g1, const float *b1, const float *g2, const float *b2, float *ln_out,
+               float *tmp, float eps);
+/* Kernel selection: 0 automatic (by row count), 1 first-generation VALU GEMV (M <= 4),
+ * 2 few-row MFMA (M <= 16), 3 many-row MFMA, 4 weight-streaming GEMV (M <= 4).
+ * Returns the previous setting. */
 int nk_gemm_force(int kind);
 /* Name of the kernel nk_gemm would launch for these shapes (for profiling and tests). */
 const char *nk_gemm_kernel_name(uint32_t M, uint32_t N, uint32_t K, int act);

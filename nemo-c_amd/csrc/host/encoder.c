@@ -235,54 +235,66 @@ static void run_pre_encode(encoder_t *e, int nwin) {
 }
 
 /* 24 conformer blocks + prompt + joint projection on the c rows in e->h: src/encoder.c:174-226.
- * Cache positions come from the device descriptor. */
+ * Cache positions come from the device descriptor.  Every LayerNorm in front of a GEMM runs in
+ * that GEMM's prologue: the output norm of block l and the FF1 norm of block l+1 run in block
+ * l+1's first GEMM, which also writes the normalised residual into the other residual buffer
+ * (the reference's h/t swap, src/encoder.c:209-216). */
 static void run_blocks(encoder_t *e, int c) {
     model_t *m = e->m;
     gpu_t *g = e->g;
     const model_cfg_t *cf = &m->cfg;
     const uint32_t D = (uint32_t)cf->d_model, FF = (uint32_t)cf->d_ff, H = (uint32_t)cf->n_heads, dh = (uint32_t)cf->head_dim;
-    const uint32_t uc = (uint32_t)c;
+    const uint32_t uc = (uint32_t)c, nl = (uint32_t)cf->n_layers;
     const float eps = cf->ln_eps, scale = 1.0f / sqrtf((float)dh);
     const int *desc = gpu_buf_dptr(e->desc);
     const int *rows = desc + NK_DESC_ROWS;
-    float *h = gpu_buf_dptr(e->h), *t = gpu_buf_dptr(e->tmp), *t2 = gpu_buf_dptr(e->t2);
+    float *R[2] = { gpu_buf_dptr(e->h), gpu_buf_dptr(e->tmp) };
+    float *lnbuf = gpu_buf_dptr(e->t2); /* LayerNorm output when the GEMM cannot take it as a prologue */
     float *ff = gpu_buf_dptr(e->ff), *att = gpu_buf_dptr(e->att), *y = gpu_buf_dptr(e->y);
-    for (int l = 0; l < cf->n_layers; ++l) {
+    float *dump = e->dump ? gpu_buf_dptr(e->dump_dev) : NULL;
+    int cur = 0;
+    for (uint32_t l = 0; l < nl; ++l) {
         const layer_dev_t *W = &m->L[l];
         float *kv = (float *)gpu_buf_dptr(e->kv) + (size_t)l * e->kv_stride;
         float *din = (float *)gpu_buf_dptr(e->din) + (size_t)l * e->din_stride;
-        /* FF1 half step; for l > 0 its norm came from the previous block's paired norm (t2) */
-        if (l == 0) nk_layernorm(g, h, W->ln_ff1_g, W->ln_ff1_b, t2, uc, D, eps);
-        nk_gemm(g, t2, D, W->ff1_w1, D, NULL, ff, FF, uc, FF, D, NK_ACT_SILU, 0, 1.0f);
-        nk_gemm(g, ff, FF, W->ff1_w2, FF, NULL, h, D, uc, D, FF, NK_ACT_NONE, 1, 0.5f);
-        /* attention: fused q|k|v projection written into cache rows pos .. pos+c-1 */
-        nk_layernorm(g, h, W->ln_att_g, W->ln_att_b, t, uc, D, eps);
-        nk_gemm_rows(g, t, D, W->wqkv, D, NULL, kv, 3 * D, rows, uc, 3 * D, D, NK_ACT_NONE, 0, 1.0f);
-        nk_attention_rel_desc(g, kv, 3 * D, desc, W->ptab, W->bias_u, W->bias_v, att, uc, (uint32_t)e->Lmax, H, dh, D, scale);
-        nk_gemm(g, att, D, W->wo, D, NULL, h, D, uc, D, D, NK_ACT_NONE, 1, 1.0f);
-        /* convolution module: GLU output appended to the conv history, causal depthwise conv over it */
-        nk_layernorm(g, h, W->ln_conv_g, W->ln_conv_b, t, uc, D, eps);
-        nk_gemm_rows(g, t, D, W->pw1, D, NULL, din, D, rows, uc, 2 * D, D, NK_ACT_GLU, 0, 1.0f);
-        nk_dwconv_ln_silu_desc(g, din, desc, W->dw_w, W->bn_g, W->bn_b, y, uc, D, (uint32_t)cf->conv_kernel, eps);
-        nk_gemm(g, y, D, W->pw2, D, NULL, h, D, uc, D, D, NK_ACT_NONE, 1, 1.0f);
-        /* FF2 half step + output norm (paired with the next block's FF1 norm) */
-        nk_layernorm(g, h, W->ln_ff2_g, W->ln_ff2_b, t, uc, D, eps);
-        nk_gemm(g, t, D, W->ff2_w1, D, NULL, ff, FF, uc, FF, D, NK_ACT_SILU, 0, 1.0f);
-        nk_gemm(g, ff, FF, W->ff2_w2, FF, NULL, h, D, uc, D, FF, NK_ACT_NONE, 1, 0.5f);
-        if (l + 1 < cf->n_layers) {
-            const layer_dev_t *Wn = &m->L[l + 1];
-            nk_layernorm2(g, h, W->ln_out_g, W->ln_out_b, Wn->ln_ff1_g, Wn->ln_ff1_b, t, t2, uc, D, eps);
+        /* FF1 half step (LN of block l-1's output, then this block's FF1 norm) */
+        if (l == 0) {
+            nk_gemm_ln(g, R[0], D, W->ff1_w1, D, NULL, ff, FF, NULL, uc, FF, D, NK_ACT_SILU, 0, 1.0f, 1, W->ln_ff1_g,
+                       W->ln_ff1_b, NULL, NULL, NULL, lnbuf, eps);
         } else {
-            nk_layernorm(g, h, W->ln_out_g, W->ln_out_b, t, uc, D, eps);
+            const layer_dev_t *Wp = &m->L[l - 1];
+            const int prev = cur;
+            cur ^= 1;
+            nk_gemm_ln(g, R[prev], D, W->ff1_w1, D, NULL, ff, FF, NULL, uc, FF, D, NK_ACT_SILU, 0, 1.0f, 2, Wp->ln_out_g,
+                       Wp->ln_out_b, W->ln_ff1_g, W->ln_ff1_b, R[cur], lnbuf, eps);
+            if (dump) nk_copy2d(g, R[cur], D, dump + (size_t)(l - 1) * D, D * nl, uc, D);
         }
-        float *sw = h; h = t; t = sw;
-        if (e->dump)
-            nk_copy2d(g, h, D, (float *)gpu_buf_dptr(e->dump_dev) + (size_t)l * D, D * (uint32_t)cf->n_layers, uc, D);
+        float *res = R[cur];
+        nk_gemm(g, ff, FF, W->ff1_w2, FF, NULL, res, D, uc, D, FF, NK_ACT_NONE, 1, 0.5f);
+        /* attention: fused q|k|v projection written into cache rows pos .. pos+c-1 */
+        nk_gemm_ln(g, res, D, W->wqkv, D, NULL, kv, 3 * D, rows, uc, 3 * D, D, NK_ACT_NONE, 0, 1.0f, 1, W->ln_att_g,
+                   W->ln_att_b, NULL, NULL, NULL, lnbuf, eps);
+        nk_attention_rel_desc(g, kv, 3 * D, desc, W->ptab, W->bias_u, W->bias_v, att, uc, (uint32_t)e->Lmax, H, dh, D, scale);
+        nk_gemm(g, att, D, W->wo, D, NULL, res, D, uc, D, D, NK_ACT_NONE, 1, 1.0f);
+        /* convolution module: GLU output appended to the conv history, causal depthwise conv over it */
+        nk_gemm_ln(g, res, D, W->pw1, D, NULL, din, D, rows, uc, 2 * D, D, NK_ACT_GLU, 0, 1.0f, 1, W->ln_conv_g,
+                   W->ln_conv_b, NULL, NULL, NULL, lnbuf, eps);
+        nk_dwconv_ln_silu_desc(g, din, desc, W->dw_w, W->bn_g, W->bn_b, y, uc, D, (uint32_t)cf->conv_kernel, eps);
+        nk_gemm(g, y, D, W->pw2, D, NULL, res, D, uc, D, D, NK_ACT_NONE, 1, 1.0f);
+        /* FF2 half step */
+        nk_gemm_ln(g, res, D, W->ff2_w1, D, NULL, ff, FF, NULL, uc, FF, D, NK_ACT_SILU, 0, 1.0f, 1, W->ln_ff2_g,
+                   W->ln_ff2_b, NULL, NULL, NULL, lnbuf, eps);
+        nk_gemm(g, ff, FF, W->ff2_w2, FF, NULL, res, D, uc, D, FF, NK_ACT_NONE, 1, 0.5f);
     }
-    /* language prompt (one-hot folded into the bias) and joint encoder projection */
+    /* last output norm in the prompt GEMM's prologue, language prompt (one-hot folded into the
+     * bias) and joint encoder projection */
+    const layer_dev_t *Wl = &m->L[nl - 1];
     const uint32_t PH = (uint32_t)cf->prompt_hidden, NP = (uint32_t)cf->num_prompts, JH = (uint32_t)cf->joint_hidden;
     float *ph = gpu_buf_dptr(e->ph), *pr = gpu_buf_dptr(e->prompted);
-    nk_gemm(g, h, D, m->prompt_w0, D + NP, m->prompt_b0_eff, ph, PH, uc, PH, D, NK_ACT_RELU, 0, 1.0f);
+    float *hn = dump ? R[cur ^ 1] : NULL;
+    nk_gemm_ln(g, R[cur], D, m->prompt_w0, D + NP, m->prompt_b0_eff, ph, PH, NULL, uc, PH, D, NK_ACT_RELU, 0, 1.0f, 1,
+               Wl->ln_out_g, Wl->ln_out_b, NULL, NULL, hn, lnbuf, eps);
+    if (dump) nk_copy2d(g, hn, D, dump + (size_t)(nl - 1) * D, D * nl, uc, D);
     nk_gemm(g, ph, PH, m->prompt_w2, PH, m->prompt_b2, pr, D, uc, D, PH, NK_ACT_NONE, 0, 1.0f);
     nk_gemm(g, pr, D, m->joint_enc_w, D, m->joint_enc_b, gpu_buf_dptr(e->joint_enc), JH, uc, JH, D, NK_ACT_NONE, 0, 1.0f);
 }

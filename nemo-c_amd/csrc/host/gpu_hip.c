@@ -10,7 +10,7 @@ extern const unsigned char nk_code_object_start[];
 extern const unsigned char nk_code_object_end[];
 
 #define GPU_MAX_FN 96
-#define GPU_MAX_TIMED 4096
+#define GPU_MAX_TIMED 32768
 
 struct gpu {
     int dev;
@@ -179,6 +179,13 @@ static hipFunction_t lookup(gpu_t *g, const char *kernel) {
     return f;
 }
 
+/* timing selection: an exact kernel name, or a prefix ending in '*' */
+static int timed_name(const char *sel, const char *kernel) {
+    const size_t n = strlen(sel);
+    if (n && sel[n - 1] == '*') return !strncmp(sel, kernel, n - 1);
+    return !strcmp(sel, kernel);
+}
+
 int gpu_begin(gpu_t *g) {
     g->failed = 0;
     g->err[0] = 0;
@@ -195,7 +202,7 @@ int gpu_launch(gpu_t *g, const char *kernel, const void *args, size_t args_size,
     size_t sz = args_size;
     void *config[] = { HIP_LAUNCH_PARAM_BUFFER_POINTER, (void *)args, HIP_LAUNCH_PARAM_BUFFER_SIZE, &sz,
                        HIP_LAUNCH_PARAM_END };
-    const int timed = !g->capturing && g->tev && g->tn < g->tmax && !strcmp(kernel, g->timed);
+    const int timed = !g->capturing && g->tev && g->tn < g->tmax && timed_name(g->timed, kernel);
     if (timed) hipEventRecord(g->tev[2 * g->tn], g->stream);
     hipError_t e = hipModuleLaunchKernel(f, gx, gy, gz, bx, by, bz, 0, g->stream, NULL, config);
     if (timed) {

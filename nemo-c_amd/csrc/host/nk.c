@@ -20,51 +20,100 @@ static int bad(gpu_t *g, const char *what) { return gpu_fail(g, what); }
 
 static int aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 
-enum { K_GEMV = 1, K_FR = 2, K_MR = 3 };
+enum { K_GEMV1 = 1, K_FR = 2, K_MR = 3, K_GEMV = 4 };
 
 static int pick(uint32_t M, uint32_t K, int act) {
-    if (g_force == K_GEMV && M <= 4) return K_GEMV;
+    if (g_force == K_GEMV1 && M <= 4) return K_GEMV1;
     if (g_force == K_FR && M <= NK_FEW_ROWS && K % 32 == 0) return K_FR;
     if (g_force == K_MR && act != NK_ACT_GLU && K % 32 == 0) return K_MR;
-    if (M <= 4) return K_GEMV;
+    const int gemv_ok = (M <= 2 && K <= 64 * 8 * 9) || (M <= 4 && K <= 64 * 8 * 2);
+    if (g_force == K_GEMV && gemv_ok) return K_GEMV;
+    if (gemv_ok) return K_GEMV;
     if (M <= NK_FEW_ROWS) return K_FR;
     return K_MR;
 }
 
+/* weight-streaming GEMV shape: chunks per lane per row (KCH) and weight rows per wavefront (NC) */
+static void gemv_shape(uint32_t N, uint32_t K, int act, uint32_t *kch, uint32_t *nc) {
+    const uint32_t nch = K / 8;
+    *kch = nch <= 64 ? 1 : nch <= 128 ? 2 : nch <= 256 ? 4 : nch <= 512 ? 8 : 9;
+    if (act == NK_ACT_GLU) { *nc = (*kch <= 4 && N / 2 >= 2048) ? 4 : 2; return; }
+    const uint32_t maxnc = *kch <= 4 ? 4 : 2;
+    *nc = (N >= 4096 && maxnc >= 4) ? 4 : (N >= 2048 ? 2 : 1);
+}
+
 const char *nk_gemm_kernel_name(uint32_t M, uint32_t N, uint32_t K, int act) {
     static char buf[32];
-    (void)N;
+    uint32_t kch, nc;
     switch (pick(M, K, act)) {
-    case K_GEMV:
+    case K_GEMV1:
         snprintf(buf, sizeof buf, "gemv_r%u_c%u", M, (act == NK_ACT_GLU || K <= 2048) ? 2u : 1u);
+        return buf;
+    case K_GEMV:
+        gemv_shape(N, K, act, &kch, &nc);
+        snprintf(buf, sizeof buf, "gemv_r%u_n%u_k%u", M, nc, kch);
         return buf;
     case K_FR: return "gemm_fr";
     default: return "gemm_mr";
     }
 }
 
-int nk_gemm_rows(gpu_t *g, const float *A, uint32_t lda, const uint16_t *W, uint32_t ldw, const float *bias,
-                 float *C, uint32_t ldc, const int *crow, uint32_t M, uint32_t N, uint32_t K, int act, int accumulate,
-                 float alpha) {
+typedef struct {
+    int mode;
+    const float *g1, *b1, *g2, *b2;
+    float *out, *tmp;
+    float eps;
+} ln_pro_t;
+
+/* The GEMM with an optional LayerNorm prologue on A.  The weight-streaming GEMV applies it in
+ * registers; the MFMA kernels get it from separate LayerNorm launches into ln.tmp. */
+static int gemm_core(gpu_t *g, const float *A, uint32_t lda, const uint16_t *W, uint32_t ldw, const float *bias,
+                     float *C, uint32_t ldc, const int *crow, uint32_t M, uint32_t N, uint32_t K, int act,
+                     int accumulate, float alpha, const ln_pro_t *ln) {
     if (!M) return 0;
     if (!N || !K || (act == NK_ACT_GLU && (N & 1))) return bad(g, "gemm: bad shape");
     if (!aligned16(A) || !aligned16(W) || lda % 4 || ldw % 8 || K % 8 || K > lda || K > ldw)
         return bad(g, "gemm: A/W must be 16-byte aligned with lda % 4 == 0, ldw % 8 == 0, K % 8 == 0");
     const uint32_t nout = act == NK_ACT_GLU ? N / 2 : N;
     if (ldc < nout) return bad(g, "gemm: ldc < output width");
+    const int kind = pick(M, K, act);
+    if (ln && ln->mode && (kind != K_GEMV || K > 64 * 8 * 2)) {
+        /* unfused LayerNorm: out = LN1(A) (if requested), tmp = LN(...) feeds the GEMM */
+        if (!ln->tmp || K != lda) return bad(g, "gemm: LayerNorm prologue needs a scratch buffer");
+        if (ln->mode == 2) {
+            float *y1 = ln->out ? ln->out : ln->tmp;
+            if (nk_layernorm2(g, A, ln->g1, ln->b1, ln->g2, ln->b2, y1, ln->tmp, M, K, ln->eps)) return -1;
+        } else {
+            if (nk_layernorm(g, A, ln->g1, ln->b1, ln->tmp, M, K, ln->eps)) return -1;
+            if (ln->out && nk_copy(g, ln->tmp, ln->out, M * K)) return -1;
+        }
+        return gemm_core(g, ln->tmp, lda, W, ldw, bias, C, ldc, crow, M, N, K, act, accumulate, alpha, NULL);
+    }
     NkGemmArgs a;
     memset(&a, 0, sizeof a);
     a.A = A; a.W = W; a.bias = bias; a.C = C; a.crow = crow;
     a.M = M; a.N = N; a.K = K; a.lda = lda; a.ldw = ldw; a.ldc = ldc;
     a.act = (uint32_t)act; a.accumulate = (uint32_t)(accumulate != 0); a.alpha = alpha; a.splits = 1;
-    const int kind = pick(M, K, act);
+    if (ln && ln->mode) {
+        if (K != lda) return bad(g, "gemm: LayerNorm prologue needs K == lda");
+        a.ln_mode = (uint32_t)ln->mode; a.ln_g1 = ln->g1; a.ln_b1 = ln->b1; a.ln_g2 = ln->g2; a.ln_b2 = ln->b2;
+        a.ln_out = ln->out; a.ln_eps = ln->eps;
+    }
     /* algorithmic HBM bytes: every weight once, A once, C written (and read when accumulating) */
     gpu_next_bytes(g, 2.0 * N * K + 4.0 * M * K + 4.0 * M * nout * (accumulate ? 2 : 1) + (bias ? 4.0 * N : 0.0));
+    char name[32];
     if (kind == K_GEMV) {
+        uint32_t kch, nc;
+        gemv_shape(N, K, act, &kch, &nc);
+        const uint32_t per_wave = act == NK_ACT_GLU ? nc / 2 : nc;
+        const uint32_t waves = (nout + per_wave - 1) / per_wave;
+        snprintf(name, sizeof name, "gemv_r%u_n%u_k%u", M, nc, kch);
+        return gpu_launch(g, name, &a, sizeof a, (waves + 3) / 4, 1, 1, 256, 1, 1);
+    }
+    if (kind == K_GEMV1) {
         const uint32_t nc = (act == NK_ACT_GLU || K <= 2048) ? 2u : 1u;
         const uint32_t per_wave = act == NK_ACT_GLU ? 1u : nc;
         const uint32_t waves = (nout + per_wave - 1) / per_wave;
-        char name[24];
         snprintf(name, sizeof name, "gemv_r%u_c%u", M, nc);
         return gpu_launch(g, name, &a, sizeof a, (waves + 3) / 4, 1, 1, 256, 1, 1);
     }
@@ -88,9 +137,24 @@ int nk_gemm_rows(gpu_t *g, const float *A, uint32_t lda, const uint16_t *W, uint
     return gpu_launch(g, "gemm_mr", &a, sizeof a, (N + 63) / 64, (M + 63) / 64, 1, 256, 1, 1);
 }
 
+int nk_gemm_rows(gpu_t *g, const float *A, uint32_t lda, const uint16_t *W, uint32_t ldw, const float *bias,
+                 float *C, uint32_t ldc, const int *crow, uint32_t M, uint32_t N, uint32_t K, int act, int accumulate,
+                 float alpha) {
+    return gemm_core(g, A, lda, W, ldw, bias, C, ldc, crow, M, N, K, act, accumulate, alpha, NULL);
+}
+
 int nk_gemm(gpu_t *g, const float *A, uint32_t lda, const uint16_t *W, uint32_t ldw, const float *bias, float *C,
             uint32_t ldc, uint32_t M, uint32_t N, uint32_t K, int act, int accumulate, float alpha) {
-    return nk_gemm_rows(g, A, lda, W, ldw, bias, C, ldc, NULL, M, N, K, act, accumulate, alpha);
+    return gemm_core(g, A, lda, W, ldw, bias, C, ldc, NULL, M, N, K, act, accumulate, alpha, NULL);
+}
+
+int nk_gemm_ln(gpu_t *g, const float *A, uint32_t lda, const uint16_t *W, uint32_t ldw, const float *bias, float *C,
+               uint32_t ldc, const int *crow, uint32_t M, uint32_t N, uint32_t K, int act, int accumulate, float alpha,
+               int ln_mode, const float *g1, const float *b1, const float *g2, const float *b2, float *ln_out,
+               float *tmp, float eps) {
+    const ln_pro_t ln = { ln_mode, g1, b1, g2, b2, ln_out, tmp, eps };
+    if (ln_mode < 0 || ln_mode > 2) return bad(g, "gemm: ln_mode must be 0, 1 or 2");
+    return gemm_core(g, A, lda, W, ldw, bias, C, ldc, crow, M, N, K, act, accumulate, alpha, &ln);
 }
 
 int nk_layernorm2(gpu_t *g, const float *X, const float *g1, const float *b1, const float *g2, const float *b2,

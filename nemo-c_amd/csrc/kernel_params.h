@@ -49,6 +49,12 @@ typedef struct {
     u32 act, accumulate, splits, pad0;
     float alpha;
     u32 pad1;
+    /* LayerNorm prologue on A (weight-streaming GEMV): ln_mode 0 none, 1 LN(g1,b1),
+     * 2 LN(LN(g1,b1); g2,b2); ln_out (optional) receives LN(A; g1,b1), rows of lda floats */
+    const float *ln_g1, *ln_b1, *ln_g2, *ln_b2;
+    float *ln_out;
+    u32 ln_mode;
+    float ln_eps;
 } NkGemmArgs;
 
 typedef struct {

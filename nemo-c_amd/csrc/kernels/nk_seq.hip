@@ -76,14 +76,17 @@ extern "C" __global__ __launch_bounds__(256) void layernorm(const NkLnArgs a) {
 }
 
 /* Relative-position attention, one workgroup of 256 threads per (head, query):
- * reference src/kernels.metal:290-348.  Four threads share a key (32 head dims each), 64 keys per
- * pass, at most two passes (L <= 128).  Every K, P and V element the workgroup needs is loaded
- * before the first score is formed: V is preloaded per output dim (thread d sums keys of one
- * parity), the scores go through LDS, and the two parities are added at the end.
+ * reference src/kernels.metal:290-348.
  *   score_j = ((q + u) . K_j + (q + v) . P[(Lmax - L) + (c - 1 - i + j)]) * scale
- *   O_i = sum_j softmax(score)_j V_j  (no mask inside the chunk) */
+ *   O_i = sum_j softmax(score)_j V_j  (no mask inside the chunk)
+ * Scores: four threads share a key (32 head dims each), 64 keys per pass, two passes (L <= 128).
+ * Output: thread (g = tid / 32, d4 = tid % 32) accumulates dims 4*d4..4*d4+3 over the keys
+ * j = g (mod 8); the 8 key groups are summed in order through LDS.  Every K, P and V load is
+ * issued before the first score is formed; q + u and q + v come from LDS. */
 extern "C" __global__ __launch_bounds__(256) void attention_rel(const NkAttnArgs a) {
-    __shared__ float s[NK_ATT_MAX_L], red[8], half_out[128];
+    __shared__ float4 qu4[32], qv4[32];
+    __shared__ float s[NK_ATT_MAX_L], red[8];
+    __shared__ float4 part[8][32];
     const u32 h = blockIdx.x, i = blockIdx.y, tid = threadIdx.x;
     const u32 off = h * 128;
     const float *Q = a.Q, *Kp = a.K, *Vp = a.V;
@@ -95,16 +98,17 @@ extern "C" __global__ __launch_bounds__(256) void attention_rel(const NkAttnArgs
         Vp += (u64)(pos - cl) * a.ldk;
         L = cl + a.c;
     }
-    const u32 ks = tid >> 2, part = tid & 3, dofs = off + part * 32;
-    /* V preload: output dim d = tid & 127, keys of parity tid >> 7 */
-    const u32 d = tid & 127, par = tid >> 7;
-    float vv[NK_ATT_MAX_L / 2];
+    const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+    /* V rows for the output phase */
+    const u32 vg = tid >> 5, d4 = tid & 31;
+    float4 vv[NK_ATT_MAX_L / 8];
 #pragma unroll
-    for (int t = 0; t < NK_ATT_MAX_L / 2; ++t) {
-        const u32 j = par + 2 * t;
-        vv[t] = j < L ? Vp[(u64)j * a.ldk + off + d] : 0.0f;
+    for (int t = 0; t < NK_ATT_MAX_L / 8; ++t) {
+        const u32 j = vg + 8 * t;
+        vv[t] = j < L ? *(const float4 *)(Vp + (u64)j * a.ldk + off + 4 * d4) : z;
     }
     /* K and P rows of this thread's keys */
+    const u32 ks = tid >> 2, part4 = tid & 3, dofs = off + part4 * 32;
     float4 kr[2][8], pr[2][8];
 #pragma unroll
     for (int p = 0; p < 2; ++p) {
@@ -113,30 +117,30 @@ extern "C" __global__ __launch_bounds__(256) void attention_rel(const NkAttnArgs
         const u32 prow = (a.Lmax - L) + (a.c - 1 - i + j);
 #pragma unroll
         for (int q = 0; q < 8; ++q) {
-            kr[p][q] = ok ? *(const float4 *)(Kp + (u64)j * a.ldk + dofs + 4 * q) : make_float4(0.f, 0.f, 0.f, 0.f);
-            pr[p][q] = ok ? *(const float4 *)(a.P + (u64)prow * a.D + dofs + 4 * q) : make_float4(0.f, 0.f, 0.f, 0.f);
+            kr[p][q] = ok ? *(const float4 *)(Kp + (u64)j * a.ldk + dofs + 4 * q) : z;
+            pr[p][q] = ok ? *(const float4 *)(a.P + (u64)prow * a.D + dofs + 4 * q) : z;
         }
     }
-    float4 qu[8], qv[8];
-#pragma unroll
-    for (int q = 0; q < 8; ++q) {
-        const float4 x = *(const float4 *)(Q + (u64)i * a.ldq + dofs + 4 * q);
-        const float4 u = *(const float4 *)(a.bu + dofs + 4 * q), w = *(const float4 *)(a.bv + dofs + 4 * q);
-        qu[q] = make_float4(x.x + u.x, x.y + u.y, x.z + u.z, x.w + u.w);
-        qv[q] = make_float4(x.x + w.x, x.y + w.y, x.z + w.z, x.w + w.w);
+    if (tid < 32) {
+        const float4 x = *(const float4 *)(Q + (u64)i * a.ldq + off + 4 * tid);
+        const float4 u = *(const float4 *)(a.bu + off + 4 * tid), w = *(const float4 *)(a.bv + off + 4 * tid);
+        qu4[tid] = make_float4(x.x + u.x, x.y + u.y, x.z + u.z, x.w + u.w);
+        qv4[tid] = make_float4(x.x + w.x, x.y + w.y, x.z + w.z, x.w + w.w);
     }
+    __syncthreads();
 #pragma unroll
     for (int p = 0; p < 2; ++p) {
         float acc = 0.0f;
 #pragma unroll
         for (int q = 0; q < 8; ++q) {
-            acc += qu[q].x * kr[p][q].x + qu[q].y * kr[p][q].y + qu[q].z * kr[p][q].z + qu[q].w * kr[p][q].w;
-            acc += qv[q].x * pr[p][q].x + qv[q].y * pr[p][q].y + qv[q].z * pr[p][q].z + qv[q].w * pr[p][q].w;
+            const float4 u = qu4[part4 * 8 + q], w = qv4[part4 * 8 + q];
+            acc += u.x * kr[p][q].x + u.y * kr[p][q].y + u.z * kr[p][q].z + u.w * kr[p][q].w;
+            acc += w.x * pr[p][q].x + w.y * pr[p][q].y + w.z * pr[p][q].z + w.w * pr[p][q].w;
         }
         acc += __shfl_xor(acc, 1, 64);
         acc += __shfl_xor(acc, 2, 64);
         const u32 j = ks + 64 * p;
-        if (part == 0 && j < L) s[j] = acc * a.scale;
+        if (part4 == 0 && j < L) s[j] = acc * a.scale;
     }
     __syncthreads();
     /* softmax over the window */
@@ -153,15 +157,26 @@ extern "C" __global__ __launch_bounds__(256) void attention_rel(const NkAttnArgs
     sum = ((red[4] + red[5]) + red[6]) + red[7];
     if (tid < L) s[tid] = ev / sum;
     __syncthreads();
-    float acc = 0.0f;
+    float4 acc = z;
 #pragma unroll
-    for (int t = 0; t < NK_ATT_MAX_L / 2; ++t) {
-        const u32 j = par + 2 * t;
-        if (j < L) acc += s[j] * vv[t];
+    for (int t = 0; t < NK_ATT_MAX_L / 8; ++t) {
+        const u32 j = vg + 8 * t;
+        if (j < L) {
+            const float p = s[j];
+            acc.x += p * vv[t].x; acc.y += p * vv[t].y; acc.z += p * vv[t].z; acc.w += p * vv[t].w;
+        }
     }
-    if (par == 1) half_out[d] = acc;
+    part[vg][d4] = acc;
     __syncthreads();
-    if (par == 0) a.O[(u64)i * a.D + off + d] = acc + half_out[d];
+    if (tid < 32) {
+        float4 o = part[0][tid];
+#pragma unroll
+        for (int g = 1; g < 8; ++g) {
+            const float4 v = part[g][tid];
+            o.x += v.x; o.y += v.y; o.z += v.z; o.w += v.w;
+        }
+        *(float4 *)(a.O + (u64)i * a.D + off + 4 * tid) = o;
+    }
 }
 
 /* Causal depthwise conv (9 taps: 8 history rows + the row itself, no bias) + LN + SiLU, one

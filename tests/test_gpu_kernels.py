@@ -110,6 +110,54 @@ def test_gemm_variants_agree(gpu, kind, M):
     assert rel_err(got, ref) < GEMM_TOL
 
 
+@pytest.mark.parametrize("kind", [1, 4])
+@pytest.mark.parametrize("M,N,K,act", [(1, 2560, 640, 0), (2, 1024, 4096, 0), (1, 1024, 4352, 0), (2, 640, 640, 2),
+                                       (3, 2048, 1024, 3), (4, 4096, 1024, 1)])
+def test_gemv_kinds(gpu, kind, M, N, K, act):
+    rng = np.random.default_rng([kind, M, N, K])
+    W = _w(rng, N, K)
+    A = rng.standard_normal((M, K)).astype(np.float32)
+    bias = (0.1 * rng.standard_normal(N)).astype(np.float32)
+    nout = N // 2 if act == 3 else N
+    C0 = rng.standard_normal((M, nout)).astype(np.float32)
+    got = run_gemm(gpu, A, W, bias, act, True, 0.5, C0=C0, kind=kind)
+    ref = oracle.gemm(A, W, bias, act, True, 0.5, C0=C0)
+    assert rel_err(got, ref) < GEMM_TOL
+
+
+@pytest.mark.parametrize("mode", [1, 2])
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 7])
+@pytest.mark.parametrize("N,act", [(4096, 1), (2048, 3), (3072, 0)])
+def test_gemm_layernorm_prologue(gpu, mode, M, N, act):
+    """GEMM on LN(A) (mode 1) or LN(LN(A)) (mode 2, the paired output / FF1 norm), with the first
+    LayerNorm's output written to ln_out: equals the oracle's layernorm(2) followed by its GEMM."""
+    import nemoasr
+
+    L = nemoasr.lib()
+    D = 1024
+    rng = np.random.default_rng([mode, M, N])
+    X = (2 * rng.standard_normal((M, D)) + 0.5).astype(np.float32)
+    g1, g2 = [(1 + 0.1 * rng.standard_normal(D)).astype(np.float32) for _ in range(2)]
+    b1, b2 = [(0.1 * rng.standard_normal(D)).astype(np.float32) for _ in range(2)]
+    W = _w(rng, N, D)
+    if mode == 1:
+        y1 = oracle.layernorm(X, g1, b1)
+        xin = y1
+    else:
+        y1, xin = oracle.layernorm2(X, g1, b1, g2, b2)
+    ref = oracle.gemm(xin, W, None, act, False, 1.0)
+    nout = N // 2 if act == 3 else N
+    dX, dW, dC = gpu.put(X), gpu.put(W), gpu.alloc(M * nout * 4)
+    dg1, db1, dg2, db2 = gpu.put(g1), gpu.put(b1), gpu.put(g2), gpu.put(b2)
+    dout, dtmp = gpu.alloc(M * D * 4), gpu.alloc(M * D * 4)
+    gpu.begin()
+    gpu.check(L.nk_gemm_ln(gpu.h, dX.ptr, D, dW.ptr, D, None, dC.ptr, nout, None, M, N, D, act, 0, 1.0, mode,
+                           dg1.ptr, db1.ptr, dg2.ptr, db2.ptr, dout.ptr, dtmp.ptr, 1e-5))
+    gpu.end()
+    assert rel_err(dC.read((M, nout)), ref) < GEMM_TOL
+    assert rel_err(dout.read((M, D)), y1) < 1e-5
+
+
 @pytest.mark.parametrize("M", [1, 7, 14])
 def test_gemm_row_scatter(gpu, M):
     """Output row m lands in row crow[m] (the QKV / GLU write into the cache at pos)."""
