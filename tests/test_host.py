@@ -1,0 +1,248 @@
+"""Host side of the path on the CPU (no GPU calls).
+
+- The product library loads and exports every function include/*.h declares.
+- The product's streaming log-mel front end, resampler, encoder-step bookkeeping and piece text
+  agree with the oracle, and, where oracle/_ref was built from the reference's own sources
+  (src/mel.c, src/resample.c, src/tokenizer.c, src/json.c), with the reference itself.  The same
+  comparison pins oracle/mel_ref.py to the reference's front end.
+- nemoasr_open fails with a message, not a fallback, when no GPU is present.
+"""
+import ctypes as C
+import glob
+import os
+import re
+
+import numpy as np
+import pytest
+
+import mel_ref
+import oracle
+import synth
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+REF_SO = os.path.join(REPO, "oracle", "_ref", "libref_host.so")
+_f32p = C.POINTER(C.c_float)
+
+
+def product():
+    import nemoasr
+
+    return nemoasr.lib()
+
+
+def ref_lib():
+    if not os.path.exists(REF_SO):
+        pytest.skip("oracle/_ref not built (the reference sources are not present)")
+    L = C.CDLL(REF_SO)
+    L.mel_create.restype = C.c_void_p
+    L.mel_destroy.argtypes = [C.c_void_p]
+    L.mel_push.argtypes = [C.c_void_p, _f32p, C.c_size_t, C.c_int, C.POINTER(_f32p), C.POINTER(C.c_size_t)]
+    L.resampler_create.restype = C.c_void_p
+    L.resampler_create.argtypes = [C.c_int, C.c_int]
+    L.resampler_destroy.argtypes = [C.c_void_p]
+    L.resampler_process.restype = C.c_size_t
+    L.resampler_process.argtypes = [C.c_void_p, _f32p, C.c_size_t, _f32p, C.c_size_t]
+    L.resampler_flush.restype = C.c_size_t
+    L.resampler_flush.argtypes = [C.c_void_p, _f32p, C.c_size_t]
+    L.tok_text.restype = C.c_void_p
+    L.tok_text.argtypes = [C.c_void_p, C.c_int]
+    return L
+
+
+# ---- exports -----------------------------------------------------------------------------------
+def declared_functions():
+    names = set()
+    for h in glob.glob(os.path.join(REPO, "include", "*.h")):
+        text = re.sub(r"/\*.*?\*/", "", open(h).read(), flags=re.S)
+        text = re.sub(r"//[^\n]*", "", text)
+        for m in re.finditer(r"^[A-Za-z_][\w \*]*?\b([a-z_][a-z0-9_]*)\s*\([^;{]*\)\s*;", text, flags=re.M):
+            if not m.group(0).lstrip().startswith(("typedef", "return")):
+                names.add(m.group(1))
+    return sorted(names)
+
+
+def test_library_exports_every_declared_function():
+    names = declared_functions()
+    assert len(names) > 40 and "nemoasr_open" in names and "nk_gemm" in names
+    L = product()
+    missing = [n for n in names if not hasattr(L, n)]
+    assert not missing, missing
+
+
+def test_open_without_gpu_fails_loudly(tiny_model_dir):
+    import torch
+
+    if torch.cuda.device_count() > 0:
+        pytest.skip("a GPU is present")
+    L = product()
+    err = C.create_string_buffer(512)
+    h = L.nemoasr_open(tiny_model_dir.encode(), b"en-US", 560, 16000, err, 512)
+    assert not h
+    assert err.value, "nemoasr_open must say why it failed"
+
+
+# ---- log-mel front end -------------------------------------------------------------------------
+def product_mel(x, pieces):
+    L = product()
+    m = L.melfe_create()
+    out, pos = [], 0
+    for i, n in enumerate(pieces):
+        seg = np.ascontiguousarray(x[pos:pos + n], np.float32)
+        pos += n
+        fr, nf = _f32p(), C.c_size_t()
+        L.melfe_push(m, seg.ctypes.data_as(_f32p), seg.size, int(pos >= x.size), C.byref(fr), C.byref(nf))
+        if nf.value:
+            out.append(np.ctypeslib.as_array(fr, shape=(nf.value * 128,)).reshape(-1, 128).copy())
+    L.melfe_destroy(m)
+    return np.concatenate(out) if out else np.zeros((0, 128), np.float32)
+
+
+def ref_mel(R, x, pieces):
+    m = R.mel_create()
+    out, pos = [], 0
+    for n in pieces:
+        seg = np.ascontiguousarray(x[pos:pos + n], np.float32)
+        pos += n
+        fr, nf = _f32p(), C.c_size_t()
+        R.mel_push(m, seg.ctypes.data_as(_f32p), seg.size, int(pos >= x.size), C.byref(fr), C.byref(nf))
+        if nf.value:
+            out.append(np.ctypeslib.as_array(fr, shape=(nf.value * 128,)).reshape(-1, 128).copy())
+    R.mel_destroy(m)
+    return np.concatenate(out) if out else np.zeros((0, 128), np.float32)
+
+
+def split(n, sizes):
+    out, i = [], 0
+    while n > 0:
+        k = min(n, sizes[i % len(sizes)])
+        out.append(k)
+        n -= k
+        i += 1
+    return out or [0]
+
+
+MEL_TOL = 1e-3  # absolute, the reference's own front-end gate (tools/compare.py:19-21)
+
+
+@pytest.mark.parametrize("seconds,sizes", [(1.0, [16000]), (2.3, [1600]), (1.7, [1, 159, 4000, 77]), (0.02, [320])])
+def test_mel_product_vs_oracle(seconds, sizes):
+    x = synth.make_audio(seconds, seed=21)
+    got = product_mel(x, split(x.size, sizes))
+    ref = mel_ref.logmel(x, final=True)
+    assert got.shape == ref.shape
+    assert np.max(np.abs(got - ref)) < MEL_TOL
+
+
+@pytest.mark.parametrize("seconds,sizes", [(1.0, [16000]), (2.3, [1600]), (1.7, [1, 159, 4000, 77]), (0.02, [320])])
+def test_mel_reference_pins_oracle_and_product(seconds, sizes):
+    R = ref_lib()
+    x = synth.make_audio(seconds, seed=22)
+    ref = ref_mel(R, x, split(x.size, sizes))
+    orc = mel_ref.logmel(x, final=True)
+    got = product_mel(x, split(x.size, sizes))
+    assert ref.shape == orc.shape == got.shape
+    assert np.max(np.abs(orc - ref)) < MEL_TOL
+    assert np.max(np.abs(got - ref)) < 1e-5  # measured: bit-identical on these clips
+
+
+def test_mel_partial_stream_matches_reference():
+    """Without the final flush only fully-covered frames come out, in both implementations."""
+    R = ref_lib()
+    x = synth.make_audio(1.0, seed=23)[:12345]
+    m1, m2 = R.mel_create(), product().melfe_create()
+    seg = np.ascontiguousarray(x, np.float32)
+    f1, n1, f2, n2 = _f32p(), C.c_size_t(), _f32p(), C.c_size_t()
+    R.mel_push(m1, seg.ctypes.data_as(_f32p), seg.size, 0, C.byref(f1), C.byref(n1))
+    product().melfe_push(m2, seg.ctypes.data_as(_f32p), seg.size, 0, C.byref(f2), C.byref(n2))
+    assert n1.value == n2.value > 0
+    a = np.ctypeslib.as_array(f1, shape=(n1.value * 128,))
+    b = np.ctypeslib.as_array(f2, shape=(n2.value * 128,))
+    assert np.max(np.abs(a - b)) < MEL_TOL
+    R.mel_destroy(m1)
+    product().melfe_destroy(m2)
+
+
+# ---- resampler ---------------------------------------------------------------------------------
+def run_resampler(create, process, flush, destroy, x, rate, pieces):
+    r = create(rate, 16000)
+    out = []
+    buf = np.zeros(1 << 20, np.float32)
+    pos = 0
+    for n in pieces:
+        seg = np.ascontiguousarray(x[pos:pos + n], np.float32)
+        pos += n
+        k = process(r, seg.ctypes.data_as(_f32p), seg.size, buf.ctypes.data_as(_f32p), buf.size)
+        out.append(buf[:k].copy())
+    k = flush(r, buf.ctypes.data_as(_f32p), buf.size)
+    out.append(buf[:k].copy())
+    destroy(r)
+    return np.concatenate(out)
+
+
+@pytest.mark.parametrize("rate", [8000, 22050, 44100, 48000])
+def test_resampler_matches_reference(rate):
+    R = ref_lib()
+    L = product()
+    rng = np.random.default_rng(rate)
+    x = (0.1 * rng.standard_normal(int(0.7 * rate))).astype(np.float32)
+    pieces = split(x.size, [rate // 10, 333, 1])
+    ref = run_resampler(R.resampler_create, R.resampler_process, R.resampler_flush, R.resampler_destroy, x, rate, pieces)
+    got = run_resampler(L.rsmp_create, L.rsmp_process, L.rsmp_flush, L.rsmp_destroy, x, rate, pieces)
+    assert got.shape == ref.shape
+    assert np.max(np.abs(got - ref)) < 1e-5
+
+
+# ---- token text --------------------------------------------------------------------------------
+PIECES = ["▁the", "s", "▁", "<unk>", "<pad>", "<s>", "</s>", "<en-US>", "<de-DE>", "<xx>", "▁▁a▁b", "ab▁", "<0x41>",
+          "é", "▁日本", "<en-us>", "<en-USA>"]
+
+
+def test_piece_text_matches_reference():
+    R = ref_lib()
+    L = product()
+    arr = (C.c_char_p * len(PIECES))(*[p.encode() for p in PIECES])
+
+    class Vocab(C.Structure):
+        _fields_ = [("pieces", C.POINTER(C.c_char_p)), ("count", C.c_int)]
+
+    v = Vocab(C.cast(arr, C.POINTER(C.c_char_p)), len(PIECES))
+    libc = C.CDLL(None)
+    libc.free.argtypes = [C.c_void_p]
+    for i, p in enumerate(PIECES):
+        t = R.tok_text(C.byref(v), i)
+        want = C.string_at(t)
+        libc.free(t)
+        out = C.create_string_buffer(256)
+        assert L.nemo_piece_text(p.encode(), 0, out, 256) == 0
+        assert out.value == want, p
+
+
+# ---- encoder-step bookkeeping ------------------------------------------------------------------
+@pytest.mark.parametrize("chunk_mel", [8, 56, 112])
+def test_enc_plan_product_vs_oracle(chunk_mel):
+    L = product()
+    for n in (1, 7, 8, 9, 63, 200):
+        for batch in (1, 13, 1000):
+            b = oracle.EncBook(0, 0, 0, 0, 0)
+            st = [0, 0, 0, 0, 0]
+            fed = 0
+            while True:
+                if fed < n:
+                    k = min(batch, n - fed)
+                    fed += k
+                    b.pending_n += k
+                    st[0] += k
+                final = fed >= n
+                while True:
+                    p = oracle.enc_plan(b, final, chunk_mel)
+                    plan = (C.c_int * 8)()
+                    so = (C.c_int * 5)()
+                    ran = L.nemo_enc_plan(plan, st[0], st[1], st[2], st[3], st[4], int(final), chunk_mel, 8, 16, so)
+                    assert ran == p.ran
+                    assert list(plan) == [p.ran, p.take, p.nwin, p.lo, p.hi, p.c, p.include_boundary, p.T3]
+                    st = list(so)
+                    assert st == [b.pending_n, b.consumed, b.emitted, b.mel_cache_n, b.closed]
+                    if not ran:
+                        break
+                if final and b.closed:
+                    break
