@@ -5,17 +5,17 @@
  * (or inside a capture).  Return 0, or -1 with the message in gpu_last_error().
  *
  * These replace the reference's launchers and dispatch sites:
- *   nk_gemm             k_gemm                       src/model.c:148-177 (policy + dispatch)
- *   nk_layernorm        k_layernorm                  src/model.c:184-189
- *   nk_layernorm2       k_layernorm2                 src/model.c:178-183
- *   nk_copy / nk_fill   k_copy / k_fill              src/model.c:190-200
- *   nk_attention_rel    attention_rel dispatch       src/encoder.c:189-194
- *   nk_dwconv_ln_silu   dwconv_ln_silu dispatch      src/encoder.c:201-203
- *   nk_conv2d_c1_s2_relu, nk_dwconv2d_s2, nk_flatten_cf   subsampling dispatches src/encoder.c:150-171
- *   nk_compact          compact_caches               src/encoder.c:230-240 (one launch for all layers)
- *   nk_lstm_cell        lstm_cell dispatch           src/decoder.c:383-385
- *   nk_joint_argmax     joint_partial + argmax_reduce src/decoder.c:393-402
- * and the GPU runtime of src/gpu.h:54-75 (gpu_* below).
+ *   nk_gemm             k_gemm                       src/model.c:70-99 (policy + dispatch)
+ *   nk_layernorm        k_layernorm                  src/model.c:106-111
+ *   nk_layernorm2       k_layernorm2                 src/model.c:100-105
+ *   nk_copy / nk_fill   k_copy / k_fill              src/model.c:112-122
+ *   nk_attention_rel    attention_rel dispatch       src/encoder.c:158-165
+ *   nk_dwconv_ln_silu   dwconv_ln_silu dispatch      src/encoder.c:172-174
+ *   nk_conv2d_c1_s2_relu, nk_dwconv2d_s2, nk_flatten_cf   subsampling dispatches src/encoder.c:120-142
+ *   nk_compact          compact_caches               src/encoder.c:199-211 (one launch for all layers)
+ *   nk_lstm_cell        lstm_cell dispatch           src/decoder.c:71-73
+ *   nk_joint_argmax     joint_partial + argmax_reduce src/decoder.c:79-90
+ * and the GPU runtime of src/gpu.h:20-41 (gpu_* below).
  */
 #ifndef NEMO_KERNELS_H
 #define NEMO_KERNELS_H
@@ -29,7 +29,7 @@ extern "C" {
 typedef struct gpu gpu_t;
 typedef struct gpu_buf gpu_buf_t;
 
-/* ---- runtime (src/gpu.h:54-75) ---------------------------------------------------------------- */
+/* ---- runtime (src/gpu.h:20-41) ---------------------------------------------------------------- */
 gpu_t *gpu_create(char *err, size_t errlen);
 void gpu_destroy(gpu_t *g);
 const char *gpu_device_name(gpu_t *g);

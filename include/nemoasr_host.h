@@ -1,7 +1,7 @@
 /* Host-side pieces of the streaming path exported for CPU tests (no GPU needed):
  *   melfe_*        streaming log-mel front end       (reference src/mel.h:17-23)
  *   rsmp_*         streaming resampler               (reference src/resample.h:9-11)
- *   nemo_enc_plan  encoder step bookkeeping          (reference src/encoder.c:242-280)
+ *   nemo_enc_plan  encoder step bookkeeping          (reference src/encoder.c:213-251)
  *   nemo_piece_text  token piece -> text             (reference src/tokenizer.c:34-50) */
 #ifndef NEMOASR_HOST_H
 #define NEMOASR_HOST_H

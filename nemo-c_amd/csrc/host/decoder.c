@@ -66,7 +66,7 @@ void decoder_destroy(decoder_t *d) {
     free(d);
 }
 
-/* src/decoder.c:360-365 */
+/* src/decoder.c:48-53 */
 void decoder_reset(decoder_t *d) {
     const size_t P = (size_t)d->m->cfg.pred_hidden;
     float *z = calloc(4 * P, sizeof(float));
@@ -86,7 +86,7 @@ double decoder_last_ms(const decoder_t *d) { return d->last_ms; }
 int decoder_last_steps(const decoder_t *d) { return d->last_steps; }
 
 /* prediction network from the committed state, input embed(last_token) or zeros for blank:
- * src/decoder.c:370-389 */
+ * src/decoder.c:57-77 */
 static void encode_pred(decoder_t *d) {
     model_t *m = d->m;
     gpu_t *g = d->g;

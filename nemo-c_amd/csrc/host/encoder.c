@@ -1,6 +1,6 @@
 /* Cache-aware streaming encoder (see encoder.h).
  *
- * Bookkeeping is that of the reference (src/encoder.c:68-296, mirroring NeMo's
+ * Bookkeeping is that of the reference (src/encoder.c:18-267, mirroring NeMo's
  * ConformerStreamingState): a 16-row mel cache, the window/lo/hi rule, append-only per-layer K/V
  * and conv histories compacted once per epoch.  Device side:
  *   - every layer's K/V rows (q | k | v, 3D floats) live in one buffer [n_layers][cap_rows][3D],
@@ -20,7 +20,7 @@
 #include <string.h>
 #include <time.h>
 
-#define MEL_CACHE 16 /* src/encoder.c:39 */
+#define MEL_CACHE 16 /* src/encoder.c:10 */
 #define MAX_GRAPHS 8
 
 static double now_ms(void) {
@@ -65,7 +65,7 @@ struct encoder {
     size_t d_frames, d_cap;
 };
 
-static int sub_len(int n) { return n / 2 + 1; } /* src/encoder.c:147 */
+static int sub_len(int n) { return n / 2 + 1; } /* src/encoder.c:118 */
 
 encoder_t *encoder_create(model_t *m, int right) {
     encoder_t *e = calloc(1, sizeof *e);
@@ -136,7 +136,7 @@ void encoder_destroy(encoder_t *e) {
     free(e);
 }
 
-/* src/encoder.c:121-132: back to the state after create; the conv history rows [0, conv_left)
+/* src/encoder.c:92-103: back to the state after create; the conv history rows [0, conv_left)
  * of every layer read as zeros again */
 void encoder_reset(encoder_t *e) {
     e->pending_n = 0;
@@ -181,7 +181,7 @@ void encoder_push(encoder_t *e, const float *mel, size_t nframes) {
     e->pending_n += nframes;
 }
 
-/* src/encoder.c:242-280: ConformerStreamingState._encode_mel_chunk bookkeeping */
+/* src/encoder.c:213-251: ConformerStreamingState._encode_mel_chunk bookkeeping */
 enc_plan_t enc_plan_step(enc_book_t *b, int final, int chunk_mel, int subsampling, int mel_cache) {
     enc_plan_t p;
     memset(&p, 0, sizeof p);
@@ -216,7 +216,7 @@ enc_plan_t enc_plan_step(enc_book_t *b, int final, int chunk_mel, int subsamplin
     return p;
 }
 
-/* subsampling of the window (nwin mel rows) into pre_out: src/encoder.c:150-171 */
+/* subsampling of the window (nwin mel rows) into pre_out: src/encoder.c:120-142 */
 static void run_pre_encode(encoder_t *e, int nwin) {
     model_t *m = e->m;
     gpu_t *g = e->g;
@@ -234,11 +234,11 @@ static void run_pre_encode(encoder_t *e, int nwin) {
     nk_gemm(g, flat, K, m->pre_out_w, K, m->pre_out_b, gpu_buf_dptr(e->pre_out), D, T3, D, K, NK_ACT_NONE, 0, 1.0f);
 }
 
-/* 24 conformer blocks + prompt + joint projection on the c rows in e->h: src/encoder.c:174-226.
+/* 24 conformer blocks + prompt + joint projection on the c rows in e->h: src/encoder.c:144-197.
  * Cache positions come from the device descriptor.  Every LayerNorm in front of a GEMM runs in
  * that GEMM's prologue: the output norm of block l and the FF1 norm of block l+1 run in block
  * l+1's first GEMM, which also writes the normalised residual into the other residual buffer
- * (the reference's h/t swap, src/encoder.c:209-216). */
+ * (the reference's h/t swap, src/encoder.c:180-187). */
 static void run_blocks(encoder_t *e, int c) {
     model_t *m = e->m;
     gpu_t *g = e->g;
@@ -325,7 +325,7 @@ static gslot_t *graph_slot(encoder_t *e, int c, int nwin, int lo) {
 }
 
 /* Once per epoch: move the live history to the front of the per-layer buffers
- * (src/encoder.c:228-240).  Regions never overlap because cap_rows >= 2*left + cmax. */
+ * (src/encoder.c:199-211).  Regions never overlap because cap_rows >= 2*left + cmax. */
 static void compact_caches(encoder_t *e) {
     const uint32_t D = (uint32_t)e->m->cfg.d_model, nl = (uint32_t)e->m->cfg.n_layers;
     const int src_kv = e->pos - e->cache_len, src_din = e->pos - e->conv_left, dst_din = e->cache_len - e->conv_left;

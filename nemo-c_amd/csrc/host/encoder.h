@@ -32,7 +32,7 @@ const float *encoder_dump_layers(const encoder_t *e);   /* frames x n_layers x d
 const float *encoder_dump_prompted(const encoder_t *e); /* frames x d_model */
 const float *encoder_dump_joint(const encoder_t *e);    /* frames x joint_hidden */
 
-/* Bookkeeping of one step (src/encoder.c:242-280), exposed for host-side tests. */
+/* Bookkeeping of one step (src/encoder.c:213-251), exposed for host-side tests. */
 typedef struct {
     size_t pending_n, consumed, emitted;
     int mel_cache_n, closed;

@@ -28,7 +28,7 @@ static char *slurp(const char *path, size_t *len) {
     return b;
 }
 
-/* src/model.c:203-249: configuration keys, defaults and the supported-architecture checks */
+/* src/model.c:125-172: configuration keys, defaults and the supported-architecture checks */
 static int parse_cfg(model_t *m, char *err, size_t errlen) {
     const jn_t *c = m->config, *enc = jn_get(c, "encoder"), *pre = jn_get(c, "preprocessor");
     const jn_t *pr = jn_get(c, "prompt"), *dec = jn_get(c, "decoder"), *jo = jn_get(c, "joint");
@@ -112,7 +112,7 @@ static void addf(reqs_t *r, const char *name, size_t numel, const float **dst) {
     r->nf++;
 }
 
-/* src/model.c:119-125: tensor present, BF16, and (if given) with the expected element count */
+/* src/model.c:41-47: tensor present, BF16, and (if given) with the expected element count */
 static const st_entry_t *need(const st_map_t *st, const char *name, size_t numel, char *err, size_t errlen) {
     const st_entry_t *t = st_lookup(st, name);
     if (!t) { snprintf(err, errlen, "missing tensor %s", name); return NULL; }
@@ -172,7 +172,7 @@ model_t *model_load(const char *dir, char *err, size_t errlen) {
 #define LF(suffix, numel, dst) do { snprintf(n, sizeof n, "encoder.layers.%zu.%s", l, suffix); addf(&r, n, numel, dst); } while (0)
         LB("feed_forward1.linear1.weight", FF * D, &L->ff1_w1);
         LB("feed_forward1.linear2.weight", D * FF, &L->ff1_w2);
-        /* q, k, v consecutive: one [3D][D] matrix (src/model.c:318-320) */
+        /* q, k, v consecutive: one [3D][D] matrix (src/model.c:240-242) */
         LB("self_attn.linear_q.weight", D * D, &L->wqkv);
         LB("self_attn.linear_k.weight", D * D, &qkv_tail);
         LB("self_attn.linear_v.weight", D * D, &qkv_tail);
@@ -272,7 +272,7 @@ model_t *model_load(const char *dir, char *err, size_t errlen) {
     m->b0_eff_buf = gpu_buf_alloc(m->gpu, PH * sizeof(float));
     m->prompt_b0_eff = gpu_buf_dptr(m->b0_eff_buf);
 
-    /* relative position tables (src/model.c:364-384): sinusoid rows for positions Lmax-1 .. -(Lmax-1)
+    /* relative position tables (src/model.c:286-306): sinusoid rows for positions Lmax-1 .. -(Lmax-1)
        in double on the host, then ptab[l] = pe . wpos[l]^T on the GPU */
     {
         const int Pr = 2 * m->Lmax - 1;
@@ -330,7 +330,7 @@ fail:
     return NULL;
 }
 
-/* src/model.c:390-400: the one-hot prompt folds into the first prompt layer's bias,
+/* src/model.c:312-322: the one-hot prompt folds into the first prompt layer's bias,
  * b_eff = b0 + W0[:, D + idx], in f32 on the host, uploaded once. */
 int model_set_language(model_t *m, const char *lang, char *err, size_t errlen) {
     const int idx = model_prompt_index(m, lang);

@@ -1,7 +1,7 @@
 /* Model configuration and weights resident in HBM.
  *
  * Reads config.json and model.safetensors with the keys, tensor names and checks of the reference
- * (src/model.c:119-145 tensor checks, :203-249 config, :293-360 tensor list, :364-384 position
+ * (src/model.c:41-67 tensor checks, :125-172 config, :215-282 tensor list, :286-306 position
  * table, :390-400 prompt fold).  Layout on the device:
  *   - one bf16 weight arena, 4 KB-aligned matrices, in the order a chunk reads them
  *     (pre-encode, then per layer ff1, qkv, out, pw1, pw2, ff2, then prompt, joint, decoder);

@@ -1,4 +1,4 @@
-/* Library API (include/nemoasr.h): the reference's src/nemoasr.c:58-261 behaviour on the HIP
+/* Library API (include/nemoasr.h): the reference's src/nemoasr.c:1-202 behaviour on the HIP
  * backend, plus the test hooks of include/nemoasr_debug.h. */
 #include "nemoasr.h"
 #include "nemoasr_debug.h"
@@ -64,7 +64,7 @@ int nemoasr_default_model_dir(char *out, size_t n) {
     return found ? 0 : -1;
 }
 
-/* latency -> right context (src/nemoasr.c:117-123) */
+/* latency -> right context (src/nemoasr.c:58-64) */
 static int right_for(int latency_ms) {
     static const int ms[] = { 80, 160, 320, 560, 1120 }, r[] = { 0, 1, 3, 6, 13 };
     for (size_t i = 0; i < sizeof ms / sizeof *ms; ++i)
@@ -156,7 +156,7 @@ static void keep_tokens(nemoasr_t *s, const int *t, int n) {
     s->n_tok += (size_t)n;
 }
 
-/* every ready chunk: encoder step, then the decoder over its frames (src/nemoasr.c:171-191) */
+/* every ready chunk: encoder step, then the decoder over its frames (src/nemoasr.c:112-132) */
 static int run_pending(nemoasr_t *s, int final, int *new_tokens, char *err, size_t errlen) {
     enc_out_t out;
     int rc, total = 0;

@@ -1,5 +1,5 @@
 /* Read-only safetensors access (memory-mapped), load time only.  The file format and the tensor
- * names are the checkpoint contract of the reference (src/safetensors.h, src/model.c:293-360). */
+ * names are the checkpoint contract of the reference (src/safetensors.h, src/model.c:215-282). */
 #ifndef NEMO_SAFETENSORS_H
 #define NEMO_SAFETENSORS_H
 #include <stddef.h>

@@ -16,7 +16,7 @@
  * LayerNorm).  With ln_out set, workgroup 0's first wavefront also writes LN(A; g1,b1) there: the
  * residual stream after a block's output norm (reference src/encoder.c:180-187).
  * Replaces gemm_spec (reference src/kernels.metal:51-118) plus the layernorm / layernorm2
- * launches in front of it (src/encoder.c:184-188, :198, :206, :210-215). */
+ * launches in front of it (src/encoder.c:155, :159, :169, :177, :180-186). */
 #include "nk_common.h"
 
 template <int CTRL>

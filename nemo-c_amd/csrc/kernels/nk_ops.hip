@@ -64,7 +64,7 @@ extern "C" __global__ __launch_bounds__(256) void fill_f32(const NkFillArgs a) {
     if (i < a.n) a.dst[i] = a.value;
 }
 
-/* Epoch compaction of the per-layer caches in one launch (reference src/encoder.c:230-240 issues
+/* Epoch compaction of the per-layer caches in one launch (reference src/encoder.c:199-211 issues
  * one copy per layer and cache).  grid = (ceil(rows*cols/256), nbuf).  Source and destination rows
  * never overlap (the host checks src_row >= dst_row + rows). */
 extern "C" __global__ __launch_bounds__(256) void compact_rows(const NkCompactArgs a) {

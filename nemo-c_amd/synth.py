@@ -1,8 +1,8 @@
 """Seeded synthetic checkpoint and audio for the streaming FastConformer-RNNT path.
 
 The checkpoint follows the tensor names, shapes and dtype (BF16) that the loader enforces
-(reference: src/model.c:119-125 `need`, src/model.c:293-360 tensor list) and the
-config.json keys it reads (src/model.c:203-249).  Weights are random: matrices
+(reference: src/model.c:41-47 `need`, src/model.c:215-282 tensor list) and the
+config.json keys it reads (src/model.c:125-172).  Weights are random: matrices
 N(0, 1/fan_in), LayerNorm gamma ~1 / beta ~0, small biases.  The joint output bias of the
 blank class can be raised to give a chosen blank probability.
 

@@ -103,7 +103,7 @@ size_t or_session_joint_log(const or_session_t *s, const int **best, const float
 /* For tests of compaction-independence: the epoch length in chunks (reference CACHE_EPOCH_CHUNKS). */
 const char *or_session_error(const or_session_t *s);
 
-/* Encoder-step bookkeeping alone (reference src/encoder.c:242-280): given the state, decide the
+/* Encoder-step bookkeeping alone (reference src/encoder.c:213-251): given the state, decide the
    next step. Exposed so host bookkeeping can be compared step by step. */
 typedef struct {
     size_t pending_n, consumed, emitted;

@@ -27,7 +27,7 @@ float or_sigmoid(float v) { return 1.0f / (1.0f + expf(-v)); }
 float or_silu(float v) { return v / (1.0f + expf(-v)); }
 
 /* GEMM with fused epilogue: src/kernels.metal:9-48 (gemm_bf16), :51-118 (gemm_spec), :120-208
- * (gemm_mma); semantics of the epilogue at :95-117 and :179-206; parameters from src/model.c:148-177.
+ * (gemm_mma); semantics of the epilogue at :95-117 and :179-206; parameters from src/model.c:70-99.
  *   act 0/1/2: C[m][n] (=|+=) alpha * act(sum_k A[m][k] W[n][k] + bias[n])
  *   act 3 (GLU): N is the full weight height, output width N/2:
  *                C[m][j] (=|+=) (sa_j + b_j) * sigmoid(sb_{j+N/2} + b_{j+N/2}) * alpha
@@ -241,7 +241,7 @@ int or_joint_argmax(const float *enc, const float *pred, const uint16_t *W, cons
     return bi;
 }
 
-/* Relative positional table: src/model.c:364-384.  pe rows r = 0..2*Lmax-2 hold position
+/* Relative positional table: src/model.c:286-306.  pe rows r = 0..2*Lmax-2 hold position
  * Lmax-1-r: pe[r][2i] = sin(pos * div_i), pe[r][2i+1] = cos(pos * div_i),
  * div_i = exp(2i * -(ln 10000 / D)), computed in double and rounded to f32; then
  * ptab = pe . wpos^T with the GEMM above. */

@@ -16,7 +16,7 @@
 #include <stdlib.h>
 #include <string.h>
 
-#define OR_MEL_CACHE 16      /* src/encoder.c:39 */
+#define OR_MEL_CACHE 16      /* src/encoder.c:10 */
 #define OR_DEC_MAX_BATCH 16  /* src/kernel_params.h:17 */
 
 static inline float bf(uint16_t v) {
@@ -33,7 +33,7 @@ static float *widen(const uint16_t *src, size_t n) {
 typedef struct {
     float *ln_ff1_g, *ln_ff1_b, *ln_att_g, *ln_att_b, *ln_conv_g, *ln_conv_b, *ln_ff2_g, *ln_ff2_b, *ln_out_g, *ln_out_b;
     float *bn_g, *bn_b, *dw_w, *bias_u, *bias_v, *ptab;
-    uint16_t *wqkv; /* [3D][D]: q, k, v rows stacked (src/model.c:318-320) */
+    uint16_t *wqkv; /* [3D][D]: q, k, v rows stacked (src/model.c:240-242) */
 } or_layer_t;
 
 struct or_model {
@@ -54,10 +54,10 @@ or_model_t *or_model_create(const or_dims_t *dims, const or_global_w_t *g, const
     const size_t D = (size_t)d->d_model, CH = (size_t)d->sub_channels;
     m->lw = malloc(sizeof(or_layer_w_t) * (size_t)d->n_layers);
     memcpy(m->lw, layers, sizeof(or_layer_w_t) * (size_t)d->n_layers);
-    /* src/model.c:246: Lmax = att_left + max trained right context + 1 + 2 */
+    /* src/model.c:168: Lmax = att_left + max trained right context + 1 + 2 */
     m->Lmax = d->att_left + d->max_right + 1 + 2;
     int f = d->feat_in;
-    for (int i = 0; i < 3; ++i) f = f / 2 + 1; /* src/model.c:304-306 */
+    for (int i = 0; i < 3; ++i) f = f / 2 + 1; /* src/model.c:226-228 */
     m->sub_freq_out = f;
     m->conv0_w = widen(g->conv0_w, CH * 9); m->conv0_b = widen(g->conv0_b, CH);
     m->conv2_w = widen(g->conv2_w, CH * 9); m->conv2_b = widen(g->conv2_b, CH);
@@ -113,7 +113,7 @@ void or_model_free(or_model_t *m) {
     free(m);
 }
 
-/* src/model.c:390-400: the one-hot prompt folds into the first prompt layer's bias:
+/* src/model.c:312-322: the one-hot prompt folds into the first prompt layer's bias:
  * b_eff[n] = b0[n] + W0[n][D + idx], both widened from bf16, summed in f32. */
 int or_model_set_language(or_model_t *m, int idx) {
     if (idx < 0 || idx >= m->d.num_prompts) return -1;
@@ -129,7 +129,7 @@ int or_model_lmax(const or_model_t *m) { return m->Lmax; }
 struct or_session {
     or_model_t *m;
     int right, chunk_frames, chunk_mel, cmax;
-    /* encoder bookkeeping (src/encoder.c:47-66) */
+    /* encoder bookkeeping (src/encoder.c:39-82) */
     float *pending;
     size_t pending_n, pending_cap;
     float mel_cache[OR_MEL_CACHE * 128];
@@ -140,7 +140,7 @@ struct or_session {
     float **k_hist, **v_hist; /* [att_left][D] each, oldest first */
     int hist_len;
     float **conv_hist;        /* [conv_kernel-1][D], oldest first; zeros at start */
-    /* decoder state (src/decoder.c:326-335) */
+    /* decoder state (src/decoder.c:14-41) */
     float *h[2], *c[2], *hp[2], *cp[2], *pred_out;
     int last_token, pred_valid;
     /* stats + dumps */
@@ -161,9 +161,9 @@ or_session_t *or_session_create(or_model_t *m, int right) {
     s->m = m;
     const or_dims_t *d = &m->d;
     s->right = right;
-    s->chunk_frames = right + 1;                      /* src/encoder.c:72-73 */
+    s->chunk_frames = right + 1;                      /* src/encoder.c:43-44 */
     s->chunk_mel = s->chunk_frames * d->subsampling;
-    s->cmax = s->chunk_frames + 2;                     /* src/encoder.c:74 (final boundary window) */
+    s->cmax = s->chunk_frames + 2;                     /* src/encoder.c:45-46 (final boundary window) */
     if (s->cmax < 16) s->cmax = 16;
     const size_t D = (size_t)d->d_model;
     s->k_hist = calloc((size_t)d->n_layers, sizeof(float *));
@@ -196,7 +196,7 @@ void or_session_free(or_session_t *s) {
     free(s);
 }
 
-/* src/encoder.c:121-132 + src/decoder.c:360-365 */
+/* src/encoder.c:92-103 + src/decoder.c:48-53 */
 void or_session_reset(or_session_t *s) {
     const or_dims_t *d = &s->m->d;
     const size_t D = (size_t)d->d_model, P = (size_t)d->pred_hidden;
@@ -229,9 +229,9 @@ size_t or_session_joint_log(const or_session_t *s, const int **best, const float
     return s->jl_n;
 }
 
-static int sub_len(int n) { return n / 2 + 1; } /* src/encoder.c:147 */
+static int sub_len(int n) { return n / 2 + 1; } /* src/encoder.c:118 */
 
-/* src/encoder.c:242-280: which pending mel rows the next step consumes and which encoder rows
+/* src/encoder.c:213-251: which pending mel rows the next step consumes and which encoder rows
  * [lo, hi) of the subsampled window it emits (ConformerStreamingState bookkeeping). */
 or_enc_plan_t or_enc_plan(or_enc_book_t *b, int final, int chunk_mel, int subsampling, int mel_cache) {
     or_enc_plan_t p;
@@ -276,7 +276,7 @@ static void dump_grow(or_session_t *s, size_t rows_needed) {
     s->d_cap = cap;
 }
 
-/* pre-encode of a window of nwin mel rows: src/encoder.c:150-171; returns T3 rows in out */
+/* pre-encode of a window of nwin mel rows: src/encoder.c:120-142; returns T3 rows in out */
 static int pre_encode(or_session_t *s, const float *win, int nwin, float **out) {
     or_model_t *m = s->m;
     const or_dims_t *d = &m->d;
@@ -302,7 +302,7 @@ static int pre_encode(or_session_t *s, const float *win, int nwin, float **out) 
     return T3;
 }
 
-/* 24 conformer blocks + prompt + joint encoder projection on c rows: src/encoder.c:174-226.
+/* 24 conformer blocks + prompt + joint encoder projection on c rows: src/encoder.c:144-197.
  * Writes joint_enc [c][joint_hidden] (and prompted [c][D]). */
 static void run_blocks(or_session_t *s, float *h, int c, float *prompted, float *joint_enc, float *dump_layers) {
     or_model_t *m = s->m;
@@ -318,11 +318,11 @@ static void run_blocks(or_session_t *s, float *h, int c, float *prompted, float 
     for (int l = 0; l < d->n_layers; ++l) {
         or_layer_t *W = &m->L[l];
         const or_layer_w_t *w = &m->lw[l];
-        /* FF1 half step; for l > 0 the LN was produced by the previous paired LN (src/encoder.c:183-186) */
+        /* FF1 half step; for l > 0 the LN was produced by the previous paired LN (src/encoder.c:154-157) */
         if (l == 0) or_layernorm(h, W->ln_ff1_g, W->ln_ff1_b, t2, c, D, eps);
         or_gemm(t2, D, w->ff1_w1, D, NULL, ff, FF, c, FF, D, OR_ACT_SILU, 0, 1.0f);
         or_gemm(ff, FF, w->ff1_w2, FF, NULL, h, D, c, D, FF, OR_ACT_NONE, 1, 0.5f);
-        /* attention (src/encoder.c:187-195) */
+        /* attention (src/encoder.c:158-166) */
         or_layernorm(h, W->ln_att_g, W->ln_att_b, t, c, D, eps);
         or_gemm(t, D, W->wqkv, D, NULL, qkv, 3 * D, c, 3 * D, D, OR_ACT_NONE, 0, 1.0f);
         memcpy(Kall, s->k_hist[l], rowb * (size_t)s->hist_len);
@@ -334,18 +334,18 @@ static void run_blocks(or_session_t *s, float *h, int c, float *prompted, float 
         or_attention_rel(qkv, 3 * D, Kall, Vall, D, W->ptab, W->bias_u, W->bias_v, att, c, L, m->Lmax, H, dh, D,
                          1.0f / sqrtf((float)dh));
         or_gemm(att, D, w->wo, D, NULL, h, D, c, D, D, OR_ACT_NONE, 1, 1.0f);
-        /* keep the last min(L, att_left) rows as the next chunk's K/V cache (src/encoder.c:225) */
+        /* keep the last min(L, att_left) rows as the next chunk's K/V cache (src/encoder.c:196) */
         const int keep = L < d->att_left ? L : d->att_left;
         memmove(s->k_hist[l], Kall + (size_t)(L - keep) * D, rowb * (size_t)keep);
         memmove(s->v_hist[l], Vall + (size_t)(L - keep) * D, rowb * (size_t)keep);
-        /* convolution module (src/encoder.c:196-204) */
+        /* convolution module (src/encoder.c:167-175) */
         or_layernorm(h, W->ln_conv_g, W->ln_conv_b, t, c, D, eps);
         memcpy(din, s->conv_hist[l], rowb * (size_t)ch);
         or_gemm(t, D, w->pw1, D, NULL, din + (size_t)ch * D, D, c, 2 * D, D, OR_ACT_GLU, 0, 1.0f);
         or_dwconv_ln_silu(din, W->dw_w, W->bn_g, W->bn_b, y, c, D, taps, eps);
         memcpy(s->conv_hist[l], din + (size_t)c * D, rowb * (size_t)ch);
         or_gemm(y, D, w->pw2, D, NULL, h, D, c, D, D, OR_ACT_NONE, 1, 1.0f);
-        /* FF2 half step + output norm (src/encoder.c:205-216) */
+        /* FF2 half step + output norm (src/encoder.c:176-187) */
         or_layernorm(h, W->ln_ff2_g, W->ln_ff2_b, t, c, D, eps);
         or_gemm(t, D, w->ff2_w1, D, NULL, ff, FF, c, FF, D, OR_ACT_SILU, 0, 1.0f);
         or_gemm(ff, FF, w->ff2_w2, FF, NULL, h, D, c, D, FF, OR_ACT_NONE, 1, 0.5f);
@@ -360,7 +360,7 @@ static void run_blocks(or_session_t *s, float *h, int c, float *prompted, float 
             for (int i = 0; i < c; ++i) memcpy(dump_layers + ((size_t)i * d->n_layers + l) * D, h + (size_t)i * D, rowb);
     }
     s->hist_len = L < d->att_left ? L : d->att_left;
-    /* prompt (one-hot folded into the bias) + joint encoder projection (src/encoder.c:218-223) */
+    /* prompt (one-hot folded into the bias) + joint encoder projection (src/encoder.c:189-194) */
     const int PH = d->prompt_hidden, NP = d->num_prompts, JH = d->joint_hidden;
     float *ph = malloc(sizeof(float) * (size_t)c * PH);
     or_gemm(h, D, m->g.prompt_w0, D + NP, m->b0_eff, ph, PH, c, PH, D, OR_ACT_RELU, 0, 1.0f);
@@ -370,7 +370,7 @@ static void run_blocks(or_session_t *s, float *h, int c, float *prompted, float 
     free(t); free(t2); free(ff); free(qkv); free(att); free(y); free(Kall); free(Vall); free(din);
 }
 
-/* prediction network: src/decoder.c:370-389 */
+/* prediction network: src/decoder.c:57-77 */
 static void encode_pred(or_session_t *s) {
     or_model_t *m = s->m;
     const or_dims_t *d = &m->d;
@@ -401,7 +401,7 @@ static void jlog(or_session_t *s, int best, float margin) {
     s->jl_n++;
 }
 
-/* greedy RNNT over `frames` rows of joint_enc: src/decoder.c:404-439 */
+/* greedy RNNT over `frames` rows of joint_enc: src/decoder.c:92-127 */
 static int decode(or_session_t *s, const float *joint_enc, int frames, int *out, int max_out) {
     or_model_t *m = s->m;
     const or_dims_t *d = &m->d;
@@ -462,7 +462,7 @@ int or_session_feed_mel(or_session_t *s, const float *mel, size_t nframes, int f
         const int cache_before = s->mel_cache_n;
         or_enc_plan_t p = or_enc_plan(&b, final, s->chunk_mel, d->subsampling, OR_MEL_CACHE);
         if (!p.ran) { s->closed = b.closed; break; }
-        /* window = mel cache ++ the consumed pending rows (src/encoder.c:252-256) */
+        /* window = mel cache ++ the consumed pending rows (src/encoder.c:223-227) */
         float *win = malloc(sizeof(float) * (size_t)p.nwin * NM);
         memcpy(win, s->mel_cache, sizeof(float) * (size_t)cache_before * NM);
         memcpy(win + (size_t)cache_before * NM, s->pending, sizeof(float) * (size_t)p.take * NM);

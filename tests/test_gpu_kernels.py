@@ -53,7 +53,7 @@ def run_gemm(gpu, A, W, bias, act, acc, alpha, C0=None, ldw=None, K=None, kind=0
     return out
 
 
-# (N, K, act, accumulate, alpha, bias, ldw) at the model's shapes (src/encoder.c:150-223, decoder.c:381-388)
+# (N, K, act, accumulate, alpha, bias, ldw) at the model's shapes (src/encoder.c:120-194, decoder.c:69-76)
 SHAPES = [
     (4096, 1024, 1, 0, 1.0, False, None),   # FF up + SiLU
     (1024, 4096, 0, 1, 0.5, False, None),   # FF down, half-step residual

@@ -1,6 +1,6 @@
 """Pins the oracle's streaming bookkeeping and decoder (oracle/oracle_stream.c) on the CPU.
 
-- The window / lo / hi rule (reference src/encoder.c:242-280) emits, over a whole stream, exactly
+- The window / lo / hi rule (reference src/encoder.c:213-251) emits, over a whole stream, exactly
   the frames of an offline subsampling of all mel frames, contiguously and in order; and the
   subsampled rows a chunk emits equal the offline rows (the 16-row mel cache covers the causal
   receptive field).  Offline reference: torch conv2d with the same causal padding.
@@ -164,7 +164,7 @@ def greedy_one_frame(om, joint_enc):
 @pytest.mark.parametrize("right", [0, 6])
 def test_decoder_equals_one_frame_greedy(right):
     """Chunking does not enter the greedy loop: the state carries across chunks and the symbol
-    count restarts at every frame (src/decoder.c:96-119), so one pass over all frames must agree."""
+    count restarts at every frame (src/decoder.c:97-123), so one pass over all frames must agree."""
     om = oracle.Model(model_dir("tiny"))
     mel = mel_ref.logmel(synth.make_audio(1.5, seed=5))
     s = _session_outputs(om, right, mel, mel.shape[0])
