@@ -47,6 +47,13 @@ int gpu_timing_set(gpu_t *g, const char *kernel, int max_launches);
 /* mean duration (ms), launch count and summed algorithmic bytes of the timed launches */
 int gpu_timing_collect(gpu_t *g, double *mean_ms, int *count, double *bytes);
 uint64_t gpu_launch_count(const gpu_t *g);
+/* hipGraph capture of the launches between capture_begin and capture_end (inside begin/end);
+ * gpu_graph_launch replays it on the stream. */
+typedef struct gpu_graph gpu_graph_t;
+int gpu_capture_begin(gpu_t *g);
+gpu_graph_t *gpu_capture_end(gpu_t *g);
+int gpu_graph_launch(gpu_t *g, gpu_graph_t *gr);
+void gpu_graph_free(gpu_graph_t *gr);
 
 /* ---- GEMM ------------------------------------------------------------------------------------
  * C[m][n] (= or +=) alpha * act(sum_k A[m][k] W[n][k] + bias[n]); W bf16 [N][ldw]; act 0 none,

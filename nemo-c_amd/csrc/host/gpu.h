@@ -74,6 +74,13 @@ int gpu_timing_collect(gpu_t *g, double *mean_ms, int *count, double *bytes);
 /* Algorithmic HBM bytes of the next launch (recorded with its timing). */
 void gpu_next_bytes(gpu_t *g, double bytes);
 
+/* Device constant tables: the row indices 0..GPU_IOTA_N-1 and GPU_ZEROS_N zero floats (kernels
+ * whose row map or bias is optional get these instead of NULL). */
+#define GPU_IOTA_N 4096
+#define GPU_ZEROS_N 8192
+const int *gpu_iota(gpu_t *g);
+const float *gpu_zeros(gpu_t *g);
+
 /* Number of kernel launches issued since creation (for tests and the launch-count check). */
 uint64_t gpu_launch_count(const gpu_t *g);
 

@@ -5,6 +5,12 @@
 #include <stdlib.h>
 #include <string.h>
 
+/* HIP extension (hip/hip_ext.h, which is C++-only): a module launch whose start / stop events
+ * are stamped by the dispatch packet itself. */
+hipError_t hipExtModuleLaunchKernel(hipFunction_t f, uint32_t gx, uint32_t gy, uint32_t gz, uint32_t lx, uint32_t ly,
+                                    uint32_t lz, size_t shared, hipStream_t stream, void **params, void **extra,
+                                    hipEvent_t start, hipEvent_t stop, uint32_t flags);
+
 /* gfx950 code object linked into the library (co_blob.S) */
 extern const unsigned char nk_code_object_start[];
 extern const unsigned char nk_code_object_end[];
@@ -28,6 +34,9 @@ struct gpu {
     uint32_t *counters;
     size_t ncounters;
     uint64_t launches;
+    /* constant tables for kernels that take no optional pointers: rows 0..GPU_IOTA_N-1 and zeros */
+    int *iota;
+    float *zeros;
     /* per-kernel timing */
     char timed[48];
     hipEvent_t *tev;
@@ -86,8 +95,23 @@ gpu_t *gpu_create(char *err, size_t errlen) {
         free(g);
         return NULL;
     }
+    int *iota = malloc(GPU_IOTA_N * sizeof(int));
+    for (int i = 0; i < GPU_IOTA_N; ++i) iota[i] = i;
+    if ((e = hipMalloc((void **)&g->iota, GPU_IOTA_N * sizeof(int))) != hipSuccess ||
+        (e = hipMemcpy(g->iota, iota, GPU_IOTA_N * sizeof(int), hipMemcpyHostToDevice)) != hipSuccess ||
+        (e = hipMalloc((void **)&g->zeros, GPU_ZEROS_N * sizeof(float))) != hipSuccess ||
+        (e = hipMemset(g->zeros, 0, GPU_ZEROS_N * sizeof(float))) != hipSuccess) {
+        snprintf(err, errlen, "constant tables: %s", hipGetErrorString(e));
+        free(iota);
+        gpu_destroy(g);
+        return NULL;
+    }
+    free(iota);
     return g;
 }
+
+const int *gpu_iota(gpu_t *g) { return g->iota; }
+const float *gpu_zeros(gpu_t *g) { return g->zeros; }
 
 void gpu_destroy(gpu_t *g) {
     if (!g) return;
@@ -99,6 +123,8 @@ void gpu_destroy(gpu_t *g) {
     }
     if (g->ws) hipFree(g->ws);
     if (g->counters) hipFree(g->counters);
+    if (g->iota) hipFree(g->iota);
+    if (g->zeros) hipFree(g->zeros);
     hipEventDestroy(g->ev0);
     hipEventDestroy(g->ev1);
     hipStreamDestroy(g->stream);
@@ -203,12 +229,15 @@ int gpu_launch(gpu_t *g, const char *kernel, const void *args, size_t args_size,
     void *config[] = { HIP_LAUNCH_PARAM_BUFFER_POINTER, (void *)args, HIP_LAUNCH_PARAM_BUFFER_SIZE, &sz,
                        HIP_LAUNCH_PARAM_END };
     const int timed = !g->capturing && g->tev && g->tn < g->tmax && timed_name(g->timed, kernel);
-    if (timed) hipEventRecord(g->tev[2 * g->tn], g->stream);
-    hipError_t e = hipModuleLaunchKernel(f, gx, gy, gz, bx, by, bz, 0, g->stream, NULL, config);
+    hipError_t e;
     if (timed) {
-        hipEventRecord(g->tev[2 * g->tn + 1], g->stream);
+        /* the start / stop events are stamped by the dispatch itself: the kernel's execution time */
+        e = hipExtModuleLaunchKernel(f, gx * bx, gy * by, gz * bz, bx, by, bz, 0, g->stream, NULL, config,
+                                     g->tev[2 * g->tn], g->tev[2 * g->tn + 1], 0);
         g->tbytes[g->tn] = g->next_bytes;
         g->tn++;
+    } else {
+        e = hipModuleLaunchKernel(f, gx, gy, gz, bx, by, bz, 0, g->stream, NULL, config);
     }
     g->next_bytes = 0.0;
     g->launches++;

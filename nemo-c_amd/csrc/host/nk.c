@@ -20,16 +20,47 @@ static int bad(gpu_t *g, const char *what) { return gpu_fail(g, what); }
 
 static int aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 
-enum { K_GEMV1 = 1, K_FR = 2, K_MR = 3, K_GEMV = 4 };
+enum { K_FR = 2, K_MR = 3, K_GEMV = 4 };
+
+/* few-row MFMA kernel plan: W wavefronts of SPW K steps (32 wide) per workgroup, K split over KS
+ * workgroups (KS > 1 only for accumulating GEMMs with no bias and no activation, whose partial
+ * products are added into C atomically; it puts four times as many workgroups on the small-N
+ * matrices). */
+typedef struct { uint32_t W, SPW, KS; } fr_plan_t;
+
+static int fr_ok(uint32_t M, uint32_t K, int act) {
+    return M <= NK_FEW_ROWS && K % 32 == 0 && K <= 4608 && (act != NK_ACT_GLU || K <= 1024);
+}
+
+static fr_plan_t fr_plan(uint32_t nout, uint32_t K, int act, int accumulate, int has_bias, int ln) {
+    const uint32_t S = K / 32;
+    fr_plan_t p = { 4, 8, 1 };
+    if (ln || act == NK_ACT_GLU) return p;
+    if (accumulate && act == NK_ACT_NONE && !has_bias && (nout + 15) / 16 < 128 && S % 4 == 0 && S / 4 <= 32) {
+        p.KS = 4;
+        p.SPW = S / 4 <= 8 ? 2 : 8;
+        return p;
+    }
+    if (S <= 32) return p;
+    if (S <= 64) { p.W = 8; return p; }
+    p.W = 16;
+    p.SPW = S <= 128 ? 8 : 9;
+    return p;
+}
+
+static const char *fr_name(fr_plan_t p, int act, int ln) {
+    static char buf[40];
+    snprintf(buf, sizeof buf, "gemm_fr%s%s_w%us%u", ln ? "_ln" : "", act == NK_ACT_GLU ? "_glu" : "", p.W, p.SPW);
+    return buf;
+}
 
 static int pick(uint32_t M, uint32_t K, int act) {
-    if (g_force == K_GEMV1 && M <= 4) return K_GEMV1;
-    if (g_force == K_FR && M <= NK_FEW_ROWS && K % 32 == 0) return K_FR;
-    if (g_force == K_MR && act != NK_ACT_GLU && K % 32 == 0) return K_MR;
     const int gemv_ok = (M <= 2 && K <= 64 * 8 * 9) || (M <= 4 && K <= 64 * 8 * 2);
-    if (g_force == K_GEMV && gemv_ok) return K_GEMV;
+    if ((g_force == K_GEMV || g_force == 1) && gemv_ok) return K_GEMV;
+    if (g_force == K_FR && fr_ok(M, K, act)) return K_FR;
+    if (g_force == K_MR && act != NK_ACT_GLU && K % 32 == 0) return K_MR;
     if (gemv_ok) return K_GEMV;
-    if (M <= NK_FEW_ROWS) return K_FR;
+    if (fr_ok(M, K, act)) return K_FR;
     return K_MR;
 }
 
@@ -46,14 +77,11 @@ const char *nk_gemm_kernel_name(uint32_t M, uint32_t N, uint32_t K, int act) {
     static char buf[32];
     uint32_t kch, nc;
     switch (pick(M, K, act)) {
-    case K_GEMV1:
-        snprintf(buf, sizeof buf, "gemv_r%u_c%u", M, (act == NK_ACT_GLU || K <= 2048) ? 2u : 1u);
-        return buf;
     case K_GEMV:
         gemv_shape(N, K, act, &kch, &nc);
         snprintf(buf, sizeof buf, "gemv_r%u_n%u_k%u", M, nc, kch);
         return buf;
-    case K_FR: return "gemm_fr";
+    case K_FR: return fr_name(fr_plan(act == NK_ACT_GLU ? N / 2 : N, K, act, 0, 1, 0), act, 0);
     default: return "gemm_mr";
     }
 }
@@ -77,7 +105,9 @@ static int gemm_core(gpu_t *g, const float *A, uint32_t lda, const uint16_t *W, 
     const uint32_t nout = act == NK_ACT_GLU ? N / 2 : N;
     if (ldc < nout) return bad(g, "gemm: ldc < output width");
     const int kind = pick(M, K, act);
-    if (ln && ln->mode && (kind != K_GEMV || K > 64 * 8 * 2)) {
+    const int ln_fused = ln && ln->mode && K == lda &&
+                         ((kind == K_GEMV && K <= 1024) || (kind == K_FR && K == 1024 && M <= 16));
+    if (ln && ln->mode && !ln_fused) {
         /* unfused LayerNorm: out = LN1(A) (if requested), tmp = LN(...) feeds the GEMM */
         if (!ln->tmp || K != lda) return bad(g, "gemm: LayerNorm prologue needs a scratch buffer");
         if (ln->mode == 2) {
@@ -103,6 +133,10 @@ static int gemm_core(gpu_t *g, const float *A, uint32_t lda, const uint16_t *W, 
     gpu_next_bytes(g, 2.0 * N * K + 4.0 * M * K + 4.0 * M * nout * (accumulate ? 2 : 1) + (bias ? 4.0 * N : 0.0));
     char name[32];
     if (kind == K_GEMV) {
+        /* the GEMV reads bias and the row map unconditionally */
+        if (N > GPU_ZEROS_N) return bad(g, "gemm: N too large for the GEMV");
+        if (!a.bias) a.bias = gpu_zeros(g);
+        if (!a.crow) a.crow = gpu_iota(g);
         uint32_t kch, nc;
         gemv_shape(N, K, act, &kch, &nc);
         const uint32_t per_wave = act == NK_ACT_GLU ? nc / 2 : nc;
@@ -110,28 +144,15 @@ static int gemm_core(gpu_t *g, const float *A, uint32_t lda, const uint16_t *W, 
         snprintf(name, sizeof name, "gemv_r%u_n%u_k%u", M, nc, kch);
         return gpu_launch(g, name, &a, sizeof a, (waves + 3) / 4, 1, 1, 256, 1, 1);
     }
-    if (kind == K_GEMV1) {
-        const uint32_t nc = (act == NK_ACT_GLU || K <= 2048) ? 2u : 1u;
-        const uint32_t per_wave = act == NK_ACT_GLU ? 1u : nc;
-        const uint32_t waves = (nout + per_wave - 1) / per_wave;
-        snprintf(name, sizeof name, "gemv_r%u_c%u", M, nc);
-        return gpu_launch(g, name, &a, sizeof a, (waves + 3) / 4, 1, 1, 256, 1, 1);
-    }
     if (K % 32) return bad(g, "gemm: K % 32 != 0 for the MFMA kernels");
     if (kind == K_FR) {
+        /* the few-row kernel reads bias and the row map unconditionally */
+        if (N > GPU_ZEROS_N) return bad(g, "gemm: N too large for the few-row kernel");
+        const fr_plan_t p = fr_plan(nout, K, act, accumulate, bias != NULL, ln_fused);
+        if (!a.bias) a.bias = gpu_zeros(g);
+        if (!a.crow) a.crow = gpu_iota(g);
         const uint32_t tiles = (nout + 15) / 16;
-        const uint32_t KS = K / 32, maxsteps = NK_FR_MAX_KC / 32;
-        uint32_t S = (KS + maxsteps - 1) / maxsteps;
-        const uint32_t want = (256 + tiles - 1) / tiles;
-        if (S < want) S = want;
-        if (S > KS) S = KS;
-        a.splits = S;
-        if (S > 1) {
-            a.ws = gpu_splitk_ws(g, (size_t)tiles * S * 512);
-            a.counters = gpu_splitk_counters(g, tiles);
-            if (!a.ws || !a.counters) return bad(g, "gemm: split-K scratch");
-        }
-        return gpu_launch(g, "gemm_fr", &a, sizeof a, tiles, S, 1, 256, 1, 1);
+        return gpu_launch(g, fr_name(p, act, ln_fused), &a, sizeof a, tiles, p.KS, 1, 64 * p.W, 1, 1);
     }
     if (act == NK_ACT_GLU) return bad(g, "gemm: GLU needs M <= 16");
     return gpu_launch(g, "gemm_mr", &a, sizeof a, (N + 63) / 64, (M + 63) / 64, 1, 256, 1, 1);

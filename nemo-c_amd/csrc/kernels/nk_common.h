@@ -6,6 +6,8 @@
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef float floatx2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef unsigned long long u64;
 typedef u32 u32x4 __attribute__((ext_vector_type(4)));
 
@@ -41,6 +43,29 @@ __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
     return v;
+}
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+#define DPP_QUAD_1032 0xB1 /* quad_perm(1,0,3,2) */
+#define DPP_QUAD_2301 0x4E /* quad_perm(2,3,0,1) */
+#define DPP_ROW_ROR4 0x124
+#define DPP_ROW_ROR8 0x128
+
+/* Sum over the 64 lanes of a wavefront, returned wave-uniform; fixed combination order
+ * (DPP within each 16-lane row, then the four row totals read from lanes 0, 16, 32, 48). */
+__device__ __forceinline__ float wsum(float v) {
+    v += dpp_f<DPP_QUAD_1032>(v);
+    v += dpp_f<DPP_QUAD_2301>(v);
+    v += dpp_f<DPP_ROW_ROR4>(v);
+    v += dpp_f<DPP_ROW_ROR8>(v);
+    const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+    const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+    const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+    return (r0 + r1) + (r2 + r3);
 }
 
 /* Dot of 8 f32 activations with 8 bf16 weights packed in a uint4, summed in index order. */

@@ -1,220 +1,258 @@
 /* bf16-weight GEMMs for gfx950 with the fused epilogue of the reference
  * (bias, SiLU / ReLU, GLU pairing, alpha scale, accumulate into C).
  *
- *   gemv_r{R}_c{NC}: M = R <= 4 rows.  Pure weight streaming on the VALU: each wavefront owns
- *       NC weight rows, every lane streams 16-byte chunks of those rows (a wavefront reads 1 KB of
- *       contiguous weights per row per pass), activations stay in registers for the pass, and a
- *       64-lane butterfly finishes each dot product.  Replaces gemm_spec
- *       (reference src/kernels.metal:51-118).
- *   gemm_fr: 5 <= M <= 16 rows.  v_mfma_f32_16x16x32_bf16 with the activations split into
- *       bf16 hi + lo (two MFMAs per step; hi + lo keeps 16 significant bits, so the product error
- *       stays near f32 summation error).  A is staged once per workgroup in LDS in fragment order;
- *       weights go straight from HBM into the B operand (16 bytes per lane).  Four wavefronts split
- *       the workgroup's K range; workgroups split K further with a deterministic fixup (the last
- *       arriving workgroup sums the partials in split order).  Replaces gemm_mma
+ *   gemm_fr_*: 5 <= M <= 16 rows (M <= 4 uses the GEMV of nk_gemv.hip).
+ *       v_mfma_f32_16x16x32_bf16 with the activations split into bf16 hi + lo (two MFMAs per
+ *       step; hi + lo keeps 16 significant bits, so the product error stays near f32 summation
+ *       error).  Weights go straight from HBM into the B operand (16 bytes per lane); the
+ *       wavefronts of a workgroup split K and sum in a fixed order.  Replaces gemm_mma
  *       (reference src/kernels.metal:120-208).
  *   gemm_mr: M > 16 rows (subsampling 1x1 convs, position table).  64x64 output tiles, both
  *       operands staged through LDS per 32-wide K step, same hi/lo split.
  */
 #include "nk_common.h"
 
-template <int R, int NC, int SEG>
-__device__ __forceinline__ void gemv_impl(const NkGemmArgs &a) {
-    const int lane = threadIdx.x & 63;
-    const u32 gw = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-    const bool glu = a.act == NK_ACT_GLU;
-    const u32 nout = glu ? a.N / 2 : a.N;
-    const u32 per_wave = glu ? 1u : (u32)NC;
-    const u32 j0 = gw * per_wave;
-    if (j0 >= nout) return; /* uniform per wavefront */
-    const u16 *wr[NC];
-#pragma unroll
-    for (int c = 0; c < NC; ++c) {
-        u32 row = glu ? (c ? j0 + a.N / 2 : j0) : j0 + c;
-        if (row >= a.N) row = a.N - 1;
-        wr[c] = a.W + (u64)row * a.ldw;
-    }
-    const u32 nch = a.K >> 3; /* 8-element (16-byte) weight chunks per row */
-    float acc[R][NC];
-#pragma unroll
-    for (int r = 0; r < R; ++r)
-#pragma unroll
-        for (int c = 0; c < NC; ++c) acc[r][c] = 0.0f;
-    for (u32 base = 0; base < nch; base += 64 * SEG) {
-        uint4 wv[NC][SEG];
-        float av[SEG][R][8];
-#pragma unroll
-        for (int s = 0; s < SEG; ++s) {
-            const u32 j = base + s * 64 + lane;
-            const bool ok = j < nch;
-#pragma unroll
-            for (int c = 0; c < NC; ++c)
-                wv[c][s] = ok ? ld_nt16(wr[c] + 8 * (u64)j) : make_uint4(0, 0, 0, 0);
-#pragma unroll
-            for (int r = 0; r < R; ++r) {
-                float4 x = make_float4(0, 0, 0, 0), y = x;
-                if (ok) {
-                    const float4 *ap = (const float4 *)(a.A + (u64)r * a.lda + 8 * (u64)j);
-                    x = ap[0];
-                    y = ap[1];
-                }
-                av[s][r][0] = x.x; av[s][r][1] = x.y; av[s][r][2] = x.z; av[s][r][3] = x.w;
-                av[s][r][4] = y.x; av[s][r][5] = y.y; av[s][r][6] = y.z; av[s][r][7] = y.w;
-            }
-        }
-#pragma unroll
-        for (int s = 0; s < SEG; ++s)
-#pragma unroll
-            for (int c = 0; c < NC; ++c)
-#pragma unroll
-                for (int r = 0; r < R; ++r) acc[r][c] = dot8(av[s][r], wv[c][s], acc[r][c]);
-    }
-#pragma unroll
-    for (int r = 0; r < R; ++r)
-#pragma unroll
-        for (int c = 0; c < NC; ++c) acc[r][c] = wave_sum(acc[r][c]);
-    if (lane == 0) {
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            if ((u32)r >= a.M) break;
-            if (glu) {
-                if constexpr (NC == 2) epi_store_glu(a, r, j0, acc[r][0], acc[r][1]);
-            } else {
-#pragma unroll
-                for (int c = 0; c < NC; ++c)
-                    if (j0 + c < nout) epi_store(a, r, j0 + c, acc[r][c]);
-            }
-        }
-    }
-}
-
-#define GEMV(R, NC, SEG) \
-    extern "C" __global__ __launch_bounds__(256) void gemv_r##R##_c##NC(const NkGemmArgs a) { gemv_impl<R, NC, SEG>(a); }
-GEMV(1, 1, 8)
-GEMV(1, 2, 8)
-GEMV(2, 1, 4)
-GEMV(2, 2, 4)
-GEMV(3, 1, 2)
-GEMV(3, 2, 2)
-GEMV(4, 1, 2)
-GEMV(4, 2, 2)
-
 /* ---- few-row MFMA GEMM ---------------------------------------------------------------------
- * grid = (ceil(nout / 16), splits), block = 256.  A workgroup owns 16 output columns and the
- * K steps [sb, se) of its split (se - sb <= NK_FR_MAX_KC / 32).
+ * grid = ceil(nout / 16) workgroups of W wavefronts; a workgroup owns 16 output columns (GLU: 16
+ * output pairs) and all of K.  Wavefront w takes the K steps [S*w/W, S*(w+1)/W) of the S = K/32
+ * steps (at most FR_SPW).  Order of work:
+ *   1. every weight load of the wavefront is issued (16 bytes per lane per step, straight into the
+ *      B operand layout);
+ *   2. activations: rows < M are read into the A operand layout, from LDS after a workgroup
+ *      LayerNorm (the _ln kernels, K <= 1024) or straight from global memory;
+ *   3. per step two MFMAs, A = hi + lo bf16 split of the f32 activations (16 significant bits);
+ *   4. the W partial tiles are summed in wavefront order through LDS; wavefront 0 applies the
+ *      epilogue.
+ * No workgroup depends on another, so there is no split-K fixup.
  * MFMA 16x16x32 bf16 lane layouts (lane l, element i):
  *   A: row l % 16, k 8*(l/16) + i;  B: k 8*(l/16) + i, column l % 16;
- *   D: row 4*(l/16) + i, column l % 16.
- */
-#define FR_STEPS (NK_FR_MAX_KC / 32)
+ *   D: row 4*(l/16) + i, column l % 16. */
 
-__device__ __forceinline__ void fr_epilogue(const NkGemmArgs &a, bool glu, u32 n0, u32 nout, int lane, floatx4 sa, floatx4 sb) {
-    const u32 col = n0 + (lane & 15);
-    if (col >= nout) return;
+/* Workgroup barrier for data exchanged through LDS only: waits for this wavefront's LDS
+ * operations but not for its outstanding global loads (a __syncthreads() would also wait for
+ * every weight load in flight).  The "memory" clobber keeps the compiler from moving memory
+ * accesses across it. */
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+/* LayerNorm of one row of 1024 floats held by a wavefront as four float4 per lane (float4 index
+ * lane + 64 j): mean = sum/D; var = sum((x-mean)^2)/D; y = (x-mean) * (1/sqrt(var+eps)) * g + b. */
+__device__ __forceinline__ void ln_wave4(floatx4 (&v)[4], const floatx4 (&g)[4], const floatx4 (&b)[4], float D,
+                                         float eps) {
+    float s = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) s += ((v[j][0] + v[j][1]) + v[j][2]) + v[j][3];
+    const float mean = wsum(s) / D;
+    float q = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const floatx4 d = v[j] - mean;
+        q += ((d[0] * d[0] + d[1] * d[1]) + d[2] * d[2]) + d[3] * d[3];
+    }
+    const float inv = 1.0f / sqrtf(wsum(q) / D + eps);
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[j][e] = (v[j][e] - mean) * inv * g[j][e] + b[j][e];
+}
+
+/* 8 f32 -> bf16 hi (round to nearest even, v_cvt_pk_bf16_f32) and bf16 lo = bf16(x - hi), packed
+ * in pairs (element 2p in the low half of word p). */
+__device__ __forceinline__ void split8(const float (&x)[8], uint4 &hi, uint4 &lo) {
+    u32 h[4], l[4];
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+        const floatx2 v = { x[2 * p], x[2 * p + 1] };
+        const u32 hb = __builtin_bit_cast(u32, __builtin_convertvector(v, bf16x2));
+        const floatx2 hv = { __uint_as_float(hb << 16), __uint_as_float(hb & 0xffff0000u) };
+        h[p] = hb;
+        l[p] = __builtin_bit_cast(u32, __builtin_convertvector(v - hv, bf16x2));
+    }
+    hi = make_uint4(h[0], h[1], h[2], h[3]);
+    lo = make_uint4(l[0], l[1], l[2], l[3]);
+}
+
+/* grid = (ceil(nout/16), KS): workgroup (tile, ks) takes the K steps [ks*S/KS, (ks+1)*S/KS) of the
+ * S = K/32 steps, wavefront w the SPW steps from w*SPW within them.  With KS > 1 the partial
+ * products are added into C atomically (the host uses this only for accumulating GEMMs with no
+ * bias and no activation). */
+template <int W, int SPW, bool LNA, bool GLU>
+__device__ __forceinline__ void fr_impl(const NkGemmArgs &a, float *sA, floatx4 *sred) {
+    const u32 tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const u32 nout = GLU ? a.N / 2 : a.N;
+    const u32 n0 = blockIdx.x * 16;
+    const u32 S = a.K >> 5, M = a.M, KS = gridDim.y;
+    const u32 Sw = S / KS, s0 = blockIdx.y * Sw;
+    /* this wavefront's K steps: [sb, sb + ns), ns <= SPW (wave-uniform) */
+    const u32 sb = s0 + wave * SPW;
+    const u32 ns = wave * SPW < Sw ? min((u32)SPW, Sw - wave * SPW) : 0u;
+    const u32 m = lane & 15, kq = 8 * (lane >> 4);
+    const bool mrow = m < M;
+
+    /* LayerNorm variant: wavefront w normalises rows w, w+4, w+8, w+12 (those below M) */
+    floatx4 v[LNA ? 4 : 1][4], g1[4], b1[4], g2[4], b2[4];
+    if constexpr (LNA) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const u32 r = min(wave + 4 * i, M - 1);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) v[i][j] = ((const floatx4 *)(a.A + (u64)r * a.lda))[lane + 64 * j];
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            g1[j] = ((const floatx4 *)a.ln_g1)[lane + 64 * j];
+            b1[j] = ((const floatx4 *)a.ln_b1)[lane + 64 * j];
+            g2[j] = ((const floatx4 *)(a.ln_mode == 2 ? a.ln_g2 : a.ln_g1))[lane + 64 * j];
+            b2[j] = ((const floatx4 *)(a.ln_mode == 2 ? a.ln_b2 : a.ln_b1))[lane + 64 * j];
+        }
+    }
+
+    /* activations in the A layout (row m of lane l; lanes of rows past M load nothing and are
+     * masked at use) */
+    float x[LNA ? 1 : SPW][8];
+    if constexpr (!LNA) {
+        if (mrow) {
+            const float *arow = a.A + (u64)m * a.lda + kq;
+#pragma unroll
+            for (int s = 0; s < SPW; ++s) {
+                const u32 t = min(sb + s, S - 1);
+                const floatx4 p = *(const floatx4 *)(arow + (u64)t * 32), q = *(const floatx4 *)(arow + (u64)t * 32 + 4);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) { x[s][e] = p[e]; x[s][4 + e] = q[e]; }
+            }
+        }
+    }
+
+    /* epilogue operands (the host always passes bias and the row map), loaded by every
+     * wavefront: lane l owns output rows 4*(l/16)+i, column n0 + l%16 */
+    u32 col = n0 + (lane & 15);
+    if (col >= nout) col = nout - 1;
+    const float eba = a.bias[col];
+    const float ebb = GLU ? a.bias[col + a.N / 2] : 0.0f;
+    int erow[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const u32 r = 4 * (lane >> 4) + i;
-        if (r >= a.M) continue;
-        if (glu) epi_store_glu(a, r, col, sa[i], sb[i]);
-        else epi_store(a, r, col, sa[i]);
+        erow[i] = a.crow[r < M ? r : 0];
     }
-}
+    __builtin_amdgcn_sched_barrier(0); /* keep the small loads ahead of the weight stream */
 
-extern "C" __global__ __launch_bounds__(256) void gemm_fr(const NkGemmArgs a) {
-    __shared__ uint4 sA[2][FR_STEPS][64];
-    __shared__ floatx4 sred[2][4][64];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const bool glu = a.act == NK_ACT_GLU;
-    const u32 nout = glu ? a.N / 2 : a.N;
-    const u32 tile = blockIdx.x, n0 = tile * 16;
-    const u32 S = a.splits, ks = blockIdx.y;
-    const u32 KS = a.K >> 5;
-    const u32 sb = (u32)(((u64)KS * ks) / S), se = (u32)(((u64)KS * (ks + 1)) / S);
-    const u32 ns = se - sb;
-
-    /* stage this split's A columns as hi/lo bf16 fragments */
-    for (u32 idx = threadIdx.x; idx < ns * 64; idx += 256) {
-        const u32 t = idx >> 6, l = idx & 63, m = l & 15;
-        const u32 k = (sb + t) * 32 + 8 * (l >> 4);
-        uint4 hi = make_uint4(0, 0, 0, 0), lo = hi;
-        if (m < a.M) {
-            const float4 *ap = (const float4 *)(a.A + (u64)m * a.lda + k);
-            const float4 x = ap[0], y = ap[1];
-            const float v[8] = { x.x, x.y, x.z, x.w, y.x, y.y, y.z, y.w };
-            u32 h[8], q[8];
+    /* 1. weights: every step of this wavefront (steps past K re-read the last one) */
+    const u16 *wa = a.W + (u64)col * a.ldw + kq;
+    const u16 *wb = GLU ? a.W + (u64)(col + a.N / 2) * a.ldw + kq : wa;
+    uint4 fa[SPW], fb[GLU ? SPW : 1];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) split_bf16(v[i], h[i], q[i]);
-            hi = make_uint4(h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16));
-            lo = make_uint4(q[0] | (q[1] << 16), q[2] | (q[3] << 16), q[4] | (q[5] << 16), q[6] | (q[7] << 16));
-        }
-        sA[0][t][l] = hi;
-        sA[1][t][l] = lo;
+    for (int s = 0; s < SPW; ++s) {
+        const u32 t = min(sb + s, S - 1);
+        fa[s] = ld_nt16(wa + (u64)t * 32);
+        if constexpr (GLU) fb[s] = ld_nt16(wb + (u64)t * 32);
     }
-    __syncthreads();
+    __builtin_amdgcn_sched_barrier(0);
 
-    u32 col = n0 + (lane & 15);
-    if (col >= nout) col = nout - 1;
-    const u16 *wa = a.W + (u64)col * a.ldw + 8 * (lane >> 4);
-    const u16 *wb = glu ? a.W + (u64)(col + a.N / 2) * a.ldw + 8 * (lane >> 4) : wa;
-    const u32 wbeg = ns * wave / 4, wend = ns * (wave + 1) / 4;
+    /* the C values to accumulate into */
+    float ec[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ec[i] = a.C[(u64)(u32)erow[i] * a.ldc + col];
+
+    /* 2. LayerNorm of the activation rows into LDS while the weights stream in */
+    if constexpr (LNA) {
+        const float D = (float)a.K;
+        const bool write1 = a.ln_out && blockIdx.x == 0 && blockIdx.y == 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const u32 r = wave + 4 * i;
+            if (r < M) {
+                ln_wave4(v[i], g1, b1, D, a.ln_eps);
+                if (write1)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) ((floatx4 *)(a.ln_out + (u64)r * a.lda))[lane + 64 * j] = v[i][j];
+                if (a.ln_mode == 2) ln_wave4(v[i], g2, b2, D, a.ln_eps);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) ((floatx4 *)(sA + (u64)r * 1024))[lane + 64 * j] = v[i][j];
+            }
+        }
+        lds_barrier();
+    }
+
+    /* 3. MFMAs: A = hi + lo */
     floatx4 acc_a = { 0.f, 0.f, 0.f, 0.f }, acc_b = acc_a;
-    uint4 fa[FR_STEPS / 4], fb[FR_STEPS / 4];
 #pragma unroll
-    for (int s = 0; s < FR_STEPS / 4; ++s) {
-        const u32 t = wbeg + s;
-        if (t < wend) {
-            fa[s] = ld_nt16(wa + (u64)(sb + t) * 32);
-            if (glu) fb[s] = ld_nt16(wb + (u64)(sb + t) * 32);
-        }
-    }
-#pragma unroll
-    for (int s = 0; s < FR_STEPS / 4; ++s) {
-        const u32 t = wbeg + s;
-        if (t < wend) {
-            const uint4 ah = sA[0][t][lane], al = sA[1][t][lane];
+    for (int s = 0; s < SPW; ++s) {
+        if ((u32)s < ns) {
+            uint4 ah, al;
+            if constexpr (LNA) {
+                const float *sp = sA + (u64)m * 1024 + (sb + s) * 32 + kq;
+                const floatx4 p = *(const floatx4 *)sp, q = *(const floatx4 *)(sp + 4);
+                const float xs[8] = { p[0], p[1], p[2], p[3], q[0], q[1], q[2], q[3] };
+                split8(xs, ah, al);
+            } else {
+                split8(x[s], ah, al);
+            }
+            if (!mrow) ah = al = make_uint4(0, 0, 0, 0);
             acc_a = mfma_bf16(ah, fa[s], acc_a);
             acc_a = mfma_bf16(al, fa[s], acc_a);
-            if (glu) {
+            if constexpr (GLU) {
                 acc_b = mfma_bf16(ah, fb[s], acc_b);
                 acc_b = mfma_bf16(al, fb[s], acc_b);
             }
         }
     }
-    sred[0][wave][lane] = acc_a;
-    sred[1][wave][lane] = acc_b;
+
+    /* 4. wavefront partials summed in order; epilogue on wavefront 0 */
+    sred[wave * 64 + lane] = acc_a;
+    if constexpr (GLU) sred[(W + wave) * 64 + lane] = acc_b;
     __syncthreads();
     if (wave != 0) return;
-    const floatx4 sa = ((sred[0][0][lane] + sred[0][1][lane]) + sred[0][2][lane]) + sred[0][3][lane];
-    const floatx4 sbv = ((sred[1][0][lane] + sred[1][1][lane]) + sred[1][2][lane]) + sred[1][3][lane];
-    if (S == 1) {
-        fr_epilogue(a, glu, n0, nout, lane, sa, sbv);
-        return;
+    floatx4 ta = sred[lane], tb = GLU ? sred[W * 64 + lane] : acc_b;
+#pragma unroll
+    for (int w = 1; w < W; ++w) {
+        ta += sred[w * 64 + lane];
+        if constexpr (GLU) tb += sred[(W + w) * 64 + lane];
     }
-    /* split-K: publish this split's 16x16 partial, the last arriving split reduces in order */
-    float *mine = a.ws + ((u64)tile * S + ks) * 512;
+    if (n0 + (lane & 15) >= nout) return;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        __hip_atomic_store(mine + lane * 4 + i, sa[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(mine + 256 + lane * 4 + i, sbv[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    __threadfence();
-    u32 prev = 0;
-    if (lane == 0) prev = atomicAdd(&a.counters[tile], 1u);
-    prev = __shfl(prev, 0, 64);
-    if (prev != S - 1) return;
-    __threadfence();
-    floatx4 ta = { 0.f, 0.f, 0.f, 0.f }, tb = ta;
-    for (u32 q = 0; q < S; ++q) {
-        const float *p = a.ws + ((u64)tile * S + q) * 512;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            ta[i] += __hip_atomic_load(p + lane * 4 + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            tb[i] += __hip_atomic_load(p + 256 + lane * 4 + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const u32 r = 4 * (lane >> 4) + i;
+        if (r >= M) continue;
+        float *dst = a.C + (u64)(u32)erow[i] * a.ldc + col;
+        if (KS > 1) { /* K split over workgroups: no bias, no activation, accumulate */
+            atomicAdd(dst, ta[i] * a.alpha);
+            continue;
         }
+        float v;
+        if constexpr (GLU) {
+            v = (ta[i] + eba) * sigmoid_f(tb[i] + ebb) * a.alpha;
+        } else {
+            v = ta[i] + eba;
+            if (a.act == NK_ACT_SILU) v = silu_f(v);
+            else if (a.act == NK_ACT_RELU) v = fmaxf(v, 0.0f);
+            v *= a.alpha;
+        }
+        *dst = a.accumulate ? ec[i] + v : v;
     }
-    if (lane == 0) __hip_atomic_store(&a.counters[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    fr_epilogue(a, glu, n0, nout, lane, ta, tb);
 }
+
+/* gemm_fr_w{W}s{SPW}: W wavefronts of SPW K steps each per workgroup */
+#define GEMM_FR(NAME, W, SPW, GLU)                                                                       \
+    extern "C" __global__ __launch_bounds__(64 * W) void NAME(const NkGemmArgs a) {                      \
+        __shared__ floatx4 sred[2 * W * 64];                                                             \
+        fr_impl<W, SPW, false, GLU>(a, nullptr, sred);                                                   \
+    }
+GEMM_FR(gemm_fr_w4s2, 4, 2, false)
+GEMM_FR(gemm_fr_w4s8, 4, 8, false)
+GEMM_FR(gemm_fr_w8s8, 8, 8, false)
+GEMM_FR(gemm_fr_w16s8, 16, 8, false)
+GEMM_FR(gemm_fr_w16s9, 16, 9, false)
+GEMM_FR(gemm_fr_glu_w4s8, 4, 8, true)
+
+/* LayerNorm prologue variants: K == 1024, M <= 16 */
+#define GEMM_FR_LN(NAME, GLU)                                                                            \
+    extern "C" __global__ __launch_bounds__(256) void NAME(const NkGemmArgs a) {                         \
+        __shared__ float sA[16 * 1024];                                                                  \
+        __shared__ floatx4 sred[2 * 4 * 64];                                                             \
+        fr_impl<4, 8, true, GLU>(a, sA, sred);                                                           \
+    }
+GEMM_FR_LN(gemm_fr_ln_w4s8, false)
+GEMM_FR_LN(gemm_fr_ln_glu_w4s8, true)
 
 /* ---- many-row MFMA GEMM ---------------------------------------------------------------------
  * grid = (ceil(N / 64), ceil(M / 64)), block = 256 (2 x 2 wavefronts, 32 x 32 outputs each).

@@ -1,0 +1,141 @@
+#!/usr/bin/env python3
+"""Kernel micro-benchmark of the streaming hot path on one MI355X (the methodology of the
+reference's tools/kbench.c:140-195: every GEMM shape of a chunk against HBM-resident weights).
+
+For each shape it reports
+  graph_us   launch-to-launch time of the kernel replayed back to back inside a hipGraph (the
+             way a chunk runs), with a fresh weight matrix per launch so nothing is served from
+             cache;
+  kernel_us  mean execution time of the same launches from dispatch-stamped events (what
+             rocprofv3 reports as the kernel duration);
+  GB/s       weight bytes / kernel_us and / graph_us.
+Plus a large device copy (HBM read + write bandwidth reference) and the per-row kernels.
+
+Usage: python kbench.py [--rows 1,7,14] [--reps 3] [--json out.json]
+"""
+import argparse
+import ctypes as C
+import json
+import os
+import sys
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, HERE)
+import nemoasr  # noqa: E402
+
+# (label, N, K, act, accumulate, alpha, ln_mode, ldw, bias) as the chunk calls them
+SHAPES = [
+    ("ff_up+ln2", 4096, 1024, 1, 0, 1.0, 2, None, False),
+    ("ff_down", 1024, 4096, 0, 1, 0.5, 0, None, False),
+    ("qkv+ln", 3072, 1024, 0, 0, 1.0, 1, None, False),
+    ("out_proj", 1024, 1024, 0, 1, 1.0, 0, None, False),
+    ("pw1_glu+ln", 2048, 1024, 3, 0, 1.0, 1, None, False),
+    ("pw2", 1024, 1024, 0, 1, 1.0, 0, None, False),
+    ("prompt_w0+ln", 2048, 1024, 2, 0, 1.0, 1, 1152, True),
+    ("prompt_w2", 1024, 2048, 0, 0, 1.0, 0, None, True),
+    ("joint_enc", 640, 1024, 0, 0, 1.0, 0, None, True),
+    ("lstm", 2560, 640, 0, 1, 1.0, 0, None, False),
+]
+
+
+def bench_gemm(gpu, M, N, K, act, acc, alpha, ln_mode, ldw, has_bias, copies, reps):
+    L = nemoasr.lib()
+    ldw = ldw or K
+    rng = np.random.default_rng([M, N, K])
+    nout = N // 2 if act == 3 else N
+    W = (rng.standard_normal((N, ldw)).astype(np.float32) / np.sqrt(K)).view(np.uint32) >> 16
+    W = W.astype(np.uint16)
+    dWs = [gpu.put(W) for _ in range(copies)]
+    dA = gpu.put(rng.standard_normal((M, K)).astype(np.float32))
+    dC = gpu.put(np.zeros((M, nout), np.float32))
+    dB = gpu.put((0.1 * rng.standard_normal(N)).astype(np.float32))
+    g = [gpu.put((1 + 0.1 * rng.standard_normal(K)).astype(np.float32)) for _ in range(4)]
+    dT = gpu.alloc(M * K * 4)
+    dO = gpu.alloc(M * K * 4)
+
+    def launch(i):
+        return L.nk_gemm_ln(gpu.h, dA.ptr, K, dWs[i % copies].ptr, ldw, dB.ptr if has_bias else None, dC.ptr, nout, None, M, N, K, act, acc,
+                            alpha, ln_mode, g[0].ptr, g[1].ptr, g[2].ptr, g[3].ptr, dO.ptr if ln_mode == 2 else None,
+                            dT.ptr, 1e-5)
+
+    name = L.nk_gemm_kernel_name(M, N, K, act).decode()
+    # graph replay
+    gpu.begin()
+    gpu.check(L.gpu_capture_begin(gpu.h))
+    for i in range(copies):
+        gpu.check(launch(i))
+    gr = L.gpu_capture_end(gpu.h)
+    gpu.end()
+    if not gr:
+        raise RuntimeError(L.gpu_last_error(gpu.h).decode())
+    best = 1e30
+    for _ in range(reps + 1):
+        gpu.begin()
+        gpu.check(L.gpu_graph_launch(gpu.h, gr))
+        best = min(best, gpu.end())
+    L.gpu_graph_free(gr)
+    graph_us = best * 1e3 / copies
+    # dispatch-stamped kernel durations (direct launches)
+    L.gpu_timing_set(gpu.h, b"gemm_fr*" if name.startswith("gemm_fr") else name.encode(), 4096)
+    gpu.begin()
+    for i in range(copies * reps):
+        gpu.check(launch(i))
+    gpu.end()
+    ms, cnt, by = C.c_double(), C.c_int(), C.c_double()
+    L.gpu_timing_collect(gpu.h, C.byref(ms), C.byref(cnt), C.byref(by))
+    L.gpu_timing_set(gpu.h, None, 0)
+    for b in dWs + [dA, dC, dB, dT, dO] + g:
+        b.free()
+    return name, graph_us, ms.value * 1e3, cnt.value
+
+
+def bench_copy(gpu, nbytes, reps):
+    L = nemoasr.lib()
+    n = nbytes // 4
+    src, dst = gpu.alloc(nbytes), gpu.alloc(nbytes)
+    best = 1e30
+    for _ in range(reps + 1):
+        gpu.begin()
+        gpu.check(L.nk_copy(gpu.h, src.ptr, dst.ptr, n))
+        best = min(best, gpu.end())
+    src.free()
+    dst.free()
+    return best * 1e3
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--rows", default="1,7,14")
+    ap.add_argument("--reps", type=int, default=3)
+    ap.add_argument("--copies", type=int, default=48, help="distinct weight matrices cycled per replay")
+    ap.add_argument("--json", default=None)
+    a = ap.parse_args()
+    gpu = nemoasr.Gpu()
+    print(f"device: {gpu.name}", flush=True)
+    out = {"device": gpu.name, "gemm": [], "copy": None}
+    cb = 256 << 20
+    cu = bench_copy(gpu, cb, a.reps)
+    out["copy"] = {"bytes": cb, "us": cu, "gbs_rw": 2 * cb / (cu * 1e-6) / 1e9}
+    print(f"copy {cb >> 20} MiB: {cu:.1f} us, {2 * cb / (cu * 1e-6) / 1e9:.0f} GB/s read+write", flush=True)
+    for M in [int(x) for x in a.rows.split(",")]:
+        for (label, N, K, act, acc, alpha, ln, ldw, hb) in SHAPES:
+            if label == "lstm" and M > 1:
+                continue
+            name, gus, kus, cnt = bench_gemm(gpu, M, N, K, act, acc, alpha, ln, ldw, hb, a.copies, a.reps)
+            wb = 2.0 * N * K
+            rec = {"M": M, "shape": label, "N": N, "K": K, "kernel": name, "graph_us": round(gus, 3),
+                   "kernel_us": round(kus, 3), "weight_bytes": wb, "gbs_kernel": round(wb / (kus * 1e-6) / 1e9, 1),
+                   "gbs_graph": round(wb / (gus * 1e-6) / 1e9, 1), "timed_launches": cnt}
+            out["gemm"].append(rec)
+            print(f"M={M:2d} {label:14s} {name:22s} graph {gus:7.2f} us ({rec['gbs_graph']:7.1f} GB/s)  "
+                  f"kernel {kus:7.2f} us ({rec['gbs_kernel']:7.1f} GB/s)", flush=True)
+    gpu.close()
+    if a.json:
+        with open(a.json, "w") as f:
+            json.dump(out, f, indent=1)
+
+
+if __name__ == "__main__":
+    main()

@@ -70,6 +70,10 @@ API = {
     "gpu_timing_set": (C.c_int, [_vp, C.c_char_p, C.c_int]),
     "gpu_timing_collect": (C.c_int, [_vp, C.POINTER(C.c_double), C.POINTER(C.c_int), C.POINTER(C.c_double)]),
     "gpu_launch_count": (C.c_uint64, [_vp]),
+    "gpu_capture_begin": (C.c_int, [_vp]),
+    "gpu_capture_end": (_vp, [_vp]),
+    "gpu_graph_launch": (C.c_int, [_vp, _vp]),
+    "gpu_graph_free": (None, [_vp]),
     "nk_gemm": (C.c_int, [_vp, _vp, _u32, _vp, _u32, _vp, _vp, _u32, _u32, _u32, _u32, C.c_int, C.c_int, C.c_float]),
     "nk_gemm_rows": (C.c_int, [_vp, _vp, _u32, _vp, _u32, _vp, _vp, _u32, _vp, _u32, _u32, _u32, C.c_int, C.c_int,
                                C.c_float]),

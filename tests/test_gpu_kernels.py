@@ -96,7 +96,7 @@ def test_gemm_many_rows(gpu, M, N, K, act):
     assert rel_err(got, ref) < GEMM_TOL
 
 
-@pytest.mark.parametrize("kind,M", [(1, 1), (1, 4), (2, 1), (2, 4), (2, 16), (3, 5), (3, 16)])
+@pytest.mark.parametrize("kind,M", [(4, 1), (4, 4), (2, 1), (2, 4), (2, 16), (3, 5), (3, 16)])
 def test_gemm_variants_agree(gpu, kind, M):
     """Every kernel the policy can pick computes the same GEMM (the reference's kbench.c:196-230
     cross-check, with a threshold)."""
@@ -110,7 +110,7 @@ def test_gemm_variants_agree(gpu, kind, M):
     assert rel_err(got, ref) < GEMM_TOL
 
 
-@pytest.mark.parametrize("kind", [1, 4])
+@pytest.mark.parametrize("kind", [4])
 @pytest.mark.parametrize("M,N,K,act", [(1, 2560, 640, 0), (2, 1024, 4096, 0), (1, 1024, 4352, 0), (2, 640, 640, 2),
                                        (3, 2048, 1024, 3), (4, 4096, 1024, 1)])
 def test_gemv_kinds(gpu, kind, M, N, K, act):
