@@ -1,19 +1,22 @@
 /* Greedy RNN-T decoder (see decoder.h).
  *
  * The loop is the reference's (src/decoder.c:92-127): committed and provisional LSTM states, the
- * joint evaluated for up to 16 remaining frames per round trip with the current prediction
- * (speculating blank), and on the first non-blank: emit, commit the provisional state, redo the
- * later frames.  A round trip is one ordered batch on the stream: [embedding row upload,
- * 2 x (Wx GEMV + bias, Wh GEMV accumulate, LSTM cell), joint.pred GEMV], joint scoring + argmax,
- * and a download of 2 ints per frame into pinned memory. */
+ * joint evaluated for up to 16 remaining frames per step with the current prediction (speculating
+ * blank), and on the first non-blank: emit, commit the provisional state, redo the later frames.
+ * It runs on the device (kernels/nk_dec.hip): one step is four launches, a graph holds a run of
+ * steps, and the host replays graphs until the device state says the chunk is done.  The host
+ * reads back the state and the emitted tokens once per graph, not once per joint evaluation. */
 #include "decoder.h"
 #include "nemo_kernels.h"
 #include "../kernel_params.h"
-#include "safetensors.h"
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
 #include <time.h>
+
+#define STEPS_FIRST 11 /* steps in the first graph of a chunk (odd: see below)        */
+#define STEPS_MORE 15  /* steps in each further graph                                  */
+#define MAX_GRAPHS_PER_CHUNK 64
 
 static double now_ms(void) {
     struct timespec ts;
@@ -21,14 +24,19 @@ static double now_ms(void) {
     return ts.tv_sec * 1e3 + ts.tv_nsec / 1e6;
 }
 
+typedef struct {
+    const float *enc;
+    gpu_graph_t *g[2]; /* first, more */
+} dgraph_t;
+
 struct decoder {
     model_t *m;
     gpu_t *g;
-    gpu_buf_t *x, *gates, *pred_out, *argmax, *part_v, *part_i, *state;
-    float *h[2], *c[2], *hp[2], *cp[2]; /* device: committed and provisional LSTM state */
-    float *x_host;                        /* pinned: embedding row */
-    int *res_host;                        /* pinned: argmax results */
-    int last_token, pred_valid, last_steps;
+    gpu_buf_t *st, *part, *tokens, *hc, *pred;
+    NkDecState *host_st; /* pinned: chunk fields in, final state out */
+    int *host_tok;       /* pinned: tokens of the chunk               */
+    dgraph_t gr[2];
+    int ngr, last_steps;
     double last_ms;
 };
 
@@ -36,113 +44,142 @@ decoder_t *decoder_create(model_t *m) {
     decoder_t *d = calloc(1, sizeof *d);
     d->m = m;
     d->g = m->gpu;
-    const size_t P = (size_t)m->cfg.pred_hidden, fs = sizeof(float);
-    d->x = gpu_buf_alloc(d->g, P * fs);
-    d->gates = gpu_buf_alloc(d->g, 4 * P * fs);
-    d->pred_out = gpu_buf_alloc(d->g, (size_t)m->cfg.joint_hidden * fs);
-    d->argmax = gpu_buf_alloc(d->g, NK_DEC_MAX_BATCH * 2 * sizeof(int));
-    d->part_v = gpu_buf_alloc(d->g, NK_DEC_MAX_BATCH * NK_JOINT_GROUPS * NK_JOINT_WAVES * fs);
-    d->part_i = gpu_buf_alloc(d->g, NK_DEC_MAX_BATCH * NK_JOINT_GROUPS * NK_JOINT_WAVES * sizeof(int));
-    d->state = gpu_buf_alloc(d->g, 8 * P * fs);
-    float *s = gpu_buf_dptr(d->state);
-    for (int l = 0; l < 2; ++l) {
-        d->h[l] = s + (0 + l) * P;
-        d->c[l] = s + (2 + l) * P;
-        d->hp[l] = s + (4 + l) * P;
-        d->cp[l] = s + (6 + l) * P;
-    }
-    d->x_host = gpu_host_alloc(d->g, P * fs);
-    d->res_host = gpu_host_alloc(d->g, NK_DEC_MAX_BATCH * 2 * sizeof(int));
+    const size_t P = (size_t)m->cfg.pred_hidden, J = (size_t)m->cfg.joint_hidden;
+    d->st = gpu_buf_alloc(d->g, 2 * sizeof(NkDecState));
+    d->part = gpu_buf_alloc(d->g, 2 * NK_DEC_MAX_BATCH * NK_DEC_GROUPS * sizeof(unsigned long long));
+    d->tokens = gpu_buf_alloc(d->g, NK_DEC_MAX_TOKENS * sizeof(int));
+    d->hc = gpu_buf_alloc(d->g, 2 * 4 * P * sizeof(float));
+    d->pred = gpu_buf_alloc(d->g, J * sizeof(float));
+    d->host_st = gpu_host_alloc(d->g, sizeof(NkDecState));
+    d->host_tok = gpu_host_alloc(d->g, NK_DEC_MAX_TOKENS * sizeof(int));
     decoder_reset(d);
     return d;
 }
 
+static void free_graphs(decoder_t *d) {
+    for (int i = 0; i < d->ngr; ++i) {
+        gpu_graph_free(d->gr[i].g[0]);
+        gpu_graph_free(d->gr[i].g[1]);
+    }
+    memset(d->gr, 0, sizeof d->gr);
+    d->ngr = 0;
+}
+
 void decoder_destroy(decoder_t *d) {
     if (!d) return;
-    gpu_buf_t *bufs[] = { d->x, d->gates, d->pred_out, d->argmax, d->part_v, d->part_i, d->state };
+    free_graphs(d);
+    gpu_buf_t *bufs[] = { d->st, d->part, d->tokens, d->hc, d->pred };
     for (size_t i = 0; i < sizeof bufs / sizeof *bufs; ++i) gpu_buf_free(bufs[i]);
-    gpu_host_free(d->x_host);
-    gpu_host_free(d->res_host);
+    gpu_host_free(d->host_st);
+    gpu_host_free(d->host_tok);
     free(d);
 }
 
-/* src/decoder.c:48-53 */
+/* src/decoder.c:48-53: zero LSTM state, last token blank, no valid prediction */
 void decoder_reset(decoder_t *d) {
     const size_t P = (size_t)d->m->cfg.pred_hidden;
-    float *z = calloc(4 * P, sizeof(float));
-    gpu_upload(d->g, gpu_buf_dptr(d->state), z, 4 * P * sizeof(float)); /* h[0], h[1], c[0], c[1] */
+    float *z = calloc(2 * 4 * P, sizeof(float));
+    gpu_upload(d->g, gpu_buf_dptr(d->hc), z, 2 * 4 * P * sizeof(float));
     free(z);
-    float *s = gpu_buf_dptr(d->state);
-    for (int l = 0; l < 2; ++l) {
-        d->h[l] = s + (0 + l) * P;
-        d->c[l] = s + (2 + l) * P;
-        d->hp[l] = s + (4 + l) * P;
-        d->cp[l] = s + (6 + l) * P;
-    }
-    d->last_token = d->m->cfg.blank_id;
-    d->pred_valid = 0;
+    NkDecState s[2];
+    memset(s, 0, sizeof s);
+    s[0].last_token = d->m->cfg.blank_id;
+    gpu_upload(d->g, gpu_buf_dptr(d->st), s, sizeof s);
 }
 double decoder_last_ms(const decoder_t *d) { return d->last_ms; }
 int decoder_last_steps(const decoder_t *d) { return d->last_steps; }
 
-/* prediction network from the committed state, input embed(last_token) or zeros for blank:
- * src/decoder.c:57-77 */
-static void encode_pred(decoder_t *d) {
-    model_t *m = d->m;
+static NkDecArgs dec_args(decoder_t *d, const float *enc, uint32_t parity, uint32_t decide_only) {
+    const model_t *m = d->m;
+    NkDecArgs a;
+    memset(&a, 0, sizeof a);
+    a.st = gpu_buf_dptr(d->st);
+    a.part = gpu_buf_dptr(d->part);
+    a.tokens = gpu_buf_dptr(d->tokens);
+    a.enc = enc;
+    a.embed = m->embed_dev;
+    a.wx0 = m->lstm_wx[0]; a.wh0 = m->lstm_wh[0]; a.wx1 = m->lstm_wx[1]; a.wh1 = m->lstm_wh[1];
+    a.b0 = m->lstm_b[0]; a.b1 = m->lstm_b[1];
+    a.hc = gpu_buf_dptr(d->hc);
+    a.wjp = m->joint_pred_w; a.bjp = m->joint_pred_b;
+    a.pred = gpu_buf_dptr(d->pred);
+    a.wout = m->joint_out_w; a.bout = m->joint_out_b;
+    a.P = (uint32_t)m->cfg.pred_hidden;
+    a.J = (uint32_t)m->cfg.joint_hidden;
+    a.V = (uint32_t)m->cfg.num_classes;
+    a.blank = (uint32_t)m->cfg.blank_id;
+    a.max_symbols = (uint32_t)m->cfg.max_symbols;
+    a.parity = parity;
+    a.enc_ld = a.J;
+    a.decide_only = decide_only;
+    return a;
+}
+
+/* `steps` steps (odd) then the decision of the last joint: step j reads state copy j%2, so the run
+ * ends with the state back in copy 0, where the next run starts. */
+static int launch_steps(decoder_t *d, const float *enc, int steps) {
     gpu_t *g = d->g;
-    const uint32_t P = (uint32_t)m->cfg.pred_hidden, J = (uint32_t)m->cfg.joint_hidden;
-    if (d->last_token == m->cfg.blank_id) memset(d->x_host, 0, P * sizeof(float));
-    else {
-        const uint16_t *row = m->embed_host + (size_t)d->last_token * P;
-        for (uint32_t i = 0; i < P; ++i) d->x_host[i] = st_bf16(row[i]);
+    const uint32_t P = (uint32_t)d->m->cfg.pred_hidden, J = (uint32_t)d->m->cfg.joint_hidden;
+    for (int j = 0; j <= steps; ++j) {
+        const NkDecArgs a = dec_args(d, enc, (uint32_t)j & 1u, j == steps);
+        if (gpu_launch(g, "dec_lstm0", &a, sizeof a, (P + 3) / 4, 1, 1, 256, 1, 1)) return -1;
+        if (j == steps) break;
+        if (gpu_launch(g, "dec_lstm1", &a, sizeof a, (P + 3) / 4, 1, 1, 256, 1, 1)) return -1;
+        if (gpu_launch(g, "dec_pred", &a, sizeof a, (J + 3) / 4, 1, 1, 256, 1, 1)) return -1;
+        if (gpu_launch(g, "dec_joint", &a, sizeof a, NK_DEC_GROUPS, NK_DEC_MAX_BATCH, 1, 256, 1, 1)) return -1;
     }
-    gpu_upload_async(g, gpu_buf_dptr(d->x), d->x_host, P * sizeof(float));
-    const float *in = gpu_buf_dptr(d->x);
-    float *gates = gpu_buf_dptr(d->gates);
-    for (int l = 0; l < 2; ++l) {
-        nk_gemm(g, in, P, m->lstm_wx[l], P, m->lstm_b[l], gates, 4 * P, 1, 4 * P, P, NK_ACT_NONE, 0, 1.0f);
-        nk_gemm(g, d->h[l], P, m->lstm_wh[l], P, NULL, gates, 4 * P, 1, 4 * P, P, NK_ACT_NONE, 1, 1.0f);
-        nk_lstm_cell(g, gates, d->c[l], d->cp[l], d->hp[l], P);
-        in = d->hp[l];
-    }
-    nk_gemm(g, d->hp[1], P, m->joint_pred_w, P, m->joint_pred_b, gpu_buf_dptr(d->pred_out), J, 1, J, P, NK_ACT_NONE, 0, 1.0f);
+    return 0;
+}
+
+static dgraph_t *graphs_for(decoder_t *d, const float *enc) {
+    for (int i = 0; i < d->ngr; ++i)
+        if (d->gr[i].enc == enc) return &d->gr[i];
+    if (d->ngr == 2) free_graphs(d);
+    dgraph_t *x = &d->gr[d->ngr++];
+    x->enc = enc;
+    return x;
 }
 
 int decoder_run(decoder_t *d, const float *joint_enc, int frames, int *out, int max_out, char *err, size_t errlen) {
     model_t *m = d->m;
     gpu_t *g = d->g;
     const double t0 = now_ms();
-    const uint32_t J = (uint32_t)m->cfg.joint_hidden, V = (uint32_t)m->cfg.num_classes;
-    int n = 0, steps = 0, t = 0, symbols = 0;
-    while (t < frames) {
-        int rows = frames - t;
-        if (rows > NK_DEC_MAX_BATCH) rows = NK_DEC_MAX_BATCH;
-        gpu_begin(g);
-        if (!d->pred_valid) encode_pred(d);
-        nk_joint_argmax(g, joint_enc, (uint32_t)t, J, (uint32_t)rows, gpu_buf_dptr(d->pred_out), m->joint_out_w,
-                        m->joint_out_b, V, J, gpu_buf_dptr(d->part_v), gpu_buf_dptr(d->part_i), gpu_buf_dptr(d->argmax));
-        gpu_download_async(g, d->res_host, gpu_buf_dptr(d->argmax), (size_t)rows * 2 * sizeof(int));
-        if (gpu_end(g, err, errlen)) return -1;
-        steps++;
-        d->pred_valid = 1;
-        int i = 0;
-        for (; i < rows; ++i) {
-            const int pred = d->res_host[2 * i];
-            if (pred == m->cfg.blank_id) { symbols = 0; continue; } /* blank: frame done, keep the prediction */
-            if (n < max_out) out[n++] = pred;
-            d->last_token = pred;
-            for (int l = 0; l < 2; ++l) { /* commit the provisional state */
-                float *s = d->h[l]; d->h[l] = d->hp[l]; d->hp[l] = s;
-                s = d->c[l]; d->c[l] = d->cp[l]; d->cp[l] = s;
-            }
-            d->pred_valid = 0;
-            symbols++;
-            if (symbols >= m->cfg.max_symbols) { symbols = 0; i++; } /* frame exhausted: move on */
-            break; /* later frames were scored with the old prediction: redo them */
-        }
-        t += i;
+    d->last_steps = 0;
+    if (frames <= 0) { d->last_ms = now_ms() - t0; return 0; }
+    const uint32_t P = (uint32_t)m->cfg.pred_hidden, J = (uint32_t)m->cfg.joint_hidden;
+    if (frames > NK_DEC_MAX_BATCH || P % 8 || P > 1024 || J % 8 || J > 1024 || m->cfg.num_classes > 32 * NK_DEC_GROUPS ||
+        (long)frames * m->cfg.max_symbols > NK_DEC_MAX_TOKENS) {
+        snprintf(err, errlen, "decoder: unsupported sizes (frames %d, pred %u, joint %u)", frames, P, J);
+        return -1;
     }
+    dgraph_t *gr = graphs_for(d, joint_enc);
+    /* chunk fields of state copy 0: frames, t, symbols, n_out, pending, joints */
+    NkDecState *h = d->host_st;
+    memset(h, 0, sizeof *h);
+    h->frames = frames;
+    int n = 0;
+    for (int run = 0;; ++run) {
+        if (run >= MAX_GRAPHS_PER_CHUNK) { snprintf(err, errlen, "decoder: no progress"); return -1; }
+        const int which = run ? 1 : 0;
+        gpu_begin(g);
+        if (!run) gpu_upload_async(g, gpu_buf_dptr(d->st), h, 6 * sizeof(int));
+        if (!gr->g[which]) {
+            if (!gpu_capture_begin(g)) {
+                launch_steps(d, joint_enc, which ? STEPS_MORE : STEPS_FIRST);
+                gr->g[which] = gpu_capture_end(g);
+            }
+        }
+        if (gr->g[which]) gpu_graph_launch(g, gr->g[which]);
+        else launch_steps(d, joint_enc, which ? STEPS_MORE : STEPS_FIRST);
+        gpu_download_async(g, h, gpu_buf_dptr(d->st), sizeof *h);
+        gpu_download_async(g, d->host_tok, gpu_buf_dptr(d->tokens), NK_DEC_MAX_TOKENS * sizeof(int));
+        if (gpu_end(g, err, errlen)) return -1;
+        if (h->done) break;
+    }
+    const int nt = h->n_out < NK_DEC_MAX_TOKENS ? h->n_out : NK_DEC_MAX_TOKENS;
+    for (int i = 0; i < nt; ++i)
+        if (n < max_out) out[n++] = d->host_tok[i];
+    d->last_steps = h->joints;
     d->last_ms = now_ms() - t0;
-    d->last_steps = steps;
     return n;
 }

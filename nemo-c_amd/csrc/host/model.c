@@ -203,6 +203,7 @@ model_t *model_load(const char *dir, char *err, size_t errlen) {
     }
     addb(&r, "joint.pred.weight", J * P, &m->joint_pred_w); addf(&r, "joint.pred.bias", J, &m->joint_pred_b);
     addb(&r, "joint.joint_net.2.weight", V * J, &m->joint_out_w); addf(&r, "joint.joint_net.2.bias", V, &m->joint_out_b);
+    addb(&r, "decoder.prediction.embed.weight", (size_t)(g->vocab_size + 1) * P, &m->embed_dev);
 #undef PB
 #undef PF
 

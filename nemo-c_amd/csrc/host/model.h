@@ -2,7 +2,7 @@
  *
  * Reads config.json and model.safetensors with the keys, tensor names and checks of the reference
  * (src/model.c:41-67 tensor checks, :125-172 config, :215-282 tensor list, :286-306 position
- * table, :390-400 prompt fold).  Layout on the device:
+ * table, :312-322 prompt fold).  Layout on the device:
  *   - one bf16 weight arena, 4 KB-aligned matrices, in the order a chunk reads them
  *     (pre-encode, then per layer ff1, qkv, out, pw1, pw2, ff2, then prompt, joint, decoder);
  *     q, k and v are packed into one [3D][D] matrix for the fused QKV GEMM;
@@ -51,7 +51,8 @@ typedef struct model {
     /* decoder + joint */
     const uint16_t *lstm_wx[2], *lstm_wh[2], *joint_enc_w, *joint_pred_w, *joint_out_w;
     const float *lstm_b[2], *joint_enc_b, *joint_pred_b, *joint_out_b;
-    uint16_t *embed_host;    /* [vocab+1][pred_hidden] bf16, read per emitted token */
+    uint16_t *embed_host;    /* [vocab+1][pred_hidden] bf16 (host copy) */
+    const uint16_t *embed_dev; /* the same table in the weight arena, read by the device decoder loop */
     double load_ms;
 } model_t;
 

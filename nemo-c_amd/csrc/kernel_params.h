@@ -168,4 +168,34 @@ typedef struct {
     u32 n, pad;
 } NkArgmaxArgs;
 
+/* ---- device-resident greedy RNNT loop -------------------------------------------------------- */
+#define NK_DEC_MAX_TOKENS 256 /* tokens per chunk: at most 16 frames x max_symbols                  */
+#define NK_DEC_GROUPS 40      /* joint workgroups per frame row, 32 vocabulary rows each (V <= 1280) */
+
+/* State of the loop, kept on the device across chunks.  Two copies alternate by iteration parity:
+ * iteration j reads copy j%2 and writes copy (j+1)%2.  The first six fields are reset by the host at
+ * the start of every chunk. */
+typedef struct {
+    int frames, t, symbols, n_out, pending, joints; /* chunk fields                                 */
+    int pred_valid, last_token, cur, done, need_pred; /* persistent: cur = committed LSTM state slot */
+    int pad[5];
+} NkDecState;
+
+typedef struct {
+    NkDecState *st;           /* [2]                                                              */
+    unsigned long long *part; /* [2][NK_DEC_MAX_BATCH][NK_DEC_GROUPS] packed (score, index) keys   */
+    int *tokens;              /* [NK_DEC_MAX_TOKENS] tokens emitted in the current chunk             */
+    const float *enc;         /* joint.enc rows of the chunk, [frames][enc_ld]                       */
+    const u16 *embed;         /* prediction embedding [blank + 1][P]                                 */
+    const u16 *wx0, *wh0, *wx1, *wh1; /* LSTM [4P][P], gate order i, f, g, o                         */
+    const float *b0, *b1;     /* [4P]                                                              */
+    float *hc;                /* LSTM state [2 slots][h0, h1, c0, c1][P]                            */
+    const u16 *wjp;           /* joint.pred [J][P]                                                  */
+    const float *bjp;
+    float *pred;              /* [J]                                                               */
+    const u16 *wout;          /* joint output [V][J]                                                */
+    const float *bout;        /* [V]                                                               */
+    u32 P, J, V, blank, max_symbols, parity, enc_ld, decide_only;
+} NkDecArgs;
+
 #endif

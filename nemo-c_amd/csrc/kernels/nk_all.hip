@@ -3,3 +3,4 @@
 #include "nk_gemv.hip"
 #include "nk_seq.hip"
 #include "nk_ops.hip"
+#include "nk_dec.hip"

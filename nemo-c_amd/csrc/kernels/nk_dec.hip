@@ -1,0 +1,270 @@
+/* Device-resident greedy RNNT loop for gfx950: the reference's decoder_run (src/decoder.c:92-127)
+ * without a host round trip per joint evaluation.
+ *
+ * One iteration of the loop is four launches, captured into a graph that holds a run of
+ * iterations (the host replays it until the chunk is done):
+ *   dec_lstm0  every wavefront first takes the decision of the previous iteration's joint (the
+ *              greedy rule of src/decoder.c:107-122: first non-blank row wins; blank rows reset
+ *              the symbol count; max_symbols moves past the frame) from the packed per-workgroup
+ *              argmax keys, workgroup 0 records it (next state copy, emitted token); then, when the
+ *              prediction must be recomputed, LSTM layer 0 from embed(last token)
+ *              (src/decoder.c:57-77; zeros for blank);
+ *   dec_lstm1  LSTM layer 1;
+ *   dec_pred   joint.pred projection of the new hidden state;
+ *   dec_joint  joint scores relu(enc[t + r] + pred) . W_out + b for up to 16 remaining frames
+ *              with one prediction (speculating blank, src/decoder.c:79-90); each workgroup
+ *              writes the best (score, lowest index) of its 32 vocabulary rows.
+ * Kernels whose work is not needed return at once.  Every value is computed in the reference's
+ * order of operations: gates = (Wx.x + b) + Wh.h; c' = f*c + i*g; h' = o*tanh(c'); the argmax keeps
+ * the lowest index on ties.  The LSTM weights are streamed with the wave64 layout of the GEMV
+ * (lane l reads the 16-byte chunks l and l + 64 of every row). */
+#include "nk_common.h"
+
+/* (score, index) -> 64-bit key whose unsigned order is: higher score first, then lower index */
+__device__ __forceinline__ unsigned long long dec_key(float v, u32 n) {
+    v += 0.0f; /* -0 -> +0 so that equal scores compare equal */
+    const u32 b = __float_as_uint(v);
+    const u32 ord = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+    return ((unsigned long long)ord << 32) | (0xffffffffu - n);
+}
+__device__ __forceinline__ u32 dec_key_index(unsigned long long k) { return 0xffffffffu - (u32)(k & 0xffffffffu); }
+
+__device__ __forceinline__ unsigned long long shfl_xor_u64(unsigned long long v, int m) {
+    const u32 lo = (u32)__shfl_xor((int)(u32)v, m, 64), hi = (u32)__shfl_xor((int)(u32)(v >> 32), m, 64);
+    return ((unsigned long long)hi << 32) | lo;
+}
+
+/* The decision of the previous joint, taken by one wavefront (every wavefront gets the same
+ * answer).  Returns the new state; *tok = emitted token or -1. */
+__device__ __forceinline__ NkDecState dec_decide(const NkDecArgs &a, const NkDecState s, int *tok) {
+    NkDecState d = s;
+    *tok = -1;
+    if (!s.pending) return d;
+    const u32 lane = threadIdx.x & 63;
+    const int rows = min(NK_DEC_MAX_BATCH, s.frames - s.t);
+    /* lane l reduces groups l/16, l/16 + 4, ... of row l % 16; then the four lanes of a row combine */
+    const unsigned long long *pp = a.part + (u64)(a.parity ^ 1) * NK_DEC_MAX_BATCH * NK_DEC_GROUPS;
+    const u32 r = lane & 15;
+    unsigned long long best = 0;
+#pragma unroll
+    for (int q = 0; q < NK_DEC_GROUPS / 4; ++q) {
+        const unsigned long long k = pp[r * NK_DEC_GROUPS + (lane >> 4) + 4 * q];
+        best = k > best ? k : best;
+    }
+    unsigned long long o = shfl_xor_u64(best, 16);
+    best = o > best ? o : best;
+    o = shfl_xor_u64(best, 32);
+    best = o > best ? o : best;
+    const u32 idx = dec_key_index(best);
+    const bool nonblank = (int)r < rows && idx != a.blank;
+    const unsigned long long mask = __ballot(nonblank);
+    d.pending = 0;
+    d.joints = s.joints + 1;
+    if (!mask) { /* every scored frame decodes to blank: frames done, prediction kept */
+        d.t = s.t + rows;
+        d.symbols = 0;
+        return d;
+    }
+    const int first = __builtin_ctzll(mask);
+    const u32 t_idx = (u32)__shfl((int)idx, first, 64);
+    *tok = (int)t_idx;
+    d.last_token = (int)t_idx;
+    d.cur = s.cur ^ 1; /* commit the provisional LSTM state */
+    d.pred_valid = 0;
+    d.n_out = s.n_out + 1;
+    d.symbols = (first > 0 ? 0 : s.symbols) + 1;
+    if (d.symbols >= (int)a.max_symbols) { d.symbols = 0; d.t = s.t + first + 1; }
+    else d.t = s.t + first;
+    return d;
+}
+
+/* One LSTM layer for unit j = global wavefront index: four gate rows of Wx and Wh (K = P <= 1024,
+ * two 16-byte chunks per lane per row), then the cell.  x_f32 (or x_bf16 for the embedding row,
+ * or zeros when x_zero) is the layer input. */
+__device__ __forceinline__ void dec_lstm_unit(const NkDecArgs &a, u32 j, const float *x_f32, const u16 *x_bf16,
+                                              bool x_zero, const u16 *Wx, const u16 *Wh, const float *bias,
+                                              const float *h_in, const float *c_in, float *h_out, float *c_out) {
+    const u32 lane = threadIdx.x & 63, P = a.P, nch = P >> 3;
+    float x[2][8], h[2][8];
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+        const u32 k = 8 * min(lane + 64 * q, nch - 1);
+        if (x_bf16) {
+            const uint4 w = *(const uint4 *)(x_bf16 + k);
+            x[q][0] = bf_lo(w.x); x[q][1] = bf_hi(w.x); x[q][2] = bf_lo(w.y); x[q][3] = bf_hi(w.y);
+            x[q][4] = bf_lo(w.z); x[q][5] = bf_hi(w.z); x[q][6] = bf_lo(w.w); x[q][7] = bf_hi(w.w);
+        } else {
+            const floatx4 p0 = *(const floatx4 *)(x_f32 + k), p1 = *(const floatx4 *)(x_f32 + k + 4);
+            x[q][0] = p0[0]; x[q][1] = p0[1]; x[q][2] = p0[2]; x[q][3] = p0[3];
+            x[q][4] = p1[0]; x[q][5] = p1[1]; x[q][6] = p1[2]; x[q][7] = p1[3];
+        }
+        const floatx4 p0 = *(const floatx4 *)(h_in + k), p1 = *(const floatx4 *)(h_in + k + 4);
+        h[q][0] = p0[0]; h[q][1] = p0[1]; h[q][2] = p0[2]; h[q][3] = p0[3];
+        h[q][4] = p1[0]; h[q][5] = p1[1]; h[q][6] = p1[2]; h[q][7] = p1[3];
+    }
+    float bg[4];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) bg[g] = bias[g * P + j];
+    const float c0 = c_in[j];
+    __builtin_amdgcn_sched_barrier(0);
+    uint4 wx[4][2], wh[4][2];
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            const u64 off = (u64)(g * P + j) * P + 8 * min(lane + 64 * q, nch - 1);
+            wx[g][q] = ld_nt16(Wx + off);
+            wh[g][q] = ld_nt16(Wh + off);
+        }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+        const bool ok = lane + 64 * q < nch;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            x[q][e] = ok && !x_zero ? x[q][e] : 0.0f;
+            h[q][e] = ok ? h[q][e] : 0.0f;
+        }
+    }
+    float gate[4];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        float sx = 0.0f, sh = 0.0f;
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            sx = dot8(x[q], wx[g][q], sx);
+            sh = dot8(h[q], wh[g][q], sh);
+        }
+        gate[g] = (wsum(sx) + bg[g]) + wsum(sh);
+    }
+    if (lane != 0) return;
+    const float ig = sigmoid_f(gate[0]), fg = sigmoid_f(gate[1]), gg = tanhf(gate[2]), og = sigmoid_f(gate[3]);
+    const float c = fg * c0 + ig * gg;
+    c_out[j] = c;
+    h_out[j] = og * tanhf(c);
+}
+
+/* decision + LSTM layer 0.  grid = ceil(P/4) x 1, block 256 (one unit per wavefront). */
+extern "C" __global__ __launch_bounds__(256) void dec_lstm0(const NkDecArgs a) {
+    const NkDecState s = a.st[a.parity];
+    int tok;
+    NkDecState d = dec_decide(a, s, &tok);
+    d.done = d.t >= d.frames;
+    d.need_pred = !d.done && !d.pred_valid && !a.decide_only;
+    const u32 j = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (j == 0 && (threadIdx.x & 63) == 0) {
+        NkDecState ns = d;
+        if (d.need_pred) ns.pred_valid = 1;
+        ns.pending = !d.done && !a.decide_only;
+        a.st[a.parity ^ 1] = ns;
+        if (tok >= 0 && d.n_out <= NK_DEC_MAX_TOKENS) a.tokens[d.n_out - 1] = tok;
+    }
+    if (!d.need_pred || j >= a.P) return;
+    const u32 P = a.P, cm = (u32)d.cur, pv = cm ^ 1u;
+    const float *hc_c = a.hc + (u64)cm * 4 * P, *none = nullptr;
+    float *hc_p = a.hc + (u64)pv * 4 * P;
+    const bool blank = d.last_token == (int)a.blank || d.last_token < 0;
+    const u16 *emb = a.embed + (u64)(blank ? 0 : d.last_token) * P;
+    dec_lstm_unit(a, j, none, emb, blank, a.wx0, a.wh0, a.b0, hc_c, hc_c + 2 * P, hc_p, hc_p + 2 * P);
+}
+
+/* LSTM layer 1 from the new layer-0 state */
+extern "C" __global__ __launch_bounds__(256) void dec_lstm1(const NkDecArgs a) {
+    const NkDecState s = a.st[a.parity ^ 1];
+    const u32 j = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (!s.need_pred || j >= a.P) return;
+    const u32 P = a.P, cm = (u32)s.cur, pv = cm ^ 1u;
+    const float *hc_c = a.hc + (u64)cm * 4 * P;
+    float *hc_p = a.hc + (u64)pv * 4 * P;
+    dec_lstm_unit(a, j, hc_p, nullptr, false, a.wx1, a.wh1, a.b1, hc_c + P, hc_c + 3 * P, hc_p + P, hc_p + 3 * P);
+}
+
+/* pred = joint.pred . h1' + b; one output per wavefront (K = P <= 1024) */
+extern "C" __global__ __launch_bounds__(256) void dec_pred(const NkDecArgs a) {
+    const NkDecState s = a.st[a.parity ^ 1];
+    const u32 j = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (!s.need_pred || j >= a.J) return;
+    const u32 P = a.P, nch = P >> 3;
+    const float *h = a.hc + (u64)(s.cur ^ 1) * 4 * P + P;
+    float x[2][8];
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+        const u32 k = 8 * min(lane + 64 * q, nch - 1);
+        const floatx4 p0 = *(const floatx4 *)(h + k), p1 = *(const floatx4 *)(h + k + 4);
+        x[q][0] = p0[0]; x[q][1] = p0[1]; x[q][2] = p0[2]; x[q][3] = p0[3];
+        x[q][4] = p1[0]; x[q][5] = p1[1]; x[q][6] = p1[2]; x[q][7] = p1[3];
+    }
+    const float b = a.bjp[j];
+    __builtin_amdgcn_sched_barrier(0);
+    uint4 w[2];
+#pragma unroll
+    for (int q = 0; q < 2; ++q) w[q] = ld_nt16(a.wjp + (u64)j * P + 8 * min(lane + 64 * q, nch - 1));
+    __builtin_amdgcn_sched_barrier(0);
+    float acc = 0.0f;
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+        const bool ok = lane + 64 * q < nch;
+        float xm[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) xm[e] = ok ? x[q][e] : 0.0f;
+        acc = dot8(xm, w[q], acc);
+    }
+    const float v = wsum(acc) + b;
+    if (lane == 0) a.pred[j] = v;
+}
+
+/* joint scores of frame t + blockIdx.y over vocabulary rows [32*blockIdx.x, +32): wavefront w
+ * scores rows 32*g + 8*w + i (i < 8); the workgroup's best key goes to part[parity][row][g].
+ * grid = (NK_DEC_GROUPS, NK_DEC_MAX_BATCH), block 256.  J <= 1024. */
+extern "C" __global__ __launch_bounds__(256) void dec_joint(const NkDecArgs a) {
+    __shared__ unsigned long long wbest[4];
+    const NkDecState s = a.st[a.parity ^ 1];
+    const int r = (int)blockIdx.y;
+    if (!s.pending || r >= min(NK_DEC_MAX_BATCH, s.frames - s.t)) return;
+    const u32 lane = threadIdx.x & 63, wave = threadIdx.x >> 6, J = a.J, nch = J >> 3;
+    const u32 n0 = blockIdx.x * 32 + wave * 8;
+    const float *e = a.enc + (u64)(s.t + r) * a.enc_ld;
+    float x[2][8];
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+        const u32 k = 8 * min(lane + 64 * q, nch - 1);
+        const floatx4 e0 = *(const floatx4 *)(e + k), e1 = *(const floatx4 *)(e + k + 4);
+        const floatx4 p0 = *(const floatx4 *)(a.pred + k), p1 = *(const floatx4 *)(a.pred + k + 4);
+        x[q][0] = e0[0] + p0[0]; x[q][1] = e0[1] + p0[1]; x[q][2] = e0[2] + p0[2]; x[q][3] = e0[3] + p0[3];
+        x[q][4] = e1[0] + p1[0]; x[q][5] = e1[1] + p1[1]; x[q][6] = e1[2] + p1[2]; x[q][7] = e1[3] + p1[3];
+    }
+    float bias[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) bias[i] = a.bout[min(n0 + i, a.V - 1)];
+    __builtin_amdgcn_sched_barrier(0);
+    uint4 w[8][2];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int q = 0; q < 2; ++q) w[i][q] = ld_nt16(a.wout + (u64)min(n0 + i, a.V - 1) * J + 8 * min(lane + 64 * q, nch - 1));
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+        const bool ok = lane + 64 * q < nch;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) x[q][k] = ok ? fmaxf(x[q][k], 0.0f) : 0.0f;
+    }
+    unsigned long long best = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int q = 0; q < 2; ++q) acc = dot8(x[q], w[i][q], acc);
+        const float v = wsum(acc) + bias[i];
+        const unsigned long long k = n0 + i < a.V ? dec_key(v, n0 + i) : 0ull;
+        best = k > best ? k : best;
+    }
+    if (lane == 0) wbest[wave] = best;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        unsigned long long b = wbest[0];
+#pragma unroll
+        for (int w2 = 1; w2 < 4; ++w2) b = wbest[w2] > b ? wbest[w2] : b;
+        a.part[((u64)a.parity * NK_DEC_MAX_BATCH + r) * NK_DEC_GROUPS + blockIdx.x] = b;
+    }
+}
