@@ -58,10 +58,12 @@ def main():
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--latency", type=int, default=80, choices=sorted(LAT_RIGHT))
     ap.add_argument("--seconds", type=float, default=10.0)
-    ap.add_argument("--cpu-sample-s", type=float, default=3.0)
+    ap.add_argument("--cpu-sample-s", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-graphs", action="store_true")
     ap.add_argument("--kernel", default=None, help="kernel whose launches are timed for the roofline")
+    ap.add_argument("--copy-calib-mib", type=int, default=0,
+                    help="first run one device copy of this many MiB (a known-size reference for HBM counters)")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py: this build runs one stream set on one GPU; --gpus {a.gpus} is not supported "
@@ -81,6 +83,14 @@ def main():
 
     s = nemoasr.Session(mdir, "en-US", a.latency)
     s.use_graphs(not a.no_graphs)
+    if a.copy_calib_mib:
+        g = nemoasr.Gpu()
+        nb = a.copy_calib_mib << 20
+        src, dst = g.alloc(nb), g.alloc(nb)
+        g.begin()
+        g.check(nemoasr.lib().nk_copy(g.h, src.ptr, dst.ptr, nb // 4))
+        g.end()
+        g.close()
 
     def clip():
         s.reset("en-US", a.latency)

@@ -36,7 +36,7 @@ struct decoder {
     NkDecState *host_st; /* pinned: chunk fields in, final state out */
     int *host_tok;       /* pinned: tokens of the chunk               */
     dgraph_t gr[2];
-    int ngr, last_steps;
+    int ngr, last_steps, use_graphs;
     double last_ms;
 };
 
@@ -52,6 +52,7 @@ decoder_t *decoder_create(model_t *m) {
     d->pred = gpu_buf_alloc(d->g, J * sizeof(float));
     d->host_st = gpu_host_alloc(d->g, sizeof(NkDecState));
     d->host_tok = gpu_host_alloc(d->g, NK_DEC_MAX_TOKENS * sizeof(int));
+    d->use_graphs = 1;
     decoder_reset(d);
     return d;
 }
@@ -87,6 +88,10 @@ void decoder_reset(decoder_t *d) {
     gpu_upload(d->g, gpu_buf_dptr(d->st), s, sizeof s);
 }
 double decoder_last_ms(const decoder_t *d) { return d->last_ms; }
+void decoder_use_graphs(decoder_t *d, int on) {
+    d->use_graphs = on;
+    if (!on) free_graphs(d);
+}
 int decoder_last_steps(const decoder_t *d) { return d->last_steps; }
 
 static NkDecArgs dec_args(decoder_t *d, const float *enc, uint32_t parity, uint32_t decide_only) {
@@ -163,7 +168,7 @@ int decoder_run(decoder_t *d, const float *joint_enc, int frames, int *out, int 
         const int which = run ? 1 : 0;
         gpu_begin(g);
         if (!run) gpu_upload_async(g, gpu_buf_dptr(d->st), h, 6 * sizeof(int));
-        if (!gr->g[which]) {
+        if (d->use_graphs && !gr->g[which]) {
             if (!gpu_capture_begin(g)) {
                 launch_steps(d, joint_enc, which ? STEPS_MORE : STEPS_FIRST);
                 gr->g[which] = gpu_capture_end(g);

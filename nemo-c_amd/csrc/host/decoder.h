@@ -13,6 +13,8 @@ void decoder_reset(decoder_t *d);
  * Returns the count, or -1 on error. */
 int decoder_run(decoder_t *d, const float *joint_enc, int frames, int *out, int max_out, char *err, size_t errlen);
 double decoder_last_ms(const decoder_t *d);
+/* 1 (default): replay each run of steps from a captured hipGraph; 0: launch every kernel directly */
+void decoder_use_graphs(decoder_t *d, int on);
 int decoder_last_steps(const decoder_t *d); /* joint evaluations (round trips) in the last run */
 
 #endif

@@ -289,7 +289,10 @@ size_t nemoasr_debug_frames(const nemoasr_t *s) { return encoder_dump_frames(s->
 const float *nemoasr_debug_dump_layers(const nemoasr_t *s) { return encoder_dump_layers(s->enc); }
 const float *nemoasr_debug_dump_prompted(const nemoasr_t *s) { return encoder_dump_prompted(s->enc); }
 const float *nemoasr_debug_dump_joint_enc(const nemoasr_t *s) { return encoder_dump_joint(s->enc); }
-void nemoasr_debug_use_graphs(nemoasr_t *s, int on) { encoder_use_graphs(s->enc, on); }
+void nemoasr_debug_use_graphs(nemoasr_t *s, int on) {
+    encoder_use_graphs(s->enc, on);
+    decoder_use_graphs(s->dec, on);
+}
 size_t nemoasr_debug_joint_steps(const nemoasr_t *s) { return s->joint_steps; }
 double nemoasr_debug_encoder_gpu_ms(const nemoasr_t *s) { return s->enc_gpu_ms; }
 const double *nemoasr_debug_chunk_ms(const nemoasr_t *s, size_t *n) {

@@ -201,7 +201,7 @@ int nk_attention_rel(gpu_t *g, const float *Q, uint32_t ldq, const float *K, con
     if ((uintptr_t)Q % 16 || (uintptr_t)K % 16 || (uintptr_t)V % 16 || ldq % 4 || ldk % 4)
         return bad(g, "attention: Q/K/V must be 16-byte aligned");
     NkAttnArgs a = { Q, K, V, P, bias_u, bias_v, O, NULL, c, L, Lmax, H, dh, D, ldq, ldk, scale, 0 };
-    return gpu_launch(g, "attention_rel", &a, sizeof a, H, c, 1, 256, 1, 1);
+    return gpu_launch(g, "attention_rel", &a, sizeof a, H, c, 1, 512, 1, 1);
 }
 
 int nk_attention_rel_desc(gpu_t *g, const float *kv, uint32_t ld, const int *desc, const float *P, const float *bias_u,
@@ -211,7 +211,7 @@ int nk_attention_rel_desc(gpu_t *g, const float *kv, uint32_t ld, const int *des
     if (dh != 128 || H * dh != D || c > Lmax || Lmax > NK_ATT_MAX_L) return bad(g, "attention: head_dim must be 128");
     if ((uintptr_t)kv % 16 || ld % 4) return bad(g, "attention: cache must be 16-byte aligned");
     NkAttnArgs a = { kv, kv + D, kv + 2 * D, P, bias_u, bias_v, O, desc, c, 0, Lmax, H, dh, D, ld, ld, scale, 0 };
-    return gpu_launch(g, "attention_rel", &a, sizeof a, H, c, 1, 256, 1, 1);
+    return gpu_launch(g, "attention_rel", &a, sizeof a, H, c, 1, 512, 1, 1);
 }
 
 int nk_dwconv_ln_silu(gpu_t *g, const float *din, const float *W, const float *gamma, const float *beta, float *Y,

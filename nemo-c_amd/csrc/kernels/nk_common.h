@@ -68,6 +68,19 @@ __device__ __forceinline__ float wsum(float v) {
     return (r0 + r1) + (r2 + r3);
 }
 
+/* Maximum over the 64 lanes of a wavefront, returned wave-uniform (DPP rows, then four lanes). */
+__device__ __forceinline__ float wmax(float v) {
+    v = fmaxf(v, dpp_f<DPP_QUAD_1032>(v));
+    v = fmaxf(v, dpp_f<DPP_QUAD_2301>(v));
+    v = fmaxf(v, dpp_f<DPP_ROW_ROR4>(v));
+    v = fmaxf(v, dpp_f<DPP_ROW_ROR8>(v));
+    const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+    const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+    const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+    return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
+}
+
 /* Dot of 8 f32 activations with 8 bf16 weights packed in a uint4, summed in index order. */
 __device__ __forceinline__ float dot8(const float *a, uint4 w, float acc) {
     acc += a[0] * bf_lo(w.x);

@@ -75,18 +75,23 @@ extern "C" __global__ __launch_bounds__(256) void layernorm(const NkLnArgs a) {
         if (tid + k * 256 < D4) y2[tid + k * 256] = v[k];
 }
 
-/* Relative-position attention, one workgroup of 256 threads per (head, query):
+/* Workgroup barrier for data exchanged through LDS only (does not wait for outstanding global
+ * loads, which a __syncthreads() would). */
+__device__ __forceinline__ void lds_sync() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+/* Relative-position attention, one workgroup of 512 threads per (head, query i):
  * reference src/kernels.metal:290-348.
  *   score_j = ((q + u) . K_j + (q + v) . P[(Lmax - L) + (c - 1 - i + j)]) * scale
  *   O_i = sum_j softmax(score)_j V_j  (no mask inside the chunk)
- * Scores: four threads share a key (32 head dims each), 64 keys per pass, two passes (L <= 128).
+ * Scores: four threads per key (32 head dims each), one key per thread quad (L <= 128).
  * Output: thread (g = tid / 32, d4 = tid % 32) accumulates dims 4*d4..4*d4+3 over the keys
- * j = g (mod 8); the 8 key groups are summed in order through LDS.  Every K, P and V load is
- * issued before the first score is formed; q + u and q + v come from LDS. */
-extern "C" __global__ __launch_bounds__(256) void attention_rel(const NkAttnArgs a) {
-    __shared__ float4 qu4[32], qv4[32];
-    __shared__ float s[NK_ATT_MAX_L], red[8];
-    __shared__ float4 part[8][32];
+ * j = g (mod 16); the 16 key groups are summed in order through LDS.  Every K, P and V load is
+ * issued at the start (indices past the window clamped to a valid row and masked at use); the
+ * barriers wait for LDS only, so the V loads stay in flight through the score phase. */
+extern "C" __global__ __launch_bounds__(512) void attention_rel(const NkAttnArgs a) {
+    __shared__ floatx4 qu4[32], qv4[32];
+    __shared__ float s[NK_ATT_MAX_L], red[16];
+    __shared__ floatx4 part[16][32];
     const u32 h = blockIdx.x, i = blockIdx.y, tid = threadIdx.x;
     const u32 off = h * 128;
     const float *Q = a.Q, *Kp = a.K, *Vp = a.V;
@@ -98,84 +103,77 @@ extern "C" __global__ __launch_bounds__(256) void attention_rel(const NkAttnArgs
         Vp += (u64)(pos - cl) * a.ldk;
         L = cl + a.c;
     }
-    const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
-    /* V rows for the output phase */
-    const u32 vg = tid >> 5, d4 = tid & 31;
-    float4 vv[NK_ATT_MAX_L / 8];
-#pragma unroll
-    for (int t = 0; t < NK_ATT_MAX_L / 8; ++t) {
-        const u32 j = vg + 8 * t;
-        vv[t] = j < L ? *(const float4 *)(Vp + (u64)j * a.ldk + off + 4 * d4) : z;
-    }
-    /* K and P rows of this thread's keys */
-    const u32 ks = tid >> 2, part4 = tid & 3, dofs = off + part4 * 32;
-    float4 kr[2][8], pr[2][8];
-#pragma unroll
-    for (int p = 0; p < 2; ++p) {
-        const u32 j = ks + 64 * p;
-        const bool ok = j < L;
-        const u32 prow = (a.Lmax - L) + (a.c - 1 - i + j);
-#pragma unroll
-        for (int q = 0; q < 8; ++q) {
-            kr[p][q] = ok ? *(const float4 *)(Kp + (u64)j * a.ldk + dofs + 4 * q) : z;
-            pr[p][q] = ok ? *(const float4 *)(a.P + (u64)prow * a.D + dofs + 4 * q) : z;
-        }
-    }
+    /* q + u, q + v for this head */
+    floatx4 qx = { 0.f, 0.f, 0.f, 0.f }, ux = qx, vx = qx;
     if (tid < 32) {
-        const float4 x = *(const float4 *)(Q + (u64)i * a.ldq + off + 4 * tid);
-        const float4 u = *(const float4 *)(a.bu + off + 4 * tid), w = *(const float4 *)(a.bv + off + 4 * tid);
-        qu4[tid] = make_float4(x.x + u.x, x.y + u.y, x.z + u.z, x.w + u.w);
-        qv4[tid] = make_float4(x.x + w.x, x.y + w.y, x.z + w.z, x.w + w.w);
+        qx = *(const floatx4 *)(Q + (u64)i * a.ldq + off + 4 * tid);
+        ux = *(const floatx4 *)(a.bu + off + 4 * tid);
+        vx = *(const floatx4 *)(a.bv + off + 4 * tid);
     }
-    __syncthreads();
-#pragma unroll
-    for (int p = 0; p < 2; ++p) {
-        float acc = 0.0f;
+    /* K and P rows of this thread's key: key ks = tid / 4, dims part4*32 .. +32; lanes past the
+     * window issue no load (their values are never used) */
+    const u32 ks = tid >> 2, part4 = tid & 3, dofs = off + part4 * 32;
+    const bool kin = ks < L;
+    const u32 prow = (a.Lmax - L) + (a.c - 1 - i + ks);
+    floatx4 kr[8], pr[8];
+    if (kin) {
 #pragma unroll
         for (int q = 0; q < 8; ++q) {
-            const float4 u = qu4[part4 * 8 + q], w = qv4[part4 * 8 + q];
-            acc += u.x * kr[p][q].x + u.y * kr[p][q].y + u.z * kr[p][q].z + u.w * kr[p][q].w;
-            acc += w.x * pr[p][q].x + w.y * pr[p][q].y + w.z * pr[p][q].z + w.w * pr[p][q].w;
+            kr[q] = *(const floatx4 *)(Kp + (u64)ks * a.ldk + dofs + 4 * q);
+            pr[q] = *(const floatx4 *)(a.P + (u64)prow * a.D + dofs + 4 * q);
         }
-        acc += __shfl_xor(acc, 1, 64);
-        acc += __shfl_xor(acc, 2, 64);
-        const u32 j = ks + 64 * p;
-        if (part4 == 0 && j < L) s[j] = acc * a.scale;
     }
-    __syncthreads();
-    /* softmax over the window */
+    /* V rows for the output phase: group vg = tid / 32 takes keys vg, vg + 16, ... */
+    const u32 vg = tid >> 5, d4 = tid & 31;
+    floatx4 vv[NK_ATT_MAX_L / 16];
+#pragma unroll
+    for (int t = 0; t < NK_ATT_MAX_L / 16; ++t)
+        if (vg + 16 * t < L) vv[t] = *(const floatx4 *)(Vp + (u64)(vg + 16 * t) * a.ldk + off + 4 * d4);
+    if (tid < 32) {
+        qu4[tid] = qx + ux;
+        qv4[tid] = qx + vx;
+    }
+    lds_sync();
+    float acc = 0.0f;
+    if (kin) {
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            const floatx4 u = qu4[part4 * 8 + q], w = qv4[part4 * 8 + q];
+            acc += u[0] * kr[q][0] + u[1] * kr[q][1] + u[2] * kr[q][2] + u[3] * kr[q][3];
+            acc += w[0] * pr[q][0] + w[1] * pr[q][1] + w[2] * pr[q][2] + w[3] * pr[q][3];
+        }
+    }
+    acc += dpp_f<DPP_QUAD_1032>(acc);
+    acc += dpp_f<DPP_QUAD_2301>(acc);
+    if (part4 == 0 && kin) s[ks] = acc * a.scale;
+    lds_sync();
+    /* softmax over the window (threads 0..127 hold one score each) */
     const int lane = tid & 63, wave = tid >> 6;
     const float sv = tid < L ? s[tid] : -INFINITY;
-    float mx = wave_max(sv);
-    if (lane == 0) red[wave] = mx;
-    __syncthreads();
-    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    float mx = wmax(sv);
+    if (wave < 2 && lane == 0) red[wave] = mx;
+    lds_sync();
+    mx = fmaxf(red[0], red[1]);
     const float ev = tid < L ? expf(sv - mx) : 0.0f;
-    float sum = wave_sum(ev);
-    if (lane == 0) red[4 + wave] = sum;
-    __syncthreads();
-    sum = ((red[4] + red[5]) + red[6]) + red[7];
+    float sum = wsum(ev);
+    if (wave < 2 && lane == 0) red[2 + wave] = sum;
+    lds_sync();
+    sum = red[2] + red[3];
     if (tid < L) s[tid] = ev / sum;
-    __syncthreads();
-    float4 acc = z;
+    lds_sync();
+    floatx4 o = { 0.f, 0.f, 0.f, 0.f };
 #pragma unroll
-    for (int t = 0; t < NK_ATT_MAX_L / 8; ++t) {
-        const u32 j = vg + 8 * t;
-        if (j < L) {
-            const float p = s[j];
-            acc.x += p * vv[t].x; acc.y += p * vv[t].y; acc.z += p * vv[t].z; acc.w += p * vv[t].w;
-        }
+    for (int t = 0; t < NK_ATT_MAX_L / 16; ++t) {
+        const u32 j = vg + 16 * t;
+        if (j < L) o += s[j] * vv[t];
     }
-    part[vg][d4] = acc;
-    __syncthreads();
+    part[vg][d4] = o;
+    lds_sync();
     if (tid < 32) {
-        float4 o = part[0][tid];
+        floatx4 r = part[0][tid];
 #pragma unroll
-        for (int g = 1; g < 8; ++g) {
-            const float4 v = part[g][tid];
-            o.x += v.x; o.y += v.y; o.z += v.z; o.w += v.w;
-        }
-        *(float4 *)(a.O + (u64)i * a.D + off + 4 * tid) = o;
+        for (int g = 1; g < 16; ++g) r += part[g][tid];
+        *(floatx4 *)(a.O + (u64)i * a.D + off + 4 * tid) = r;
     }
 }
 

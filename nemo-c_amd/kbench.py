@@ -91,6 +91,82 @@ def bench_gemm(gpu, M, N, K, act, acc, alpha, ln_mode, ldw, has_bias, copies, re
     return name, graph_us, ms.value * 1e3, cnt.value
 
 
+def graph_us(gpu, launch, copies, reps):
+    """launch-to-launch time of `copies` launches replayed back to back in one hipGraph"""
+    L = nemoasr.lib()
+    gpu.begin()
+    gpu.check(L.gpu_capture_begin(gpu.h))
+    for i in range(copies):
+        gpu.check(launch(i))
+    gr = L.gpu_capture_end(gpu.h)
+    gpu.end()
+    if not gr:
+        raise RuntimeError(L.gpu_last_error(gpu.h).decode())
+    best = 1e30
+    for _ in range(reps + 1):
+        gpu.begin()
+        gpu.check(L.gpu_graph_launch(gpu.h, gr))
+        best = min(best, gpu.end())
+    L.gpu_graph_free(gr)
+    return best * 1e3 / copies
+
+
+def bench_attention(gpu, c, cache, use_desc, copies, reps):
+    """relative-position attention of one layer (8 heads x 128) over cache + c keys; a distinct
+    K/V cache and position table per launch, as the 24 layers of a chunk"""
+    L = nemoasr.lib()
+    H, dh, D, Lmax = 8, 128, 1024, 72
+    Lw = cache + c
+    rng = np.random.default_rng([c, cache])
+    pos = cache + 8
+    kvs = [gpu.put(rng.standard_normal((pos + c, 3 * D)).astype(np.float32)) for _ in range(copies)]
+    Ps = [gpu.put(rng.standard_normal((2 * Lmax - 1, D)).astype(np.float32)) for _ in range(copies)]
+    bu, bv, dO = gpu.put(np.zeros(D, np.float32)), gpu.put(np.zeros(D, np.float32)), gpu.alloc(c * D * 4)
+    desc = np.zeros(20, np.int32)
+    desc[:4] = [pos, cache, Lw, c]
+    ddesc = gpu.put(desc)
+    row = 3 * D * 4
+    scale = float(1.0 / np.sqrt(dh))
+
+    def launch(i):
+        kv, P = kvs[i % copies], Ps[i % copies]
+        if use_desc:
+            return L.nk_attention_rel_desc(gpu.h, kv.ptr, 3 * D, ddesc.ptr, P.ptr, bu.ptr, bv.ptr, dO.ptr, c, Lmax, H, dh,
+                                           D, scale)
+        return L.nk_attention_rel(gpu.h, kv.at(pos * row), 3 * D, kv.at((pos - cache) * row + D * 4),
+                                  kv.at((pos - cache) * row + 2 * D * 4), 3 * D, P.ptr, bu.ptr, bv.ptr, dO.ptr, c, Lw,
+                                  Lmax, H, dh, D, scale)
+
+    us = graph_us(gpu, launch, copies, reps)
+    for b in kvs + Ps + [bu, bv, dO, ddesc]:
+        b.free()
+    return us
+
+
+def bench_dwconv(gpu, c, use_desc, copies, reps):
+    L = nemoasr.lib()
+    D, taps = 1024, 9
+    rng = np.random.default_rng(c)
+    dins = [gpu.put(rng.standard_normal((taps - 1 + c + 8, D)).astype(np.float32)) for _ in range(copies)]
+    Ws = [gpu.put((rng.standard_normal((D, taps)) / 3).astype(np.float32)) for _ in range(copies)]
+    g, b, dY = gpu.put(np.ones(D, np.float32)), gpu.put(np.zeros(D, np.float32)), gpu.alloc(c * D * 4)
+    desc = np.zeros(20, np.int32)
+    desc[:4] = [taps - 1 + 8, 0, c, c]
+    ddesc = gpu.put(desc)
+
+    def launch(i):
+        if use_desc:
+            return L.nk_dwconv_ln_silu_desc(gpu.h, dins[i % copies].ptr, ddesc.ptr, Ws[i % copies].ptr, g.ptr, b.ptr,
+                                            dY.ptr, c, D, taps, 1e-5)
+        return L.nk_dwconv_ln_silu(gpu.h, dins[i % copies].at(8 * D * 4), Ws[i % copies].ptr, g.ptr, b.ptr, dY.ptr, c,
+                                   D, taps, 1e-5)
+
+    us = graph_us(gpu, launch, copies, reps)
+    for x in dins + Ws + [g, b, dY, ddesc]:
+        x.free()
+    return us
+
+
 def bench_copy(gpu, nbytes, reps):
     L = nemoasr.lib()
     n = nbytes // 4
@@ -111,6 +187,7 @@ def main():
     ap.add_argument("--reps", type=int, default=3)
     ap.add_argument("--copies", type=int, default=48, help="distinct weight matrices cycled per replay")
     ap.add_argument("--json", default=None)
+    ap.add_argument("--no-gemm", action="store_true")
     a = ap.parse_args()
     gpu = nemoasr.Gpu()
     print(f"device: {gpu.name}", flush=True)
@@ -119,7 +196,7 @@ def main():
     cu = bench_copy(gpu, cb, a.reps)
     out["copy"] = {"bytes": cb, "us": cu, "gbs_rw": 2 * cb / (cu * 1e-6) / 1e9}
     print(f"copy {cb >> 20} MiB: {cu:.1f} us, {2 * cb / (cu * 1e-6) / 1e9:.0f} GB/s read+write", flush=True)
-    for M in [int(x) for x in a.rows.split(",")]:
+    for M in ([] if a.no_gemm else [int(x) for x in a.rows.split(",")]):
         for (label, N, K, act, acc, alpha, ln, ldw, hb) in SHAPES:
             if label == "lstm" and M > 1:
                 continue
@@ -131,6 +208,16 @@ def main():
             out["gemm"].append(rec)
             print(f"M={M:2d} {label:14s} {name:22s} graph {gus:7.2f} us ({rec['gbs_graph']:7.1f} GB/s)  "
                   f"kernel {kus:7.2f} us ({rec['gbs_kernel']:7.1f} GB/s)", flush=True)
+    out["rows"] = []
+    for c in [int(x) for x in a.rows.split(",")]:
+        for desc in (0, 1):
+            us = bench_attention(gpu, c, 56, desc, 24, a.reps)
+            out["rows"].append({"kernel": "attention_rel", "c": c, "cache": 56, "desc": desc, "graph_us": round(us, 3)})
+            print(f"c={c:2d} attention_rel cache 56 desc={desc} graph {us:7.2f} us", flush=True)
+        for desc in (0, 1):
+            us = bench_dwconv(gpu, c, desc, 24, a.reps)
+            out["rows"].append({"kernel": "dwconv_ln_silu", "c": c, "desc": desc, "graph_us": round(us, 3)})
+            print(f"c={c:2d} dwconv_ln_silu  desc={desc} graph {us:7.2f} us", flush=True)
     gpu.close()
     if a.json:
         with open(a.json, "w") as f:
