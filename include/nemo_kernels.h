@@ -98,11 +98,27 @@ int nk_attention_rel_desc(gpu_t *g, const float *kv, uint32_t ld, const int *des
                           float scale);
 int nk_dwconv_ln_silu_desc(gpu_t *g, const float *din_base, const int *desc, const float *W, const float *gamma,
                            const float *beta, float *Y, uint32_t c, uint32_t D, uint32_t taps, float eps);
+/* Batched streams: output row m is described by rows[4m .. 4m+3] = { cache row of the chunk row,
+ * its index i in its stream's chunk, that chunk's rows c, the stream's cached rows } (device). */
+int nk_attention_rel_rows(gpu_t *g, const float *kv, uint32_t ld, const int *rows, uint32_t M, const float *P,
+                          const float *bias_u, const float *bias_v, float *O, uint32_t Lmax, uint32_t H, uint32_t dh,
+                          uint32_t D, float scale);
+int nk_dwconv_ln_silu_rows(gpu_t *g, const float *din_base, const int *rows, uint32_t M, const float *W,
+                           const float *gamma, const float *beta, float *Y, uint32_t D, uint32_t taps, float eps);
 int nk_conv2d_c1_s2_relu(gpu_t *g, const float *X, const float *W, const float *bias, float *Y, uint32_t T,
                          uint32_t F, uint32_t T1, uint32_t F1, uint32_t C);
 int nk_dwconv2d_s2(gpu_t *g, const float *X, const float *W, const float *bias, float *Y, uint32_t T, uint32_t F,
                    uint32_t T1, uint32_t F1, uint32_t C);
 int nk_flatten_cf(gpu_t *g, const float *X, float *Y, uint32_t T, uint32_t F, uint32_t C);
+/* The same three over `batch` windows of one size stored back to back (batched streams). */
+int nk_conv2d_c1_s2_relu_b(gpu_t *g, const float *X, const float *W, const float *bias, float *Y, uint32_t T,
+                           uint32_t F, uint32_t T1, uint32_t F1, uint32_t C, uint32_t batch);
+int nk_dwconv2d_s2_b(gpu_t *g, const float *X, const float *W, const float *bias, float *Y, uint32_t T, uint32_t F,
+                     uint32_t T1, uint32_t F1, uint32_t C, uint32_t batch);
+int nk_flatten_cf_b(gpu_t *g, const float *X, float *Y, uint32_t T, uint32_t F, uint32_t C, uint32_t batch);
+/* dst[m] = src[map[m]] for m < rows (cols floats per row) */
+int nk_gather_rows(gpu_t *g, const float *src, uint32_t src_ld, const int *map, float *dst, uint32_t dst_ld,
+                   uint32_t rows, uint32_t cols);
 int nk_copy(gpu_t *g, const float *src, float *dst, uint32_t n);
 int nk_copy2d(gpu_t *g, const float *src, uint32_t src_ld, float *dst, uint32_t dst_ld, uint32_t rows, uint32_t cols);
 int nk_fill(gpu_t *g, float *dst, uint32_t n, float value);
@@ -111,6 +127,15 @@ int nk_compact(gpu_t *g, float *base, uint64_t stride, uint32_t nbuf, uint32_t r
 
 /* ---- RNNT decoder ------------------------------------------------------------------------------ */
 int nk_lstm_cell(gpu_t *g, const float *gates, const float *c_in, float *c_out, float *h_out, uint32_t H);
+/* Batched decoder pieces (rows of many streams; see kernel_params.h for the layouts):
+ * LSTM input rows [x | h], the LSTM cell on rows, joint input rows relu(enc + pred), row argmax. */
+int nk_lstm_input_rows(gpu_t *g, const uint16_t *embed, const int *tok, const float *xsrc, const float *hc,
+                       const int *hrow, float *A, uint32_t n, uint32_t P, uint32_t blank);
+int nk_lstm_cell_rows(gpu_t *g, const float *gates, float *hc, const int *crow_in, const int *crow_out,
+                      const int *hrow_out, float *hout, uint32_t n, uint32_t P);
+int nk_joint_in_rows(gpu_t *g, const float *enc, const float *pred, const int *erow, const int *prow, float *jin,
+                     uint32_t rows, uint32_t J);
+int nk_argmax_rows(gpu_t *g, const float *logits, uint32_t ld, uint32_t rows, uint32_t V, int *out);
 /* argmax over V classes of W . relu(enc[enc_row + r] + pred) + bias for r < rows (<= 16);
  * out[2r] = index (lowest on ties), out[2r+1] = value bits.  part_v/part_i: scratch of
  * rows * 256 entries. */

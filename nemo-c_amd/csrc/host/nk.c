@@ -58,7 +58,7 @@ static int pick(uint32_t M, uint32_t K, int act) {
     const int gemv_ok = (M <= 2 && K <= 64 * 8 * 9) || (M <= 4 && K <= 64 * 8 * 2);
     if ((g_force == K_GEMV || g_force == 1) && gemv_ok) return K_GEMV;
     if (g_force == K_FR && fr_ok(M, K, act)) return K_FR;
-    if (g_force == K_MR && act != NK_ACT_GLU && K % 32 == 0) return K_MR;
+    if (g_force == K_MR && K % 32 == 0) return K_MR;
     if (gemv_ok) return K_GEMV;
     if (fr_ok(M, K, act)) return K_FR;
     return K_MR;
@@ -82,7 +82,7 @@ const char *nk_gemm_kernel_name(uint32_t M, uint32_t N, uint32_t K, int act) {
         snprintf(buf, sizeof buf, "gemv_r%u_n%u_k%u", M, nc, kch);
         return buf;
     case K_FR: return fr_name(fr_plan(act == NK_ACT_GLU ? N / 2 : N, K, act, 0, 1, 0), act, 0);
-    default: return "gemm_mr";
+    default: return "gemm_mm*";
     }
 }
 
@@ -154,7 +154,29 @@ static int gemm_core(gpu_t *g, const float *A, uint32_t lda, const uint16_t *W, 
         const uint32_t tiles = (nout + 15) / 16;
         return gpu_launch(g, fr_name(p, act, ln_fused), &a, sizeof a, tiles, p.KS, 1, 64 * p.W, 1, 1);
     }
-    if (act == NK_ACT_GLU) return bad(g, "gemm: GLU needs M <= 16");
+    /* many rows: 128 x 128 tiles when they fill the GPU, else 64 x 64 (K split over up to four
+     * workgroups for accumulating GEMMs with no bias and no activation) */
+    const int glu = act == NK_ACT_GLU;
+    const uint32_t S = K / 32;
+    if (nout % (glu ? 64 : 128) == 0) {
+        const uint32_t t128 = ((M + 127) / 128) * (nout / (glu ? 64 : 128));
+        if (t128 >= 240)
+            return gpu_launch(g, glu ? "gemm_mm128_glu" : "gemm_mm128", &a, sizeof a, nout / (glu ? 64 : 128),
+                              (M + 127) / 128, 1, 256, 1, 1);
+    }
+    if (nout % (glu ? 32 : 64) == 0) {
+        const uint32_t t64 = ((M + 63) / 64) * (nout / (glu ? 32 : 64));
+        uint32_t kz = 1;
+        if (t64 < 200 && accumulate && !bias && act == NK_ACT_NONE) {
+            kz = 256 / t64;
+            if (kz > 4) kz = 4;
+            if (kz > S) kz = S;
+            if (kz < 1) kz = 1;
+        }
+        return gpu_launch(g, glu ? "gemm_mm64_glu" : "gemm_mm64", &a, sizeof a, nout / (glu ? 32 : 64), (M + 63) / 64,
+                          kz, 256, 1, 1);
+    }
+    if (glu) return bad(g, "gemm: GLU needs N/2 to be a multiple of 32");
     return gpu_launch(g, "gemm_mr", &a, sizeof a, (N + 63) / 64, (M + 63) / 64, 1, 256, 1, 1);
 }
 
@@ -200,7 +222,7 @@ int nk_attention_rel(gpu_t *g, const float *Q, uint32_t ldq, const float *K, con
     if ((uintptr_t)K % 8 || (uintptr_t)P % 8 || ldk % 2) return bad(g, "attention: K/P must be 8-byte aligned");
     if ((uintptr_t)Q % 16 || (uintptr_t)K % 16 || (uintptr_t)V % 16 || ldq % 4 || ldk % 4)
         return bad(g, "attention: Q/K/V must be 16-byte aligned");
-    NkAttnArgs a = { Q, K, V, P, bias_u, bias_v, O, NULL, c, L, Lmax, H, dh, D, ldq, ldk, scale, 0 };
+    NkAttnArgs a = { Q, K, V, P, bias_u, bias_v, O, NULL, NULL, c, L, Lmax, H, dh, D, ldq, ldk, scale, 0 };
     return gpu_launch(g, "attention_rel", &a, sizeof a, H, c, 1, 512, 1, 1);
 }
 
@@ -210,7 +232,7 @@ int nk_attention_rel_desc(gpu_t *g, const float *kv, uint32_t ld, const int *des
     if (!c) return 0;
     if (dh != 128 || H * dh != D || c > Lmax || Lmax > NK_ATT_MAX_L) return bad(g, "attention: head_dim must be 128");
     if ((uintptr_t)kv % 16 || ld % 4) return bad(g, "attention: cache must be 16-byte aligned");
-    NkAttnArgs a = { kv, kv + D, kv + 2 * D, P, bias_u, bias_v, O, desc, c, 0, Lmax, H, dh, D, ld, ld, scale, 0 };
+    NkAttnArgs a = { kv, kv + D, kv + 2 * D, P, bias_u, bias_v, O, desc, NULL, c, 0, Lmax, H, dh, D, ld, ld, scale, 0 };
     return gpu_launch(g, "attention_rel", &a, sizeof a, H, c, 1, 512, 1, 1);
 }
 
@@ -218,7 +240,7 @@ int nk_dwconv_ln_silu(gpu_t *g, const float *din, const float *W, const float *g
                       uint32_t c, uint32_t D, uint32_t taps, float eps) {
     if (!c) return 0;
     if (D > NK_ROW_MAX || D % 4 || taps != NK_CONV_TAPS) return bad(g, "dwconv: 9 taps, D a multiple of 4, at most 4096");
-    NkDwArgs a = { din, W, gamma, beta, Y, NULL, c, D, taps, eps };
+    NkDwArgs a = { din, W, gamma, beta, Y, NULL, NULL, c, D, taps, eps };
     return gpu_launch(g, "dwconv_ln_silu", &a, sizeof a, c, 1, 1, NK_LN_THREADS, 1, 1);
 }
 
@@ -226,27 +248,93 @@ int nk_dwconv_ln_silu_desc(gpu_t *g, const float *din_base, const int *desc, con
                            const float *beta, float *Y, uint32_t c, uint32_t D, uint32_t taps, float eps) {
     if (!c) return 0;
     if (D > NK_ROW_MAX || D % 4 || taps != NK_CONV_TAPS) return bad(g, "dwconv: 9 taps, D a multiple of 4, at most 4096");
-    NkDwArgs a = { din_base, W, gamma, beta, Y, desc, c, D, taps, eps };
+    NkDwArgs a = { din_base, W, gamma, beta, Y, desc, NULL, c, D, taps, eps };
     return gpu_launch(g, "dwconv_ln_silu", &a, sizeof a, c, 1, 1, NK_LN_THREADS, 1, 1);
+}
+
+int nk_attention_rel_rows(gpu_t *g, const float *kv, uint32_t ld, const int *rows, uint32_t M, const float *P,
+                          const float *bias_u, const float *bias_v, float *O, uint32_t Lmax, uint32_t H, uint32_t dh,
+                          uint32_t D, float scale) {
+    if (!M) return 0;
+    if (dh != 128 || H * dh != D || Lmax > NK_ATT_MAX_L) return bad(g, "attention: head_dim must be 128");
+    if ((uintptr_t)kv % 16 || ld % 4) return bad(g, "attention: cache must be 16-byte aligned");
+    NkAttnArgs a = { kv, kv + D, kv + 2 * D, P, bias_u, bias_v, O, NULL, rows, 0, 0, Lmax, H, dh, D, ld, ld, scale, 0 };
+    return gpu_launch(g, "attention_rel", &a, sizeof a, H, M, 1, 512, 1, 1);
+}
+
+int nk_dwconv_ln_silu_rows(gpu_t *g, const float *din_base, const int *rows, uint32_t M, const float *W,
+                           const float *gamma, const float *beta, float *Y, uint32_t D, uint32_t taps, float eps) {
+    if (!M) return 0;
+    if (D > NK_ROW_MAX || D % 4 || taps != NK_CONV_TAPS) return bad(g, "dwconv: 9 taps, D a multiple of 4, at most 4096");
+    NkDwArgs a = { din_base, W, gamma, beta, Y, NULL, rows, M, D, taps, eps };
+    return gpu_launch(g, "dwconv_ln_silu", &a, sizeof a, M, 1, 1, NK_LN_THREADS, 1, 1);
 }
 
 static uint32_t blocks_for(uint64_t n) { return (uint32_t)((n + 255) / 256); }
 
+int nk_conv2d_c1_s2_relu_b(gpu_t *g, const float *X, const float *W, const float *bias, float *Y, uint32_t T,
+                           uint32_t F, uint32_t T1, uint32_t F1, uint32_t C, uint32_t batch) {
+    NkConvArgs a = { X, W, bias, Y, T, F, T1, F1, C, 0, T * F, T1 * F1 * C };
+    return gpu_launch(g, "conv2d_c1_s2_relu", &a, sizeof a, blocks_for((uint64_t)T1 * F1 * C), batch, 1, 256, 1, 1);
+}
+
+int nk_dwconv2d_s2_b(gpu_t *g, const float *X, const float *W, const float *bias, float *Y, uint32_t T, uint32_t F,
+                     uint32_t T1, uint32_t F1, uint32_t C, uint32_t batch) {
+    NkConvArgs a = { X, W, bias, Y, T, F, T1, F1, C, 0, T * F * C, T1 * F1 * C };
+    return gpu_launch(g, "dwconv2d_s2", &a, sizeof a, blocks_for((uint64_t)T1 * F1 * C), batch, 1, 256, 1, 1);
+}
+
+int nk_flatten_cf_b(gpu_t *g, const float *X, float *Y, uint32_t T, uint32_t F, uint32_t C, uint32_t batch) {
+    NkFlatArgs a = { X, Y, T, F, C, 0 };
+    return gpu_launch(g, "flatten_cf", &a, sizeof a, blocks_for((uint64_t)T * F * C), batch, 1, 256, 1, 1);
+}
+
 int nk_conv2d_c1_s2_relu(gpu_t *g, const float *X, const float *W, const float *bias, float *Y, uint32_t T,
                          uint32_t F, uint32_t T1, uint32_t F1, uint32_t C) {
-    NkConvArgs a = { X, W, bias, Y, T, F, T1, F1, C, 0 };
-    return gpu_launch(g, "conv2d_c1_s2_relu", &a, sizeof a, blocks_for((uint64_t)T1 * F1 * C), 1, 1, 256, 1, 1);
+    return nk_conv2d_c1_s2_relu_b(g, X, W, bias, Y, T, F, T1, F1, C, 1);
 }
 
 int nk_dwconv2d_s2(gpu_t *g, const float *X, const float *W, const float *bias, float *Y, uint32_t T, uint32_t F,
                    uint32_t T1, uint32_t F1, uint32_t C) {
-    NkConvArgs a = { X, W, bias, Y, T, F, T1, F1, C, 0 };
-    return gpu_launch(g, "dwconv2d_s2", &a, sizeof a, blocks_for((uint64_t)T1 * F1 * C), 1, 1, 256, 1, 1);
+    return nk_dwconv2d_s2_b(g, X, W, bias, Y, T, F, T1, F1, C, 1);
 }
 
 int nk_flatten_cf(gpu_t *g, const float *X, float *Y, uint32_t T, uint32_t F, uint32_t C) {
-    NkFlatArgs a = { X, Y, T, F, C, 0 };
-    return gpu_launch(g, "flatten_cf", &a, sizeof a, blocks_for((uint64_t)T * F * C), 1, 1, 256, 1, 1);
+    return nk_flatten_cf_b(g, X, Y, T, F, C, 1);
+}
+
+int nk_gather_rows(gpu_t *g, const float *src, uint32_t src_ld, const int *map, float *dst, uint32_t dst_ld,
+                   uint32_t rows, uint32_t cols) {
+    if (!rows) return 0;
+    NkGatherArgs a = { src, dst, map, rows, cols, src_ld, dst_ld };
+    return gpu_launch(g, "gather_rows", &a, sizeof a, blocks_for((uint64_t)rows * cols), 1, 1, 256, 1, 1);
+}
+
+int nk_lstm_input_rows(gpu_t *g, const uint16_t *embed, const int *tok, const float *xsrc, const float *hc,
+                       const int *hrow, float *A, uint32_t n, uint32_t P, uint32_t blank) {
+    if (!n) return 0;
+    NkLstmInArgs a = { embed, tok, xsrc, hc, hrow, A, n, P, blank, 0 };
+    return gpu_launch(g, "lstm_input_rows", &a, sizeof a, blocks_for(2 * P), n, 1, 256, 1, 1);
+}
+
+int nk_lstm_cell_rows(gpu_t *g, const float *gates, float *hc, const int *crow_in, const int *crow_out,
+                      const int *hrow_out, float *hout, uint32_t n, uint32_t P) {
+    if (!n) return 0;
+    NkLstmRowsArgs a = { gates, hc, crow_in, crow_out, hrow_out, hout, n, P };
+    return gpu_launch(g, "lstm_cell_rows", &a, sizeof a, blocks_for(P), n, 1, 256, 1, 1);
+}
+
+int nk_joint_in_rows(gpu_t *g, const float *enc, const float *pred, const int *erow, const int *prow, float *jin,
+                     uint32_t rows, uint32_t J) {
+    if (!rows) return 0;
+    NkJointInArgs a = { enc, pred, erow, prow, jin, rows, J };
+    return gpu_launch(g, "joint_in_rows", &a, sizeof a, blocks_for(J), rows, 1, 256, 1, 1);
+}
+
+int nk_argmax_rows(gpu_t *g, const float *logits, uint32_t ld, uint32_t rows, uint32_t V, int *out) {
+    if (!rows) return 0;
+    NkArgmaxRowsArgs a = { logits, out, rows, V, ld, 0 };
+    return gpu_launch(g, "argmax_rows", &a, sizeof a, rows, 1, 1, 256, 1, 1);
 }
 
 int nk_copy(gpu_t *g, const float *src, float *dst, uint32_t n) {

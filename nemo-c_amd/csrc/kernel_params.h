@@ -84,31 +84,40 @@ typedef struct {
  * Q: [c][ldq]; K, V: [L][ldk] (the window: cached rows then the chunk's rows);
  * P: [2*Lmax-1][D]; O: [c][D].
  * With desc set, Q/K/V are the cache bases (rows of ldq = ldk floats) and the window comes from
- * the descriptor: Q row pos + i, K/V rows pos - cache_len .. pos + c - 1, L = cache_len + c. */
+ * the descriptor: Q row pos + i, K/V rows pos - cache_len .. pos + c - 1, L = cache_len + c.
+ * With rows set (batched streams), Q/K/V are the cache bases and output row m is described by
+ * rows[4m .. 4m+3] = { cache row of the query, its index i in the stream's chunk, the chunk's
+ * rows c, the stream's cached rows }; the window is the cache_len + c rows ending with the chunk. */
 typedef struct {
     const float *Q, *K, *V, *P, *bu, *bv;
     float *O;
     const int *desc;
+    const int *rows;
     u32 c, L, Lmax, H, dh, D, ldq, ldk;
     float scale;
     u32 pad;
 } NkAttnArgs;
 
 /* Causal depthwise conv + LN + SiLU. din: [(taps-1) + c][D]; W: [D][taps].
- * With desc set, din is the conv cache base and the rows start at pos - (taps-1). */
+ * With desc set, din is the conv cache base and the rows start at pos - (taps-1).
+ * With rows set (batched streams, same table as the attention), din is the conv cache base and
+ * output row m convolves cache rows rows[4m] - (taps-1) .. rows[4m]. */
 typedef struct {
     const float *din, *W, *g, *b;
     float *Y;
     const int *desc;
+    const int *rows;
     u32 c, D, taps;
     float eps;
 } NkDwArgs;
 
-/* Subsampling convs. X [T][F] (conv 0) or [T][F][C]; Y [T1][F1][C]. */
+/* Subsampling convs. X [T][F] (conv 0) or [T][F][C]; Y [T1][F1][C].  grid.y runs over a batch
+ * of windows of the same size, xs / ys floats apart. */
 typedef struct {
     const float *X, *W, *bias;
     float *Y;
     u32 T, F, T1, F1, C, pad;
+    u32 xs, ys;
 } NkConvArgs;
 
 typedef struct {
@@ -197,5 +206,53 @@ typedef struct {
     const float *bout;        /* [V]                                                               */
     u32 P, J, V, blank, max_symbols, parity, enc_ld, decide_only;
 } NkDecArgs;
+
+/* ---- batched streams ---------------------------------------------------------------------- */
+/* dst[m][0:cols] = src[map[m]][0:cols] for m < rows */
+typedef struct {
+    const float *src;
+    float *dst;
+    const int *map;
+    u32 rows, cols, src_ld, dst_ld;
+} NkGatherArgs;
+
+/* LSTM input rows of the batched decoder: A[n] = [x_n | h_n] (2P floats).  x_n is the bf16
+ * embedding row tok[n] widened (zeros for blank) when tok is set, else row n of xsrc; h_n is
+ * row hrow[n] of the state array hc (rows of P floats). */
+typedef struct {
+    const u16 *embed;
+    const int *tok;
+    const float *xsrc;
+    const float *hc;
+    const int *hrow;
+    float *A;
+    u32 n, P, blank, pad;
+} NkLstmInArgs;
+
+/* LSTM cell on rows: gates [n][4P] (order i, f, g, o); c = hc[crow_in[n]]; writes c' to
+ * hc[crow_out[n]], h' to hc[hrow_out[n]] and to hout[n] (contiguous, for the next layer). */
+typedef struct {
+    const float *gates;
+    float *hc;
+    const int *crow_in, *crow_out, *hrow_out;
+    float *hout;
+    u32 n, P;
+} NkLstmRowsArgs;
+
+/* joint input rows: jin[r] = relu(enc[erow[r]] + pred[prow[r]]) (J floats) */
+typedef struct {
+    const float *enc, *pred;
+    const int *erow, *prow;
+    float *jin;
+    u32 rows, J;
+} NkJointInArgs;
+
+/* per-row argmax over the first V of ld logits, lowest index on ties:
+ * out[2r] = index, out[2r+1] = value bits */
+typedef struct {
+    const float *logits;
+    int *out;
+    u32 rows, V, ld, pad;
+} NkArgmaxRowsArgs;
 
 #endif

@@ -81,6 +81,12 @@ __device__ __forceinline__ float wmax(float v) {
     return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
 }
 
+/* Workgroup barrier for data exchanged through LDS only: waits for this wavefront's LDS
+ * operations but not for its outstanding global loads (a __syncthreads() would also wait for
+ * every weight load in flight).  The "memory" clobber keeps the compiler from moving memory
+ * accesses across it. */
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 /* Dot of 8 f32 activations with 8 bf16 weights packed in a uint4, summed in index order. */
 __device__ __forceinline__ float dot8(const float *a, uint4 w, float acc) {
     acc += a[0] * bf_lo(w.x);

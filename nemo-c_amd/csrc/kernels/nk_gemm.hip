@@ -28,12 +28,6 @@
  *   A: row l % 16, k 8*(l/16) + i;  B: k 8*(l/16) + i, column l % 16;
  *   D: row 4*(l/16) + i, column l % 16. */
 
-/* Workgroup barrier for data exchanged through LDS only: waits for this wavefront's LDS
- * operations but not for its outstanding global loads (a __syncthreads() would also wait for
- * every weight load in flight).  The "memory" clobber keeps the compiler from moving memory
- * accesses across it. */
-__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
-
 /* LayerNorm of one row of 1024 floats held by a wavefront as four float4 per lane (float4 index
  * lane + 64 j): mean = sum/D; var = sum((x-mean)^2)/D; y = (x-mean) * (1/sqrt(var+eps)) * g + b. */
 __device__ __forceinline__ void ln_wave4(floatx4 (&v)[4], const floatx4 (&g)[4], const floatx4 (&b)[4], float D,

@@ -6,10 +6,12 @@
 /* Subsampling conv 0: 1 -> C channels, 3x3, stride 2, causal padding (2 before, 1 after) on
  * time and frequency, + bias, ReLU.  X [T][F] -> Y [T1][F1][C].  One thread per output, channel
  * fastest.  Reference src/kernels.metal:411-432. */
-extern "C" __global__ __launch_bounds__(256) void conv2d_c1_s2_relu(const NkConvArgs a) {
+extern "C" __global__ __launch_bounds__(256) void conv2d_c1_s2_relu(NkConvArgs a) {
     const u64 idx = (u64)blockIdx.x * 256 + threadIdx.x;
     const u64 total = (u64)a.T1 * a.F1 * a.C;
     if (idx >= total) return;
+    a.X += (u64)blockIdx.y * a.xs;
+    a.Y += (u64)blockIdx.y * a.ys;
     const u32 o = (u32)(idx % a.C), f1 = (u32)((idx / a.C) % a.F1), t1 = (u32)(idx / ((u64)a.C * a.F1));
     float acc = a.bias[o];
     for (u32 kh = 0; kh < 3; ++kh) {
@@ -26,10 +28,12 @@ extern "C" __global__ __launch_bounds__(256) void conv2d_c1_s2_relu(const NkConv
 
 /* Depthwise 3x3 stride-2 conv, same causal padding, + bias, no activation:
  * reference src/kernels.metal:434-454.  X [T][F][C] -> Y [T1][F1][C]. */
-extern "C" __global__ __launch_bounds__(256) void dwconv2d_s2(const NkConvArgs a) {
+extern "C" __global__ __launch_bounds__(256) void dwconv2d_s2(NkConvArgs a) {
     const u64 idx = (u64)blockIdx.x * 256 + threadIdx.x;
     const u64 total = (u64)a.T1 * a.F1 * a.C;
     if (idx >= total) return;
+    a.X += (u64)blockIdx.y * a.xs;
+    a.Y += (u64)blockIdx.y * a.ys;
     const u32 c = (u32)(idx % a.C), f1 = (u32)((idx / a.C) % a.F1), t1 = (u32)(idx / ((u64)a.C * a.F1));
     float acc = a.bias[c];
     for (u32 kh = 0; kh < 3; ++kh) {
@@ -46,10 +50,12 @@ extern "C" __global__ __launch_bounds__(256) void dwconv2d_s2(const NkConvArgs a
 
 /* [T][F][C] -> [T][C*F] channel-major flatten: reference src/kernels.metal:456-462.
  * One thread per output element (reads gather, writes are coalesced). */
-extern "C" __global__ __launch_bounds__(256) void flatten_cf(const NkFlatArgs a) {
+extern "C" __global__ __launch_bounds__(256) void flatten_cf(NkFlatArgs a) {
     const u64 idx = (u64)blockIdx.x * 256 + threadIdx.x;
     const u64 total = (u64)a.T * a.C * a.F;
     if (idx >= total) return;
+    a.X += (u64)blockIdx.y * total; /* grid.y: windows of the same size, back to back */
+    a.Y += (u64)blockIdx.y * total;
     const u32 f = (u32)(idx % a.F), c = (u32)((idx / a.F) % a.C), t = (u32)(idx / ((u64)a.F * a.C));
     a.Y[idx] = a.X[((u64)t * a.F + f) * a.C + c];
 }
@@ -154,4 +160,81 @@ extern "C" __global__ __launch_bounds__(256) void copy2d_f32(const NkCopy2dArgs 
     if (idx >= (u64)a.rows * a.cols) return;
     const u32 r = (u32)(idx / a.cols), c = (u32)(idx % a.cols);
     a.dst[(u64)r * a.dst_ld + c] = a.src[(u64)r * a.src_ld + c];
+}
+
+/* ---- batched streams ------------------------------------------------------------------------ */
+
+/* dst[m] = src[map[m]] row gather (the batched row select of the subsampled windows) */
+extern "C" __global__ __launch_bounds__(256) void gather_rows(const NkGatherArgs a) {
+    const u64 idx = (u64)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= (u64)a.rows * a.cols) return;
+    const u32 m = (u32)(idx / a.cols), k = (u32)(idx % a.cols);
+    a.dst[(u64)m * a.dst_ld + k] = a.src[(u64)(u32)a.map[m] * a.src_ld + k];
+}
+
+/* LSTM input rows [x | h] of the batched decoder (one thread per element; grid.y = row) */
+extern "C" __global__ __launch_bounds__(256) void lstm_input_rows(const NkLstmInArgs a) {
+    const u32 n = blockIdx.y, k = blockIdx.x * 256 + threadIdx.x;
+    if (n >= a.n || k >= 2 * a.P) return;
+    float v;
+    if (k < a.P) {
+        if (a.tok) {
+            const int t = a.tok[n];
+            v = (t < 0 || (u32)t == a.blank) ? 0.0f : bf2f(a.embed[(u64)t * a.P + k]);
+        } else {
+            v = a.xsrc[(u64)n * a.P + k];
+        }
+    } else {
+        v = a.hc[(u64)(u32)a.hrow[n] * a.P + (k - a.P)];
+    }
+    a.A[(u64)n * 2 * a.P + k] = v;
+}
+
+/* LSTM cell on batched rows, reference src/kernels.metal:474-486 (c' = f*c + i*g, h' = o*tanh(c')) */
+extern "C" __global__ __launch_bounds__(256) void lstm_cell_rows(const NkLstmRowsArgs a) {
+    const u32 n = blockIdx.y, j = blockIdx.x * 256 + threadIdx.x;
+    if (n >= a.n || j >= a.P) return;
+    const float *gt = a.gates + (u64)n * 4 * a.P;
+    const float ig = sigmoid_f(gt[j]), fg = sigmoid_f(gt[a.P + j]), gg = tanhf(gt[2 * a.P + j]), og = sigmoid_f(gt[3 * a.P + j]);
+    const float c = fg * a.hc[(u64)(u32)a.crow_in[n] * a.P + j] + ig * gg;
+    const float h = og * tanhf(c);
+    a.hc[(u64)(u32)a.crow_out[n] * a.P + j] = c;
+    a.hc[(u64)(u32)a.hrow_out[n] * a.P + j] = h;
+    a.hout[(u64)n * a.P + j] = h;
+}
+
+/* joint input rows relu(enc + pred), reference src/kernels.metal:488-519 (the r vector) */
+extern "C" __global__ __launch_bounds__(256) void joint_in_rows(const NkJointInArgs a) {
+    const u32 r = blockIdx.y, k = blockIdx.x * 256 + threadIdx.x;
+    if (r >= a.rows || k >= a.J) return;
+    a.jin[(u64)r * a.J + k] = fmaxf(a.enc[(u64)(u32)a.erow[r] * a.J + k] + a.pred[(u64)(u32)a.prow[r] * a.J + k], 0.0f);
+}
+
+/* argmax of each row of joint logits, lowest index on ties (src/kernels.metal:521-550) */
+extern "C" __global__ __launch_bounds__(256) void argmax_rows(const NkArgmaxRowsArgs a) {
+    __shared__ float bv[256];
+    __shared__ int bi[256];
+    const u32 r = blockIdx.x, tid = threadIdx.x;
+    const float *x = a.logits + (u64)r * a.ld;
+    float best = -INFINITY;
+    int bidx = 0x7fffffff;
+    for (u32 n = tid; n < a.V; n += 256) {
+        const float v = x[n];
+        if (v > best || (v == best && (int)n < bidx)) { best = v; bidx = (int)n; }
+    }
+    bv[tid] = best;
+    bi[tid] = bidx;
+    __syncthreads();
+    for (u32 st = 128; st > 0; st >>= 1) {
+        if (tid < st) {
+            const float ov = bv[tid + st];
+            const int oi = bi[tid + st];
+            if (ov > bv[tid] || (ov == bv[tid] && oi < bi[tid])) { bv[tid] = ov; bi[tid] = oi; }
+        }
+        __syncthreads();
+    }
+    if (tid == 0) {
+        a.out[2 * r] = bi[0];
+        a.out[2 * r + 1] = __float_as_int(bv[0]);
+    }
 }

@@ -75,10 +75,6 @@ extern "C" __global__ __launch_bounds__(256) void layernorm(const NkLnArgs a) {
         if (tid + k * 256 < D4) y2[tid + k * 256] = v[k];
 }
 
-/* Workgroup barrier for data exchanged through LDS only (does not wait for outstanding global
- * loads, which a __syncthreads() would). */
-__device__ __forceinline__ void lds_sync() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
-
 /* Relative-position attention, one workgroup of 512 threads per (head, query i):
  * reference src/kernels.metal:290-348.
  *   score_j = ((q + u) . K_j + (q + v) . P[(Lmax - L) + (c - 1 - i + j)]) * scale
@@ -92,11 +88,19 @@ extern "C" __global__ __launch_bounds__(512) void attention_rel(const NkAttnArgs
     __shared__ floatx4 qu4[32], qv4[32];
     __shared__ float s[NK_ATT_MAX_L], red[16];
     __shared__ floatx4 part[16][32];
-    const u32 h = blockIdx.x, i = blockIdx.y, tid = threadIdx.x;
+    const u32 h = blockIdx.x, orow = blockIdx.y, tid = threadIdx.x;
     const u32 off = h * 128;
     const float *Q = a.Q, *Kp = a.K, *Vp = a.V;
-    u32 L = a.L;
-    if (a.desc) {
+    u32 L = a.L, i = orow, c = a.c;
+    if (a.rows) { /* batched streams: this row's stream window */
+        const u32 qrow = (u32)a.rows[4 * orow], cl = (u32)a.rows[4 * orow + 3];
+        i = (u32)a.rows[4 * orow + 1];
+        c = (u32)a.rows[4 * orow + 2];
+        Q += (u64)(qrow - i) * a.ldq;
+        Kp += (u64)(qrow - i - cl) * a.ldk;
+        Vp += (u64)(qrow - i - cl) * a.ldk;
+        L = cl + c;
+    } else if (a.desc) {
         const u32 pos = (u32)a.desc[NK_DESC_POS], cl = (u32)a.desc[NK_DESC_CACHE];
         Q += (u64)pos * a.ldq;
         Kp += (u64)(pos - cl) * a.ldk;
@@ -114,7 +118,7 @@ extern "C" __global__ __launch_bounds__(512) void attention_rel(const NkAttnArgs
      * window issue no load (their values are never used) */
     const u32 ks = tid >> 2, part4 = tid & 3, dofs = off + part4 * 32;
     const bool kin = ks < L;
-    const u32 prow = (a.Lmax - L) + (a.c - 1 - i + ks);
+    const u32 prow = (a.Lmax - L) + (c - 1 - i + ks);
     floatx4 kr[8], pr[8];
     if (kin) {
 #pragma unroll
@@ -133,7 +137,7 @@ extern "C" __global__ __launch_bounds__(512) void attention_rel(const NkAttnArgs
         qu4[tid] = qx + ux;
         qv4[tid] = qx + vx;
     }
-    lds_sync();
+    lds_barrier();
     float acc = 0.0f;
     if (kin) {
 #pragma unroll
@@ -146,21 +150,21 @@ extern "C" __global__ __launch_bounds__(512) void attention_rel(const NkAttnArgs
     acc += dpp_f<DPP_QUAD_1032>(acc);
     acc += dpp_f<DPP_QUAD_2301>(acc);
     if (part4 == 0 && kin) s[ks] = acc * a.scale;
-    lds_sync();
+    lds_barrier();
     /* softmax over the window (threads 0..127 hold one score each) */
     const int lane = tid & 63, wave = tid >> 6;
     const float sv = tid < L ? s[tid] : -INFINITY;
     float mx = wmax(sv);
     if (wave < 2 && lane == 0) red[wave] = mx;
-    lds_sync();
+    lds_barrier();
     mx = fmaxf(red[0], red[1]);
     const float ev = tid < L ? expf(sv - mx) : 0.0f;
     float sum = wsum(ev);
     if (wave < 2 && lane == 0) red[2 + wave] = sum;
-    lds_sync();
+    lds_barrier();
     sum = red[2] + red[3];
     if (tid < L) s[tid] = ev / sum;
-    lds_sync();
+    lds_barrier();
     floatx4 o = { 0.f, 0.f, 0.f, 0.f };
 #pragma unroll
     for (int t = 0; t < NK_ATT_MAX_L / 16; ++t) {
@@ -168,12 +172,12 @@ extern "C" __global__ __launch_bounds__(512) void attention_rel(const NkAttnArgs
         if (j < L) o += s[j] * vv[t];
     }
     part[vg][d4] = o;
-    lds_sync();
+    lds_barrier();
     if (tid < 32) {
         floatx4 r = part[0][tid];
 #pragma unroll
         for (int g = 1; g < 16; ++g) r += part[g][tid];
-        *(floatx4 *)(a.O + (u64)i * a.D + off + 4 * tid) = r;
+        *(floatx4 *)(a.O + (u64)orow * a.D + off + 4 * tid) = r;
     }
 }
 
@@ -185,7 +189,8 @@ extern "C" __global__ __launch_bounds__(256) void dwconv_ln_silu(const NkDwArgs 
     __shared__ float red[4];
     const u32 t = blockIdx.x, tid = threadIdx.x, D4 = a.D >> 2;
     const float *din = a.din;
-    if (a.desc) din += (u64)((u32)a.desc[NK_DESC_POS] - (DW_TAPS - 1)) * a.D;
+    if (a.rows) din += ((long long)a.rows[4 * t] - (DW_TAPS - 1) - (long long)t) * (long long)a.D;
+    else if (a.desc) din += (u64)((u32)a.desc[NK_DESC_POS] - (DW_TAPS - 1)) * a.D;
     float4 v[LN_VEC], g[LN_VEC], b[LN_VEC];
     const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll

@@ -188,6 +188,7 @@ def main():
     ap.add_argument("--copies", type=int, default=48, help="distinct weight matrices cycled per replay")
     ap.add_argument("--json", default=None)
     ap.add_argument("--no-gemm", action="store_true")
+    ap.add_argument("--batch-rows", default="", help="many-row (batched streams) GEMM sizes, e.g. 448,3584")
     a = ap.parse_args()
     gpu = nemoasr.Gpu()
     print(f"device: {gpu.name}", flush=True)
@@ -208,6 +209,25 @@ def main():
             out["gemm"].append(rec)
             print(f"M={M:2d} {label:14s} {name:22s} graph {gus:7.2f} us ({rec['gbs_graph']:7.1f} GB/s)  "
                   f"kernel {kus:7.2f} us ({rec['gbs_kernel']:7.1f} GB/s)", flush=True)
+    out["batched"] = []
+    for M in [int(x) for x in a.batch_rows.split(",") if x]:
+        tot_us, tot_fl = 0.0, 0.0
+        for (label, N, K, act, acc, alpha, ln, ldw, hb) in SHAPES:
+            if label == "lstm":
+                continue
+            name, gus, kus, cnt = bench_gemm(gpu, M, N, K, act, acc, alpha, 0, ldw, hb, 8, a.reps)
+            fl = 2.0 * M * N * K
+            per_layer = {"ff_up+ln2": 2, "ff_down": 2, "qkv+ln": 1, "out_proj": 1, "pw1_glu+ln": 1, "pw2": 1}.get(label, 0)
+            cnt_chunk = 24 * per_layer if per_layer else 1
+            tot_us += gus * cnt_chunk
+            tot_fl += fl * cnt_chunk
+            rec = {"M": M, "shape": label, "N": N, "K": K, "kernel": name, "graph_us": round(gus, 3),
+                   "tflops": round(fl / (gus * 1e-6) / 1e12, 1), "mfma_frac": round(fl / (gus * 1e-6) / 2.5e15, 4)}
+            out["batched"].append(rec)
+            print(f"M={M:5d} {label:14s} {name:18s} graph {gus:8.2f} us  {rec['tflops']:7.1f} TFLOP/s "
+                  f"({rec['mfma_frac']:.3f} of 2.5 PF bf16; issued MFMA work is 2x: A = hi + lo)", flush=True)
+        print(f"M={M:5d} chunk GEMMs (24 layers + prompt + joint.enc, no LN launches): {tot_us / 1e3:.3f} ms, "
+              f"{tot_fl / (tot_us * 1e-6) / 1e12:.1f} TFLOP/s = {tot_fl / (tot_us * 1e-6) / 2.5e15:.3f} of peak", flush=True)
     out["rows"] = []
     for c in [int(x) for x in a.rows.split(",")]:
         for desc in (0, 1):

@@ -96,6 +96,37 @@ def test_gemm_many_rows(gpu, M, N, K, act):
     assert rel_err(got, ref) < GEMM_TOL
 
 
+# batched multi-stream shapes (64 streams x 7 rows, 256 x 14) through the many-row MFMA kernels:
+# 128x128 and 64x64 tiles, GLU pairing, K split over workgroups with atomic accumulation, row maps
+@pytest.mark.parametrize("M,N,K,act,acc,bias", [
+    (448, 4096, 1024, 1, 0, False), (448, 1024, 4096, 0, 1, False), (448, 3072, 1024, 0, 0, False),
+    (448, 2048, 1024, 3, 0, False), (448, 1024, 1024, 0, 1, False), (448, 640, 1024, 0, 0, True),
+    (3584, 4096, 1024, 1, 0, False), (3584, 2048, 1024, 3, 0, False), (3584, 1024, 4096, 0, 1, False),
+    (100, 2048, 1024, 2, 0, True), (37, 1024, 2048, 0, 0, True)])
+def test_gemm_batched_rows(gpu, M, N, K, act, acc, bias):
+    rng = np.random.default_rng([M, N, K, act])
+    W = _w(rng, N, K)
+    A = rng.standard_normal((M, K)).astype(np.float32)
+    b = (0.1 * rng.standard_normal(N)).astype(np.float32) if bias else None
+    nout = N // 2 if act == 3 else N
+    C0 = rng.standard_normal((M, nout)).astype(np.float32) if acc else None
+    got = run_gemm(gpu, A, W, b, act, acc, 0.5 if acc else 1.0, C0=C0)
+    ref = oracle.gemm(A, W, b, act, acc, 0.5 if acc else 1.0, C0=C0)
+    assert rel_err(got, ref) < GEMM_TOL, (M, N, K, act)
+
+
+def test_gemm_batched_row_map(gpu):
+    """Output row m lands in row crow[m] (the per-stream cache scatter of the batched QKV / pw1)."""
+    rng = np.random.default_rng(7)
+    M, N, K = 96, 2048, 1024
+    W = _w(rng, N, K)
+    A = rng.standard_normal((M, K)).astype(np.float32)
+    rows = rng.permutation(300)[:M]
+    got = run_gemm(gpu, A, W, None, 3, False, 1.0, rows=rows)
+    ref = oracle.gemm(A, W, None, 3, False, 1.0)
+    assert rel_err(got[rows], ref) < GEMM_TOL
+
+
 @pytest.mark.parametrize("kind,M", [(4, 1), (4, 4), (2, 1), (2, 4), (2, 16), (3, 5), (3, 16)])
 def test_gemm_variants_agree(gpu, kind, M):
     """Every kernel the policy can pick computes the same GEMM (the reference's kbench.c:196-230
