@@ -1,0 +1,892 @@
+/* Multi-stream batching on one GPU (include/nemoasr_batch.h).
+ *
+ * Every stream keeps the reference's per-stream state: the mel bookkeeping of
+ * src/encoder.c:213-251 (through enc_plan_step), a K/V and conv history, and the greedy decoder
+ * state of src/decoder.c:14-23 (committed and provisional LSTM states, last token, whether the
+ * prediction is valid).  A batched step takes one chunk from every stream that has one:
+ *   - windows of equal length are subsampled together (batched conv launches, the 1x1 convs and
+ *     the output projection as GEMMs over all their rows), and the rows each stream keeps
+ *     ([lo, hi) of its window) are gathered into one matrix of M = sum(c_s) rows;
+ *   - the 24 conformer blocks run once on those M rows: every GEMM is one many-row launch, the
+ *     fused QKV and GLU GEMMs write each row to its stream's cache row, and attention and the
+ *     depthwise conv read each row's stream window through a row table
+ *     {cache row, index in chunk, chunk rows, cached rows};
+ *   - the greedy RNNT loop then advances every stream's chunk together: one step runs the
+ *     prediction network for the streams whose prediction is stale (LSTM layers as GEMMs over
+ *     those streams' [x | h] rows with the input and recurrent weights side by side) and the
+ *     joint + argmax for up to 16 pending frames of every stream, and the host applies the
+ *     reference's rules to each stream's row of results.
+ * Device layout: caches [n_layers][S][cap_rows][3D] (K/V) and [n_layers][S][cap_rows][D] (conv
+ * history); LSTM states [S][2 sets][h0, c0, h1, c1][P].  The encoder launch sequence of a step
+ * depends only on (M, the window groups), so it is captured as a hipGraph and replayed when the
+ * same shape recurs (the lockstep steady state of a batch replays one graph). */
+#include "nemoasr_batch.h"
+#include "encoder.h"
+#include "mel.h"
+#include "model.h"
+#include "nemo_kernels.h"
+#include "../kernel_params.h"
+#include <math.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+#include <time.h>
+
+#define MEL_CACHE 16      /* src/encoder.c:10 */
+#define DEC_WIN 16        /* frames scored per stream per joint evaluation, src/decoder.c:96-97 */
+#define MAX_BGRAPHS 8
+#define MAX_SIG_GROUPS 8
+
+static double now_ms(void) {
+    struct timespec ts;
+    clock_gettime(CLOCK_MONOTONIC, &ts);
+    return ts.tv_sec * 1e3 + ts.tv_nsec / 1e6;
+}
+
+static int sub_len(int n) { return n / 2 + 1; } /* src/encoder.c:118 */
+
+typedef struct {
+    melfe_t *mel;
+    float *pending;
+    size_t pending_n, pending_cap;
+    float mel_cache[MEL_CACHE * MEL_NMEL];
+    int mel_cache_n;
+    size_t consumed, emitted;
+    int closed, final;
+    int pos, cache_len;                 /* cache rows of this stream */
+    int last_token, pred_valid, cur;    /* decoder; cur = committed LSTM slot set */
+    int frames, t, symbols, erow0;      /* the chunk in the decoder */
+    int *tok;
+    size_t n_tok, cap_tok, n_text;
+    int printed_any;
+    /* the chunk of the current step */
+    int c, nwin, lo, row0, cache_before, gk, gj; /* gk, gj: window group and index in it */
+    enc_book_t book;
+    enc_plan_t plan;
+} bstream_t;
+
+typedef struct {
+    int M, ng, nwin[MAX_SIG_GROUPS], cnt[MAX_SIG_GROUPS];
+    gpu_graph_t *graph;
+    int seen;
+    unsigned long long last_use;
+} bgraph_t;
+
+struct nemoasr_batch {
+    model_t *m;
+    gpu_t *g;
+    int S, latency_ms, right, chunk_frames, chunk_mel, cmax, left, conv_left, Lmax, cap_rows;
+    int nwin_max, T1max, T2max, T3max, F1, F2, F3;
+    int Mmax;
+    bstream_t *st;
+    int *order, *gid;              /* streams with a chunk this step, in row order; their group */
+    int ng, *g_nwin, *g_cnt, *g_woff, *g_poff, *g_fill, *ord;
+    float *wtmp;                   /* host scratch for chunks that emit no rows */
+    /* encoder */
+    gpu_buf_t *win, *c0, *c1, *c2, *c3, *c4, *flat, *pre_out;
+    gpu_buf_t *h, *tmp, *lnb, *ff, *att, *y, *ph, *prompted, *joint_enc, *kv, *din, *etab;
+    size_t kv_lstride, din_lstride;
+    float *stage_win;
+    int *stage_tab;
+    bgraph_t gr[MAX_BGRAPHS];
+    unsigned long long tick;
+    int use_graphs;
+    /* decoder */
+    int P, J, V, Vp;
+    gpu_buf_t *wcat[2], *wout, *bout, *hc, *lin, *gates, *hout, *hout2, *pred, *jin, *logits, *amax, *dtab;
+    int *stage_dtab, *stage_amax;
+    /* accounting */
+    double *step_ms;
+    size_t n_step, cap_step;
+    nemoasr_batch_stats_t stats;
+    /* test hook: joint.enc rows per stream */
+    int dump;
+    float **dj;
+    size_t *dj_n, *dj_cap;
+};
+
+/* latency -> right context (src/nemoasr.c:58-64) */
+static int right_for(int latency_ms) {
+    static const int ms[] = { 80, 160, 320, 560, 1120 }, r[] = { 0, 1, 3, 6, 13 };
+    for (size_t i = 0; i < sizeof ms / sizeof *ms; ++i)
+        if (ms[i] == latency_ms) return r[i];
+    return -1;
+}
+
+int nemoasr_batch_streams(const nemoasr_batch_t *b) { return b->S; }
+
+static bgraph_t *bgraph_slot(nemoasr_batch_t *b, int M) {
+    if (b->ng > MAX_SIG_GROUPS) return NULL;
+    bgraph_t *free_slot = NULL, *lru = &b->gr[0];
+    for (int i = 0; i < MAX_BGRAPHS; ++i) {
+        bgraph_t *s = &b->gr[i];
+        if (s->seen && s->M == M && s->ng == b->ng && !memcmp(s->nwin, b->g_nwin, (size_t)b->ng * sizeof(int)) &&
+            !memcmp(s->cnt, b->g_cnt, (size_t)b->ng * sizeof(int)))
+            return s;
+        if (!s->seen && !free_slot) free_slot = s;
+        if (s->last_use < lru->last_use) lru = s;
+    }
+    bgraph_t *s = free_slot ? free_slot : lru;
+    gpu_graph_free(s->graph);
+    memset(s, 0, sizeof *s);
+    s->M = M;
+    s->ng = b->ng;
+    memcpy(s->nwin, b->g_nwin, (size_t)b->ng * sizeof(int));
+    memcpy(s->cnt, b->g_cnt, (size_t)b->ng * sizeof(int));
+    return s;
+}
+
+static void drop_graphs(nemoasr_batch_t *b) {
+    for (int i = 0; i < MAX_BGRAPHS; ++i) {
+        gpu_graph_free(b->gr[i].graph);
+        memset(&b->gr[i], 0, sizeof b->gr[i]);
+    }
+}
+
+/* bf16 matrices of the batched decoder: [Wx | Wh] per LSTM layer ([4P][2P]) and the joint output
+ * weights padded to a multiple of 64 rows (padding rows zero; the argmax reads the first V) */
+static int build_decoder_weights(nemoasr_batch_t *b) {
+    model_t *m = b->m;
+    gpu_t *g = b->g;
+    const size_t P = (size_t)b->P, J = (size_t)b->J, V = (size_t)b->V, Vp = (size_t)b->Vp;
+    uint16_t *wx = malloc(4 * P * P * 2), *wh = malloc(4 * P * P * 2), *cat = malloc(4 * P * 2 * P * 2);
+    int rc = 0;
+    for (int l = 0; l < 2 && !rc; ++l) {
+        rc |= gpu_download(g, wx, m->lstm_wx[l], 4 * P * P * 2);
+        rc |= gpu_download(g, wh, m->lstm_wh[l], 4 * P * P * 2);
+        for (size_t r = 0; r < 4 * P; ++r) {
+            memcpy(cat + r * 2 * P, wx + r * P, P * 2);
+            memcpy(cat + r * 2 * P + P, wh + r * P, P * 2);
+        }
+        b->wcat[l] = gpu_buf_alloc(g, 4 * P * 2 * P * 2);
+        rc |= gpu_upload(g, gpu_buf_dptr(b->wcat[l]), cat, 4 * P * 2 * P * 2);
+    }
+    uint16_t *wo = calloc(Vp * J, 2);
+    float *bo = calloc(Vp, sizeof(float));
+    rc |= gpu_download(g, wo, m->joint_out_w, V * J * 2);
+    rc |= gpu_download(g, bo, m->joint_out_b, V * sizeof(float));
+    b->wout = gpu_buf_alloc(g, Vp * J * 2);
+    b->bout = gpu_buf_alloc(g, Vp * sizeof(float));
+    rc |= gpu_upload(g, gpu_buf_dptr(b->wout), wo, Vp * J * 2);
+    rc |= gpu_upload(g, gpu_buf_dptr(b->bout), bo, Vp * sizeof(float));
+    free(wx);
+    free(wh);
+    free(cat);
+    free(wo);
+    free(bo);
+    return rc;
+}
+
+static void stream_clear(nemoasr_batch_t *b, int s) {
+    bstream_t *x = &b->st[s];
+    melfe_destroy(x->mel);
+    int *tok = x->tok;
+    size_t cap = x->cap_tok;
+    float *pend = x->pending;
+    size_t pcap = x->pending_cap;
+    memset(x, 0, sizeof *x);
+    x->tok = tok;
+    x->cap_tok = cap;
+    x->pending = pend;
+    x->pending_cap = pcap;
+    x->mel = melfe_create();
+    x->pos = b->conv_left; /* rows [0, conv_left) of every layer stay zero: the empty conv history */
+    x->last_token = b->m->cfg.blank_id;
+    if (b->dump) b->dj_n[s] = 0;
+}
+
+/* device state of one stream back to that after open: zero LSTM states and conv history */
+static int stream_zero_device(nemoasr_batch_t *b, int s) {
+    const size_t D = (size_t)b->m->cfg.d_model, P = (size_t)b->P;
+    const size_t n = (size_t)b->conv_left * D > 8 * P ? (size_t)b->conv_left * D : 8 * P;
+    float *z = calloc(n, sizeof(float));
+    int rc = gpu_upload(b->g, (float *)gpu_buf_dptr(b->hc) + (size_t)s * 8 * P, z, 8 * P * sizeof(float));
+    for (int l = 0; l < b->m->cfg.n_layers; ++l)
+        rc |= gpu_upload(b->g, (float *)gpu_buf_dptr(b->din) + (size_t)l * b->din_lstride + (size_t)s * b->cap_rows * D, z,
+                         (size_t)b->conv_left * D * sizeof(float));
+    free(z);
+    return rc;
+}
+
+nemoasr_batch_t *nemoasr_batch_open(const char *model_dir, const char *language, int latency_ms, int n_streams,
+                                    char *err, size_t errlen) {
+    if (errlen) err[0] = 0;
+    const int right = right_for(latency_ms);
+    if (right < 0) { snprintf(err, errlen, "latency must be one of 80, 160, 320, 560, 1120 ms"); return NULL; }
+    if (n_streams < 1 || n_streams > 4096) { snprintf(err, errlen, "n_streams must be 1..4096"); return NULL; }
+    nemoasr_batch_t *b = calloc(1, sizeof *b);
+    b->m = model_load(model_dir, err, errlen);
+    if (!b->m) { free(b); return NULL; }
+    model_t *m = b->m;
+    if (!model_right_context_trained(m, right)) {
+        snprintf(err, errlen, "latency %d ms not trained for this checkpoint", latency_ms);
+        nemoasr_batch_close(b);
+        return NULL;
+    }
+    if (model_set_language(m, language ? language : "auto", err, errlen)) { nemoasr_batch_close(b); return NULL; }
+    const model_cfg_t *c = &m->cfg;
+    b->g = m->gpu;
+    b->S = n_streams;
+    b->latency_ms = latency_ms;
+    b->right = right;
+    b->chunk_frames = right + 1;
+    b->chunk_mel = b->chunk_frames * c->subsampling;
+    b->cmax = b->chunk_frames + 2; /* a final boundary window can yield up to chunk_frames + 2 rows */
+    b->left = c->att_left;
+    b->conv_left = c->conv_kernel - 1;
+    b->Lmax = m->Lmax;
+    /* compaction moves the live rows to the front; source and destination never overlap when
+     * cap_rows >= 2 * left + cmax */
+    b->cap_rows = b->left + NK_CACHE_EPOCH_CHUNKS * b->cmax;
+    if (b->cap_rows < 2 * b->left + 2 * b->cmax) b->cap_rows = 2 * b->left + 2 * b->cmax;
+    b->P = c->pred_hidden;
+    b->J = c->joint_hidden;
+    b->V = c->num_classes;
+    b->Vp = (b->V + 63) / 64 * 64;
+    if (b->P % 8 || b->J % 32 || b->P * 2 % 32 || c->d_model % 64 || c->d_ff % 64) {
+        snprintf(err, errlen, "batch: unsupported model sizes");
+        nemoasr_batch_close(b);
+        return NULL;
+    }
+    const size_t S = (size_t)n_streams, D = (size_t)c->d_model, CH = (size_t)c->sub_channels, F = (size_t)c->feat_in;
+    const size_t fs = sizeof(float);
+    b->nwin_max = MEL_CACHE + b->chunk_mel;
+    b->T1max = sub_len(b->nwin_max);
+    b->T2max = sub_len(b->T1max);
+    b->T3max = sub_len(b->T2max);
+    b->F1 = (int)F / 2 + 1;
+    b->F2 = b->F1 / 2 + 1;
+    b->F3 = b->F2 / 2 + 1;
+    b->Mmax = n_streams * b->cmax;
+    const size_t Mm = (size_t)b->Mmax;
+    gpu_t *g = b->g;
+    b->win = gpu_buf_alloc(g, S * (size_t)b->nwin_max * F * fs);
+    b->c0 = gpu_buf_alloc(g, S * (size_t)b->T1max * b->F1 * CH * fs);
+    b->c1 = gpu_buf_alloc(g, S * (size_t)b->T2max * b->F2 * CH * fs);
+    b->c2 = gpu_buf_alloc(g, S * (size_t)b->T2max * b->F2 * CH * fs);
+    b->c3 = gpu_buf_alloc(g, S * (size_t)b->T3max * b->F3 * CH * fs);
+    b->c4 = gpu_buf_alloc(g, S * (size_t)b->T3max * b->F3 * CH * fs);
+    b->flat = gpu_buf_alloc(g, S * (size_t)b->T3max * b->F3 * CH * fs);
+    b->pre_out = gpu_buf_alloc(g, S * (size_t)b->T3max * D * fs);
+    b->h = gpu_buf_alloc(g, Mm * D * fs);
+    b->tmp = gpu_buf_alloc(g, Mm * D * fs);
+    b->lnb = gpu_buf_alloc(g, Mm * D * fs);
+    b->ff = gpu_buf_alloc(g, Mm * (size_t)c->d_ff * fs);
+    b->att = gpu_buf_alloc(g, Mm * D * fs);
+    b->y = gpu_buf_alloc(g, Mm * D * fs);
+    b->ph = gpu_buf_alloc(g, Mm * (size_t)c->prompt_hidden * fs);
+    b->prompted = gpu_buf_alloc(g, Mm * D * fs);
+    b->joint_enc = gpu_buf_alloc(g, Mm * (size_t)b->J * fs);
+    b->kv_lstride = S * (size_t)b->cap_rows * 3 * D;
+    b->din_lstride = S * (size_t)b->cap_rows * D;
+    b->kv = gpu_buf_alloc(g, (size_t)c->n_layers * b->kv_lstride * fs);
+    b->din = gpu_buf_alloc(g, (size_t)c->n_layers * b->din_lstride * fs);
+    b->etab = gpu_buf_alloc(g, 6 * Mm * sizeof(int));
+    b->stage_win = gpu_host_alloc(g, S * (size_t)b->nwin_max * F * fs);
+    b->stage_tab = gpu_host_alloc(g, 6 * Mm * sizeof(int));
+    b->wtmp = malloc((size_t)b->nwin_max * F * fs);
+    const size_t P = (size_t)b->P, J = (size_t)b->J, R = S * DEC_WIN;
+    b->hc = gpu_buf_alloc(g, S * 8 * P * fs);
+    b->lin = gpu_buf_alloc(g, S * 2 * P * fs);
+    b->gates = gpu_buf_alloc(g, S * 4 * P * fs);
+    b->hout = gpu_buf_alloc(g, S * P * fs);
+    b->hout2 = gpu_buf_alloc(g, S * P * fs);
+    b->pred = gpu_buf_alloc(g, S * J * fs);
+    b->jin = gpu_buf_alloc(g, R * J * fs);
+    b->logits = gpu_buf_alloc(g, R * (size_t)b->Vp * fs);
+    b->amax = gpu_buf_alloc(g, 2 * R * sizeof(int));
+    b->dtab = gpu_buf_alloc(g, (10 * S + 2 * R) * sizeof(int));
+    b->stage_dtab = gpu_host_alloc(g, (10 * S + 2 * R) * sizeof(int));
+    b->stage_amax = gpu_host_alloc(g, 2 * R * sizeof(int));
+    if (!b->win || !b->kv || !b->din || !b->ff || !b->stage_win || !b->stage_dtab) {
+        snprintf(err, errlen, "batch: out of memory for %d streams", n_streams);
+        nemoasr_batch_close(b);
+        return NULL;
+    }
+    if (build_decoder_weights(b)) {
+        snprintf(err, errlen, "batch: decoder weight setup failed: %s", gpu_last_error(g));
+        nemoasr_batch_close(b);
+        return NULL;
+    }
+    b->st = calloc(S, sizeof *b->st);
+    b->order = malloc(S * sizeof(int));
+    b->gid = malloc(S * sizeof(int));
+    b->g_nwin = malloc(S * sizeof(int));
+    b->g_cnt = malloc(S * sizeof(int));
+    b->g_woff = malloc(S * sizeof(int));
+    b->g_poff = malloc(S * sizeof(int));
+    b->g_fill = malloc(S * sizeof(int));
+    b->ord = malloc(S * sizeof(int));
+    for (int s = 0; s < n_streams; ++s) stream_clear(b, s);
+    b->use_graphs = 1;
+    return b;
+}
+
+void nemoasr_batch_close(nemoasr_batch_t *b) {
+    if (!b) return;
+    drop_graphs(b);
+    gpu_buf_t *bufs[] = { b->win, b->c0, b->c1, b->c2, b->c3, b->c4, b->flat, b->pre_out, b->h, b->tmp, b->lnb,
+                          b->ff, b->att, b->y, b->ph, b->prompted, b->joint_enc, b->kv, b->din, b->etab, b->wcat[0],
+                          b->wcat[1], b->wout, b->bout, b->hc, b->lin, b->gates, b->hout, b->hout2, b->pred,
+                          b->jin, b->logits, b->amax, b->dtab };
+    for (size_t i = 0; i < sizeof bufs / sizeof *bufs; ++i) gpu_buf_free(bufs[i]);
+    gpu_host_free(b->stage_win);
+    gpu_host_free(b->stage_tab);
+    gpu_host_free(b->stage_dtab);
+    gpu_host_free(b->stage_amax);
+    if (b->st)
+        for (int s = 0; s < b->S; ++s) {
+            melfe_destroy(b->st[s].mel);
+            free(b->st[s].pending);
+            free(b->st[s].tok);
+        }
+    if (b->dj) {
+        for (int s = 0; s < b->S; ++s) free(b->dj[s]);
+        free(b->dj);
+        free(b->dj_n);
+        free(b->dj_cap);
+    }
+    free(b->st);
+    free(b->order);
+    free(b->gid);
+    free(b->g_nwin);
+    free(b->g_cnt);
+    free(b->g_woff);
+    free(b->g_poff);
+    free(b->g_fill);
+    free(b->ord);
+    free(b->wtmp);
+    free(b->step_ms);
+    model_free(b->m);
+    free(b);
+}
+
+static int check_stream(const nemoasr_batch_t *b, int s, char *err, size_t errlen) {
+    if (s < 0 || s >= b->S) { snprintf(err, errlen, "stream %d out of range (0..%d)", s, b->S - 1); return -1; }
+    return 0;
+}
+
+static void queue_mel(bstream_t *x, const float *mel, size_t nframes) {
+    if (!nframes) return;
+    if (x->pending_n + nframes > x->pending_cap) {
+        x->pending_cap = (x->pending_n + nframes) * 2;
+        x->pending = realloc(x->pending, x->pending_cap * MEL_NMEL * sizeof(float));
+    }
+    memcpy(x->pending + x->pending_n * MEL_NMEL, mel, nframes * MEL_NMEL * sizeof(float));
+    x->pending_n += nframes;
+}
+
+int nemoasr_batch_push_mel(nemoasr_batch_t *b, int stream, const float *mel, size_t nframes, int final, char *err,
+                           size_t errlen) {
+    if (errlen) err[0] = 0;
+    if (check_stream(b, stream, err, errlen)) return -1;
+    bstream_t *x = &b->st[stream];
+    if (x->final) { snprintf(err, errlen, "stream %d already ended", stream); return -1; }
+    queue_mel(x, mel, nframes);
+    if (final) x->final = 1;
+    return 0;
+}
+
+int nemoasr_batch_push(nemoasr_batch_t *b, int stream, const float *samples, size_t n, int final, char *err,
+                       size_t errlen) {
+    if (errlen) err[0] = 0;
+    if (check_stream(b, stream, err, errlen)) return -1;
+    bstream_t *x = &b->st[stream];
+    if (x->final) { snprintf(err, errlen, "stream %d already ended", stream); return -1; }
+    /* a final push with no samples and an empty front end flushes nothing (src/nemoasr.c:146) */
+    if (!(final && n == 0 && melfe_samples(x->mel) == 0)) {
+        const float *frames;
+        size_t nf;
+        melfe_push(x->mel, samples, n, final, &frames, &nf);
+        queue_mel(x, frames, nf);
+    }
+    if (final) x->final = 1;
+    return 0;
+}
+
+/* Window of the planned chunk (mel cache ++ the rows taken) into dst; advance the stream's mel
+ * bookkeeping exactly as a single-stream encoder step does. */
+static void take_window(bstream_t *x, float *dst) {
+    const enc_plan_t *p = &x->plan;
+    const size_t rowb = MEL_NMEL * sizeof(float);
+    memcpy(dst, x->mel_cache, (size_t)x->cache_before * rowb);
+    memcpy(dst + (size_t)x->cache_before * MEL_NMEL, x->pending, (size_t)p->take * rowb);
+    memcpy(x->mel_cache, dst + (size_t)(p->nwin - x->book.mel_cache_n) * MEL_NMEL, (size_t)x->book.mel_cache_n * rowb);
+    memmove(x->pending, x->pending + (size_t)p->take * MEL_NMEL, (x->pending_n - (size_t)p->take) * rowb);
+    x->pending_n = x->book.pending_n;
+    x->consumed = x->book.consumed;
+    x->emitted = x->book.emitted;
+    x->mel_cache_n = x->book.mel_cache_n;
+}
+
+/* The next chunk of one stream that yields rows (chunks that yield none are consumed on the way).
+ * Returns 1 if the stream consumed input. */
+static int plan_stream(nemoasr_batch_t *b, bstream_t *x) {
+    int ran = 0;
+    x->c = 0;
+    for (;;) {
+        x->book = (enc_book_t){ x->pending_n, x->consumed, x->emitted, x->mel_cache_n, x->closed };
+        x->cache_before = x->mel_cache_n;
+        x->plan = enc_plan_step(&x->book, x->final, b->chunk_mel, b->m->cfg.subsampling, MEL_CACHE);
+        x->closed = x->book.closed;
+        if (!x->plan.ran) return ran;
+        ran = 1;
+        if (x->plan.c <= 0) {
+            take_window(x, b->wtmp);
+            continue;
+        }
+        x->c = x->plan.c;
+        x->nwin = x->plan.nwin;
+        x->lo = x->plan.lo;
+        return 1;
+    }
+}
+
+/* subsampling of `cnt` windows of nwin rows (back to back in win) into pre_out rows:
+ * src/encoder.c:120-142 */
+static void launch_pre_encode(nemoasr_batch_t *b, const float *win, int nwin, int cnt, float *pre_out) {
+    model_t *m = b->m;
+    gpu_t *g = b->g;
+    const uint32_t CH = (uint32_t)m->cfg.sub_channels, F = (uint32_t)m->cfg.feat_in, n = (uint32_t)cnt;
+    const uint32_t T1 = (uint32_t)sub_len(nwin), F1 = F / 2 + 1, T2 = T1 / 2 + 1, F2 = F1 / 2 + 1, T3 = T2 / 2 + 1,
+                   F3 = F2 / 2 + 1;
+    float *c0 = gpu_buf_dptr(b->c0), *c1 = gpu_buf_dptr(b->c1), *c2 = gpu_buf_dptr(b->c2), *c3 = gpu_buf_dptr(b->c3);
+    float *c4 = gpu_buf_dptr(b->c4), *flat = gpu_buf_dptr(b->flat);
+    nk_conv2d_c1_s2_relu_b(g, win, m->conv0_w, m->conv0_b, c0, (uint32_t)nwin, F, T1, F1, CH, n);
+    nk_dwconv2d_s2_b(g, c0, m->conv2_w, m->conv2_b, c1, T1, F1, T2, F2, CH, n);
+    nk_gemm(g, c1, CH, m->conv3_w, CH, m->conv3_b, c2, CH, n * T2 * F2, CH, CH, NK_ACT_RELU, 0, 1.0f);
+    nk_dwconv2d_s2_b(g, c2, m->conv5_w, m->conv5_b, c3, T2, F2, T3, F3, CH, n);
+    nk_gemm(g, c3, CH, m->conv6_w, CH, m->conv6_b, c4, CH, n * T3 * F3, CH, CH, NK_ACT_RELU, 0, 1.0f);
+    nk_flatten_cf_b(g, c4, flat, T3, F3, CH, n);
+    const uint32_t D = (uint32_t)m->cfg.d_model, K = CH * F3;
+    nk_gemm(g, flat, K, m->pre_out_w, K, m->pre_out_b, pre_out, D, n * T3, D, K, NK_ACT_NONE, 0, 1.0f);
+}
+
+/* conformer blocks + prompt + joint projection on the M rows in h (src/encoder.c:144-197).
+ * The order of operations and the LayerNorm placement are those of the single-stream encoder;
+ * crow maps every row to its stream's cache row, rows is the attention/conv row table. */
+static void launch_blocks(nemoasr_batch_t *b, uint32_t M, const int *crow, const int *rows) {
+    model_t *m = b->m;
+    gpu_t *g = b->g;
+    const model_cfg_t *cf = &m->cfg;
+    const uint32_t D = (uint32_t)cf->d_model, FF = (uint32_t)cf->d_ff, H = (uint32_t)cf->n_heads,
+                   dh = (uint32_t)cf->head_dim, nl = (uint32_t)cf->n_layers;
+    const float eps = cf->ln_eps, scale = 1.0f / sqrtf((float)dh);
+    float *R[2] = { gpu_buf_dptr(b->h), gpu_buf_dptr(b->tmp) };
+    float *lnbuf = gpu_buf_dptr(b->lnb), *ff = gpu_buf_dptr(b->ff), *att = gpu_buf_dptr(b->att), *y = gpu_buf_dptr(b->y);
+    int cur = 0;
+    for (uint32_t l = 0; l < nl; ++l) {
+        const layer_dev_t *W = &m->L[l];
+        float *kv = (float *)gpu_buf_dptr(b->kv) + (size_t)l * b->kv_lstride;
+        float *din = (float *)gpu_buf_dptr(b->din) + (size_t)l * b->din_lstride;
+        if (l == 0) {
+            nk_gemm_ln(g, R[0], D, W->ff1_w1, D, NULL, ff, FF, NULL, M, FF, D, NK_ACT_SILU, 0, 1.0f, 1, W->ln_ff1_g,
+                       W->ln_ff1_b, NULL, NULL, NULL, lnbuf, eps);
+        } else {
+            const layer_dev_t *Wp = &m->L[l - 1];
+            const int prev = cur;
+            cur ^= 1;
+            nk_gemm_ln(g, R[prev], D, W->ff1_w1, D, NULL, ff, FF, NULL, M, FF, D, NK_ACT_SILU, 0, 1.0f, 2, Wp->ln_out_g,
+                       Wp->ln_out_b, W->ln_ff1_g, W->ln_ff1_b, R[cur], lnbuf, eps);
+        }
+        float *res = R[cur];
+        nk_gemm(g, ff, FF, W->ff1_w2, FF, NULL, res, D, M, D, FF, NK_ACT_NONE, 1, 0.5f);
+        nk_gemm_ln(g, res, D, W->wqkv, D, NULL, kv, 3 * D, crow, M, 3 * D, D, NK_ACT_NONE, 0, 1.0f, 1, W->ln_att_g,
+                   W->ln_att_b, NULL, NULL, NULL, lnbuf, eps);
+        nk_attention_rel_rows(g, kv, 3 * D, rows, M, W->ptab, W->bias_u, W->bias_v, att, (uint32_t)b->Lmax, H, dh, D,
+                              scale);
+        nk_gemm(g, att, D, W->wo, D, NULL, res, D, M, D, D, NK_ACT_NONE, 1, 1.0f);
+        nk_gemm_ln(g, res, D, W->pw1, D, NULL, din, D, crow, M, 2 * D, D, NK_ACT_GLU, 0, 1.0f, 1, W->ln_conv_g,
+                   W->ln_conv_b, NULL, NULL, NULL, lnbuf, eps);
+        nk_dwconv_ln_silu_rows(g, din, rows, M, W->dw_w, W->bn_g, W->bn_b, y, D, (uint32_t)cf->conv_kernel, eps);
+        nk_gemm(g, y, D, W->pw2, D, NULL, res, D, M, D, D, NK_ACT_NONE, 1, 1.0f);
+        nk_gemm_ln(g, res, D, W->ff2_w1, D, NULL, ff, FF, NULL, M, FF, D, NK_ACT_SILU, 0, 1.0f, 1, W->ln_ff2_g,
+                   W->ln_ff2_b, NULL, NULL, NULL, lnbuf, eps);
+        nk_gemm(g, ff, FF, W->ff2_w2, FF, NULL, res, D, M, D, FF, NK_ACT_NONE, 1, 0.5f);
+    }
+    const layer_dev_t *Wl = &m->L[nl - 1];
+    const uint32_t PH = (uint32_t)cf->prompt_hidden, NP = (uint32_t)cf->num_prompts, JH = (uint32_t)b->J;
+    float *ph = gpu_buf_dptr(b->ph), *pr = gpu_buf_dptr(b->prompted);
+    nk_gemm_ln(g, R[cur], D, m->prompt_w0, D + NP, m->prompt_b0_eff, ph, PH, NULL, M, PH, D, NK_ACT_RELU, 0, 1.0f, 1,
+               Wl->ln_out_g, Wl->ln_out_b, NULL, NULL, NULL, lnbuf, eps);
+    nk_gemm(g, ph, PH, m->prompt_w2, PH, m->prompt_b2, pr, D, M, D, PH, NK_ACT_NONE, 0, 1.0f);
+    nk_gemm(g, pr, D, m->joint_enc_w, D, m->joint_enc_b, gpu_buf_dptr(b->joint_enc), JH, M, JH, D, NK_ACT_NONE, 0, 1.0f);
+}
+
+static void launch_encoder(nemoasr_batch_t *b, int M) {
+    const size_t F = (size_t)b->m->cfg.feat_in, D = (size_t)b->m->cfg.d_model;
+    const int *tab = gpu_buf_dptr(b->etab);
+    for (int k = 0; k < b->ng; ++k)
+        launch_pre_encode(b, (const float *)gpu_buf_dptr(b->win) + (size_t)b->g_woff[k] * F, b->g_nwin[k], b->g_cnt[k],
+                          (float *)gpu_buf_dptr(b->pre_out) + (size_t)b->g_poff[k] * D);
+    nk_gather_rows(b->g, gpu_buf_dptr(b->pre_out), (uint32_t)D, tab + 5 * M, gpu_buf_dptr(b->h), (uint32_t)D, (uint32_t)M,
+                   (uint32_t)D);
+    launch_blocks(b, (uint32_t)M, tab, tab + M);
+}
+
+/* move a stream's live cache rows to the front of its region, every layer (src/encoder.c:199-211) */
+static void compact_stream(nemoasr_batch_t *b, int s) {
+    bstream_t *x = &b->st[s];
+    const uint32_t D = (uint32_t)b->m->cfg.d_model, nl = (uint32_t)b->m->cfg.n_layers;
+    float *kv = (float *)gpu_buf_dptr(b->kv) + (size_t)s * b->cap_rows * 3 * D;
+    float *din = (float *)gpu_buf_dptr(b->din) + (size_t)s * b->cap_rows * D;
+    if (x->cache_len > 0)
+        nk_compact(b->g, kv, b->kv_lstride, nl, (uint32_t)x->cache_len, 3 * D, (uint32_t)(x->pos - x->cache_len), 0);
+    nk_compact(b->g, din, b->din_lstride, nl, (uint32_t)b->conv_left, D, (uint32_t)(x->pos - b->conv_left),
+               (uint32_t)(x->cache_len - b->conv_left));
+    x->pos = x->cache_len;
+}
+
+/* One batched encoder step.  Returns the number of streams that consumed input; *M_out = rows. */
+static int encoder_batch_step(nemoasr_batch_t *b, int *M_out, char *err, size_t errlen) {
+    const size_t F = (size_t)b->m->cfg.feat_in;
+    int consumed = 0, nact = 0;
+    for (int s = 0; s < b->S; ++s) {
+        bstream_t *x = &b->st[s];
+        consumed += plan_stream(b, x);
+        if (x->c > 0) b->order[nact++] = s;
+    }
+    *M_out = 0;
+    if (!nact) return consumed;
+    /* windows grouped by length, in order of first appearance; streams keep their order inside a
+     * group and rows follow the group order */
+    b->ng = 0;
+    for (int i = 0; i < nact; ++i) {
+        const bstream_t *x = &b->st[b->order[i]];
+        int k = 0;
+        while (k < b->ng && b->g_nwin[k] != x->nwin) ++k;
+        if (k == b->ng) { b->g_nwin[k] = x->nwin; b->g_cnt[k] = 0; b->ng++; }
+        b->gid[i] = k;
+        b->g_cnt[k]++;
+    }
+    int woff = 0, poff = 0;
+    for (int k = 0; k < b->ng; ++k) {
+        b->g_woff[k] = woff;
+        b->g_poff[k] = poff;
+        woff += b->g_cnt[k] * b->g_nwin[k];
+        poff += b->g_cnt[k] * sub_len(sub_len(sub_len(b->g_nwin[k])));
+    }
+    /* row order: group by group */
+    int M = 0;
+    int *fill = b->g_fill, *ord = b->ord;
+    memset(fill, 0, (size_t)b->ng * sizeof(int));
+    int n2 = 0;
+    for (int k = 0; k < b->ng; ++k)
+        for (int i = 0; i < nact; ++i)
+            if (b->gid[i] == k) ord[n2++] = b->order[i];
+    memcpy(b->order, ord, (size_t)nact * sizeof(int));
+    gpu_t *g = b->g;
+    gpu_begin(g);
+    int *crow = b->stage_tab;
+    for (int i = 0; i < nact; ++i) {
+        const int s = b->order[i];
+        bstream_t *x = &b->st[s];
+        int k = 0;
+        while (b->g_nwin[k] != x->nwin) ++k;
+        const int j = fill[k]++;
+        const int T3 = sub_len(sub_len(sub_len(x->nwin)));
+        x->gk = k;
+        x->gj = j;
+        take_window(x, b->stage_win + ((size_t)b->g_woff[k] + (size_t)j * x->nwin) * F);
+        if (x->pos + x->c > b->cap_rows) compact_stream(b, s);
+        const int L = x->cache_len + x->c;
+        if (L > b->Lmax || x->pos < x->cache_len || x->pos < b->conv_left || x->pos + x->c > b->cap_rows ||
+            x->lo + x->c > T3) {
+            snprintf(err, errlen, "stream %d: cache bookkeeping out of range (pos %d, cache %d, c %d)", s, x->pos,
+                     x->cache_len, x->c);
+            gpu_end(g, NULL, 0);
+            return -1;
+        }
+        x->row0 = M;
+        M += x->c;
+    }
+    if (M > b->Mmax) {
+        snprintf(err, errlen, "batch: %d rows exceed %d", M, b->Mmax);
+        gpu_end(g, NULL, 0);
+        return -1;
+    }
+    /* tables: crow[M], rows[4M], gather map[M] */
+    int *rows = crow + M, *gmap = crow + 5 * M;
+    for (int i = 0; i < nact; ++i) {
+        const int s = b->order[i];
+        const bstream_t *x = &b->st[s];
+        const int k = x->gk, j = x->gj;
+        const int T3 = sub_len(sub_len(sub_len(x->nwin)));
+        for (int r = 0; r < x->c; ++r) {
+            const int m = x->row0 + r;
+            crow[m] = s * b->cap_rows + x->pos + r;
+            rows[4 * m] = crow[m];
+            rows[4 * m + 1] = r;
+            rows[4 * m + 2] = x->c;
+            rows[4 * m + 3] = x->cache_len;
+            gmap[m] = b->g_poff[k] + j * T3 + x->lo + r;
+        }
+    }
+    gpu_upload_async(g, gpu_buf_dptr(b->win), b->stage_win, (size_t)woff * F * sizeof(float));
+    gpu_upload_async(g, gpu_buf_dptr(b->etab), crow, (size_t)6 * M * sizeof(int));
+    bgraph_t *gs = b->use_graphs ? bgraph_slot(b, M) : NULL;
+    if (gs) {
+        gs->last_use = ++b->tick;
+        if (!gs->graph && gs->seen >= 1 && !gpu_capture_begin(g)) {
+            launch_encoder(b, M);
+            gs->graph = gpu_capture_end(g);
+        }
+        gs->seen++;
+        if (gs->graph) gpu_graph_launch(g, gs->graph);
+        else launch_encoder(b, M);
+    } else {
+        launch_encoder(b, M);
+    }
+    for (int i = 0; i < nact; ++i) {
+        bstream_t *x = &b->st[b->order[i]];
+        const int L = x->cache_len + x->c;
+        x->pos += x->c;
+        x->cache_len = L < b->left ? L : b->left;
+    }
+    if (gpu_end(g, err, errlen)) return -1;
+    *M_out = M;
+    return consumed;
+}
+
+/* ---- batched greedy RNNT --------------------------------------------------------------------- */
+
+/* rows of the LSTM state buffer: stream s, slot set k: h0, c0, h1, c1 */
+static int hc_row(int s, int k, int which) { return (s * 2 + k) * 4 + which; }
+
+static void keep_token(bstream_t *x, int t) {
+    if (x->n_tok == x->cap_tok) {
+        x->cap_tok = x->cap_tok ? 2 * x->cap_tok : 256;
+        x->tok = realloc(x->tok, x->cap_tok * sizeof(int));
+    }
+    x->tok[x->n_tok++] = t;
+}
+
+/* The greedy loop of src/decoder.c:92-127 for the chunks of the streams in order[0..nact). */
+static int decoder_batch_run(nemoasr_batch_t *b, int nact, char *err, size_t errlen) {
+    model_t *m = b->m;
+    gpu_t *g = b->g;
+    const int S = b->S, blank = m->cfg.blank_id, maxsym = m->cfg.max_symbols;
+    const uint32_t P = (uint32_t)b->P, J = (uint32_t)b->J;
+    int *T = b->stage_dtab;
+    int *tok = T, *h0c = T + S, *c0c = T + 2 * S, *c0p = T + 3 * S, *h0p = T + 4 * S, *h1c = T + 5 * S, *c1c = T + 6 * S;
+    int *c1p = T + 7 * S, *h1p = T + 8 * S, *pidx = T + 9 * S, *erow = T + 10 * S, *prow = erow + S * DEC_WIN;
+    const int *D = gpu_buf_dptr(b->dtab);
+    const int *dtok = D, *dh0c = D + S, *dc0c = D + 2 * S, *dc0p = D + 3 * S, *dh0p = D + 4 * S, *dh1c = D + 5 * S;
+    const int *dc1c = D + 6 * S, *dc1p = D + 7 * S, *dh1p = D + 8 * S, *dpidx = D + 9 * S, *derow = D + 10 * S;
+    const int *dprow = derow + S * DEC_WIN;
+    float *hc = gpu_buf_dptr(b->hc), *lin = gpu_buf_dptr(b->lin), *gates = gpu_buf_dptr(b->gates);
+    float *hout = gpu_buf_dptr(b->hout), *hout2 = gpu_buf_dptr(b->hout2), *pred = gpu_buf_dptr(b->pred);
+    int *rcount = malloc((size_t)nact * sizeof(int));
+    for (int it = 0;; ++it) {
+        if (it > 1 << 20) { free(rcount); snprintf(err, errlen, "decoder: no progress"); return -1; }
+        int n = 0, R = 0;
+        for (int i = 0; i < nact; ++i) {
+            const int s = b->order[i];
+            bstream_t *x = &b->st[s];
+            rcount[i] = 0;
+            if (x->t >= x->frames) continue;
+            if (!x->pred_valid) {
+                const int kc = x->cur, kp = x->cur ^ 1;
+                tok[n] = x->last_token;
+                h0c[n] = hc_row(s, kc, 0); c0c[n] = hc_row(s, kc, 1); h1c[n] = hc_row(s, kc, 2); c1c[n] = hc_row(s, kc, 3);
+                h0p[n] = hc_row(s, kp, 0); c0p[n] = hc_row(s, kp, 1); h1p[n] = hc_row(s, kp, 2); c1p[n] = hc_row(s, kp, 3);
+                pidx[n] = s;
+                n++;
+            }
+            int r = x->frames - x->t;
+            if (r > DEC_WIN) r = DEC_WIN;
+            for (int k = 0; k < r; ++k) {
+                erow[R + k] = x->erow0 + x->t + k;
+                prow[R + k] = s;
+            }
+            rcount[i] = r;
+            R += r;
+        }
+        if (!R) break;
+        gpu_begin(g);
+        gpu_upload_async(g, gpu_buf_dptr(b->dtab), T, (size_t)(10 * S + 2 * S * DEC_WIN) * sizeof(int));
+        if (n) {
+            /* prediction network from the committed state, input embed(last token) (zeros for blank) */
+            const uint32_t un = (uint32_t)n;
+            nk_lstm_input_rows(g, m->embed_dev, dtok, NULL, hc, dh0c, lin, un, P, (uint32_t)blank);
+            nk_gemm(g, lin, 2 * P, gpu_buf_dptr(b->wcat[0]), 2 * P, m->lstm_b[0], gates, 4 * P, un, 4 * P, 2 * P,
+                    NK_ACT_NONE, 0, 1.0f);
+            nk_lstm_cell_rows(g, gates, hc, dc0c, dc0p, dh0p, hout, un, P);
+            nk_lstm_input_rows(g, NULL, NULL, hout, hc, dh1c, lin, un, P, (uint32_t)blank);
+            nk_gemm(g, lin, 2 * P, gpu_buf_dptr(b->wcat[1]), 2 * P, m->lstm_b[1], gates, 4 * P, un, 4 * P, 2 * P,
+                    NK_ACT_NONE, 0, 1.0f);
+            nk_lstm_cell_rows(g, gates, hc, dc1c, dc1p, dh1p, hout2, un, P);
+            nk_gemm_rows(g, hout2, P, m->joint_pred_w, P, m->joint_pred_b, pred, J, dpidx, un, J, P, NK_ACT_NONE, 0,
+                         1.0f);
+        }
+        /* joint + argmax for every stream's pending frames (speculating blank) */
+        const uint32_t uR = (uint32_t)R, Vp = (uint32_t)b->Vp;
+        nk_joint_in_rows(g, gpu_buf_dptr(b->joint_enc), pred, derow, dprow, gpu_buf_dptr(b->jin), uR, J);
+        nk_gemm(g, gpu_buf_dptr(b->jin), J, gpu_buf_dptr(b->wout), J, gpu_buf_dptr(b->bout), gpu_buf_dptr(b->logits),
+                Vp, uR, Vp, J, NK_ACT_NONE, 0, 1.0f);
+        nk_argmax_rows(g, gpu_buf_dptr(b->logits), Vp, uR, (uint32_t)b->V, gpu_buf_dptr(b->amax));
+        gpu_download_async(g, b->stage_amax, gpu_buf_dptr(b->amax), (size_t)2 * R * sizeof(int));
+        if (gpu_end(g, err, errlen)) { free(rcount); return -1; }
+        b->stats.joint_steps++;
+        const int *res = b->stage_amax;
+        int r0 = 0;
+        for (int i = 0; i < nact; ++i) {
+            bstream_t *x = &b->st[b->order[i]];
+            const int rows = rcount[i];
+            if (!rows) continue;
+            x->pred_valid = 1;
+            int k = 0;
+            for (; k < rows; ++k) {
+                const int pr = res[2 * (r0 + k)];
+                if (pr == blank) { x->symbols = 0; continue; }
+                keep_token(x, pr);
+                b->stats.tokens++;
+                x->last_token = pr;
+                x->cur ^= 1; /* commit the provisional state */
+                x->pred_valid = 0;
+                x->symbols++;
+                if (x->symbols >= maxsym) { x->symbols = 0; k++; }
+                break;
+            }
+            x->t += k;
+            r0 += rows;
+        }
+    }
+    free(rcount);
+    return 0;
+}
+
+int nemoasr_batch_step(nemoasr_batch_t *b, char *err, size_t errlen) {
+    if (errlen) err[0] = 0;
+    const double t0 = now_ms();
+    int M = 0;
+    const int consumed = encoder_batch_step(b, &M, err, errlen);
+    if (consumed < 0) return -1;
+    if (!M) return consumed;
+    const double t1 = now_ms();
+    int nact = 0;
+    for (int s = 0; s < b->S; ++s) {
+        bstream_t *x = &b->st[s];
+        if (x->c <= 0) continue;
+        nact++;
+    }
+    /* order[] holds the streams of this step in row order */
+    for (int i = 0; i < nact; ++i) {
+        bstream_t *x = &b->st[b->order[i]];
+        x->frames = x->c;
+        x->t = 0;
+        x->symbols = 0;
+        x->erow0 = x->row0;
+    }
+    if (b->dump) {
+        const size_t J = (size_t)b->J;
+        float *all = malloc((size_t)M * J * sizeof(float));
+        if (gpu_download(b->g, all, gpu_buf_dptr(b->joint_enc), (size_t)M * J * sizeof(float))) {
+            free(all);
+            snprintf(err, errlen, "batch: dump download failed");
+            return -1;
+        }
+        for (int i = 0; i < nact; ++i) {
+            const int s = b->order[i];
+            const bstream_t *x = &b->st[s];
+            if (b->dj_n[s] + (size_t)x->c > b->dj_cap[s]) {
+                b->dj_cap[s] = (b->dj_n[s] + (size_t)x->c) * 2 + 64;
+                b->dj[s] = realloc(b->dj[s], b->dj_cap[s] * J * sizeof(float));
+            }
+            memcpy(b->dj[s] + b->dj_n[s] * J, all + (size_t)x->row0 * J, (size_t)x->c * J * sizeof(float));
+            b->dj_n[s] += (size_t)x->c;
+        }
+        free(all);
+    }
+    if (decoder_batch_run(b, nact, err, errlen)) return -1;
+    const double t2 = now_ms();
+    b->stats.steps++;
+    b->stats.chunks += (size_t)nact;
+    b->stats.rows += (size_t)M;
+    b->stats.encoder_ms += t1 - t0;
+    b->stats.decoder_ms += t2 - t1;
+    if (b->n_step == b->cap_step) {
+        b->cap_step = b->cap_step ? 2 * b->cap_step : 256;
+        b->step_ms = realloc(b->step_ms, b->cap_step * sizeof(double));
+    }
+    b->step_ms[b->n_step++] = t2 - t0;
+    return consumed;
+}
+
+int nemoasr_batch_run(nemoasr_batch_t *b, char *err, size_t errlen) {
+    int steps = 0;
+    for (;;) {
+        const int rc = nemoasr_batch_step(b, err, errlen);
+        if (rc < 0) return -1;
+        if (rc == 0) return steps;
+        steps++;
+    }
+}
+
+const int *nemoasr_batch_tokens(const nemoasr_batch_t *b, int stream, size_t *n) {
+    if (stream < 0 || stream >= b->S) { *n = 0; return NULL; }
+    *n = b->st[stream].n_tok;
+    return b->st[stream].tok;
+}
+
+/* token pieces as text, leading spaces of the first printed piece dropped (src/nemoasr.c:123-129) */
+char *nemoasr_batch_text(nemoasr_batch_t *b, int stream) {
+    if (stream < 0 || stream >= b->S) return NULL;
+    bstream_t *x = &b->st[stream];
+    char *out = NULL;
+    size_t len = 0, cap = 0;
+    for (; x->n_text < x->n_tok; ++x->n_text) {
+        char *txt = piece_text(&b->m->vocab, x->tok[x->n_text]);
+        const char *p = txt;
+        if (!x->printed_any) while (*p == ' ') p++;
+        const size_t k = strlen(p);
+        if (k) {
+            if (len + k + 1 > cap) {
+                cap = (len + k + 1) * 2;
+                out = realloc(out, cap);
+            }
+            memcpy(out + len, p, k + 1);
+            len += k;
+            x->printed_any = 1;
+        }
+        free(txt);
+    }
+    return out;
+}
+
+int nemoasr_batch_reset_stream(nemoasr_batch_t *b, int stream, char *err, size_t errlen) {
+    if (errlen) err[0] = 0;
+    if (check_stream(b, stream, err, errlen)) return -1;
+    stream_clear(b, stream);
+    b->st[stream].n_tok = 0;
+    if (stream_zero_device(b, stream)) { snprintf(err, errlen, "batch: reset upload failed"); return -1; }
+    return 0;
+}
+
+void nemoasr_batch_stats(const nemoasr_batch_t *b, nemoasr_batch_stats_t *out) { *out = b->stats; }
+
+const double *nemoasr_batch_step_ms(const nemoasr_batch_t *b, size_t *n) {
+    *n = b->n_step;
+    return b->step_ms;
+}
+
+/* ---- test hooks ---------------------------------------------------------------------------- */
+void nemoasr_batch_debug_use_graphs(nemoasr_batch_t *b, int on) {
+    b->use_graphs = on;
+    if (!on) drop_graphs(b);
+}
+
+void nemoasr_batch_debug_set_dump(nemoasr_batch_t *b, int on) {
+    b->dump = on;
+    if (on && !b->dj) {
+        b->dj = calloc((size_t)b->S, sizeof(float *));
+        b->dj_n = calloc((size_t)b->S, sizeof(size_t));
+        b->dj_cap = calloc((size_t)b->S, sizeof(size_t));
+    }
+}
+
+const float *nemoasr_batch_debug_joint_enc(const nemoasr_batch_t *b, int stream, size_t *frames) {
+    if (!b->dj || stream < 0 || stream >= b->S) { *frames = 0; return NULL; }
+    *frames = b->dj_n[stream];
+    return b->dj[stream];
+}

@@ -1,6 +1,7 @@
 """ctypes binding of libnemoasr_hip.so for tests, the benchmark and smoke checks.
 
-Exposes the public API (include/nemoasr.h), the test hooks (include/nemoasr_debug.h), the
+Exposes the public API (include/nemoasr.h), the multi-stream batch API (include/nemoasr_batch.h),
+the test hooks (include/nemoasr_debug.h), the
 kernel-level C ABI (include/nemo_kernels.h) and the exported host helpers
 (include/nemoasr_host.h).  Loading the library needs no GPU; creating a session or a device
 context does, and fails loudly without one — there is no CPU fallback.
@@ -37,6 +38,22 @@ API = {
     "nemoasr_gpu_name": (C.c_char_p, [_vp]),
     "nemoasr_latency_ms": (C.c_int, [_vp]),
     "nemoasr_stats": (None, [_vp, _vp]),
+    # include/nemoasr_batch.h
+    "nemoasr_batch_open": (_vp, [C.c_char_p, C.c_char_p, C.c_int, C.c_int, C.c_char_p, C.c_size_t]),
+    "nemoasr_batch_close": (None, [_vp]),
+    "nemoasr_batch_streams": (C.c_int, [_vp]),
+    "nemoasr_batch_push": (C.c_int, [_vp, C.c_int, _f32p, C.c_size_t, C.c_int, C.c_char_p, C.c_size_t]),
+    "nemoasr_batch_push_mel": (C.c_int, [_vp, C.c_int, _f32p, C.c_size_t, C.c_int, C.c_char_p, C.c_size_t]),
+    "nemoasr_batch_step": (C.c_int, [_vp, C.c_char_p, C.c_size_t]),
+    "nemoasr_batch_run": (C.c_int, [_vp, C.c_char_p, C.c_size_t]),
+    "nemoasr_batch_tokens": (_i32p, [_vp, C.c_int, C.POINTER(C.c_size_t)]),
+    "nemoasr_batch_text": (_vp, [_vp, C.c_int]),
+    "nemoasr_batch_reset_stream": (C.c_int, [_vp, C.c_int, C.c_char_p, C.c_size_t]),
+    "nemoasr_batch_stats": (None, [_vp, _vp]),
+    "nemoasr_batch_step_ms": (C.POINTER(C.c_double), [_vp, C.POINTER(C.c_size_t)]),
+    "nemoasr_batch_debug_use_graphs": (None, [_vp, C.c_int]),
+    "nemoasr_batch_debug_set_dump": (None, [_vp, C.c_int]),
+    "nemoasr_batch_debug_joint_enc": (_f32p, [_vp, C.c_int, C.POINTER(C.c_size_t)]),
     # include/nemoasr_debug.h
     "nemoasr_debug_feed_mel": (C.c_int, [_vp, _f32p, C.c_size_t, C.c_int, C.c_char_p, C.c_size_t]),
     "nemoasr_debug_tokens": (_i32p, [_vp, C.POINTER(C.c_size_t)]),
@@ -96,7 +113,18 @@ API = {
     "nk_copy2d": (C.c_int, [_vp, _vp, _u32, _vp, _u32, _u32, _u32]),
     "nk_fill": (C.c_int, [_vp, _vp, _u32, C.c_float]),
     "nk_compact": (C.c_int, [_vp, _vp, C.c_uint64, _u32, _u32, _u32, _u32, _u32]),
+    "nk_attention_rel_rows": (C.c_int, [_vp, _vp, _u32, _vp, _u32, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32,
+                                        C.c_float]),
+    "nk_dwconv_ln_silu_rows": (C.c_int, [_vp, _vp, _vp, _u32, _vp, _vp, _vp, _vp, _u32, _u32, C.c_float]),
+    "nk_conv2d_c1_s2_relu_b": (C.c_int, [_vp, _vp, _vp, _vp, _vp] + [_u32] * 6),
+    "nk_dwconv2d_s2_b": (C.c_int, [_vp, _vp, _vp, _vp, _vp] + [_u32] * 6),
+    "nk_flatten_cf_b": (C.c_int, [_vp, _vp, _vp, _u32, _u32, _u32, _u32]),
+    "nk_gather_rows": (C.c_int, [_vp, _vp, _u32, _vp, _vp, _u32, _u32, _u32]),
     "nk_lstm_cell": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _u32]),
+    "nk_lstm_input_rows": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32]),
+    "nk_lstm_cell_rows": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32]),
+    "nk_joint_in_rows": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32]),
+    "nk_argmax_rows": (C.c_int, [_vp, _vp, _u32, _u32, _u32, _vp]),
     "nk_joint_argmax": (C.c_int, [_vp, _vp, _u32, _u32, _u32, _vp, _vp, _vp, _u32, _u32, _vp, _vp, _vp]),
     # include/nemoasr_host.h
     "melfe_create": (_vp, []),
@@ -303,6 +331,93 @@ class Session:
     def close(self):
         if self.h:
             lib().nemoasr_close(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+
+class Batch:
+    """Many streams on one model (include/nemoasr_batch.h)."""
+
+    def __init__(self, model_dir: str, language: str = "en-US", latency_ms: int = 560, streams: int = 64):
+        err = C.create_string_buffer(1024)
+        self.h = lib().nemoasr_batch_open(model_dir.encode(), language.encode(), latency_ms, streams, err, 1024)
+        if not self.h:
+            raise RuntimeError("nemoasr_batch_open: " + err.value.decode())
+        self.n = streams
+
+    def _check(self, rc: int, what: str, err) -> int:
+        if rc < 0:
+            raise RuntimeError(f"{what}: " + err.value.decode())
+        return rc
+
+    def push(self, stream: int, audio: np.ndarray, final: bool = False):
+        a = np.ascontiguousarray(audio, dtype=np.float32)
+        err = C.create_string_buffer(1024)
+        self._check(lib().nemoasr_batch_push(self.h, stream, fp(a), a.size, int(final), err, 1024), "push", err)
+
+    def push_mel(self, stream: int, mel: np.ndarray, final: bool = False):
+        m = np.ascontiguousarray(mel, dtype=np.float32).reshape(-1, 128)
+        err = C.create_string_buffer(1024)
+        self._check(lib().nemoasr_batch_push_mel(self.h, stream, fp(m), m.shape[0], int(final), err, 1024),
+                    "push_mel", err)
+
+    def step(self) -> int:
+        err = C.create_string_buffer(1024)
+        return self._check(lib().nemoasr_batch_step(self.h, err, 1024), "step", err)
+
+    def run(self) -> int:
+        err = C.create_string_buffer(1024)
+        return self._check(lib().nemoasr_batch_run(self.h, err, 1024), "run", err)
+
+    def tokens(self, stream: int) -> list[int]:
+        n = C.c_size_t()
+        p = lib().nemoasr_batch_tokens(self.h, stream, C.byref(n))
+        return np.ctypeslib.as_array(p, shape=(n.value,)).tolist() if n.value else []
+
+    def text(self, stream: int) -> str:
+        p = lib().nemoasr_batch_text(self.h, stream)
+        if not p:
+            return ""
+        s = C.cast(p, C.c_char_p).value.decode("utf-8", "replace")
+        lib().nemoasr_free(p)
+        return s
+
+    def reset_stream(self, stream: int):
+        err = C.create_string_buffer(1024)
+        self._check(lib().nemoasr_batch_reset_stream(self.h, stream, err, 1024), "reset_stream", err)
+
+    def stats(self) -> dict:
+        class St(C.Structure):
+            _fields_ = [("steps", C.c_size_t), ("chunks", C.c_size_t), ("rows", C.c_size_t),
+                        ("joint_steps", C.c_size_t), ("tokens", C.c_size_t), ("encoder_ms", C.c_double),
+                        ("decoder_ms", C.c_double)]
+        st = St()
+        lib().nemoasr_batch_stats(self.h, C.byref(st))
+        return {k: getattr(st, k) for k, _ in St._fields_}
+
+    def step_ms(self) -> np.ndarray:
+        n = C.c_size_t()
+        p = lib().nemoasr_batch_step_ms(self.h, C.byref(n))
+        return np.ctypeslib.as_array(p, shape=(n.value,)).copy() if n.value else np.zeros(0)
+
+    def use_graphs(self, on: bool):
+        lib().nemoasr_batch_debug_use_graphs(self.h, int(on))
+
+    def set_dump(self, on: bool):
+        lib().nemoasr_batch_debug_set_dump(self.h, int(on))
+
+    def joint_enc(self, stream: int, joint_hidden: int) -> np.ndarray:
+        n = C.c_size_t()
+        p = lib().nemoasr_batch_debug_joint_enc(self.h, stream, C.byref(n))
+        if not n.value:
+            return np.zeros((0, joint_hidden), np.float32)
+        return np.ctypeslib.as_array(p, shape=(n.value * joint_hidden,)).reshape(n.value, joint_hidden).copy()
+
+    def close(self):
+        if self.h:
+            lib().nemoasr_batch_close(self.h)
             self.h = None
 
     def __del__(self):

@@ -1,0 +1,143 @@
+"""Multi-stream batching (include/nemoasr_batch.h) against the oracle.
+
+Every stream of a batch must emit exactly the tokens that the oracle's single-stream session emits
+for that stream's audio, whatever the other streams do: different lengths, staggered starts,
+streams ending while others continue, a slot reused after reset.  The joint.enc rows of each stream
+(the joint's encoder input) are held to the encoder gate of the single-stream tests (1e-3
+relative).
+"""
+import numpy as np
+import pytest
+
+import mel_ref
+import oracle
+import synth
+from conftest import model_dir, rel_err
+
+pytestmark = pytest.mark.gpu
+
+LAT_RIGHT = {80: 0, 160: 1, 320: 3, 560: 6, 1120: 13}
+
+
+_ORACLE = {}
+
+
+def oracle_run(om, latency, mel, key=None):
+    """Oracle tokens and joint.enc rows of one stream (cached by key across parametrizations)."""
+    if key is not None and key in _ORACLE:
+        return _ORACLE[key]
+    o = oracle.Session(om, LAT_RIGHT[latency], dump=True)
+    o.feed_mel(mel, final=True)
+    _, _, oj, _ = o.dumps()
+    if key is not None:
+        _ORACLE[key] = (list(o.tokens), oj)
+    print(f"  oracle {key or ''}: {mel.shape[0]} mel rows, {len(o.tokens)} tokens", flush=True)
+    return list(o.tokens), oj
+
+
+def drive(b, mels, starts, piece):
+    """Feed each stream `piece` mel rows per tick from tick starts[s] on, one batch step per tick."""
+    pos = [0] * len(mels)
+    tick = 0
+    while any(p < m.shape[0] for p, m in zip(pos, mels)):
+        for s, m in enumerate(mels):
+            if tick < starts[s] or pos[s] >= m.shape[0]:
+                continue
+            end = min(pos[s] + piece, m.shape[0])
+            b.push_mel(s, m[pos[s]:end], final=end >= m.shape[0])
+            pos[s] = end
+        b.step()
+        tick += 1
+    b.run()
+
+
+def check_streams(b, om, latency, mels, J, tag=None):
+    for s, m in enumerate(mels):
+        toks, oj = oracle_run(om, latency, m, None if tag is None else (tag, s))
+        gj = b.joint_enc(s, J)
+        assert gj.shape == oj.shape, (s, gj.shape, oj.shape)
+        err = rel_err(gj, oj)
+        assert err <= 1e-3, (s, err)
+        assert b.tokens(s) == toks, f"stream {s}: {len(b.tokens(s))} tokens vs oracle {len(toks)}"
+
+
+@pytest.mark.parametrize("latency", [80, 560, 1120])
+def test_tiny_batch_matches_oracle(latency):
+    import nemoasr
+
+    mdir = model_dir("tiny")
+    om = oracle.Model(mdir, "en-US")
+    secs = [2.0, 1.3, 2.6, 0.4, 1.9, 2.2]
+    mels = [mel_ref.logmel(synth.make_audio(t, seed=40 + i)) for i, t in enumerate(secs)]
+    starts = [0, 0, 3, 5, 1, 9]
+    b = nemoasr.Batch(mdir, "en-US", latency, streams=len(mels))
+    b.set_dump(True)
+    drive(b, mels, starts, piece=8 * (LAT_RIGHT[latency] + 1))
+    check_streams(b, om, latency, mels, om.dims.joint_hidden)
+    st = b.stats()
+    assert st["chunks"] > 0 and st["tokens"] == sum(len(b.tokens(s)) for s in range(len(mels)))
+    b.close()
+
+
+@pytest.mark.parametrize("graphs", [False, True])
+def test_full_batch_matches_oracle(graphs):
+    """Full-size model, 560 ms, four streams in lockstep (graph replay of the steady step) and
+    one that starts late and ends early."""
+    import nemoasr
+
+    mdir = model_dir("full")
+    om = oracle.Model(mdir, "en-US")
+    secs = [2.5, 2.5, 2.0, 2.5, 1.2]
+    mels = [mel_ref.logmel(synth.make_audio(t, seed=60 + i)) for i, t in enumerate(secs)]
+    b = nemoasr.Batch(mdir, "en-US", 560, streams=len(mels))
+    b.use_graphs(graphs)
+    b.set_dump(True)
+    drive(b, mels, [0, 0, 0, 0, 4], piece=56)
+    check_streams(b, om, 560, mels, om.dims.joint_hidden, tag="full560")
+    b.close()
+
+
+def test_batch_matches_sessions_full():
+    """Sixteen streams at 560 ms against sixteen single-stream sessions (GPU against GPU)."""
+    import nemoasr
+
+    mdir = model_dir("full")
+    mels = [mel_ref.logmel(synth.make_audio(1.5 + 0.1 * (i % 5), seed=80 + i)) for i in range(16)]
+    b = nemoasr.Batch(mdir, "en-US", 560, streams=16)
+    for s, m in enumerate(mels):
+        b.push_mel(s, m, final=True)
+    b.run()
+    sess = nemoasr.Session(mdir, "en-US", 560)
+    for s, m in enumerate(mels):
+        sess.reset("en-US", 560)
+        sess.feed_mel(m, final=True)
+        assert b.tokens(s) == sess.tokens(), s
+    sess.close()
+    b.close()
+
+
+def test_batch_audio_and_reset():
+    """Audio pushed in 100 ms blocks, text per stream, and a slot reused after reset_stream."""
+    import nemoasr
+
+    mdir = model_dir("tiny")
+    om = oracle.Model(mdir, "en-US")
+    audios = [synth.make_audio(t, seed=90 + i) for i, t in enumerate([1.8, 2.3, 1.1])]
+    b = nemoasr.Batch(mdir, "en-US", 560, streams=3)
+    for i in range(0, max(a.size for a in audios), 1600):
+        for s, a in enumerate(audios):
+            if i < a.size:
+                b.push(s, a[i:i + 1600], final=i + 1600 >= a.size)
+        b.step()
+    b.run()
+    for s, a in enumerate(audios):
+        toks, _ = oracle_run(om, 560, mel_ref.logmel(a))
+        assert b.tokens(s) == toks, s
+        b.text(s)
+    first = b.tokens(1)
+    b.reset_stream(1)
+    assert b.tokens(1) == []
+    b.push(1, audios[1], final=True)
+    b.run()
+    assert b.tokens(1) == first
+    b.close()

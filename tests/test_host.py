@@ -79,6 +79,20 @@ def test_open_without_gpu_fails_loudly(tiny_model_dir):
     h = L.nemoasr_open(tiny_model_dir.encode(), b"en-US", 560, 16000, err, 512)
     assert not h
     assert err.value, "nemoasr_open must say why it failed"
+    L.nemoasr_batch_open.restype = C.c_void_p
+    err = C.create_string_buffer(512)
+    h = L.nemoasr_batch_open(tiny_model_dir.encode(), b"en-US", 560, 8, err, 512)
+    assert not h
+    assert err.value, "nemoasr_batch_open must say why it failed"
+
+
+def test_batch_open_rejects_bad_arguments(tiny_model_dir):
+    L = product()
+    L.nemoasr_batch_open.restype = C.c_void_p
+    for lat, n in ((500, 4), (560, 0), (560, 5000)):
+        err = C.create_string_buffer(512)
+        assert not L.nemoasr_batch_open(tiny_model_dir.encode(), b"en-US", lat, n, err, 512)
+        assert err.value
 
 
 # ---- log-mel front end -------------------------------------------------------------------------
