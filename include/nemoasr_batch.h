@@ -27,7 +27,9 @@ typedef struct {
     size_t rows;           /* encoder rows (frames) over all chunks    */
     size_t joint_steps;    /* batched joint evaluations                */
     size_t tokens;
+    double frontend_ms;    /* wall time of the host log-mel front end  */
     double encoder_ms, decoder_ms; /* wall time of the two phases     */
+    double encoder_gpu_ms; /* GPU time of the encoder steps (hipEvents) */
 } nemoasr_batch_stats_t;
 
 /* Load the model and allocate n_streams streams (caches for all of them live in HBM).
@@ -64,6 +66,10 @@ const double *nemoasr_batch_step_ms(const nemoasr_batch_t *b, size_t *n);
 void nemoasr_batch_debug_use_graphs(nemoasr_batch_t *b, int on);
 void nemoasr_batch_debug_set_dump(nemoasr_batch_t *b, int on);
 const float *nemoasr_batch_debug_joint_enc(const nemoasr_batch_t *b, int stream, size_t *frames);
+/* Per-kernel timing of direct launches (kernel: exact name or a prefix ending in '*'): mean ms per
+   launch, launches, and the summed algorithmic bytes and flops of those launches. */
+int nemoasr_batch_debug_time_kernel(nemoasr_batch_t *b, const char *kernel, int max_launches);
+int nemoasr_batch_debug_kernel_ms(nemoasr_batch_t *b, double *mean_ms, int *count, double *bytes, double *flops);
 
 #ifdef __cplusplus
 }

@@ -27,15 +27,18 @@
 #include "nemo_kernels.h"
 #include "../kernel_params.h"
 #include <math.h>
+#include <pthread.h>
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
 #include <time.h>
+#include <unistd.h>
 
 #define MEL_CACHE 16      /* src/encoder.c:10 */
 #define DEC_WIN 16        /* frames scored per stream per joint evaluation, src/decoder.c:96-97 */
 #define MAX_BGRAPHS 8
 #define MAX_SIG_GROUPS 8
+#define POOL_MAX 16       /* host threads for the log-mel front end of a step */
 
 static double now_ms(void) {
     struct timespec ts;
@@ -47,6 +50,9 @@ static int sub_len(int n) { return n / 2 + 1; } /* src/encoder.c:118 */
 
 typedef struct {
     melfe_t *mel;
+    float *aq;                          /* audio queued for the front end */
+    size_t aq_n, aq_cap;
+    int ended, fe_final;                /* no more input; the front end flushes at the next step */
     float *pending;
     size_t pending_n, pending_cap;
     float mel_cache[MEL_CACHE * MEL_NMEL];
@@ -72,7 +78,23 @@ typedef struct {
     unsigned long long last_use;
 } bgraph_t;
 
+/* Persistent worker threads: the front end of the streams with queued audio runs in parallel
+ * (each stream's state is touched by one thread only). */
+typedef struct {
+    pthread_t th[POOL_MAX];
+    int n, started, quit;
+    unsigned gen;
+    pthread_mutex_t mu;
+    pthread_cond_t go, done;
+    int busy;
+    int next, count;
+    const int *list;
+    struct nemoasr_batch *b;
+} pool_t;
+
 struct nemoasr_batch {
+    pool_t pool;
+    int *fe_list;
     model_t *m;
     gpu_t *g;
     int S, latency_ms, right, chunk_frames, chunk_mel, cmax, left, conv_left, Lmax, cap_rows;
@@ -143,6 +165,9 @@ static void drop_graphs(nemoasr_batch_t *b) {
     }
 }
 
+static void pool_start(pool_t *p, struct nemoasr_batch *b);
+static void pool_stop(pool_t *p);
+
 /* bf16 matrices of the batched decoder: [Wx | Wh] per LSTM layer ([4P][2P]) and the joint output
  * weights padded to a multiple of 64 rows (padding rows zero; the argmax reads the first V) */
 static int build_decoder_weights(nemoasr_batch_t *b) {
@@ -182,13 +207,15 @@ static void stream_clear(nemoasr_batch_t *b, int s) {
     melfe_destroy(x->mel);
     int *tok = x->tok;
     size_t cap = x->cap_tok;
-    float *pend = x->pending;
-    size_t pcap = x->pending_cap;
+    float *pend = x->pending, *aq = x->aq;
+    size_t pcap = x->pending_cap, acap = x->aq_cap;
     memset(x, 0, sizeof *x);
     x->tok = tok;
     x->cap_tok = cap;
     x->pending = pend;
     x->pending_cap = pcap;
+    x->aq = aq;
+    x->aq_cap = acap;
     x->mel = melfe_create();
     x->pos = b->conv_left; /* rows [0, conv_left) of every layer stay zero: the empty conv history */
     x->last_token = b->m->cfg.blank_id;
@@ -318,12 +345,16 @@ nemoasr_batch_t *nemoasr_batch_open(const char *model_dir, const char *language,
     b->g_fill = malloc(S * sizeof(int));
     b->ord = malloc(S * sizeof(int));
     for (int s = 0; s < n_streams; ++s) stream_clear(b, s);
+    b->fe_list = malloc(S * sizeof(int));
+    pool_start(&b->pool, b);
     b->use_graphs = 1;
     return b;
 }
 
 void nemoasr_batch_close(nemoasr_batch_t *b) {
     if (!b) return;
+    pool_stop(&b->pool);
+    free(b->fe_list);
     drop_graphs(b);
     gpu_buf_t *bufs[] = { b->win, b->c0, b->c1, b->c2, b->c3, b->c4, b->flat, b->pre_out, b->h, b->tmp, b->lnb,
                           b->ff, b->att, b->y, b->ph, b->prompted, b->joint_enc, b->kv, b->din, b->etab, b->wcat[0],
@@ -337,6 +368,7 @@ void nemoasr_batch_close(nemoasr_batch_t *b) {
     if (b->st)
         for (int s = 0; s < b->S; ++s) {
             melfe_destroy(b->st[s].mel);
+            free(b->st[s].aq);
             free(b->st[s].pending);
             free(b->st[s].tok);
         }
@@ -376,31 +408,135 @@ static void queue_mel(bstream_t *x, const float *mel, size_t nframes) {
     x->pending_n += nframes;
 }
 
+/* log-mel of the audio queued for one stream (src/nemoasr.c:134-160 without resampling: audio
+ * is pushed at 16 kHz); a final push with no samples and an empty front end flushes nothing
+ * (src/nemoasr.c:146) */
+static void front_end(bstream_t *x) {
+    if (!x->aq_n && !x->fe_final) return;
+    if (!(x->fe_final && x->aq_n == 0 && melfe_samples(x->mel) == 0)) {
+        const float *frames;
+        size_t nf;
+        melfe_push(x->mel, x->aq, x->aq_n, x->fe_final, &frames, &nf);
+        queue_mel(x, frames, nf);
+    }
+    x->aq_n = 0;
+    if (x->fe_final) {
+        x->fe_final = 0;
+        x->final = 1;
+    }
+}
+
+static void *pool_main(void *arg) {
+    pool_t *p = arg;
+    unsigned seen = 0;
+    for (;;) {
+        pthread_mutex_lock(&p->mu);
+        while (!p->quit && p->gen == seen) pthread_cond_wait(&p->go, &p->mu);
+        if (p->quit) {
+            pthread_mutex_unlock(&p->mu);
+            return NULL;
+        }
+        seen = p->gen;
+        pthread_mutex_unlock(&p->mu);
+        for (;;) {
+            const int i = __atomic_fetch_add(&p->next, 1, __ATOMIC_RELAXED);
+            if (i >= p->count) break;
+            front_end(&p->b->st[p->list[i]]);
+        }
+        pthread_mutex_lock(&p->mu);
+        if (--p->busy == 0) pthread_cond_signal(&p->done);
+        pthread_mutex_unlock(&p->mu);
+    }
+}
+
+static void pool_start(pool_t *p, struct nemoasr_batch *b) {
+    long nc = sysconf(_SC_NPROCESSORS_ONLN);
+    const char *env = getenv("NEMOASR_THREADS");
+    if (env && atoi(env) > 0) nc = atoi(env);
+    int n = (int)(nc < 1 ? 1 : nc) - 1; /* the calling thread works too */
+    if (n > POOL_MAX) n = POOL_MAX;
+    if (n > b->S - 1) n = b->S - 1;
+    p->b = b;
+    pthread_mutex_init(&p->mu, NULL);
+    pthread_cond_init(&p->go, NULL);
+    pthread_cond_init(&p->done, NULL);
+    p->started = 1;
+    for (int i = 0; i < n; ++i) {
+        if (pthread_create(&p->th[i], NULL, pool_main, p)) break;
+        p->n++;
+    }
+}
+
+static void pool_stop(pool_t *p) {
+    if (!p->started) return;
+    pthread_mutex_lock(&p->mu);
+    p->quit = 1;
+    pthread_cond_broadcast(&p->go);
+    pthread_mutex_unlock(&p->mu);
+    for (int i = 0; i < p->n; ++i) pthread_join(p->th[i], NULL);
+    pthread_mutex_destroy(&p->mu);
+    pthread_cond_destroy(&p->go);
+    pthread_cond_destroy(&p->done);
+    p->started = 0;
+}
+
+/* front end of every stream with queued audio, spread over the pool */
+static void front_end_all(nemoasr_batch_t *b) {
+    int count = 0;
+    for (int s = 0; s < b->S; ++s)
+        if (b->st[s].aq_n || b->st[s].fe_final) b->fe_list[count++] = s;
+    if (!count) return;
+    pool_t *p = &b->pool;
+    if (count == 1 || p->n == 0) {
+        for (int i = 0; i < count; ++i) front_end(&b->st[b->fe_list[i]]);
+        return;
+    }
+    pthread_mutex_lock(&p->mu);
+    p->list = b->fe_list;
+    p->count = count;
+    p->next = 0;
+    p->busy = p->n;
+    p->gen++;
+    pthread_cond_broadcast(&p->go);
+    pthread_mutex_unlock(&p->mu);
+    for (;;) {
+        const int i = __atomic_fetch_add(&p->next, 1, __ATOMIC_RELAXED);
+        if (i >= count) break;
+        front_end(&b->st[b->fe_list[i]]);
+    }
+    pthread_mutex_lock(&p->mu);
+    while (p->busy > 0) pthread_cond_wait(&p->done, &p->mu);
+    pthread_mutex_unlock(&p->mu);
+}
+
 int nemoasr_batch_push_mel(nemoasr_batch_t *b, int stream, const float *mel, size_t nframes, int final, char *err,
                            size_t errlen) {
     if (errlen) err[0] = 0;
     if (check_stream(b, stream, err, errlen)) return -1;
     bstream_t *x = &b->st[stream];
-    if (x->final) { snprintf(err, errlen, "stream %d already ended", stream); return -1; }
+    if (x->ended) { snprintf(err, errlen, "stream %d already ended", stream); return -1; }
+    front_end(x); /* audio queued before these frames goes first */
     queue_mel(x, mel, nframes);
-    if (final) x->final = 1;
+    if (final) x->ended = x->final = 1;
     return 0;
 }
 
+/* audio is only queued here; its log-mel is computed by the next step, for all streams at once */
 int nemoasr_batch_push(nemoasr_batch_t *b, int stream, const float *samples, size_t n, int final, char *err,
                        size_t errlen) {
     if (errlen) err[0] = 0;
     if (check_stream(b, stream, err, errlen)) return -1;
     bstream_t *x = &b->st[stream];
-    if (x->final) { snprintf(err, errlen, "stream %d already ended", stream); return -1; }
-    /* a final push with no samples and an empty front end flushes nothing (src/nemoasr.c:146) */
-    if (!(final && n == 0 && melfe_samples(x->mel) == 0)) {
-        const float *frames;
-        size_t nf;
-        melfe_push(x->mel, samples, n, final, &frames, &nf);
-        queue_mel(x, frames, nf);
+    if (x->ended) { snprintf(err, errlen, "stream %d already ended", stream); return -1; }
+    if (n) {
+        if (x->aq_n + n > x->aq_cap) {
+            x->aq_cap = (x->aq_n + n) * 2;
+            x->aq = realloc(x->aq, x->aq_cap * sizeof(float));
+        }
+        memcpy(x->aq + x->aq_n, samples, n * sizeof(float));
+        x->aq_n += n;
     }
-    if (final) x->final = 1;
+    if (final) x->ended = x->fe_final = 1;
     return 0;
 }
 
@@ -541,6 +677,9 @@ static void compact_stream(nemoasr_batch_t *b, int s) {
 static int encoder_batch_step(nemoasr_batch_t *b, int *M_out, char *err, size_t errlen) {
     const size_t F = (size_t)b->m->cfg.feat_in;
     int consumed = 0, nact = 0;
+    const double tf = now_ms();
+    front_end_all(b);
+    b->stats.frontend_ms += now_ms() - tf;
     for (int s = 0; s < b->S; ++s) {
         bstream_t *x = &b->st[s];
         consumed += plan_stream(b, x);
@@ -644,6 +783,7 @@ static int encoder_batch_step(nemoasr_batch_t *b, int *M_out, char *err, size_t 
         x->cache_len = L < b->left ? L : b->left;
     }
     if (gpu_end(g, err, errlen)) return -1;
+    b->stats.encoder_gpu_ms += gpu_last_ms(g);
     *M_out = M;
     return consumed;
 }
@@ -889,4 +1029,14 @@ const float *nemoasr_batch_debug_joint_enc(const nemoasr_batch_t *b, int stream,
     if (!b->dj || stream < 0 || stream >= b->S) { *frames = 0; return NULL; }
     *frames = b->dj_n[stream];
     return b->dj[stream];
+}
+
+int nemoasr_batch_debug_time_kernel(nemoasr_batch_t *b, const char *kernel, int max_launches) {
+    return gpu_timing_set(b->g, kernel, max_launches);
+}
+
+int nemoasr_batch_debug_kernel_ms(nemoasr_batch_t *b, double *mean_ms, int *count, double *bytes, double *flops) {
+    const int rc = gpu_timing_collect(b->g, mean_ms, count, bytes);
+    if (flops) *flops = gpu_timing_last_flops(b->g);
+    return rc;
 }

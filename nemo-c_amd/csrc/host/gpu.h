@@ -71,8 +71,11 @@ uint32_t *gpu_splitk_counters(gpu_t *g, size_t n_needed);
  * bracketed by a pair of hipEvents; gpu_timing_collect returns the mean duration in ms. */
 int gpu_timing_set(gpu_t *g, const char *kernel, int max_launches);
 int gpu_timing_collect(gpu_t *g, double *mean_ms, int *count, double *bytes);
-/* Algorithmic HBM bytes of the next launch (recorded with its timing). */
+/* Algorithmic HBM bytes and flops of the next launch (recorded with its timing); the flops of
+ * the launches summed by the last gpu_timing_collect. */
 void gpu_next_bytes(gpu_t *g, double bytes);
+void gpu_next_flops(gpu_t *g, double flops);
+double gpu_timing_last_flops(const gpu_t *g);
 
 /* Device constant tables: the row indices 0..GPU_IOTA_N-1 and GPU_ZEROS_N zero floats (kernels
  * whose row map or bias is optional get these instead of NULL). */

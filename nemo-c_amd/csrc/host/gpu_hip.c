@@ -40,7 +40,7 @@ struct gpu {
     /* per-kernel timing */
     char timed[48];
     hipEvent_t *tev;
-    double *tbytes, next_bytes;
+    double *tbytes, next_bytes, *tflops, next_flops, last_flops;
     int tmax, tn;
 };
 struct gpu_buf {
@@ -235,11 +235,13 @@ int gpu_launch(gpu_t *g, const char *kernel, const void *args, size_t args_size,
         e = hipExtModuleLaunchKernel(f, gx * bx, gy * by, gz * bz, bx, by, bz, 0, g->stream, NULL, config,
                                      g->tev[2 * g->tn], g->tev[2 * g->tn + 1], 0);
         g->tbytes[g->tn] = g->next_bytes;
+        g->tflops[g->tn] = g->next_flops;
         g->tn++;
     } else {
         e = hipModuleLaunchKernel(f, gx, gy, gz, bx, by, bz, 0, g->stream, NULL, config);
     }
     g->next_bytes = 0.0;
+    g->next_flops = 0.0;
     g->launches++;
     if (e != hipSuccess) {
         char what[96];
@@ -328,8 +330,10 @@ int gpu_timing_set(gpu_t *g, const char *kernel, int max_launches) {
         for (int i = 0; i < 2 * g->tmax; ++i) hipEventDestroy(g->tev[i]);
         free(g->tev);
         free(g->tbytes);
+        free(g->tflops);
         g->tev = NULL;
         g->tbytes = NULL;
+        g->tflops = NULL;
     }
     g->tn = g->tmax = 0;
     g->timed[0] = 0;
@@ -337,6 +341,7 @@ int gpu_timing_set(gpu_t *g, const char *kernel, int max_launches) {
     if (max_launches > GPU_MAX_TIMED) max_launches = GPU_MAX_TIMED;
     g->tev = calloc((size_t)max_launches * 2, sizeof(hipEvent_t));
     g->tbytes = calloc((size_t)max_launches, sizeof(double));
+    g->tflops = calloc((size_t)max_launches, sizeof(double));
     for (int i = 0; i < 2 * max_launches; ++i)
         if (hipEventCreate(&g->tev[i]) != hipSuccess) return fail(g, "timing events", hipErrorOutOfMemory);
     g->tmax = max_launches;
@@ -345,6 +350,8 @@ int gpu_timing_set(gpu_t *g, const char *kernel, int max_launches) {
 }
 
 void gpu_next_bytes(gpu_t *g, double bytes) { g->next_bytes = bytes; }
+void gpu_next_flops(gpu_t *g, double flops) { g->next_flops = flops; }
+double gpu_timing_last_flops(const gpu_t *g) { return g->last_flops; }
 
 int gpu_timing_collect(gpu_t *g, double *mean_ms, int *count, double *bytes) {
     *mean_ms = 0.0;
@@ -353,11 +360,13 @@ int gpu_timing_collect(gpu_t *g, double *mean_ms, int *count, double *bytes) {
     if (!g->tev) return 0;
     hipStreamSynchronize(g->stream);
     double sum = 0.0;
+    g->last_flops = 0.0;
     for (int i = 0; i < g->tn; ++i) {
         float ms = 0.0f;
         if (hipEventElapsedTime(&ms, g->tev[2 * i], g->tev[2 * i + 1]) != hipSuccess) return fail(g, "timing", hipErrorInvalidValue);
         sum += ms;
         if (bytes) *bytes += g->tbytes[i];
+        g->last_flops += g->tflops[i];
     }
     *count = g->tn;
     *mean_ms = g->tn ? sum / g->tn : 0.0;

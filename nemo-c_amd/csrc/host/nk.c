@@ -131,6 +131,7 @@ static int gemm_core(gpu_t *g, const float *A, uint32_t lda, const uint16_t *W, 
     }
     /* algorithmic HBM bytes: every weight once, A once, C written (and read when accumulating) */
     gpu_next_bytes(g, 2.0 * N * K + 4.0 * M * K + 4.0 * M * nout * (accumulate ? 2 : 1) + (bias ? 4.0 * N : 0.0));
+    gpu_next_flops(g, 2.0 * M * N * K);
     char name[32];
     if (kind == K_GEMV) {
         /* the GEMV reads bias and the row map unconditionally */

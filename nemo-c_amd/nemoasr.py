@@ -54,6 +54,9 @@ API = {
     "nemoasr_batch_debug_use_graphs": (None, [_vp, C.c_int]),
     "nemoasr_batch_debug_set_dump": (None, [_vp, C.c_int]),
     "nemoasr_batch_debug_joint_enc": (_f32p, [_vp, C.c_int, C.POINTER(C.c_size_t)]),
+    "nemoasr_batch_debug_time_kernel": (C.c_int, [_vp, C.c_char_p, C.c_int]),
+    "nemoasr_batch_debug_kernel_ms": (C.c_int, [_vp, C.POINTER(C.c_double), C.POINTER(C.c_int),
+                                                C.POINTER(C.c_double), C.POINTER(C.c_double)]),
     # include/nemoasr_debug.h
     "nemoasr_debug_feed_mel": (C.c_int, [_vp, _f32p, C.c_size_t, C.c_int, C.c_char_p, C.c_size_t]),
     "nemoasr_debug_tokens": (_i32p, [_vp, C.POINTER(C.c_size_t)]),
@@ -391,8 +394,8 @@ class Batch:
     def stats(self) -> dict:
         class St(C.Structure):
             _fields_ = [("steps", C.c_size_t), ("chunks", C.c_size_t), ("rows", C.c_size_t),
-                        ("joint_steps", C.c_size_t), ("tokens", C.c_size_t), ("encoder_ms", C.c_double),
-                        ("decoder_ms", C.c_double)]
+                        ("joint_steps", C.c_size_t), ("tokens", C.c_size_t), ("frontend_ms", C.c_double),
+                        ("encoder_ms", C.c_double), ("decoder_ms", C.c_double), ("encoder_gpu_ms", C.c_double)]
         st = St()
         lib().nemoasr_batch_stats(self.h, C.byref(st))
         return {k: getattr(st, k) for k, _ in St._fields_}
@@ -414,6 +417,15 @@ class Batch:
         if not n.value:
             return np.zeros((0, joint_hidden), np.float32)
         return np.ctypeslib.as_array(p, shape=(n.value * joint_hidden,)).reshape(n.value, joint_hidden).copy()
+
+    def time_kernel(self, name: str | None, max_launches: int = 32768):
+        lib().nemoasr_batch_debug_time_kernel(self.h, name.encode() if name else None, max_launches)
+
+    def kernel_ms(self):
+        """(mean ms per launch, launches, summed algorithmic bytes, summed flops) of the timed kernel."""
+        ms, n, by, fl = C.c_double(), C.c_int(), C.c_double(), C.c_double()
+        lib().nemoasr_batch_debug_kernel_ms(self.h, C.byref(ms), C.byref(n), C.byref(by), C.byref(fl))
+        return ms.value, n.value, by.value, fl.value
 
     def close(self):
         if self.h:
