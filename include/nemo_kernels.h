@@ -74,7 +74,8 @@ int nk_gemm_ln(gpu_t *g, const float *A, uint32_t lda, const uint16_t *W, uint32
                int ln_mode, const float *g1, const float *b1, const float *g2, const float *b2, float *ln_out,
                float *tmp, float eps);
 /* Kernel selection: 0 automatic (by row count), 1 first-generation VALU GEMV (M <= 4),
- * 2 few-row MFMA (M <= 16), 3 many-row MFMA, 4 weight-streaming GEMV (M <= 4).
+ * 2 few-row MFMA (M <= 16), 3 many-row MFMA, 4 weight-streaming GEMV (M <= 4),
+ * 5 first-generation many-row MFMA (register-staged).
  * Returns the previous setting. */
 int nk_gemm_force(int kind);
 /* Name of the kernel nk_gemm would launch for these shapes (for profiling and tests). */

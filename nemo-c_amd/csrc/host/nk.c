@@ -20,7 +20,7 @@ static int bad(gpu_t *g, const char *what) { return gpu_fail(g, what); }
 
 static int aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 
-enum { K_FR = 2, K_MR = 3, K_GEMV = 4 };
+enum { K_FR = 2, K_MR = 3, K_GEMV = 4, K_MM_OLD = 5 };
 
 /* few-row MFMA kernel plan: W wavefronts of SPW K steps (32 wide) per workgroup, K split over KS
  * workgroups (KS > 1 only for accumulating GEMMs with no bias and no activation, whose partial
@@ -58,7 +58,7 @@ static int pick(uint32_t M, uint32_t K, int act) {
     const int gemv_ok = (M <= 2 && K <= 64 * 8 * 9) || (M <= 4 && K <= 64 * 8 * 2);
     if ((g_force == K_GEMV || g_force == 1) && gemv_ok) return K_GEMV;
     if (g_force == K_FR && fr_ok(M, K, act)) return K_FR;
-    if (g_force == K_MR && K % 32 == 0) return K_MR;
+    if ((g_force == K_MR || g_force == K_MM_OLD) && K % 32 == 0) return K_MR;
     if (gemv_ok) return K_GEMV;
     if (fr_ok(M, K, act)) return K_FR;
     return K_MR;
@@ -82,7 +82,7 @@ const char *nk_gemm_kernel_name(uint32_t M, uint32_t N, uint32_t K, int act) {
         snprintf(buf, sizeof buf, "gemv_r%u_n%u_k%u", M, nc, kch);
         return buf;
     case K_FR: return fr_name(fr_plan(act == NK_ACT_GLU ? N / 2 : N, K, act, 0, 1, 0), act, 0);
-    default: return "gemm_mm*";
+    default: return "gemm_m*";
     }
 }
 
@@ -92,6 +92,53 @@ typedef struct {
     float *out, *tmp;
     float eps;
 } ln_pro_t;
+
+/* Many-row GEMM on the direct-to-LDS MFMA kernels (kernels/nk_mx.hip).  Tile choice: the largest
+ * of 128x128, 64x128, 64x64 whose tile count reaches 160 workgroups; otherwise K is split (only for
+ * accumulating GEMMs with no bias and no activation, whose partial products are added atomically)
+ * or the smallest tile that divides the columns is used.  Returns 1 when no tile divides the
+ * output columns (the caller falls back), else the launch status. */
+static int launch_mx(gpu_t *g, NkGemmArgs *a, uint32_t M, uint32_t nout, uint32_t K, int glu, int splittable) {
+    static const struct { const char *name, *glu_name; uint32_t bm, bn; } cfg[] = {
+        { "gemm_mx128x128", "gemm_mx128x128_glu", 128, 128 },
+        { "gemm_mx64x128", "gemm_mx64x128_glu", 64, 128 },
+        { "gemm_mx64x64", "gemm_mx64x64_glu", 64, 64 },
+    };
+    const uint32_t S = K / 32;
+    int pick_i = -1, last_ok = -1;
+    uint32_t tiles = 0;
+    for (int i = 0; i < 3; ++i) {
+        const uint32_t cols = glu ? cfg[i].bn / 2 : cfg[i].bn;
+        if (nout % cols) continue;
+        const uint32_t t = ((M + cfg[i].bm - 1) / cfg[i].bm) * (nout / cols);
+        if (cfg[i].bm == 128 && M < 512) continue;
+        last_ok = i;
+        if (t >= 160) { pick_i = i; tiles = t; break; }
+    }
+    if (last_ok < 0) return 1;
+    uint32_t kz = 1;
+    if (pick_i < 0) {
+        /* too few tiles: split K of the 64x128 tile when allowed, else the smallest tile */
+        int i = last_ok;
+        if (splittable) {
+            for (int j = 0; j < 3; ++j)
+                if (cfg[j].bm == 64 && cfg[j].bn == 128 && nout % (glu ? 64 : 128) == 0) i = j;
+        }
+        const uint32_t cols = glu ? cfg[i].bn / 2 : cfg[i].bn;
+        tiles = ((M + cfg[i].bm - 1) / cfg[i].bm) * (nout / cols);
+        if (splittable) {
+            kz = (224 + tiles - 1) / tiles;
+            if (kz > 8) kz = 8;
+            if (kz > S / 2) kz = S / 2 > 0 ? S / 2 : 1;
+        }
+        pick_i = i;
+    }
+    const uint32_t tm = (M + cfg[pick_i].bm - 1) / cfg[pick_i].bm;
+    a->splits = kz;
+    a->group_m = tm <= 8 ? tm : (tm + 3) / 4;
+    const uint32_t total = tiles * kz, per = (total + 7) / 8;
+    return gpu_launch(g, glu ? cfg[pick_i].glu_name : cfg[pick_i].name, a, sizeof *a, 8 * per, 1, 1, 256, 1, 1);
+}
 
 /* The GEMM with an optional LayerNorm prologue on A.  The weight-streaming GEMV applies it in
  * registers; the MFMA kernels get it from separate LayerNorm launches into ln.tmp. */
@@ -155,9 +202,13 @@ static int gemm_core(gpu_t *g, const float *A, uint32_t lda, const uint16_t *W, 
         const uint32_t tiles = (nout + 15) / 16;
         return gpu_launch(g, fr_name(p, act, ln_fused), &a, sizeof a, tiles, p.KS, 1, 64 * p.W, 1, 1);
     }
-    /* many rows: 128 x 128 tiles when they fill the GPU, else 64 x 64 (K split over up to four
-     * workgroups for accumulating GEMMs with no bias and no activation) */
     const int glu = act == NK_ACT_GLU;
+    if (g_force != K_MM_OLD) {
+        const int rc = launch_mx(g, &a, M, nout, K, glu, accumulate && !bias && act == NK_ACT_NONE);
+        if (rc <= 0) return rc;
+    }
+    /* many rows, first-generation kernels: 128 x 128 tiles when they fill the GPU, else 64 x 64
+     * (K split over up to four workgroups for accumulating GEMMs with no bias and no activation) */
     const uint32_t S = K / 32;
     if (nout % (glu ? 64 : 128) == 0) {
         const uint32_t t128 = ((M + 127) / 128) * (nout / (glu ? 64 : 128));

@@ -46,7 +46,7 @@ typedef struct {
     float *ws;      /* split-K partials (few-row MFMA kernel)          */
     u32 *counters;  /* split-K arrival counters, self-resetting         */
     u32 M, N, K, lda, ldw, ldc;
-    u32 act, accumulate, splits, pad0;
+    u32 act, accumulate, splits, group_m; /* group_m: row tiles per group of the many-row tile order */
     float alpha;
     u32 pad1;
     /* LayerNorm prologue on A (weight-streaming GEMV): ln_mode 0 none, 1 LN(g1,b1),

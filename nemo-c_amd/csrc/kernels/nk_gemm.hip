@@ -49,22 +49,6 @@ __device__ __forceinline__ void ln_wave4(floatx4 (&v)[4], const floatx4 (&g)[4],
         for (int e = 0; e < 4; ++e) v[j][e] = (v[j][e] - mean) * inv * g[j][e] + b[j][e];
 }
 
-/* 8 f32 -> bf16 hi (round to nearest even, v_cvt_pk_bf16_f32) and bf16 lo = bf16(x - hi), packed
- * in pairs (element 2p in the low half of word p). */
-__device__ __forceinline__ void split8(const float (&x)[8], uint4 &hi, uint4 &lo) {
-    u32 h[4], l[4];
-#pragma unroll
-    for (int p = 0; p < 4; ++p) {
-        const floatx2 v = { x[2 * p], x[2 * p + 1] };
-        const u32 hb = __builtin_bit_cast(u32, __builtin_convertvector(v, bf16x2));
-        const floatx2 hv = { __uint_as_float(hb << 16), __uint_as_float(hb & 0xffff0000u) };
-        h[p] = hb;
-        l[p] = __builtin_bit_cast(u32, __builtin_convertvector(v - hv, bf16x2));
-    }
-    hi = make_uint4(h[0], h[1], h[2], h[3]);
-    lo = make_uint4(l[0], l[1], l[2], l[3]);
-}
-
 /* grid = (ceil(nout/16), KS): workgroup (tile, ks) takes the K steps [ks*S/KS, (ks+1)*S/KS) of the
  * S = K/32 steps, wavefront w the SPW steps from w*SPW within them.  With KS > 1 the partial
  * products are added into C atomically (the host uses this only for accumulating GEMMs with no

@@ -1,0 +1,234 @@
+/* Many-row bf16-weight GEMM for gfx950, fed by direct global -> LDS loads (M > 16: the batched
+ * multi-stream encoder and decoder): C[crow(m)][n] (= or +=) alpha * act(A W^T + b); GLU pairs
+ * weight rows n and n + N/2.
+ *
+ * Workgroup tile BM x BN, 4 wavefronts as WGM (along M) x 4/WGM (along N); each wavefront owns a
+ * (BM/WGM) x (BN*WGM/4) block of 16x16 tiles of v_mfma_f32_16x16x32_bf16.
+ *
+ * Operand staging: a ring of NS LDS stages, each holding one K step (32) of A (f32, BM x 128 B)
+ * and W (bf16, BN x 64 B).  Stages are filled by global_load_lds_dwordx4 (16 bytes per lane
+ * straight into LDS, no registers), issued NS-1 steps ahead of their use, so a wavefront only waits
+ * for a stage's loads right before the barrier that publishes it.  A DMA instruction writes 64
+ * consecutive 16-byte LDS granules in lane order; the global address each lane reads is chosen so
+ * that granule g of row r holds K-granule (g ^ swizzle(r)), which makes the 16-row fragment reads
+ * (ds_read_b128) hit distinct banks.
+ *
+ * A is f32 in memory and in LDS; each fragment (8 consecutive K of one row per lane) is split in
+ * registers into bf16 hi = RNE(a) and lo = RNE(a - hi) (v_cvt_pk_bf16_f32), and every K step
+ * issues the hi and the lo product: 16 significant bits of A against exact bf16 weights, f32
+ * accumulation.  The reference's many-row path multiplies f32 A by bf16 W in f32
+ * (src/kernels.metal:120-208, simdgroup_float8x8).
+ *
+ * Tile order: the grid is 8 x (tiles per XCD); workgroup b runs on XCD b % 8 and takes tile
+ * (b % 8) * per + b / 8 of an order that walks groups of group_m row tiles across all column tiles
+ * (row tile fastest), so the workgroups of one XCD share weight columns and a few row panels in
+ * that XCD's L2.  grid tiles past the end exit at once.  splits > 1 splits K; partial products
+ * are then added into C atomically (the host uses it only for accumulating GEMMs with no bias and
+ * no activation). */
+#include "nk_common.h"
+
+typedef __attribute__((address_space(3))) char lds_char_t;
+
+/* 16 bytes per lane from global memory straight into LDS: lane i writes LDS bytes
+ * [lds + 16 i, +16) of the wavefront-uniform base `lds`.  Issued as inline assembly, so the
+ * compiler does not track these loads: the kernel waits for them itself (wait_vm_lgkm) before the
+ * barrier that publishes a stage, and drains them before its epilogue. */
+__device__ __forceinline__ void dma16(const void *g, lds_char_t *lds) {
+    const u32 base = __builtin_amdgcn_readfirstlane((u32)(size_t)lds);
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(base) : "memory");
+}
+
+/* s_waitcnt vmcnt(N) lgkmcnt(0) */
+template <int N> __device__ __forceinline__ void wait_vm_lgkm() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(N) : "memory");
+}
+
+__device__ __forceinline__ void barrier_mem() { asm volatile("s_barrier" ::: "memory"); }
+
+template <int BM, int BN, int WGM, int NS, bool GLU>
+__device__ __forceinline__ void mx_impl(const NkGemmArgs &a, lds_char_t *const (&ring)[NS]) {
+    constexpr int WGN = 4 / WGM;
+    constexpr int WTM = BM / WGM, WTN = BN / WGN;
+    constexpr int TI = WTM / 16, TJ = WTN / 16;
+    constexpr int A_BYTES = BM * 128, STAGE = A_BYTES + BN * 64;
+    constexpr int AI = BM * 8 / 256; /* A granules per thread per stage */
+    constexpr int BI = BN * 4 / 256; /* W granules per thread per stage */
+    static_assert(AI >= 1 && BI >= 1 && TI >= 1 && TJ >= (GLU ? 2 : 1), "tile shape");
+    const u32 tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const u32 wm = wave / WGN, wn = wave % WGN;
+    const u32 M = a.M;
+    const u32 nout = GLU ? a.N / 2 : a.N;
+    const u32 TMt = (M + BM - 1) / BM, TNt = nout / (GLU ? BN / 2 : BN), KZ = a.splits;
+
+    /* tile of this workgroup */
+    const u32 per = gridDim.x / 8;
+    const u32 t = (blockIdx.x % 8) * per + blockIdx.x / 8;
+    if (t >= TMt * TNt * KZ) return;
+    const u32 kz = t / (TMt * TNt), tt = t % (TMt * TNt);
+    const u32 G = a.group_m, gsz = G * TNt, grp = tt / gsz, first = grp * G;
+    const u32 gh = min(TMt - first, G), within = tt % gsz;
+    const u32 tm = first + within % gh, tn = within / gh;
+    const u32 m0 = tm * BM;
+    const u32 c0 = tn * (GLU ? BN / 2 : BN); /* first output column */
+    const u32 S = a.K >> 5;
+    const u32 s_begin = (u32)(((u64)S * kz) / KZ), s_end = (u32)(((u64)S * (kz + 1)) / KZ);
+    const u32 nst = s_end - s_begin;
+
+    /* DMA sources: granule p of a stage region is written by lane p % 64 of instruction p / 64
+     * (instruction j of wavefront w covers p in [(4j + w) * 64, +64)) */
+    const float *asrc[AI];
+#pragma unroll
+    for (int j = 0; j < AI; ++j) {
+        const u32 p = (4 * j + wave) * 64 + lane, r = p >> 3, kg = (p & 7) ^ (r & 7);
+        asrc[j] = a.A + (u64)min(m0 + r, M - 1) * a.lda + 4 * kg + (u64)s_begin * 32;
+    }
+    const u16 *bsrc[BI];
+#pragma unroll
+    for (int j = 0; j < BI; ++j) {
+        const u32 p = (4 * j + wave) * 64 + lane, n = p >> 2, kg = (p & 3) ^ ((n >> 1) & 3);
+        u32 col;
+        if (GLU) col = n < BN / 2 ? c0 + n : a.N / 2 + c0 + (n - BN / 2);
+        else col = c0 + n;
+        bsrc[j] = a.W + (u64)col * a.ldw + 8 * kg + (u64)s_begin * 32;
+    }
+    auto issue = [&](u32 q, int slot) { /* loads of local step q into ring slot `slot` */
+        lds_char_t *st = ring[slot];
+#pragma unroll
+        for (int j = 0; j < AI; ++j) dma16(asrc[j] + (u64)q * 32, st + (4 * j + wave) * 1024);
+#pragma unroll
+        for (int j = 0; j < BI; ++j) dma16(bsrc[j] + (u64)q * 32, st + A_BYTES + (4 * j + wave) * 1024);
+    };
+
+    /* fragment addresses inside a stage */
+    const u32 fr = lane & 15, fg = lane >> 4;
+    u32 aoff[TI][2];
+#pragma unroll
+    for (int i = 0; i < TI; ++i) {
+        const u32 r = wm * WTM + 16 * i + fr;
+        aoff[i][0] = (r * 8 + ((2 * fg) ^ (r & 7))) * 16;
+        aoff[i][1] = (r * 8 + ((2 * fg + 1) ^ (r & 7))) * 16;
+    }
+    u32 boff[TJ];
+#pragma unroll
+    for (int j = 0; j < TJ; ++j) {
+        u32 n;
+        if (GLU) n = j < TJ / 2 ? wn * (WTN / 2) + 16 * j : BN / 2 + wn * (WTN / 2) + 16 * (j - TJ / 2);
+        else n = wn * WTN + 16 * j;
+        n += fr;
+        boff[j] = A_BYTES + (n * 4 + (fg ^ ((n >> 1) & 3))) * 16;
+    }
+
+    floatx4 acc[TI][TJ];
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) acc[i][j] = (floatx4){ 0.f, 0.f, 0.f, 0.f };
+
+    /* Every step issues the loads of the step NS-1 ahead, clamped to the last one (the extra
+     * copies land in slots nobody reads), so the loads in flight behind step q are always (NS-2)
+     * steps' worth.  The loop is unrolled by NS so every ring slot address is a constant. */
+#pragma unroll
+    for (int u = 0; u < NS - 1; ++u) issue(min((u32)u, nst - 1), u);
+    for (u32 q0 = 0; q0 < nst; q0 += NS) {
+#pragma unroll
+    for (int u = 0; u < NS; ++u) {
+        const u32 q = q0 + u;
+        if (q >= nst) break;
+        /* this wavefront's loads of step q are done, then the barrier publishes every wavefront's
+         * part and retires all reads of the slot the next issue overwrites */
+        wait_vm_lgkm<(NS - 2) * (AI + BI)>();
+        barrier_mem();
+        issue(min(q + NS - 1, nst - 1), (u + NS - 1) % NS);
+        const lds_char_t *st = ring[u];
+        uint4 fb[TJ];
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) fb[j] = *(const __attribute__((address_space(3))) uint4 *)(st + boff[j]);
+        uint4 fh[TI], fl[TI];
+#pragma unroll
+        for (int i = 0; i < TI; ++i) {
+            const floatx4 x0 = *(const __attribute__((address_space(3))) floatx4 *)(st + aoff[i][0]);
+            const floatx4 x1 = *(const __attribute__((address_space(3))) floatx4 *)(st + aoff[i][1]);
+            const float x[8] = { x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3] };
+            split8(x, fh[i], fl[i]);
+        }
+#pragma unroll
+        for (int i = 0; i < TI; ++i)
+#pragma unroll
+            for (int j = 0; j < TJ; ++j) acc[i][j] = mfma_bf16(fh[i], fb[j], acc[i][j]);
+#pragma unroll
+        for (int i = 0; i < TI; ++i)
+#pragma unroll
+            for (int j = 0; j < TJ; ++j) acc[i][j] = mfma_bf16(fl[i], fb[j], acc[i][j]);
+    }
+    }
+
+    wait_vm_lgkm<0>(); /* no load into LDS may land after the workgroup ends */
+
+    /* epilogue: lane l holds rows 16 i + 4 (l/16) + e, column 16 j + l%16 of each tile; every
+     * operand (row map, bias, the C values to accumulate into) is loaded before the first store */
+    constexpr int TO = GLU ? TJ / 2 : TJ;
+    u32 orow[TI][4];
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const u32 r = min(m0 + wm * WTM + 16 * i + 4 * fg + e, M - 1);
+            orow[i][e] = a.crow ? (u32)a.crow[r] : r;
+        }
+    u32 ocol[TO];
+    float ba[TO], bb[TO];
+#pragma unroll
+    for (int j = 0; j < TO; ++j) {
+        ocol[j] = c0 + (GLU ? wn * (WTN / 2) : wn * WTN) + 16 * j + fr;
+        ba[j] = a.bias ? a.bias[ocol[j]] : 0.0f;
+        bb[j] = (GLU && a.bias) ? a.bias[ocol[j] + a.N / 2] : 0.0f;
+    }
+    const bool rmw = a.accumulate && KZ == 1;
+    float cv[TO][TI][4];
+#pragma unroll
+    for (int j = 0; j < TO; ++j)
+#pragma unroll
+        for (int i = 0; i < TI; ++i)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) cv[j][i][e] = rmw ? a.C[(u64)orow[i][e] * a.ldc + ocol[j]] : 0.0f;
+#pragma unroll
+    for (int j = 0; j < TO; ++j) {
+#pragma unroll
+        for (int i = 0; i < TI; ++i)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                if (m0 + wm * WTM + 16 * i + 4 * fg + e >= M) continue;
+                float *dst = a.C + (u64)orow[i][e] * a.ldc + ocol[j];
+                if (KZ > 1) {
+                    atomicAdd(dst, acc[i][j][e] * a.alpha);
+                    continue;
+                }
+                float v;
+                if constexpr (GLU) {
+                    v = (acc[i][j][e] + ba[j]) * sigmoid_f(acc[i][j + TJ / 2][e] + bb[j]) * a.alpha;
+                } else {
+                    v = acc[i][j][e] + ba[j];
+                    if (a.act == NK_ACT_SILU) v = silu_f(v);
+                    else if (a.act == NK_ACT_RELU) v = fmaxf(v, 0.0f);
+                    v *= a.alpha;
+                }
+                *dst = rmw ? cv[j][i][e] + v : v;
+            }
+    }
+}
+
+#define GEMM_MX(NAME, BM, BN, WGM, GLU)                                                                   \
+    extern "C" __global__ __launch_bounds__(256) void NAME(const NkGemmArgs a) {                          \
+        __shared__ uint4 r0[(BM * 128 + BN * 64) / 16], r1[(BM * 128 + BN * 64) / 16];                    \
+        __shared__ uint4 r2[(BM * 128 + BN * 64) / 16], r3[(BM * 128 + BN * 64) / 16];                    \
+        lds_char_t *const ring[4] = { (lds_char_t *)r0, (lds_char_t *)r1, (lds_char_t *)r2,              \
+                                      (lds_char_t *)r3 };                                                 \
+        mx_impl<BM, BN, WGM, 4, GLU>(a, ring);                                                            \
+    }
+GEMM_MX(gemm_mx128x128, 128, 128, 2, false)
+GEMM_MX(gemm_mx64x128, 64, 128, 2, false)
+GEMM_MX(gemm_mx64x64, 64, 64, 2, false)
+GEMM_MX(gemm_mx128x128_glu, 128, 128, 2, true)
+GEMM_MX(gemm_mx64x128_glu, 64, 128, 2, true)
+GEMM_MX(gemm_mx64x64_glu, 64, 64, 2, true)

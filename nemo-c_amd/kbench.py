@@ -189,6 +189,7 @@ def main():
     ap.add_argument("--json", default=None)
     ap.add_argument("--no-gemm", action="store_true")
     ap.add_argument("--batch-rows", default="", help="many-row (batched streams) GEMM sizes, e.g. 448,3584")
+    ap.add_argument("--batch-force", default="0", help="kernel selections to compare (nk_gemm_force), e.g. 0,5")
     a = ap.parse_args()
     gpu = nemoasr.Gpu()
     print(f"device: {gpu.name}", flush=True)
@@ -210,7 +211,8 @@ def main():
             print(f"M={M:2d} {label:14s} {name:22s} graph {gus:7.2f} us ({rec['gbs_graph']:7.1f} GB/s)  "
                   f"kernel {kus:7.2f} us ({rec['gbs_kernel']:7.1f} GB/s)", flush=True)
     out["batched"] = []
-    for M in [int(x) for x in a.batch_rows.split(",") if x]:
+    for M, force in [(int(x), int(f)) for x in a.batch_rows.split(",") if x for f in a.batch_force.split(",")]:
+        nemoasr.lib().nk_gemm_force(force)
         tot_us, tot_fl = 0.0, 0.0
         for (label, N, K, act, acc, alpha, ln, ldw, hb) in SHAPES:
             if label == "lstm":
@@ -223,13 +225,15 @@ def main():
             tot_fl += fl * cnt_chunk
             rec = {"M": M, "shape": label, "N": N, "K": K, "kernel": name, "graph_us": round(gus, 3),
                    "tflops": round(fl / (gus * 1e-6) / 1e12, 1), "mfma_frac": round(fl / (gus * 1e-6) / 2.5e15, 4)}
+            rec["force"] = force
             out["batched"].append(rec)
-            print(f"M={M:5d} {label:14s} {name:18s} graph {gus:8.2f} us  {rec['tflops']:7.1f} TFLOP/s "
+            print(f"M={M:5d} f{force} {label:14s} {name:18s} graph {gus:8.2f} us  {rec['tflops']:7.1f} TFLOP/s "
                   f"({rec['mfma_frac']:.3f} of 2.5 PF bf16; issued MFMA work is 2x: A = hi + lo)", flush=True)
-        print(f"M={M:5d} chunk GEMMs (24 layers + prompt + joint.enc, no LN launches): {tot_us / 1e3:.3f} ms, "
+        nemoasr.lib().nk_gemm_force(0)
+        print(f"M={M:5d} f{force} chunk GEMMs (24 layers + prompt + joint.enc, no LN launches): {tot_us / 1e3:.3f} ms, "
               f"{tot_fl / (tot_us * 1e-6) / 1e12:.1f} TFLOP/s = {tot_fl / (tot_us * 1e-6) / 2.5e15:.3f} of peak", flush=True)
     out["rows"] = []
-    for c in [int(x) for x in a.rows.split(",")]:
+    for c in [int(x) for x in a.rows.split(",") if int(x) <= 16]:
         for desc in (0, 1):
             us = bench_attention(gpu, c, 56, desc, 24, a.reps)
             out["rows"].append({"kernel": "attention_rel", "c": c, "cache": 56, "desc": desc, "graph_us": round(us, 3)})

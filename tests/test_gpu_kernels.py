@@ -97,12 +97,16 @@ def test_gemm_many_rows(gpu, M, N, K, act):
 
 
 # batched multi-stream shapes (64 streams x 7 rows, 256 x 14) through the many-row MFMA kernels:
-# 128x128 and 64x64 tiles, GLU pairing, K split over workgroups with atomic accumulation, row maps
+# each tile shape (128x128, 64x128, 64x64, plain and GLU), K split over workgroups with atomic
+# accumulation, row counts that are not tile multiples, K of one or two steps, row maps
 @pytest.mark.parametrize("M,N,K,act,acc,bias", [
     (448, 4096, 1024, 1, 0, False), (448, 1024, 4096, 0, 1, False), (448, 3072, 1024, 0, 0, False),
     (448, 2048, 1024, 3, 0, False), (448, 1024, 1024, 0, 1, False), (448, 640, 1024, 0, 0, True),
     (3584, 4096, 1024, 1, 0, False), (3584, 2048, 1024, 3, 0, False), (3584, 1024, 4096, 0, 1, False),
-    (100, 2048, 1024, 2, 0, True), (37, 1024, 2048, 0, 0, True)])
+    (100, 2048, 1024, 2, 0, True), (37, 1024, 2048, 0, 0, True),
+    (445, 4096, 1024, 1, 0, False), (1000, 2048, 1024, 3, 0, False), (3584, 1024, 1024, 0, 1, False),
+    (20, 3072, 1024, 0, 0, False), (448, 2560, 1280, 0, 0, True), (1024, 1088, 640, 0, 0, True),
+    (64, 256, 32, 2, 0, True), (96, 128, 64, 0, 1, False)])
 def test_gemm_batched_rows(gpu, M, N, K, act, acc, bias):
     rng = np.random.default_rng([M, N, K, act])
     W = _w(rng, N, K)
@@ -127,7 +131,7 @@ def test_gemm_batched_row_map(gpu):
     assert rel_err(got[rows], ref) < GEMM_TOL
 
 
-@pytest.mark.parametrize("kind,M", [(4, 1), (4, 4), (2, 1), (2, 4), (2, 16), (3, 5), (3, 16)])
+@pytest.mark.parametrize("kind,M", [(4, 1), (4, 4), (2, 1), (2, 4), (2, 16), (3, 5), (3, 16), (3, 100), (5, 16), (5, 100)])
 def test_gemm_variants_agree(gpu, kind, M):
     """Every kernel the policy can pick computes the same GEMM (the reference's kbench.c:196-230
     cross-check, with a threshold)."""
