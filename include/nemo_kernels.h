@@ -104,6 +104,11 @@ int nk_dwconv_ln_silu_desc(gpu_t *g, const float *din_base, const int *desc, con
 int nk_attention_rel_rows(gpu_t *g, const float *kv, uint32_t ld, const int *rows, uint32_t M, const float *P,
                           const float *bias_u, const float *bias_v, float *O, uint32_t Lmax, uint32_t H, uint32_t dh,
                           uint32_t D, float scale);
+/* Whole chunks of batched streams: chunks[4k..4k+3] = { cache row of chunk k's first row, its
+ * first output row, its rows c (<= 16), its stream's cached rows } with cached + c <= 80. */
+int nk_attention_rel_chunks(gpu_t *g, const float *kv, uint32_t ld, const int *chunks, uint32_t nchunks, const float *P,
+                            const float *bias_u, const float *bias_v, float *O, uint32_t Lmax, uint32_t H, uint32_t dh,
+                            uint32_t D, float scale);
 int nk_dwconv_ln_silu_rows(gpu_t *g, const float *din_base, const int *rows, uint32_t M, const float *W,
                            const float *gamma, const float *beta, float *Y, uint32_t D, uint32_t taps, float eps);
 int nk_conv2d_c1_s2_relu(gpu_t *g, const float *X, const float *W, const float *bias, float *Y, uint32_t T,

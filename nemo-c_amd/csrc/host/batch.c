@@ -112,7 +112,7 @@ struct nemoasr_batch {
     int *stage_tab;
     bgraph_t gr[MAX_BGRAPHS];
     unsigned long long tick;
-    int use_graphs;
+    int use_graphs, chunk_attn;
     /* decoder */
     int P, J, V, Vp;
     gpu_buf_t *wcat[2], *wout, *bout, *hc, *lin, *gates, *hout, *hout2, *pred, *jin, *logits, *amax, *dtab;
@@ -308,9 +308,9 @@ nemoasr_batch_t *nemoasr_batch_open(const char *model_dir, const char *language,
     b->din_lstride = S * (size_t)b->cap_rows * D;
     b->kv = gpu_buf_alloc(g, (size_t)c->n_layers * b->kv_lstride * fs);
     b->din = gpu_buf_alloc(g, (size_t)c->n_layers * b->din_lstride * fs);
-    b->etab = gpu_buf_alloc(g, 6 * Mm * sizeof(int));
+    b->etab = gpu_buf_alloc(g, (6 * Mm + 4 * S) * sizeof(int));
     b->stage_win = gpu_host_alloc(g, S * (size_t)b->nwin_max * F * fs);
-    b->stage_tab = gpu_host_alloc(g, 6 * Mm * sizeof(int));
+    b->stage_tab = gpu_host_alloc(g, (6 * Mm + 4 * S) * sizeof(int));
     b->wtmp = malloc((size_t)b->nwin_max * F * fs);
     const size_t P = (size_t)b->P, J = (size_t)b->J, R = S * DEC_WIN;
     b->hc = gpu_buf_alloc(g, S * 8 * P * fs);
@@ -348,6 +348,8 @@ nemoasr_batch_t *nemoasr_batch_open(const char *model_dir, const char *language,
     b->fe_list = malloc(S * sizeof(int));
     pool_start(&b->pool, b);
     b->use_graphs = 1;
+    /* whole-chunk attention when every window fits its LDS tables */
+    b->chunk_attn = b->Lmax <= NK_ATTC_MAX_L && b->cmax <= NK_ATTC_MAX_C;
     return b;
 }
 
@@ -601,7 +603,8 @@ static void launch_pre_encode(nemoasr_batch_t *b, const float *win, int nwin, in
 /* conformer blocks + prompt + joint projection on the M rows in h (src/encoder.c:144-197).
  * The order of operations and the LayerNorm placement are those of the single-stream encoder;
  * crow maps every row to its stream's cache row, rows is the attention/conv row table. */
-static void launch_blocks(nemoasr_batch_t *b, uint32_t M, const int *crow, const int *rows) {
+static void launch_blocks(nemoasr_batch_t *b, uint32_t M, const int *crow, const int *rows, const int *chunks,
+                          uint32_t nchunks) {
     model_t *m = b->m;
     gpu_t *g = b->g;
     const model_cfg_t *cf = &m->cfg;
@@ -629,8 +632,12 @@ static void launch_blocks(nemoasr_batch_t *b, uint32_t M, const int *crow, const
         nk_gemm(g, ff, FF, W->ff1_w2, FF, NULL, res, D, M, D, FF, NK_ACT_NONE, 1, 0.5f);
         nk_gemm_ln(g, res, D, W->wqkv, D, NULL, kv, 3 * D, crow, M, 3 * D, D, NK_ACT_NONE, 0, 1.0f, 1, W->ln_att_g,
                    W->ln_att_b, NULL, NULL, NULL, lnbuf, eps);
-        nk_attention_rel_rows(g, kv, 3 * D, rows, M, W->ptab, W->bias_u, W->bias_v, att, (uint32_t)b->Lmax, H, dh, D,
-                              scale);
+        if (b->chunk_attn)
+            nk_attention_rel_chunks(g, kv, 3 * D, chunks, nchunks, W->ptab, W->bias_u, W->bias_v, att, (uint32_t)b->Lmax, H,
+                                    dh, D, scale);
+        else
+            nk_attention_rel_rows(g, kv, 3 * D, rows, M, W->ptab, W->bias_u, W->bias_v, att, (uint32_t)b->Lmax, H, dh, D,
+                                  scale);
         nk_gemm(g, att, D, W->wo, D, NULL, res, D, M, D, D, NK_ACT_NONE, 1, 1.0f);
         nk_gemm_ln(g, res, D, W->pw1, D, NULL, din, D, crow, M, 2 * D, D, NK_ACT_GLU, 0, 1.0f, 1, W->ln_conv_g,
                    W->ln_conv_b, NULL, NULL, NULL, lnbuf, eps);
@@ -649,7 +656,7 @@ static void launch_blocks(nemoasr_batch_t *b, uint32_t M, const int *crow, const
     nk_gemm(g, pr, D, m->joint_enc_w, D, m->joint_enc_b, gpu_buf_dptr(b->joint_enc), JH, M, JH, D, NK_ACT_NONE, 0, 1.0f);
 }
 
-static void launch_encoder(nemoasr_batch_t *b, int M) {
+static void launch_encoder(nemoasr_batch_t *b, int M, int nact) {
     const size_t F = (size_t)b->m->cfg.feat_in, D = (size_t)b->m->cfg.d_model;
     const int *tab = gpu_buf_dptr(b->etab);
     for (int k = 0; k < b->ng; ++k)
@@ -657,7 +664,7 @@ static void launch_encoder(nemoasr_batch_t *b, int M) {
                           (float *)gpu_buf_dptr(b->pre_out) + (size_t)b->g_poff[k] * D);
     nk_gather_rows(b->g, gpu_buf_dptr(b->pre_out), (uint32_t)D, tab + 5 * M, gpu_buf_dptr(b->h), (uint32_t)D, (uint32_t)M,
                    (uint32_t)D);
-    launch_blocks(b, (uint32_t)M, tab, tab + M);
+    launch_blocks(b, (uint32_t)M, tab, tab + M, tab + 6 * M, (uint32_t)nact);
 }
 
 /* move a stream's live cache rows to the front of its region, every layer (src/encoder.c:199-211) */
@@ -744,8 +751,8 @@ static int encoder_batch_step(nemoasr_batch_t *b, int *M_out, char *err, size_t 
         gpu_end(g, NULL, 0);
         return -1;
     }
-    /* tables: crow[M], rows[4M], gather map[M] */
-    int *rows = crow + M, *gmap = crow + 5 * M;
+    /* tables: crow[M], rows[4M], gather map[M], chunks[4 nact] */
+    int *rows = crow + M, *gmap = crow + 5 * M, *chunks = crow + 6 * M;
     for (int i = 0; i < nact; ++i) {
         const int s = b->order[i];
         const bstream_t *x = &b->st[s];
@@ -760,21 +767,25 @@ static int encoder_batch_step(nemoasr_batch_t *b, int *M_out, char *err, size_t 
             rows[4 * m + 3] = x->cache_len;
             gmap[m] = b->g_poff[k] + j * T3 + x->lo + r;
         }
+        chunks[4 * i] = s * b->cap_rows + x->pos;
+        chunks[4 * i + 1] = x->row0;
+        chunks[4 * i + 2] = x->c;
+        chunks[4 * i + 3] = x->cache_len;
     }
     gpu_upload_async(g, gpu_buf_dptr(b->win), b->stage_win, (size_t)woff * F * sizeof(float));
-    gpu_upload_async(g, gpu_buf_dptr(b->etab), crow, (size_t)6 * M * sizeof(int));
+    gpu_upload_async(g, gpu_buf_dptr(b->etab), crow, (size_t)(6 * M + 4 * nact) * sizeof(int));
     bgraph_t *gs = b->use_graphs ? bgraph_slot(b, M) : NULL;
     if (gs) {
         gs->last_use = ++b->tick;
         if (!gs->graph && gs->seen >= 1 && !gpu_capture_begin(g)) {
-            launch_encoder(b, M);
+            launch_encoder(b, M, nact);
             gs->graph = gpu_capture_end(g);
         }
         gs->seen++;
         if (gs->graph) gpu_graph_launch(g, gs->graph);
-        else launch_encoder(b, M);
+        else launch_encoder(b, M, nact);
     } else {
-        launch_encoder(b, M);
+        launch_encoder(b, M, nact);
     }
     for (int i = 0; i < nact; ++i) {
         bstream_t *x = &b->st[b->order[i]];

@@ -314,6 +314,16 @@ int nk_attention_rel_rows(gpu_t *g, const float *kv, uint32_t ld, const int *row
     return gpu_launch(g, "attention_rel", &a, sizeof a, H, M, 1, 512, 1, 1);
 }
 
+int nk_attention_rel_chunks(gpu_t *g, const float *kv, uint32_t ld, const int *chunks, uint32_t nchunks, const float *P,
+                            const float *bias_u, const float *bias_v, float *O, uint32_t Lmax, uint32_t H, uint32_t dh,
+                            uint32_t D, float scale) {
+    if (!nchunks) return 0;
+    if (dh != 128 || H * dh != D) return bad(g, "attention: head_dim must be 128");
+    if ((uintptr_t)kv % 16 || ld % 4 || (uintptr_t)P % 16 || D % 4) return bad(g, "attention: cache must be 16-byte aligned");
+    NkAttnChunkArgs a = { kv, P, bias_u, bias_v, O, chunks, H, dh, D, ld, Lmax, scale };
+    return gpu_launch(g, "attention_rel_chunks", &a, sizeof a, H, nchunks, 1, 256, 1, 1);
+}
+
 int nk_dwconv_ln_silu_rows(gpu_t *g, const float *din_base, const int *rows, uint32_t M, const float *W,
                            const float *gamma, const float *beta, float *Y, uint32_t D, uint32_t taps, float eps) {
     if (!M) return 0;
@@ -327,13 +337,13 @@ static uint32_t blocks_for(uint64_t n) { return (uint32_t)((n + 255) / 256); }
 int nk_conv2d_c1_s2_relu_b(gpu_t *g, const float *X, const float *W, const float *bias, float *Y, uint32_t T,
                            uint32_t F, uint32_t T1, uint32_t F1, uint32_t C, uint32_t batch) {
     NkConvArgs a = { X, W, bias, Y, T, F, T1, F1, C, 0, T * F, T1 * F1 * C };
-    return gpu_launch(g, "conv2d_c1_s2_relu", &a, sizeof a, blocks_for((uint64_t)T1 * F1 * C), batch, 1, 256, 1, 1);
+    return gpu_launch(g, "conv2d_c1_s2_relu", &a, sizeof a, T1 * ((F1 + 7) / 8), batch, 1, 256, 1, 1);
 }
 
 int nk_dwconv2d_s2_b(gpu_t *g, const float *X, const float *W, const float *bias, float *Y, uint32_t T, uint32_t F,
                      uint32_t T1, uint32_t F1, uint32_t C, uint32_t batch) {
     NkConvArgs a = { X, W, bias, Y, T, F, T1, F1, C, 0, T * F * C, T1 * F1 * C };
-    return gpu_launch(g, "dwconv2d_s2", &a, sizeof a, blocks_for((uint64_t)T1 * F1 * C), batch, 1, 256, 1, 1);
+    return gpu_launch(g, "dwconv2d_s2", &a, sizeof a, T1 * ((F1 + 7) / 8), batch, 1, 256, 1, 1);
 }
 
 int nk_flatten_cf_b(gpu_t *g, const float *X, float *Y, uint32_t T, uint32_t F, uint32_t C, uint32_t batch) {

@@ -98,6 +98,21 @@ typedef struct {
     u32 pad;
 } NkAttnArgs;
 
+/* Relative-position attention of whole chunks (batched streams): one workgroup per (head, chunk)
+ * stages the chunk's K/V window and position rows in LDS once for all its query rows.
+ * chunks[4k..4k+3] = { cache row of the chunk's first row, its first output row, rows c, cached
+ * rows }; L = cached + c <= NK_ATTC_MAX_L, c <= NK_ATTC_MAX_C. */
+#define NK_ATTC_MAX_L 80
+#define NK_ATTC_MAX_C 16
+typedef struct {
+    const float *kv; /* q | k | v rows of ld floats */
+    const float *P, *bu, *bv;
+    float *O;
+    const int *chunks;
+    u32 H, dh, D, ld, Lmax;
+    float scale;
+} NkAttnChunkArgs;
+
 /* Causal depthwise conv + LN + SiLU. din: [(taps-1) + c][D]; W: [D][taps].
  * With desc set, din is the conv cache base and the rows start at pos - (taps-1).
  * With rows set (batched streams, same table as the attention), din is the conv cache base and

@@ -153,4 +153,23 @@ __device__ __forceinline__ floatx4 mfma_bf16(uint4 a, uint4 b, floatx4 acc) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a), as_bf16x8(b), acc, 0, 0, 0);
 }
 
+typedef __attribute__((address_space(3))) char lds_char_t;
+
+/* 16 bytes per lane from global memory straight into LDS: lane i writes LDS bytes
+ * [lds + 16 i, +16) of the wavefront-uniform base `lds`.  Issued as inline assembly, so the
+ * compiler does not track these loads: a kernel waits for them itself (wait_vm_lgkm) before the
+ * barrier that publishes the data, and drains them all before it can end. */
+__device__ __forceinline__ void dma16(const void *g, lds_char_t *lds) {
+    const u32 base = __builtin_amdgcn_readfirstlane((u32)(size_t)lds);
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(base) : "memory");
+}
+
+/* s_waitcnt vmcnt(N) lgkmcnt(0) */
+template <int N> __device__ __forceinline__ void wait_vm_lgkm() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(N) : "memory");
+}
+
+__device__ __forceinline__ void barrier_mem() { asm volatile("s_barrier" ::: "memory"); }
+
 #endif

@@ -3,49 +3,70 @@
  * RNNT decoder's LSTM cell and joint argmax.  Each states the reference kernel it replaces. */
 #include "nk_common.h"
 
-/* Subsampling conv 0: 1 -> C channels, 3x3, stride 2, causal padding (2 before, 1 after) on
- * time and frequency, + bias, ReLU.  X [T][F] -> Y [T1][F1][C].  One thread per output, channel
- * fastest.  Reference src/kernels.metal:411-432. */
+/* The two stride-2 3x3 convolutions of the subsampling, same causal padding (2 rows/columns
+ * before, reference src/kernels.metal:411-454).  Workgroup = one output row t1 and 8 output
+ * columns f1 (grid.x = T1 * ceil(F1/8), grid.y = windows of one size back to back, X and Y strides
+ * xs / ys); thread = output channel, holding its 9 taps and bias in registers for the 8 columns.
+ * Each output sums bias, then taps in (kh, kw) order. */
+#define CONV_FB 8
+/* 1 input channel -> C channels + ReLU: X [T][F] -> Y [T1][F1][C] */
 extern "C" __global__ __launch_bounds__(256) void conv2d_c1_s2_relu(NkConvArgs a) {
-    const u64 idx = (u64)blockIdx.x * 256 + threadIdx.x;
-    const u64 total = (u64)a.T1 * a.F1 * a.C;
-    if (idx >= total) return;
-    a.X += (u64)blockIdx.y * a.xs;
-    a.Y += (u64)blockIdx.y * a.ys;
-    const u32 o = (u32)(idx % a.C), f1 = (u32)((idx / a.C) % a.F1), t1 = (u32)(idx / ((u64)a.C * a.F1));
-    float acc = a.bias[o];
-    for (u32 kh = 0; kh < 3; ++kh) {
-        const int ti = (int)(2 * t1 + kh) - 2;
-        if (ti < 0 || ti >= (int)a.T) continue;
-        for (u32 kw = 0; kw < 3; ++kw) {
-            const int fi = (int)(2 * f1 + kw) - 2;
-            if (fi < 0 || fi >= (int)a.F) continue;
-            acc += a.W[o * 9 + kh * 3 + kw] * a.X[(u64)ti * a.F + fi];
+    const u32 nfb = (a.F1 + CONV_FB - 1) / CONV_FB;
+    const u32 t1 = blockIdx.x / nfb, f0 = (blockIdx.x % nfb) * CONV_FB;
+    const float *X = a.X + (u64)blockIdx.y * a.xs;
+    float *Y = a.Y + (u64)blockIdx.y * a.ys;
+    const u32 fe = min(f0 + CONV_FB, a.F1);
+    for (u32 o = threadIdx.x; o < a.C; o += 256) {
+        float w[9];
+#pragma unroll
+        for (int k = 0; k < 9; ++k) w[k] = a.W[o * 9 + k];
+        const float bo = a.bias[o];
+        for (u32 f1 = f0; f1 < fe; ++f1) {
+            float acc = bo;
+#pragma unroll
+            for (int kh = 0; kh < 3; ++kh) {
+                const int ti = (int)(2 * t1 + kh) - 2;
+                if (ti < 0 || ti >= (int)a.T) continue;
+#pragma unroll
+                for (int kw = 0; kw < 3; ++kw) {
+                    const int fi = (int)(2 * f1 + kw) - 2;
+                    if (fi < 0 || fi >= (int)a.F) continue;
+                    acc += w[kh * 3 + kw] * X[(u64)ti * a.F + fi];
+                }
+            }
+            Y[((u64)t1 * a.F1 + f1) * a.C + o] = fmaxf(acc, 0.0f);
         }
     }
-    a.Y[idx] = fmaxf(acc, 0.0f);
 }
 
-/* Depthwise 3x3 stride-2 conv, same causal padding, + bias, no activation:
- * reference src/kernels.metal:434-454.  X [T][F][C] -> Y [T1][F1][C]. */
+/* depthwise, + bias, no activation: X [T][F][C] -> Y [T1][F1][C] */
 extern "C" __global__ __launch_bounds__(256) void dwconv2d_s2(NkConvArgs a) {
-    const u64 idx = (u64)blockIdx.x * 256 + threadIdx.x;
-    const u64 total = (u64)a.T1 * a.F1 * a.C;
-    if (idx >= total) return;
-    a.X += (u64)blockIdx.y * a.xs;
-    a.Y += (u64)blockIdx.y * a.ys;
-    const u32 c = (u32)(idx % a.C), f1 = (u32)((idx / a.C) % a.F1), t1 = (u32)(idx / ((u64)a.C * a.F1));
-    float acc = a.bias[c];
-    for (u32 kh = 0; kh < 3; ++kh) {
-        const int ti = (int)(2 * t1 + kh) - 2;
-        if (ti < 0 || ti >= (int)a.T) continue;
-        for (u32 kw = 0; kw < 3; ++kw) {
-            const int fi = (int)(2 * f1 + kw) - 2;
-            if (fi < 0 || fi >= (int)a.F) continue;
-            acc += a.W[c * 9 + kh * 3 + kw] * a.X[((u64)ti * a.F + fi) * a.C + c];
+    const u32 nfb = (a.F1 + CONV_FB - 1) / CONV_FB;
+    const u32 t1 = blockIdx.x / nfb, f0 = (blockIdx.x % nfb) * CONV_FB;
+    const float *X = a.X + (u64)blockIdx.y * a.xs;
+    float *Y = a.Y + (u64)blockIdx.y * a.ys;
+    const u32 fe = min(f0 + CONV_FB, a.F1);
+    for (u32 c = threadIdx.x; c < a.C; c += 256) {
+        float w[9];
+#pragma unroll
+        for (int k = 0; k < 9; ++k) w[k] = a.W[c * 9 + k];
+        const float bc = a.bias[c];
+        for (u32 f1 = f0; f1 < fe; ++f1) {
+            float acc = bc;
+#pragma unroll
+            for (int kh = 0; kh < 3; ++kh) {
+                const int ti = (int)(2 * t1 + kh) - 2;
+                if (ti < 0 || ti >= (int)a.T) continue;
+#pragma unroll
+                for (int kw = 0; kw < 3; ++kw) {
+                    const int fi = (int)(2 * f1 + kw) - 2;
+                    if (fi < 0 || fi >= (int)a.F) continue;
+                    acc += w[kh * 3 + kw] * X[((u64)ti * a.F + fi) * a.C + c];
+                }
+            }
+            Y[((u64)t1 * a.F1 + f1) * a.C + c] = acc;
         }
     }
-    a.Y[idx] = acc;
 }
 
 /* [T][F][C] -> [T][C*F] channel-major flatten: reference src/kernels.metal:456-462.

@@ -181,6 +181,91 @@ extern "C" __global__ __launch_bounds__(512) void attention_rel(const NkAttnArgs
     }
 }
 
+/* Relative-position attention of whole chunks (batched streams), the math of attention_rel above
+ * (reference src/kernels.metal:290-348).  One workgroup per (head, chunk): the chunk's L = cached
+ * + c keys and values and its L + c - 1 position rows are brought into LDS by direct global -> LDS
+ * loads (16 bytes per lane, granule g of row r stored at slot g ^ (r % 8), so the row-parallel
+ * 16-byte reads below are conflict-free), then every query row of the chunk is scored against
+ * them: wavefront w takes rows w, w+4, ...; lane l takes keys l and l+64; softmax by wavefront
+ * reductions; output lane l accumulates dims 2l, 2l+1 over the keys in order. */
+extern "C" __global__ __launch_bounds__(256) void attention_rel_chunks(const NkAttnChunkArgs a) {
+    __shared__ floatx4 Ks[NK_ATTC_MAX_L * 32], Vs[NK_ATTC_MAX_L * 32];
+    __shared__ floatx4 Ps[(NK_ATTC_MAX_L + NK_ATTC_MAX_C) * 32];
+    __shared__ floatx4 qu[NK_ATTC_MAX_C * 32], qv[NK_ATTC_MAX_C * 32];
+    __shared__ float sc[NK_ATTC_MAX_C][NK_ATTC_MAX_L];
+    const u32 h = blockIdx.x, ch = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int *cd = a.chunks + 4 * ch;
+    const u32 qrow0 = (u32)cd[0], m0 = (u32)cd[1], c = (u32)cd[2], cl = (u32)cd[3];
+    const u32 L = cl + c, NP = L + c - 1;
+    if (c == 0 || c > NK_ATTC_MAX_C || L > NK_ATTC_MAX_L || L > a.Lmax) return; /* host-checked */
+    const u32 off = h * 128;
+    const float *Kg = a.kv + a.D + (u64)(qrow0 - cl) * a.ld + off;
+    const float *Vg = a.kv + 2 * a.D + (u64)(qrow0 - cl) * a.ld + off;
+    const float *Pg = a.P + (u64)(a.Lmax - L) * a.D + off;
+    /* LDS granule p = 32 r + s of a table holds granule s ^ (r % 8) of row r; one DMA instruction
+     * fills 64 granules (two rows); rows past the end re-read the last row (never used) */
+    for (u32 blk = wave; blk < (L + 1) / 2; blk += 4) {
+        const u32 p = blk * 64 + lane, r = p >> 5, g = (p & 31) ^ (r & 7), rr = min(r, L - 1);
+        dma16(Kg + (u64)rr * a.ld + 4 * g, (lds_char_t *)&Ks[blk * 64]);
+        dma16(Vg + (u64)rr * a.ld + 4 * g, (lds_char_t *)&Vs[blk * 64]);
+    }
+    for (u32 blk = wave; blk < (NP + 1) / 2; blk += 4) {
+        const u32 p = blk * 64 + lane, r = p >> 5, g = (p & 31) ^ (r & 7), rr = min(r, NP - 1);
+        dma16(Pg + (u64)rr * a.D + 4 * g, (lds_char_t *)&Ps[blk * 64]);
+    }
+    for (u32 idx = tid; idx < c * 32; idx += 256) {
+        const u32 i = idx >> 5, g = idx & 31;
+        const floatx4 q = *(const floatx4 *)(a.kv + (u64)(qrow0 + i) * a.ld + off + 4 * g);
+        qu[idx] = q + *(const floatx4 *)(a.bu + off + 4 * g);
+        qv[idx] = q + *(const floatx4 *)(a.bv + off + 4 * g);
+    }
+    wait_vm_lgkm<0>();
+    barrier_mem();
+    const u32 j0 = lane, j1 = lane + 64;
+    for (u32 i = wave; i < c; i += 4) {
+        /* position row of (i, j): (Lmax - L) + (c - 1 - i + j), i.e. row c - 1 - i + j of Ps */
+        const u32 p0 = c - 1 - i + j0, p1 = c - 1 - i + j1;
+        float s0 = 0.0f, s1 = 0.0f;
+        if (j0 < L) {
+#pragma unroll 8
+            for (u32 g = 0; g < 32; ++g) {
+                const floatx4 u = qu[i * 32 + g], w = qv[i * 32 + g];
+                const floatx4 k = Ks[j0 * 32 + (g ^ (j0 & 7))], pp = Ps[p0 * 32 + (g ^ (p0 & 7))];
+                s0 += u[0] * k[0] + u[1] * k[1] + u[2] * k[2] + u[3] * k[3];
+                s0 += w[0] * pp[0] + w[1] * pp[1] + w[2] * pp[2] + w[3] * pp[3];
+            }
+        }
+        if (j1 < L) {
+#pragma unroll 8
+            for (u32 g = 0; g < 32; ++g) {
+                const floatx4 u = qu[i * 32 + g], w = qv[i * 32 + g];
+                const floatx4 k = Ks[j1 * 32 + (g ^ (j1 & 7))], pp = Ps[p1 * 32 + (g ^ (p1 & 7))];
+                s1 += u[0] * k[0] + u[1] * k[1] + u[2] * k[2] + u[3] * k[3];
+                s1 += w[0] * pp[0] + w[1] * pp[1] + w[2] * pp[2] + w[3] * pp[3];
+            }
+        }
+        s0 = j0 < L ? s0 * a.scale : -INFINITY;
+        s1 = j1 < L ? s1 * a.scale : -INFINITY;
+        const float mx = wave_max(fmaxf(s0, s1));
+        const float e0 = j0 < L ? expf(s0 - mx) : 0.0f, e1 = j1 < L ? expf(s1 - mx) : 0.0f;
+        const float sum = wave_sum(e0 + e1);
+        if (j0 < L) sc[i][j0] = e0 / sum;
+        if (j1 < L) sc[i][j1] = e1 / sum;
+    }
+    lds_barrier();
+    const u32 gq = lane >> 1, hf = (lane & 1) * 2;
+    for (u32 i = wave; i < c; i += 4) {
+        float o0 = 0.0f, o1 = 0.0f;
+        for (u32 j = 0; j < L; ++j) {
+            const float pj = sc[i][j];
+            const floatx4 v = Vs[j * 32 + (gq ^ (j & 7))];
+            o0 += pj * v[hf];
+            o1 += pj * v[hf + 1];
+        }
+        *(floatx2 *)(a.O + (u64)(m0 + i) * a.D + off + 2 * lane) = (floatx2){ o0, o1 };
+    }
+}
+
 /* Causal depthwise conv (9 taps: 8 history rows + the row itself, no bias) + LN + SiLU, one
  * workgroup per output row: reference src/kernels.metal:359-409.  Thread t owns channels
  * 4t..4t+3 (+1024k); all 9 input rows and the 4x9 taps are loaded up front. */

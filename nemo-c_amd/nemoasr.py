@@ -118,6 +118,8 @@ API = {
     "nk_compact": (C.c_int, [_vp, _vp, C.c_uint64, _u32, _u32, _u32, _u32, _u32]),
     "nk_attention_rel_rows": (C.c_int, [_vp, _vp, _u32, _vp, _u32, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32,
                                         C.c_float]),
+    "nk_attention_rel_chunks": (C.c_int, [_vp, _vp, _u32, _vp, _u32, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32,
+                                          C.c_float]),
     "nk_dwconv_ln_silu_rows": (C.c_int, [_vp, _vp, _vp, _u32, _vp, _vp, _vp, _vp, _u32, _u32, C.c_float]),
     "nk_conv2d_c1_s2_relu_b": (C.c_int, [_vp, _vp, _vp, _vp, _vp] + [_u32] * 6),
     "nk_dwconv2d_s2_b": (C.c_int, [_vp, _vp, _vp, _vp, _vp] + [_u32] * 6),

@@ -267,6 +267,51 @@ def test_attention_rel(gpu, c, cache):
     assert rel_err(dO.read((c, D)), ref) < 1e-5
 
 
+@pytest.mark.parametrize("Lmax", [72, 73])
+def test_attention_batched_streams(gpu, Lmax):
+    """Several streams' chunks in one launch, each at its own cache position and fill level: the
+    per-row table kernel and the whole-chunk kernel against the oracle chunk by chunk."""
+    import nemoasr
+
+    lib = nemoasr.lib()
+    H, dh, D = 8, 128, 1024
+    rng = np.random.default_rng([Lmax, 5])
+    chunks_spec = [(7, 56), (7, 0), (1, 56), (14, 56), (16, 56), (9, 23), (7, 49), (3, 1)]
+    cap = 96
+    kv = rng.standard_normal((len(chunks_spec) * cap, 3 * D)).astype(np.float32)
+    P = rng.standard_normal((2 * Lmax - 1, D)).astype(np.float32)
+    bu = (0.1 * rng.standard_normal(D)).astype(np.float32)
+    bv = (0.1 * rng.standard_normal(D)).astype(np.float32)
+    rows, chunks, refs, m = [], [], [], 0
+    for s, (c, cache) in enumerate(chunks_spec):
+        pos = s * cap + cache + 3 + s  # first cache row of the chunk inside stream s's region
+        L = cache + c
+        Q = kv[pos:pos + c, :]
+        K = kv[pos - cache:pos + c, D:2 * D]
+        V = kv[pos - cache:pos + c, 2 * D:]
+        refs.append(oracle.attention_rel(Q, K, V, P, bu, bv, c, L, Lmax, H, dh))
+        for i in range(c):
+            rows += [pos + i, i, c, cache]
+        chunks += [pos, m, c, cache]
+        m += c
+    ref = np.concatenate(refs)
+    dkv, dP, dbu, dbv = gpu.put(kv), gpu.put(P), gpu.put(bu), gpu.put(bv)
+    drows, dch = gpu.put(np.asarray(rows, np.int32)), gpu.put(np.asarray(chunks, np.int32))
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(dh)))
+    for which in ("rows", "chunks"):
+        dO = gpu.alloc(m * D * 4)
+        gpu.begin()
+        if which == "rows":
+            gpu.check(lib.nk_attention_rel_rows(gpu.h, dkv.ptr, 3 * D, drows.ptr, m, dP.ptr, dbu.ptr, dbv.ptr, dO.ptr,
+                                                Lmax, H, dh, D, scale))
+        else:
+            gpu.check(lib.nk_attention_rel_chunks(gpu.h, dkv.ptr, 3 * D, dch.ptr, len(chunks_spec), dP.ptr, dbu.ptr,
+                                                  dbv.ptr, dO.ptr, Lmax, H, dh, D, scale))
+        gpu.end()
+        assert rel_err(dO.read((m, D)), ref) < 1e-5, which
+        dO.free()
+
+
 @pytest.mark.parametrize("c", [1, 7, 14])
 def test_dwconv_ln_silu(gpu, c):
     import nemoasr
