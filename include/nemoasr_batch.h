@@ -65,6 +65,9 @@ const double *nemoasr_batch_step_ms(const nemoasr_batch_t *b, size_t *n);
    set_dump(1) keeps every stream's joint.enc rows (the joint's encoder input) on the host. */
 void nemoasr_batch_debug_use_graphs(nemoasr_batch_t *b, int on);
 void nemoasr_batch_debug_set_dump(nemoasr_batch_t *b, int on);
+/* 1 (default): the greedy loop runs on the device, graph-replayed runs of steps; 0: one host round
+   trip per joint evaluation.  Select before the first step of a batch. */
+void nemoasr_batch_debug_device_decoder(nemoasr_batch_t *b, int on);
 const float *nemoasr_batch_debug_joint_enc(const nemoasr_batch_t *b, int stream, size_t *frames);
 /* Per-kernel timing of direct launches (kernel: exact name or a prefix ending in '*'): mean ms per
    launch, launches, and the summed algorithmic bytes and flops of those launches. */

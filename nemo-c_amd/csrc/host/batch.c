@@ -117,6 +117,12 @@ struct nemoasr_batch {
     int P, J, V, Vp;
     gpu_buf_t *wcat[2], *wout, *bout, *hc, *lin, *gates, *hout, *hout2, *pred, *jin, *logits, *amax, *dtab;
     int *stage_dtab, *stage_amax;
+    /* device-resident loop (kernels/nk_bdec.hip) */
+    int device_dec, W, tok_ld;
+    gpu_buf_t *bst, *bsetup, *btok, *lin1, *gates1, *predtmp;
+    NkBDecStream *stage_bst;
+    int *stage_bsetup, *stage_btok;
+    gpu_graph_t *dgraph;
     /* accounting */
     double *step_ms;
     size_t n_step, cap_step;
@@ -222,6 +228,14 @@ static void stream_clear(nemoasr_batch_t *b, int s) {
     if (b->dump) b->dj_n[s] = 0;
 }
 
+/* decoder state of a fresh stream on the device: no valid prediction, last token blank, slot set 0 */
+static int bdec_state_reset(nemoasr_batch_t *b, int s) {
+    NkBDecStream x;
+    memset(&x, 0, sizeof x);
+    x.last_token = b->m->cfg.blank_id;
+    return gpu_upload(b->g, (NkBDecStream *)gpu_buf_dptr(b->bst) + s, &x, sizeof x);
+}
+
 /* device state of one stream back to that after open: zero LSTM states and conv history */
 static int stream_zero_device(nemoasr_batch_t *b, int s) {
     const size_t D = (size_t)b->m->cfg.d_model, P = (size_t)b->P;
@@ -232,7 +246,7 @@ static int stream_zero_device(nemoasr_batch_t *b, int s) {
         rc |= gpu_upload(b->g, (float *)gpu_buf_dptr(b->din) + (size_t)l * b->din_lstride + (size_t)s * b->cap_rows * D, z,
                          (size_t)b->conv_left * D * sizeof(float));
     free(z);
-    return rc;
+    return rc | bdec_state_reset(b, s);
 }
 
 nemoasr_batch_t *nemoasr_batch_open(const char *model_dir, const char *language, int latency_ms, int n_streams,
@@ -325,7 +339,18 @@ nemoasr_batch_t *nemoasr_batch_open(const char *model_dir, const char *language,
     b->dtab = gpu_buf_alloc(g, (10 * S + 2 * R) * sizeof(int));
     b->stage_dtab = gpu_host_alloc(g, (10 * S + 2 * R) * sizeof(int));
     b->stage_amax = gpu_host_alloc(g, 2 * R * sizeof(int));
-    if (!b->win || !b->kv || !b->din || !b->ff || !b->stage_win || !b->stage_dtab) {
+    b->W = b->cmax;
+    b->tok_ld = c->max_symbols * b->cmax + 16;
+    b->bst = gpu_buf_alloc(g, S * sizeof(NkBDecStream));
+    b->bsetup = gpu_buf_alloc(g, 2 * S * sizeof(int));
+    b->btok = gpu_buf_alloc(g, S * (size_t)b->tok_ld * sizeof(int));
+    b->lin1 = gpu_buf_alloc(g, S * 2 * P * fs);
+    b->gates1 = gpu_buf_alloc(g, S * 4 * P * fs);
+    b->predtmp = gpu_buf_alloc(g, S * J * fs);
+    b->stage_bst = gpu_host_alloc(g, S * sizeof(NkBDecStream));
+    b->stage_bsetup = gpu_host_alloc(g, 2 * S * sizeof(int));
+    b->stage_btok = gpu_host_alloc(g, S * (size_t)b->tok_ld * sizeof(int));
+    if (!b->win || !b->kv || !b->din || !b->ff || !b->stage_win || !b->stage_dtab || !b->btok || !b->stage_btok) {
         snprintf(err, errlen, "batch: out of memory for %d streams", n_streams);
         nemoasr_batch_close(b);
         return NULL;
@@ -345,6 +370,13 @@ nemoasr_batch_t *nemoasr_batch_open(const char *model_dir, const char *language,
     b->g_fill = malloc(S * sizeof(int));
     b->ord = malloc(S * sizeof(int));
     for (int s = 0; s < n_streams; ++s) stream_clear(b, s);
+    for (int s = 0; s < n_streams; ++s)
+        if (bdec_state_reset(b, s)) {
+            snprintf(err, errlen, "batch: decoder state upload failed");
+            nemoasr_batch_close(b);
+            return NULL;
+        }
+    b->device_dec = 1;
     b->fe_list = malloc(S * sizeof(int));
     pool_start(&b->pool, b);
     b->use_graphs = 1;
@@ -361,12 +393,17 @@ void nemoasr_batch_close(nemoasr_batch_t *b) {
     gpu_buf_t *bufs[] = { b->win, b->c0, b->c1, b->c2, b->c3, b->c4, b->flat, b->pre_out, b->h, b->tmp, b->lnb,
                           b->ff, b->att, b->y, b->ph, b->prompted, b->joint_enc, b->kv, b->din, b->etab, b->wcat[0],
                           b->wcat[1], b->wout, b->bout, b->hc, b->lin, b->gates, b->hout, b->hout2, b->pred,
-                          b->jin, b->logits, b->amax, b->dtab };
+                          b->jin, b->logits, b->amax, b->dtab, b->bst, b->bsetup, b->btok, b->lin1, b->gates1,
+                          b->predtmp };
     for (size_t i = 0; i < sizeof bufs / sizeof *bufs; ++i) gpu_buf_free(bufs[i]);
     gpu_host_free(b->stage_win);
     gpu_host_free(b->stage_tab);
     gpu_host_free(b->stage_dtab);
     gpu_host_free(b->stage_amax);
+    gpu_host_free(b->stage_bst);
+    gpu_host_free(b->stage_bsetup);
+    gpu_host_free(b->stage_btok);
+    gpu_graph_free(b->dgraph);
     if (b->st)
         for (int s = 0; s < b->S; ++s) {
             melfe_destroy(b->st[s].mel);
@@ -907,6 +944,112 @@ static int decoder_batch_run(nemoasr_batch_t *b, int nact, char *err, size_t err
     return 0;
 }
 
+/* ---- device-resident batched greedy loop (kernels/nk_bdec.hip) --------------------------------- */
+#define BDEC_STEPS 10 /* steps per graph run; the host reads the state back once per run */
+
+static NkBDecArgs bdec_args(nemoasr_batch_t *b) {
+    model_t *m = b->m;
+    NkBDecArgs a;
+    memset(&a, 0, sizeof a);
+    a.st = gpu_buf_dptr(b->bst);
+    a.setup = gpu_buf_dptr(b->bsetup);
+    a.tokens = gpu_buf_dptr(b->btok);
+    a.enc = gpu_buf_dptr(b->joint_enc);
+    a.embed = m->embed_dev;
+    a.hc = gpu_buf_dptr(b->hc);
+    a.A0 = gpu_buf_dptr(b->lin);
+    a.A1 = gpu_buf_dptr(b->lin1);
+    a.g0 = gpu_buf_dptr(b->gates);
+    a.g1 = gpu_buf_dptr(b->gates1);
+    a.b0 = m->lstm_b[0];
+    a.b1 = m->lstm_b[1];
+    a.hout = gpu_buf_dptr(b->hout);
+    a.predtmp = gpu_buf_dptr(b->predtmp);
+    a.pred = gpu_buf_dptr(b->pred);
+    a.bjp = m->joint_pred_b;
+    a.jin = gpu_buf_dptr(b->jin);
+    a.logits = gpu_buf_dptr(b->logits);
+    a.S = (uint32_t)b->S;
+    a.W = (uint32_t)b->W;
+    a.P = (uint32_t)b->P;
+    a.J = (uint32_t)b->J;
+    a.V = (uint32_t)b->V;
+    a.ldl = (uint32_t)b->Vp;
+    a.blank = (uint32_t)m->cfg.blank_id;
+    a.max_symbols = (uint32_t)m->cfg.max_symbols;
+    a.tok_ld = (uint32_t)b->tok_ld;
+    return a;
+}
+
+/* `steps` decoder steps over all streams (fixed shapes: one graph serves every run) */
+static void launch_bdec_steps(nemoasr_batch_t *b, int steps) {
+    gpu_t *g = b->g;
+    const NkBDecArgs a = bdec_args(b);
+    const uint32_t S = a.S, P = a.P, J = a.J, Vp = a.ldl, R = a.S * a.W;
+    for (int k = 0; k < steps; ++k) {
+        nk_gemm(g, a.A0, 2 * P, gpu_buf_dptr(b->wcat[0]), 2 * P, NULL, a.g0, 4 * P, S, 4 * P, 2 * P, NK_ACT_NONE, 1, 1.0f);
+        gpu_launch(g, "bdec_cell0", &a, sizeof a, (P + 255) / 256, S, 1, 256, 1, 1);
+        nk_gemm(g, a.A1, 2 * P, gpu_buf_dptr(b->wcat[1]), 2 * P, NULL, a.g1, 4 * P, S, 4 * P, 2 * P, NK_ACT_NONE, 1, 1.0f);
+        gpu_launch(g, "bdec_cell1", &a, sizeof a, (P + 255) / 256, S, 1, 256, 1, 1);
+        nk_gemm(g, a.hout, P, b->m->joint_pred_w, P, NULL, a.predtmp, J, S, J, P, NK_ACT_NONE, 1, 1.0f);
+        gpu_launch(g, "bdec_joint_in", &a, sizeof a, (J + 255) / 256, R, 1, 256, 1, 1);
+        nk_gemm(g, a.jin, J, gpu_buf_dptr(b->wout), J, gpu_buf_dptr(b->bout), (float *)a.logits, Vp, R, Vp, J, NK_ACT_NONE, 0,
+                1.0f);
+        gpu_launch(g, "bdec_decide", &a, sizeof a, S, 1, 1, 256, 1, 1);
+    }
+}
+
+/* the chunks of order[0..nact) through the device loop: one setup launch, then graph runs of
+ * BDEC_STEPS steps until every chunk is done */
+static int decoder_batch_device(nemoasr_batch_t *b, int nact, char *err, size_t errlen) {
+    gpu_t *g = b->g;
+    const int S = b->S;
+    int *su = b->stage_bsetup;
+    memset(su, 0, (size_t)2 * S * sizeof(int));
+    int maxc = 0;
+    for (int i = 0; i < nact; ++i) {
+        const bstream_t *x = &b->st[b->order[i]];
+        su[2 * b->order[i]] = x->c;
+        su[2 * b->order[i] + 1] = x->row0;
+        if (x->c > maxc) maxc = x->c;
+    }
+    if (maxc > b->W) { snprintf(err, errlen, "decoder: chunk of %d frames exceeds %d", maxc, b->W); return -1; }
+    const NkBDecArgs a = bdec_args(b);
+    const int max_runs = (maxc * b->m->cfg.max_symbols + maxc) / BDEC_STEPS + 3;
+    for (int run = 0;; ++run) {
+        if (run >= max_runs) { snprintf(err, errlen, "decoder: no progress"); return -1; }
+        gpu_begin(g);
+        if (run == 0) {
+            gpu_upload_async(g, gpu_buf_dptr(b->bsetup), su, (size_t)2 * S * sizeof(int));
+            gpu_launch(g, "bdec_setup", &a, sizeof a, (uint32_t)S, 1, 1, 256, 1, 1);
+        }
+        if (b->use_graphs && !b->dgraph && !gpu_capture_begin(g)) {
+            launch_bdec_steps(b, BDEC_STEPS);
+            b->dgraph = gpu_capture_end(g);
+        }
+        if (b->dgraph) gpu_graph_launch(g, b->dgraph);
+        else launch_bdec_steps(b, BDEC_STEPS);
+        gpu_download_async(g, b->stage_bst, gpu_buf_dptr(b->bst), (size_t)S * sizeof(NkBDecStream));
+        gpu_download_async(g, b->stage_btok, gpu_buf_dptr(b->btok), (size_t)S * b->tok_ld * sizeof(int));
+        if (gpu_end(g, err, errlen)) return -1;
+        b->stats.joint_steps += BDEC_STEPS;
+        int done = 1;
+        for (int i = 0; i < nact && done; ++i) {
+            const NkBDecStream *x = &b->stage_bst[b->order[i]];
+            done = x->t >= x->frames;
+        }
+        if (done) break;
+    }
+    for (int i = 0; i < nact; ++i) {
+        const int s = b->order[i];
+        const int n = b->stage_bst[s].n_out;
+        if (n > b->tok_ld) { snprintf(err, errlen, "decoder: stream %d emitted %d tokens in a chunk", s, n); return -1; }
+        for (int k = 0; k < n; ++k) keep_token(&b->st[s], b->stage_btok[(size_t)s * b->tok_ld + k]);
+        b->stats.tokens += (size_t)n;
+    }
+    return 0;
+}
+
 int nemoasr_batch_step(nemoasr_batch_t *b, char *err, size_t errlen) {
     if (errlen) err[0] = 0;
     const double t0 = now_ms();
@@ -949,7 +1092,7 @@ int nemoasr_batch_step(nemoasr_batch_t *b, char *err, size_t errlen) {
         }
         free(all);
     }
-    if (decoder_batch_run(b, nact, err, errlen)) return -1;
+    if (b->device_dec ? decoder_batch_device(b, nact, err, errlen) : decoder_batch_run(b, nact, err, errlen)) return -1;
     const double t2 = now_ms();
     b->stats.steps++;
     b->stats.chunks += (size_t)nact;
@@ -1024,8 +1167,14 @@ const double *nemoasr_batch_step_ms(const nemoasr_batch_t *b, size_t *n) {
 /* ---- test hooks ---------------------------------------------------------------------------- */
 void nemoasr_batch_debug_use_graphs(nemoasr_batch_t *b, int on) {
     b->use_graphs = on;
-    if (!on) drop_graphs(b);
+    if (!on) {
+        drop_graphs(b);
+        gpu_graph_free(b->dgraph);
+        b->dgraph = NULL;
+    }
 }
+
+void nemoasr_batch_debug_device_decoder(nemoasr_batch_t *b, int on) { b->device_dec = on; }
 
 void nemoasr_batch_debug_set_dump(nemoasr_batch_t *b, int on) {
     b->dump = on;

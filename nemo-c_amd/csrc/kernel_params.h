@@ -270,4 +270,32 @@ typedef struct {
     u32 rows, V, ld, pad;
 } NkArgmaxRowsArgs;
 
+/* Device-resident greedy loop of many streams (kernels/nk_bdec.hip).  Per-stream state; the
+ * first eight fields follow the reference's decoder (src/decoder.c:14-23, :92-127): frames of the
+ * current chunk, next frame t, symbols emitted at frame t, whether the prediction is valid, the
+ * committed LSTM slot set, the last token; then tokens emitted in this chunk, the chunk's first
+ * joint.enc row, and whether this step recomputes the prediction. */
+typedef struct {
+    int frames, t, symbols, pred_valid, cur, last_token, n_out, erow0;
+    int need, pad[7];
+} NkBDecStream;
+
+typedef struct {
+    NkBDecStream *st;      /* [S]                                                        */
+    const int *setup;      /* [S][2] frames, first joint.enc row of a new chunk (setup)    */
+    int *tokens;           /* [S][tok_ld] tokens emitted in the current chunk              */
+    const float *enc;      /* joint.enc rows [*][J]                                        */
+    const u16 *embed;      /* [blank + 1][P] bf16                                          */
+    float *hc;             /* [S][2 slot sets][h0, c0, h1, c1][P]                          */
+    float *A0, *A1;        /* [S][2P] LSTM layer inputs [x | h]                            */
+    float *g0, *g1;        /* [S][4P] gates (initialised to the bias, GEMMs accumulate)    */
+    const float *b0, *b1;  /* [4P]                                                         */
+    float *hout;           /* [S][P] new layer-1 state, input of joint.pred                */
+    float *predtmp, *pred; /* [S][J] recomputed / current prediction                       */
+    const float *bjp;      /* [J]                                                          */
+    float *jin;            /* [S*W][J] joint inputs relu(enc + pred)                       */
+    const float *logits;   /* [S*W][ldl]                                                   */
+    u32 S, W, P, J, V, ldl, blank, max_symbols, tok_ld, pad;
+} NkBDecArgs;
+
 #endif

@@ -6,3 +6,4 @@
 #include "nk_seq.hip"
 #include "nk_ops.hip"
 #include "nk_dec.hip"
+#include "nk_bdec.hip"

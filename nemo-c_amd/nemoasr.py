@@ -53,6 +53,7 @@ API = {
     "nemoasr_batch_step_ms": (C.POINTER(C.c_double), [_vp, C.POINTER(C.c_size_t)]),
     "nemoasr_batch_debug_use_graphs": (None, [_vp, C.c_int]),
     "nemoasr_batch_debug_set_dump": (None, [_vp, C.c_int]),
+    "nemoasr_batch_debug_device_decoder": (None, [_vp, C.c_int]),
     "nemoasr_batch_debug_joint_enc": (_f32p, [_vp, C.c_int, C.POINTER(C.c_size_t)]),
     "nemoasr_batch_debug_time_kernel": (C.c_int, [_vp, C.c_char_p, C.c_int]),
     "nemoasr_batch_debug_kernel_ms": (C.c_int, [_vp, C.POINTER(C.c_double), C.POINTER(C.c_int),
@@ -412,6 +413,9 @@ class Batch:
 
     def set_dump(self, on: bool):
         lib().nemoasr_batch_debug_set_dump(self.h, int(on))
+
+    def device_decoder(self, on: bool):
+        lib().nemoasr_batch_debug_device_decoder(self.h, int(on))
 
     def joint_enc(self, stream: int, joint_hidden: int) -> np.ndarray:
         n = C.c_size_t()

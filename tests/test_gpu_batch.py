@@ -61,8 +61,10 @@ def check_streams(b, om, latency, mels, J, tag=None):
         assert b.tokens(s) == toks, f"stream {s}: {len(b.tokens(s))} tokens vs oracle {len(toks)}"
 
 
+@pytest.mark.parametrize("device_loop", [True, False])
 @pytest.mark.parametrize("latency", [80, 560, 1120])
-def test_tiny_batch_matches_oracle(latency):
+def test_tiny_batch_matches_oracle(latency, device_loop):
+    """Both greedy loops: device-resident (graph runs of steps) and one host round trip per step."""
     import nemoasr
 
     mdir = model_dir("tiny")
@@ -71,9 +73,10 @@ def test_tiny_batch_matches_oracle(latency):
     mels = [mel_ref.logmel(synth.make_audio(t, seed=40 + i)) for i, t in enumerate(secs)]
     starts = [0, 0, 3, 5, 1, 9]
     b = nemoasr.Batch(mdir, "en-US", latency, streams=len(mels))
+    b.device_decoder(device_loop)
     b.set_dump(True)
     drive(b, mels, starts, piece=8 * (LAT_RIGHT[latency] + 1))
-    check_streams(b, om, latency, mels, om.dims.joint_hidden)
+    check_streams(b, om, latency, mels, om.dims.joint_hidden, tag=("tiny", latency))
     st = b.stats()
     assert st["chunks"] > 0 and st["tokens"] == sum(len(b.tokens(s)) for s in range(len(mels)))
     b.close()
@@ -93,7 +96,7 @@ def test_full_batch_matches_oracle(graphs):
     b.use_graphs(graphs)
     b.set_dump(True)
     drive(b, mels, [0, 0, 0, 0, 4], piece=56)
-    check_streams(b, om, 560, mels, om.dims.joint_hidden, tag="full560")
+    check_streams(b, om, 560, mels, om.dims.joint_hidden, tag=("full", 560))
     b.close()
 
 
