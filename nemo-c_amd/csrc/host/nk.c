@@ -117,6 +117,9 @@ static int launch_mx(gpu_t *g, NkGemmArgs *a, uint32_t M, uint32_t nout, uint32_
     }
     if (last_ok < 0) return 1;
     uint32_t kz = 1;
+    /* K splits add partial tiles atomically; with fewer than 64 rows that costs more than the idle
+     * CUs it fills (measured), so few-row GEMMs take the smallest tile instead */
+    if (M <= 64) splittable = 0;
     if (pick_i < 0) {
         /* too few tiles: split K of the 64x128 tile when allowed, else the smallest tile */
         int i = last_ok;
