@@ -45,7 +45,7 @@ def bench_gemm(gpu, M, N, K, act, acc, alpha, ln_mode, ldw, has_bias, copies, re
     ldw = ldw or K
     rng = np.random.default_rng([M, N, K])
     nout = N // 2 if act == 3 else N
-    W = (rng.standard_normal((N, ldw)).astype(np.float32) / np.sqrt(K)).view(np.uint32) >> 16
+    W = (rng.standard_normal((N, ldw)).astype(np.float32) / np.float32(np.sqrt(K))).view(np.uint32) >> 16
     W = W.astype(np.uint16)
     dWs = [gpu.put(W) for _ in range(copies)]
     dA = gpu.put(rng.standard_normal((M, K)).astype(np.float32))
