@@ -73,6 +73,14 @@ int nk_gemm_ln(gpu_t *g, const float *A, uint32_t lda, const uint16_t *W, uint32
                uint32_t ldc, const int *crow, uint32_t M, uint32_t N, uint32_t K, int act, int accumulate, float alpha,
                int ln_mode, const float *g1, const float *b1, const float *g2, const float *b2, float *ln_out,
                float *tmp, float eps);
+/* Row argmax of A W^T + bias over the first V columns without storing the scores: keys[m][p] is
+ * the best packed (score, lowest column) key of column part p of row m (N/32 parts; the largest
+ * key wins, and its low 32 bits hold 0xffffffff - column).  N % 64 == 0. */
+int nk_gemm_argmax(gpu_t *g, const float *A, uint32_t lda, const uint16_t *W, uint32_t ldw, const float *bias,
+                   unsigned long long *keys, uint32_t keys_ld, uint32_t M, uint32_t N, uint32_t K, uint32_t V);
+/* 1: many-row MFMA kernels take 64-wide K stages where K allows; 0 (default): 32-wide.  Returns
+ * the previous setting. */
+int nk_gemm_mx_k64(int on);
 /* Kernel selection: 0 automatic (by row count), 1 first-generation VALU GEMV (M <= 4),
  * 2 few-row MFMA (M <= 16), 3 many-row MFMA, 4 weight-streaming GEMV (M <= 4),
  * 5 first-generation many-row MFMA (register-staged).

@@ -119,7 +119,8 @@ struct nemoasr_batch {
     int *stage_dtab, *stage_amax;
     /* device-resident loop (kernels/nk_bdec.hip) */
     int device_dec, W, tok_ld;
-    gpu_buf_t *bst, *bsetup, *btok, *lin1, *gates1, *predtmp;
+    gpu_buf_t *bst, *bsetup, *btok, *lin1, *gates1, *predtmp, *wcati[2], *bi[2], *keys;
+    int nkeys;
     NkBDecStream *stage_bst;
     int *stage_bsetup, *stage_btok;
     gpu_graph_t *dgraph;
@@ -191,6 +192,22 @@ static int build_decoder_weights(nemoasr_batch_t *b) {
         }
         b->wcat[l] = gpu_buf_alloc(g, 4 * P * 2 * P * 2);
         rc |= gpu_upload(g, gpu_buf_dptr(b->wcat[l]), cat, 4 * P * 2 * P * 2);
+        /* the same rows interleaved by unit (row 4u + q = gate q of unit u) for the device loop,
+           whose GEMM epilogue applies the LSTM cell, and the bias in the same order */
+        uint16_t *ci = malloc(4 * P * 2 * P * 2);
+        float *bh = malloc(4 * P * sizeof(float)), *bih = malloc(4 * P * sizeof(float));
+        for (size_t u = 0; u < P; ++u)
+            for (size_t q = 0; q < 4; ++q) memcpy(ci + (4 * u + q) * 2 * P, cat + (q * P + u) * 2 * P, 2 * P * 2);
+        rc |= gpu_download(g, bh, m->lstm_b[l], 4 * P * sizeof(float));
+        for (size_t u = 0; u < P; ++u)
+            for (size_t q = 0; q < 4; ++q) bih[4 * u + q] = bh[q * P + u];
+        b->wcati[l] = gpu_buf_alloc(g, 4 * P * 2 * P * 2);
+        b->bi[l] = gpu_buf_alloc(g, 4 * P * sizeof(float));
+        rc |= gpu_upload(g, gpu_buf_dptr(b->wcati[l]), ci, 4 * P * 2 * P * 2);
+        rc |= gpu_upload(g, gpu_buf_dptr(b->bi[l]), bih, 4 * P * sizeof(float));
+        free(ci);
+        free(bh);
+        free(bih);
     }
     uint16_t *wo = calloc(Vp * J, 2);
     float *bo = calloc(Vp, sizeof(float));
@@ -342,6 +359,8 @@ nemoasr_batch_t *nemoasr_batch_open(const char *model_dir, const char *language,
     b->W = b->cmax;
     b->tok_ld = c->max_symbols * b->cmax + 16;
     b->bst = gpu_buf_alloc(g, S * sizeof(NkBDecStream));
+    b->nkeys = 2 * (b->Vp / 64);
+    b->keys = gpu_buf_alloc(g, S * (size_t)b->W * b->nkeys * sizeof(unsigned long long));
     b->bsetup = gpu_buf_alloc(g, 2 * S * sizeof(int));
     b->btok = gpu_buf_alloc(g, S * (size_t)b->tok_ld * sizeof(int));
     b->lin1 = gpu_buf_alloc(g, S * 2 * P * fs);
@@ -376,7 +395,9 @@ nemoasr_batch_t *nemoasr_batch_open(const char *model_dir, const char *language,
             nemoasr_batch_close(b);
             return NULL;
         }
-    b->device_dec = 1;
+    /* the device loop's GEMMs cover K = 2P <= 1280 and K = P <= 640 in one pass of their
+       wavefronts; larger prediction networks use the host-driven loop */
+    b->device_dec = b->P <= 640 && b->P % 16 == 0 && b->J % 16 == 0;
     b->fe_list = malloc(S * sizeof(int));
     pool_start(&b->pool, b);
     b->use_graphs = 1;
@@ -394,7 +415,7 @@ void nemoasr_batch_close(nemoasr_batch_t *b) {
                           b->ff, b->att, b->y, b->ph, b->prompted, b->joint_enc, b->kv, b->din, b->etab, b->wcat[0],
                           b->wcat[1], b->wout, b->bout, b->hc, b->lin, b->gates, b->hout, b->hout2, b->pred,
                           b->jin, b->logits, b->amax, b->dtab, b->bst, b->bsetup, b->btok, b->lin1, b->gates1,
-                          b->predtmp };
+                          b->predtmp, b->wcati[0], b->wcati[1], b->bi[0], b->bi[1], b->keys };
     for (size_t i = 0; i < sizeof bufs / sizeof *bufs; ++i) gpu_buf_free(bufs[i]);
     gpu_host_free(b->stage_win);
     gpu_host_free(b->stage_tab);
@@ -952,6 +973,8 @@ static NkBDecArgs bdec_args(nemoasr_batch_t *b) {
     NkBDecArgs a;
     memset(&a, 0, sizeof a);
     a.st = gpu_buf_dptr(b->bst);
+    a.keys = gpu_buf_dptr(b->keys);
+    a.nkeys = (uint32_t)b->nkeys;
     a.setup = gpu_buf_dptr(b->bsetup);
     a.tokens = gpu_buf_dptr(b->btok);
     a.enc = gpu_buf_dptr(b->joint_enc);
@@ -982,20 +1005,39 @@ static NkBDecArgs bdec_args(nemoasr_batch_t *b) {
 }
 
 /* `steps` decoder steps over all streams (fixed shapes: one graph serves every run) */
+typedef struct {
+    NkGemmArgs g;
+    NkBDecArgs d;
+} bdec_launch_t;
+
+static int launch_bdec_gemm(nemoasr_batch_t *b, const char *kernel, const float *A, uint32_t lda, const uint16_t *W,
+                            const float *bias, uint32_t N, uint32_t K, uint32_t waves) {
+    bdec_launch_t x;
+    memset(&x, 0, sizeof x);
+    x.g.A = A;
+    x.g.lda = lda;
+    x.g.W = W;
+    x.g.ldw = K;
+    x.g.bias = bias;
+    x.g.M = (uint32_t)b->S;
+    x.g.N = N;
+    x.g.K = K;
+    x.d = bdec_args(b);
+    return gpu_launch(b->g, kernel, &x, sizeof x, N / 16, ((uint32_t)b->S + 63) / 64, 1, 64 * waves, 1, 1);
+}
+
 static void launch_bdec_steps(nemoasr_batch_t *b, int steps) {
     gpu_t *g = b->g;
     const NkBDecArgs a = bdec_args(b);
     const uint32_t S = a.S, P = a.P, J = a.J, Vp = a.ldl, R = a.S * a.W;
     for (int k = 0; k < steps; ++k) {
-        nk_gemm(g, a.A0, 2 * P, gpu_buf_dptr(b->wcat[0]), 2 * P, NULL, a.g0, 4 * P, S, 4 * P, 2 * P, NK_ACT_NONE, 1, 1.0f);
-        gpu_launch(g, "bdec_cell0", &a, sizeof a, (P + 255) / 256, S, 1, 256, 1, 1);
-        nk_gemm(g, a.A1, 2 * P, gpu_buf_dptr(b->wcat[1]), 2 * P, NULL, a.g1, 4 * P, S, 4 * P, 2 * P, NK_ACT_NONE, 1, 1.0f);
-        gpu_launch(g, "bdec_cell1", &a, sizeof a, (P + 255) / 256, S, 1, 256, 1, 1);
-        nk_gemm(g, a.hout, P, b->m->joint_pred_w, P, NULL, a.predtmp, J, S, J, P, NK_ACT_NONE, 1, 1.0f);
+        launch_bdec_gemm(b, "bdec_lstm0_w8s5", a.A0, 2 * P, gpu_buf_dptr(b->wcati[0]), gpu_buf_dptr(b->bi[0]), 4 * P, 2 * P, 8);
+        launch_bdec_gemm(b, "bdec_lstm1_w8s5", a.A1, 2 * P, gpu_buf_dptr(b->wcati[1]), gpu_buf_dptr(b->bi[1]), 4 * P, 2 * P, 8);
+        launch_bdec_gemm(b, "bdec_pred_w4s5", a.hout, P, b->m->joint_pred_w, b->m->joint_pred_b, J, P, 4);
         gpu_launch(g, "bdec_joint_in", &a, sizeof a, (J + 255) / 256, R, 1, 256, 1, 1);
-        nk_gemm(g, a.jin, J, gpu_buf_dptr(b->wout), J, gpu_buf_dptr(b->bout), (float *)a.logits, Vp, R, Vp, J, NK_ACT_NONE, 0,
-                1.0f);
-        gpu_launch(g, "bdec_decide", &a, sizeof a, S, 1, 1, 256, 1, 1);
+        nk_gemm_argmax(g, a.jin, J, gpu_buf_dptr(b->wout), J, gpu_buf_dptr(b->bout), gpu_buf_dptr(b->keys),
+                       (uint32_t)b->nkeys, R, Vp, J, a.V);
+        gpu_launch(g, "bdec_decide", &a, sizeof a, S, 1, 1, 64, 1, 1);
     }
 }
 
@@ -1021,7 +1063,7 @@ static int decoder_batch_device(nemoasr_batch_t *b, int nact, char *err, size_t 
         gpu_begin(g);
         if (run == 0) {
             gpu_upload_async(g, gpu_buf_dptr(b->bsetup), su, (size_t)2 * S * sizeof(int));
-            gpu_launch(g, "bdec_setup", &a, sizeof a, (uint32_t)S, 1, 1, 256, 1, 1);
+            gpu_launch(g, "bdec_setup", &a, sizeof a, (uint32_t)S, 1, 1, 64, 1, 1);
         }
         if (b->use_graphs && !b->dgraph && !gpu_capture_begin(g)) {
             launch_bdec_steps(b, BDEC_STEPS);
@@ -1174,7 +1216,9 @@ void nemoasr_batch_debug_use_graphs(nemoasr_batch_t *b, int on) {
     }
 }
 
-void nemoasr_batch_debug_device_decoder(nemoasr_batch_t *b, int on) { b->device_dec = on; }
+void nemoasr_batch_debug_device_decoder(nemoasr_batch_t *b, int on) {
+    b->device_dec = on && b->P <= 640 && b->P % 16 == 0 && b->J % 16 == 0;
+}
 
 void nemoasr_batch_debug_set_dump(nemoasr_batch_t *b, int on) {
     b->dump = on;

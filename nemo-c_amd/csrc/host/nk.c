@@ -8,6 +8,13 @@
 #include <string.h>
 
 static int g_force = 0;
+static int g_mx_k64 = 0; /* many-row kernels with 64-wide K stages where K allows (measured: no gain) */
+
+int nk_gemm_mx_k64(int on) {
+    const int prev = g_mx_k64;
+    g_mx_k64 = on;
+    return prev;
+}
 
 int nk_gemm_force(int kind) {
     int prev = g_force;
@@ -113,7 +120,9 @@ static int launch_mx(gpu_t *g, NkGemmArgs *a, uint32_t M, uint32_t nout, uint32_
         const uint32_t t = ((M + cfg[i].bm - 1) / cfg[i].bm) * (nout / cols);
         if (cfg[i].bm == 128 && M < 512) continue;
         last_ok = i;
-        if (t >= 160) { pick_i = i; tiles = t; break; }
+        /* two workgroups per CU: the largest tile with at least ~400 tiles was the fastest at every
+         * measured shape (448 to 3584 rows, N 1024 to 4096, K 1024 and 4096) */
+        if (t >= 400) { pick_i = i; tiles = t; break; }
     }
     if (last_ok < 0) return 1;
     uint32_t kz = 1;
@@ -140,7 +149,27 @@ static int launch_mx(gpu_t *g, NkGemmArgs *a, uint32_t M, uint32_t nout, uint32_
     a->splits = kz;
     a->group_m = tm <= 8 ? tm : (tm + 3) / 4;
     const uint32_t total = tiles * kz, per = (total + 7) / 8;
-    return gpu_launch(g, glu ? cfg[pick_i].glu_name : cfg[pick_i].name, a, sizeof *a, 8 * per, 1, 1, 256, 1, 1);
+    /* K steps of 64 (half the barriers per MFMA) when every workgroup's share of K allows it */
+    const int k64 = K % 64 == 0 && g_mx_k64;
+    char name[40];
+    snprintf(name, sizeof name, "%s%s", glu ? cfg[pick_i].glu_name : cfg[pick_i].name, k64 ? "_k64" : "");
+    return gpu_launch(g, name, a, sizeof *a, 8 * per, 1, 1, 256, 1, 1);
+}
+
+int nk_gemm_argmax(gpu_t *g, const float *A, uint32_t lda, const uint16_t *W, uint32_t ldw, const float *bias,
+                   unsigned long long *keys, uint32_t keys_ld, uint32_t M, uint32_t N, uint32_t K, uint32_t V) {
+    if (!M) return 0;
+    if (N % 64 || K % 32 || V > N || keys_ld < 2 * (N / 64) || !aligned16(A) || !aligned16(W) || lda % 4 || ldw % 8)
+        return bad(g, "gemm_argmax: N % 64 == 0, K % 32 == 0, V <= N, keys_ld >= N/32, aligned operands");
+    NkGemmArgs a;
+    memset(&a, 0, sizeof a);
+    a.A = A; a.W = W; a.bias = bias; a.M = M; a.N = N; a.K = K; a.lda = lda; a.ldw = ldw; a.ldc = N;
+    a.alpha = 1.0f; a.splits = 1; a.keys = keys; a.keys_ld = keys_ld; a.keys_n = V;
+    const uint32_t tm = (M + 63) / 64, tiles = tm * (N / 64), per = (tiles + 7) / 8;
+    a.group_m = tm <= 8 ? tm : (tm + 3) / 4;
+    gpu_next_flops(g, 2.0 * M * N * K);
+    return gpu_launch(g, K % 64 == 0 && g_mx_k64 ? "gemm_mx64x64_argmax_k64" : "gemm_mx64x64_argmax", &a, sizeof a,
+                      8 * per, 1, 1, 256, 1, 1);
 }
 
 /* The GEMM with an optional LayerNorm prologue on A.  The weight-streaming GEMV applies it in

@@ -55,6 +55,10 @@ typedef struct {
     float *ln_out;
     u32 ln_mode;
     float ln_eps;
+    /* argmax epilogue of the many-row kernel (joint scores): per row, the best (score, lowest
+     * column) of each wavefront's columns < keys_n as a packed key, keys[row * keys_ld + part] */
+    unsigned long long *keys;
+    u32 keys_ld, keys_n;
 } NkGemmArgs;
 
 typedef struct {
@@ -282,6 +286,8 @@ typedef struct {
 
 typedef struct {
     NkBDecStream *st;      /* [S]                                                        */
+    const unsigned long long *keys; /* [S*W][nkeys] joint argmax partials (packed keys)     */
+    u32 nkeys, pad2;
     const int *setup;      /* [S][2] frames, first joint.enc row of a new chunk (setup)    */
     int *tokens;           /* [S][tok_ld] tokens emitted in the current chunk              */
     const float *enc;      /* joint.enc rows [*][J]                                        */

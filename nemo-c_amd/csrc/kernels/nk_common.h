@@ -153,6 +153,20 @@ __device__ __forceinline__ floatx4 mfma_bf16(uint4 a, uint4 b, floatx4 acc) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a), as_bf16x8(b), acc, 0, 0, 0);
 }
 
+/* (score, index) -> 64-bit key whose unsigned order is: higher score first, then lower index */
+__device__ __forceinline__ unsigned long long dec_key(float v, u32 n) {
+    v += 0.0f; /* -0 -> +0 so that equal scores compare equal */
+    const u32 b = __float_as_uint(v);
+    const u32 ord = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+    return ((unsigned long long)ord << 32) | (0xffffffffu - n);
+}
+__device__ __forceinline__ u32 dec_key_index(unsigned long long k) { return 0xffffffffu - (u32)(k & 0xffffffffu); }
+
+__device__ __forceinline__ unsigned long long shfl_xor_u64(unsigned long long v, int m) {
+    const u32 lo = (u32)__shfl_xor((int)(u32)v, m, 64), hi = (u32)__shfl_xor((int)(u32)(v >> 32), m, 64);
+    return ((unsigned long long)hi << 32) | lo;
+}
+
 typedef __attribute__((address_space(3))) char lds_char_t;
 
 /* 16 bytes per lane from global memory straight into LDS: lane i writes LDS bytes

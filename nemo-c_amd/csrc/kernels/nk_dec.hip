@@ -20,20 +20,6 @@
  * (lane l reads the 16-byte chunks l and l + 64 of every row). */
 #include "nk_common.h"
 
-/* (score, index) -> 64-bit key whose unsigned order is: higher score first, then lower index */
-__device__ __forceinline__ unsigned long long dec_key(float v, u32 n) {
-    v += 0.0f; /* -0 -> +0 so that equal scores compare equal */
-    const u32 b = __float_as_uint(v);
-    const u32 ord = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
-    return ((unsigned long long)ord << 32) | (0xffffffffu - n);
-}
-__device__ __forceinline__ u32 dec_key_index(unsigned long long k) { return 0xffffffffu - (u32)(k & 0xffffffffu); }
-
-__device__ __forceinline__ unsigned long long shfl_xor_u64(unsigned long long v, int m) {
-    const u32 lo = (u32)__shfl_xor((int)(u32)v, m, 64), hi = (u32)__shfl_xor((int)(u32)(v >> 32), m, 64);
-    return ((unsigned long long)hi << 32) | lo;
-}
-
 /* The decision of the previous joint, taken by one wavefront (every wavefront gets the same
  * answer).  Returns the new state; *tok = emitted token or -1. */
 __device__ __forceinline__ NkDecState dec_decide(const NkDecArgs &a, const NkDecState s, int *tok) {

@@ -5,13 +5,15 @@
  * Workgroup tile BM x BN, 4 wavefronts as WGM (along M) x 4/WGM (along N); each wavefront owns a
  * (BM/WGM) x (BN*WGM/4) block of 16x16 tiles of v_mfma_f32_16x16x32_bf16.
  *
- * Operand staging: a ring of NS LDS stages, each holding one K step (32) of A (f32, BM x 128 B)
- * and W (bf16, BN x 64 B).  Stages are filled by global_load_lds_dwordx4 (16 bytes per lane
+ * Operand staging: a ring of NS LDS stages (NS = 3..8 by tile size), each holding one K step of
+ * KS = 32 or 64 columns of A (f32, BM x 4KS B) and W (bf16, BN x 2KS B); a stage of 64 feeds two
+ * rounds of MFMAs per barrier.  Stages are filled by global_load_lds_dwordx4 (16 bytes per lane
  * straight into LDS, no registers), issued NS-1 steps ahead of their use, so a wavefront only waits
  * for a stage's loads right before the barrier that publishes it.  A DMA instruction writes 64
  * consecutive 16-byte LDS granules in lane order; the global address each lane reads is chosen so
  * that granule g of row r holds K-granule (g ^ swizzle(r)), which makes the 16-row fragment reads
- * (ds_read_b128) hit distinct banks.
+ * (ds_read_b128) hit distinct banks (swz_a / swz_b below; measured: the plain r % 8 swizzle left
+ * half the accesses conflicting and cost a third of the kernel time at 3584 rows).
  *
  * A is f32 in memory and in LDS; each fragment (8 consecutive K of one row per lane) is split in
  * registers into bf16 hi = RNE(a) and lo = RNE(a - hi) (v_cvt_pk_bf16_f32), and every K step
@@ -27,14 +29,28 @@
  * no activation). */
 #include "nk_common.h"
 
-template <int BM, int BN, int WGM, int NS, bool GLU>
+/* LDS granule swizzles.  A 16-byte fragment read of 16 consecutive rows at one K granule is
+ * served 16 lanes per cycle (64 banks): granule g of row r lives in slot g ^ swz(r), chosen so the
+ * 16 rows land in 16 different bank groups (and 8 consecutive rows in 8, for 8-lane service).
+ * A rows hold 8 granules (K stage 32) or 16 (64); W rows 4 or 8. */
+__device__ __forceinline__ u32 swz_a(u32 r, int ag) {
+    return ag == 16 ? (r & 15) : (((r >> 1) & 7) ^ ((r & 1) << 2));
+}
+__device__ __forceinline__ u32 swz_b(u32 n, int bg) {
+    return bg == 4 ? (((n >> 1) & 3) ^ ((n >> 3) & 1)) : (((n >> 1) & 7) ^ ((n & 1) << 2));
+}
+
+template <int BM, int BN, int WGM, int NS, int KS, bool GLU, int EPI = 0>
 __device__ __forceinline__ void mx_impl(const NkGemmArgs &a, lds_char_t *const (&ring)[NS]) {
     constexpr int WGN = 4 / WGM;
     constexpr int WTM = BM / WGM, WTN = BN / WGN;
     constexpr int TI = WTM / 16, TJ = WTN / 16;
-    constexpr int A_BYTES = BM * 128, STAGE = A_BYTES + BN * 64;
-    constexpr int AI = BM * 8 / 256; /* A granules per thread per stage */
-    constexpr int BI = BN * 4 / 256; /* W granules per thread per stage */
+    constexpr int AG = KS / 4, BG = KS / 8; /* 16-byte granules per A row / W row of a stage */
+    constexpr int H = KS / 32;              /* 32-wide MFMA steps per stage */
+    constexpr int A_BYTES = BM * KS * 4;
+    constexpr int AI = BM * AG / 256; /* A granules per thread per stage */
+    constexpr int BI = BN * BG / 256; /* W granules per thread per stage */
+    static_assert(KS == 32 || KS == 64, "stage width");
     static_assert(AI >= 1 && BI >= 1 && TI >= 1 && TJ >= (GLU ? 2 : 1), "tile shape");
     const u32 tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const u32 wm = wave / WGN, wn = wave % WGN;
@@ -52,7 +68,7 @@ __device__ __forceinline__ void mx_impl(const NkGemmArgs &a, lds_char_t *const (
     const u32 tm = first + within % gh, tn = within / gh;
     const u32 m0 = tm * BM;
     const u32 c0 = tn * (GLU ? BN / 2 : BN); /* first output column */
-    const u32 S = a.K >> 5;
+    const u32 S = a.K / KS;
     const u32 s_begin = (u32)(((u64)S * kz) / KZ), s_end = (u32)(((u64)S * (kz + 1)) / KZ);
     const u32 nst = s_end - s_begin;
 
@@ -61,43 +77,47 @@ __device__ __forceinline__ void mx_impl(const NkGemmArgs &a, lds_char_t *const (
     const float *asrc[AI];
 #pragma unroll
     for (int j = 0; j < AI; ++j) {
-        const u32 p = (4 * j + wave) * 64 + lane, r = p >> 3, kg = (p & 7) ^ (r & 7);
-        asrc[j] = a.A + (u64)min(m0 + r, M - 1) * a.lda + 4 * kg + (u64)s_begin * 32;
+        const u32 p = (4 * j + wave) * 64 + lane, r = p / AG, kg = (p % AG) ^ swz_a(r, AG);
+        asrc[j] = a.A + (u64)min(m0 + r, M - 1) * a.lda + 4 * kg + (u64)s_begin * KS;
     }
     const u16 *bsrc[BI];
 #pragma unroll
     for (int j = 0; j < BI; ++j) {
-        const u32 p = (4 * j + wave) * 64 + lane, n = p >> 2, kg = (p & 3) ^ ((n >> 1) & 3);
+        const u32 p = (4 * j + wave) * 64 + lane, n = p / BG, kg = (p % BG) ^ swz_b(n, BG);
         u32 col;
         if (GLU) col = n < BN / 2 ? c0 + n : a.N / 2 + c0 + (n - BN / 2);
         else col = c0 + n;
-        bsrc[j] = a.W + (u64)col * a.ldw + 8 * kg + (u64)s_begin * 32;
+        bsrc[j] = a.W + (u64)col * a.ldw + 8 * kg + (u64)s_begin * KS;
     }
     auto issue = [&](u32 q, int slot) { /* loads of local step q into ring slot `slot` */
         lds_char_t *st = ring[slot];
 #pragma unroll
-        for (int j = 0; j < AI; ++j) dma16(asrc[j] + (u64)q * 32, st + (4 * j + wave) * 1024);
+        for (int j = 0; j < AI; ++j) dma16(asrc[j] + (u64)q * KS, st + (4 * j + wave) * 1024);
 #pragma unroll
-        for (int j = 0; j < BI; ++j) dma16(bsrc[j] + (u64)q * 32, st + A_BYTES + (4 * j + wave) * 1024);
+        for (int j = 0; j < BI; ++j) dma16(bsrc[j] + (u64)q * KS, st + A_BYTES + (4 * j + wave) * 1024);
     };
 
     /* fragment addresses inside a stage */
     const u32 fr = lane & 15, fg = lane >> 4;
-    u32 aoff[TI][2];
+    u32 aoff[H][TI][2];
 #pragma unroll
-    for (int i = 0; i < TI; ++i) {
-        const u32 r = wm * WTM + 16 * i + fr;
-        aoff[i][0] = (r * 8 + ((2 * fg) ^ (r & 7))) * 16;
-        aoff[i][1] = (r * 8 + ((2 * fg + 1) ^ (r & 7))) * 16;
-    }
-    u32 boff[TJ];
+    for (int h = 0; h < H; ++h)
+#pragma unroll
+        for (int i = 0; i < TI; ++i) {
+            const u32 r = wm * WTM + 16 * i + fr;
+            aoff[h][i][0] = (r * AG + ((8 * h + 2 * fg) ^ swz_a(r, AG))) * 16;
+            aoff[h][i][1] = (r * AG + ((8 * h + 2 * fg + 1) ^ swz_a(r, AG))) * 16;
+        }
+    u32 boff[H][TJ];
 #pragma unroll
     for (int j = 0; j < TJ; ++j) {
         u32 n;
         if (GLU) n = j < TJ / 2 ? wn * (WTN / 2) + 16 * j : BN / 2 + wn * (WTN / 2) + 16 * (j - TJ / 2);
         else n = wn * WTN + 16 * j;
         n += fr;
-        boff[j] = A_BYTES + (n * 4 + (fg ^ ((n >> 1) & 3))) * 16;
+#pragma unroll
+        for (int h = 0; h < H; ++h)
+            boff[h][j] = A_BYTES + (n * BG + ((4 * h + fg) ^ swz_b(n, BG))) * 16;
     }
 
     floatx4 acc[TI][TJ];
@@ -122,29 +142,69 @@ __device__ __forceinline__ void mx_impl(const NkGemmArgs &a, lds_char_t *const (
         barrier_mem();
         issue(min(q + NS - 1, nst - 1), (u + NS - 1) % NS);
         const lds_char_t *st = ring[u];
-        uint4 fb[TJ];
 #pragma unroll
-        for (int j = 0; j < TJ; ++j) fb[j] = *(const __attribute__((address_space(3))) uint4 *)(st + boff[j]);
-        uint4 fh[TI], fl[TI];
+        for (int h = 0; h < H; ++h) {
+            uint4 fb[TJ];
 #pragma unroll
-        for (int i = 0; i < TI; ++i) {
-            const floatx4 x0 = *(const __attribute__((address_space(3))) floatx4 *)(st + aoff[i][0]);
-            const floatx4 x1 = *(const __attribute__((address_space(3))) floatx4 *)(st + aoff[i][1]);
-            const float x[8] = { x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3] };
-            split8(x, fh[i], fl[i]);
+            for (int j = 0; j < TJ; ++j) fb[j] = *(const __attribute__((address_space(3))) uint4 *)(st + boff[h][j]);
+            uint4 fh[TI], fl[TI];
+#pragma unroll
+            for (int i = 0; i < TI; ++i) {
+                const floatx4 x0 = *(const __attribute__((address_space(3))) floatx4 *)(st + aoff[h][i][0]);
+                const floatx4 x1 = *(const __attribute__((address_space(3))) floatx4 *)(st + aoff[h][i][1]);
+                const float x[8] = { x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3] };
+                split8(x, fh[i], fl[i]);
+            }
+#pragma unroll
+            for (int i = 0; i < TI; ++i)
+#pragma unroll
+                for (int j = 0; j < TJ; ++j) acc[i][j] = mfma_bf16(fh[i], fb[j], acc[i][j]);
+#pragma unroll
+            for (int i = 0; i < TI; ++i)
+#pragma unroll
+                for (int j = 0; j < TJ; ++j) acc[i][j] = mfma_bf16(fl[i], fb[j], acc[i][j]);
         }
-#pragma unroll
-        for (int i = 0; i < TI; ++i)
-#pragma unroll
-            for (int j = 0; j < TJ; ++j) acc[i][j] = mfma_bf16(fh[i], fb[j], acc[i][j]);
-#pragma unroll
-        for (int i = 0; i < TI; ++i)
-#pragma unroll
-            for (int j = 0; j < TJ; ++j) acc[i][j] = mfma_bf16(fl[i], fb[j], acc[i][j]);
     }
     }
 
     wait_vm_lgkm<0>(); /* no load into LDS may land after the workgroup ends */
+
+    if constexpr (EPI == 1) {
+        /* argmax partials: per row, the best (score + bias, lowest column) over this wavefront's
+         * columns below keys_n, as one packed key per (row, column tile, wavefront column) */
+        unsigned long long best[TI][4];
+#pragma unroll
+        for (int i = 0; i < TI; ++i)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) best[i][e] = 0;
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) {
+            const u32 col = c0 + wn * WTN + 16 * j + fr;
+            const bool ok = col < a.keys_n;
+            const float bj = a.bias ? a.bias[col] : 0.0f;
+#pragma unroll
+            for (int i = 0; i < TI; ++i)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const unsigned long long k = ok ? dec_key(acc[i][j][e] + bj, col) : 0ull;
+                    best[i][e] = k > best[i][e] ? k : best[i][e];
+                }
+        }
+#pragma unroll
+        for (int i = 0; i < TI; ++i)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                unsigned long long k = best[i][e];
+#pragma unroll
+                for (int msk = 1; msk < 16; msk <<= 1) {
+                    const unsigned long long o = shfl_xor_u64(k, msk);
+                    k = o > k ? o : k;
+                }
+                const u32 r = m0 + wm * WTM + 16 * i + 4 * fg + e;
+                if (fr == 0 && r < M) a.keys[(u64)r * a.keys_ld + tn * WGN + wn] = k;
+            }
+        return;
+    }
 
     /* epilogue: lane l holds rows 16 i + 4 (l/16) + e, column 16 j + l%16 of each tile; every
      * operand (row map, bias, the C values to accumulate into) is loaded before the first store */
@@ -199,17 +259,30 @@ __device__ __forceinline__ void mx_impl(const NkGemmArgs &a, lds_char_t *const (
     }
 }
 
-#define GEMM_MX(NAME, BM, BN, WGM, GLU)                                                                   \
+/* NS ring stages of KS-wide K steps: (BM*4 + BN*2)*KS bytes each, sized so that two workgroups fit
+ * a CU's 160 KB of LDS (measured: the second workgroup overlaps one's loads and barriers with the
+ * other's MFMAs; 3584 rows, 128x128: 117 -> 79 us with the swizzles).  K % 32 kernels: 3 x 24 KB
+ * for 128x128, 4 x 16 KB for 64x128, 4 x 12 KB for 64x64; K % 64 kernels (suffix _k64, half the
+ * barriers per MFMA): 2 x 48 KB, 2 x 32 KB, 3 x 24 KB */
+#define GEMM_MX(NAME, BM, BN, WGM, NS, KS, GLU, EPI)                                                      \
     extern "C" __global__ __launch_bounds__(256) void NAME(const NkGemmArgs a) {                          \
-        __shared__ uint4 r0[(BM * 128 + BN * 64) / 16], r1[(BM * 128 + BN * 64) / 16];                    \
-        __shared__ uint4 r2[(BM * 128 + BN * 64) / 16], r3[(BM * 128 + BN * 64) / 16];                    \
-        lds_char_t *const ring[4] = { (lds_char_t *)r0, (lds_char_t *)r1, (lds_char_t *)r2,              \
-                                      (lds_char_t *)r3 };                                                 \
-        mx_impl<BM, BN, WGM, 4, GLU>(a, ring);                                                            \
+        __shared__ uint4 ring_mem[NS][(BM * 4 + BN * 2) * KS / 16];                                      \
+        lds_char_t *ring[NS];                                                                             \
+        _Pragma("unroll") for (int i = 0; i < NS; ++i) ring[i] = (lds_char_t *)ring_mem[i];               \
+        mx_impl<BM, BN, WGM, NS, KS, GLU, EPI>(a, ring);                                                  \
     }
-GEMM_MX(gemm_mx128x128, 128, 128, 2, false)
-GEMM_MX(gemm_mx64x128, 64, 128, 2, false)
-GEMM_MX(gemm_mx64x64, 64, 64, 2, false)
-GEMM_MX(gemm_mx128x128_glu, 128, 128, 2, true)
-GEMM_MX(gemm_mx64x128_glu, 64, 128, 2, true)
-GEMM_MX(gemm_mx64x64_glu, 64, 64, 2, true)
+GEMM_MX(gemm_mx128x128, 128, 128, 2, 3, 32, false, 0)
+GEMM_MX(gemm_mx64x128, 64, 128, 2, 4, 32, false, 0)
+GEMM_MX(gemm_mx64x64, 64, 64, 2, 4, 32, false, 0)
+GEMM_MX(gemm_mx128x128_glu, 128, 128, 2, 3, 32, true, 0)
+GEMM_MX(gemm_mx64x128_glu, 64, 128, 2, 4, 32, true, 0)
+GEMM_MX(gemm_mx64x64_glu, 64, 64, 2, 4, 32, true, 0)
+GEMM_MX(gemm_mx128x128_k64, 128, 128, 2, 2, 64, false, 0)
+GEMM_MX(gemm_mx64x128_k64, 64, 128, 2, 2, 64, false, 0)
+GEMM_MX(gemm_mx64x64_k64, 64, 64, 2, 3, 64, false, 0)
+GEMM_MX(gemm_mx128x128_glu_k64, 128, 128, 2, 2, 64, true, 0)
+GEMM_MX(gemm_mx64x128_glu_k64, 64, 128, 2, 2, 64, true, 0)
+GEMM_MX(gemm_mx64x64_glu_k64, 64, 64, 2, 3, 64, true, 0)
+/* joint scores -> argmax partials (keys), 64x64 tiles: two keys per row per column tile */
+GEMM_MX(gemm_mx64x64_argmax, 64, 64, 2, 4, 32, false, 1)
+GEMM_MX(gemm_mx64x64_argmax_k64, 64, 64, 2, 3, 64, false, 1)

@@ -184,8 +184,8 @@ extern "C" __global__ __launch_bounds__(512) void attention_rel(const NkAttnArgs
 /* Relative-position attention of whole chunks (batched streams), the math of attention_rel above
  * (reference src/kernels.metal:290-348).  One workgroup per (head, chunk): the chunk's L = cached
  * + c keys and values and its L + c - 1 position rows are brought into LDS by direct global -> LDS
- * loads (16 bytes per lane, granule g of row r stored at slot g ^ (r % 8), so the row-parallel
- * 16-byte reads below are conflict-free), then every query row of the chunk is scored against
+ * loads (16 bytes per lane, granule g of row r stored at slot g ^ (r % 16), so the row-parallel
+ * 16-byte reads below, 16 lanes per cycle, are conflict-free), then every query row of the chunk is scored against
  * them: wavefront w takes rows w, w+4, ...; lane l takes keys l and l+64; softmax by wavefront
  * reductions; output lane l accumulates dims 2l, 2l+1 over the keys in order. */
 extern "C" __global__ __launch_bounds__(256) void attention_rel_chunks(const NkAttnChunkArgs a) {
@@ -205,12 +205,12 @@ extern "C" __global__ __launch_bounds__(256) void attention_rel_chunks(const NkA
     /* LDS granule p = 32 r + s of a table holds granule s ^ (r % 8) of row r; one DMA instruction
      * fills 64 granules (two rows); rows past the end re-read the last row (never used) */
     for (u32 blk = wave; blk < (L + 1) / 2; blk += 4) {
-        const u32 p = blk * 64 + lane, r = p >> 5, g = (p & 31) ^ (r & 7), rr = min(r, L - 1);
+        const u32 p = blk * 64 + lane, r = p >> 5, g = (p & 31) ^ (r & 15), rr = min(r, L - 1);
         dma16(Kg + (u64)rr * a.ld + 4 * g, (lds_char_t *)&Ks[blk * 64]);
         dma16(Vg + (u64)rr * a.ld + 4 * g, (lds_char_t *)&Vs[blk * 64]);
     }
     for (u32 blk = wave; blk < (NP + 1) / 2; blk += 4) {
-        const u32 p = blk * 64 + lane, r = p >> 5, g = (p & 31) ^ (r & 7), rr = min(r, NP - 1);
+        const u32 p = blk * 64 + lane, r = p >> 5, g = (p & 31) ^ (r & 15), rr = min(r, NP - 1);
         dma16(Pg + (u64)rr * a.D + 4 * g, (lds_char_t *)&Ps[blk * 64]);
     }
     for (u32 idx = tid; idx < c * 32; idx += 256) {
@@ -230,7 +230,7 @@ extern "C" __global__ __launch_bounds__(256) void attention_rel_chunks(const NkA
 #pragma unroll 8
             for (u32 g = 0; g < 32; ++g) {
                 const floatx4 u = qu[i * 32 + g], w = qv[i * 32 + g];
-                const floatx4 k = Ks[j0 * 32 + (g ^ (j0 & 7))], pp = Ps[p0 * 32 + (g ^ (p0 & 7))];
+                const floatx4 k = Ks[j0 * 32 + (g ^ (j0 & 15))], pp = Ps[p0 * 32 + (g ^ (p0 & 15))];
                 s0 += u[0] * k[0] + u[1] * k[1] + u[2] * k[2] + u[3] * k[3];
                 s0 += w[0] * pp[0] + w[1] * pp[1] + w[2] * pp[2] + w[3] * pp[3];
             }
@@ -239,7 +239,7 @@ extern "C" __global__ __launch_bounds__(256) void attention_rel_chunks(const NkA
 #pragma unroll 8
             for (u32 g = 0; g < 32; ++g) {
                 const floatx4 u = qu[i * 32 + g], w = qv[i * 32 + g];
-                const floatx4 k = Ks[j1 * 32 + (g ^ (j1 & 7))], pp = Ps[p1 * 32 + (g ^ (p1 & 7))];
+                const floatx4 k = Ks[j1 * 32 + (g ^ (j1 & 15))], pp = Ps[p1 * 32 + (g ^ (p1 & 15))];
                 s1 += u[0] * k[0] + u[1] * k[1] + u[2] * k[2] + u[3] * k[3];
                 s1 += w[0] * pp[0] + w[1] * pp[1] + w[2] * pp[2] + w[3] * pp[3];
             }
@@ -258,7 +258,7 @@ extern "C" __global__ __launch_bounds__(256) void attention_rel_chunks(const NkA
         float o0 = 0.0f, o1 = 0.0f;
         for (u32 j = 0; j < L; ++j) {
             const float pj = sc[i][j];
-            const floatx4 v = Vs[j * 32 + (gq ^ (j & 7))];
+            const floatx4 v = Vs[j * 32 + (gq ^ (j & 15))];
             o0 += pj * v[hf];
             o1 += pj * v[hf + 1];
         }

@@ -107,16 +107,55 @@ def test_gemm_many_rows(gpu, M, N, K, act):
     (445, 4096, 1024, 1, 0, False), (1000, 2048, 1024, 3, 0, False), (3584, 1024, 1024, 0, 1, False),
     (20, 3072, 1024, 0, 0, False), (448, 2560, 1280, 0, 0, True), (1024, 1088, 640, 0, 0, True),
     (64, 256, 32, 2, 0, True), (96, 128, 64, 0, 1, False)])
-def test_gemm_batched_rows(gpu, M, N, K, act, acc, bias):
+@pytest.mark.parametrize("k64", [1, 0])
+def test_gemm_batched_rows(gpu, M, N, K, act, acc, bias, k64):
+    import nemoasr
+
+    nemoasr.lib().nk_gemm_mx_k64(k64)
     rng = np.random.default_rng([M, N, K, act])
     W = _w(rng, N, K)
     A = rng.standard_normal((M, K)).astype(np.float32)
     b = (0.1 * rng.standard_normal(N)).astype(np.float32) if bias else None
     nout = N // 2 if act == 3 else N
     C0 = rng.standard_normal((M, nout)).astype(np.float32) if acc else None
-    got = run_gemm(gpu, A, W, b, act, acc, 0.5 if acc else 1.0, C0=C0)
+    try:
+        got = run_gemm(gpu, A, W, b, act, acc, 0.5 if acc else 1.0, C0=C0)
+    finally:
+        nemoasr.lib().nk_gemm_mx_k64(1)
     ref = oracle.gemm(A, W, b, act, acc, 0.5 if acc else 1.0, C0=C0)
     assert rel_err(got, ref) < GEMM_TOL, (M, N, K, act)
+
+
+@pytest.mark.parametrize("M,V", [(576, 1025), (64, 1025), (100, 97), (4096, 1025)])
+def test_gemm_argmax_keys(gpu, M, V):
+    """Row argmax of the joint scores from the GEMM's key epilogue: the best key over a row's column
+    parts names the oracle's argmax (lowest index on ties), padding columns never win."""
+    import nemoasr
+
+    L = nemoasr.lib()
+    rng = np.random.default_rng([M, V])
+    J, N = 640, ((V + 63) // 64) * 64
+    W = np.zeros((N, J), np.uint16)
+    W[:V] = _w(rng, V, J)
+    bias = np.zeros(N, np.float32)
+    bias[:V] = rng.standard_normal(V).astype(np.float32)
+    A = np.maximum(rng.standard_normal((M, J)), 0).astype(np.float32)
+    A[1] = A[0]  # identical rows
+    nk = N // 32
+    dA, dW, dB, dK = gpu.put(A), gpu.put(W), gpu.put(bias), gpu.alloc(M * nk * 8)
+    gpu.begin()
+    gpu.check(L.nk_gemm_argmax(gpu.h, dA.ptr, J, dW.ptr, J, dB.ptr, dK.ptr, nk, M, N, J, V))
+    gpu.end()
+    keys = dK.read((M, nk), np.uint64)
+    got = (0xFFFFFFFF - (keys.max(axis=1) & 0xFFFFFFFF)).astype(np.int64)
+    scores = oracle.gemm(A, W[:V], bias[:V], 0, False, 1.0)
+    ref = scores.argmax(axis=1)
+    # the GPU sums in another order: accept a different winner only on a near tie
+    bad = np.nonzero(got != ref)[0]
+    for r in bad:
+        assert abs(scores[r, got[r]] - scores[r, ref[r]]) < 1e-4 * max(1.0, abs(scores[r, ref[r]])), r
+    assert len(bad) <= max(1, M // 500)
+    assert got[0] == got[1]
 
 
 def test_gemm_batched_row_map(gpu):
