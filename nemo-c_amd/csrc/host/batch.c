@@ -119,7 +119,7 @@ struct nemoasr_batch {
     int *stage_dtab, *stage_amax;
     /* device-resident loop (kernels/nk_bdec.hip) */
     int device_dec, W, tok_ld;
-    gpu_buf_t *bst, *bsetup, *btok, *lin1, *gates1, *predtmp, *wcati[2], *bi[2], *keys;
+    gpu_buf_t *bst, *bsetup, *btok, *lin1, *tx, *wcati[2], *bi[2], *keys;
     int nkeys;
     NkBDecStream *stage_bst;
     int *stage_bsetup, *stage_btok;
@@ -209,6 +209,32 @@ static int build_decoder_weights(nemoasr_batch_t *b) {
         free(bh);
         free(bih);
     }
+    /* layer-0 input table Tx = embed . Wx0^T + b0 (rows interleaved like wcati), one row per token
+       and the blank row (zero input: the bias); the device loop looks it up instead of multiplying
+       the embedding half of [x | h0] */
+    const size_t NT = (size_t)m->cfg.blank_id + 1;
+    uint16_t *eb = malloc(NT * P * 2);
+    float *ef = malloc(NT * P * sizeof(float));
+    gpu_buf_t *edev = gpu_buf_alloc(g, NT * P * sizeof(float));
+    b->tx = gpu_buf_alloc(g, NT * 4 * P * sizeof(float));
+    rc |= !eb || !ef || !edev || !b->tx;
+    if (!rc) {
+        rc |= gpu_download(g, eb, m->embed_dev, NT * P * 2);
+        for (size_t i = 0; i < NT * P; ++i) {
+            const uint32_t u = (uint32_t)eb[i] << 16;
+            memcpy(&ef[i], &u, sizeof u);
+            if (i / P == (size_t)m->cfg.blank_id) ef[i] = 0.0f;
+        }
+        rc |= gpu_upload(g, gpu_buf_dptr(edev), ef, NT * P * sizeof(float));
+        rc |= gpu_begin(g);
+        rc |= nk_gemm(g, gpu_buf_dptr(edev), (uint32_t)P, gpu_buf_dptr(b->wcati[0]), (uint32_t)(2 * P),
+                      gpu_buf_dptr(b->bi[0]), gpu_buf_dptr(b->tx), (uint32_t)(4 * P), (uint32_t)NT, (uint32_t)(4 * P),
+                      (uint32_t)P, NK_ACT_NONE, 0, 1.0f) < 0;
+        rc |= gpu_end(g, NULL, 0);
+    }
+    free(eb);
+    free(ef);
+    gpu_buf_free(edev);
     uint16_t *wo = calloc(Vp * J, 2);
     float *bo = calloc(Vp, sizeof(float));
     rc |= gpu_download(g, wo, m->joint_out_w, V * J * 2);
@@ -223,6 +249,13 @@ static int build_decoder_weights(nemoasr_batch_t *b) {
     free(wo);
     free(bo);
     return rc;
+}
+
+/* the device loop's GEMMs cover K = 2P <= 1280 and K = P <= 640 in one pass of their wavefronts,
+   its decision scores at most 16 frames with at most 64 keys each; other shapes use the host-driven
+   loop */
+static int device_dec_ok(const nemoasr_batch_t *b) {
+    return b->P <= 640 && b->P % 32 == 0 && b->J % 32 == 0 && b->W <= NK_ATTC_MAX_C && b->nkeys <= 64;
 }
 
 static void stream_clear(nemoasr_batch_t *b, int s) {
@@ -364,8 +397,6 @@ nemoasr_batch_t *nemoasr_batch_open(const char *model_dir, const char *language,
     b->bsetup = gpu_buf_alloc(g, 2 * S * sizeof(int));
     b->btok = gpu_buf_alloc(g, S * (size_t)b->tok_ld * sizeof(int));
     b->lin1 = gpu_buf_alloc(g, S * 2 * P * fs);
-    b->gates1 = gpu_buf_alloc(g, S * 4 * P * fs);
-    b->predtmp = gpu_buf_alloc(g, S * J * fs);
     b->stage_bst = gpu_host_alloc(g, S * sizeof(NkBDecStream));
     b->stage_bsetup = gpu_host_alloc(g, 2 * S * sizeof(int));
     b->stage_btok = gpu_host_alloc(g, S * (size_t)b->tok_ld * sizeof(int));
@@ -395,9 +426,7 @@ nemoasr_batch_t *nemoasr_batch_open(const char *model_dir, const char *language,
             nemoasr_batch_close(b);
             return NULL;
         }
-    /* the device loop's GEMMs cover K = 2P <= 1280 and K = P <= 640 in one pass of their
-       wavefronts; larger prediction networks use the host-driven loop */
-    b->device_dec = b->P <= 640 && b->P % 16 == 0 && b->J % 16 == 0;
+    b->device_dec = device_dec_ok(b);
     b->fe_list = malloc(S * sizeof(int));
     pool_start(&b->pool, b);
     b->use_graphs = 1;
@@ -414,8 +443,8 @@ void nemoasr_batch_close(nemoasr_batch_t *b) {
     gpu_buf_t *bufs[] = { b->win, b->c0, b->c1, b->c2, b->c3, b->c4, b->flat, b->pre_out, b->h, b->tmp, b->lnb,
                           b->ff, b->att, b->y, b->ph, b->prompted, b->joint_enc, b->kv, b->din, b->etab, b->wcat[0],
                           b->wcat[1], b->wout, b->bout, b->hc, b->lin, b->gates, b->hout, b->hout2, b->pred,
-                          b->jin, b->logits, b->amax, b->dtab, b->bst, b->bsetup, b->btok, b->lin1, b->gates1,
-                          b->predtmp, b->wcati[0], b->wcati[1], b->bi[0], b->bi[1], b->keys };
+                          b->jin, b->logits, b->amax, b->dtab, b->bst, b->bsetup, b->btok, b->lin1, b->tx,
+                          b->wcati[0], b->wcati[1], b->bi[0], b->bi[1], b->keys };
     for (size_t i = 0; i < sizeof bufs / sizeof *bufs; ++i) gpu_buf_free(bufs[i]);
     gpu_host_free(b->stage_win);
     gpu_host_free(b->stage_tab);
@@ -978,26 +1007,17 @@ static NkBDecArgs bdec_args(nemoasr_batch_t *b) {
     a.setup = gpu_buf_dptr(b->bsetup);
     a.tokens = gpu_buf_dptr(b->btok);
     a.enc = gpu_buf_dptr(b->joint_enc);
-    a.embed = m->embed_dev;
+    a.tx = gpu_buf_dptr(b->tx);
     a.hc = gpu_buf_dptr(b->hc);
     a.A0 = gpu_buf_dptr(b->lin);
     a.A1 = gpu_buf_dptr(b->lin1);
-    a.g0 = gpu_buf_dptr(b->gates);
-    a.g1 = gpu_buf_dptr(b->gates1);
-    a.b0 = m->lstm_b[0];
-    a.b1 = m->lstm_b[1];
     a.hout = gpu_buf_dptr(b->hout);
-    a.predtmp = gpu_buf_dptr(b->predtmp);
     a.pred = gpu_buf_dptr(b->pred);
-    a.bjp = m->joint_pred_b;
     a.jin = gpu_buf_dptr(b->jin);
-    a.logits = gpu_buf_dptr(b->logits);
     a.S = (uint32_t)b->S;
     a.W = (uint32_t)b->W;
     a.P = (uint32_t)b->P;
     a.J = (uint32_t)b->J;
-    a.V = (uint32_t)b->V;
-    a.ldl = (uint32_t)b->Vp;
     a.blank = (uint32_t)m->cfg.blank_id;
     a.max_symbols = (uint32_t)m->cfg.max_symbols;
     a.tok_ld = (uint32_t)b->tok_ld;
@@ -1011,13 +1031,13 @@ typedef struct {
 } bdec_launch_t;
 
 static int launch_bdec_gemm(nemoasr_batch_t *b, const char *kernel, const float *A, uint32_t lda, const uint16_t *W,
-                            const float *bias, uint32_t N, uint32_t K, uint32_t waves) {
+                            uint32_t ldw, const float *bias, uint32_t N, uint32_t K, uint32_t waves) {
     bdec_launch_t x;
     memset(&x, 0, sizeof x);
     x.g.A = A;
     x.g.lda = lda;
     x.g.W = W;
-    x.g.ldw = K;
+    x.g.ldw = ldw;
     x.g.bias = bias;
     x.g.M = (uint32_t)b->S;
     x.g.N = N;
@@ -1029,14 +1049,16 @@ static int launch_bdec_gemm(nemoasr_batch_t *b, const char *kernel, const float 
 static void launch_bdec_steps(nemoasr_batch_t *b, int steps) {
     gpu_t *g = b->g;
     const NkBDecArgs a = bdec_args(b);
-    const uint32_t S = a.S, P = a.P, J = a.J, Vp = a.ldl, R = a.S * a.W;
+    const uint32_t S = a.S, P = a.P, J = a.J, Vp = (uint32_t)b->Vp, R = a.S * a.W;
     for (int k = 0; k < steps; ++k) {
-        launch_bdec_gemm(b, "bdec_lstm0_w8s5", a.A0, 2 * P, gpu_buf_dptr(b->wcati[0]), gpu_buf_dptr(b->bi[0]), 4 * P, 2 * P, 8);
-        launch_bdec_gemm(b, "bdec_lstm1_w8s5", a.A1, 2 * P, gpu_buf_dptr(b->wcati[1]), gpu_buf_dptr(b->bi[1]), 4 * P, 2 * P, 8);
-        launch_bdec_gemm(b, "bdec_pred_w4s5", a.hout, P, b->m->joint_pred_w, b->m->joint_pred_b, J, P, 4);
-        gpu_launch(g, "bdec_joint_in", &a, sizeof a, (J + 255) / 256, R, 1, 256, 1, 1);
+        /* layer 0: the Wh0 half of the interleaved [Wx0 | Wh0] rows (row stride 2P) */
+        launch_bdec_gemm(b, "bdec_lstm0_w4s5", a.A0, P, (const uint16_t *)gpu_buf_dptr(b->wcati[0]) + P, 2 * P, NULL,
+                         4 * P, P, 4);
+        launch_bdec_gemm(b, "bdec_lstm1_w8s5", a.A1, 2 * P, gpu_buf_dptr(b->wcati[1]), 2 * P, gpu_buf_dptr(b->bi[1]),
+                         4 * P, 2 * P, 8);
+        launch_bdec_gemm(b, "bdec_pred_w4s5", a.hout, P, b->m->joint_pred_w, P, b->m->joint_pred_b, J, P, 4);
         nk_gemm_argmax(g, a.jin, J, gpu_buf_dptr(b->wout), J, gpu_buf_dptr(b->bout), gpu_buf_dptr(b->keys),
-                       (uint32_t)b->nkeys, R, Vp, J, a.V);
+                       (uint32_t)b->nkeys, R, Vp, J, (uint32_t)b->V);
         gpu_launch(g, "bdec_decide", &a, sizeof a, S, 1, 1, 64, 1, 1);
     }
 }
@@ -1217,7 +1239,7 @@ void nemoasr_batch_debug_use_graphs(nemoasr_batch_t *b, int on) {
 }
 
 void nemoasr_batch_debug_device_decoder(nemoasr_batch_t *b, int on) {
-    b->device_dec = on && b->P <= 640 && b->P % 16 == 0 && b->J % 16 == 0;
+    b->device_dec = on && device_dec_ok(b);
 }
 
 void nemoasr_batch_debug_set_dump(nemoasr_batch_t *b, int on) {

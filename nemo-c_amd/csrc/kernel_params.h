@@ -291,17 +291,14 @@ typedef struct {
     const int *setup;      /* [S][2] frames, first joint.enc row of a new chunk (setup)    */
     int *tokens;           /* [S][tok_ld] tokens emitted in the current chunk              */
     const float *enc;      /* joint.enc rows [*][J]                                        */
-    const u16 *embed;      /* [blank + 1][P] bf16                                          */
+    const float *tx;       /* [blank + 1][4P] embed . Wx0^T + b0, rows interleaved by unit */
     float *hc;             /* [S][2 slot sets][h0, c0, h1, c1][P]                          */
-    float *A0, *A1;        /* [S][2P] LSTM layer inputs [x | h]                            */
-    float *g0, *g1;        /* [S][4P] gates (initialised to the bias, GEMMs accumulate)    */
-    const float *b0, *b1;  /* [4P]                                                         */
+    float *A0;             /* [S][P] layer-0 input h0                                      */
+    float *A1;             /* [S][2P] layer-1 input [h0' | h1]                             */
     float *hout;           /* [S][P] new layer-1 state, input of joint.pred                */
-    float *predtmp, *pred; /* [S][J] recomputed / current prediction                       */
-    const float *bjp;      /* [J]                                                          */
+    float *pred;           /* [S][J] current prediction                                    */
     float *jin;            /* [S*W][J] joint inputs relu(enc + pred)                       */
-    const float *logits;   /* [S*W][ldl]                                                   */
-    u32 S, W, P, J, V, ldl, blank, max_symbols, tok_ld, pad;
+    u32 S, W, P, J, blank, max_symbols, tok_ld, pad;
 } NkBDecArgs;
 
 #endif

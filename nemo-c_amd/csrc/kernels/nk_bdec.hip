@@ -1,28 +1,34 @@
 /* Device-resident greedy RNNT loop of many streams at once (the batched decoder): the reference's
  * decoder_run (src/decoder.c:92-127) for every stream of a batch, one joint evaluation per step,
- * with no host round trip per step.  A step is six launches:
- *   bdec_lstm<0>  gates = [x | h0] . [Wx0 | Wh0]^T + b0 for all S streams, with the LSTM cell in the
- *                 epilogue (weight rows interleaved by unit: row 4u + q is gate q of unit u, so a
- *                 16-column tile holds the four gates of four units); streams whose prediction is
+ * with no host round trip per step.  A step is five launches:
+ *   bdec_lstm<0>  gates = Tx[last token] + h0 . Wh0^T for all S streams, where Tx = embed . Wx0^T + b0
+ *                 is a table built once per model (the embedding half of layer 0's input is one of
+ *                 V rows, so its product is looked up instead of recomputed), with the LSTM cell in
+ *                 the epilogue (weight rows interleaved by unit: row 4u + q is gate q of unit u, so
+ *                 a 16-column tile holds the four gates of four units); streams whose prediction is
  *                 stale write their provisional layer-0 state and the layer-1 input [h0' | h1];
- *   bdec_lstm<1>  the same for layer 1; writes h1' (the joint.pred input);
- *   bdec_pred     pred = h1' . Wjp^T + bjp, stored for the streams that recomputed it;
- *   bdec_joint_in the joint inputs relu(enc[t + k] + pred) of the W frames after each stream's t;
+ *   bdec_lstm<1>  gates = [h0' | h1] . [Wx1 | Wh1]^T + b1, the same cell; writes h1' (the joint.pred
+ *                 input);
+ *   bdec_pred     pred = h1' . Wjp^T + bjp for the streams that recomputed it, and their joint inputs
+ *                 relu(enc[t + k] + pred) for the frames k of the chunk after the stream's t;
  *   gemm_mx64x64_argmax  joint scores with an argmax epilogue: per row, the best (score, lowest
  *                 index) of each wavefront's 32 columns as a packed key;
  *   bdec_decide   per stream: the best key of each scored frame, the greedy rule (first non-blank
  *                 frame wins: emit, commit the provisional LSTM state, the prediction becomes stale;
  *                 blank frames reset the symbol count; max_symbols moves past the frame), then the
- *                 next step's layer-0 input [embed(last token) | h0].
- * Streams whose prediction is valid or whose chunk is done keep stale rows in the GEMM inputs;
- * their results are never stored.  LSTM states live in two slot sets per stream; committing a token
- * flips the committed set (the reference swaps its h/hp and c/cp buffers).
+ *                 next step's layer-0 input h0.
+ * After a decision every stream still inside its chunk has emitted a token, so its prediction is
+ * recomputed by the next step, which also writes its joint inputs; a prediction carried over from
+ * the previous chunk gets its joint inputs from bdec_setup.  Streams whose chunk is done keep stale
+ * rows in the GEMM inputs; their results are never stored.  LSTM states live in two slot sets per
+ * stream; committing a token flips the committed set (the reference swaps its h/hp and c/cp
+ * buffers).
  *
  * bdec_lstm / bdec_pred are GEMMs over at most 64 rows per workgroup (grid.y = row blocks of 64):
  * a workgroup owns 16 columns; its W wavefronts split K (SPW steps of 32 each), issue every load
  * (activations of four 16-row tiles in the MFMA A layout, weights in the B layout) before the first
- * MFMA, multiply with A split into bf16 hi + lo, and sum their partial tiles in wavefront order
- * through LDS; wavefront 0 applies the epilogue. */
+ * MFMA, multiply with A split into bf16 hi + lo, and leave their partial tiles in LDS; the epilogue
+ * sums them with every thread working on its own (row, unit) cell or output. */
 #include "nk_common.h"
 
 __device__ __forceinline__ u32 hc_row(u32 s, u32 k, u32 which) { return (s * 2 + k) * 4 + which; }
@@ -32,11 +38,12 @@ __device__ __forceinline__ void ld8f(float (&d)[8], const float *p) {
     d[0] = x[0]; d[1] = x[1]; d[2] = x[2]; d[3] = x[3]; d[4] = y[0]; d[5] = y[1]; d[6] = y[2]; d[7] = y[3];
 }
 
-/* sum over K of one 64-row x 16-column tile: wavefront 0 returns tot[ti] (rows 16 ti + 4 (l/16) + e,
- * column l % 16); other wavefronts return false */
+/* per-wavefront partial sums over its K range of one 64-row x 16-column tile, left in
+ * sred[(wave * 4 + ti) * 64 + lane] in the MFMA D layout (row 16 ti + 4 (lane / 16) + e, column
+ * lane % 16); ends with a barrier */
 template <int W, int SPW>
-__device__ __forceinline__ bool fr64_tile(const float *A, u32 lda, const u16 *Wt, u32 ldw, u32 M, u32 K, u32 r0,
-                                          floatx4 *sred, floatx4 (&tot)[4]) {
+__device__ __forceinline__ void fr64_partials(const float *A, u32 lda, const u16 *Wt, u32 M, u32 K, u32 r0,
+                                              floatx4 *sred) {
     const u32 tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const u32 S = K >> 5, sb = wave * SPW, ns = sb < S ? min((u32)SPW, S - sb) : 0u;
     const u32 m = lane & 15, kq = 8 * (lane >> 4);
@@ -69,192 +76,202 @@ __device__ __forceinline__ bool fr64_tile(const float *A, u32 lda, const u16 *Wt
 #pragma unroll
     for (int ti = 0; ti < 4; ++ti) sred[(wave * 4 + ti) * 64 + lane] = acc[ti];
     __syncthreads();
-    if (wave != 0) return false;
-#pragma unroll
-    for (int ti = 0; ti < 4; ++ti) {
-        floatx4 t = sred[ti * 64 + lane];
-#pragma unroll
-        for (int w = 1; w < W; ++w) t += sred[(w * 4 + ti) * 64 + lane];
-        tot[ti] = t;
-    }
-    return true;
 }
 
-/* need / committed slot set of the workgroup's 64 streams, staged in LDS before the GEMM phase
- * (fr64_tile's barrier publishes them) */
-__device__ __forceinline__ void stage_state(const NkBDecArgs &d, u32 r0, int *sneed, int *scur) {
+/* the tile's value at local row rl, column c: the W partials summed in wavefront order */
+template <int W>
+__device__ __forceinline__ float tile_at(const floatx4 *sred, u32 rl, u32 c) {
+    const u32 ti = rl >> 4, ln = ((rl & 15) >> 2) * 16 + c, e = rl & 3;
+    float v = ((const float *)&sred[ti * 64 + ln])[e];
+#pragma unroll
+    for (int w = 1; w < W; ++w) v += ((const float *)&sred[(w * 4 + ti) * 64 + ln])[e];
+    return v;
+}
+
+/* the workgroup's 64 streams in LDS, staged before the GEMM phase (whose barrier publishes them):
+ * need, committed slot set, layer-0 table row, frame position, frames left to score (at most W),
+ * first joint.enc row */
+struct BDecStage {
+    int need[64], cur[64], tok[64], t[64], lim[64], erow[64];
+};
+
+__device__ __forceinline__ void stage_state(const NkBDecArgs &d, u32 r0, BDecStage &ss) {
     if (threadIdx.x < 64) {
-        const u32 s = min(r0 + threadIdx.x, d.S - 1);
-        const NkBDecStream *p = d.st + s;
-        sneed[threadIdx.x] = r0 + threadIdx.x < d.S ? p->need : 0;
-        scur[threadIdx.x] = p->cur;
+        const u32 i = threadIdx.x, s = min(r0 + i, d.S - 1);
+        const NkBDecStream p = d.st[s];
+        ss.need[i] = r0 + i < d.S ? p.need : 0;
+        ss.cur[i] = p.cur;
+        ss.tok[i] = p.last_token >= 0 && p.last_token < (int)d.blank ? p.last_token : (int)d.blank;
+        ss.t[i] = p.t;
+        ss.lim[i] = min((int)d.W, p.frames - p.t);
+        ss.erow[i] = p.erow0;
     }
 }
 
-/* LSTM layer L (0 or 1) on all streams; grid (4P/16, ceil(S/64)); a.W: [Wx | Wh] with rows
- * interleaved by unit, a.bias interleaved the same way.  Epilogue: the four gates of a unit sit in
- * four consecutive lanes; the first lane of each quad runs the cell for its 16 rows, all cell-state
- * loads issued before the first use. */
+/* LSTM layer L (0 or 1) on all streams; grid (4P/16, ceil(S/64)), 64 W threads.  Layer 0: a.A = h0
+ * [S][P], a.W = Wh0 rows interleaved by unit, gates start from the table row d.tx[tok] (bias
+ * included); layer 1: a.A = [h0' | h1] [S][2P], a.W = [Wx1 | Wh1] interleaved, a.bias interleaved.
+ * Epilogue: thread t < 256 runs the cell of row t / 4, unit 4 blockIdx.x + t % 4. */
 template <int W, int SPW, int L>
-__device__ __forceinline__ void bdec_lstm_impl(const NkGemmArgs &a, const NkBDecArgs &d, floatx4 *sred, int *sneed,
-                                               int *scur) {
-    const u32 lane = threadIdx.x & 63, n0 = blockIdx.x * 16, r0 = blockIdx.y * 64, col = n0 + (lane & 15);
-    stage_state(d, r0, sneed, scur);
-    floatx4 tot[4];
-    if (!fr64_tile<W, SPW>(a.A, a.lda, a.W + (u64)col * a.ldw, a.ldw, a.M, a.K, r0, sred, tot)) return;
-    const float bias = a.bias[col];
-    const u32 P = d.P, u = col >> 2, base = lane & ~3u;
-    const bool leader = (lane & 3) == 0;
+__device__ __forceinline__ void bdec_lstm_impl(const NkGemmArgs &a, const NkBDecArgs &d, floatx4 *sred,
+                                               BDecStage &ss) {
+    static_assert(W >= 4, "the cell epilogue uses 256 threads");
+    const u32 lane = threadIdx.x & 63, r0 = blockIdx.y * 64, col = blockIdx.x * 16 + (lane & 15);
+    stage_state(d, r0, ss);
+    fr64_partials<W, SPW>(a.A, a.lda, a.W + (u64)col * a.ldw, a.M, a.K, r0, sred);
+    const u32 t = threadIdx.x;
+    if (t >= 256) return;
+    const u32 rl = t >> 2, j = t & 3, s = r0 + rl, P = d.P, u = blockIdx.x * 4 + j;
+    if (s >= d.S || !ss.need[rl]) return;
+    const u32 kc = (u32)ss.cur[rl];
     constexpr u32 CI = L == 0 ? 1 : 3, HI = L == 0 ? 0 : 2;
-    float c_in[4][4], h1c[4][4];
+    const float c_in = d.hc[(u64)hc_row(s, kc, CI) * P + u];
+    const float h1c = L == 0 ? d.hc[(u64)hc_row(s, kc, 2) * P + u] : 0.0f;
+    const floatx4 g0 = L == 0 ? *(const floatx4 *)(d.tx + (u64)ss.tok[rl] * 4 * P + 4 * u)
+                              : *(const floatx4 *)(a.bias + 4 * u);
+    float g[4];
 #pragma unroll
-    for (int ti = 0; ti < 4; ++ti)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const u32 rl = 16 * ti + 4 * (lane >> 4) + e, s = min(r0 + rl, d.S - 1), kc = (u32)scur[rl];
-            c_in[ti][e] = d.hc[(u64)hc_row(s, kc, CI) * P + u];
-            h1c[ti][e] = L == 0 ? d.hc[(u64)hc_row(s, kc, 2) * P + u] : 0.0f;
-        }
-#pragma unroll
-    for (int ti = 0; ti < 4; ++ti)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const float v = tot[ti][e] + bias;
-            const float gi = __shfl(v, (int)base, 64), gf = __shfl(v, (int)base + 1, 64);
-            const float gg = __shfl(v, (int)base + 2, 64), go = __shfl(v, (int)base + 3, 64);
-            const u32 rl = 16 * ti + 4 * (lane >> 4) + e, s = r0 + rl;
-            if (!leader || s >= d.S || !sneed[rl]) continue;
-            const u32 kp = (u32)scur[rl] ^ 1u;
-            const float c = sigmoid_f(gf) * c_in[ti][e] + sigmoid_f(gi) * tanhf(gg);
-            const float h = sigmoid_f(go) * tanhf(c);
-            d.hc[(u64)hc_row(s, kp, CI) * P + u] = c;
-            d.hc[(u64)hc_row(s, kp, HI) * P + u] = h;
-            if (L == 0) {
-                d.A1[(u64)s * 2 * P + u] = h;
-                d.A1[(u64)s * 2 * P + P + u] = h1c[ti][e];
-            } else {
-                d.hout[(u64)s * P + u] = h;
-            }
-        }
+    for (int q = 0; q < 4; ++q) g[q] = g0[q] + tile_at<W>(sred, rl, 4 * j + q);
+    const u32 kp = kc ^ 1u;
+    const float c = sigmoid_f(g[1]) * c_in + sigmoid_f(g[0]) * tanhf(g[2]);
+    const float h = sigmoid_f(g[3]) * tanhf(c);
+    d.hc[(u64)hc_row(s, kp, CI) * P + u] = c;
+    d.hc[(u64)hc_row(s, kp, HI) * P + u] = h;
+    if (L == 0) {
+        d.A1[(u64)s * 2 * P + u] = h;
+        d.A1[(u64)s * 2 * P + P + u] = h1c;
+    } else {
+        d.hout[(u64)s * P + u] = h;
+    }
 }
 
-/* joint.pred for the streams that recompute their prediction; grid (J/16, ceil(S/64)) */
+/* joint inputs of stream s at column j: rows s W + k for the lim >= 1 frames after its t (loads
+ * of clamped rows first, so that they are all in flight together) */
+__device__ __forceinline__ void write_jin(const NkBDecArgs &d, u32 s, u32 j, float p, int t, int lim, int erow) {
+    float e[NK_ATTC_MAX_C];
+#pragma unroll
+    for (int k = 0; k < NK_ATTC_MAX_C; ++k) e[k] = d.enc[(u64)(erow + t + min(k, lim - 1)) * d.J + j];
+#pragma unroll
+    for (int k = 0; k < NK_ATTC_MAX_C; ++k)
+        if (k < lim) d.jin[(u64)(s * d.W + k) * d.J + j] = fmaxf(e[k] + p, 0.0f);
+}
+
+/* joint.pred for the streams that recompute their prediction, and their joint inputs; grid
+ * (J/16, ceil(S/64)), 64 W threads; thread t handles column t % 16 of rows t / 16 + 16 i */
 template <int W, int SPW>
-__device__ __forceinline__ void bdec_pred_impl(const NkGemmArgs &a, const NkBDecArgs &d, floatx4 *sred, int *sneed,
-                                               int *scur) {
-    const u32 lane = threadIdx.x & 63, n0 = blockIdx.x * 16, r0 = blockIdx.y * 64, j = n0 + (lane & 15);
-    stage_state(d, r0, sneed, scur);
-    floatx4 tot[4];
-    if (!fr64_tile<W, SPW>(a.A, a.lda, a.W + (u64)j * a.ldw, a.ldw, a.M, a.K, r0, sred, tot)) return;
+__device__ __forceinline__ void bdec_pred_impl(const NkGemmArgs &a, const NkBDecArgs &d, floatx4 *sred,
+                                               BDecStage &ss) {
+    const u32 lane = threadIdx.x & 63, r0 = blockIdx.y * 64, col = blockIdx.x * 16 + (lane & 15);
+    stage_state(d, r0, ss);
+    fr64_partials<W, SPW>(a.A, a.lda, a.W + (u64)col * a.ldw, a.M, a.K, r0, sred);
+    const u32 c = threadIdx.x & 15, j = blockIdx.x * 16 + c;
     const float bias = a.bias[j];
-#pragma unroll
-    for (int ti = 0; ti < 4; ++ti)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const u32 rl = 16 * ti + 4 * (lane >> 4) + e, s = r0 + rl;
-            if (s < d.S && sneed[rl]) d.pred[(u64)s * d.J + j] = tot[ti][e] + bias;
-        }
+    for (u32 rl = threadIdx.x >> 4; rl < 64; rl += 4 * W) {
+        const u32 s = r0 + rl;
+        if (s >= d.S || !ss.need[rl]) continue;
+        const float p = tile_at<W>(sred, rl, c) + bias;
+        d.pred[(u64)s * d.J + j] = p;
+        write_jin(d, s, j, p, ss.t[rl], ss.lim[rl], ss.erow[rl]);
+    }
 }
 
 #define BDEC_GEMM(NAME, IMPL, W, SPW)                                                                     \
     extern "C" __global__ __launch_bounds__(64 * W) void NAME(const NkGemmArgs a, const NkBDecArgs d) {   \
         __shared__ floatx4 sred[W * 4 * 64];                                                              \
-        __shared__ int sneed[64], scur[64];                                                               \
-        IMPL(a, d, sred, sneed, scur);                                                                    \
+        __shared__ BDecStage ss;                                                                          \
+        IMPL(a, d, sred, ss);                                                                             \
     }
-/* K = 2P = 1280 (40 steps): 8 wavefronts x 5 steps; K = P = 640: 4 x 5; tiny models fit both */
-BDEC_GEMM(bdec_lstm0_w8s5, (bdec_lstm_impl<8, 5, 0>), 8, 5)
+/* layer 0: K = P <= 640 (20 steps): 4 wavefronts x 5 steps; layer 1: K = 2P <= 1280: 8 x 5;
+ * joint.pred: K = P: 4 x 5 */
+BDEC_GEMM(bdec_lstm0_w4s5, (bdec_lstm_impl<4, 5, 0>), 4, 5)
 BDEC_GEMM(bdec_lstm1_w8s5, (bdec_lstm_impl<8, 5, 1>), 8, 5)
 BDEC_GEMM(bdec_pred_w4s5, (bdec_pred_impl<4, 5>), 4, 5)
 
-/* joint input rows: row s*W + k is frame t + k of stream s (rows past the chunk are left as they
- * are: their scores are never read); grid (ceil(J/256), S*W) */
-extern "C" __global__ __launch_bounds__(256) void bdec_joint_in(const NkBDecArgs a) {
-    const u32 r = blockIdx.y, i = blockIdx.x * 256 + threadIdx.x;
-    if (i >= a.J) return;
-    const u32 s = r / a.W, k = r % a.W;
-    const NkBDecStream *p = a.st + s;
-    const int t = p->t, frames = p->frames;
-    if (t >= frames || t + (int)k >= frames) return;
-    a.jin[(u64)r * a.J + i] = fmaxf(a.enc[(u64)(p->erow0 + t + (int)k) * a.J + i] + a.pred[(u64)s * a.J + i], 0.0f);
+/* next step's layer-0 input of stream s (one wavefront): its committed h0 (slot set cur),
+ * P / 4 <= 192 float4 */
+__device__ __forceinline__ void bdec_prepare(const NkBDecArgs &a, u32 s, int cur) {
+    const u32 n4 = a.P >> 2, lane = threadIdx.x;
+    const floatx4 *h0 = (const floatx4 *)(a.hc + (u64)hc_row(s, (u32)cur, 0) * a.P);
+    floatx4 *A = (floatx4 *)(a.A0 + (u64)s * a.P);
+    floatx4 v[3];
+#pragma unroll
+    for (int i = 0; i < 3; ++i) v[i] = h0[min(lane + 64 * i, n4 - 1)];
+#pragma unroll
+    for (int i = 0; i < 3; ++i)
+        if (lane + 64 * i < n4) A[lane + 64 * i] = v[i];
 }
 
-/* next step's layer-0 input for stream s (all threads of the workgroup): [embed(last) | h0] */
-__device__ __forceinline__ void bdec_prepare(const NkBDecArgs &a, u32 s, const NkBDecStream &st) {
-    if (!(st.t < st.frames && !st.pred_valid)) return;
-    const u32 P = a.P;
-    float *A = a.A0 + (u64)s * 2 * P;
-    const bool emb = st.last_token >= 0 && (u32)st.last_token != a.blank;
-    const float *h0 = a.hc + (u64)hc_row(s, (u32)st.cur, 0) * P;
-    for (u32 j = threadIdx.x; j < P; j += blockDim.x) {
-        A[j] = emb ? bf2f(a.embed[(u64)st.last_token * P + j]) : 0.0f;
-        A[P + j] = h0[j];
-    }
-}
-
-/* new chunk: frames and first joint.enc row from the host, fresh frame position and counters */
+/* new chunk: frames and first joint.enc row from the host, fresh frame position and counters; a
+ * prediction carried over from the previous chunk gets its joint inputs here.  grid S, 64 threads */
 extern "C" __global__ __launch_bounds__(64) void bdec_setup(const NkBDecArgs a) {
     const u32 s = blockIdx.x;
-    NkBDecStream x = a.st[s];
-    x.frames = a.setup[2 * s];
-    x.erow0 = a.setup[2 * s + 1];
-    x.t = 0;
-    x.symbols = 0;
-    x.n_out = 0;
-    x.need = x.t < x.frames && !x.pred_valid;
-    if (threadIdx.x == 0) a.st[s] = x;
-    bdec_prepare(a, s, x);
+    NkBDecStream *sp = a.st + s;
+    const int frames = a.setup[2 * s], erow0 = a.setup[2 * s + 1], pred_valid = sp->pred_valid, cur = sp->cur;
+    const int need = 0 < frames && !pred_valid;
+    if (threadIdx.x == 0) {
+        sp->frames = frames;
+        sp->erow0 = erow0;
+        sp->t = 0;
+        sp->symbols = 0;
+        sp->n_out = 0;
+        sp->need = need;
+    }
+    if (need) bdec_prepare(a, s, cur);
+    if (0 < frames && pred_valid) {
+        const int lim = min((int)a.W, frames);
+        for (u32 j = threadIdx.x; j < a.J; j += 64) write_jin(a, s, j, a.pred[(u64)s * a.J + j], 0, lim, erow0);
+    }
 }
 
-/* per stream (one wavefront): best key of each scored frame, the greedy rule, next step's input.
- * All keys of the scored frames (at most 16 x 64) are loaded before the first reduction. */
+/* per stream (one wavefront): lane 4 r + p takes the maximum of keys p, p + 4, ... of scored frame r
+ * (at most 16 frames, nkeys <= 64), two exchanges finish each frame's maximum, a ballot finds the
+ * first non-blank frame; then the greedy rule and the next step's input. */
 extern "C" __global__ __launch_bounds__(64) void bdec_decide(const NkBDecArgs a) {
-    const u32 s = blockIdx.x, lane = threadIdx.x;
-    NkBDecStream x = a.st[s];
-    if (x.t >= x.frames) return;
-    const int rows = min(min((int)a.W, x.frames - x.t), NK_ATTC_MAX_C);
-    unsigned long long kv[NK_ATTC_MAX_C];
+    const u32 s = blockIdx.x, lane = threadIdx.x, row = lane >> 2, part = lane & 3;
+    NkBDecStream *sp = a.st + s;
+    const int frames = sp->frames, t = sp->t;
+    if (t >= frames) return;
+    int symbols = sp->symbols, cur = sp->cur, last = sp->last_token, n_out = sp->n_out, pred_valid = 1;
+    const int rows = min(min((int)a.W, frames - t), NK_ATTC_MAX_C);
+    const bool live = (int)row < rows;
+    const unsigned long long *kr = a.keys + (u64)(s * a.W + min((int)row, rows - 1)) * a.nkeys;
+    unsigned long long kv[16];
 #pragma unroll
-    for (int k = 0; k < NK_ATTC_MAX_C; ++k) {
-        const bool ok = k < rows && lane < a.nkeys;
-        const u32 kk = ok ? (u32)k : 0u, q = ok ? lane : 0u;
-        const unsigned long long v = a.keys[(u64)(s * a.W + kk) * a.nkeys + q];
-        kv[k] = ok ? v : 0ull;
-    }
-    int best_idx[NK_ATTC_MAX_C];
+    for (int i = 0; i < 16; ++i) kv[i] = kr[min(part + 4 * i, a.nkeys - 1)]; /* repeats change no maximum */
 #pragma unroll
-    for (int k = 0; k < NK_ATTC_MAX_C; ++k) {
-        unsigned long long kb = kv[k];
+    for (int w = 8; w >= 1; w >>= 1)
 #pragma unroll
-        for (int msk = 1; msk < 64; msk <<= 1) {
-            const unsigned long long o = shfl_xor_u64(kb, msk);
-            kb = o > kb ? o : kb;
-        }
-        best_idx[k] = (int)dec_key_index(kb);
-    }
-    x.pred_valid = 1;
-    int k = 0;
-    int emitted = -1;
+        for (int i = 0; i < w; ++i) kv[i] = kv[i + w] > kv[i] ? kv[i + w] : kv[i];
+    unsigned long long kb = kv[0];
 #pragma unroll
-    for (int q = 0; q < NK_ATTC_MAX_C; ++q) {
-        if (q >= rows || emitted >= 0) continue;
-        const int p = best_idx[q];
-        k = q + 1;
-        if (p == (int)a.blank) { x.symbols = 0; continue; }
-        emitted = p;
-        k = q;
+    for (int msk = 1; msk < 4; msk <<= 1) {
+        const unsigned long long o = shfl_xor_u64(kb, msk);
+        kb = o > kb ? o : kb;
     }
-    if (emitted >= 0) {
-        if (lane == 0 && x.n_out < (int)a.tok_ld) a.tokens[(u64)s * a.tok_ld + (u32)x.n_out] = emitted;
-        x.n_out++;
-        x.last_token = emitted;
-        x.cur ^= 1;
-        x.pred_valid = 0;
-        x.symbols++;
-        if (x.symbols >= (int)a.max_symbols) { x.symbols = 0; k++; }
+    const int idx = (int)dec_key_index(kb);
+    const unsigned long long nb = __ballot(part == 0 && live && idx != (int)a.blank);
+    const int f = nb ? (__ffsll((long long)nb) - 1) >> 2 : rows; /* first non-blank frame */
+    const int emitted = __shfl(idx, 4 * min(f, NK_ATTC_MAX_C - 1), 64);
+    int k = f;
+    if (f > 0) symbols = 0;
+    if (f < rows) {
+        if (lane == 0 && n_out < (int)a.tok_ld) a.tokens[(u64)s * a.tok_ld + (u32)n_out] = emitted;
+        n_out++;
+        last = emitted;
+        cur ^= 1;
+        pred_valid = 0;
+        symbols++;
+        if (symbols >= (int)a.max_symbols) { symbols = 0; k++; }
     }
-    x.t += k;
-    x.need = x.t < x.frames && !x.pred_valid;
-    if (lane == 0) a.st[s] = x;
-    bdec_prepare(a, s, x);
+    const int nt = t + k, need = nt < frames && !pred_valid;
+    if (lane == 0) {
+        sp->t = nt;
+        sp->symbols = symbols;
+        sp->pred_valid = pred_valid;
+        sp->cur = cur;
+        sp->last_token = last;
+        sp->n_out = n_out;
+        sp->need = need;
+    }
+    if (need) bdec_prepare(a, s, cur);
 }
