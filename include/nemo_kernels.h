@@ -107,6 +107,23 @@ int nk_attention_rel_desc(gpu_t *g, const float *kv, uint32_t ld, const int *des
                           float scale);
 int nk_dwconv_ln_silu_desc(gpu_t *g, const float *din_base, const int *desc, const float *W, const float *gamma,
                            const float *beta, float *Y, uint32_t c, uint32_t D, uint32_t taps, float eps);
+/* Launch fusions of the single-stream chunk (descriptor window, c <= 4 rows):
+ * C[i] += alpha * attention_i . Wo^T for the c rows (attention as nk_attention_rel_desc; each head's
+ * share of the product is added atomically, so the sum order of the H shares varies); Wo [D][ldw]
+ * bf16, D % 128 == 0.  Replaces nk_attention_rel_desc + nk_gemm(O, Wo, accumulate). */
+int nk_attention_out_desc(gpu_t *g, const float *kv, uint32_t ld, const int *desc, const float *P, const float *bias_u,
+                          const float *bias_v, uint32_t c, uint32_t Lmax, uint32_t H, uint32_t dh, uint32_t D,
+                          float scale, const uint16_t *Wo, uint32_t ldw, float *C, uint32_t ldc, float alpha);
+/* C[i][n] (= or +=) alpha * sum_k y_i[k] W[n][k] with y = SiLU(LN(dwconv(din))) of the c <= 2 rows
+ * (as nk_dwconv_ln_silu_desc; 9 taps, D <= 1024, D % 8 == 0).  Bit-identical to that launch
+ * followed by nk_gemm(y, W, no bias, no activation). */
+int nk_dwconv_pw_desc(gpu_t *g, const float *din_base, const int *desc, const float *dw_w, const float *gamma,
+                      const float *beta, float eps, const uint16_t *W, uint32_t ldw, float *C, uint32_t ldc, uint32_t c,
+                      uint32_t D, uint32_t N, int accumulate, float alpha);
+/* Shapes of the fused kernels: output columns per wavefront of the attention fusion (4, 8 or 16) and
+ * weight rows per wavefront of the conv fusion (1, 2 or 4).  0 leaves a setting; returns the
+ * previous settings as attn * 16 + dw. */
+int nk_fuse_shape(int attn_cpw, int dw_nc);
 /* Batched streams: output row m is described by rows[4m .. 4m+3] = { cache row of the chunk row,
  * its index i in its stream's chunk, that chunk's rows c, the stream's cached rows } (device). */
 int nk_attention_rel_rows(gpu_t *g, const float *kv, uint32_t ld, const int *rows, uint32_t M, const float *P,

@@ -25,6 +25,9 @@ const float *nemoasr_debug_dump_prompted(const nemoasr_t *s);
 const float *nemoasr_debug_dump_joint_enc(const nemoasr_t *s);
 /* 0: launch every kernel directly; 1: replay chunks as hipGraphs (default). */
 void nemoasr_debug_use_graphs(nemoasr_t *s, int on);
+/* 1 (default): chunks of at most two rows run attention + output projection and depthwise conv +
+ * pointwise conv as one launch each; 0: the separate launches. */
+void nemoasr_debug_fuse(nemoasr_t *s, int on);
 /* Round trips of the decoder since open/reset, and GPU time of the encoder chunks (ms). */
 size_t nemoasr_debug_joint_steps(const nemoasr_t *s);
 double nemoasr_debug_encoder_gpu_ms(const nemoasr_t *s);

@@ -56,6 +56,7 @@ struct encoder {
     int *stage_desc;
     /* graphs */
     int use_graphs;
+    int fuse; /* single-stream launch fusions (kernels/nk_fuse.hip) */
     gslot_t gs[MAX_GRAPHS];
     unsigned long long tick;
     /* dumps */
@@ -111,6 +112,7 @@ encoder_t *encoder_create(model_t *m, int right) {
     e->stage_win = gpu_host_alloc(g, nwin * F * fs + NK_DESC_INTS * sizeof(int) + 256);
     e->stage_desc = (int *)((char *)e->stage_win + ((nwin * F * fs + 255) / 256) * 256);
     e->use_graphs = 1;
+    e->fuse = 1;
     e->pos = e->conv_left; /* rows [0, conv_left) stay zero: the empty conv history */
     return e;
 }
@@ -159,6 +161,11 @@ int encoder_chunk_mel(const encoder_t *e) { return e->chunk_mel; }
 void encoder_use_graphs(encoder_t *e, int on) {
     e->use_graphs = on;
     if (!on) drop_graphs(e);
+}
+
+void encoder_fuse(encoder_t *e, int on) {
+    if (e->fuse != on) drop_graphs(e);
+    e->fuse = on;
 }
 
 void encoder_set_dump(encoder_t *e, int on) {
@@ -252,6 +259,9 @@ static void run_blocks(encoder_t *e, int c) {
     float *lnbuf = gpu_buf_dptr(e->t2); /* LayerNorm output when the GEMM cannot take it as a prologue */
     float *ff = gpu_buf_dptr(e->ff), *att = gpu_buf_dptr(e->att), *y = gpu_buf_dptr(e->y);
     float *dump = e->dump ? gpu_buf_dptr(e->dump_dev) : NULL;
+    /* one or two rows per chunk: attention + out_proj and dwconv + pw2 as one launch each */
+    const int fuse_att = e->fuse && uc <= 4 && dh == 128 && D % 128 == 0;
+    const int fuse_conv = e->fuse && uc <= 2 && D <= 1024 && D % 8 == 0 && cf->conv_kernel == NK_CONV_TAPS;
     int cur = 0;
     for (uint32_t l = 0; l < nl; ++l) {
         const layer_dev_t *W = &m->L[l];
@@ -274,13 +284,23 @@ static void run_blocks(encoder_t *e, int c) {
         /* attention: fused q|k|v projection written into cache rows pos .. pos+c-1 */
         nk_gemm_ln(g, res, D, W->wqkv, D, NULL, kv, 3 * D, rows, uc, 3 * D, D, NK_ACT_NONE, 0, 1.0f, 1, W->ln_att_g,
                    W->ln_att_b, NULL, NULL, NULL, lnbuf, eps);
-        nk_attention_rel_desc(g, kv, 3 * D, desc, W->ptab, W->bias_u, W->bias_v, att, uc, (uint32_t)e->Lmax, H, dh, D, scale);
-        nk_gemm(g, att, D, W->wo, D, NULL, res, D, uc, D, D, NK_ACT_NONE, 1, 1.0f);
+        if (fuse_att) {
+            nk_attention_out_desc(g, kv, 3 * D, desc, W->ptab, W->bias_u, W->bias_v, uc, (uint32_t)e->Lmax, H, dh, D,
+                                  scale, W->wo, D, res, D, 1.0f);
+        } else {
+            nk_attention_rel_desc(g, kv, 3 * D, desc, W->ptab, W->bias_u, W->bias_v, att, uc, (uint32_t)e->Lmax, H, dh,
+                                  D, scale);
+            nk_gemm(g, att, D, W->wo, D, NULL, res, D, uc, D, D, NK_ACT_NONE, 1, 1.0f);
+        }
         /* convolution module: GLU output appended to the conv history, causal depthwise conv over it */
         nk_gemm_ln(g, res, D, W->pw1, D, NULL, din, D, rows, uc, 2 * D, D, NK_ACT_GLU, 0, 1.0f, 1, W->ln_conv_g,
                    W->ln_conv_b, NULL, NULL, NULL, lnbuf, eps);
-        nk_dwconv_ln_silu_desc(g, din, desc, W->dw_w, W->bn_g, W->bn_b, y, uc, D, (uint32_t)cf->conv_kernel, eps);
-        nk_gemm(g, y, D, W->pw2, D, NULL, res, D, uc, D, D, NK_ACT_NONE, 1, 1.0f);
+        if (fuse_conv) {
+            nk_dwconv_pw_desc(g, din, desc, W->dw_w, W->bn_g, W->bn_b, eps, W->pw2, D, res, D, uc, D, D, 1, 1.0f);
+        } else {
+            nk_dwconv_ln_silu_desc(g, din, desc, W->dw_w, W->bn_g, W->bn_b, y, uc, D, (uint32_t)cf->conv_kernel, eps);
+            nk_gemm(g, y, D, W->pw2, D, NULL, res, D, uc, D, D, NK_ACT_NONE, 1, 1.0f);
+        }
         /* FF2 half step */
         nk_gemm_ln(g, res, D, W->ff2_w1, D, NULL, ff, FF, NULL, uc, FF, D, NK_ACT_SILU, 0, 1.0f, 1, W->ln_ff2_g,
                    W->ln_ff2_b, NULL, NULL, NULL, lnbuf, eps);

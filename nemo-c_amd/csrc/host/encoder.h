@@ -25,6 +25,8 @@ int encoder_step(encoder_t *e, int final, enc_out_t *out, char *err, size_t errl
 
 /* Replay each chunk shape as a captured hipGraph (default on). */
 void encoder_use_graphs(encoder_t *e, int on);
+/* 1 (default): fused attention + out_proj and dwconv + pw2 launches for chunks of few rows. */
+void encoder_fuse(encoder_t *e, int on);
 /* Keep per-layer block outputs of every chunk (test hook). */
 void encoder_set_dump(encoder_t *e, int on);
 size_t encoder_dump_frames(const encoder_t *e);

@@ -293,6 +293,7 @@ void nemoasr_debug_use_graphs(nemoasr_t *s, int on) {
     encoder_use_graphs(s->enc, on);
     decoder_use_graphs(s->dec, on);
 }
+void nemoasr_debug_fuse(nemoasr_t *s, int on) { encoder_fuse(s->enc, on); }
 size_t nemoasr_debug_joint_steps(const nemoasr_t *s) { return s->joint_steps; }
 double nemoasr_debug_encoder_gpu_ms(const nemoasr_t *s) { return s->enc_gpu_ms; }
 const double *nemoasr_debug_chunk_ms(const nemoasr_t *s, size_t *n) {

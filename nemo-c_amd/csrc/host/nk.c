@@ -336,6 +336,63 @@ int nk_dwconv_ln_silu_desc(gpu_t *g, const float *din_base, const int *desc, con
     return gpu_launch(g, "dwconv_ln_silu", &a, sizeof a, c, 1, 1, NK_LN_THREADS, 1, 1);
 }
 
+/* measured at one row (80 ms chunks): 8 columns per wavefront (128 workgroups) and one weight row
+ * per wavefront were the fastest of {4, 8, 16} x {1, 2, 4} */
+static int g_attn_cpw = 8, g_dw_nc = 1;
+
+int nk_fuse_shape(int attn_cpw, int dw_nc) {
+    const int prev = g_attn_cpw * 16 + g_dw_nc;
+    if (attn_cpw == 4 || attn_cpw == 8 || attn_cpw == 16) g_attn_cpw = attn_cpw;
+    if (dw_nc == 1 || dw_nc == 2 || dw_nc == 4) g_dw_nc = dw_nc;
+    return prev;
+}
+
+int nk_attention_out_desc(gpu_t *g, const float *kv, uint32_t ld, const int *desc, const float *P, const float *bias_u,
+                          const float *bias_v, uint32_t c, uint32_t Lmax, uint32_t H, uint32_t dh, uint32_t D,
+                          float scale, const uint16_t *Wo, uint32_t ldw, float *C, uint32_t ldc, float alpha) {
+    if (!c) return 0;
+    if (dh != 128 || H * dh != D || c > 4 || c > Lmax || Lmax > NK_ATT_MAX_L || D % (8u * (uint32_t)g_attn_cpw))
+        return bad(g, "attention_out: head_dim 128, c <= 4, D a multiple of the column tile");
+    if ((uintptr_t)kv % 16 || ld % 4 || !aligned16(Wo) || ldw % 8 || ldw < D || ldc < D)
+        return bad(g, "attention_out: aligned cache and weights, ldw and ldc >= D");
+    NkAttnOutArgs p;
+    memset(&p, 0, sizeof p);
+    p.at = (NkAttnArgs){ kv, kv + D, kv + 2 * D, P, bias_u, bias_v, NULL, desc, NULL, c, 0, Lmax, H, dh, D, ld, ld, scale, 0 };
+    p.Wo = Wo;
+    p.C = C;
+    p.ldw = ldw;
+    p.ldc = ldc;
+    p.alpha = alpha;
+    gpu_next_bytes(g, 2.0 * D * D + 4.0 * 2 * c * D);
+    gpu_next_flops(g, 2.0 * c * D * D);
+    const uint32_t cols = 8u * (uint32_t)g_attn_cpw;
+    char name[32];
+    snprintf(name, sizeof name, "attention_rel_out_c%d", g_attn_cpw);
+    return gpu_launch(g, name, &p, sizeof p, H, D / cols, c, 512, 1, 1);
+}
+
+int nk_dwconv_pw_desc(gpu_t *g, const float *din_base, const int *desc, const float *dw_w, const float *gamma,
+                      const float *beta, float eps, const uint16_t *W, uint32_t ldw, float *C, uint32_t ldc, uint32_t c,
+                      uint32_t D, uint32_t N, int accumulate, float alpha) {
+    if (!c) return 0;
+    if (c > 2 || D > 1024 || D % 8 || !N || N > GPU_ZEROS_N)
+        return bad(g, "dwconv_pw: c <= 2, D <= 1024 and a multiple of 8, N <= the zero-bias length");
+    if (!aligned16(W) || ldw % 8 || ldw < D || ldc < N || (uintptr_t)din_base % 16)
+        return bad(g, "dwconv_pw: aligned operands, ldw >= D, ldc >= N");
+    NkGemvDwArgs p;
+    memset(&p, 0, sizeof p);
+    p.g.W = W; p.g.bias = gpu_zeros(g); p.g.C = C; p.g.crow = gpu_iota(g);
+    p.g.M = c; p.g.N = N; p.g.K = D; p.g.lda = D; p.g.ldw = ldw; p.g.ldc = ldc;
+    p.g.act = NK_ACT_NONE; p.g.accumulate = (uint32_t)(accumulate != 0); p.g.alpha = alpha; p.g.splits = 1;
+    p.d = (NkDwArgs){ din_base, dw_w, gamma, beta, NULL, desc, NULL, c, D, NK_CONV_TAPS, eps };
+    gpu_next_bytes(g, 2.0 * N * D + 4.0 * c * N * (accumulate ? 2 : 1));
+    gpu_next_flops(g, 2.0 * c * N * D);
+    const uint32_t kch = D / 8 <= 64 ? 1 : 2, nc = (uint32_t)g_dw_nc, waves = (N + nc - 1) / nc;
+    char name[32];
+    snprintf(name, sizeof name, "gemv_dw_r%u_n%u_k%u", c, nc, kch);
+    return gpu_launch(g, name, &p, sizeof p, (waves + 3) / 4, 1, 1, 256, 1, 1);
+}
+
 int nk_attention_rel_rows(gpu_t *g, const float *kv, uint32_t ld, const int *rows, uint32_t M, const float *P,
                           const float *bias_u, const float *bias_v, float *O, uint32_t Lmax, uint32_t H, uint32_t dh,
                           uint32_t D, float scale) {

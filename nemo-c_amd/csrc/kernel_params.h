@@ -130,6 +130,24 @@ typedef struct {
     float eps;
 } NkDwArgs;
 
+/* Attention fused with its output projection (single stream, window from the descriptor):
+ * C[row] += alpha * O[row] . Wo^T with O the attention output of `at` (at.O unused); Wo [D][ldw]. */
+typedef struct {
+    NkAttnArgs at;
+    const u16 *Wo;
+    float *C;
+    u32 ldw, ldc;
+    float alpha;
+    u32 pad;
+} NkAttnOutArgs;
+
+/* Depthwise conv + LN + SiLU (d, window from the descriptor; d.Y unused) as the prologue of the
+ * GEMV g that consumes it (g.A unused, g.K = d.D). */
+typedef struct {
+    NkGemmArgs g;
+    NkDwArgs d;
+} NkGemvDwArgs;
+
 /* Subsampling convs. X [T][F] (conv 0) or [T][F][C]; Y [T1][F1][C].  grid.y runs over a batch
  * of windows of the same size, xs / ys floats apart. */
 typedef struct {

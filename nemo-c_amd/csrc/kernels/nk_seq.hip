@@ -75,20 +75,26 @@ extern "C" __global__ __launch_bounds__(256) void layernorm(const NkLnArgs a) {
         if (tid + k * 256 < D4) y2[tid + k * 256] = v[k];
 }
 
-/* Relative-position attention, one workgroup of 512 threads per (head, query i):
+/* Relative-position attention of one (head h, query row orow) on a workgroup of 512 threads:
  * reference src/kernels.metal:290-348.
  *   score_j = ((q + u) . K_j + (q + v) . P[(Lmax - L) + (c - 1 - i + j)]) * scale
  *   O_i = sum_j softmax(score)_j V_j  (no mask inside the chunk)
  * Scores: four threads per key (32 head dims each), one key per thread quad (L <= 128).
  * Output: thread (g = tid / 32, d4 = tid % 32) accumulates dims 4*d4..4*d4+3 over the keys
  * j = g (mod 16); the 16 key groups are summed in order through LDS.  Every K, P and V load is
- * issued at the start (indices past the window clamped to a valid row and masked at use); the
- * barriers wait for LDS only, so the V loads stay in flight through the score phase. */
-extern "C" __global__ __launch_bounds__(512) void attention_rel(const NkAttnArgs a) {
-    __shared__ floatx4 qu4[32], qv4[32];
-    __shared__ float s[NK_ATT_MAX_L], red[16];
-    __shared__ floatx4 part[16][32];
-    const u32 h = blockIdx.x, orow = blockIdx.y, tid = threadIdx.x;
+ * issued at the start (indices past the window clamped to a valid row and masked at use), then
+ * after_loads() (a fused caller's own loads, so that the waits for K, P and V never wait for
+ * them); the barriers wait for LDS only, so the V loads stay in flight through the score phase.
+ * Returns dims 4 tid .. 4 tid + 3 of the head's output row on threads tid < 32. */
+struct AttnShared {
+    floatx4 qu4[32], qv4[32];
+    float s[NK_ATT_MAX_L], red[16];
+    floatx4 part[16][32];
+};
+
+template <class F>
+__device__ __forceinline__ floatx4 attn_rel_core(const NkAttnArgs &a, u32 h, u32 orow, AttnShared &sh, F &&after_loads) {
+    const u32 tid = threadIdx.x;
     const u32 off = h * 128;
     const float *Q = a.Q, *Kp = a.K, *Vp = a.V;
     u32 L = a.L, i = orow, c = a.c;
@@ -133,52 +139,63 @@ extern "C" __global__ __launch_bounds__(512) void attention_rel(const NkAttnArgs
 #pragma unroll
     for (int t = 0; t < NK_ATT_MAX_L / 16; ++t)
         if (vg + 16 * t < L) vv[t] = *(const floatx4 *)(Vp + (u64)(vg + 16 * t) * a.ldk + off + 4 * d4);
+    __builtin_amdgcn_sched_barrier(0);
+    after_loads();
+    __builtin_amdgcn_sched_barrier(0);
     if (tid < 32) {
-        qu4[tid] = qx + ux;
-        qv4[tid] = qx + vx;
+        sh.qu4[tid] = qx + ux;
+        sh.qv4[tid] = qx + vx;
     }
     lds_barrier();
     float acc = 0.0f;
     if (kin) {
 #pragma unroll
         for (int q = 0; q < 8; ++q) {
-            const floatx4 u = qu4[part4 * 8 + q], w = qv4[part4 * 8 + q];
+            const floatx4 u = sh.qu4[part4 * 8 + q], w = sh.qv4[part4 * 8 + q];
             acc += u[0] * kr[q][0] + u[1] * kr[q][1] + u[2] * kr[q][2] + u[3] * kr[q][3];
             acc += w[0] * pr[q][0] + w[1] * pr[q][1] + w[2] * pr[q][2] + w[3] * pr[q][3];
         }
     }
     acc += dpp_f<DPP_QUAD_1032>(acc);
     acc += dpp_f<DPP_QUAD_2301>(acc);
-    if (part4 == 0 && kin) s[ks] = acc * a.scale;
+    if (part4 == 0 && kin) sh.s[ks] = acc * a.scale;
     lds_barrier();
     /* softmax over the window (threads 0..127 hold one score each) */
     const int lane = tid & 63, wave = tid >> 6;
-    const float sv = tid < L ? s[tid] : -INFINITY;
+    const float sv = tid < L ? sh.s[tid] : -INFINITY;
     float mx = wmax(sv);
-    if (wave < 2 && lane == 0) red[wave] = mx;
+    if (wave < 2 && lane == 0) sh.red[wave] = mx;
     lds_barrier();
-    mx = fmaxf(red[0], red[1]);
+    mx = fmaxf(sh.red[0], sh.red[1]);
     const float ev = tid < L ? expf(sv - mx) : 0.0f;
     float sum = wsum(ev);
-    if (wave < 2 && lane == 0) red[2 + wave] = sum;
+    if (wave < 2 && lane == 0) sh.red[2 + wave] = sum;
     lds_barrier();
-    sum = red[2] + red[3];
-    if (tid < L) s[tid] = ev / sum;
+    sum = sh.red[2] + sh.red[3];
+    if (tid < L) sh.s[tid] = ev / sum;
     lds_barrier();
     floatx4 o = { 0.f, 0.f, 0.f, 0.f };
 #pragma unroll
     for (int t = 0; t < NK_ATT_MAX_L / 16; ++t) {
         const u32 j = vg + 16 * t;
-        if (j < L) o += s[j] * vv[t];
+        if (j < L) o += sh.s[j] * vv[t];
     }
-    part[vg][d4] = o;
+    sh.part[vg][d4] = o;
     lds_barrier();
+    floatx4 r = { 0.f, 0.f, 0.f, 0.f };
     if (tid < 32) {
-        floatx4 r = part[0][tid];
+        r = sh.part[0][tid];
 #pragma unroll
-        for (int g = 1; g < 16; ++g) r += part[g][tid];
-        *(floatx4 *)(a.O + (u64)orow * a.D + off + 4 * tid) = r;
+        for (int g = 1; g < 16; ++g) r += sh.part[g][tid];
     }
+    return r;
+}
+
+/* one workgroup of 512 threads per (head, query row) */
+extern "C" __global__ __launch_bounds__(512) void attention_rel(const NkAttnArgs a) {
+    __shared__ AttnShared sh;
+    const floatx4 r = attn_rel_core(a, blockIdx.x, blockIdx.y, sh, [] {});
+    if (threadIdx.x < 32) *(floatx4 *)(a.O + (u64)blockIdx.y * a.D + blockIdx.x * 128 + 4 * threadIdx.x) = r;
 }
 
 /* Relative-position attention of whole chunks (batched streams), the math of attention_rel above

@@ -67,6 +67,7 @@ API = {
     "nemoasr_debug_dump_prompted": (_f32p, [_vp]),
     "nemoasr_debug_dump_joint_enc": (_f32p, [_vp]),
     "nemoasr_debug_use_graphs": (None, [_vp, C.c_int]),
+    "nemoasr_debug_fuse": (None, [_vp, C.c_int]),
     "nemoasr_debug_joint_steps": (C.c_size_t, [_vp]),
     "nemoasr_debug_encoder_gpu_ms": (C.c_double, [_vp]),
     "nemoasr_debug_chunk_ms": (C.POINTER(C.c_double), [_vp, C.POINTER(C.c_size_t)]),
@@ -112,6 +113,11 @@ API = {
                                         C.c_float]),
     "nk_dwconv_ln_silu": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, C.c_float]),
     "nk_dwconv_ln_silu_desc": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, C.c_float]),
+    "nk_attention_out_desc": (C.c_int, [_vp, _vp, _u32, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, C.c_float,
+                                        _vp, _u32, _vp, _u32, C.c_float]),
+    "nk_dwconv_pw_desc": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, C.c_float, _vp, _u32, _vp, _u32, _u32, _u32, _u32,
+                                    C.c_int, C.c_float]),
+    "nk_fuse_shape": (C.c_int, [C.c_int, C.c_int]),
     "nk_conv2d_c1_s2_relu": (C.c_int, [_vp, _vp, _vp, _vp, _vp] + [_u32] * 5),
     "nk_dwconv2d_s2": (C.c_int, [_vp, _vp, _vp, _vp, _vp] + [_u32] * 5),
     "nk_flatten_cf": (C.c_int, [_vp, _vp, _vp, _u32, _u32, _u32]),
@@ -291,6 +297,9 @@ class Session:
 
     def use_graphs(self, on: bool):
         lib().nemoasr_debug_use_graphs(self.h, int(on))
+
+    def fuse(self, on: bool):
+        lib().nemoasr_debug_fuse(self.h, int(on))
 
     def dumps(self, n_layers: int, d_model: int, joint_hidden: int):
         F = lib().nemoasr_debug_frames(self.h)

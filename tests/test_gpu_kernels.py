@@ -370,6 +370,88 @@ def test_dwconv_ln_silu(gpu, c):
     assert rel_err(dY.read((c, D)), ref) < 1e-5
 
 
+@pytest.mark.parametrize("c,cache,cpw", [(1, 56, 16), (1, 56, 8), (1, 56, 4), (1, 0, 16), (2, 56, 16), (4, 40, 8)])
+def test_attention_out_fused(gpu, c, cache, cpw):
+    """Attention fused with its output projection: residual += attention . Wo^T against the
+    oracle's attention times the same bf16 weights (float64 product), and against the two
+    separate launches; the heads' shares are added atomically, so only float tolerance applies."""
+    import nemoasr
+
+    lib = nemoasr.lib()
+    H, dh, D, Lmax = 8, 128, 1024, 72
+    L = cache + c
+    rng = np.random.default_rng([c, cache, cpw])
+    pos = cache + 5
+    kv = rng.standard_normal((pos + c + 2, 3 * D)).astype(np.float32)
+    P = rng.standard_normal((2 * Lmax - 1, D)).astype(np.float32)
+    bu = (0.1 * rng.standard_normal(D)).astype(np.float32)
+    bv = (0.1 * rng.standard_normal(D)).astype(np.float32)
+    Wo = _w(rng, D, D)
+    res0 = rng.standard_normal((c, D)).astype(np.float32)
+    att = oracle.attention_rel(kv[pos:pos + c, :], kv[pos - cache:pos + c, D:2 * D], kv[pos - cache:pos + c, 2 * D:],
+                               P, bu, bv, c, L, Lmax, H, dh)
+    ref = res0 + (att.astype(np.float64) @ oracle.bf16_to_f32(Wo).astype(np.float64).T)
+    desc = np.zeros(20, np.int32)
+    desc[:4] = [pos, cache, L, c]
+    dkv, dP, dbu, dbv, dW = gpu.put(kv), gpu.put(P), gpu.put(bu), gpu.put(bv), gpu.put(Wo)
+    ddesc, dres, dO, dres2 = gpu.put(desc), gpu.put(res0), gpu.alloc(c * D * 4), gpu.put(res0)
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(dh)))
+    prev = lib.nk_fuse_shape(cpw, 0)
+    try:
+        gpu.begin()
+        gpu.check(lib.nk_attention_out_desc(gpu.h, dkv.ptr, 3 * D, ddesc.ptr, dP.ptr, dbu.ptr, dbv.ptr, c, Lmax, H, dh,
+                                            D, scale, dW.ptr, D, dres.ptr, D, 1.0))
+        gpu.check(lib.nk_attention_rel_desc(gpu.h, dkv.ptr, 3 * D, ddesc.ptr, dP.ptr, dbu.ptr, dbv.ptr, dO.ptr, c, Lmax,
+                                            H, dh, D, scale))
+        gpu.check(lib.nk_gemm(gpu.h, dO.ptr, D, dW.ptr, D, None, dres2.ptr, D, c, D, D, 0, 1, 1.0))
+        gpu.end()
+    finally:
+        lib.nk_fuse_shape(prev // 16, prev % 16)
+    got, sep = dres.read((c, D)), dres2.read((c, D))
+    assert rel_err(got, ref) < 1e-5
+    assert rel_err(got, sep) < 1e-6
+
+
+@pytest.mark.parametrize("c,D,N,nc,acc", [(1, 1024, 1024, 2, 1), (1, 1024, 1024, 1, 1), (1, 1024, 1024, 4, 0),
+                                          (2, 1024, 1024, 2, 1), (2, 1024, 1000, 4, 1), (1, 256, 192, 2, 1),
+                                          (2, 64, 64, 1, 0)])
+def test_dwconv_pw_fused(gpu, c, D, N, nc, acc):
+    """Depthwise conv + LN + SiLU as the prologue of the pointwise GEMV: bit-identical to the two
+    separate launches (same per-thread conv, reductions and dot-product order), and against the
+    oracle's conv times the same bf16 weights."""
+    import nemoasr
+
+    lib = nemoasr.lib()
+    taps, eps, pos = 9, 1e-5, 20
+    rng = np.random.default_rng([c, D, N, nc])
+    din = rng.standard_normal((pos + c + 3, D)).astype(np.float32)
+    Wd = (rng.standard_normal((D, taps)) / 3).astype(np.float32)
+    g = (1 + 0.1 * rng.standard_normal(D)).astype(np.float32)
+    b = (0.1 * rng.standard_normal(D)).astype(np.float32)
+    Wp = _w(rng, N, D)
+    C0 = rng.standard_normal((c, N)).astype(np.float32)
+    y = oracle.dwconv_ln_silu(din[pos - (taps - 1):pos + c], Wd, g, b, c)
+    ref = (C0 if acc else 0) + y.astype(np.float64) @ oracle.bf16_to_f32(Wp).astype(np.float64).T
+    desc = np.zeros(20, np.int32)
+    desc[:4] = [pos, 0, c, c]
+    ddin, dWd, dg, db, dWp, ddesc = gpu.put(din), gpu.put(Wd), gpu.put(g), gpu.put(b), gpu.put(Wp), gpu.put(desc)
+    dC, dC2, dY = gpu.put(C0), gpu.put(C0), gpu.alloc(c * D * 4)
+    prev = lib.nk_fuse_shape(0, nc)
+    try:
+        gpu.begin()
+        gpu.check(lib.nk_dwconv_pw_desc(gpu.h, ddin.ptr, ddesc.ptr, dWd.ptr, dg.ptr, db.ptr, eps, dWp.ptr, D, dC.ptr, N,
+                                        c, D, N, acc, 1.0))
+        gpu.check(lib.nk_dwconv_ln_silu_desc(gpu.h, ddin.ptr, ddesc.ptr, dWd.ptr, dg.ptr, db.ptr, dY.ptr, c, D, taps,
+                                             eps))
+        gpu.check(lib.nk_gemm(gpu.h, dY.ptr, D, dWp.ptr, D, None, dC2.ptr, N, c, N, D, 0, acc, 1.0))
+        gpu.end()
+    finally:
+        lib.nk_fuse_shape(0, prev % 16)
+    got = dC.read((c, N))
+    np.testing.assert_array_equal(got, dC2.read((c, N)))
+    assert rel_err(got, ref) < 1e-5
+
+
 @pytest.mark.parametrize("nwin", [8, 24, 72, 128, 33])
 def test_subsampling_convs(gpu, nwin):
     import nemoasr

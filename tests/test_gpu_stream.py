@@ -82,6 +82,28 @@ def test_graph_replay_matches(latency):
     s.close()
 
 
+@pytest.mark.parametrize("latency", [80, 160])
+def test_fused_launches_match_separate(latency):
+    """The one- and two-row chunks' fused launches (attention + out_proj, dwconv + pw2) against the
+    separate launches: every layer's activations within float rounding, identical tokens."""
+    import nemoasr
+
+    mdir = model_dir("full")
+    d = oracle.Model(mdir, "en-US").dims
+    mel = mel_ref.logmel(synth.make_audio(1.5, seed=21))
+    out = []
+    for fuse in (True, False):
+        s = nemoasr.Session(mdir, "en-US", latency)
+        s.fuse(fuse)
+        s.set_dump(True)
+        s.feed_mel(mel, final=True)
+        out.append((s.tokens(), s.dumps(d.n_layers, d.d_model, d.joint_hidden)))
+        s.close()
+    (tf, (lf, pf, jf)), (ts, (ls, ps, js)) = out
+    assert tf == ts
+    assert rel_err(lf, ls) < 1e-5 and rel_err(jf, js) < 1e-5
+
+
 def test_audio_api_tiny():
     """nemoasr_feed from audio in 100 ms blocks (the library's intended use, tools/libtest.c:20-26)
     gives the oracle's tokens from its own mel restatement."""
