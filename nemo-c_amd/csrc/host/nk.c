@@ -101,9 +101,9 @@ typedef struct {
 } ln_pro_t;
 
 /* Many-row GEMM on the direct-to-LDS MFMA kernels (kernels/nk_mx.hip).  Tile choice: the largest
- * of 128x128, 64x128, 64x64 whose tile count reaches 160 workgroups; otherwise K is split (only for
- * accumulating GEMMs with no bias and no activation, whose partial products are added atomically)
- * or the smallest tile that divides the columns is used.  Returns 1 when no tile divides the
+ * of 128x128, 64x128, 64x64 whose tile count reaches about 400 workgroups; otherwise the smallest
+ * tile that divides the columns, with K split for accumulating GEMMs with no bias and no activation
+ * (whose partial products are added atomically).  Returns 1 when no tile divides the
  * output columns (the caller falls back), else the launch status. */
 static int launch_mx(gpu_t *g, NkGemmArgs *a, uint32_t M, uint32_t nout, uint32_t K, int glu, int splittable) {
     static const struct { const char *name, *glu_name; uint32_t bm, bn; } cfg[] = {
@@ -126,24 +126,22 @@ static int launch_mx(gpu_t *g, NkGemmArgs *a, uint32_t M, uint32_t nout, uint32_
     }
     if (last_ok < 0) return 1;
     uint32_t kz = 1;
-    /* K splits add partial tiles atomically; with fewer than 64 rows that costs more than the idle
-     * CUs it fills (measured), so few-row GEMMs take the smallest tile instead */
-    if (M <= 64) splittable = 0;
     if (pick_i < 0) {
-        /* too few tiles: split K of the 64x128 tile when allowed, else the smallest tile */
-        int i = last_ok;
+        /* too few tiles: the smallest tile that divides the columns, with K split over up to four
+         * workgroups when allowed (partial products added atomically): about 448 workgroups, at
+         * least 16 K steps per share from 112 tiles on and 32 from 200 on (measured on 64 x 64
+         * tiles, 64 to 896 rows, K 1024 to 4096) */
+        pick_i = last_ok;
+        const uint32_t cols = glu ? cfg[pick_i].bn / 2 : cfg[pick_i].bn;
+        tiles = ((M + cfg[pick_i].bm - 1) / cfg[pick_i].bm) * (nout / cols);
         if (splittable) {
-            for (int j = 0; j < 3; ++j)
-                if (cfg[j].bm == 64 && cfg[j].bn == 128 && nout % (glu ? 64 : 128) == 0) i = j;
+            kz = 448 / tiles;
+            if (kz > 4) kz = 4;
+            if (tiles >= 112 && kz > S / 16) kz = S / 16;
+            if (tiles >= 200 && kz > S / 32) kz = S / 32;
+            if (kz > S) kz = S;
+            if (kz < 1) kz = 1;
         }
-        const uint32_t cols = glu ? cfg[i].bn / 2 : cfg[i].bn;
-        tiles = ((M + cfg[i].bm - 1) / cfg[i].bm) * (nout / cols);
-        if (splittable) {
-            kz = (224 + tiles - 1) / tiles;
-            if (kz > 8) kz = 8;
-            if (kz > S / 2) kz = S / 2 > 0 ? S / 2 : 1;
-        }
-        pick_i = i;
     }
     const uint32_t tm = (M + cfg[pick_i].bm - 1) / cfg[pick_i].bm;
     a->splits = kz;

@@ -106,12 +106,13 @@ def test_gemm_many_rows(gpu, M, N, K, act):
     (100, 2048, 1024, 2, 0, True), (37, 1024, 2048, 0, 0, True),
     (445, 4096, 1024, 1, 0, False), (1000, 2048, 1024, 3, 0, False), (3584, 1024, 1024, 0, 1, False),
     (20, 3072, 1024, 0, 0, False), (448, 2560, 1280, 0, 0, True), (1024, 1088, 640, 0, 0, True),
-    (64, 256, 32, 2, 0, True), (96, 128, 64, 0, 1, False)])
+    (64, 256, 32, 2, 0, True), (96, 128, 64, 0, 1, False), (64, 1024, 1024, 0, 1, False),
+    (64, 2560, 1280, 0, 1, False), (224, 1024, 1024, 0, 1, False), (896, 1024, 4096, 0, 1, False)])
 @pytest.mark.parametrize("k64", [1, 0])
 def test_gemm_batched_rows(gpu, M, N, K, act, acc, bias, k64):
     import nemoasr
 
-    nemoasr.lib().nk_gemm_mx_k64(k64)
+    prev = nemoasr.lib().nk_gemm_mx_k64(k64)
     rng = np.random.default_rng([M, N, K, act])
     W = _w(rng, N, K)
     A = rng.standard_normal((M, K)).astype(np.float32)
@@ -121,7 +122,7 @@ def test_gemm_batched_rows(gpu, M, N, K, act, acc, bias, k64):
     try:
         got = run_gemm(gpu, A, W, b, act, acc, 0.5 if acc else 1.0, C0=C0)
     finally:
-        nemoasr.lib().nk_gemm_mx_k64(1)
+        nemoasr.lib().nk_gemm_mx_k64(prev)
     ref = oracle.gemm(A, W, b, act, acc, 0.5 if acc else 1.0, C0=C0)
     assert rel_err(got, ref) < GEMM_TOL, (M, N, K, act)
 
