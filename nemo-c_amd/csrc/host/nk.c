@@ -421,16 +421,23 @@ int nk_dwconv_ln_silu_rows(gpu_t *g, const float *din_base, const int *rows, uin
 
 static uint32_t blocks_for(uint64_t n) { return (uint32_t)((n + 255) / 256); }
 
+/* output columns per workgroup of the subsampling convs: one (every output its own workgroup, one
+ * memory round trip) unless the batch has thousands of output positions, then eight (fewer
+ * workgroups, the filter taps loaded once for eight columns) */
+static uint32_t conv_fb(uint32_t T1, uint32_t F1, uint32_t batch) { return (uint64_t)T1 * F1 * batch >= 4096 ? 8 : 1; }
+
 int nk_conv2d_c1_s2_relu_b(gpu_t *g, const float *X, const float *W, const float *bias, float *Y, uint32_t T,
                            uint32_t F, uint32_t T1, uint32_t F1, uint32_t C, uint32_t batch) {
-    NkConvArgs a = { X, W, bias, Y, T, F, T1, F1, C, 0, T * F, T1 * F1 * C };
-    return gpu_launch(g, "conv2d_c1_s2_relu", &a, sizeof a, T1 * ((F1 + 7) / 8), batch, 1, 256, 1, 1);
+    const uint32_t fb = conv_fb(T1, F1, batch);
+    NkConvArgs a = { X, W, bias, Y, T, F, T1, F1, C, fb, T * F, T1 * F1 * C };
+    return gpu_launch(g, "conv2d_c1_s2_relu", &a, sizeof a, T1 * ((F1 + fb - 1) / fb), batch, 1, 256, 1, 1);
 }
 
 int nk_dwconv2d_s2_b(gpu_t *g, const float *X, const float *W, const float *bias, float *Y, uint32_t T, uint32_t F,
                      uint32_t T1, uint32_t F1, uint32_t C, uint32_t batch) {
-    NkConvArgs a = { X, W, bias, Y, T, F, T1, F1, C, 0, T * F * C, T1 * F1 * C };
-    return gpu_launch(g, "dwconv2d_s2", &a, sizeof a, T1 * ((F1 + 7) / 8), batch, 1, 256, 1, 1);
+    const uint32_t fb = conv_fb(T1, F1, batch);
+    NkConvArgs a = { X, W, bias, Y, T, F, T1, F1, C, fb, T * F * C, T1 * F1 * C };
+    return gpu_launch(g, "dwconv2d_s2", &a, sizeof a, T1 * ((F1 + fb - 1) / fb), batch, 1, 256, 1, 1);
 }
 
 int nk_flatten_cf_b(gpu_t *g, const float *X, float *Y, uint32_t T, uint32_t F, uint32_t C, uint32_t batch) {

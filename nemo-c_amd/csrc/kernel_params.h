@@ -148,12 +148,13 @@ typedef struct {
     NkDwArgs d;
 } NkGemvDwArgs;
 
-/* Subsampling convs. X [T][F] (conv 0) or [T][F][C]; Y [T1][F1][C].  grid.y runs over a batch
- * of windows of the same size, xs / ys floats apart. */
+/* Subsampling convs. X [T][F] (conv 0) or [T][F][C]; Y [T1][F1][C].  grid.x = T1 * ceil(F1 / fb):
+ * a workgroup computes fb consecutive output columns of one output row, its threads the channels;
+ * grid.y runs over a batch of windows of the same size, xs / ys floats apart. */
 typedef struct {
     const float *X, *W, *bias;
     float *Y;
-    u32 T, F, T1, F1, C, pad;
+    u32 T, F, T1, F1, C, fb;
     u32 xs, ys;
 } NkConvArgs;
 

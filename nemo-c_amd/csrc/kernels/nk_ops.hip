@@ -8,14 +8,13 @@
  * columns f1 (grid.x = T1 * ceil(F1/8), grid.y = windows of one size back to back, X and Y strides
  * xs / ys); thread = output channel, holding its 9 taps and bias in registers for the 8 columns.
  * Each output sums bias, then taps in (kh, kw) order. */
-#define CONV_FB 8
 /* 1 input channel -> C channels + ReLU: X [T][F] -> Y [T1][F1][C] */
 extern "C" __global__ __launch_bounds__(256) void conv2d_c1_s2_relu(NkConvArgs a) {
-    const u32 nfb = (a.F1 + CONV_FB - 1) / CONV_FB;
-    const u32 t1 = blockIdx.x / nfb, f0 = (blockIdx.x % nfb) * CONV_FB;
+    const u32 nfb = (a.F1 + a.fb - 1) / a.fb;
+    const u32 t1 = blockIdx.x / nfb, f0 = (blockIdx.x % nfb) * a.fb;
     const float *X = a.X + (u64)blockIdx.y * a.xs;
     float *Y = a.Y + (u64)blockIdx.y * a.ys;
-    const u32 fe = min(f0 + CONV_FB, a.F1);
+    const u32 fe = min(f0 + a.fb, a.F1);
     for (u32 o = threadIdx.x; o < a.C; o += 256) {
         float w[9];
 #pragma unroll
@@ -41,11 +40,11 @@ extern "C" __global__ __launch_bounds__(256) void conv2d_c1_s2_relu(NkConvArgs a
 
 /* depthwise, + bias, no activation: X [T][F][C] -> Y [T1][F1][C] */
 extern "C" __global__ __launch_bounds__(256) void dwconv2d_s2(NkConvArgs a) {
-    const u32 nfb = (a.F1 + CONV_FB - 1) / CONV_FB;
-    const u32 t1 = blockIdx.x / nfb, f0 = (blockIdx.x % nfb) * CONV_FB;
+    const u32 nfb = (a.F1 + a.fb - 1) / a.fb;
+    const u32 t1 = blockIdx.x / nfb, f0 = (blockIdx.x % nfb) * a.fb;
     const float *X = a.X + (u64)blockIdx.y * a.xs;
     float *Y = a.Y + (u64)blockIdx.y * a.ys;
-    const u32 fe = min(f0 + CONV_FB, a.F1);
+    const u32 fe = min(f0 + a.fb, a.F1);
     for (u32 c = threadIdx.x; c < a.C; c += 256) {
         float w[9];
 #pragma unroll
