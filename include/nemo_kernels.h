@@ -150,6 +150,17 @@ int nk_flatten_cf_b(gpu_t *g, const float *X, float *Y, uint32_t T, uint32_t F, 
 /* dst[m] = src[map[m]] for m < rows (cols floats per row) */
 int nk_gather_rows(gpu_t *g, const float *src, uint32_t src_ld, const int *map, float *dst, uint32_t dst_ld,
                    uint32_t rows, uint32_t cols);
+/* dst row map[m] = src row m, m < rows (distinct targets). */
+int nk_scatter_rows(gpu_t *g, const float *src, uint32_t src_ld, const int *map, float *dst, uint32_t dst_ld,
+                    uint32_t rows, uint32_t cols);
+/* Log-mel rows of F frames (all pointers device): frame f reads the 512 pre-emphasised samples
+ * span[tab[2f] ..] and writes row tab[2f+1] of out (rows of 128 floats); tables as the host front
+ * end's (window [512], filterbank [128][257], filter bin ranges, double twiddles [256], bit reversal
+ * [512]).  The power spectrum equals the host front end's (same double arithmetic, no contraction);
+ * the log may differ by rounding. */
+int nk_mel_frames(gpu_t *g, const float *span, const int *tab, uint32_t F, const float *win, const float *fb,
+                  const int *fb_lo, const int *fb_hi, const double *tw_re, const double *tw_im, const uint16_t *rev,
+                  float *out);
 int nk_copy(gpu_t *g, const float *src, float *dst, uint32_t n);
 int nk_copy2d(gpu_t *g, const float *src, uint32_t src_ld, float *dst, uint32_t dst_ld, uint32_t rows, uint32_t cols);
 int nk_fill(gpu_t *g, float *dst, uint32_t n, float value);

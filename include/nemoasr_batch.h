@@ -68,6 +68,10 @@ void nemoasr_batch_debug_set_dump(nemoasr_batch_t *b, int on);
 /* 1 (default): the greedy loop runs on the device, graph-replayed runs of steps; 0: one host round
    trip per joint evaluation.  Select before the first step of a batch. */
 void nemoasr_batch_debug_device_decoder(nemoasr_batch_t *b, int on);
+/* 1 (default): log-mel on the GPU (frames computed when a window takes them, kept in per-stream
+   device rings; within one stream audio and mel input cannot be mixed); 0: on the host's threads.
+   Only before any input; returns -1 afterwards. */
+int nemoasr_batch_debug_gpu_frontend(nemoasr_batch_t *b, int on);
 const float *nemoasr_batch_debug_joint_enc(const nemoasr_batch_t *b, int stream, size_t *frames);
 /* Per-kernel timing of direct launches (kernel: exact name or a prefix ending in '*'): mean ms per
    launch, launches, and the summed algorithmic bytes and flops of those launches. */

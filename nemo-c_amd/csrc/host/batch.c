@@ -39,6 +39,7 @@
 #define MAX_BGRAPHS 8
 #define MAX_SIG_GROUPS 8
 #define POOL_MAX 16       /* host threads for the log-mel front end of a step */
+#define MEL_RING 512      /* device log-mel rows kept per stream (GPU front end) */
 
 static double now_ms(void) {
     struct timespec ts;
@@ -57,6 +58,9 @@ typedef struct {
     size_t pending_n, pending_cap;
     float mel_cache[MEL_CACHE * MEL_NMEL];
     int mel_cache_n;
+    int src;                            /* GPU front end: 0 no input yet, 1 audio, 2 mel rows */
+    size_t fr_taken;                    /* frames taken into windows so far */
+    size_t fr_lo;                       /* oldest frame a window of the current step may read */
     size_t consumed, emitted;
     int closed, final;
     int pos, cache_len;                 /* cache rows of this stream */
@@ -104,6 +108,17 @@ struct nemoasr_batch {
     int *order, *gid;              /* streams with a chunk this step, in row order; their group */
     int ng, *g_nwin, *g_cnt, *g_woff, *g_poff, *g_fill, *ord;
     float *wtmp;                   /* host scratch for chunks that emit no rows */
+    /* GPU log-mel front end: per-stream rings of mel rows; each step stages the sample spans of the
+     * frames its windows take (frames are computed when taken), then one mel_frames launch fills
+     * the rings and a row gather builds the windows */
+    int gpu_fe;
+    gpu_buf_t *ring, *meltab, *span_dev, *ftab_dev, *wmap_dev, *hrow_dev, *hmap_dev;
+    float *stage_span, *stage_hrow;
+    int *stage_ftab, *stage_wmap, *stage_hmap;
+    size_t span_cap, span_n;       /* floats */
+    size_t ftab_cap, ftab_n;       /* ints (two per frame) */
+    size_t hrow_cap, hrow_n;       /* floats of mel rows given by the host (push_mel) */
+    size_t hmap_cap, wmap_cap;     /* ints */
     /* encoder */
     gpu_buf_t *win, *c0, *c1, *c2, *c3, *c4, *flat, *pre_out;
     gpu_buf_t *h, *tmp, *lnb, *ff, *att, *y, *ph, *prompted, *joint_enc, *kv, *din, *etab;
@@ -248,6 +263,73 @@ static int build_decoder_weights(nemoasr_batch_t *b) {
     free(cat);
     free(wo);
     free(bo);
+    return rc;
+}
+
+/* ---- GPU log-mel front end ---------------------------------------------------------------------- */
+/* device tables in one buffer: twiddles (2 x 256 double), window [512], filterbank [128][257],
+ * filter bin ranges (2 x 128 int), bit reversal [512] u16 */
+#define MT_TWR 0
+#define MT_TWI (MT_TWR + 256 * 8)
+#define MT_WIN (MT_TWI + 256 * 8)
+#define MT_FB (MT_WIN + MEL_NFFT * 4)
+#define MT_LO (MT_FB + MEL_NMEL * MEL_NBIN * 4)
+#define MT_HI (MT_LO + MEL_NMEL * 4)
+#define MT_REV (MT_HI + MEL_NMEL * 4)
+#define MT_BYTES (MT_REV + MEL_NFFT * 2)
+
+/* grow a pinned staging buffer and its device twin to hold `need` elements of `esz` bytes,
+ * keeping the first `keep` elements of the staging buffer */
+static int grow_stage(gpu_t *g, void **stage, gpu_buf_t **dev, size_t *cap, size_t need, size_t keep, size_t esz) {
+    if (need <= *cap) return 0;
+    size_t nc = *cap ? *cap : 1024;
+    while (nc < need) nc *= 2;
+    void *ns = gpu_host_alloc(g, nc * esz);
+    gpu_buf_t *nd = dev ? gpu_buf_alloc(g, nc * esz) : NULL;
+    if (!ns || (dev && !nd)) {
+        gpu_host_free(ns);
+        gpu_buf_free(nd);
+        return -1;
+    }
+    if (keep && *stage) memcpy(ns, *stage, keep * esz);
+    gpu_host_free(*stage);
+    *stage = ns;
+    if (dev) {
+        gpu_buf_free(*dev);
+        *dev = nd;
+    }
+    *cap = nc;
+    return 0;
+}
+
+static int mel_gpu_setup(nemoasr_batch_t *b) {
+    gpu_t *g = b->g;
+    const size_t S = (size_t)b->S;
+    b->gpu_fe = 1;
+    b->ring = gpu_buf_alloc(g, S * MEL_RING * MEL_NMEL * sizeof(float));
+    b->meltab = gpu_buf_alloc(g, MT_BYTES);
+    b->wmap_dev = gpu_buf_alloc(g, S * (size_t)b->nwin_max * sizeof(int));
+    b->stage_wmap = gpu_host_alloc(g, S * (size_t)b->nwin_max * sizeof(int));
+    b->wmap_cap = S * (size_t)b->nwin_max;
+    if (!b->ring || !b->meltab || !b->wmap_dev || !b->stage_wmap) return -1;
+    melfe_t *mf = melfe_create();
+    melfe_tables_t t;
+    melfe_tables(mf, &t);
+    char *h = calloc(1, MT_BYTES);
+    memcpy(h + MT_TWR, t.tw_re, 256 * 8);
+    memcpy(h + MT_TWI, t.tw_im, 256 * 8);
+    memcpy(h + MT_WIN, t.win, MEL_NFFT * 4);
+    memcpy(h + MT_FB, t.fb, MEL_NMEL * MEL_NBIN * 4);
+    memcpy(h + MT_LO, t.fb_lo, MEL_NMEL * 4);
+    memcpy(h + MT_HI, t.fb_hi, MEL_NMEL * 4);
+    memcpy(h + MT_REV, t.rev, MEL_NFFT * 2);
+    const int rc = gpu_upload(g, gpu_buf_dptr(b->meltab), h, MT_BYTES);
+    free(h);
+    melfe_destroy(mf);
+    const size_t fr = S * (size_t)b->nwin_max;
+    if (grow_stage(g, (void **)&b->stage_span, &b->span_dev, &b->span_cap, fr * MEL_HOP + S * MEL_NFFT, 0, sizeof(float)) ||
+        grow_stage(g, (void **)&b->stage_ftab, &b->ftab_dev, &b->ftab_cap, 2 * fr, 0, sizeof(int)))
+        return -1;
     return rc;
 }
 
@@ -427,6 +509,11 @@ nemoasr_batch_t *nemoasr_batch_open(const char *model_dir, const char *language,
             return NULL;
         }
     b->device_dec = device_dec_ok(b);
+    if (mel_gpu_setup(b)) {
+        snprintf(err, errlen, "batch: log-mel front end setup failed: %s", gpu_last_error(g));
+        nemoasr_batch_close(b);
+        return NULL;
+    }
     b->fe_list = malloc(S * sizeof(int));
     pool_start(&b->pool, b);
     b->use_graphs = 1;
@@ -444,10 +531,16 @@ void nemoasr_batch_close(nemoasr_batch_t *b) {
                           b->ff, b->att, b->y, b->ph, b->prompted, b->joint_enc, b->kv, b->din, b->etab, b->wcat[0],
                           b->wcat[1], b->wout, b->bout, b->hc, b->lin, b->gates, b->hout, b->hout2, b->pred,
                           b->jin, b->logits, b->amax, b->dtab, b->bst, b->bsetup, b->btok, b->lin1, b->tx,
-                          b->wcati[0], b->wcati[1], b->bi[0], b->bi[1], b->keys };
+                          b->wcati[0], b->wcati[1], b->bi[0], b->bi[1], b->keys, b->ring, b->meltab, b->span_dev,
+                          b->ftab_dev, b->wmap_dev, b->hrow_dev, b->hmap_dev };
     for (size_t i = 0; i < sizeof bufs / sizeof *bufs; ++i) gpu_buf_free(bufs[i]);
     gpu_host_free(b->stage_win);
     gpu_host_free(b->stage_tab);
+    gpu_host_free(b->stage_span);
+    gpu_host_free(b->stage_hrow);
+    gpu_host_free(b->stage_ftab);
+    gpu_host_free(b->stage_wmap);
+    gpu_host_free(b->stage_hmap);
     gpu_host_free(b->stage_dtab);
     gpu_host_free(b->stage_amax);
     gpu_host_free(b->stage_bst);
@@ -500,13 +593,18 @@ static void queue_mel(bstream_t *x, const float *mel, size_t nframes) {
 /* log-mel of the audio queued for one stream (src/nemoasr.c:134-160 without resampling: audio
  * is pushed at 16 kHz); a final push with no samples and an empty front end flushes nothing
  * (src/nemoasr.c:146) */
-static void front_end(bstream_t *x) {
+static void front_end(const nemoasr_batch_t *b, bstream_t *x) {
     if (!x->aq_n && !x->fe_final) return;
     if (!(x->fe_final && x->aq_n == 0 && melfe_samples(x->mel) == 0)) {
-        const float *frames;
-        size_t nf;
-        melfe_push(x->mel, x->aq, x->aq_n, x->fe_final, &frames, &nf);
-        queue_mel(x, frames, nf);
+        if (b->gpu_fe) {
+            /* samples only: the frames are computed on the GPU when a window takes them */
+            x->pending_n = melfe_append(x->mel, x->aq, x->aq_n, x->fe_final);
+        } else {
+            const float *frames;
+            size_t nf;
+            melfe_push(x->mel, x->aq, x->aq_n, x->fe_final, &frames, &nf);
+            queue_mel(x, frames, nf);
+        }
     }
     x->aq_n = 0;
     if (x->fe_final) {
@@ -530,7 +628,7 @@ static void *pool_main(void *arg) {
         for (;;) {
             const int i = __atomic_fetch_add(&p->next, 1, __ATOMIC_RELAXED);
             if (i >= p->count) break;
-            front_end(&p->b->st[p->list[i]]);
+            front_end(p->b, &p->b->st[p->list[i]]);
         }
         pthread_mutex_lock(&p->mu);
         if (--p->busy == 0) pthread_cond_signal(&p->done);
@@ -577,7 +675,7 @@ static void front_end_all(nemoasr_batch_t *b) {
     if (!count) return;
     pool_t *p = &b->pool;
     if (count == 1 || p->n == 0) {
-        for (int i = 0; i < count; ++i) front_end(&b->st[b->fe_list[i]]);
+        for (int i = 0; i < count; ++i) front_end(b, &b->st[b->fe_list[i]]);
         return;
     }
     pthread_mutex_lock(&p->mu);
@@ -591,7 +689,7 @@ static void front_end_all(nemoasr_batch_t *b) {
     for (;;) {
         const int i = __atomic_fetch_add(&p->next, 1, __ATOMIC_RELAXED);
         if (i >= count) break;
-        front_end(&b->st[b->fe_list[i]]);
+        front_end(b, &b->st[b->fe_list[i]]);
     }
     pthread_mutex_lock(&p->mu);
     while (p->busy > 0) pthread_cond_wait(&p->done, &p->mu);
@@ -604,8 +702,13 @@ int nemoasr_batch_push_mel(nemoasr_batch_t *b, int stream, const float *mel, siz
     if (check_stream(b, stream, err, errlen)) return -1;
     bstream_t *x = &b->st[stream];
     if (x->ended) { snprintf(err, errlen, "stream %d already ended", stream); return -1; }
-    front_end(x); /* audio queued before these frames goes first */
+    if (b->gpu_fe && x->src == 1) {
+        snprintf(err, errlen, "stream %d: audio and mel input cannot be mixed before a reset", stream);
+        return -1;
+    }
+    front_end(b, x); /* audio queued before these frames goes first */
     queue_mel(x, mel, nframes);
+    if (nframes || final) x->src = 2;
     if (final) x->ended = x->final = 1;
     return 0;
 }
@@ -617,6 +720,11 @@ int nemoasr_batch_push(nemoasr_batch_t *b, int stream, const float *samples, siz
     if (check_stream(b, stream, err, errlen)) return -1;
     bstream_t *x = &b->st[stream];
     if (x->ended) { snprintf(err, errlen, "stream %d already ended", stream); return -1; }
+    if (b->gpu_fe && x->src == 2) {
+        snprintf(err, errlen, "stream %d: audio and mel input cannot be mixed before a reset", stream);
+        return -1;
+    }
+    x->src = 1;
     if (n) {
         if (x->aq_n + n > x->aq_cap) {
             x->aq_cap = (x->aq_n + n) * 2;
@@ -629,24 +737,73 @@ int nemoasr_batch_push(nemoasr_batch_t *b, int stream, const float *samples, siz
     return 0;
 }
 
-/* Window of the planned chunk (mel cache ++ the rows taken) into dst; advance the stream's mel
- * bookkeeping exactly as a single-stream encoder step does. */
-static void take_window(bstream_t *x, float *dst) {
+/* Window of the planned chunk (mel cache ++ the rows taken); advance the stream's mel bookkeeping
+ * exactly as a single-stream encoder step does.  Host front end: the window's rows go into dst.
+ * GPU front end: the frames taken are staged (their sample spans for mel_frames, or the host's mel
+ * rows for a scatter into the ring) and, when wrow >= 0, the window's ring rows go into the gather
+ * map from row wrow on. */
+static int take_window(nemoasr_batch_t *b, int s, float *dst, long wrow, char *err, size_t errlen) {
+    bstream_t *x = &b->st[s];
     const enc_plan_t *p = &x->plan;
-    const size_t rowb = MEL_NMEL * sizeof(float);
-    memcpy(dst, x->mel_cache, (size_t)x->cache_before * rowb);
-    memcpy(dst + (size_t)x->cache_before * MEL_NMEL, x->pending, (size_t)p->take * rowb);
-    memcpy(x->mel_cache, dst + (size_t)(p->nwin - x->book.mel_cache_n) * MEL_NMEL, (size_t)x->book.mel_cache_n * rowb);
-    memmove(x->pending, x->pending + (size_t)p->take * MEL_NMEL, (x->pending_n - (size_t)p->take) * rowb);
+    const size_t rowb = MEL_NMEL * sizeof(float), take = (size_t)p->take;
+    if (b->gpu_fe) {
+        gpu_t *g = b->g;
+        const size_t f0 = x->fr_taken - (size_t)x->cache_before;
+        if (x->fr_taken + take - x->fr_lo > MEL_RING) {
+            snprintf(err, errlen, "stream %d: more than %d log-mel frames in one step", s, MEL_RING);
+            return -1;
+        }
+        if (wrow >= 0)
+            for (int i = 0; i < p->nwin; ++i) b->stage_wmap[wrow + i] = s * MEL_RING + (int)((f0 + (size_t)i) % MEL_RING);
+        if (take && x->src == 2) {
+            const size_t hr = b->hrow_n / MEL_NMEL;
+            if (grow_stage(g, (void **)&b->stage_hrow, &b->hrow_dev, &b->hrow_cap, b->hrow_n + take * MEL_NMEL, b->hrow_n,
+                           sizeof(float)) ||
+                grow_stage(g, (void **)&b->stage_hmap, &b->hmap_dev, &b->hmap_cap, hr + take, hr, sizeof(int))) {
+                snprintf(err, errlen, "batch: out of memory for staged mel rows");
+                return -1;
+            }
+            memcpy(b->stage_hrow + b->hrow_n, x->pending, take * rowb);
+            for (size_t t = 0; t < take; ++t) b->stage_hmap[hr + t] = s * MEL_RING + (int)((x->fr_taken + t) % MEL_RING);
+            b->hrow_n += take * MEL_NMEL;
+            memmove(x->pending, x->pending + take * MEL_NMEL, (x->pending_n - take) * rowb);
+        } else if (take) {
+            const size_t len = melfe_span_len(take);
+            if (grow_stage(g, (void **)&b->stage_span, &b->span_dev, &b->span_cap, b->span_n + len, b->span_n,
+                           sizeof(float)) ||
+                grow_stage(g, (void **)&b->stage_ftab, &b->ftab_dev, &b->ftab_cap, b->ftab_n + 2 * take, b->ftab_n,
+                           sizeof(int))) {
+                snprintf(err, errlen, "batch: out of memory for staged audio");
+                return -1;
+            }
+            if (melfe_take(x->mel, b->stage_span + b->span_n, take) != take) {
+                snprintf(err, errlen, "stream %d: front end has fewer frames than planned", s);
+                return -1;
+            }
+            for (size_t t = 0; t < take; ++t) {
+                b->stage_ftab[b->ftab_n + 2 * t] = (int)(b->span_n + t * MEL_HOP);
+                b->stage_ftab[b->ftab_n + 2 * t + 1] = s * MEL_RING + (int)((x->fr_taken + t) % MEL_RING);
+            }
+            b->span_n += len;
+            b->ftab_n += 2 * take;
+        }
+        x->fr_taken += take;
+    } else {
+        memcpy(dst, x->mel_cache, (size_t)x->cache_before * rowb);
+        memcpy(dst + (size_t)x->cache_before * MEL_NMEL, x->pending, take * rowb);
+        memcpy(x->mel_cache, dst + (size_t)(p->nwin - x->book.mel_cache_n) * MEL_NMEL, (size_t)x->book.mel_cache_n * rowb);
+        memmove(x->pending, x->pending + take * MEL_NMEL, (x->pending_n - take) * rowb);
+    }
     x->pending_n = x->book.pending_n;
     x->consumed = x->book.consumed;
     x->emitted = x->book.emitted;
     x->mel_cache_n = x->book.mel_cache_n;
+    return 0;
 }
 
 /* The next chunk of one stream that yields rows (chunks that yield none are consumed on the way).
  * Returns 1 if the stream consumed input. */
-static int plan_stream(nemoasr_batch_t *b, bstream_t *x) {
+static int plan_stream(nemoasr_batch_t *b, bstream_t *x, char *err, size_t errlen) {
     int ran = 0;
     x->c = 0;
     for (;;) {
@@ -657,7 +814,7 @@ static int plan_stream(nemoasr_batch_t *b, bstream_t *x) {
         if (!x->plan.ran) return ran;
         ran = 1;
         if (x->plan.c <= 0) {
-            take_window(x, b->wtmp);
+            if (take_window(b, (int)(x - b->st), b->wtmp, -1, err, errlen)) return -1;
             continue;
         }
         x->c = x->plan.c;
@@ -774,9 +931,13 @@ static int encoder_batch_step(nemoasr_batch_t *b, int *M_out, char *err, size_t 
     const double tf = now_ms();
     front_end_all(b);
     b->stats.frontend_ms += now_ms() - tf;
+    b->span_n = b->ftab_n = b->hrow_n = 0;
     for (int s = 0; s < b->S; ++s) {
         bstream_t *x = &b->st[s];
-        consumed += plan_stream(b, x);
+        x->fr_lo = x->fr_taken - (size_t)x->mel_cache_n;
+        const int r = plan_stream(b, x, err, errlen);
+        if (r < 0) return -1;
+        consumed += r;
         if (x->c > 0) b->order[nact++] = s;
     }
     *M_out = 0;
@@ -820,7 +981,11 @@ static int encoder_batch_step(nemoasr_batch_t *b, int *M_out, char *err, size_t 
         const int T3 = sub_len(sub_len(sub_len(x->nwin)));
         x->gk = k;
         x->gj = j;
-        take_window(x, b->stage_win + ((size_t)b->g_woff[k] + (size_t)j * x->nwin) * F);
+        const size_t wr = (size_t)b->g_woff[k] + (size_t)j * x->nwin;
+        if (take_window(b, s, b->stage_win + wr * F, (long)wr, err, errlen)) {
+            gpu_end(g, NULL, 0);
+            return -1;
+        }
         if (x->pos + x->c > b->cap_rows) compact_stream(b, s);
         const int L = x->cache_len + x->c;
         if (L > b->Lmax || x->pos < x->cache_len || x->pos < b->conv_left || x->pos + x->c > b->cap_rows ||
@@ -859,7 +1024,32 @@ static int encoder_batch_step(nemoasr_batch_t *b, int *M_out, char *err, size_t 
         chunks[4 * i + 2] = x->c;
         chunks[4 * i + 3] = x->cache_len;
     }
-    gpu_upload_async(g, gpu_buf_dptr(b->win), b->stage_win, (size_t)woff * F * sizeof(float));
+    if (b->gpu_fe) {
+        /* log-mel of the frames taken into the rings, the host's mel rows scattered into them, then
+           every window gathered from its stream's ring */
+        const char *t = gpu_buf_dptr(b->meltab);
+        float *ring = gpu_buf_dptr(b->ring);
+        const size_t nf = b->ftab_n / 2, nh = b->hrow_n / MEL_NMEL;
+        if (nf) {
+            gpu_upload_async(g, gpu_buf_dptr(b->span_dev), b->stage_span, b->span_n * sizeof(float));
+            gpu_upload_async(g, gpu_buf_dptr(b->ftab_dev), b->stage_ftab, b->ftab_n * sizeof(int));
+            nk_mel_frames(g, gpu_buf_dptr(b->span_dev), gpu_buf_dptr(b->ftab_dev), (uint32_t)nf,
+                          (const float *)(t + MT_WIN), (const float *)(t + MT_FB), (const int *)(t + MT_LO),
+                          (const int *)(t + MT_HI), (const double *)(t + MT_TWR), (const double *)(t + MT_TWI),
+                          (const uint16_t *)(t + MT_REV), ring);
+        }
+        if (nh) {
+            gpu_upload_async(g, gpu_buf_dptr(b->hrow_dev), b->stage_hrow, b->hrow_n * sizeof(float));
+            gpu_upload_async(g, gpu_buf_dptr(b->hmap_dev), b->stage_hmap, nh * sizeof(int));
+            nk_scatter_rows(g, gpu_buf_dptr(b->hrow_dev), MEL_NMEL, gpu_buf_dptr(b->hmap_dev), ring, MEL_NMEL,
+                            (uint32_t)nh, MEL_NMEL);
+        }
+        gpu_upload_async(g, gpu_buf_dptr(b->wmap_dev), b->stage_wmap, (size_t)woff * sizeof(int));
+        nk_gather_rows(g, ring, MEL_NMEL, gpu_buf_dptr(b->wmap_dev), gpu_buf_dptr(b->win), (uint32_t)F, (uint32_t)woff,
+                       (uint32_t)F);
+    } else {
+        gpu_upload_async(g, gpu_buf_dptr(b->win), b->stage_win, (size_t)woff * F * sizeof(float));
+    }
     gpu_upload_async(g, gpu_buf_dptr(b->etab), crow, (size_t)(6 * M + 4 * nact) * sizeof(int));
     bgraph_t *gs = b->use_graphs ? bgraph_slot(b, M) : NULL;
     if (gs) {
@@ -1236,6 +1426,15 @@ void nemoasr_batch_debug_use_graphs(nemoasr_batch_t *b, int on) {
         gpu_graph_free(b->dgraph);
         b->dgraph = NULL;
     }
+}
+
+int nemoasr_batch_debug_gpu_frontend(nemoasr_batch_t *b, int on) {
+    for (int s = 0; s < b->S; ++s) {
+        const bstream_t *x = &b->st[s];
+        if (x->src || x->pending_n || x->aq_n || x->consumed) return -1;
+    }
+    b->gpu_fe = on != 0;
+    return 0;
 }
 
 void nemoasr_batch_debug_device_decoder(nemoasr_batch_t *b, int on) {

@@ -13,6 +13,9 @@ struct melfe {
     float prev;
     int started, closed;
     size_t total, next;     /* samples received; next frame index to emit */
+    size_t end;             /* frames complete so far (next .. end-1 not yet taken) */
+    float *span;            /* melfe_push's span buffer */
+    size_t span_cap;
     float win[MEL_NFFT];
     float fb[MEL_NMEL][MEL_NBIN];
     int fb_lo[MEL_NMEL], fb_hi[MEL_NMEL]; /* nonzero bin range per filter */
@@ -77,6 +80,7 @@ void melfe_destroy(melfe_t *m) {
     if (!m) return;
     free(m->y);
     free(m->out);
+    free(m->span);
     free(m);
 }
 size_t melfe_samples(const melfe_t *m) { return m->total; }
@@ -114,17 +118,19 @@ static float at(const melfe_t *m, long g) {
     return (i >= 0 && i < (long)m->ny) ? m->y[i] : 0.0f;
 }
 
-void melfe_push(melfe_t *m, const float *x, size_t n, int final, const float **frames, size_t *nframes) {
-    *frames = NULL;
-    *nframes = 0;
-    if (m->closed) return;
+size_t melfe_append(melfe_t *m, const float *x, size_t n, int final) {
+    if (m->closed) return m->end > m->next ? m->end - m->next : 0;
     if (m->ny + n > m->cap) {
         while (m->ny + n > m->cap) m->cap *= 2;
         m->y = realloc(m->y, m->cap * sizeof(float));
     }
-    for (size_t i = 0; i < n; ++i) {
-        m->y[m->ny++] = m->started ? x[i] - PRE_EMPH * m->prev : x[i];
-        m->prev = x[i];
+    if (n) {
+        /* y[i] = x[i] - 0.97 x[i-1] (the first sample of the stream passes unchanged) */
+        float *y = m->y + m->ny;
+        y[0] = m->started ? x[0] - PRE_EMPH * m->prev : x[0];
+        for (size_t i = 1; i < n; ++i) y[i] = x[i] - PRE_EMPH * x[i - 1];
+        m->ny += n;
+        m->prev = x[n - 1];
         m->started = 1;
     }
     m->total += n;
@@ -132,32 +138,24 @@ void melfe_push(melfe_t *m, const float *x, size_t n, int final, const float **f
     if (final) end = m->total / MEL_HOP + 1;
     else end = m->total >= HALF ? (m->total - HALF) / MEL_HOP + 1 : 0; /* every sample of the frame is in */
     if (final) m->closed = 1;
-    if (end <= m->next) return;
-    const size_t cnt = end - m->next;
-    if (cnt * MEL_NMEL > m->out_cap) {
-        m->out_cap = cnt * MEL_NMEL;
-        m->out = realloc(m->out, m->out_cap * sizeof(float));
-    }
-    double re[MEL_NFFT], im[MEL_NFFT];
-    float pw[MEL_NBIN];
-    for (size_t t = m->next; t < end; ++t) {
-        const long base = (long)t * MEL_HOP - HALF;
-        for (int k = 0; k < MEL_NFFT; ++k) {
-            re[k] = (double)(at(m, base + k) * m->win[k]);
-            im[k] = 0.0;
-        }
-        fft(m, re, im);
-        for (int k = 0; k < MEL_NBIN; ++k) pw[k] = (float)(re[k] * re[k] + im[k] * im[k]);
-        float *row = m->out + (t - m->next) * MEL_NMEL;
-        for (int b = 0; b < MEL_NMEL; ++b) {
-            float acc = 0.0f;
-            for (int k = m->fb_lo[b]; k < m->fb_hi[b]; ++k) acc += m->fb[b][k] * pw[k];
-            row[b] = logf(acc + LOG_FLOOR);
-        }
-    }
-    *frames = m->out;
-    *nframes = cnt;
-    m->next = end;
+    if (end > m->end) m->end = end;
+    return m->end > m->next ? m->end - m->next : 0;
+}
+
+size_t melfe_span_len(size_t cnt) { return cnt ? (cnt - 1) * MEL_HOP + MEL_NFFT : 0; }
+
+size_t melfe_take(melfe_t *m, float *span, size_t kmax) {
+    size_t cnt = m->end > m->next ? m->end - m->next : 0;
+    if (cnt > kmax) cnt = kmax;
+    if (!cnt) return 0;
+    const long base = (long)m->next * MEL_HOP - HALF, len = (long)melfe_span_len(cnt), n = (long)m->total;
+    /* samples inside the stream come straight from the buffer; reflected ones through at() */
+    long lo = base < 0 ? -base : 0, hi = n - base < len ? n - base : len;
+    if (hi < lo || base + lo < (long)m->y0 || base + hi > (long)(m->y0 + m->ny)) lo = hi = 0;
+    for (long i = 0; i < lo; ++i) span[i] = at(m, base + i);
+    if (hi > lo) memcpy(span + lo, m->y + (base + lo - (long)m->y0), (size_t)(hi - lo) * sizeof(float));
+    for (long i = hi > lo ? hi : lo; i < len; ++i) span[i] = at(m, base + i);
+    m->next += cnt;
     /* drop samples no future frame reads */
     const long keep = (long)m->next * MEL_HOP - HALF - 4;
     if (keep > (long)m->y0) {
@@ -167,4 +165,55 @@ void melfe_push(melfe_t *m, const float *x, size_t n, int final, const float **f
         m->ny -= drop;
         m->y0 += drop;
     }
+    return cnt;
+}
+
+void melfe_compute(const melfe_t *m, const float *span, size_t cnt, float *out) {
+    double re[MEL_NFFT], im[MEL_NFFT];
+    float pw[MEL_NBIN];
+    for (size_t t = 0; t < cnt; ++t) {
+        const float *fr = span + t * MEL_HOP;
+        for (int k = 0; k < MEL_NFFT; ++k) {
+            re[k] = (double)(fr[k] * m->win[k]);
+            im[k] = 0.0;
+        }
+        fft(m, re, im);
+        for (int k = 0; k < MEL_NBIN; ++k) pw[k] = (float)(re[k] * re[k] + im[k] * im[k]);
+        float *row = out + t * MEL_NMEL;
+        for (int b = 0; b < MEL_NMEL; ++b) {
+            float acc = 0.0f;
+            for (int k = m->fb_lo[b]; k < m->fb_hi[b]; ++k) acc += m->fb[b][k] * pw[k];
+            row[b] = logf(acc + LOG_FLOOR);
+        }
+    }
+}
+
+void melfe_push(melfe_t *m, const float *x, size_t n, int final, const float **frames, size_t *nframes) {
+    *frames = NULL;
+    *nframes = 0;
+    const size_t cnt = melfe_append(m, x, n, final);
+    if (!cnt) return;
+    const size_t len = melfe_span_len(cnt);
+    if (len > m->span_cap) {
+        m->span_cap = len;
+        m->span = realloc(m->span, m->span_cap * sizeof(float));
+    }
+    if (cnt * MEL_NMEL > m->out_cap) {
+        m->out_cap = cnt * MEL_NMEL;
+        m->out = realloc(m->out, m->out_cap * sizeof(float));
+    }
+    melfe_take(m, m->span, cnt);
+    melfe_compute(m, m->span, cnt, m->out);
+    *frames = m->out;
+    *nframes = cnt;
+}
+
+void melfe_tables(const melfe_t *m, melfe_tables_t *t) {
+    t->win = m->win;
+    t->fb = &m->fb[0][0];
+    t->fb_lo = m->fb_lo;
+    t->fb_hi = m->fb_hi;
+    t->tw_re = m->tw_re;
+    t->tw_im = m->tw_im;
+    t->rev = m->rev;
 }

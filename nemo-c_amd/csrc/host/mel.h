@@ -23,4 +23,28 @@ void melfe_push(melfe_t *m, const float *x, size_t n, int final, const float **f
 size_t melfe_samples(const melfe_t *m);
 size_t melfe_frames(const melfe_t *m);
 
+/* melfe_push in three parts, for front ends that compute the frames elsewhere (the batched GPU
+ * front end):
+ *   melfe_append  appends n samples (final flushes the tail) and returns how many complete frames
+ *                 are waiting to be taken;
+ *   melfe_take    writes the pre-emphasised samples the first cnt = min(kmax, waiting) frames read
+ *                 (melfe_span_len(cnt) floats: frame t reads span[t*MEL_HOP .. t*MEL_HOP + MEL_NFFT),
+ *                 reflection at both ends applied), marks them taken and returns cnt;
+ *   melfe_compute turns cnt frames of a span into log-mel rows (the host computation). */
+size_t melfe_append(melfe_t *m, const float *x, size_t n, int final);
+size_t melfe_span_len(size_t cnt);
+size_t melfe_take(melfe_t *m, float *span, size_t kmax);
+void melfe_compute(const melfe_t *m, const float *span, size_t cnt, float *out);
+
+/* The front end's constant tables (identical for every instance): window [MEL_NFFT], filterbank
+ * [MEL_NMEL][MEL_NBIN] with each filter's nonzero bin range [fb_lo, fb_hi), FFT twiddles
+ * e^{-2 pi i k / MEL_NFFT} for k < MEL_NFFT/2 (double), bit-reversal permutation [MEL_NFFT]. */
+typedef struct {
+    const float *win, *fb;
+    const int *fb_lo, *fb_hi;
+    const double *tw_re, *tw_im;
+    const unsigned short *rev;
+} melfe_tables_t;
+void melfe_tables(const melfe_t *m, melfe_tables_t *t);
+
 #endif

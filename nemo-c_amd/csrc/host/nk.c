@@ -440,6 +440,14 @@ int nk_dwconv2d_s2_b(gpu_t *g, const float *X, const float *W, const float *bias
     return gpu_launch(g, "dwconv2d_s2", &a, sizeof a, T1 * ((F1 + fb - 1) / fb), batch, 1, 256, 1, 1);
 }
 
+int nk_mel_frames(gpu_t *g, const float *span, const int *tab, uint32_t F, const float *win, const float *fb,
+                  const int *fb_lo, const int *fb_hi, const double *tw_re, const double *tw_im, const uint16_t *rev,
+                  float *out) {
+    if (!F) return 0;
+    NkMelArgs a = { span, tab, win, fb, fb_lo, fb_hi, tw_re, tw_im, rev, out, F, 0 };
+    return gpu_launch(g, "mel_frames", &a, sizeof a, F, 1, 1, 256, 1, 1);
+}
+
 int nk_flatten_cf_b(gpu_t *g, const float *X, float *Y, uint32_t T, uint32_t F, uint32_t C, uint32_t batch) {
     NkFlatArgs a = { X, Y, T, F, C, 0 };
     return gpu_launch(g, "flatten_cf", &a, sizeof a, blocks_for((uint64_t)T * F * C), batch, 1, 256, 1, 1);
@@ -464,6 +472,13 @@ int nk_gather_rows(gpu_t *g, const float *src, uint32_t src_ld, const int *map, 
     if (!rows) return 0;
     NkGatherArgs a = { src, dst, map, rows, cols, src_ld, dst_ld };
     return gpu_launch(g, "gather_rows", &a, sizeof a, blocks_for((uint64_t)rows * cols), 1, 1, 256, 1, 1);
+}
+
+int nk_scatter_rows(gpu_t *g, const float *src, uint32_t src_ld, const int *map, float *dst, uint32_t dst_ld,
+                    uint32_t rows, uint32_t cols) {
+    if (!rows) return 0;
+    NkGatherArgs a = { src, dst, map, rows, cols, src_ld, dst_ld };
+    return gpu_launch(g, "scatter_rows", &a, sizeof a, blocks_for((uint64_t)rows * cols), 1, 1, 256, 1, 1);
 }
 
 int nk_lstm_input_rows(gpu_t *g, const uint16_t *embed, const int *tok, const float *xsrc, const float *hc,

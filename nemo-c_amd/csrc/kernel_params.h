@@ -148,6 +148,21 @@ typedef struct {
     NkDwArgs d;
 } NkGemvDwArgs;
 
+/* Batched log-mel front end: frame f reads span[tab[2f] .. + 512) (pre-emphasised samples, edge
+ * reflection already applied) and writes log-mel row tab[2f+1] of out ([*][128]).  Tables: window
+ * [512], filterbank [128][257] with each filter's nonzero bins [fb_lo, fb_hi), twiddles
+ * e^{-2 pi i k/512} for k < 256 (double), bit reversal [512]. */
+typedef struct {
+    const float *span;
+    const int *tab;
+    const float *win, *fb;
+    const int *fb_lo, *fb_hi;
+    const double *tw_re, *tw_im;
+    const unsigned short *rev;
+    float *out;
+    u32 F, pad;
+} NkMelArgs;
+
 /* Subsampling convs. X [T][F] (conv 0) or [T][F][C]; Y [T1][F1][C].  grid.x = T1 * ceil(F1 / fb):
  * a workgroup computes fb consecutive output columns of one output row, its threads the channels;
  * grid.y runs over a batch of windows of the same size, xs / ys floats apart. */

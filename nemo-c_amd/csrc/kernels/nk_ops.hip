@@ -68,6 +68,46 @@ extern "C" __global__ __launch_bounds__(256) void dwconv2d_s2(NkConvArgs a) {
     }
 }
 
+/* Log-mel of one 512-sample frame per workgroup (reference src/mel.c:115-173, the host front end's
+ * computation step for step): window, radix-2 decimation-in-time FFT in double (bit-reversed load,
+ * nine stages of 256 butterflies, one per thread, with the host's twiddle table and operation
+ * order), power in double rounded to float, each filter's sum over its bins in ascending order in
+ * float, log(x + 2^-24).  Floating-point contraction is off, so the spectrum equals the host's. */
+extern "C" __global__ __launch_bounds__(256) void mel_frames(const NkMelArgs a) {
+#pragma clang fp contract(off)
+    __shared__ double re[512], im[512];
+    __shared__ float pw[257];
+    const u32 f = blockIdx.x, t = threadIdx.x;
+    const float *fr = a.span + a.tab[2 * f];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const u32 k = t + 256 * h, j = a.rev[k];
+        re[j] = (double)(fr[k] * a.win[k]);
+        im[j] = 0.0;
+    }
+    __syncthreads();
+    for (u32 len = 2; len <= 512; len <<= 1) {
+        const u32 hl = len >> 1, stride = 512 / len, k = t % hl, ia = (t / hl) * len + k, ib = ia + hl;
+        const double wr = a.tw_re[k * stride], wi = a.tw_im[k * stride];
+        const double br = re[ib], bi = im[ib], ar = re[ia], ai = im[ia];
+        const double xr = br * wr - bi * wi, xi = br * wi + bi * wr;
+        re[ib] = ar - xr;
+        im[ib] = ai - xi;
+        re[ia] = ar + xr;
+        im[ia] = ai + xi;
+        __syncthreads();
+    }
+    pw[t] = (float)(re[t] * re[t] + im[t] * im[t]);
+    if (t == 0) pw[256] = (float)(re[256] * re[256] + im[256] * im[256]);
+    __syncthreads();
+    if (t < 128) {
+        float acc = 0.0f;
+        const float *w = a.fb + (u64)t * 257;
+        for (int k = a.fb_lo[t]; k < a.fb_hi[t]; ++k) acc += w[k] * pw[k];
+        a.out[(u64)(u32)a.tab[2 * f + 1] * 128 + t] = logf(acc + 5.9604644775390625e-08f);
+    }
+}
+
 /* [T][F][C] -> [T][C*F] channel-major flatten: reference src/kernels.metal:456-462.
  * One thread per output element (reads gather, writes are coalesced). */
 extern "C" __global__ __launch_bounds__(256) void flatten_cf(NkFlatArgs a) {
@@ -190,6 +230,14 @@ extern "C" __global__ __launch_bounds__(256) void gather_rows(const NkGatherArgs
     if (idx >= (u64)a.rows * a.cols) return;
     const u32 m = (u32)(idx / a.cols), k = (u32)(idx % a.cols);
     a.dst[(u64)m * a.dst_ld + k] = a.src[(u64)(u32)a.map[m] * a.src_ld + k];
+}
+
+/* dst row map[m] = src row m (rows of `cols` floats; the map's targets are distinct) */
+extern "C" __global__ __launch_bounds__(256) void scatter_rows(const NkGatherArgs a) {
+    const u64 idx = (u64)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= (u64)a.rows * a.cols) return;
+    const u32 m = (u32)(idx / a.cols), k = (u32)(idx % a.cols);
+    a.dst[(u64)(u32)a.map[m] * a.dst_ld + k] = a.src[(u64)m * a.src_ld + k];
 }
 
 /* LSTM input rows [x | h] of the batched decoder (one thread per element; grid.y = row) */

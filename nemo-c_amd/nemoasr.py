@@ -52,6 +52,7 @@ API = {
     "nemoasr_batch_stats": (None, [_vp, _vp]),
     "nemoasr_batch_step_ms": (C.POINTER(C.c_double), [_vp, C.POINTER(C.c_size_t)]),
     "nemoasr_batch_debug_use_graphs": (None, [_vp, C.c_int]),
+    "nemoasr_batch_debug_gpu_frontend": (C.c_int, [_vp, C.c_int]),
     "nemoasr_batch_debug_set_dump": (None, [_vp, C.c_int]),
     "nemoasr_batch_debug_device_decoder": (None, [_vp, C.c_int]),
     "nemoasr_batch_debug_joint_enc": (_f32p, [_vp, C.c_int, C.POINTER(C.c_size_t)]),
@@ -118,6 +119,8 @@ API = {
     "nk_dwconv_pw_desc": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, C.c_float, _vp, _u32, _vp, _u32, _u32, _u32, _u32,
                                     C.c_int, C.c_float]),
     "nk_fuse_shape": (C.c_int, [C.c_int, C.c_int]),
+    "nk_mel_frames": (C.c_int, [_vp, _vp, _vp, _u32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "nk_scatter_rows": (C.c_int, [_vp, _vp, _u32, _vp, _vp, _u32, _u32, _u32]),
     "nk_conv2d_c1_s2_relu": (C.c_int, [_vp, _vp, _vp, _vp, _vp] + [_u32] * 5),
     "nk_dwconv2d_s2": (C.c_int, [_vp, _vp, _vp, _vp, _vp] + [_u32] * 5),
     "nk_flatten_cf": (C.c_int, [_vp, _vp, _vp, _u32, _u32, _u32]),
@@ -421,6 +424,10 @@ class Batch:
 
     def use_graphs(self, on: bool):
         lib().nemoasr_batch_debug_use_graphs(self.h, int(on))
+
+    def gpu_frontend(self, on: bool):
+        if lib().nemoasr_batch_debug_gpu_frontend(self.h, int(on)):
+            raise RuntimeError("front end can only be chosen before any input")
 
     def set_dump(self, on: bool):
         lib().nemoasr_batch_debug_set_dump(self.h, int(on))

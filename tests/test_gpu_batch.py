@@ -119,14 +119,17 @@ def test_batch_matches_sessions_full():
     b.close()
 
 
-def test_batch_audio_and_reset():
-    """Audio pushed in 100 ms blocks, text per stream, and a slot reused after reset_stream."""
+@pytest.mark.parametrize("gpu_fe", [True, False])
+def test_batch_audio_and_reset(gpu_fe):
+    """Audio pushed in 100 ms blocks, text per stream, and a slot reused after reset_stream; log-mel
+    on the GPU (default) and on the host."""
     import nemoasr
 
     mdir = model_dir("tiny")
     om = oracle.Model(mdir, "en-US")
     audios = [synth.make_audio(t, seed=90 + i) for i, t in enumerate([1.8, 2.3, 1.1])]
     b = nemoasr.Batch(mdir, "en-US", 560, streams=3)
+    b.gpu_frontend(gpu_fe)
     for i in range(0, max(a.size for a in audios), 1600):
         for s, a in enumerate(audios):
             if i < a.size:
@@ -143,4 +146,58 @@ def test_batch_audio_and_reset():
     b.push(1, audios[1], final=True)
     b.run()
     assert b.tokens(1) == first
+    b.close()
+
+
+@pytest.mark.parametrize("latency", [80, 1120])
+def test_batch_gpu_frontend_matches_host(latency):
+    """The GPU log-mel front end against the host's, full model, audio fed in uneven pieces: the
+    same tokens and joint.enc rows within float rounding (the spectra are computed identically;
+    only the log may round differently), and the oracle's tokens."""
+    import nemoasr
+
+    mdir = model_dir("full")
+    om = oracle.Model(mdir, "en-US")
+    audios = [synth.make_audio(t, seed=200 + i) for i, t in enumerate([2.2, 1.6, 2.9, 0.7])]
+    out = []
+    for gpu_fe in (True, False):
+        b = nemoasr.Batch(mdir, "en-US", latency, streams=len(audios))
+        b.gpu_frontend(gpu_fe)
+        b.set_dump(True)
+        pieces = [2100, 900, 4700, 1600]
+        pos = [0] * len(audios)
+        while any(p < a.size for p, a in zip(pos, audios)):
+            for s, a in enumerate(audios):
+                if pos[s] < a.size:
+                    n = pieces[s % len(pieces)]
+                    b.push(s, a[pos[s]:pos[s] + n], final=pos[s] + n >= a.size)
+                    pos[s] += n
+            b.step()
+        b.run()
+        out.append([(b.tokens(s), b.joint_enc(s, om.dims.joint_hidden)) for s in range(len(audios))])
+        b.close()
+    for s, a in enumerate(audios):
+        (tg, jg), (th, jh) = out[0][s], out[1][s]
+        assert tg == th, s
+        assert rel_err(jg, jh) < 1e-4, s
+        toks, _ = oracle_run(om, latency, mel_ref.logmel(a))
+        assert tg == toks, s
+
+
+def test_batch_mixed_input_rejected():
+    """With the GPU front end a stream takes either audio or mel rows until it is reset."""
+    import nemoasr
+
+    mdir = model_dir("tiny")
+    b = nemoasr.Batch(mdir, "en-US", 560, streams=2)
+    b.push(0, np.zeros(1600, np.float32))
+    with pytest.raises(RuntimeError):
+        b.push_mel(0, np.zeros((8, 128), np.float32))
+    b.push_mel(1, np.zeros((8, 128), np.float32))
+    with pytest.raises(RuntimeError):
+        b.push(1, np.zeros(1600, np.float32))
+    with pytest.raises(RuntimeError):
+        b.gpu_frontend(False)
+    b.reset_stream(1)
+    b.push(1, np.zeros(1600, np.float32))
     b.close()

@@ -6,10 +6,13 @@ Tolerances: relative to the largest reference magnitude (tools/compare.py:30-32 
 sums in a different order than the oracle (and the MFMA kernels split activations into bf16
 hi + lo), so results agree to f32 rounding, not bit for bit.  Index outputs (argmax) are exact.
 """
+import ctypes as C
+
 import numpy as np
 import pytest
 
 import oracle
+import synth
 from conftest import rel_err
 
 pytestmark = pytest.mark.gpu
@@ -451,6 +454,65 @@ def test_dwconv_pw_fused(gpu, c, D, N, nc, acc):
     got = dC.read((c, N))
     np.testing.assert_array_equal(got, dC2.read((c, N)))
     assert rel_err(got, ref) < 1e-5
+
+
+class _MelTables(C.Structure):
+    _fields_ = [("win", C.POINTER(C.c_float)), ("fb", C.POINTER(C.c_float)), ("fb_lo", C.POINTER(C.c_int)),
+                ("fb_hi", C.POINTER(C.c_int)), ("tw_re", C.POINTER(C.c_double)), ("tw_im", C.POINTER(C.c_double)),
+                ("rev", C.POINTER(C.c_ushort))]
+
+
+@pytest.mark.parametrize("seconds,seed", [(0.5, 1), (1.37, 2), (0.02, 3)])
+def test_mel_frames(gpu, seconds, seed):
+    """GPU log-mel frames against the host front end's own computation on the same sample spans
+    (the first frames read reflected samples at the start, the last ones at the final end): the
+    spectra are computed identically in double; the device log and the host's libm log round
+    differently in about half the values, by at most two ulp."""
+    import nemoasr
+
+    L = nemoasr.lib()
+    f32p = C.POINTER(C.c_float)
+    L.melfe_create.restype = C.c_void_p
+    L.melfe_destroy.argtypes = [C.c_void_p]
+    L.melfe_append.restype = C.c_size_t
+    L.melfe_append.argtypes = [C.c_void_p, f32p, C.c_size_t, C.c_int]
+    L.melfe_span_len.restype = C.c_size_t
+    L.melfe_span_len.argtypes = [C.c_size_t]
+    L.melfe_take.restype = C.c_size_t
+    L.melfe_take.argtypes = [C.c_void_p, f32p, C.c_size_t]
+    L.melfe_compute.argtypes = [C.c_void_p, f32p, C.c_size_t, f32p]
+    L.melfe_tables.argtypes = [C.c_void_p, C.POINTER(_MelTables)]
+    x = (0.1 * synth.make_audio(seconds, seed=seed)).astype(np.float32)
+    m = L.melfe_create()
+    try:
+        cnt = L.melfe_append(m, x.ctypes.data_as(f32p), x.size, 1)
+        span = np.zeros(L.melfe_span_len(cnt), np.float32)
+        assert L.melfe_take(m, span.ctypes.data_as(f32p), cnt) == cnt
+        ref = np.zeros((cnt, 128), np.float32)
+        L.melfe_compute(m, span.ctypes.data_as(f32p), cnt, ref.ctypes.data_as(f32p))
+        t = _MelTables()
+        L.melfe_tables(m, C.byref(t))
+        win = np.ctypeslib.as_array(t.win, (512,)).copy()
+        fb = np.ctypeslib.as_array(t.fb, (128 * 257,)).copy()
+        lo = np.ctypeslib.as_array(t.fb_lo, (128,)).copy()
+        hi = np.ctypeslib.as_array(t.fb_hi, (128,)).copy()
+        twr = np.ctypeslib.as_array(t.tw_re, (256,)).copy()
+        twi = np.ctypeslib.as_array(t.tw_im, (256,)).copy()
+        rev = np.ctypeslib.as_array(t.rev, (512,)).copy()
+    finally:
+        L.melfe_destroy(m)
+    # frames written to shuffled output rows, to check the row table
+    perm = np.random.default_rng(seed).permutation(cnt).astype(np.int32)
+    tab = np.stack([np.arange(cnt, dtype=np.int32) * 160, perm], axis=1).astype(np.int32)
+    bufs = [gpu.put(a) for a in (span, tab, win, fb, lo, hi, twr, twi, rev)]
+    dout = gpu.alloc(cnt * 128 * 4)
+    gpu.begin()
+    gpu.check(L.nk_mel_frames(gpu.h, bufs[0].ptr, bufs[1].ptr, cnt, *[b.ptr for b in bufs[2:]], dout.ptr))
+    gpu.end()
+    got = dout.read((cnt, 128))[perm]
+    assert np.abs(got - ref).max() <= 4e-6, np.abs(got - ref).max()
+    ulps = np.abs(got - ref) / np.spacing(np.abs(ref))
+    assert ulps.max() <= 2, ulps.max()
 
 
 @pytest.mark.parametrize("nwin", [8, 24, 72, 128, 33])
