@@ -10,8 +10,9 @@ src/main.c:234-246); value = RTFx = audio seconds / wall seconds over the timed 
 A second leg runs the batched multi-stream path (include/nemoasr_batch.h): by default 64 streams
 at 560 ms (M = 448 encoder rows per step), each stream with its own seeded 20 s clip and a start
 offset of 0-7 chunks of pre-filled caches; it reports aggregate RTFx, p50 step latency (one chunk of
-every stream: front end + encoder + RNNT loop), the encoder's GEMM TFLOP/s per step and the MFMA
-roofline of the many-row GEMM kernels.
+every stream, from the step's start to its tokens: front end + encoder + RNNT loop), the step period
+(the RNNT loop of a step overlaps the next step's front end and encoder, so steps start faster than
+they finish), the encoder's GEMM TFLOP/s per step and the MFMA roofline of the many-row GEMM kernels.
 
 Also reported: p50 chunk latency (encoder step + its decoder round trips), the per-chunk HBM rate
 of the encoder (1,176,502,272 bytes of bf16 weights streamed per chunk / chunk GPU time), the
@@ -119,6 +120,7 @@ def batch_leg(a, nemoasr, synth, mdir, cfg):
         "streams": S, "latency_ms": lat, "rtfx": round(rtfx, 2), "audio_s_per_pass": S * nsamp / 16000.0,
         "wall_s_per_pass": round(wall / a.steps, 4),
         "p50_step_ms": round(float(np.median(sm)), 3), "p90_step_ms": round(float(np.percentile(sm, 90)), 3),
+        "step_period_ms": round(wall / steps * 1e3, 3),
         "steps_per_pass": int(tot["steps"] / a.steps), "rows_per_step": round(tot["rows"] / steps, 1),
         "frontend_ms_per_step": round(tot["frontend_ms"] / steps, 3),
         "encoder_ms_per_step": round(tot["encoder_ms"] / steps, 3),

@@ -138,7 +138,21 @@ struct nemoasr_batch {
     int nkeys;
     NkBDecStream *stage_bst;
     int *stage_bsetup, *stage_btok;
-    gpu_graph_t *dgraph;
+    gpu_graph_t *dgraph[2];        /* one per joint.enc buffer */
+    /* pipelined greedy loop: a worker thread runs each step's loop on its own GPU context (its own
+     * stream) while the caller's next step runs its front end and encoder; the step's joint.enc
+     * rows are copied to jdec[parity] for it.  The queue holds one step: the next hand-off waits
+     * for the previous loop, and every read of tokens or counters waits for the worker first. */
+    gpu_t *gd;
+    gpu_buf_t *jdec[2];
+    int jpar;
+    pthread_t dth;
+    pthread_mutex_t dmu;
+    pthread_cond_t dcv;
+    int dstarted, dquit, dstate, drc; /* dstate: 0 idle, 1 queued, 2 running */
+    char derr[256];
+    int dnact, *dorder, *dc, *drow0, dbuf;
+    double dt0;
     /* accounting */
     double *step_ms;
     size_t n_step, cap_step;
@@ -188,6 +202,8 @@ static void drop_graphs(nemoasr_batch_t *b) {
 }
 
 static void pool_start(pool_t *p, struct nemoasr_batch *b);
+static int dec_start(nemoasr_batch_t *b);
+static void dec_stop(nemoasr_batch_t *b);
 static void pool_stop(pool_t *p);
 
 /* bf16 matrices of the batched decoder: [Wx | Wh] per LSTM layer ([4P][2P]) and the joint output
@@ -509,6 +525,20 @@ nemoasr_batch_t *nemoasr_batch_open(const char *model_dir, const char *language,
             return NULL;
         }
     b->device_dec = device_dec_ok(b);
+    if (b->device_dec) {
+        /* the greedy loop's own GPU context and worker thread */
+        b->gd = gpu_create(err, errlen);
+        b->jdec[0] = gpu_buf_alloc(g, Mm * (size_t)b->J * fs);
+        b->jdec[1] = gpu_buf_alloc(g, Mm * (size_t)b->J * fs);
+        b->dorder = malloc(S * sizeof(int));
+        b->dc = malloc(S * sizeof(int));
+        b->drow0 = malloc(S * sizeof(int));
+        if (!b->gd || !b->jdec[0] || !b->jdec[1] || !b->dorder || !b->dc || !b->drow0 || dec_start(b)) {
+            if (!err[0]) snprintf(err, errlen, "batch: decoder context setup failed");
+            nemoasr_batch_close(b);
+            return NULL;
+        }
+    }
     if (mel_gpu_setup(b)) {
         snprintf(err, errlen, "batch: log-mel front end setup failed: %s", gpu_last_error(g));
         nemoasr_batch_close(b);
@@ -524,6 +554,7 @@ nemoasr_batch_t *nemoasr_batch_open(const char *model_dir, const char *language,
 
 void nemoasr_batch_close(nemoasr_batch_t *b) {
     if (!b) return;
+    dec_stop(b);
     pool_stop(&b->pool);
     free(b->fe_list);
     drop_graphs(b);
@@ -532,7 +563,7 @@ void nemoasr_batch_close(nemoasr_batch_t *b) {
                           b->wcat[1], b->wout, b->bout, b->hc, b->lin, b->gates, b->hout, b->hout2, b->pred,
                           b->jin, b->logits, b->amax, b->dtab, b->bst, b->bsetup, b->btok, b->lin1, b->tx,
                           b->wcati[0], b->wcati[1], b->bi[0], b->bi[1], b->keys, b->ring, b->meltab, b->span_dev,
-                          b->ftab_dev, b->wmap_dev, b->hrow_dev, b->hmap_dev };
+                          b->ftab_dev, b->wmap_dev, b->hrow_dev, b->hmap_dev, b->jdec[0], b->jdec[1] };
     for (size_t i = 0; i < sizeof bufs / sizeof *bufs; ++i) gpu_buf_free(bufs[i]);
     gpu_host_free(b->stage_win);
     gpu_host_free(b->stage_tab);
@@ -546,7 +577,10 @@ void nemoasr_batch_close(nemoasr_batch_t *b) {
     gpu_host_free(b->stage_bst);
     gpu_host_free(b->stage_bsetup);
     gpu_host_free(b->stage_btok);
-    gpu_graph_free(b->dgraph);
+    free(b->dorder);
+    free(b->dc);
+    free(b->drow0);
+    for (int i = 0; i < 2; ++i) gpu_graph_free(b->dgraph[i]);
     if (b->st)
         for (int s = 0; s < b->S; ++s) {
             melfe_destroy(b->st[s].mel);
@@ -571,6 +605,7 @@ void nemoasr_batch_close(nemoasr_batch_t *b) {
     free(b->ord);
     free(b->wtmp);
     free(b->step_ms);
+    gpu_destroy(b->gd);
     model_free(b->m);
     free(b);
 }
@@ -1070,6 +1105,9 @@ static int encoder_batch_step(nemoasr_batch_t *b, int *M_out, char *err, size_t 
         x->pos += x->c;
         x->cache_len = L < b->left ? L : b->left;
     }
+    /* the rows the greedy loop of this step reads (the loop of the previous step reads the other
+       buffer while the next encoder step runs) */
+    if (b->device_dec) nk_copy(g, gpu_buf_dptr(b->joint_enc), gpu_buf_dptr(b->jdec[b->jpar]), (uint32_t)(M * b->J));
     if (gpu_end(g, err, errlen)) return -1;
     b->stats.encoder_gpu_ms += gpu_last_ms(g);
     *M_out = M;
@@ -1196,7 +1234,7 @@ static NkBDecArgs bdec_args(nemoasr_batch_t *b) {
     a.nkeys = (uint32_t)b->nkeys;
     a.setup = gpu_buf_dptr(b->bsetup);
     a.tokens = gpu_buf_dptr(b->btok);
-    a.enc = gpu_buf_dptr(b->joint_enc);
+    a.enc = gpu_buf_dptr(b->jdec[b->dbuf]);
     a.tx = gpu_buf_dptr(b->tx);
     a.hc = gpu_buf_dptr(b->hc);
     a.A0 = gpu_buf_dptr(b->lin);
@@ -1233,11 +1271,11 @@ static int launch_bdec_gemm(nemoasr_batch_t *b, const char *kernel, const float 
     x.g.N = N;
     x.g.K = K;
     x.d = bdec_args(b);
-    return gpu_launch(b->g, kernel, &x, sizeof x, N / 16, ((uint32_t)b->S + 63) / 64, 1, 64 * waves, 1, 1);
+    return gpu_launch(b->gd, kernel, &x, sizeof x, N / 16, ((uint32_t)b->S + 63) / 64, 1, 64 * waves, 1, 1);
 }
 
 static void launch_bdec_steps(nemoasr_batch_t *b, int steps) {
-    gpu_t *g = b->g;
+    gpu_t *g = b->gd;
     const NkBDecArgs a = bdec_args(b);
     const uint32_t S = a.S, P = a.P, J = a.J, Vp = (uint32_t)b->Vp, R = a.S * a.W;
     for (int k = 0; k < steps; ++k) {
@@ -1255,17 +1293,16 @@ static void launch_bdec_steps(nemoasr_batch_t *b, int steps) {
 
 /* the chunks of order[0..nact) through the device loop: one setup launch, then graph runs of
  * BDEC_STEPS steps until every chunk is done */
-static int decoder_batch_device(nemoasr_batch_t *b, int nact, char *err, size_t errlen) {
-    gpu_t *g = b->g;
-    const int S = b->S;
+static int decoder_batch_device(nemoasr_batch_t *b, char *err, size_t errlen) {
+    gpu_t *g = b->gd;
+    const int S = b->S, nact = b->dnact;
     int *su = b->stage_bsetup;
     memset(su, 0, (size_t)2 * S * sizeof(int));
     int maxc = 0;
     for (int i = 0; i < nact; ++i) {
-        const bstream_t *x = &b->st[b->order[i]];
-        su[2 * b->order[i]] = x->c;
-        su[2 * b->order[i] + 1] = x->row0;
-        if (x->c > maxc) maxc = x->c;
+        su[2 * b->dorder[i]] = b->dc[i];
+        su[2 * b->dorder[i] + 1] = b->drow0[i];
+        if (b->dc[i] > maxc) maxc = b->dc[i];
     }
     if (maxc > b->W) { snprintf(err, errlen, "decoder: chunk of %d frames exceeds %d", maxc, b->W); return -1; }
     const NkBDecArgs a = bdec_args(b);
@@ -1277,11 +1314,11 @@ static int decoder_batch_device(nemoasr_batch_t *b, int nact, char *err, size_t 
             gpu_upload_async(g, gpu_buf_dptr(b->bsetup), su, (size_t)2 * S * sizeof(int));
             gpu_launch(g, "bdec_setup", &a, sizeof a, (uint32_t)S, 1, 1, 64, 1, 1);
         }
-        if (b->use_graphs && !b->dgraph && !gpu_capture_begin(g)) {
+        if (b->use_graphs && !b->dgraph[b->dbuf] && !gpu_capture_begin(g)) {
             launch_bdec_steps(b, BDEC_STEPS);
-            b->dgraph = gpu_capture_end(g);
+            b->dgraph[b->dbuf] = gpu_capture_end(g);
         }
-        if (b->dgraph) gpu_graph_launch(g, b->dgraph);
+        if (b->dgraph[b->dbuf]) gpu_graph_launch(g, b->dgraph[b->dbuf]);
         else launch_bdec_steps(b, BDEC_STEPS);
         gpu_download_async(g, b->stage_bst, gpu_buf_dptr(b->bst), (size_t)S * sizeof(NkBDecStream));
         gpu_download_async(g, b->stage_btok, gpu_buf_dptr(b->btok), (size_t)S * b->tok_ld * sizeof(int));
@@ -1289,19 +1326,91 @@ static int decoder_batch_device(nemoasr_batch_t *b, int nact, char *err, size_t 
         b->stats.joint_steps += BDEC_STEPS;
         int done = 1;
         for (int i = 0; i < nact && done; ++i) {
-            const NkBDecStream *x = &b->stage_bst[b->order[i]];
+            const NkBDecStream *x = &b->stage_bst[b->dorder[i]];
             done = x->t >= x->frames;
         }
         if (done) break;
     }
     for (int i = 0; i < nact; ++i) {
-        const int s = b->order[i];
+        const int s = b->dorder[i];
         const int n = b->stage_bst[s].n_out;
         if (n > b->tok_ld) { snprintf(err, errlen, "decoder: stream %d emitted %d tokens in a chunk", s, n); return -1; }
         for (int k = 0; k < n; ++k) keep_token(&b->st[s], b->stage_btok[(size_t)s * b->tok_ld + k]);
         b->stats.tokens += (size_t)n;
     }
     return 0;
+}
+
+static void record_step(nemoasr_batch_t *b, double ms) {
+    if (b->n_step == b->cap_step) {
+        b->cap_step = b->cap_step ? 2 * b->cap_step : 256;
+        b->step_ms = realloc(b->step_ms, b->cap_step * sizeof(double));
+    }
+    b->step_ms[b->n_step++] = ms;
+}
+
+static void *dec_main(void *arg) {
+    nemoasr_batch_t *b = arg;
+    pthread_mutex_lock(&b->dmu);
+    for (;;) {
+        while (!b->dquit && b->dstate != 1) pthread_cond_wait(&b->dcv, &b->dmu);
+        if (b->dquit) break;
+        b->dstate = 2;
+        pthread_mutex_unlock(&b->dmu);
+        char err[256] = "";
+        const double t1 = now_ms();
+        const int rc = decoder_batch_device(b, err, sizeof err);
+        const double t2 = now_ms();
+        b->stats.decoder_ms += t2 - t1;
+        record_step(b, t2 - b->dt0);
+        pthread_mutex_lock(&b->dmu);
+        if (rc && !b->drc) {
+            b->drc = -1;
+            snprintf(b->derr, sizeof b->derr, "%s", err);
+        }
+        b->dstate = 0;
+        pthread_cond_broadcast(&b->dcv);
+    }
+    pthread_mutex_unlock(&b->dmu);
+    return NULL;
+}
+
+/* wait until the worker is idle; report an error of the loop it ran */
+static int dec_drain(const nemoasr_batch_t *cb, char *err, size_t errlen) {
+    nemoasr_batch_t *b = (nemoasr_batch_t *)cb;
+    if (!b->dstarted) return 0;
+    pthread_mutex_lock(&b->dmu);
+    while (b->dstate) pthread_cond_wait(&b->dcv, &b->dmu);
+    const int rc = b->drc;
+    if (rc && errlen) snprintf(err, errlen, "%s", b->derr);
+    b->drc = 0;
+    pthread_mutex_unlock(&b->dmu);
+    return rc;
+}
+
+static int dec_start(nemoasr_batch_t *b) {
+    pthread_mutex_init(&b->dmu, NULL);
+    pthread_cond_init(&b->dcv, NULL);
+    if (pthread_create(&b->dth, NULL, dec_main, b)) {
+        pthread_mutex_destroy(&b->dmu);
+        pthread_cond_destroy(&b->dcv);
+        return -1;
+    }
+    b->dstarted = 1;
+    return 0;
+}
+
+static void dec_stop(nemoasr_batch_t *b) {
+    if (!b->dstarted) return;
+    pthread_mutex_lock(&b->dmu);
+    while (b->dstate) pthread_cond_wait(&b->dcv, &b->dmu);
+    b->dquit = 1;
+    pthread_cond_broadcast(&b->dcv);
+    pthread_mutex_unlock(&b->dmu);
+    pthread_join(b->dth, NULL);
+    pthread_mutex_destroy(&b->dmu);
+    pthread_cond_destroy(&b->dcv);
+    b->dstarted = 0;
 }
 
 int nemoasr_batch_step(nemoasr_batch_t *b, char *err, size_t errlen) {
@@ -1346,18 +1455,34 @@ int nemoasr_batch_step(nemoasr_batch_t *b, char *err, size_t errlen) {
         }
         free(all);
     }
-    if (b->device_dec ? decoder_batch_device(b, nact, err, errlen) : decoder_batch_run(b, nact, err, errlen)) return -1;
-    const double t2 = now_ms();
     b->stats.steps++;
     b->stats.chunks += (size_t)nact;
     b->stats.rows += (size_t)M;
     b->stats.encoder_ms += t1 - t0;
-    b->stats.decoder_ms += t2 - t1;
-    if (b->n_step == b->cap_step) {
-        b->cap_step = b->cap_step ? 2 * b->cap_step : 256;
-        b->step_ms = realloc(b->step_ms, b->cap_step * sizeof(double));
+    if (b->device_dec) {
+        /* hand the step's greedy loop to the worker once it has finished the previous one; this
+           step's joint.enc rows are already in jdec[jpar] (copied by the encoder step) */
+        if (dec_drain(b, err, errlen)) return -1;
+        for (int i = 0; i < nact; ++i) {
+            const bstream_t *x = &b->st[b->order[i]];
+            b->dorder[i] = b->order[i];
+            b->dc[i] = x->c;
+            b->drow0[i] = x->row0;
+        }
+        b->dnact = nact;
+        b->dbuf = b->jpar;
+        b->dt0 = t0;
+        b->jpar ^= 1;
+        pthread_mutex_lock(&b->dmu);
+        b->dstate = 1;
+        pthread_cond_broadcast(&b->dcv);
+        pthread_mutex_unlock(&b->dmu);
+        return consumed;
     }
-    b->step_ms[b->n_step++] = t2 - t0;
+    if (decoder_batch_run(b, nact, err, errlen)) return -1;
+    const double t2 = now_ms();
+    b->stats.decoder_ms += t2 - t1;
+    record_step(b, t2 - t0);
     return consumed;
 }
 
@@ -1366,12 +1491,13 @@ int nemoasr_batch_run(nemoasr_batch_t *b, char *err, size_t errlen) {
     for (;;) {
         const int rc = nemoasr_batch_step(b, err, errlen);
         if (rc < 0) return -1;
-        if (rc == 0) return steps;
+        if (rc == 0) return dec_drain(b, err, errlen) ? -1 : steps;
         steps++;
     }
 }
 
 const int *nemoasr_batch_tokens(const nemoasr_batch_t *b, int stream, size_t *n) {
+    dec_drain(b, NULL, 0);
     if (stream < 0 || stream >= b->S) { *n = 0; return NULL; }
     *n = b->st[stream].n_tok;
     return b->st[stream].tok;
@@ -1379,6 +1505,7 @@ const int *nemoasr_batch_tokens(const nemoasr_batch_t *b, int stream, size_t *n)
 
 /* token pieces as text, leading spaces of the first printed piece dropped (src/nemoasr.c:123-129) */
 char *nemoasr_batch_text(nemoasr_batch_t *b, int stream) {
+    dec_drain(b, NULL, 0);
     if (stream < 0 || stream >= b->S) return NULL;
     bstream_t *x = &b->st[stream];
     char *out = NULL;
@@ -1405,26 +1532,34 @@ char *nemoasr_batch_text(nemoasr_batch_t *b, int stream) {
 int nemoasr_batch_reset_stream(nemoasr_batch_t *b, int stream, char *err, size_t errlen) {
     if (errlen) err[0] = 0;
     if (check_stream(b, stream, err, errlen)) return -1;
+    if (dec_drain(b, err, errlen)) return -1;
     stream_clear(b, stream);
     b->st[stream].n_tok = 0;
     if (stream_zero_device(b, stream)) { snprintf(err, errlen, "batch: reset upload failed"); return -1; }
     return 0;
 }
 
-void nemoasr_batch_stats(const nemoasr_batch_t *b, nemoasr_batch_stats_t *out) { *out = b->stats; }
+void nemoasr_batch_stats(const nemoasr_batch_t *b, nemoasr_batch_stats_t *out) {
+    dec_drain(b, NULL, 0);
+    *out = b->stats;
+}
 
 const double *nemoasr_batch_step_ms(const nemoasr_batch_t *b, size_t *n) {
+    dec_drain(b, NULL, 0);
     *n = b->n_step;
     return b->step_ms;
 }
 
 /* ---- test hooks ---------------------------------------------------------------------------- */
 void nemoasr_batch_debug_use_graphs(nemoasr_batch_t *b, int on) {
+    dec_drain(b, NULL, 0);
     b->use_graphs = on;
     if (!on) {
         drop_graphs(b);
-        gpu_graph_free(b->dgraph);
-        b->dgraph = NULL;
+        for (int i = 0; i < 2; ++i) {
+            gpu_graph_free(b->dgraph[i]);
+            b->dgraph[i] = NULL;
+        }
     }
 }
 
@@ -1438,7 +1573,8 @@ int nemoasr_batch_debug_gpu_frontend(nemoasr_batch_t *b, int on) {
 }
 
 void nemoasr_batch_debug_device_decoder(nemoasr_batch_t *b, int on) {
-    b->device_dec = on && device_dec_ok(b);
+    dec_drain(b, NULL, 0);
+    b->device_dec = on && b->gd && device_dec_ok(b);
 }
 
 void nemoasr_batch_debug_set_dump(nemoasr_batch_t *b, int on) {
