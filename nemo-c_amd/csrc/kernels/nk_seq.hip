@@ -199,17 +199,23 @@ extern "C" __global__ __launch_bounds__(512) void attention_rel(const NkAttnArgs
 }
 
 /* Relative-position attention of whole chunks (batched streams), the math of attention_rel above
- * (reference src/kernels.metal:290-348).  One workgroup per (head, chunk): the chunk's L = cached
- * + c keys and values and its L + c - 1 position rows are brought into LDS by direct global -> LDS
- * loads (16 bytes per lane, granule g of row r stored at slot g ^ (r % 16), so the row-parallel
- * 16-byte reads below, 16 lanes per cycle, are conflict-free), then every query row of the chunk is scored against
- * them: wavefront w takes rows w, w+4, ...; lane l takes keys l and l+64; softmax by wavefront
- * reductions; output lane l accumulates dims 2l, 2l+1 over the keys in order. */
+ * (reference src/kernels.metal:290-348), on fp32 matrix cores (v_mfma_f32_16x16x4f32: fp32
+ * products and sums, so results equal the vector-unit ones up to summation order).  One workgroup
+ * per (head, chunk); the chunk's c <= 16 query rows are one 16-row tile:
+ *   S1 = (Q + u) K^T   [16][80]  five 16-column tiles over the L <= 80 keys
+ *   S2 = (Q + v) P^T   [16][96]  six tiles over the chunk's L + c - 1 position rows
+ *   score(i, j) = (S1[i][j] + S2[i][c - 1 - i + j]) * scale,  softmax over j < L
+ *   O = softmax . V    [16][128] eight tiles
+ * The eleven score tiles are spread over the four wavefronts; a lane reads its K or P row (32
+ * consecutive dims of the row) straight from global memory and holds its query row's matching 32
+ * dims of q + u and q + v in registers (step s of the K loop is dim 32 (lane / 16) + s on both
+ * operands).  V goes to LDS by direct loads (granule g of row r at slot g ^ (r % 16), so the
+ * column reads of the P.V product are conflict-free); scores and probabilities go through LDS. */
+#define ATC_SLD 97 /* score row stride in floats: 96 position columns + 1 */
 extern "C" __global__ __launch_bounds__(256) void attention_rel_chunks(const NkAttnChunkArgs a) {
-    __shared__ floatx4 Ks[NK_ATTC_MAX_L * 32], Vs[NK_ATTC_MAX_L * 32];
-    __shared__ floatx4 Ps[(NK_ATTC_MAX_L + NK_ATTC_MAX_C) * 32];
-    __shared__ floatx4 qu[NK_ATTC_MAX_C * 32], qv[NK_ATTC_MAX_C * 32];
-    __shared__ float sc[NK_ATTC_MAX_C][NK_ATTC_MAX_L];
+    __shared__ floatx4 Vs[NK_ATTC_MAX_L * 32];
+    __shared__ float S1[16 * ATC_SLD], S2[16 * ATC_SLD];
+    static_assert(NK_ATTC_MAX_L == 80 && NK_ATTC_MAX_C <= 16, "tile counts assume 80 keys, 16 query rows");
     const u32 h = blockIdx.x, ch = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int *cd = a.chunks + 4 * ch;
     const u32 qrow0 = (u32)cd[0], m0 = (u32)cd[1], c = (u32)cd[2], cl = (u32)cd[3];
@@ -219,67 +225,92 @@ extern "C" __global__ __launch_bounds__(256) void attention_rel_chunks(const NkA
     const float *Kg = a.kv + a.D + (u64)(qrow0 - cl) * a.ld + off;
     const float *Vg = a.kv + 2 * a.D + (u64)(qrow0 - cl) * a.ld + off;
     const float *Pg = a.P + (u64)(a.Lmax - L) * a.D + off;
-    /* LDS granule p = 32 r + s of a table holds granule s ^ (r % 8) of row r; one DMA instruction
-     * fills 64 granules (two rows); rows past the end re-read the last row (never used) */
-    for (u32 blk = wave; blk < (L + 1) / 2; blk += 4) {
+    /* V rows 0 .. 79 into LDS, two rows per direct-load instruction (rows past L re-read row L - 1:
+     * finite values, weighted by zero probabilities) */
+    for (u32 blk = wave; blk < NK_ATTC_MAX_L / 2; blk += 4) {
         const u32 p = blk * 64 + lane, r = p >> 5, g = (p & 31) ^ (r & 15), rr = min(r, L - 1);
-        dma16(Kg + (u64)rr * a.ld + 4 * g, (lds_char_t *)&Ks[blk * 64]);
         dma16(Vg + (u64)rr * a.ld + 4 * g, (lds_char_t *)&Vs[blk * 64]);
     }
-    for (u32 blk = wave; blk < (NP + 1) / 2; blk += 4) {
-        const u32 p = blk * 64 + lane, r = p >> 5, g = (p & 31) ^ (r & 15), rr = min(r, NP - 1);
-        dma16(Pg + (u64)rr * a.D + 4 * g, (lds_char_t *)&Ps[blk * 64]);
+    /* query row qi = lane % 16 (zero past c), dims 32 kq .. 32 kq + 31 */
+    const u32 qi = lane & 15, kq = lane >> 4;
+    float qu[32], qv[32];
+    {
+        const bool ok = qi < c;
+        const floatx4 *qp = (const floatx4 *)(a.kv + (u64)(qrow0 + min(qi, c - 1)) * a.ld + off + 32 * kq);
+        const floatx4 *up = (const floatx4 *)(a.bu + off + 32 * kq), *vp = (const floatx4 *)(a.bv + off + 32 * kq);
+#pragma unroll
+        for (int v4 = 0; v4 < 8; ++v4) {
+            const floatx4 q = qp[v4], u = up[v4], w = vp[v4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                qu[4 * v4 + e] = ok ? q[e] + u[e] : 0.0f;
+                qv[4 * v4 + e] = ok ? q[e] + w[e] : 0.0f;
+            }
+        }
     }
-    for (u32 idx = tid; idx < c * 32; idx += 256) {
-        const u32 i = idx >> 5, g = idx & 31;
-        const floatx4 q = *(const floatx4 *)(a.kv + (u64)(qrow0 + i) * a.ld + off + 4 * g);
-        qu[idx] = q + *(const floatx4 *)(a.bu + off + 4 * g);
-        qv[idx] = q + *(const floatx4 *)(a.bv + off + 4 * g);
+    /* score tiles: T < 5 content (K rows 16 T ..), T >= 5 position (P rows 16 (T - 5) ..) */
+    for (u32 T = wave; T < 11; T += 4) {
+        const bool pos = T >= 5;
+        const u32 col0 = (pos ? T - 5 : T) * 16, row = col0 + qi;
+        const floatx4 *src = (const floatx4 *)((pos ? Pg + (u64)min(row, NP - 1) * a.D : Kg + (u64)min(row, L - 1) * a.ld) +
+                                               32 * kq);
+        float b[32];
+#pragma unroll
+        for (int v4 = 0; v4 < 8; ++v4) {
+            const floatx4 x = src[v4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) b[4 * v4 + e] = x[e];
+        }
+        floatx4 acc = { 0.f, 0.f, 0.f, 0.f };
+        if (pos) {
+#pragma unroll
+            for (int k = 0; k < 32; ++k) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(qv[k], b[k], acc, 0, 0, 0);
+        } else {
+#pragma unroll
+            for (int k = 0; k < 32; ++k) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(qu[k], b[k], acc, 0, 0, 0);
+        }
+        float *S = pos ? S2 : S1;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) S[(4 * kq + r) * ATC_SLD + col0 + qi] = acc[r];
     }
     wait_vm_lgkm<0>();
     barrier_mem();
-    const u32 j0 = lane, j1 = lane + 64;
-    for (u32 i = wave; i < c; i += 4) {
-        /* position row of (i, j): (Lmax - L) + (c - 1 - i + j), i.e. row c - 1 - i + j of Ps */
-        const u32 p0 = c - 1 - i + j0, p1 = c - 1 - i + j1;
-        float s0 = 0.0f, s1 = 0.0f;
-        if (j0 < L) {
-#pragma unroll 8
-            for (u32 g = 0; g < 32; ++g) {
-                const floatx4 u = qu[i * 32 + g], w = qv[i * 32 + g];
-                const floatx4 k = Ks[j0 * 32 + (g ^ (j0 & 15))], pp = Ps[p0 * 32 + (g ^ (p0 & 15))];
-                s0 += u[0] * k[0] + u[1] * k[1] + u[2] * k[2] + u[3] * k[3];
-                s0 += w[0] * pp[0] + w[1] * pp[1] + w[2] * pp[2] + w[3] * pp[3];
-            }
+    /* scores and softmax: wavefront w takes rows w, w + 4, ...; lane takes keys lane, lane + 64;
+     * the probabilities replace S1 (zero for rows past c and keys past L) */
+    for (u32 i = wave; i < 16; i += 4) {
+        const u32 j0 = lane, j1 = lane + 64;
+        if (i < c) {
+            const bool v0 = j0 < L, v1 = j1 < L;
+            const float s0 = v0 ? (S1[i * ATC_SLD + j0] + S2[i * ATC_SLD + (c - 1 - i + j0)]) * a.scale : -INFINITY;
+            const float s1 = v1 ? (S1[i * ATC_SLD + j1] + S2[i * ATC_SLD + (v1 ? c - 1 - i + j1 : 0)]) * a.scale : -INFINITY;
+            const float mx = wave_max(fmaxf(s0, s1));
+            const float e0 = v0 ? expf(s0 - mx) : 0.0f, e1 = v1 ? expf(s1 - mx) : 0.0f;
+            const float sum = wave_sum(e0 + e1);
+            S1[i * ATC_SLD + j0] = e0 / sum;
+            if (j1 < NK_ATTC_MAX_L) S1[i * ATC_SLD + j1] = e1 / sum;
+        } else {
+            S1[i * ATC_SLD + j0] = 0.0f;
+            if (j1 < NK_ATTC_MAX_L) S1[i * ATC_SLD + j1] = 0.0f;
         }
-        if (j1 < L) {
-#pragma unroll 8
-            for (u32 g = 0; g < 32; ++g) {
-                const floatx4 u = qu[i * 32 + g], w = qv[i * 32 + g];
-                const floatx4 k = Ks[j1 * 32 + (g ^ (j1 & 15))], pp = Ps[p1 * 32 + (g ^ (p1 & 15))];
-                s1 += u[0] * k[0] + u[1] * k[1] + u[2] * k[2] + u[3] * k[3];
-                s1 += w[0] * pp[0] + w[1] * pp[1] + w[2] * pp[2] + w[3] * pp[3];
-            }
-        }
-        s0 = j0 < L ? s0 * a.scale : -INFINITY;
-        s1 = j1 < L ? s1 * a.scale : -INFINITY;
-        const float mx = wave_max(fmaxf(s0, s1));
-        const float e0 = j0 < L ? expf(s0 - mx) : 0.0f, e1 = j1 < L ? expf(s1 - mx) : 0.0f;
-        const float sum = wave_sum(e0 + e1);
-        if (j0 < L) sc[i][j0] = e0 / sum;
-        if (j1 < L) sc[i][j1] = e1 / sum;
     }
     lds_barrier();
-    const u32 gq = lane >> 1, hf = (lane & 1) * 2;
-    for (u32 i = wave; i < c; i += 4) {
-        float o0 = 0.0f, o1 = 0.0f;
-        for (u32 j = 0; j < L; ++j) {
-            const float pj = sc[i][j];
-            const floatx4 v = Vs[j * 32 + (gq ^ (j & 15))];
-            o0 += pj * v[hf];
-            o1 += pj * v[hf + 1];
+    /* O = P V: wavefront w takes output column tiles w and w + 4; step s of the K loop is key
+     * 20 (lane / 16) + s on both operands */
+    for (u32 dt = wave; dt < 8; dt += 4) {
+        const u32 d = dt * 16 + qi, gq = d >> 2, e = d & 3;
+        floatx4 acc = { 0.f, 0.f, 0.f, 0.f };
+#pragma unroll
+        for (u32 k = 0; k < NK_ATTC_MAX_L / 4; ++k) {
+            const u32 j = (NK_ATTC_MAX_L / 4) * kq + k;
+            const float pa = S1[qi * ATC_SLD + j];
+            const float vb = ((const float *)&Vs[j * 32 + (gq ^ (j & 15))])[e];
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(pa, vb, acc, 0, 0, 0);
         }
-        *(floatx2 *)(a.O + (u64)(m0 + i) * a.D + off + 2 * lane) = (floatx2){ o0, o1 };
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const u32 i = 4 * kq + r;
+            if (i < c) a.O[(u64)(m0 + i) * a.D + off + d] = acc[r];
+        }
     }
 }
 
