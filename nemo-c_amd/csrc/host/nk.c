@@ -287,6 +287,8 @@ int nk_layernorm2(gpu_t *g, const float *X, const float *g1, const float *b1, co
     if (!M) return 0;
     if (D > NK_ROW_MAX || D % 4) return bad(g, "layernorm: D must be a multiple of 4, at most 4096");
     NkLnArgs a = { X, g1, b1, g2, b2, Y1, Y2, M, D, eps, 0 };
+    /* many rows: one wavefront per row (D <= 1024), no barriers */
+    if (M > 16 && D <= 1024) return gpu_launch(g, "layernorm_rows", &a, sizeof a, (M + 3) / 4, 1, 1, 256, 1, 1);
     return gpu_launch(g, "layernorm", &a, sizeof a, M, 1, 1, NK_LN_THREADS, 1, 1);
 }
 

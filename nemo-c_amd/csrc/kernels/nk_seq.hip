@@ -75,6 +75,61 @@ extern "C" __global__ __launch_bounds__(256) void layernorm(const NkLnArgs a) {
         if (tid + k * 256 < D4) y2[tid + k * 256] = v[k];
 }
 
+/* One row per wavefront (D <= 1024: lane l holds float4s l, l+64, l+128, l+192), four rows per
+ * workgroup: the same LayerNorm (two-pass mean and variance) with wavefront reductions and no
+ * barriers, for the batched path's many rows.  Y2 as in layernorm. */
+__device__ __forceinline__ void ln_row64(float4 (&v)[4], const float4 (&g)[4], const float4 (&b)[4], u32 lane, u32 D4,
+                                         u32 D, float eps) {
+    float s = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) s += ((v[k].x + v[k].y) + v[k].z) + v[k].w;
+    const float mean = wsum(s) / (float)D;
+    float q = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+        if (lane + 64 * k < D4) {
+            const float dx = v[k].x - mean, dy = v[k].y - mean, dz = v[k].z - mean, dw = v[k].w - mean;
+            q += ((dx * dx + dy * dy) + dz * dz) + dw * dw;
+        }
+    const float inv = 1.0f / sqrtf(wsum(q) / (float)D + eps);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        v[k].x = (v[k].x - mean) * inv * g[k].x + b[k].x;
+        v[k].y = (v[k].y - mean) * inv * g[k].y + b[k].y;
+        v[k].z = (v[k].z - mean) * inv * g[k].z + b[k].z;
+        v[k].w = (v[k].w - mean) * inv * g[k].w + b[k].w;
+    }
+}
+
+extern "C" __global__ __launch_bounds__(256) void layernorm_rows(const NkLnArgs a) {
+    const u32 lane = threadIdx.x & 63, row = blockIdx.x * 4 + (threadIdx.x >> 6), D4 = a.D >> 2;
+    if (row >= a.M) return; /* uniform per wavefront; no barriers */
+    const float4 *x = (const float4 *)(a.X + (u64)row * a.D);
+    float4 v[4], g1[4], b1[4], g2[4], b2[4];
+    const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const u32 i = lane + 64 * k;
+        const bool ok = i < D4;
+        v[k] = ok ? x[i] : z;
+        g1[k] = ok ? ((const float4 *)a.g1)[i] : z;
+        b1[k] = ok ? ((const float4 *)a.b1)[i] : z;
+        g2[k] = ok && a.Y2 ? ((const float4 *)a.g2)[i] : z;
+        b2[k] = ok && a.Y2 ? ((const float4 *)a.b2)[i] : z;
+    }
+    ln_row64(v, g1, b1, lane, D4, a.D, a.eps);
+    float4 *y1 = (float4 *)(a.Y1 + (u64)row * a.D);
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+        if (lane + 64 * k < D4) y1[lane + 64 * k] = v[k];
+    if (!a.Y2) return;
+    ln_row64(v, g2, b2, lane, D4, a.D, a.eps);
+    float4 *y2 = (float4 *)(a.Y2 + (u64)row * a.D);
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+        if (lane + 64 * k < D4) y2[lane + 64 * k] = v[k];
+}
+
 /* Relative-position attention of one (head h, query row orow) on a workgroup of 512 threads:
  * reference src/kernels.metal:290-348.
  *   score_j = ((q + u) . K_j + (q + v) . P[(Lmax - L) + (c - 1 - i + j)]) * scale
