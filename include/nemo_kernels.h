@@ -78,6 +78,11 @@ int nk_gemm_ln(gpu_t *g, const float *A, uint32_t lda, const uint16_t *W, uint32
  * key wins, and its low 32 bits hold 0xffffffff - column).  N % 64 == 0. */
 int nk_gemm_argmax(gpu_t *g, const float *A, uint32_t lda, const uint16_t *W, uint32_t ldw, const float *bias,
                    unsigned long long *keys, uint32_t keys_ld, uint32_t M, uint32_t N, uint32_t K, uint32_t V);
+/* Same, computing only the first min(M, *mrows * mrows_mul) rows, a count read on the device (the
+ * launch covers M rows; mrows NULL: all M). */
+int nk_gemm_argmax_rows(gpu_t *g, const float *A, uint32_t lda, const uint16_t *W, uint32_t ldw, const float *bias,
+                        unsigned long long *keys, uint32_t keys_ld, uint32_t M, uint32_t N, uint32_t K, uint32_t V,
+                        const int *mrows, uint32_t mrows_mul);
 /* 1: many-row MFMA kernels take 64-wide K stages where K allows; 0 (default): 32-wide.  Returns
  * the previous setting. */
 int nk_gemm_mx_k64(int on);

@@ -134,7 +134,7 @@ struct nemoasr_batch {
     int *stage_dtab, *stage_amax;
     /* device-resident loop (kernels/nk_bdec.hip) */
     int device_dec, W, tok_ld;
-    gpu_buf_t *bst, *bsetup, *btok, *lin1, *tx, *wcati[2], *bi[2], *keys;
+    gpu_buf_t *bst, *bsetup, *btok, *lin1, *tx, *wcati[2], *bi[2], *keys, *brows, *bcnt;
     int nkeys;
     NkBDecStream *stage_bst;
     int *stage_bsetup, *stage_btok;
@@ -493,10 +493,12 @@ nemoasr_batch_t *nemoasr_batch_open(const char *model_dir, const char *language,
     b->nkeys = 2 * (b->Vp / 64);
     b->keys = gpu_buf_alloc(g, S * (size_t)b->W * b->nkeys * sizeof(unsigned long long));
     b->bsetup = gpu_buf_alloc(g, 2 * S * sizeof(int));
+    b->brows = gpu_buf_alloc(g, S * sizeof(NkBDecRow));
+    b->bcnt = gpu_buf_alloc(g, 2 * sizeof(int));
     b->btok = gpu_buf_alloc(g, S * (size_t)b->tok_ld * sizeof(int));
     b->lin1 = gpu_buf_alloc(g, S * 2 * P * fs);
     b->stage_bst = gpu_host_alloc(g, S * sizeof(NkBDecStream));
-    b->stage_bsetup = gpu_host_alloc(g, 2 * S * sizeof(int));
+    b->stage_bsetup = gpu_host_alloc(g, (2 * S + 2) * sizeof(int));
     b->stage_btok = gpu_host_alloc(g, S * (size_t)b->tok_ld * sizeof(int));
     if (!b->win || !b->kv || !b->din || !b->ff || !b->stage_win || !b->stage_dtab || !b->btok || !b->stage_btok) {
         snprintf(err, errlen, "batch: out of memory for %d streams", n_streams);
@@ -563,7 +565,8 @@ void nemoasr_batch_close(nemoasr_batch_t *b) {
                           b->wcat[1], b->wout, b->bout, b->hc, b->lin, b->gates, b->hout, b->hout2, b->pred,
                           b->jin, b->logits, b->amax, b->dtab, b->bst, b->bsetup, b->btok, b->lin1, b->tx,
                           b->wcati[0], b->wcati[1], b->bi[0], b->bi[1], b->keys, b->ring, b->meltab, b->span_dev,
-                          b->ftab_dev, b->wmap_dev, b->hrow_dev, b->hmap_dev, b->jdec[0], b->jdec[1] };
+                          b->ftab_dev, b->wmap_dev, b->hrow_dev, b->hmap_dev, b->jdec[0], b->jdec[1], b->brows,
+                          b->bcnt };
     for (size_t i = 0; i < sizeof bufs / sizeof *bufs; ++i) gpu_buf_free(bufs[i]);
     gpu_host_free(b->stage_win);
     gpu_host_free(b->stage_tab);
@@ -1223,7 +1226,7 @@ static int decoder_batch_run(nemoasr_batch_t *b, int nact, char *err, size_t err
 }
 
 /* ---- device-resident batched greedy loop (kernels/nk_bdec.hip) --------------------------------- */
-#define BDEC_STEPS 10 /* steps per graph run; the host reads the state back once per run */
+#define BDEC_STEPS 10 /* steps per graph run (even: step parities repeat); the host reads the state back once per run */
 
 static NkBDecArgs bdec_args(nemoasr_batch_t *b) {
     model_t *m = b->m;
@@ -1242,6 +1245,8 @@ static NkBDecArgs bdec_args(nemoasr_batch_t *b) {
     a.hout = gpu_buf_dptr(b->hout);
     a.pred = gpu_buf_dptr(b->pred);
     a.jin = gpu_buf_dptr(b->jin);
+    a.rows = gpu_buf_dptr(b->brows);
+    a.cnt = gpu_buf_dptr(b->bcnt);
     a.S = (uint32_t)b->S;
     a.W = (uint32_t)b->W;
     a.P = (uint32_t)b->P;
@@ -1258,8 +1263,8 @@ typedef struct {
     NkBDecArgs d;
 } bdec_launch_t;
 
-static int launch_bdec_gemm(nemoasr_batch_t *b, const char *kernel, const float *A, uint32_t lda, const uint16_t *W,
-                            uint32_t ldw, const float *bias, uint32_t N, uint32_t K, uint32_t waves) {
+static int launch_bdec_gemm(nemoasr_batch_t *b, uint32_t par, const char *kernel, const float *A, uint32_t lda,
+                            const uint16_t *W, uint32_t ldw, const float *bias, uint32_t N, uint32_t K, uint32_t waves) {
     bdec_launch_t x;
     memset(&x, 0, sizeof x);
     x.g.A = A;
@@ -1271,22 +1276,27 @@ static int launch_bdec_gemm(nemoasr_batch_t *b, const char *kernel, const float 
     x.g.N = N;
     x.g.K = K;
     x.d = bdec_args(b);
+    x.d.par = par;
     return gpu_launch(b->gd, kernel, &x, sizeof x, N / 16, ((uint32_t)b->S + 63) / 64, 1, 64 * waves, 1, 1);
 }
 
 static void launch_bdec_steps(nemoasr_batch_t *b, int steps) {
     gpu_t *g = b->gd;
-    const NkBDecArgs a = bdec_args(b);
+    NkBDecArgs a = bdec_args(b);
     const uint32_t S = a.S, P = a.P, J = a.J, Vp = (uint32_t)b->Vp, R = a.S * a.W;
     for (int k = 0; k < steps; ++k) {
+        /* step parity: the rows come from counter par ^ 1, the decisions append to counter par */
+        const uint32_t par = (uint32_t)k & 1u;
+        a.par = par;
         /* layer 0: the Wh0 half of the interleaved [Wx0 | Wh0] rows (row stride 2P) */
-        launch_bdec_gemm(b, "bdec_lstm0_w4s5", a.A0, P, (const uint16_t *)gpu_buf_dptr(b->wcati[0]) + P, 2 * P, NULL,
-                         4 * P, P, 4);
-        launch_bdec_gemm(b, "bdec_lstm1_w8s5", a.A1, 2 * P, gpu_buf_dptr(b->wcati[1]), 2 * P, gpu_buf_dptr(b->bi[1]),
-                         4 * P, 2 * P, 8);
-        launch_bdec_gemm(b, "bdec_pred_w4s5", a.hout, P, b->m->joint_pred_w, P, b->m->joint_pred_b, J, P, 4);
-        nk_gemm_argmax(g, a.jin, J, gpu_buf_dptr(b->wout), J, gpu_buf_dptr(b->bout), gpu_buf_dptr(b->keys),
-                       (uint32_t)b->nkeys, R, Vp, J, (uint32_t)b->V);
+        launch_bdec_gemm(b, par, "bdec_lstm0_w4s5", a.A0, P, (const uint16_t *)gpu_buf_dptr(b->wcati[0]) + P, 2 * P,
+                         NULL, 4 * P, P, 4);
+        launch_bdec_gemm(b, par, "bdec_lstm1_w8s5", a.A1, 2 * P, gpu_buf_dptr(b->wcati[1]), 2 * P,
+                         gpu_buf_dptr(b->bi[1]), 4 * P, 2 * P, 8);
+        launch_bdec_gemm(b, par, "bdec_pred_w4s5", a.hout, P, b->m->joint_pred_w, P, b->m->joint_pred_b, J, P, 4);
+        /* more than one row block: only the step's rows are scored */
+        nk_gemm_argmax_rows(g, a.jin, J, gpu_buf_dptr(b->wout), J, gpu_buf_dptr(b->bout), gpu_buf_dptr(b->keys),
+                            (uint32_t)b->nkeys, R, Vp, J, (uint32_t)b->V, S > 64 ? a.cnt + (par ^ 1u) : NULL, a.W);
         gpu_launch(g, "bdec_decide", &a, sizeof a, S, 1, 1, 64, 1, 1);
     }
 }
@@ -1297,7 +1307,7 @@ static int decoder_batch_device(nemoasr_batch_t *b, char *err, size_t errlen) {
     gpu_t *g = b->gd;
     const int S = b->S, nact = b->dnact;
     int *su = b->stage_bsetup;
-    memset(su, 0, (size_t)2 * S * sizeof(int));
+    memset(su, 0, (size_t)(2 * S + 2) * sizeof(int));
     int maxc = 0;
     for (int i = 0; i < nact; ++i) {
         su[2 * b->dorder[i]] = b->dc[i];
@@ -1312,6 +1322,7 @@ static int decoder_batch_device(nemoasr_batch_t *b, char *err, size_t errlen) {
         gpu_begin(g);
         if (run == 0) {
             gpu_upload_async(g, gpu_buf_dptr(b->bsetup), su, (size_t)2 * S * sizeof(int));
+            gpu_upload_async(g, gpu_buf_dptr(b->bcnt), su + 2 * S, 2 * sizeof(int)); /* zero row counters */
             gpu_launch(g, "bdec_setup", &a, sizeof a, (uint32_t)S, 1, 1, 64, 1, 1);
         }
         if (b->use_graphs && !b->dgraph[b->dbuf] && !gpu_capture_begin(g)) {

@@ -156,6 +156,12 @@ static int launch_mx(gpu_t *g, NkGemmArgs *a, uint32_t M, uint32_t nout, uint32_
 
 int nk_gemm_argmax(gpu_t *g, const float *A, uint32_t lda, const uint16_t *W, uint32_t ldw, const float *bias,
                    unsigned long long *keys, uint32_t keys_ld, uint32_t M, uint32_t N, uint32_t K, uint32_t V) {
+    return nk_gemm_argmax_rows(g, A, lda, W, ldw, bias, keys, keys_ld, M, N, K, V, NULL, 0);
+}
+
+int nk_gemm_argmax_rows(gpu_t *g, const float *A, uint32_t lda, const uint16_t *W, uint32_t ldw, const float *bias,
+                        unsigned long long *keys, uint32_t keys_ld, uint32_t M, uint32_t N, uint32_t K, uint32_t V,
+                        const int *mrows, uint32_t mrows_mul) {
     if (!M) return 0;
     if (N % 64 || K % 32 || V > N || keys_ld < 2 * (N / 64) || !aligned16(A) || !aligned16(W) || lda % 4 || ldw % 8)
         return bad(g, "gemm_argmax: N % 64 == 0, K % 32 == 0, V <= N, keys_ld >= N/32, aligned operands");
@@ -163,6 +169,7 @@ int nk_gemm_argmax(gpu_t *g, const float *A, uint32_t lda, const uint16_t *W, ui
     memset(&a, 0, sizeof a);
     a.A = A; a.W = W; a.bias = bias; a.M = M; a.N = N; a.K = K; a.lda = lda; a.ldw = ldw; a.ldc = N;
     a.alpha = 1.0f; a.splits = 1; a.keys = keys; a.keys_ld = keys_ld; a.keys_n = V;
+    a.mrows = mrows; a.mrows_mul = mrows_mul;
     const uint32_t tm = (M + 63) / 64, tiles = tm * (N / 64), per = (tiles + 7) / 8;
     a.group_m = tm <= 8 ? tm : (tm + 3) / 4;
     gpu_next_flops(g, 2.0 * M * N * K);

@@ -59,6 +59,10 @@ typedef struct {
      * column) of each wavefront's columns < keys_n as a packed key, keys[row * keys_ld + part] */
     unsigned long long *keys;
     u32 keys_ld, keys_n;
+    /* many-row kernel: with mrows set, only the first min(M, *mrows * mrows_mul) rows are computed
+     * (a row count known on the device only; the grid covers M) */
+    const int *mrows;
+    u32 mrows_mul, pad2;
 } NkGemmArgs;
 
 typedef struct {
@@ -315,8 +319,15 @@ typedef struct {
  * joint.enc row, and whether this step recomputes the prediction. */
 typedef struct {
     int frames, t, symbols, pred_valid, cur, last_token, n_out, erow0;
-    int need, pad[7];
+    int need, slot, pad[6];
 } NkBDecStream;
+
+/* One row of a decoder step: the streams still inside their chunk, in the order their previous
+ * decision (or the chunk's setup) appended them; the step's GEMM rows and joint-input rows follow
+ * this order.  need: the prediction is recomputed (LSTM and joint.pred rows are used). */
+typedef struct {
+    int s, need, cur, tok, t, lim, erow, pad;
+} NkBDecRow;
 
 typedef struct {
     NkBDecStream *st;      /* [S]                                                        */
@@ -327,12 +338,14 @@ typedef struct {
     const float *enc;      /* joint.enc rows [*][J]                                        */
     const float *tx;       /* [blank + 1][4P] embed . Wx0^T + b0, rows interleaved by unit */
     float *hc;             /* [S][2 slot sets][h0, c0, h1, c1][P]                          */
-    float *A0;             /* [S][P] layer-0 input h0                                      */
-    float *A1;             /* [S][2P] layer-1 input [h0' | h1]                             */
-    float *hout;           /* [S][P] new layer-1 state, input of joint.pred                */
+    float *A0;             /* [S][P] layer-0 input h0, by row                              */
+    float *A1;             /* [S][2P] layer-1 input [h0' | h1], by row                     */
+    float *hout;           /* [S][P] new layer-1 state, input of joint.pred, by row        */
     float *pred;           /* [S][J] current prediction                                    */
-    float *jin;            /* [S*W][J] joint inputs relu(enc + pred)                       */
-    u32 S, W, P, J, blank, max_symbols, tok_ld, pad;
+    float *jin;            /* [S*W][J] joint inputs relu(enc + pred), rows slot * W + k    */
+    NkBDecRow *rows;       /* [S] the step's rows                                          */
+    int *cnt;              /* [2] row counts by step parity: step par reads cnt[par ^ 1]    */
+    u32 S, W, P, J, blank, max_symbols, tok_ld, par;
 } NkBDecArgs;
 
 #endif

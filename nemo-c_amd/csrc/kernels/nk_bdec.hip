@@ -19,10 +19,13 @@
  *                 next step's layer-0 input h0.
  * After a decision every stream still inside its chunk has emitted a token, so its prediction is
  * recomputed by the next step, which also writes its joint inputs; a prediction carried over from
- * the previous chunk gets its joint inputs from bdec_setup.  Streams whose chunk is done keep stale
- * rows in the GEMM inputs; their results are never stored.  LSTM states live in two slot sets per
- * stream; committing a token flips the committed set (the reference swaps its h/hp and c/cp
- * buffers).
+ * the previous chunk gets its joint inputs from bdec_setup.  The GEMM rows of a step are the
+ * streams still inside their chunk, compacted: each decision (or the chunk's setup) appends its
+ * stream with an atomic slot counter (two counters by step parity; layer 0 clears the one the
+ * step's decisions fill), and with more than 64 streams the workgroups of row blocks past the count
+ * return at once, so a step costs what its live streams need.  A row's results do not depend on its
+ * position.  LSTM states live in two slot sets per stream; committing a token flips the committed
+ * set (the reference swaps its h/hp and c/cp buffers).
  *
  * bdec_lstm / bdec_pred are GEMMs over at most 64 rows per workgroup (grid.y = row blocks of 64):
  * a workgroup owns 16 columns; its W wavefronts split K (SPW steps of 32 each), issue every load
@@ -88,24 +91,46 @@ __device__ __forceinline__ float tile_at(const floatx4 *sred, u32 rl, u32 c) {
     return v;
 }
 
-/* the workgroup's 64 streams in LDS, staged before the GEMM phase (whose barrier publishes them):
- * need, committed slot set, layer-0 table row, frame position, frames left to score (at most W),
- * first joint.enc row */
+/* rows of the current step (appended by the previous decision or the chunk's setup) */
+__device__ __forceinline__ int step_rows(const NkBDecArgs &d) { return d.cnt[d.par ^ 1u]; }
+
+/* the workgroup's 64 rows in LDS, staged before the GEMM phase (whose barrier publishes them):
+ * stream, need, committed slot set, layer-0 table row, frame position, frames left to score (at
+ * most W), first joint.enc row */
 struct BDecStage {
-    int need[64], cur[64], tok[64], t[64], lim[64], erow[64];
+    int s[64], need[64], cur[64], tok[64], t[64], lim[64], erow[64];
 };
 
 __device__ __forceinline__ void stage_state(const NkBDecArgs &d, u32 r0, BDecStage &ss) {
     if (threadIdx.x < 64) {
-        const u32 i = threadIdx.x, s = min(r0 + i, d.S - 1);
-        const NkBDecStream p = d.st[s];
-        ss.need[i] = r0 + i < d.S ? p.need : 0;
+        const u32 i = threadIdx.x;
+        const NkBDecRow p = d.rows[min(r0 + i, d.S - 1)];
+        const bool ok = (int)(r0 + i) < step_rows(d);
+        ss.s[i] = p.s;
+        ss.need[i] = ok ? p.need : 0;
         ss.cur[i] = p.cur;
-        ss.tok[i] = p.last_token >= 0 && p.last_token < (int)d.blank ? p.last_token : (int)d.blank;
+        ss.tok[i] = p.tok;
         ss.t[i] = p.t;
-        ss.lim[i] = min((int)d.W, p.frames - p.t);
-        ss.erow[i] = p.erow0;
+        ss.lim[i] = p.lim;
+        ss.erow[i] = p.erow;
     }
+}
+
+/* the decision of a stream still inside its chunk appends it to the next step's rows */
+__device__ __forceinline__ int append_row(const NkBDecArgs &d, u32 par, int s, int need, int cur, int last, int t,
+                                          int frames, int erow) {
+    const int slot = atomicAdd(d.cnt + par, 1);
+    NkBDecRow r;
+    r.s = s;
+    r.need = need;
+    r.cur = cur;
+    r.tok = last >= 0 && last < (int)d.blank ? last : (int)d.blank;
+    r.t = t;
+    r.lim = min((int)d.W, frames - t);
+    r.erow = erow;
+    r.pad = 0;
+    d.rows[slot] = r;
+    return slot;
 }
 
 /* LSTM layer L (0 or 1) on all streams; grid (4P/16, ceil(S/64)), 64 W threads.  Layer 0: a.A = h0
@@ -117,12 +142,15 @@ __device__ __forceinline__ void bdec_lstm_impl(const NkGemmArgs &a, const NkBDec
                                                BDecStage &ss) {
     static_assert(W >= 4, "the cell epilogue uses 256 threads");
     const u32 lane = threadIdx.x & 63, r0 = blockIdx.y * 64, col = blockIdx.x * 16 + (lane & 15);
+    if (L == 0 && blockIdx.x == 0 && threadIdx.x == 0) d.cnt[d.par] = 0; /* this step's decisions append here */
+    if (gridDim.y > 1 && (int)r0 >= step_rows(d)) return; /* no rows in this block */
     stage_state(d, r0, ss);
     fr64_partials<W, SPW>(a.A, a.lda, a.W + (u64)col * a.ldw, a.M, a.K, r0, sred);
     const u32 t = threadIdx.x;
     if (t >= 256) return;
-    const u32 rl = t >> 2, j = t & 3, s = r0 + rl, P = d.P, u = blockIdx.x * 4 + j;
-    if (s >= d.S || !ss.need[rl]) return;
+    const u32 rl = t >> 2, j = t & 3, r = r0 + rl, P = d.P, u = blockIdx.x * 4 + j;
+    if (!ss.need[rl]) return;
+    const u32 s = (u32)ss.s[rl];
     const u32 kc = (u32)ss.cur[rl];
     constexpr u32 CI = L == 0 ? 1 : 3, HI = L == 0 ? 0 : 2;
     const float c_in = d.hc[(u64)hc_row(s, kc, CI) * P + u];
@@ -138,22 +166,22 @@ __device__ __forceinline__ void bdec_lstm_impl(const NkGemmArgs &a, const NkBDec
     d.hc[(u64)hc_row(s, kp, CI) * P + u] = c;
     d.hc[(u64)hc_row(s, kp, HI) * P + u] = h;
     if (L == 0) {
-        d.A1[(u64)s * 2 * P + u] = h;
-        d.A1[(u64)s * 2 * P + P + u] = h1c;
+        d.A1[(u64)r * 2 * P + u] = h;
+        d.A1[(u64)r * 2 * P + P + u] = h1c;
     } else {
-        d.hout[(u64)s * P + u] = h;
+        d.hout[(u64)r * P + u] = h;
     }
 }
 
-/* joint inputs of stream s at column j: rows s W + k for the lim >= 1 frames after its t (loads
+/* joint inputs of step row r at column j: rows r W + k for the lim >= 1 frames after its t (loads
  * of clamped rows first, so that they are all in flight together) */
-__device__ __forceinline__ void write_jin(const NkBDecArgs &d, u32 s, u32 j, float p, int t, int lim, int erow) {
+__device__ __forceinline__ void write_jin(const NkBDecArgs &d, u32 r, u32 j, float p, int t, int lim, int erow) {
     float e[NK_ATTC_MAX_C];
 #pragma unroll
     for (int k = 0; k < NK_ATTC_MAX_C; ++k) e[k] = d.enc[(u64)(erow + t + min(k, lim - 1)) * d.J + j];
 #pragma unroll
     for (int k = 0; k < NK_ATTC_MAX_C; ++k)
-        if (k < lim) d.jin[(u64)(s * d.W + k) * d.J + j] = fmaxf(e[k] + p, 0.0f);
+        if (k < lim) d.jin[(u64)(r * d.W + k) * d.J + j] = fmaxf(e[k] + p, 0.0f);
 }
 
 /* joint.pred for the streams that recompute their prediction, and their joint inputs; grid
@@ -162,16 +190,17 @@ template <int W, int SPW>
 __device__ __forceinline__ void bdec_pred_impl(const NkGemmArgs &a, const NkBDecArgs &d, floatx4 *sred,
                                                BDecStage &ss) {
     const u32 lane = threadIdx.x & 63, r0 = blockIdx.y * 64, col = blockIdx.x * 16 + (lane & 15);
+    if (gridDim.y > 1 && (int)r0 >= step_rows(d)) return; /* no rows in this block */
     stage_state(d, r0, ss);
     fr64_partials<W, SPW>(a.A, a.lda, a.W + (u64)col * a.ldw, a.M, a.K, r0, sred);
     const u32 c = threadIdx.x & 15, j = blockIdx.x * 16 + c;
     const float bias = a.bias[j];
     for (u32 rl = threadIdx.x >> 4; rl < 64; rl += 4 * W) {
-        const u32 s = r0 + rl;
-        if (s >= d.S || !ss.need[rl]) continue;
+        if (!ss.need[rl]) continue;
+        const u32 s = (u32)ss.s[rl];
         const float p = tile_at<W>(sred, rl, c) + bias;
         d.pred[(u64)s * d.J + j] = p;
-        write_jin(d, s, j, p, ss.t[rl], ss.lim[rl], ss.erow[rl]);
+        write_jin(d, r0 + rl, j, p, ss.t[rl], ss.lim[rl], ss.erow[rl]);
     }
 }
 
@@ -187,12 +216,12 @@ BDEC_GEMM(bdec_lstm0_w4s5, (bdec_lstm_impl<4, 5, 0>), 4, 5)
 BDEC_GEMM(bdec_lstm1_w8s5, (bdec_lstm_impl<8, 5, 1>), 8, 5)
 BDEC_GEMM(bdec_pred_w4s5, (bdec_pred_impl<4, 5>), 4, 5)
 
-/* next step's layer-0 input of stream s (one wavefront): its committed h0 (slot set cur),
- * P / 4 <= 192 float4 */
-__device__ __forceinline__ void bdec_prepare(const NkBDecArgs &a, u32 s, int cur) {
+/* next step's layer-0 input of stream s at step row r (one wavefront): its committed h0 (slot set
+ * cur), P / 4 <= 192 float4 */
+__device__ __forceinline__ void bdec_prepare(const NkBDecArgs &a, u32 r, u32 s, int cur) {
     const u32 n4 = a.P >> 2, lane = threadIdx.x;
     const floatx4 *h0 = (const floatx4 *)(a.hc + (u64)hc_row(s, (u32)cur, 0) * a.P);
-    floatx4 *A = (floatx4 *)(a.A0 + (u64)s * a.P);
+    floatx4 *A = (floatx4 *)(a.A0 + (u64)r * a.P);
     floatx4 v[3];
 #pragma unroll
     for (int i = 0; i < 3; ++i) v[i] = h0[min(lane + 64 * i, n4 - 1)];
@@ -201,13 +230,17 @@ __device__ __forceinline__ void bdec_prepare(const NkBDecArgs &a, u32 s, int cur
         if (lane + 64 * i < n4) A[lane + 64 * i] = v[i];
 }
 
-/* new chunk: frames and first joint.enc row from the host, fresh frame position and counters; a
+/* new chunk: frames and first joint.enc row from the host, fresh frame position and counters; the
+ * streams with frames become the first step's rows (row counter 1, zeroed by the host); a
  * prediction carried over from the previous chunk gets its joint inputs here.  grid S, 64 threads */
 extern "C" __global__ __launch_bounds__(64) void bdec_setup(const NkBDecArgs a) {
     const u32 s = blockIdx.x;
     NkBDecStream *sp = a.st + s;
     const int frames = a.setup[2 * s], erow0 = a.setup[2 * s + 1], pred_valid = sp->pred_valid, cur = sp->cur;
-    const int need = 0 < frames && !pred_valid;
+    const int last = sp->last_token, need = 0 < frames && !pred_valid;
+    int slot = 0;
+    if (frames > 0 && threadIdx.x == 0) slot = append_row(a, 1u, (int)s, need, cur, last, 0, frames, erow0);
+    slot = __shfl(slot, 0, 64);
     if (threadIdx.x == 0) {
         sp->frames = frames;
         sp->erow0 = erow0;
@@ -215,17 +248,19 @@ extern "C" __global__ __launch_bounds__(64) void bdec_setup(const NkBDecArgs a) 
         sp->symbols = 0;
         sp->n_out = 0;
         sp->need = need;
+        sp->slot = slot;
     }
-    if (need) bdec_prepare(a, s, cur);
+    if (need) bdec_prepare(a, (u32)slot, s, cur);
     if (0 < frames && pred_valid) {
         const int lim = min((int)a.W, frames);
-        for (u32 j = threadIdx.x; j < a.J; j += 64) write_jin(a, s, j, a.pred[(u64)s * a.J + j], 0, lim, erow0);
+        for (u32 j = threadIdx.x; j < a.J; j += 64) write_jin(a, (u32)slot, j, a.pred[(u64)s * a.J + j], 0, lim, erow0);
     }
 }
 
 /* per stream (one wavefront): lane 4 r + p takes the maximum of keys p, p + 4, ... of scored frame r
- * (at most 16 frames, nkeys <= 64), two exchanges finish each frame's maximum, a ballot finds the
- * first non-blank frame; then the greedy rule and the next step's input. */
+ * (at most 16 frames, nkeys <= 64; the stream's key rows follow its step row), two exchanges finish
+ * each frame's maximum, a ballot finds the first non-blank frame; then the greedy rule, and a
+ * stream still inside its chunk is appended to the next step's rows with its layer-0 input. */
 extern "C" __global__ __launch_bounds__(64) void bdec_decide(const NkBDecArgs a) {
     const u32 s = blockIdx.x, lane = threadIdx.x, row = lane >> 2, part = lane & 3;
     NkBDecStream *sp = a.st + s;
@@ -234,7 +269,7 @@ extern "C" __global__ __launch_bounds__(64) void bdec_decide(const NkBDecArgs a)
     int symbols = sp->symbols, cur = sp->cur, last = sp->last_token, n_out = sp->n_out, pred_valid = 1;
     const int rows = min(min((int)a.W, frames - t), NK_ATTC_MAX_C);
     const bool live = (int)row < rows;
-    const unsigned long long *kr = a.keys + (u64)(s * a.W + min((int)row, rows - 1)) * a.nkeys;
+    const unsigned long long *kr = a.keys + (u64)((u32)sp->slot * a.W + min((int)row, rows - 1)) * a.nkeys;
     unsigned long long kv[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i) kv[i] = kr[min(part + 4 * i, a.nkeys - 1)]; /* repeats change no maximum */
@@ -264,6 +299,9 @@ extern "C" __global__ __launch_bounds__(64) void bdec_decide(const NkBDecArgs a)
         if (symbols >= (int)a.max_symbols) { symbols = 0; k++; }
     }
     const int nt = t + k, need = nt < frames && !pred_valid;
+    int slot = 0;
+    if (nt < frames && lane == 0) slot = append_row(a, a.par, (int)s, need, cur, last, nt, frames, sp->erow0);
+    slot = __shfl(slot, 0, 64);
     if (lane == 0) {
         sp->t = nt;
         sp->symbols = symbols;
@@ -272,6 +310,7 @@ extern "C" __global__ __launch_bounds__(64) void bdec_decide(const NkBDecArgs a)
         sp->last_token = last;
         sp->n_out = n_out;
         sp->need = need;
+        sp->slot = slot;
     }
-    if (need) bdec_prepare(a, s, cur);
+    if (need) bdec_prepare(a, (u32)slot, s, cur);
 }

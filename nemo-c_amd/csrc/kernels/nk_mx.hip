@@ -54,7 +54,7 @@ __device__ __forceinline__ void mx_impl(const NkGemmArgs &a, lds_char_t *const (
     static_assert(AI >= 1 && BI >= 1 && TI >= 1 && TJ >= (GLU ? 2 : 1), "tile shape");
     const u32 tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const u32 wm = wave / WGN, wn = wave % WGN;
-    const u32 M = a.M;
+    const u32 M = a.mrows ? min(a.M, (u32)max(*a.mrows, 0) * a.mrows_mul) : a.M;
     const u32 nout = GLU ? a.N / 2 : a.N;
     const u32 TMt = (M + BM - 1) / BM, TNt = nout / (GLU ? BN / 2 : BN), KZ = a.splits;
 

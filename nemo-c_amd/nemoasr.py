@@ -105,6 +105,7 @@ API = {
     "nk_gemm_force": (C.c_int, [C.c_int]),
     "nk_gemm_mx_k64": (C.c_int, [C.c_int]),
     "nk_gemm_argmax": (C.c_int, [_vp, _vp, _u32, _vp, _u32, _vp, _vp, _u32, _u32, _u32, _u32, _u32]),
+    "nk_gemm_argmax_rows": (C.c_int, [_vp, _vp, _u32, _vp, _u32, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _vp, _u32]),
     "nk_gemm_kernel_name": (C.c_char_p, [_u32, _u32, _u32, C.c_int]),
     "nk_layernorm": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _u32, _u32, C.c_float]),
     "nk_layernorm2": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32, C.c_float]),

@@ -119,6 +119,28 @@ def test_batch_matches_sessions_full():
     b.close()
 
 
+@pytest.mark.parametrize("latency", [560, 1120])
+def test_batch_many_streams_compacted(latency):
+    """130 streams, three row blocks of the greedy loop's GEMMs: the compacted step rows, the row
+    blocks past the live count that return at once and the joint GEMM's device-side row count,
+    with streams of different lengths and starts (so the live count changes from step to step),
+    against single-stream sessions."""
+    import nemoasr
+
+    mdir = model_dir("tiny")
+    S = 130
+    mels = [mel_ref.logmel(synth.make_audio(0.4 + 0.07 * (i % 23), seed=300 + i)) for i in range(S)]
+    b = nemoasr.Batch(mdir, "en-US", latency, streams=S)
+    drive(b, mels, [i % 5 for i in range(S)], piece=8 * (LAT_RIGHT[latency] + 1))
+    sess = nemoasr.Session(mdir, "en-US", latency)
+    for s, m in enumerate(mels):
+        sess.reset("en-US", latency)
+        sess.feed_mel(m, final=True)
+        assert b.tokens(s) == sess.tokens(), s
+    sess.close()
+    b.close()
+
+
 @pytest.mark.parametrize("gpu_fe", [True, False])
 def test_batch_audio_and_reset(gpu_fe):
     """Audio pushed in 100 ms blocks, text per stream, and a slot reused after reset_stream; log-mel
