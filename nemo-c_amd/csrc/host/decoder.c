@@ -32,13 +32,15 @@ typedef struct {
 struct decoder {
     model_t *m;
     gpu_t *g;
-    gpu_buf_t *st, *part, *tokens, *hc, *pred;
+    gpu_buf_t *st, *part, *tokens, *hc, *pred, *tx;
     NkDecState *host_st; /* pinned: chunk fields in, final state out */
     int *host_tok;       /* pinned: tokens of the chunk               */
     dgraph_t gr[2];
     int ngr, last_steps, use_graphs;
     double last_ms;
 };
+
+static NkDecArgs dec_args(decoder_t *d, const float *enc, uint32_t parity, uint32_t decide_only);
 
 decoder_t *decoder_create(model_t *m) {
     decoder_t *d = calloc(1, sizeof *d);
@@ -52,6 +54,16 @@ decoder_t *decoder_create(model_t *m) {
     d->pred = gpu_buf_alloc(d->g, J * sizeof(float));
     d->host_st = gpu_host_alloc(d->g, sizeof(NkDecState));
     d->host_tok = gpu_host_alloc(d->g, NK_DEC_MAX_TOKENS * sizeof(int));
+    /* the layer-0 input table, one row per token and the blank's (zero input) row */
+    const uint32_t nv = (uint32_t)m->cfg.blank_id + 1;
+    d->tx = gpu_buf_alloc(d->g, (size_t)nv * 4 * P * sizeof(float));
+    const NkDecArgs a = dec_args(d, NULL, 0, 0);
+    gpu_begin(d->g);
+    gpu_launch(d->g, "dec_tx_build", &a, sizeof a, (uint32_t)(P + 3) / 4, nv, 1, 256, 1, 1);
+    if (gpu_end(d->g, NULL, 0)) {
+        decoder_destroy(d);
+        return NULL;
+    }
     d->use_graphs = 1;
     decoder_reset(d);
     return d;
@@ -69,7 +81,7 @@ static void free_graphs(decoder_t *d) {
 void decoder_destroy(decoder_t *d) {
     if (!d) return;
     free_graphs(d);
-    gpu_buf_t *bufs[] = { d->st, d->part, d->tokens, d->hc, d->pred };
+    gpu_buf_t *bufs[] = { d->st, d->part, d->tokens, d->hc, d->pred, d->tx };
     for (size_t i = 0; i < sizeof bufs / sizeof *bufs; ++i) gpu_buf_free(bufs[i]);
     gpu_host_free(d->host_st);
     gpu_host_free(d->host_tok);
@@ -109,6 +121,7 @@ static NkDecArgs dec_args(decoder_t *d, const float *enc, uint32_t parity, uint3
     a.wjp = m->joint_pred_w; a.bjp = m->joint_pred_b;
     a.pred = gpu_buf_dptr(d->pred);
     a.wout = m->joint_out_w; a.bout = m->joint_out_b;
+    a.tx = gpu_buf_dptr(d->tx);
     a.P = (uint32_t)m->cfg.pred_hidden;
     a.J = (uint32_t)m->cfg.joint_hidden;
     a.V = (uint32_t)m->cfg.num_classes;

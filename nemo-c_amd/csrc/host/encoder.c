@@ -46,7 +46,7 @@ struct encoder {
     size_t consumed, emitted;
     int closed;
     /* device buffers */
-    gpu_buf_t *win, *c0, *c1, *c2, *c3, *c4, *flat, *pre_out;
+    gpu_buf_t *win, *c0, *c1, *c2, *c3, *c4, *flat;
     gpu_buf_t *h, *tmp, *t2, *ff, *att, *y, *ph, *prompted, *joint_enc;
     gpu_buf_t *kv, *din, *desc;
     size_t kv_stride, din_stride; /* floats per layer */
@@ -93,7 +93,6 @@ encoder_t *encoder_create(model_t *m, int right) {
     e->c3 = gpu_buf_alloc(g, T3 * F3 * CH * fs);
     e->c4 = gpu_buf_alloc(g, T3 * F3 * CH * fs);
     e->flat = gpu_buf_alloc(g, T3 * F3 * CH * fs);
-    e->pre_out = gpu_buf_alloc(g, T3 * D * fs);
     e->h = gpu_buf_alloc(g, cm * D * fs);
     e->tmp = gpu_buf_alloc(g, cm * D * fs);
     e->t2 = gpu_buf_alloc(g, cm * D * fs);
@@ -127,7 +126,7 @@ static void drop_graphs(encoder_t *e) {
 void encoder_destroy(encoder_t *e) {
     if (!e) return;
     drop_graphs(e);
-    gpu_buf_t *bufs[] = { e->win, e->c0, e->c1, e->c2, e->c3, e->c4, e->flat, e->pre_out, e->h, e->tmp, e->t2, e->ff,
+    gpu_buf_t *bufs[] = { e->win, e->c0, e->c1, e->c2, e->c3, e->c4, e->flat, e->h, e->tmp, e->t2, e->ff,
                           e->att, e->y, e->ph, e->prompted, e->joint_enc, e->kv, e->din, e->desc, e->dump_dev };
     for (size_t i = 0; i < sizeof bufs / sizeof *bufs; ++i) gpu_buf_free(bufs[i]);
     gpu_host_free(e->stage_win);
@@ -223,8 +222,10 @@ enc_plan_t enc_plan_step(enc_book_t *b, int final, int chunk_mel, int subsamplin
     return p;
 }
 
-/* subsampling of the window (nwin mel rows) into pre_out: src/encoder.c:120-142 */
-static void run_pre_encode(encoder_t *e, int nwin) {
+/* subsampling of the window (nwin mel rows): src/encoder.c:120-142.  The output projection runs
+ * only on the c rows the chunk emits (rows lo .. lo+c-1 of the subsampled window; the reference
+ * projects all T3 rows and copies these, src/encoder.c:142, :258) and writes them into h. */
+static void run_pre_encode(encoder_t *e, int nwin, int lo, int c) {
     model_t *m = e->m;
     gpu_t *g = e->g;
     const uint32_t CH = (uint32_t)m->cfg.sub_channels, F = (uint32_t)m->cfg.feat_in;
@@ -238,7 +239,8 @@ static void run_pre_encode(encoder_t *e, int nwin) {
     nk_gemm(g, c3, CH, m->conv6_w, CH, m->conv6_b, c4, CH, T3 * F3, CH, CH, NK_ACT_RELU, 0, 1.0f);
     nk_flatten_cf(g, c4, flat, T3, F3, CH);
     const uint32_t D = (uint32_t)m->cfg.d_model, K = CH * F3;
-    nk_gemm(g, flat, K, m->pre_out_w, K, m->pre_out_b, gpu_buf_dptr(e->pre_out), D, T3, D, K, NK_ACT_NONE, 0, 1.0f);
+    nk_gemm(g, flat + (size_t)lo * K, K, m->pre_out_w, K, m->pre_out_b, gpu_buf_dptr(e->h), D, (uint32_t)c, D, K,
+            NK_ACT_NONE, 0, 1.0f);
 }
 
 /* 24 conformer blocks + prompt + joint projection on the c rows in e->h: src/encoder.c:144-197.
@@ -319,11 +321,9 @@ static void run_blocks(encoder_t *e, int c) {
     nk_gemm(g, pr, D, m->joint_enc_w, D, m->joint_enc_b, gpu_buf_dptr(e->joint_enc), JH, uc, JH, D, NK_ACT_NONE, 0, 1.0f);
 }
 
-/* everything a chunk launches after the uploads: pre-encode, row select, blocks */
+/* everything a chunk launches after the uploads: pre-encode (its emitted rows into h), blocks */
 static void launch_chunk(encoder_t *e, int nwin, int lo, int c) {
-    const uint32_t D = (uint32_t)e->m->cfg.d_model;
-    run_pre_encode(e, nwin);
-    nk_copy(e->g, (float *)gpu_buf_dptr(e->pre_out) + (size_t)lo * D, gpu_buf_dptr(e->h), (uint32_t)c * D);
+    run_pre_encode(e, nwin, lo, c);
     run_blocks(e, c);
 }
 

@@ -77,6 +77,11 @@ static int right_for(int latency_ms) {
 static void warmup(model_t *m, int right, char *err, size_t errlen) {
     encoder_t *e = encoder_create(m, right);
     decoder_t *d = decoder_create(m);
+    if (!e || !d) {
+        decoder_destroy(d);
+        encoder_destroy(e);
+        return;
+    }
     melfe_t *ms = melfe_create();
     static const float zeros[1600];
     int tok[64];
@@ -115,6 +120,11 @@ nemoasr_t *nemoasr_open(const char *model_dir, const char *language, int latency
     s->enc = encoder_create(s->m, right);
     s->dec = decoder_create(s->m);
     s->mel = melfe_create();
+    if (!s->enc || !s->dec) {
+        snprintf(err, errlen, "nemoasr_open: GPU setup failed: %s", gpu_last_error(s->m->gpu));
+        nemoasr_close(s);
+        return NULL;
+    }
     s->input_rate = input_rate;
     s->latency_ms = latency_ms;
     if (input_rate != MEL_SR) s->rs = rsmp_create(input_rate, MEL_SR);

@@ -261,6 +261,8 @@ typedef struct {
     float *pred;              /* [J]                                                               */
     const u16 *wout;          /* joint output [V][J]                                                */
     const float *bout;        /* [V]                                                               */
+    float *tx;                /* [blank + 1][4P] layer-0 input gates Wx0 . embed(v) + b0 (zero input
+                                 for the blank row): read by dec_lstm0, written by dec_tx_build    */
     u32 P, J, V, blank, max_symbols, parity, enc_ld, decide_only;
 } NkDecArgs;
 

@@ -8,7 +8,9 @@
  *              the symbol count; max_symbols moves past the frame) from the packed per-workgroup
  *              argmax keys, workgroup 0 records it (next state copy, emitted token); then, when the
  *              prediction must be recomputed, LSTM layer 0 from embed(last token)
- *              (src/decoder.c:57-77; zeros for blank);
+ *              (src/decoder.c:57-77; zeros for blank); its input half Wx0 . embed(v) + b0 is a
+ *              per-token table built once by dec_tx_build with this kernel's own lane layout and
+ *              sums, so the gates are the same bits while only Wh0 is streamed;
  *   dec_lstm1  LSTM layer 1;
  *   dec_pred   joint.pred projection of the new hidden state;
  *   dec_joint  joint scores relu(enc[t + r] + pred) . W_out + b for up to 16 remaining frames
@@ -64,14 +66,9 @@ __device__ __forceinline__ NkDecState dec_decide(const NkDecArgs &a, const NkDec
     return d;
 }
 
-/* One LSTM layer for unit j = global wavefront index: four gate rows of Wx and Wh (K = P <= 1024,
- * two 16-byte chunks per lane per row), then the cell.  x_f32 (or x_bf16 for the embedding row,
- * or zeros when x_zero) is the layer input. */
-__device__ __forceinline__ void dec_lstm_unit(const NkDecArgs &a, u32 j, const float *x_f32, const u16 *x_bf16,
-                                              bool x_zero, const u16 *Wx, const u16 *Wh, const float *bias,
-                                              const float *h_in, const float *c_in, float *h_out, float *c_out) {
-    const u32 lane = threadIdx.x & 63, P = a.P, nch = P >> 3;
-    float x[2][8], h[2][8];
+/* lane l's 16-byte chunks l and l + 64 of a row of P floats (or bf16), zero past the row */
+__device__ __forceinline__ void dec_row_chunks(float (&x)[2][8], const float *x_f32, const u16 *x_bf16, bool zero,
+                                               u32 lane, u32 nch) {
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
         const u32 k = 8 * min(lane + 64 * q, nch - 1);
@@ -84,13 +81,35 @@ __device__ __forceinline__ void dec_lstm_unit(const NkDecArgs &a, u32 j, const f
             x[q][0] = p0[0]; x[q][1] = p0[1]; x[q][2] = p0[2]; x[q][3] = p0[3];
             x[q][4] = p1[0]; x[q][5] = p1[1]; x[q][6] = p1[2]; x[q][7] = p1[3];
         }
-        const floatx4 p0 = *(const floatx4 *)(h_in + k), p1 = *(const floatx4 *)(h_in + k + 4);
-        h[q][0] = p0[0]; h[q][1] = p0[1]; h[q][2] = p0[2]; h[q][3] = p0[3];
-        h[q][4] = p1[0]; h[q][5] = p1[1]; h[q][6] = p1[2]; h[q][7] = p1[3];
     }
+}
+
+/* wavefront sums of the four gate rows g*P + j of W against the lane's chunks of x */
+__device__ __forceinline__ void dec_gate_dots(float (&out)[4], float (&x)[2][8], const uint4 (&w)[4][2]) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        float sx = 0.0f;
+#pragma unroll
+        for (int q = 0; q < 2; ++q) sx = dot8(x[q], w[g][q], sx);
+        out[g] = wsum(sx);
+    }
+}
+
+/* One LSTM layer for unit j = global wavefront index: four gate rows of Wx and Wh (K = P <= 1024,
+ * two 16-byte chunks per lane per row), then the cell.  x_f32 (or x_bf16 for the embedding row,
+ * or zeros when x_zero) is the layer input; with tx_row set, the input half Wx.x + b of the gates
+ * comes from that table row instead (no Wx stream). */
+__device__ __forceinline__ void dec_lstm_unit(const NkDecArgs &a, u32 j, const float *x_f32, const u16 *x_bf16,
+                                              bool x_zero, const u16 *Wx, const u16 *Wh, const float *bias,
+                                              const float *tx_row, const float *h_in, const float *c_in,
+                                              float *h_out, float *c_out) {
+    const u32 lane = threadIdx.x & 63, P = a.P, nch = P >> 3;
+    float x[2][8], h[2][8];
+    if (!tx_row) dec_row_chunks(x, x_f32, x_bf16, x_zero, lane, nch);
+    dec_row_chunks(h, h_in, nullptr, false, lane, nch);
     float bg[4];
 #pragma unroll
-    for (int g = 0; g < 4; ++g) bg[g] = bias[g * P + j];
+    for (int g = 0; g < 4; ++g) bg[g] = tx_row ? tx_row[g * P + j] : bias[g * P + j];
     const float c0 = c_in[j];
     __builtin_amdgcn_sched_barrier(0);
     uint4 wx[4][2], wh[4][2];
@@ -99,7 +118,7 @@ __device__ __forceinline__ void dec_lstm_unit(const NkDecArgs &a, u32 j, const f
 #pragma unroll
         for (int q = 0; q < 2; ++q) {
             const u64 off = (u64)(g * P + j) * P + 8 * min(lane + 64 * q, nch - 1);
-            wx[g][q] = ld_nt16(Wx + off);
+            if (!tx_row) wx[g][q] = ld_nt16(Wx + off);
             wh[g][q] = ld_nt16(Wh + off);
         }
     __builtin_amdgcn_sched_barrier(0);
@@ -108,26 +127,46 @@ __device__ __forceinline__ void dec_lstm_unit(const NkDecArgs &a, u32 j, const f
         const bool ok = lane + 64 * q < nch;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-            x[q][e] = ok && !x_zero ? x[q][e] : 0.0f;
+            if (!tx_row) x[q][e] = ok && !x_zero ? x[q][e] : 0.0f;
             h[q][e] = ok ? h[q][e] : 0.0f;
         }
     }
-    float gate[4];
+    float sxg[4], shg[4], gate[4];
+    if (!tx_row) dec_gate_dots(sxg, x, wx);
+    dec_gate_dots(shg, h, wh);
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
-        float sx = 0.0f, sh = 0.0f;
-#pragma unroll
-        for (int q = 0; q < 2; ++q) {
-            sx = dot8(x[q], wx[g][q], sx);
-            sh = dot8(h[q], wh[g][q], sh);
-        }
-        gate[g] = (wsum(sx) + bg[g]) + wsum(sh);
-    }
+    for (int g = 0; g < 4; ++g) gate[g] = (tx_row ? bg[g] : sxg[g] + bg[g]) + shg[g];
     if (lane != 0) return;
     const float ig = sigmoid_f(gate[0]), fg = sigmoid_f(gate[1]), gg = tanhf(gate[2]), og = sigmoid_f(gate[3]);
     const float c = fg * c0 + ig * gg;
     c_out[j] = c;
     h_out[j] = og * tanhf(c);
+}
+
+/* the layer-0 input table: row v = Wx0 . embed(v) + b0 (the blank row: b0), gate-major [4P], in
+ * dec_lstm_unit's lane layout and summation order.  grid = ceil(P/4) x (blank + 1), block 256. */
+extern "C" __global__ __launch_bounds__(256) void dec_tx_build(const NkDecArgs a) {
+    const u32 j = blockIdx.x * 4 + (threadIdx.x >> 6), v = blockIdx.y, lane = threadIdx.x & 63, P = a.P, nch = P >> 3;
+    if (j >= P) return;
+    const bool zero = v == a.blank;
+    float x[2][8];
+    dec_row_chunks(x, nullptr, a.embed + (u64)(zero ? 0u : v) * P, zero, lane, nch);
+    uint4 wx[4][2];
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+#pragma unroll
+        for (int q = 0; q < 2; ++q) wx[g][q] = ld_nt16(a.wx0 + (u64)(g * P + j) * P + 8 * min(lane + 64 * q, nch - 1));
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+        const bool ok = lane + 64 * q < nch;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[q][e] = ok && !zero ? x[q][e] : 0.0f;
+    }
+    float sx[4];
+    dec_gate_dots(sx, x, wx);
+    if (lane != 0) return;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) a.tx[(u64)v * 4 * P + g * P + j] = sx[g] + a.b0[g * P + j];
 }
 
 /* decision + LSTM layer 0.  grid = ceil(P/4) x 1, block 256 (one unit per wavefront). */
@@ -150,8 +189,8 @@ extern "C" __global__ __launch_bounds__(256) void dec_lstm0(const NkDecArgs a) {
     const float *hc_c = a.hc + (u64)cm * 4 * P, *none = nullptr;
     float *hc_p = a.hc + (u64)pv * 4 * P;
     const bool blank = d.last_token == (int)a.blank || d.last_token < 0;
-    const u16 *emb = a.embed + (u64)(blank ? 0 : d.last_token) * P;
-    dec_lstm_unit(a, j, none, emb, blank, a.wx0, a.wh0, a.b0, hc_c, hc_c + 2 * P, hc_p, hc_p + 2 * P);
+    const float *tx_row = a.tx + (u64)(blank ? a.blank : (u32)d.last_token) * 4 * P;
+    dec_lstm_unit(a, j, none, nullptr, blank, a.wx0, a.wh0, a.b0, tx_row, hc_c, hc_c + 2 * P, hc_p, hc_p + 2 * P);
 }
 
 /* LSTM layer 1 from the new layer-0 state */
@@ -162,7 +201,8 @@ extern "C" __global__ __launch_bounds__(256) void dec_lstm1(const NkDecArgs a) {
     const u32 P = a.P, cm = (u32)s.cur, pv = cm ^ 1u;
     const float *hc_c = a.hc + (u64)cm * 4 * P;
     float *hc_p = a.hc + (u64)pv * 4 * P;
-    dec_lstm_unit(a, j, hc_p, nullptr, false, a.wx1, a.wh1, a.b1, hc_c + P, hc_c + 3 * P, hc_p + P, hc_p + 3 * P);
+    dec_lstm_unit(a, j, hc_p, nullptr, false, a.wx1, a.wh1, a.b1, nullptr, hc_c + P, hc_c + 3 * P, hc_p + P,
+                  hc_p + 3 * P);
 }
 
 /* pred = joint.pred . h1' + b; one output per wavefront (K = P <= 1024) */
