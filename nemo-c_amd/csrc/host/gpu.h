@@ -45,6 +45,17 @@ int gpu_download(gpu_t *g, void *dst, const void *src_dev, size_t n);
 int gpu_upload_async(gpu_t *g, void *dst_dev, const void *src_pinned, size_t n);
 int gpu_download_async(gpu_t *g, void *dst_pinned, const void *src_dev, size_t n);
 
+/* Load-time copy of byte ranges of an open file into device memory, synchronous: reader threads
+ * pread pieces of at most a few MiB into pinned staging slots and queue each slot's copy
+ * asynchronously; a slot is refilled once its copy has completed, so the disk or page-cache
+ * reads overlap the PCIe transfers.  Returns 0, or -1 with the error in gpu_last_error. */
+typedef struct {
+    uint64_t off;   /* file offset */
+    uint64_t bytes;
+    void *dst;      /* device address */
+} gpu_file_range_t;
+int gpu_upload_file(gpu_t *g, int fd, const gpu_file_range_t *ranges, size_t n);
+
 int gpu_begin(gpu_t *g);
 /* Launch `kernel` with one by-value argument block of `args_size` bytes; grid in workgroups. */
 int gpu_launch(gpu_t *g, const char *kernel, const void *args, size_t args_size,

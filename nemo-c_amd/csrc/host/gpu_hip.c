@@ -1,9 +1,12 @@
 /* HIP runtime layer for one gfx950 GPU (see gpu.h).  Plain C over the HIP runtime API. */
 #include "gpu.h"
+#include <errno.h>
 #include <hip/hip_runtime_api.h>
+#include <pthread.h>
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
+#include <unistd.h>
 
 /* HIP extension (hip/hip_ext.h, which is C++-only): a module launch whose start / stop events
  * are stamped by the dispatch packet itself. */
@@ -184,6 +187,120 @@ int gpu_download_async(gpu_t *g, void *dst, const void *src, size_t n) {
     if (!n) return 0;
     hipError_t e = hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToHost, g->stream);
     return e == hipSuccess ? 0 : fail(g, "download_async", e);
+}
+
+/* ---- file -> device loader ---------------------------------------------------------------- */
+
+#define UPF_THREADS 4
+#define UPF_SLOTS 2             /* staging slots per reader thread */
+#define UPF_PIECE (8u << 20)    /* bytes per slot */
+
+typedef struct {
+    uint64_t off, bytes;
+    char *dst;
+} upf_piece_t;
+
+typedef struct {
+    gpu_t *g;
+    int fd;
+    const upf_piece_t *pc;
+    size_t npc;
+    char *stage;
+    hipEvent_t ev[UPF_THREADS * UPF_SLOTS];
+    pthread_mutex_t mu;
+    size_t next;   /* next piece to take (under mu) */
+    int failed;    /* set under mu; readers stop taking pieces */
+    char msg[200];
+} upf_t;
+
+typedef struct {
+    upf_t *u;
+    int id;
+} upf_worker_t;
+
+static void upf_error(upf_t *u, const char *msg) {
+    pthread_mutex_lock(&u->mu);
+    if (!u->failed) snprintf(u->msg, sizeof u->msg, "%s", msg);
+    u->failed = 1;
+    pthread_mutex_unlock(&u->mu);
+}
+
+static void *upf_reader(void *arg) {
+    const upf_worker_t *w = arg;
+    upf_t *u = w->u;
+    hipError_t e = hipSetDevice(u->g->dev);
+    if (e != hipSuccess) { upf_error(u, hipGetErrorString(e)); return NULL; }
+    int used[UPF_SLOTS] = { 0 }, k = 0;
+    for (;;) {
+        pthread_mutex_lock(&u->mu);
+        const size_t i = u->failed ? u->npc : u->next++;
+        pthread_mutex_unlock(&u->mu);
+        if (i >= u->npc) break;
+        const int slot = w->id * UPF_SLOTS + k;
+        char *buf = u->stage + (size_t)slot * UPF_PIECE;
+        if (used[k] && (e = hipEventSynchronize(u->ev[slot])) != hipSuccess) { upf_error(u, hipGetErrorString(e)); break; }
+        const upf_piece_t *p = &u->pc[i];
+        uint64_t got = 0;
+        while (got < p->bytes) {
+            const ssize_t r = pread(u->fd, buf + got, (size_t)(p->bytes - got), (off_t)(p->off + got));
+            if (r < 0 && errno == EINTR) continue;
+            if (r <= 0) { upf_error(u, r < 0 ? strerror(errno) : "file shorter than its header says"); return NULL; }
+            got += (uint64_t)r;
+        }
+        if ((e = hipMemcpyAsync(p->dst, buf, p->bytes, hipMemcpyHostToDevice, u->g->stream)) != hipSuccess ||
+            (e = hipEventRecord(u->ev[slot], u->g->stream)) != hipSuccess) {
+            upf_error(u, hipGetErrorString(e));
+            break;
+        }
+        used[k] = 1;
+        k = (k + 1) % UPF_SLOTS;
+    }
+    return NULL;
+}
+
+int gpu_upload_file(gpu_t *g, int fd, const gpu_file_range_t *ranges, size_t n) {
+    size_t npc = 0;
+    for (size_t i = 0; i < n; ++i) npc += (size_t)((ranges[i].bytes + UPF_PIECE - 1) / UPF_PIECE);
+    if (!npc) return 0;
+    upf_t u = { .g = g, .fd = fd, .npc = npc };
+    upf_piece_t *pc = malloc(npc * sizeof *pc);
+    size_t j = 0;
+    for (size_t i = 0; i < n; ++i)
+        for (uint64_t o = 0; o < ranges[i].bytes; o += UPF_PIECE) {
+            const uint64_t b = ranges[i].bytes - o < UPF_PIECE ? ranges[i].bytes - o : UPF_PIECE;
+            pc[j++] = (upf_piece_t){ ranges[i].off + o, b, (char *)ranges[i].dst + o };
+        }
+    u.pc = pc;
+    /* work queued elsewhere on the device (the zero fill of fresh buffers) lands first */
+    hipError_t e = hipDeviceSynchronize();
+    if (e != hipSuccess) { free(pc); return fail(g, "upload_file sync", e); }
+    const int nthr = npc < UPF_THREADS ? (int)npc : UPF_THREADS;
+    e = hipHostMalloc((void **)&u.stage, (size_t)nthr * UPF_SLOTS * UPF_PIECE, hipHostMallocDefault);
+    if (e != hipSuccess) { free(pc); return fail(g, "staging buffer", e); }
+    int nev = 0;
+    while (nev < nthr * UPF_SLOTS && (e = hipEventCreateWithFlags(&u.ev[nev], hipEventDisableTiming)) == hipSuccess) ++nev;
+    pthread_mutex_init(&u.mu, NULL);
+    pthread_t th[UPF_THREADS];
+    upf_worker_t wk[UPF_THREADS];
+    int started = 0;
+    if (nev == nthr * UPF_SLOTS)
+        for (; started < nthr; ++started) {
+            wk[started] = (upf_worker_t){ &u, started };
+            if (pthread_create(&th[started], NULL, upf_reader, &wk[started])) break;
+        }
+    else
+        upf_error(&u, hipGetErrorString(e));
+    if (started == 0 && !u.failed) upf_error(&u, "cannot start a reader thread");
+    for (int t = 0; t < started; ++t) pthread_join(th[t], NULL);
+    /* the readers have queued every copy they took; wait for them before the staging goes */
+    e = hipStreamSynchronize(g->stream);
+    if (e != hipSuccess) upf_error(&u, hipGetErrorString(e));
+    for (int i = 0; i < nev; ++i) hipEventDestroy(u.ev[i]);
+    hipHostFree(u.stage);
+    pthread_mutex_destroy(&u.mu);
+    free(pc);
+    if (u.failed) return gpu_fail(g, u.msg);
+    return 0;
 }
 
 static hipFunction_t lookup(gpu_t *g, const char *kernel) {

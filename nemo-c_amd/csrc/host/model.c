@@ -2,11 +2,13 @@
 #include "nemo_kernels.h"
 #include "safetensors.h"
 #include "../kernel_params.h"
+#include <fcntl.h>
 #include <math.h>
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
 #include <time.h>
+#include <unistd.h>
 
 static double now_ms(void) {
     struct timespec ts;
@@ -139,6 +141,7 @@ model_t *model_load(const char *dir, char *err, size_t errlen) {
     if (!m->config) { snprintf(err, errlen, "config.json: %s", jerr); free(m); return NULL; }
     if (parse_cfg(m, err, errlen)) { model_free(m); return NULL; }
     st_map_t st;
+    gpu_buf_t *wpos_d = NULL;
     snprintf(path, sizeof path, "%s/model.safetensors", dir);
     if (st_map(path, &st, err, errlen)) { model_free(m); return NULL; }
     m->gpu = gpu_create(err, errlen);
@@ -232,19 +235,37 @@ model_t *model_load(const char *dir, char *err, size_t errlen) {
     m->farena = gpu_buf_alloc(m->gpu, fcount * sizeof(float));
     if (!m->warena || !m->farena) { snprintf(err, errlen, "cannot allocate the weight arenas (%zu MB)", wbytes >> 20); goto fail; }
     m->warena_bytes = wbytes;
+    /* the per-layer linear_pos weights feed the position tables only: they go to a temporary
+       buffer with the same file -> device copy as the arena */
+    wpos_d = gpu_buf_alloc(m->gpu, nl * D * D * sizeof(uint16_t));
+    if (!wpos_d) { snprintf(err, errlen, "cannot allocate the position weights"); goto fail; }
     {
         char *wbase = gpu_buf_dptr(m->warena);
+        gpu_file_range_t *rg = calloc(r.nb + nl, sizeof *rg);
         size_t off = 0;
         for (size_t i = 0; i < r.nb; ++i) {
             const int packed = strstr(r.b[i].name, "linear_k.weight") || strstr(r.b[i].name, "linear_v.weight");
             if (!packed) off = up_to(off, WALIGN);
-            if (gpu_upload(m->gpu, wbase + off, st_ptr(&st, bt[i]), bt[i]->nbytes)) {
-                snprintf(err, errlen, "weight upload: %s", gpu_last_error(m->gpu));
-                goto fail;
-            }
+            rg[i] = (gpu_file_range_t){ bt[i]->offset, bt[i]->nbytes, wbase + off };
             *r.b[i].dst = (const uint16_t *)(wbase + off);
             off += bt[i]->nbytes;
         }
+        int urc = 0;
+        for (size_t l = 0; l < nl && !urc; ++l) {
+            snprintf(n, sizeof n, "encoder.layers.%zu.self_attn.linear_pos.weight", l);
+            const st_entry_t *t = need(&st, n, D * D, err, errlen);
+            if (!t) urc = -2;
+            else rg[r.nb + l] = (gpu_file_range_t){ t->offset, t->nbytes, (uint16_t *)gpu_buf_dptr(wpos_d) + l * D * D };
+        }
+        if (!urc) {
+            const int fd = open(path, O_RDONLY);
+            urc = fd < 0 ? -3 : gpu_upload_file(m->gpu, fd, rg, r.nb + nl);
+            if (fd >= 0) close(fd);
+            if (urc == -3) snprintf(err, errlen, "cannot open %s", path);
+            else if (urc) snprintf(err, errlen, "weight upload: %s", gpu_last_error(m->gpu));
+        }
+        free(rg);
+        if (urc) goto fail;
         float *fh = calloc(fcount ? fcount : 1, sizeof(float));
         float *fbase = gpu_buf_dptr(m->farena);
         size_t fo = 0;
@@ -287,16 +308,9 @@ model_t *model_load(const char *dir, char *err, size_t errlen) {
             }
         }
         gpu_buf_t *pe_d = gpu_buf_alloc(m->gpu, (size_t)Pr * D * sizeof(float));
-        gpu_buf_t *wpos_d = gpu_buf_alloc(m->gpu, nl * D * D * sizeof(uint16_t));
         m->ptab_buf = gpu_buf_alloc(m->gpu, nl * (size_t)Pr * D * sizeof(float));
-        int rc = !pe_d || !wpos_d || !m->ptab_buf;
+        int rc = !pe_d || !m->ptab_buf;
         if (!rc) rc = gpu_upload(m->gpu, gpu_buf_dptr(pe_d), peh, (size_t)Pr * D * sizeof(float));
-        for (size_t l = 0; l < nl && !rc; ++l) {
-            snprintf(n, sizeof n, "encoder.layers.%zu.self_attn.linear_pos.weight", l);
-            const st_entry_t *t = need(&st, n, D * D, err, errlen);
-            if (!t) { rc = -2; break; }
-            rc = gpu_upload(m->gpu, (uint16_t *)gpu_buf_dptr(wpos_d) + l * D * D, st_ptr(&st, t), t->nbytes);
-        }
         free(peh);
         if (!rc) {
             gpu_begin(m->gpu);
@@ -307,11 +321,12 @@ model_t *model_load(const char *dir, char *err, size_t errlen) {
                 m->L[l].ptab = dst;
             }
             rc = gpu_end(m->gpu, err, errlen);
-        } else if (rc != -2) {
+        } else {
             snprintf(err, errlen, "position table: %s", gpu_last_error(m->gpu));
         }
         gpu_buf_free(pe_d);
         gpu_buf_free(wpos_d);
+        wpos_d = NULL;
         if (rc) goto fail;
     }
     free(bt);
@@ -322,6 +337,7 @@ model_t *model_load(const char *dir, char *err, size_t errlen) {
     m->load_ms = now_ms() - t0;
     return m;
 fail:
+    gpu_buf_free(wpos_d);
     free(bt);
     free(ft);
     free(r.b);
