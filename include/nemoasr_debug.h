@@ -23,6 +23,9 @@ size_t nemoasr_debug_frames(const nemoasr_t *s);
 const float *nemoasr_debug_dump_layers(const nemoasr_t *s);
 const float *nemoasr_debug_dump_prompted(const nemoasr_t *s);
 const float *nemoasr_debug_dump_joint_enc(const nemoasr_t *s);
+/* Log-mel frames (128 floats each) the front end produced from fed audio since open/reset while
+   dumps were on (the reference CLI's --dump-mel, src/main.c:128). */
+const float *nemoasr_debug_dump_mel(const nemoasr_t *s, size_t *nframes);
 /* 0: launch every kernel directly; 1: replay chunks as hipGraphs (default). */
 void nemoasr_debug_use_graphs(nemoasr_t *s, int on);
 /* 1 (default): chunks of at most two rows run attention + output projection and depthwise conv +

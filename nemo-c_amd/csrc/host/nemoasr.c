@@ -41,6 +41,10 @@ struct nemoasr {
     double enc_gpu_ms;
     double load_ms;
     nemoasr_stats_t stats;
+    /* test hook: the front end's log-mel frames since open/reset, kept while dumps are on */
+    int dump;
+    float *mel_dump;
+    size_t n_mel_dump, cap_mel_dump;
 };
 
 int nemoasr_default_model_dir(char *out, size_t n) {
@@ -143,6 +147,7 @@ void nemoasr_close(nemoasr_t *s) {
     free(s->text);
     free(s->all_tok);
     free(s->chunk_ms);
+    free(s->mel_dump);
     free(s);
 }
 
@@ -220,6 +225,14 @@ char *nemoasr_feed(nemoasr_t *s, const float *samples, size_t n, int final, char
         const float *frames;
         size_t nf;
         melfe_push(s->mel, in, count, final, &frames, &nf);
+        if (nf && s->dump) {
+            if (s->n_mel_dump + nf > s->cap_mel_dump) {
+                s->cap_mel_dump = (s->n_mel_dump + nf) * 2;
+                s->mel_dump = realloc(s->mel_dump, s->cap_mel_dump * MEL_NMEL * sizeof(float));
+            }
+            memcpy(s->mel_dump + s->n_mel_dump * MEL_NMEL, frames, nf * MEL_NMEL * sizeof(float));
+            s->n_mel_dump += nf;
+        }
         if (nf) encoder_push(s->enc, frames, nf);
         if (run_pending(s, final, NULL, err, errlen) < 0) return NULL;
     }
@@ -257,6 +270,12 @@ int nemoasr_reset(nemoasr_t *s, const char *language, int latency_ms, char *err,
     } else {
         encoder_destroy(s->enc);
         s->enc = encoder_create(s->m, right);
+        if (!s->enc) {
+            snprintf(err, errlen, "nemoasr_reset: GPU setup failed: %s", gpu_last_error(s->m->gpu));
+            s->finished = 1;
+            return -1;
+        }
+        encoder_set_dump(s->enc, s->dump);
     }
     melfe_destroy(s->mel);
     s->mel = melfe_create();
@@ -270,6 +289,7 @@ int nemoasr_reset(nemoasr_t *s, const char *language, int latency_ms, char *err,
     s->latency_ms = latency_ms;
     s->n_tok = 0;
     s->n_chunk = 0;
+    s->n_mel_dump = 0;
     s->joint_steps = 0;
     s->enc_gpu_ms = 0;
     memset(&s->stats, 0, sizeof s->stats);
@@ -294,7 +314,14 @@ const int *nemoasr_debug_tokens(const nemoasr_t *s, size_t *n) {
     *n = s->n_tok;
     return s->all_tok;
 }
-void nemoasr_debug_set_dump(nemoasr_t *s, int on) { encoder_set_dump(s->enc, on); }
+void nemoasr_debug_set_dump(nemoasr_t *s, int on) {
+    s->dump = on;
+    encoder_set_dump(s->enc, on);
+}
+const float *nemoasr_debug_dump_mel(const nemoasr_t *s, size_t *nframes) {
+    *nframes = s->n_mel_dump;
+    return s->mel_dump;
+}
 size_t nemoasr_debug_frames(const nemoasr_t *s) { return encoder_dump_frames(s->enc); }
 const float *nemoasr_debug_dump_layers(const nemoasr_t *s) { return encoder_dump_layers(s->enc); }
 const float *nemoasr_debug_dump_prompted(const nemoasr_t *s) { return encoder_dump_prompted(s->enc); }

@@ -66,6 +66,7 @@ API = {
     "nemoasr_debug_frames": (C.c_size_t, [_vp]),
     "nemoasr_debug_dump_layers": (_f32p, [_vp]),
     "nemoasr_debug_dump_prompted": (_f32p, [_vp]),
+    "nemoasr_debug_dump_mel": (_f32p, [_vp, C.POINTER(C.c_size_t)]),
     "nemoasr_debug_dump_joint_enc": (_f32p, [_vp]),
     "nemoasr_debug_use_graphs": (None, [_vp, C.c_int]),
     "nemoasr_debug_fuse": (None, [_vp, C.c_int]),
@@ -314,6 +315,14 @@ class Session:
         pr = np.ctypeslib.as_array(lib().nemoasr_debug_dump_prompted(self.h), shape=(F * d_model,))
         je = np.ctypeslib.as_array(lib().nemoasr_debug_dump_joint_enc(self.h), shape=(F * joint_hidden,))
         return (lay.reshape(F, n_layers, d_model).copy(), pr.reshape(F, d_model).copy(), je.reshape(F, joint_hidden).copy())
+
+    def mel_dump(self) -> np.ndarray:
+        """Log-mel frames (n, 128) the front end produced from fed audio while dumps were on."""
+        n = C.c_size_t()
+        p = lib().nemoasr_debug_dump_mel(self.h, C.byref(n))
+        if not n.value:
+            return np.zeros((0, 128), np.float32)
+        return np.ctypeslib.as_array(p, shape=(n.value * 128,)).reshape(n.value, 128).copy()
 
     def stats(self) -> dict:
         class St(C.Structure):

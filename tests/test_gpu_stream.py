@@ -7,6 +7,9 @@ through its CPU restatement.  Gates (from the scope of this path):
   - joint.enc rows (the joint's encoder input): <= 1e-3; joint logits are checked per kernel;
   - emitted token ids: identical.
 """
+import os
+import wave
+
 import numpy as np
 import pytest
 
@@ -142,3 +145,40 @@ def test_reset_replays_identically():
     s.feed_mel(mel, final=True)
     assert s.tokens() == o.tokens
     s.close()
+
+
+@pytest.mark.parametrize("latency", [80, 560])
+def test_parity_harness_end_to_end(tmp_path, latency):
+    """The real-checkpoint harness (parity.py: WAV in, CLI-format dumps out, compare.py gates) on a
+    synthetic checkpoint, against a reference directory in the MLX dump format that the oracle
+    writes from the same WAV samples."""
+    import parity
+
+    mdir = model_dir("tiny")
+    pcm = np.clip(np.round(synth.make_audio(2.5, seed=21) * 32768), -32768, 32767).astype(np.int16)
+    wav = str(tmp_path / "in.wav")
+    with wave.open(wav, "wb") as w:
+        w.setnchannels(1)
+        w.setsampwidth(2)
+        w.setframerate(16000)
+        w.writeframes(pcm.tobytes())
+    x = pcm.astype(np.float32) / np.float32(32768)
+    om = oracle.Model(mdir, "en-US")
+    o = oracle.Session(om, LAT_RIGHT[latency], dump=True)
+    mel = mel_ref.logmel(x)
+    o.feed_mel(mel, final=True)
+    _, prompted, _, _ = o.dumps()
+    ref = str(tmp_path / "ref")
+    os.makedirs(ref)
+    mel.astype(np.float32).tofile(os.path.join(ref, "mel.f32"))
+    prompted.astype(np.float32).tofile(os.path.join(ref, "enc_all.f32"))
+    with open(os.path.join(ref, "tokens.txt"), "w") as f:
+        f.write(" ".join(map(str, o.tokens)) + "\n\n")
+
+    res = parity.run(mdir, wav, latency)
+    out = str(tmp_path / "out")
+    parity.write_dumps(out, res["mel"], res["enc"], res["tokens"])
+    ok, rep = parity.compare(ref, out, om.dims.d_model)
+    print("\n".join(rep))
+    assert ok, rep
+    assert res["mel"].shape == mel.shape and len(o.tokens) > 0
