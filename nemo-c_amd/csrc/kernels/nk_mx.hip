@@ -12,8 +12,7 @@
  * for a stage's loads right before the barrier that publishes it.  A DMA instruction writes 64
  * consecutive 16-byte LDS granules in lane order; the global address each lane reads is chosen so
  * that granule g of row r holds K-granule (g ^ swizzle(r)), which makes the 16-row fragment reads
- * (ds_read_b128) hit distinct banks (swz_a / swz_b below; measured: the plain r % 8 swizzle left
- * half the accesses conflicting and cost a third of the kernel time at 3584 rows).
+ * (ds_read_b128) hit distinct banks (swz_a / swz_b below).
  *
  * A is f32 in memory and in LDS; each fragment (8 consecutive K of one row per lane) is split in
  * registers into bf16 hi = RNE(a) and lo = RNE(a - hi) (v_cvt_pk_bf16_f32), and every K step
@@ -29,15 +28,18 @@
  * no activation). */
 #include "nk_common.h"
 
-/* LDS granule swizzles.  A 16-byte fragment read of 16 consecutive rows at one K granule is
- * served 16 lanes per cycle (64 banks): granule g of row r lives in slot g ^ swz(r), chosen so the
- * 16 rows land in 16 different bank groups (and 8 consecutive rows in 8, for 8-lane service).
- * A rows hold 8 granules (K stage 32) or 16 (64); W rows 4 or 8. */
+/* LDS granule swizzles: granule g of row r lives in slot g ^ swz(r).  A fragment read is one
+ * ds_read_b128 per lane over 16 consecutive rows at one K granule (lanes 16 f .. 16 f + 15).  The
+ * K-stage-32 forms (A rows of 8 granules, W rows of 4) were chosen by the SQ_LDS_BANK_CONFLICT
+ * counter on gfx950 over candidate functions: these two read with zero conflict cycles, where
+ * the earlier ((r>>1)&7)^((r&1)<<2) and ((n>>1)&3)^((n>>3)&1) cost 4 extra cycles per read (a
+ * 2-way conflict; 1-3% of kernel time) and the plain r % 8 cost a third of the kernel time at
+ * 3584 rows.  The K-stage-64 forms (16 and 8 granules per row) are unmeasured by the counter. */
 __device__ __forceinline__ u32 swz_a(u32 r, int ag) {
-    return ag == 16 ? (r & 15) : (((r >> 1) & 7) ^ ((r & 1) << 2));
+    return ag == 16 ? (r & 15) : ((r & 7) ^ ((r >> 3) & 1));
 }
 __device__ __forceinline__ u32 swz_b(u32 n, int bg) {
-    return bg == 4 ? (((n >> 1) & 3) ^ ((n >> 3) & 1)) : (((n >> 1) & 7) ^ ((n & 1) << 2));
+    return bg == 4 ? ((n >> 1) & 3) : (((n >> 1) & 7) ^ ((n & 1) << 2));
 }
 
 template <int BM, int BN, int WGM, int NS, int KS, bool GLU, int EPI = 0>
