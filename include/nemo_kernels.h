@@ -152,6 +152,12 @@ int nk_conv2d_c1_s2_relu_b(gpu_t *g, const float *X, const float *W, const float
 int nk_dwconv2d_s2_b(gpu_t *g, const float *X, const float *W, const float *bias, float *Y, uint32_t T, uint32_t F,
                      uint32_t T1, uint32_t F1, uint32_t C, uint32_t batch);
 int nk_flatten_cf_b(gpu_t *g, const float *X, float *Y, uint32_t T, uint32_t F, uint32_t C, uint32_t batch);
+/* conv 0 + ReLU and conv 2 in one pass (src/encoder.c:124-130, kernels.metal:411-454): X [T][F]
+   -> Y [T2][F2][C] per window, equal to nk_conv2d_c1_s2_relu_b then nk_dwconv2d_s2_b without
+   conv 0's [T1][F1][C] output.  F <= 256. */
+int nk_conv2d_c1_dw_s2_b(gpu_t *g, const float *X, const float *W0, const float *b0, const float *W2,
+                         const float *b2, float *Y, uint32_t T, uint32_t F, uint32_t T1, uint32_t F1, uint32_t T2,
+                         uint32_t F2, uint32_t C, uint32_t batch);
 /* dst[m] = src[map[m]] for m < rows (cols floats per row) */
 int nk_gather_rows(gpu_t *g, const float *src, uint32_t src_ld, const int *map, float *dst, uint32_t dst_ld,
                    uint32_t rows, uint32_t cols);

@@ -120,7 +120,7 @@ struct nemoasr_batch {
     size_t hrow_cap, hrow_n;       /* floats of mel rows given by the host (push_mel) */
     size_t hmap_cap, wmap_cap;     /* ints */
     /* encoder */
-    gpu_buf_t *win, *c0, *c1, *c2, *c3, *c4, *flat, *pre_out;
+    gpu_buf_t *win, *c1, *c2, *c3, *c4, *flat, *pre_out;
     gpu_buf_t *h, *tmp, *lnb, *ff, *att, *y, *ph, *prompted, *joint_enc, *kv, *din, *etab;
     size_t kv_lstride, din_lstride;
     float *stage_win;
@@ -150,6 +150,12 @@ struct nemoasr_batch {
     pthread_mutex_t dmu;
     pthread_cond_t dcv;
     int dstarted, dquit, dstate, drc; /* dstate: 0 idle, 1 queued, 2 running */
+    /* Held by the worker while it captures a graph of the loop, and by the caller's thread for the
+     * whole encoder part of a step (its own capture, staging allocations, synchronous copies):
+     * a capture on one thread never overlaps allocations, synchronous copies or a capture on the
+     * other.  Without it, a staging allocation of the encoder step that met the worker's first
+     * capture failed now and then, and some steps decoded other tokens. */
+    pthread_mutex_t cmu;
     char derr[256];
     int dnact, *dorder, *dc, *drow0, dbuf;
     double dt0;
@@ -450,7 +456,6 @@ nemoasr_batch_t *nemoasr_batch_open(const char *model_dir, const char *language,
     const size_t Mm = (size_t)b->Mmax;
     gpu_t *g = b->g;
     b->win = gpu_buf_alloc(g, S * (size_t)b->nwin_max * F * fs);
-    b->c0 = gpu_buf_alloc(g, S * (size_t)b->T1max * b->F1 * CH * fs);
     b->c1 = gpu_buf_alloc(g, S * (size_t)b->T2max * b->F2 * CH * fs);
     b->c2 = gpu_buf_alloc(g, S * (size_t)b->T2max * b->F2 * CH * fs);
     b->c3 = gpu_buf_alloc(g, S * (size_t)b->T3max * b->F3 * CH * fs);
@@ -560,7 +565,7 @@ void nemoasr_batch_close(nemoasr_batch_t *b) {
     pool_stop(&b->pool);
     free(b->fe_list);
     drop_graphs(b);
-    gpu_buf_t *bufs[] = { b->win, b->c0, b->c1, b->c2, b->c3, b->c4, b->flat, b->pre_out, b->h, b->tmp, b->lnb,
+    gpu_buf_t *bufs[] = { b->win, b->c1, b->c2, b->c3, b->c4, b->flat, b->pre_out, b->h, b->tmp, b->lnb,
                           b->ff, b->att, b->y, b->ph, b->prompted, b->joint_enc, b->kv, b->din, b->etab, b->wcat[0],
                           b->wcat[1], b->wout, b->bout, b->hc, b->lin, b->gates, b->hout, b->hout2, b->pred,
                           b->jin, b->logits, b->amax, b->dtab, b->bst, b->bsetup, b->btok, b->lin1, b->tx,
@@ -870,10 +875,11 @@ static void launch_pre_encode(nemoasr_batch_t *b, const float *win, int nwin, in
     const uint32_t CH = (uint32_t)m->cfg.sub_channels, F = (uint32_t)m->cfg.feat_in, n = (uint32_t)cnt;
     const uint32_t T1 = (uint32_t)sub_len(nwin), F1 = F / 2 + 1, T2 = T1 / 2 + 1, F2 = F1 / 2 + 1, T3 = T2 / 2 + 1,
                    F3 = F2 / 2 + 1;
-    float *c0 = gpu_buf_dptr(b->c0), *c1 = gpu_buf_dptr(b->c1), *c2 = gpu_buf_dptr(b->c2), *c3 = gpu_buf_dptr(b->c3);
+    float *c1 = gpu_buf_dptr(b->c1), *c2 = gpu_buf_dptr(b->c2), *c3 = gpu_buf_dptr(b->c3);
     float *c4 = gpu_buf_dptr(b->c4), *flat = gpu_buf_dptr(b->flat);
-    nk_conv2d_c1_s2_relu_b(g, win, m->conv0_w, m->conv0_b, c0, (uint32_t)nwin, F, T1, F1, CH, n);
-    nk_dwconv2d_s2_b(g, c0, m->conv2_w, m->conv2_b, c1, T1, F1, T2, F2, CH, n);
+    /* conv 0 + ReLU and the first depthwise conv in one launch (conv 0's output is not stored) */
+    nk_conv2d_c1_dw_s2_b(g, win, m->conv0_w, m->conv0_b, m->conv2_w, m->conv2_b, c1, (uint32_t)nwin, F, T1, F1, T2,
+                         F2, CH, n);
     nk_gemm(g, c1, CH, m->conv3_w, CH, m->conv3_b, c2, CH, n * T2 * F2, CH, CH, NK_ACT_RELU, 0, 1.0f);
     nk_dwconv2d_s2_b(g, c2, m->conv5_w, m->conv5_b, c3, T2, F2, T3, F3, CH, n);
     nk_gemm(g, c3, CH, m->conv6_w, CH, m->conv6_b, c4, CH, n * T3 * F3, CH, CH, NK_ACT_RELU, 0, 1.0f);
@@ -1325,9 +1331,13 @@ static int decoder_batch_device(nemoasr_batch_t *b, char *err, size_t errlen) {
             gpu_upload_async(g, gpu_buf_dptr(b->bcnt), su + 2 * S, 2 * sizeof(int)); /* zero row counters */
             gpu_launch(g, "bdec_setup", &a, sizeof a, (uint32_t)S, 1, 1, 64, 1, 1);
         }
-        if (b->use_graphs && !b->dgraph[b->dbuf] && !gpu_capture_begin(g)) {
-            launch_bdec_steps(b, BDEC_STEPS);
-            b->dgraph[b->dbuf] = gpu_capture_end(g);
+        if (b->use_graphs && !b->dgraph[b->dbuf]) {
+            if (b->dstarted) pthread_mutex_lock(&b->cmu);
+            if (!gpu_capture_begin(g)) {
+                launch_bdec_steps(b, BDEC_STEPS);
+                b->dgraph[b->dbuf] = gpu_capture_end(g);
+            }
+            if (b->dstarted) pthread_mutex_unlock(&b->cmu);
         }
         if (b->dgraph[b->dbuf]) gpu_graph_launch(g, b->dgraph[b->dbuf]);
         else launch_bdec_steps(b, BDEC_STEPS);
@@ -1401,9 +1411,11 @@ static int dec_drain(const nemoasr_batch_t *cb, char *err, size_t errlen) {
 
 static int dec_start(nemoasr_batch_t *b) {
     pthread_mutex_init(&b->dmu, NULL);
+    pthread_mutex_init(&b->cmu, NULL);
     pthread_cond_init(&b->dcv, NULL);
     if (pthread_create(&b->dth, NULL, dec_main, b)) {
         pthread_mutex_destroy(&b->dmu);
+        pthread_mutex_destroy(&b->cmu);
         pthread_cond_destroy(&b->dcv);
         return -1;
     }
@@ -1420,16 +1432,44 @@ static void dec_stop(nemoasr_batch_t *b) {
     pthread_mutex_unlock(&b->dmu);
     pthread_join(b->dth, NULL);
     pthread_mutex_destroy(&b->dmu);
+    pthread_mutex_destroy(&b->cmu);
     pthread_cond_destroy(&b->dcv);
     b->dstarted = 0;
+}
+
+/* debug dumps: the step's joint.enc rows, appended per stream */
+static int step_dump(nemoasr_batch_t *b, int M, char *err, size_t errlen) {
+    if (!b->dump) return 0;
+    const size_t J = (size_t)b->J;
+    float *all = malloc((size_t)M * J * sizeof(float));
+    if (gpu_download(b->g, all, gpu_buf_dptr(b->joint_enc), (size_t)M * J * sizeof(float))) {
+        free(all);
+        snprintf(err, errlen, "batch: dump download failed");
+        return -1;
+    }
+    for (int s = 0; s < b->S; ++s) {
+        const bstream_t *x = &b->st[s];
+        if (x->c <= 0) continue;
+        if (b->dj_n[s] + (size_t)x->c > b->dj_cap[s]) {
+            b->dj_cap[s] = (b->dj_n[s] + (size_t)x->c) * 2 + 64;
+            b->dj[s] = realloc(b->dj[s], b->dj_cap[s] * J * sizeof(float));
+        }
+        memcpy(b->dj[s] + b->dj_n[s] * J, all + (size_t)x->row0 * J, (size_t)x->c * J * sizeof(float));
+        b->dj_n[s] += (size_t)x->c;
+    }
+    free(all);
+    return 0;
 }
 
 int nemoasr_batch_step(nemoasr_batch_t *b, char *err, size_t errlen) {
     if (errlen) err[0] = 0;
     const double t0 = now_ms();
     int M = 0;
+    if (b->dstarted) pthread_mutex_lock(&b->cmu);
     const int consumed = encoder_batch_step(b, &M, err, errlen);
-    if (consumed < 0) return -1;
+    const int rc = consumed < 0 || !M ? 0 : step_dump(b, M, err, errlen);
+    if (b->dstarted) pthread_mutex_unlock(&b->cmu);
+    if (consumed < 0 || rc) return -1;
     if (!M) return consumed;
     const double t1 = now_ms();
     int nact = 0;
@@ -1445,26 +1485,6 @@ int nemoasr_batch_step(nemoasr_batch_t *b, char *err, size_t errlen) {
         x->t = 0;
         x->symbols = 0;
         x->erow0 = x->row0;
-    }
-    if (b->dump) {
-        const size_t J = (size_t)b->J;
-        float *all = malloc((size_t)M * J * sizeof(float));
-        if (gpu_download(b->g, all, gpu_buf_dptr(b->joint_enc), (size_t)M * J * sizeof(float))) {
-            free(all);
-            snprintf(err, errlen, "batch: dump download failed");
-            return -1;
-        }
-        for (int i = 0; i < nact; ++i) {
-            const int s = b->order[i];
-            const bstream_t *x = &b->st[s];
-            if (b->dj_n[s] + (size_t)x->c > b->dj_cap[s]) {
-                b->dj_cap[s] = (b->dj_n[s] + (size_t)x->c) * 2 + 64;
-                b->dj[s] = realloc(b->dj[s], b->dj_cap[s] * J * sizeof(float));
-            }
-            memcpy(b->dj[s] + b->dj_n[s] * J, all + (size_t)x->row0 * J, (size_t)x->c * J * sizeof(float));
-            b->dj_n[s] += (size_t)x->c;
-        }
-        free(all);
     }
     b->stats.steps++;
     b->stats.chunks += (size_t)nact;

@@ -46,7 +46,7 @@ struct encoder {
     size_t consumed, emitted;
     int closed;
     /* device buffers */
-    gpu_buf_t *win, *c0, *c1, *c2, *c3, *c4, *flat;
+    gpu_buf_t *win, *c1, *c2, *c3, *c4, *flat;
     gpu_buf_t *h, *tmp, *t2, *ff, *att, *y, *ph, *prompted, *joint_enc;
     gpu_buf_t *kv, *din, *desc;
     size_t kv_stride, din_stride; /* floats per layer */
@@ -87,7 +87,6 @@ encoder_t *encoder_create(model_t *m, int right) {
     gpu_t *g = e->g;
     const size_t cm = (size_t)e->cmax, fs = sizeof(float);
     e->win = gpu_buf_alloc(g, nwin * F * fs);
-    e->c0 = gpu_buf_alloc(g, T1 * F1 * CH * fs);
     e->c1 = gpu_buf_alloc(g, T2 * F2 * CH * fs);
     e->c2 = gpu_buf_alloc(g, T2 * F2 * CH * fs);
     e->c3 = gpu_buf_alloc(g, T3 * F3 * CH * fs);
@@ -126,7 +125,7 @@ static void drop_graphs(encoder_t *e) {
 void encoder_destroy(encoder_t *e) {
     if (!e) return;
     drop_graphs(e);
-    gpu_buf_t *bufs[] = { e->win, e->c0, e->c1, e->c2, e->c3, e->c4, e->flat, e->h, e->tmp, e->t2, e->ff,
+    gpu_buf_t *bufs[] = { e->win, e->c1, e->c2, e->c3, e->c4, e->flat, e->h, e->tmp, e->t2, e->ff,
                           e->att, e->y, e->ph, e->prompted, e->joint_enc, e->kv, e->din, e->desc, e->dump_dev };
     for (size_t i = 0; i < sizeof bufs / sizeof *bufs; ++i) gpu_buf_free(bufs[i]);
     gpu_host_free(e->stage_win);
@@ -230,10 +229,11 @@ static void run_pre_encode(encoder_t *e, int nwin, int lo, int c) {
     gpu_t *g = e->g;
     const uint32_t CH = (uint32_t)m->cfg.sub_channels, F = (uint32_t)m->cfg.feat_in;
     const uint32_t T1 = (uint32_t)sub_len(nwin), F1 = F / 2 + 1, T2 = T1 / 2 + 1, F2 = F1 / 2 + 1, T3 = T2 / 2 + 1, F3 = F2 / 2 + 1;
-    float *win = gpu_buf_dptr(e->win), *c0 = gpu_buf_dptr(e->c0), *c1 = gpu_buf_dptr(e->c1), *c2 = gpu_buf_dptr(e->c2);
+    float *win = gpu_buf_dptr(e->win), *c1 = gpu_buf_dptr(e->c1), *c2 = gpu_buf_dptr(e->c2);
     float *c3 = gpu_buf_dptr(e->c3), *c4 = gpu_buf_dptr(e->c4), *flat = gpu_buf_dptr(e->flat);
-    nk_conv2d_c1_s2_relu(g, win, m->conv0_w, m->conv0_b, c0, (uint32_t)nwin, F, T1, F1, CH);
-    nk_dwconv2d_s2(g, c0, m->conv2_w, m->conv2_b, c1, T1, F1, T2, F2, CH);
+    /* conv 0 + ReLU and the first depthwise conv in one launch (conv 0's output is not stored) */
+    nk_conv2d_c1_dw_s2_b(g, win, m->conv0_w, m->conv0_b, m->conv2_w, m->conv2_b, c1, (uint32_t)nwin, F, T1, F1, T2,
+                         F2, CH, 1);
     nk_gemm(g, c1, CH, m->conv3_w, CH, m->conv3_b, c2, CH, T2 * F2, CH, CH, NK_ACT_RELU, 0, 1.0f);
     nk_dwconv2d_s2(g, c2, m->conv5_w, m->conv5_b, c3, T2, F2, T3, F3, CH);
     nk_gemm(g, c3, CH, m->conv6_w, CH, m->conv6_b, c4, CH, T3 * F3, CH, CH, NK_ACT_RELU, 0, 1.0f);

@@ -449,6 +449,17 @@ int nk_dwconv2d_s2_b(gpu_t *g, const float *X, const float *W, const float *bias
     return gpu_launch(g, "dwconv2d_s2", &a, sizeof a, T1 * ((F1 + fb - 1) / fb), batch, 1, 256, 1, 1);
 }
 
+int nk_conv2d_c1_dw_s2_b(gpu_t *g, const float *X, const float *W0, const float *b0, const float *W2,
+                         const float *b2, float *Y, uint32_t T, uint32_t F, uint32_t T1, uint32_t F1, uint32_t T2,
+                         uint32_t F2, uint32_t C, uint32_t batch) {
+    if (F > NK_CONV02_FMAX) return gpu_fail(g, "nk_conv2d_c1_dw_s2: more than 256 mel bins");
+    if (!T2 || !F2 || !batch) return 0;
+    /* whole output rows per workgroup when there are enough rows to fill the GPU */
+    const uint32_t fb = (uint64_t)T2 * batch >= 1024 ? F2 : 4;
+    NkConv02Args a = { X, W0, b0, W2, b2, Y, T, F, T1, F1, T2, F2, C, fb, T * F, T2 * F2 * C };
+    return gpu_launch(g, "conv2d_c1_dw_s2", &a, sizeof a, T2 * ((F2 + fb - 1) / fb), batch, 1, 256, 1, 1);
+}
+
 int nk_mel_frames(gpu_t *g, const float *span, const int *tab, uint32_t F, const float *win, const float *fb,
                   const int *fb_lo, const int *fb_hi, const double *tw_re, const double *tw_im, const uint16_t *rev,
                   float *out) {

@@ -177,6 +177,17 @@ typedef struct {
     u32 xs, ys;
 } NkConvArgs;
 
+/* conv 0 and conv 2 of the subsampling in one pass: X [T][F] -> Y [T2][F2][C], conv 0's
+ * [T1][F1][C] output never stored.  grid.x = T2 * ceil(F2 / fb), grid.y = windows (xs / ys floats
+ * apart); F <= NK_CONV02_FMAX. */
+#define NK_CONV02_FMAX 256
+typedef struct {
+    const float *X, *W0, *b0, *W2, *b2;
+    float *Y;
+    u32 T, F, T1, F1, T2, F2, C, fb;
+    u32 xs, ys;
+} NkConv02Args;
+
 typedef struct {
     const float *X;
     float *Y;

@@ -68,6 +68,79 @@ extern "C" __global__ __launch_bounds__(256) void dwconv2d_s2(NkConvArgs a) {
     }
 }
 
+/* conv 0 (1 -> C channels + ReLU) followed by conv 2 (depthwise, + bias) without storing conv 0's
+ * output: X [T][F] -> Y [T2][F2][C].  Workgroup = one output row t2 and fb output columns of one
+ * window; thread = channel.  The seven X rows the output row reads (4 t2 - 6 .. 4 t2) are staged
+ * in LDS.  Every conv 0 value is computed exactly as conv2d_c1_s2_relu computes it (bias, then the
+ * taps in (kh, kw) order, taps outside X skipped, ReLU) and every output exactly as dwconv2d_s2
+ * computes it (bias, then the taps in order, positions outside conv 0's T1 x F1 skipped), so the
+ * result equals the two kernels' bit for bit.  A thread walks its columns left to right; the conv
+ * 0 column 2 f2 of output f2 is column 2 (f2 + 1) - 2 of the next, and is kept. */
+extern "C" __global__ __launch_bounds__(256) void conv2d_c1_dw_s2(NkConv02Args a) {
+    __shared__ float xs[7][NK_CONV02_FMAX];
+    const u32 nfb = (a.F2 + a.fb - 1) / a.fb;
+    const u32 t2 = blockIdx.x / nfb, f0 = (blockIdx.x % nfb) * a.fb;
+    const float *X = a.X + (u64)blockIdx.y * a.xs;
+    float *Y = a.Y + (u64)blockIdx.y * a.ys;
+    const u32 fe = min(f0 + a.fb, a.F2);
+    const int ti0 = 4 * (int)t2 - 6; /* X row of LDS row 0 */
+    for (u32 i = threadIdx.x; i < 7 * a.F; i += 256) {
+        const int r = (int)(i / a.F), ti = ti0 + r;
+        xs[r][i % a.F] = (ti >= 0 && ti < (int)a.T) ? X[(u64)ti * a.F + i % a.F] : 0.0f;
+    }
+    __syncthreads();
+    for (u32 c = threadIdx.x; c < a.C; c += 256) {
+        float w0[9], w2[9];
+#pragma unroll
+        for (int k = 0; k < 9; ++k) {
+            w0[k] = a.W0[c * 9 + k];
+            w2[k] = a.W2[c * 9 + k];
+        }
+        const float bias0 = a.b0[c], bias2 = a.b2[c];
+        /* conv 0 at (t1, f1) = (2 t2 + kh2 - 2, f1); ok = inside conv 0's output */
+        auto conv0 = [&](int kh2, int f1, bool &ok) -> float {
+            const int t1 = 2 * (int)t2 + kh2 - 2;
+            ok = t1 >= 0 && t1 < (int)a.T1 && f1 >= 0 && f1 < (int)a.F1;
+            if (!ok) return 0.0f;
+            float acc = bias0;
+#pragma unroll
+            for (int kh = 0; kh < 3; ++kh) {
+                const int ti = 2 * t1 + kh - 2;
+                if (ti < 0 || ti >= (int)a.T) continue;
+#pragma unroll
+                for (int kw = 0; kw < 3; ++kw) {
+                    const int fi = 2 * f1 + kw - 2;
+                    if (fi < 0 || fi >= (int)a.F) continue;
+                    acc += w0[kh * 3 + kw] * xs[ti - ti0][fi];
+                }
+            }
+            return fmaxf(acc, 0.0f);
+        };
+        float keep[3];
+        bool keep_ok[3];
+        for (u32 f2 = f0; f2 < fe; ++f2) {
+            float v[3][3];
+            bool ok[3][3];
+#pragma unroll
+            for (int kh2 = 0; kh2 < 3; ++kh2) {
+                if (f2 == f0) v[kh2][0] = conv0(kh2, 2 * (int)f2 - 2, ok[kh2][0]);
+                else { v[kh2][0] = keep[kh2]; ok[kh2][0] = keep_ok[kh2]; }
+                v[kh2][1] = conv0(kh2, 2 * (int)f2 - 1, ok[kh2][1]);
+                v[kh2][2] = conv0(kh2, 2 * (int)f2, ok[kh2][2]);
+                keep[kh2] = v[kh2][2];
+                keep_ok[kh2] = ok[kh2][2];
+            }
+            float acc = bias2;
+#pragma unroll
+            for (int kh2 = 0; kh2 < 3; ++kh2)
+#pragma unroll
+                for (int kw2 = 0; kw2 < 3; ++kw2)
+                    if (ok[kh2][kw2]) acc += w2[kh2 * 3 + kw2] * v[kh2][kw2];
+            Y[((u64)t2 * a.F2 + f2) * a.C + c] = acc;
+        }
+    }
+}
+
 /* Log-mel of one 512-sample frame per workgroup (reference src/mel.c:115-173, the host front end's
  * computation step for step): window, radix-2 decimation-in-time FFT in double (bit-reversed load,
  * nine stages of 256 butterflies, one per thread, with the host's twiddle table and operation

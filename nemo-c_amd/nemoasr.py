@@ -137,6 +137,7 @@ API = {
     "nk_dwconv_ln_silu_rows": (C.c_int, [_vp, _vp, _vp, _u32, _vp, _vp, _vp, _vp, _u32, _u32, C.c_float]),
     "nk_conv2d_c1_s2_relu_b": (C.c_int, [_vp, _vp, _vp, _vp, _vp] + [_u32] * 6),
     "nk_dwconv2d_s2_b": (C.c_int, [_vp, _vp, _vp, _vp, _vp] + [_u32] * 6),
+    "nk_conv2d_c1_dw_s2_b": (C.c_int, [_vp] * 7 + [_u32] * 8),
     "nk_flatten_cf_b": (C.c_int, [_vp, _vp, _vp, _u32, _u32, _u32, _u32]),
     "nk_gather_rows": (C.c_int, [_vp, _vp, _u32, _vp, _vp, _u32, _u32, _u32]),
     "nk_lstm_cell": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _u32]),

@@ -545,6 +545,39 @@ def test_subsampling_convs(gpu, nwin):
     np.testing.assert_array_equal(dfl.read(fl.shape), oracle.flatten_cf(dy1.read(y1.shape)))
 
 
+@pytest.mark.parametrize("nwin,batch,F,C", [(9, 1, 128, 256), (23, 3, 128, 256), (61, 2, 128, 256),
+                                          (121, 40, 128, 256), (128, 9, 128, 256), (17, 2, 80, 96)])
+def test_subsampling_conv02_fused(gpu, nwin, batch, F, C):
+    """conv 0 + conv 2 in one launch equals the two launches bit for bit (and the oracle), with
+    whole-row and 4-column workgroups (the launcher picks by rows x windows)."""
+    import nemoasr
+
+    lib = nemoasr.lib()
+    rng = np.random.default_rng(nwin * 7 + batch)
+    X = rng.standard_normal((batch, nwin, F)).astype(np.float32)
+    W0 = (rng.standard_normal((C, 9)) / 3).astype(np.float32)
+    b0 = (0.1 * rng.standard_normal(C)).astype(np.float32)
+    W2 = (rng.standard_normal((C, 9)) / 3).astype(np.float32)
+    b2 = (0.1 * rng.standard_normal(C)).astype(np.float32)
+    T1, F1 = nwin // 2 + 1, F // 2 + 1
+    T2, F2 = T1 // 2 + 1, F1 // 2 + 1
+    dX, dW0, db0, dW2, db2 = gpu.put(X), gpu.put(W0), gpu.put(b0), gpu.put(W2), gpu.put(b2)
+    dy0 = gpu.alloc(batch * T1 * F1 * C * 4)
+    dy1, dyf = gpu.alloc(batch * T2 * F2 * C * 4), gpu.alloc(batch * T2 * F2 * C * 4)
+    gpu.begin()
+    gpu.check(lib.nk_conv2d_c1_s2_relu_b(gpu.h, dX.ptr, dW0.ptr, db0.ptr, dy0.ptr, nwin, F, T1, F1, C, batch))
+    gpu.check(lib.nk_dwconv2d_s2_b(gpu.h, dy0.ptr, dW2.ptr, db2.ptr, dy1.ptr, T1, F1, T2, F2, C, batch))
+    gpu.check(lib.nk_conv2d_c1_dw_s2_b(gpu.h, dX.ptr, dW0.ptr, db0.ptr, dW2.ptr, db2.ptr, dyf.ptr, nwin, F, T1, F1,
+                                       T2, F2, C, batch))
+    gpu.end()
+    sep, fused = dy1.read((batch, T2, F2, C)), dyf.read((batch, T2, F2, C))
+    np.testing.assert_array_equal(fused, sep)
+    for w in range(batch):
+        ref = oracle.dwconv2d_s2(oracle.conv2d_c1_s2_relu(X[w], W0, b0), W2, b2)
+        assert ref.shape == (T2, F2, C)
+        assert rel_err(fused[w], ref) < 1e-6
+
+
 def test_lstm_cell(gpu):
     import nemoasr
 
