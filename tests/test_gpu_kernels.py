@@ -546,10 +546,11 @@ def test_subsampling_convs(gpu, nwin):
 
 
 @pytest.mark.parametrize("nwin,batch,F,C", [(9, 1, 128, 256), (23, 3, 128, 256), (61, 2, 128, 256),
-                                          (121, 40, 128, 256), (128, 9, 128, 256), (17, 2, 80, 96)])
+                                          (121, 40, 128, 256), (128, 9, 128, 256), (121, 12, 128, 256),
+                                          (17, 2, 80, 96)])
 def test_subsampling_conv02_fused(gpu, nwin, batch, F, C):
     """conv 0 + conv 2 in one launch equals the two launches bit for bit (and the oracle), with
-    whole-row and 4-column workgroups (the launcher picks by rows x windows)."""
+    whole-row, 4-column and 1-column workgroups (the launcher picks by rows x windows)."""
     import nemoasr
 
     lib = nemoasr.lib()
