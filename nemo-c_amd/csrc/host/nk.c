@@ -294,8 +294,13 @@ int nk_layernorm2(gpu_t *g, const float *X, const float *g1, const float *b1, co
     if (!M) return 0;
     if (D > NK_ROW_MAX || D % 4) return bad(g, "layernorm: D must be a multiple of 4, at most 4096");
     NkLnArgs a = { X, g1, b1, g2, b2, Y1, Y2, M, D, eps, 0 };
-    /* many rows: one wavefront per row (D <= 1024), no barriers */
-    if (M > 16 && D <= 1024) return gpu_launch(g, "layernorm_rows", &a, sizeof a, (M + 3) / 4, 1, 1, 256, 1, 1);
+    /* many rows: a wavefront per row (D <= 1024), no barriers; 2 or 4 rows per wavefront from
+     * 1024 / 2048 rows */
+    if (M > 16 && D <= 1024) {
+        const uint32_t R = M >= 2048 ? 4 : M >= 1024 ? 2 : 1, W = (M + R - 1) / R;
+        return gpu_launch(g, R == 4 ? "layernorm_rows_r4" : R == 2 ? "layernorm_rows_r2" : "layernorm_rows", &a,
+                          sizeof a, (W + 3) / 4, 1, 1, 256, 1, 1);
+    }
     return gpu_launch(g, "layernorm", &a, sizeof a, M, 1, 1, NK_LN_THREADS, 1, 1);
 }
 

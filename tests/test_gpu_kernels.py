@@ -251,7 +251,8 @@ def test_gemm_row_scatter(gpu, M):
     np.testing.assert_array_equal(got[40 + M:], C0[40 + M:])
 
 
-@pytest.mark.parametrize("M,D", [(1, 1024), (7, 1024), (16, 1024), (3, 256), (17, 1024), (448, 1024), (3585, 1024),
+@pytest.mark.parametrize("M,D", [(1, 1024), (7, 1024), (16, 1024), (3, 256), (17, 1024), (448, 1024), (1101, 1024),
+                                 (2050, 1024), (2049, 640), (3585, 1024),
                                  (50, 640), (33, 64)])
 def test_layernorm_and_pair(gpu, M, D):
     import nemoasr
