@@ -244,7 +244,13 @@ static void *upf_reader(void *arg) {
         while (got < p->bytes) {
             const ssize_t r = pread(u->fd, buf + got, (size_t)(p->bytes - got), (off_t)(p->off + got));
             if (r < 0 && errno == EINTR) continue;
-            if (r <= 0) { upf_error(u, r < 0 ? strerror(errno) : "file shorter than its header says"); return NULL; }
+            if (r <= 0) {
+                char msg[96];
+                if (r < 0) snprintf(msg, sizeof msg, "weight file read failed (errno %d)", errno);
+                else snprintf(msg, sizeof msg, "weight file shorter than its header says");
+                upf_error(u, msg);
+                return NULL;
+            }
             got += (uint64_t)r;
         }
         if ((e = hipMemcpyAsync(p->dst, buf, p->bytes, hipMemcpyHostToDevice, u->g->stream)) != hipSuccess ||
@@ -264,6 +270,7 @@ int gpu_upload_file(gpu_t *g, int fd, const gpu_file_range_t *ranges, size_t n) 
     if (!npc) return 0;
     upf_t u = { .g = g, .fd = fd, .npc = npc };
     upf_piece_t *pc = malloc(npc * sizeof *pc);
+    if (!pc) return gpu_fail(g, "upload_file: out of host memory");
     size_t j = 0;
     for (size_t i = 0; i < n; ++i)
         for (uint64_t o = 0; o < ranges[i].bytes; o += UPF_PIECE) {
