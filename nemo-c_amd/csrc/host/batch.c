@@ -431,7 +431,8 @@ nemoasr_batch_t *nemoasr_batch_open(const char *model_dir, const char *language,
     b->conv_left = c->conv_kernel - 1;
     b->Lmax = m->Lmax;
     /* compaction moves the live rows to the front; source and destination never overlap when
-     * cap_rows >= 2 * left + cmax */
+     * cap_rows >= 2 * left + cmax.  (Regions twice as deep, compacted half as often, measured no
+     * faster at 64 and 256 streams.) */
     b->cap_rows = b->left + NK_CACHE_EPOCH_CHUNKS * b->cmax;
     if (b->cap_rows < 2 * b->left + 2 * b->cmax) b->cap_rows = 2 * b->left + 2 * b->cmax;
     b->P = c->pred_hidden;

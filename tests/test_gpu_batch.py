@@ -141,6 +141,27 @@ def test_batch_many_streams_compacted(latency):
     b.close()
 
 
+@pytest.mark.parametrize("latency", [80, 560])
+def test_batch_cache_compaction(latency):
+    """Streams long enough that their K/V and conv cache regions (56 + 8 x cmax rows) fill and
+    are compacted at least once, next to a short stream, with staggered starts, against
+    single-stream sessions."""
+    import nemoasr
+
+    mdir = model_dir("tiny")
+    secs = [9.5, 8.8, 10.2, 2.0] if latency == 80 else [24.0, 22.5, 25.0, 6.0]
+    mels = [mel_ref.logmel(synth.make_audio(t, seed=500 + i)) for i, t in enumerate(secs)]
+    b = nemoasr.Batch(mdir, "en-US", latency, streams=len(mels))
+    drive(b, mels, [0, 3, 1, 7], piece=8 * (LAT_RIGHT[latency] + 1))
+    sess = nemoasr.Session(mdir, "en-US", latency)
+    for s, m in enumerate(mels):
+        sess.reset("en-US", latency)
+        sess.feed_mel(m, final=True)
+        assert b.tokens(s) == sess.tokens(), s
+    sess.close()
+    b.close()
+
+
 @pytest.mark.parametrize("gpu_fe", [True, False])
 def test_batch_audio_and_reset(gpu_fe):
     """Audio pushed in 100 ms blocks, text per stream, and a slot reused after reset_stream; log-mel
