@@ -83,9 +83,10 @@ int nk_gemm_argmax(gpu_t *g, const float *A, uint32_t lda, const uint16_t *W, ui
 int nk_gemm_argmax_rows(gpu_t *g, const float *A, uint32_t lda, const uint16_t *W, uint32_t ldw, const float *bias,
                         unsigned long long *keys, uint32_t keys_ld, uint32_t M, uint32_t N, uint32_t K, uint32_t V,
                         const int *mrows, uint32_t mrows_mul);
-/* 1: many-row MFMA kernels take 64-wide K stages where K allows; 0 (default): 32-wide.  Returns
- * the previous setting. */
-int nk_gemm_mx_k64(int on);
+/* K split of the many-row residual updates (accumulate, no bias, no activation): -1 (default) by
+ * tile count, 0 never, 1 always where K has more than one block.  All three give the same bits.
+ * Returns the previous setting. */
+int nk_gemm_split(int mode);
 /* Kernel selection: 0 automatic (by row count), 1 first-generation VALU GEMV (M <= 4),
  * 2 few-row MFMA (M <= 16), 3 many-row MFMA, 4 weight-streaming GEMV (M <= 4),
  * 5 first-generation many-row MFMA (register-staged).

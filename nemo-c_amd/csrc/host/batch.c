@@ -421,6 +421,7 @@ nemoasr_batch_t *nemoasr_batch_open(const char *model_dir, const char *language,
     if (model_set_language(m, language ? language : "auto", err, errlen)) { nemoasr_batch_close(b); return NULL; }
     const model_cfg_t *c = &m->cfg;
     b->g = m->gpu;
+    gpu_set_many_rows(b->g, 1);
     b->S = n_streams;
     b->latency_ms = latency_ms;
     b->right = right;
@@ -536,6 +537,7 @@ nemoasr_batch_t *nemoasr_batch_open(const char *model_dir, const char *language,
     if (b->device_dec) {
         /* the greedy loop's own GPU context and worker thread */
         b->gd = gpu_create(err, errlen);
+        if (b->gd) gpu_set_many_rows(b->gd, 1);
         b->jdec[0] = gpu_buf_alloc(g, Mm * (size_t)b->J * fs);
         b->jdec[1] = gpu_buf_alloc(g, Mm * (size_t)b->J * fs);
         b->dorder = malloc(S * sizeof(int));

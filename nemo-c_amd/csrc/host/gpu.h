@@ -74,9 +74,14 @@ int gpu_graph_launch(gpu_t *g, gpu_graph_t *gr);
 void gpu_graph_free(gpu_graph_t *gr);
 int gpu_capturing(const gpu_t *g);
 
-/* Split-K scratch of the few-row GEMM: partial sums and self-resetting arrival counters. */
-float *gpu_splitk_ws(gpu_t *g, size_t floats_needed);
-uint32_t *gpu_splitk_counters(gpu_t *g, size_t n_needed);
+/* Scratch of the ordered split-K combines: partial sums and arrival counters (zero between launches:
+ * every launch's last arrivals reset theirs).  GPU_SCRATCH_FLOATS / GPU_SCRATCH_COUNTERS are
+ * allocated at creation; larger requests grow the scratch outside a capture and return NULL (no
+ * error recorded) inside one.  Launches on one gpu_t run in stream order, so they may share it. */
+#define GPU_SCRATCH_FLOATS (1u << 20)
+#define GPU_SCRATCH_COUNTERS 4096u
+float *gpu_scratch_ws(gpu_t *g, size_t floats_needed);
+uint32_t *gpu_scratch_counters(gpu_t *g, size_t n_needed);
 
 /* Per-kernel timing on the launch stream: when a name is set, every launch of that kernel is
  * bracketed by a pair of hipEvents; gpu_timing_collect returns the mean duration in ms. */
@@ -94,6 +99,12 @@ double gpu_timing_last_flops(const gpu_t *g);
 #define GPU_ZEROS_N 8192
 const int *gpu_iota(gpu_t *g);
 const float *gpu_zeros(gpu_t *g);
+
+/* Row policy of the kernel launchers on this context: 0 (default) picks GEMM and LayerNorm kernels by
+ * row count; 1 always uses the many-row kernels (batched streams: every row's arithmetic is then
+ * the same whatever the number of rows in the launch). */
+void gpu_set_many_rows(gpu_t *g, int on);
+int gpu_many_rows(const gpu_t *g);
 
 /* Number of kernel launches issued since creation (for tests and the launch-count check). */
 uint64_t gpu_launch_count(const gpu_t *g);

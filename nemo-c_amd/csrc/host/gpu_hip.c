@@ -28,6 +28,7 @@ struct gpu {
     hipEvent_t ev0, ev1;
     double last_ms;
     int in_batch, capturing, failed;
+    int many_rows;
     char name[256];
     char err[512];
     struct { char name[48]; hipFunction_t f; } fn[GPU_MAX_FN];
@@ -103,17 +104,24 @@ gpu_t *gpu_create(char *err, size_t errlen) {
     if ((e = hipMalloc((void **)&g->iota, GPU_IOTA_N * sizeof(int))) != hipSuccess ||
         (e = hipMemcpy(g->iota, iota, GPU_IOTA_N * sizeof(int), hipMemcpyHostToDevice)) != hipSuccess ||
         (e = hipMalloc((void **)&g->zeros, GPU_ZEROS_N * sizeof(float))) != hipSuccess ||
-        (e = hipMemset(g->zeros, 0, GPU_ZEROS_N * sizeof(float))) != hipSuccess) {
+        (e = hipMemset(g->zeros, 0, GPU_ZEROS_N * sizeof(float))) != hipSuccess ||
+        (e = hipMalloc((void **)&g->ws, GPU_SCRATCH_FLOATS * sizeof(float))) != hipSuccess ||
+        (e = hipMalloc((void **)&g->counters, GPU_SCRATCH_COUNTERS * sizeof(uint32_t))) != hipSuccess ||
+        (e = hipMemset(g->counters, 0, GPU_SCRATCH_COUNTERS * sizeof(uint32_t))) != hipSuccess) {
         snprintf(err, errlen, "constant tables: %s", hipGetErrorString(e));
         free(iota);
         gpu_destroy(g);
         return NULL;
     }
     free(iota);
+    g->ws_floats = GPU_SCRATCH_FLOATS;
+    g->ncounters = GPU_SCRATCH_COUNTERS;
     return g;
 }
 
 const int *gpu_iota(gpu_t *g) { return g->iota; }
+void gpu_set_many_rows(gpu_t *g, int on) { g->many_rows = on != 0; }
+int gpu_many_rows(const gpu_t *g) { return g->many_rows; }
 const float *gpu_zeros(gpu_t *g) { return g->zeros; }
 
 void gpu_destroy(gpu_t *g) {
@@ -424,27 +432,29 @@ void gpu_graph_free(gpu_graph_t *gr) {
     free(gr);
 }
 
-float *gpu_splitk_ws(gpu_t *g, size_t floats) {
+float *gpu_scratch_ws(gpu_t *g, size_t floats) {
     if (floats > g->ws_floats) {
-        if (g->capturing) { fail(g, "split-K scratch grown during capture", hipErrorInvalidValue); return NULL; }
+        if (g->capturing) return NULL;
         hipStreamSynchronize(g->stream);
+        float *p = NULL;
+        if (hipMalloc((void **)&p, floats * sizeof(float)) != hipSuccess) return NULL;
         if (g->ws) hipFree(g->ws);
-        size_t n = floats < (1u << 20) ? (1u << 20) : floats;
-        if (hipMalloc((void **)&g->ws, n * sizeof(float)) != hipSuccess) { g->ws = NULL; g->ws_floats = 0; return NULL; }
-        g->ws_floats = n;
+        g->ws = p;
+        g->ws_floats = floats;
     }
     return g->ws;
 }
 
-uint32_t *gpu_splitk_counters(gpu_t *g, size_t n) {
+uint32_t *gpu_scratch_counters(gpu_t *g, size_t n) {
     if (n > g->ncounters) {
-        if (g->capturing) { fail(g, "split-K counters grown during capture", hipErrorInvalidValue); return NULL; }
+        if (g->capturing) return NULL;
         hipStreamSynchronize(g->stream);
+        uint32_t *p = NULL;
+        if (hipMalloc((void **)&p, n * sizeof(uint32_t)) != hipSuccess) return NULL;
+        if (hipMemset(p, 0, n * sizeof(uint32_t)) != hipSuccess) { hipFree(p); return NULL; }
         if (g->counters) hipFree(g->counters);
-        size_t m = n < 4096 ? 4096 : n;
-        if (hipMalloc((void **)&g->counters, m * sizeof(uint32_t)) != hipSuccess) { g->counters = NULL; g->ncounters = 0; return NULL; }
-        if (hipMemset(g->counters, 0, m * sizeof(uint32_t)) != hipSuccess) return NULL;
-        g->ncounters = m;
+        g->counters = p;
+        g->ncounters = n;
     }
     return g->counters;
 }

@@ -8,12 +8,21 @@
 #include <string.h>
 
 static int g_force = 0;
-static int g_mx_k64 = 0; /* many-row kernels with 64-wide K stages where K allows (measured: no gain) */
+static int g_split = -1; /* many-row residual updates: -1 K split chosen by tile count, 0 never, 1 always */
 
-int nk_gemm_mx_k64(int on) {
-    const int prev = g_mx_k64;
-    g_mx_k64 = on;
+int nk_gemm_split(int mode) {
+    const int prev = g_split;
+    g_split = mode < 0 ? -1 : mode > 0 ? 1 : 0;
     return prev;
+}
+
+/* Blocks of the many-row residual updates' K sum, a function of K alone (so a row's result does
+ * not depend on how many rows share the launch): 2 blocks of 512 for K = 1024, K/1024 blocks for
+ * larger multiples of 1024, else one. */
+static uint32_t mx_kblocks(uint32_t K) {
+    if (K == 1024) return 2;
+    if (K >= 2048 && K % 1024 == 0 && K / 1024 <= 8) return K / 1024;
+    return 1;
 }
 
 int nk_gemm_force(int kind) {
@@ -102,16 +111,17 @@ typedef struct {
 
 /* Many-row GEMM on the direct-to-LDS MFMA kernels (kernels/nk_mx.hip).  Tile choice: the largest
  * of 128x128, 64x128, 64x64 whose tile count reaches about 400 workgroups; otherwise the smallest
- * tile that divides the columns, with K split for accumulating GEMMs with no bias and no activation
- * (whose partial products are added atomically).  Returns 1 when no tile divides the
- * output columns (the caller falls back), else the launch status. */
-static int launch_mx(gpu_t *g, NkGemmArgs *a, uint32_t M, uint32_t nout, uint32_t K, int glu, int splittable) {
-    static const struct { const char *name, *glu_name; uint32_t bm, bn; } cfg[] = {
-        { "gemm_mx128x128", "gemm_mx128x128_glu", 128, 128 },
-        { "gemm_mx64x128", "gemm_mx64x128_glu", 64, 128 },
-        { "gemm_mx64x64", "gemm_mx64x64_glu", 64, 64 },
+ * tile that divides the output columns.  Residual updates (accumulate, no bias, no activation) run
+ * on the _acc kernels, whose K sum is blocked (mx_kblocks); below ~400 tiles their K is split one
+ * block per workgroup, combined in block order by the tile's last workgroup (same bits as
+ * unsplit).  Returns 1 when no tile divides the output columns (the caller falls back), else the
+ * launch status. */
+static int launch_mx(gpu_t *g, NkGemmArgs *a, uint32_t M, uint32_t nout, uint32_t K, int glu, int resid) {
+    static const struct { const char *name, *glu_name, *acc_name; uint32_t bm, bn; } cfg[] = {
+        { "gemm_mx128x128", "gemm_mx128x128_glu", "gemm_mx128x128_acc", 128, 128 },
+        { "gemm_mx64x128", "gemm_mx64x128_glu", "gemm_mx64x128_acc", 64, 128 },
+        { "gemm_mx64x64", "gemm_mx64x64_glu", "gemm_mx64x64_acc", 64, 64 },
     };
-    const uint32_t S = K / 32;
     int pick_i = -1, last_ok = -1;
     uint32_t tiles = 0;
     for (int i = 0; i < 3; ++i) {
@@ -125,32 +135,29 @@ static int launch_mx(gpu_t *g, NkGemmArgs *a, uint32_t M, uint32_t nout, uint32_
         if (t >= 400) { pick_i = i; tiles = t; break; }
     }
     if (last_ok < 0) return 1;
-    uint32_t kz = 1;
     if (pick_i < 0) {
-        /* too few tiles: the smallest tile that divides the columns, with K split over up to four
-         * workgroups when allowed (partial products added atomically): about 448 workgroups, at
-         * least 16 K steps per share from 112 tiles on and 32 from 200 on (measured on 64 x 64
-         * tiles, 64 to 896 rows, K 1024 to 4096) */
         pick_i = last_ok;
         const uint32_t cols = glu ? cfg[pick_i].bn / 2 : cfg[pick_i].bn;
         tiles = ((M + cfg[pick_i].bm - 1) / cfg[pick_i].bm) * (nout / cols);
-        if (splittable) {
-            kz = 448 / tiles;
-            if (kz > 4) kz = 4;
-            if (tiles >= 112 && kz > S / 16) kz = S / 16;
-            if (tiles >= 200 && kz > S / 32) kz = S / 32;
-            if (kz > S) kz = S;
-            if (kz < 1) kz = 1;
+    }
+    uint32_t kz = 1;
+    a->kblocks = 1;
+    if (resid) {
+        a->kblocks = mx_kblocks(K);
+        /* split below ~400 tiles (measured on 64 x 64 tiles: about 448 workgroups at 448 rows) */
+        if (a->kblocks > 1 && (g_split == 1 || (g_split < 0 && tiles < 400))) kz = a->kblocks;
+        if (kz > 1) {
+            a->ws = gpu_scratch_ws(g, (size_t)tiles * kz * cfg[pick_i].bm * cfg[pick_i].bn);
+            a->counters = gpu_scratch_counters(g, tiles);
+            /* no scratch (a capture that cannot grow it): unsplit gives the same bits */
+            if (!a->ws || !a->counters) kz = 1;
         }
     }
     const uint32_t tm = (M + cfg[pick_i].bm - 1) / cfg[pick_i].bm;
     a->splits = kz;
     a->group_m = tm <= 8 ? tm : (tm + 3) / 4;
     const uint32_t total = tiles * kz, per = (total + 7) / 8;
-    /* K steps of 64 (half the barriers per MFMA) when every workgroup's share of K allows it */
-    const int k64 = K % 64 == 0 && g_mx_k64;
-    char name[40];
-    snprintf(name, sizeof name, "%s%s", glu ? cfg[pick_i].glu_name : cfg[pick_i].name, k64 ? "_k64" : "");
+    const char *name = resid ? cfg[pick_i].acc_name : glu ? cfg[pick_i].glu_name : cfg[pick_i].name;
     return gpu_launch(g, name, a, sizeof *a, 8 * per, 1, 1, 256, 1, 1);
 }
 
@@ -173,8 +180,7 @@ int nk_gemm_argmax_rows(gpu_t *g, const float *A, uint32_t lda, const uint16_t *
     const uint32_t tm = (M + 63) / 64, tiles = tm * (N / 64), per = (tiles + 7) / 8;
     a.group_m = tm <= 8 ? tm : (tm + 3) / 4;
     gpu_next_flops(g, 2.0 * M * N * K);
-    return gpu_launch(g, K % 64 == 0 && g_mx_k64 ? "gemm_mx64x64_argmax_k64" : "gemm_mx64x64_argmax", &a, sizeof a,
-                      8 * per, 1, 1, 256, 1, 1);
+    return gpu_launch(g, "gemm_mx64x64_argmax", &a, sizeof a, 8 * per, 1, 1, 256, 1, 1);
 }
 
 /* The GEMM with an optional LayerNorm prologue on A.  The weight-streaming GEMV applies it in
@@ -188,7 +194,9 @@ static int gemm_core(gpu_t *g, const float *A, uint32_t lda, const uint16_t *W, 
         return bad(g, "gemm: A/W must be 16-byte aligned with lda % 4 == 0, ldw % 8 == 0, K % 8 == 0");
     const uint32_t nout = act == NK_ACT_GLU ? N / 2 : N;
     if (ldc < nout) return bad(g, "gemm: ldc < output width");
-    const int kind = pick(M, K, act);
+    /* batched streams: always the many-row kernels (a row's result then does not depend on how many
+     * other rows share the launch) */
+    const int kind = gpu_many_rows(g) && !g_force && K % 32 == 0 ? K_MR : pick(M, K, act);
     const int ln_fused = ln && ln->mode && K == lda &&
                          ((kind == K_GEMV && K <= 1024) || (kind == K_FR && K == 1024 && M <= 16));
     if (ln && ln->mode && !ln_fused) {
@@ -237,6 +245,12 @@ static int gemm_core(gpu_t *g, const float *A, uint32_t lda, const uint16_t *W, 
         if (!a.bias) a.bias = gpu_zeros(g);
         if (!a.crow) a.crow = gpu_iota(g);
         const uint32_t tiles = (nout + 15) / 16;
+        if (p.KS > 1) {
+            /* partial tiles of 16 x 16 floats per K share, one arrival counter per column tile */
+            a.ws = gpu_scratch_ws(g, (size_t)tiles * p.KS * 256);
+            a.counters = gpu_scratch_counters(g, tiles);
+            if (!a.ws || !a.counters) return bad(g, "gemm: split-K scratch unavailable");
+        }
         return gpu_launch(g, fr_name(p, act, ln_fused), &a, sizeof a, tiles, p.KS, 1, 64 * p.W, 1, 1);
     }
     const int glu = act == NK_ACT_GLU;
@@ -244,27 +258,16 @@ static int gemm_core(gpu_t *g, const float *A, uint32_t lda, const uint16_t *W, 
         const int rc = launch_mx(g, &a, M, nout, K, glu, accumulate && !bias && act == NK_ACT_NONE);
         if (rc <= 0) return rc;
     }
-    /* many rows, first-generation kernels: 128 x 128 tiles when they fill the GPU, else 64 x 64
-     * (K split over up to four workgroups for accumulating GEMMs with no bias and no activation) */
-    const uint32_t S = K / 32;
+    /* many rows, first-generation kernels: 128 x 128 tiles when they fill the GPU, else 64 x 64 */
     if (nout % (glu ? 64 : 128) == 0) {
         const uint32_t t128 = ((M + 127) / 128) * (nout / (glu ? 64 : 128));
         if (t128 >= 240)
             return gpu_launch(g, glu ? "gemm_mm128_glu" : "gemm_mm128", &a, sizeof a, nout / (glu ? 64 : 128),
                               (M + 127) / 128, 1, 256, 1, 1);
     }
-    if (nout % (glu ? 32 : 64) == 0) {
-        const uint32_t t64 = ((M + 63) / 64) * (nout / (glu ? 32 : 64));
-        uint32_t kz = 1;
-        if (t64 < 200 && accumulate && !bias && act == NK_ACT_NONE) {
-            kz = 256 / t64;
-            if (kz > 4) kz = 4;
-            if (kz > S) kz = S;
-            if (kz < 1) kz = 1;
-        }
+    if (nout % (glu ? 32 : 64) == 0)
         return gpu_launch(g, glu ? "gemm_mm64_glu" : "gemm_mm64", &a, sizeof a, nout / (glu ? 32 : 64), (M + 63) / 64,
-                          kz, 256, 1, 1);
-    }
+                          1, 256, 1, 1);
     if (glu) return bad(g, "gemm: GLU needs N/2 to be a multiple of 32");
     return gpu_launch(g, "gemm_mr", &a, sizeof a, (N + 63) / 64, (M + 63) / 64, 1, 256, 1, 1);
 }
@@ -296,7 +299,7 @@ int nk_layernorm2(gpu_t *g, const float *X, const float *g1, const float *b1, co
     NkLnArgs a = { X, g1, b1, g2, b2, Y1, Y2, M, D, eps, 0 };
     /* many rows: a wavefront per row (D <= 1024), no barriers; 2 or 4 rows per wavefront from
      * 1024 / 2048 rows */
-    if (M > 16 && D <= 1024) {
+    if ((M > 16 || gpu_many_rows(g)) && D <= 1024) {
         const uint32_t R = M >= 2048 ? 4 : M >= 1024 ? 2 : 1, W = (M + R - 1) / R;
         return gpu_launch(g, R == 4 ? "layernorm_rows_r4" : R == 2 ? "layernorm_rows_r2" : "layernorm_rows", &a,
                           sizeof a, (W + 3) / 4, 1, 1, 256, 1, 1);
@@ -372,6 +375,10 @@ int nk_attention_out_desc(gpu_t *g, const float *kv, uint32_t ld, const int *des
     p.at = (NkAttnArgs){ kv, kv + D, kv + 2 * D, P, bias_u, bias_v, NULL, desc, NULL, c, 0, Lmax, H, dh, D, ld, ld, scale, 0 };
     p.Wo = Wo;
     p.C = C;
+    /* per-head partials [c][column tiles][H][columns], one arrival counter per (row, column tile) */
+    p.ws = gpu_scratch_ws(g, (size_t)c * D * H);
+    p.counters = gpu_scratch_counters(g, (size_t)c * (D / (8u * (uint32_t)g_attn_cpw)));
+    if (!p.ws || !p.counters) return bad(g, "attention_out: scratch unavailable");
     p.ldw = ldw;
     p.ldc = ldc;
     p.alpha = alpha;

@@ -43,12 +43,15 @@ typedef struct {
     const float *bias;
     float *C;
     const int *crow;
-    float *ws;      /* split-K partials (few-row MFMA kernel)          */
-    u32 *counters;  /* split-K arrival counters, self-resetting         */
+    float *ws;      /* split-K partials, stored agent-coherent          */
+    u32 *counters;  /* split-K arrival counters, one per output tile; the last arrival resets it */
     u32 M, N, K, lda, ldw, ldc;
     u32 act, accumulate, splits, group_m; /* group_m: row tiles per group of the many-row tile order */
     float alpha;
-    u32 pad1;
+    /* many-row accumulating kernels: K is summed in kblocks equal blocks, each block from zero,
+     * the block sums added in order; splits is 1 or kblocks (one block per workgroup) and gives
+     * the same bits either way */
+    u32 kblocks;
     /* LayerNorm prologue on A (weight-streaming GEMV): ln_mode 0 none, 1 LN(g1,b1),
      * 2 LN(LN(g1,b1); g2,b2); ln_out (optional) receives LN(A; g1,b1), rows of lda floats */
     const float *ln_g1, *ln_b1, *ln_g2, *ln_b2;
@@ -140,6 +143,8 @@ typedef struct {
     NkAttnArgs at;
     const u16 *Wo;
     float *C;
+    float *ws;     /* per-head partial products, [row][column tile][head][columns] */
+    u32 *counters; /* one per (row, column tile); the last of the H heads to arrive resets it */
     u32 ldw, ldc;
     float alpha;
     u32 pad;

@@ -22,8 +22,7 @@
  *      LayerNorm (the _ln kernels, K <= 1024) or straight from global memory;
  *   3. per step two MFMAs, A = hi + lo bf16 split of the f32 activations (16 significant bits);
  *   4. the W partial tiles are summed in wavefront order through LDS; wavefront 0 applies the
- *      epilogue.
- * No workgroup depends on another, so there is no split-K fixup.
+ *      epilogue (after the ordered combine of the K split, when there is one).
  * MFMA 16x16x32 bf16 lane layouts (lane l, element i):
  *   A: row l % 16, k 8*(l/16) + i;  B: k 8*(l/16) + i, column l % 16;
  *   D: row 4*(l/16) + i, column l % 16. */
@@ -50,9 +49,10 @@ __device__ __forceinline__ void ln_wave4(floatx4 (&v)[4], const floatx4 (&g)[4],
 }
 
 /* grid = (ceil(nout/16), KS): workgroup (tile, ks) takes the K steps [ks*S/KS, (ks+1)*S/KS) of the
- * S = K/32 steps, wavefront w the SPW steps from w*SPW within them.  With KS > 1 the partial
- * products are added into C atomically (the host uses this only for accumulating GEMMs with no
- * bias and no activation). */
+ * S = K/32 steps, wavefront w the SPW steps from w*SPW within them.  With KS > 1 (the host uses it
+ * only for accumulating GEMMs with no bias and no activation) every workgroup stores its partial
+ * tile agent-coherent and the tile's last workgroup to arrive adds the KS partials in ks order
+ * and updates C (nk_common.h), so the result does not depend on arrival order. */
 template <int W, int SPW, bool LNA, bool GLU>
 __device__ __forceinline__ void fr_impl(const NkGemmArgs &a, float *sA, floatx4 *sred) {
     const u32 tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -186,16 +186,27 @@ __device__ __forceinline__ void fr_impl(const NkGemmArgs &a, float *sA, floatx4 
         ta += sred[w * 64 + lane];
         if constexpr (GLU) tb += sred[(W + w) * 64 + lane];
     }
+    if (KS > 1) { /* K split over workgroups: no bias, no activation, accumulate */
+        float *wsb = a.ws + (u64)blockIdx.x * KS * 256;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) st_agent(wsb + (blockIdx.y * 4 + i) * 64 + lane, ta[i]);
+        wait_stores();
+        u32 last = 0;
+        if (lane == 0) last = arrive_last(a.counters + blockIdx.x, KS) ? 1u : 0u;
+        if (!__builtin_amdgcn_readfirstlane(last)) return;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            float t = 0.0f;
+            for (u32 ks = 0; ks < KS; ++ks) t += ks == blockIdx.y ? ta[i] : ld_agent(wsb + (ks * 4 + i) * 64 + lane);
+            ta[i] = t;
+        }
+    }
     if (n0 + (lane & 15) >= nout) return;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const u32 r = 4 * (lane >> 4) + i;
         if (r >= M) continue;
         float *dst = a.C + (u64)(u32)erow[i] * a.ldc + col;
-        if (KS > 1) { /* K split over workgroups: no bias, no activation, accumulate */
-            atomicAdd(dst, ta[i] * a.alpha);
-            continue;
-        }
         float v;
         if constexpr (GLU) {
             v = (ta[i] + eba) * sigmoid_f(tb[i] + ebb) * a.alpha;

@@ -12,8 +12,6 @@
  * 16-byte fragment reads of 16 consecutive rows conflict-free.
  * GLU: a workgroup's BN weight rows are BN/2 rows of the first half and the matching BN/2 of the
  * second; each wavefront holds both halves of its output columns.
- * grid.z > 1 splits K; the partial products are then added into C atomically (the host uses it
- * only for accumulating GEMMs with no bias and no activation).
  * Replaces the reference's many-row gemm_mma path (src/kernels.metal:120-208, row blocks on
  * grid.y, src/model.c:86-95). */
 #include "nk_common.h"
@@ -43,8 +41,8 @@ __device__ __forceinline__ void mm_impl(const NkGemmArgs &a, u16 *smem) {
     const u32 M = a.M, m0 = blockIdx.y * BM;
     const u32 nout = GLU ? a.N / 2 : a.N;
     const u32 c0 = blockIdx.x * (GLU ? BN / 2 : BN); /* first output column of the workgroup */
-    const u32 S = a.K >> 5, KZ = gridDim.z;
-    const u32 s_begin = (u32)(((u64)S * blockIdx.z) / KZ), s_end = (u32)(((u64)S * (blockIdx.z + 1)) / KZ);
+    const u32 S = a.K >> 5;
+    const u32 s_begin = 0, s_end = S;
 
     /* global -> register tile loads (rows past M re-read row M-1; their outputs are dropped) */
     const float *arow[AF];
@@ -161,7 +159,7 @@ __device__ __forceinline__ void mm_impl(const NkGemmArgs &a, u16 *smem) {
         ba[j] = a.bias ? a.bias[cc] : 0.0f;
         bb[j] = (GLU && a.bias) ? a.bias[cc + a.N / 2] : 0.0f;
     }
-    const bool rmw = a.accumulate && KZ == 1;
+    const bool rmw = a.accumulate;
     float cv[TO][TI][4];
 #pragma unroll
     for (int j = 0; j < TO; ++j)
@@ -180,10 +178,6 @@ __device__ __forceinline__ void mm_impl(const NkGemmArgs &a, u16 *smem) {
                 const u32 r = m0 + wm * (BM / 2) + 16 * i + 4 * (lane >> 4) + e;
                 if (r >= M) continue;
                 float *dst = a.C + (u64)orow[i][e] * a.ldc + ocol[j];
-                if (KZ > 1) {
-                    atomicAdd(dst, acc[i][j][e] * a.alpha);
-                    continue;
-                }
                 float v;
                 if constexpr (GLU) {
                     v = (acc[i][j][e] + ba[j]) * sigmoid_f(acc[i][j + TJ / 2][e] + bb[j]) * a.alpha;

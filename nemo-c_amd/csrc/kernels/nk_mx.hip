@@ -5,9 +5,9 @@
  * Workgroup tile BM x BN, 4 wavefronts as WGM (along M) x 4/WGM (along N); each wavefront owns a
  * (BM/WGM) x (BN*WGM/4) block of 16x16 tiles of v_mfma_f32_16x16x32_bf16.
  *
- * Operand staging: a ring of NS LDS stages (NS = 3..8 by tile size), each holding one K step of
- * KS = 32 or 64 columns of A (f32, BM x 4KS B) and W (bf16, BN x 2KS B); a stage of 64 feeds two
- * rounds of MFMAs per barrier.  Stages are filled by global_load_lds_dwordx4 (16 bytes per lane
+ * Operand staging: a ring of NS LDS stages (NS = 3 or 4 by tile size), each holding one K step of
+ * KS = 32 columns of A (f32, BM x 4KS B) and W (bf16, BN x 2KS B).  Stages are filled by
+ * global_load_lds_dwordx4 (16 bytes per lane
  * straight into LDS, no registers), issued NS-1 steps ahead of their use, so a wavefront only waits
  * for a stage's loads right before the barrier that publishes it.  A DMA instruction writes 64
  * consecutive 16-byte LDS granules in lane order; the global address each lane reads is chosen so
@@ -23,9 +23,15 @@
  * Tile order: the grid is 8 x (tiles per XCD); workgroup b runs on XCD b % 8 and takes tile
  * (b % 8) * per + b / 8 of an order that walks groups of group_m row tiles across all column tiles
  * (row tile fastest), so the workgroups of one XCD share weight columns and a few row panels in
- * that XCD's L2.  grid tiles past the end exit at once.  splits > 1 splits K; partial products
- * are then added into C atomically (the host uses it only for accumulating GEMMs with no bias and
- * no activation). */
+ * that XCD's L2.  grid tiles past the end exit at once.
+ *
+ * Accumulating GEMMs without bias or activation (the residual updates: C += alpha * A W^T) run on
+ * the _acc kernels.  They sum K in kblocks equal blocks, each from zero, and add the block sums in
+ * block order; with splits = kblocks every workgroup computes one block, stores it agent-coherent
+ * and the last workgroup of the tile to arrive adds them in the same order (nk_common.h).  The two
+ * forms give the same bits, so the host may split K or not by the row count (how many other
+ * streams share the step) without changing any row's result, and no result depends on which
+ * workgroup finishes first. */
 #include "nk_common.h"
 
 /* LDS granule swizzles: granule g of row r lives in slot g ^ swz(r).  A fragment read is one
@@ -34,26 +40,24 @@
  * counter on gfx950 over candidate functions: these two read with zero conflict cycles, where
  * the earlier ((r>>1)&7)^((r&1)<<2) and ((n>>1)&3)^((n>>3)&1) cost 4 extra cycles per read (a
  * 2-way conflict; 1-3% of kernel time) and the plain r % 8 cost a third of the kernel time at
- * 3584 rows.  The K-stage-64 forms (16 and 8 granules per row) are unmeasured by the counter. */
-__device__ __forceinline__ u32 swz_a(u32 r, int ag) {
-    return ag == 16 ? (r & 15) : ((r & 7) ^ ((r >> 3) & 1));
-}
-__device__ __forceinline__ u32 swz_b(u32 n, int bg) {
-    return bg == 4 ? ((n >> 1) & 3) : (((n >> 1) & 7) ^ ((n & 1) << 2));
-}
+ * 3584 rows. */
+__device__ __forceinline__ u32 swz_a(u32 r) { return (r & 7) ^ ((r >> 3) & 1); }
+__device__ __forceinline__ u32 swz_b(u32 n) { return (n >> 1) & 3; }
 
-template <int BM, int BN, int WGM, int NS, int KS, bool GLU, int EPI = 0>
-__device__ __forceinline__ void mx_impl(const NkGemmArgs &a, lds_char_t *const (&ring)[NS]) {
+/* EPI: 0 bias / activation / GLU / accumulate epilogue; 1 argmax keys; 2 blocked-K residual
+ * update with the ordered split combine (flag: LDS word for the arrival result) */
+template <int BM, int BN, int WGM, int NS, bool GLU, int EPI = 0>
+__device__ __forceinline__ void mx_impl(const NkGemmArgs &a, lds_char_t *const (&ring)[NS], u32 *flag) {
+    constexpr int KS = 32;
     constexpr int WGN = 4 / WGM;
     constexpr int WTM = BM / WGM, WTN = BN / WGN;
     constexpr int TI = WTM / 16, TJ = WTN / 16;
     constexpr int AG = KS / 4, BG = KS / 8; /* 16-byte granules per A row / W row of a stage */
-    constexpr int H = KS / 32;              /* 32-wide MFMA steps per stage */
     constexpr int A_BYTES = BM * KS * 4;
     constexpr int AI = BM * AG / 256; /* A granules per thread per stage */
     constexpr int BI = BN * BG / 256; /* W granules per thread per stage */
-    static_assert(KS == 32 || KS == 64, "stage width");
     static_assert(AI >= 1 && BI >= 1 && TI >= 1 && TJ >= (GLU ? 2 : 1), "tile shape");
+    static_assert(EPI != 2 || !GLU, "the residual update has no GLU");
     const u32 tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const u32 wm = wave / WGN, wn = wave % WGN;
     const u32 M = a.mrows ? min(a.M, (u32)max(*a.mrows, 0) * a.mrows_mul) : a.M;
@@ -73,19 +77,21 @@ __device__ __forceinline__ void mx_impl(const NkGemmArgs &a, lds_char_t *const (
     const u32 S = a.K / KS;
     const u32 s_begin = (u32)(((u64)S * kz) / KZ), s_end = (u32)(((u64)S * (kz + 1)) / KZ);
     const u32 nst = s_end - s_begin;
+    /* K steps per block of the blocked sum (EPI 2; the whole range otherwise) */
+    const u32 spb = EPI == 2 ? S / a.kblocks : nst;
 
     /* DMA sources: granule p of a stage region is written by lane p % 64 of instruction p / 64
      * (instruction j of wavefront w covers p in [(4j + w) * 64, +64)) */
     const float *asrc[AI];
 #pragma unroll
     for (int j = 0; j < AI; ++j) {
-        const u32 p = (4 * j + wave) * 64 + lane, r = p / AG, kg = (p % AG) ^ swz_a(r, AG);
+        const u32 p = (4 * j + wave) * 64 + lane, r = p / AG, kg = (p % AG) ^ swz_a(r);
         asrc[j] = a.A + (u64)min(m0 + r, M - 1) * a.lda + 4 * kg + (u64)s_begin * KS;
     }
     const u16 *bsrc[BI];
 #pragma unroll
     for (int j = 0; j < BI; ++j) {
-        const u32 p = (4 * j + wave) * 64 + lane, n = p / BG, kg = (p % BG) ^ swz_b(n, BG);
+        const u32 p = (4 * j + wave) * 64 + lane, n = p / BG, kg = (p % BG) ^ swz_b(n);
         u32 col;
         if (GLU) col = n < BN / 2 ? c0 + n : a.N / 2 + c0 + (n - BN / 2);
         else col = c0 + n;
@@ -101,32 +107,35 @@ __device__ __forceinline__ void mx_impl(const NkGemmArgs &a, lds_char_t *const (
 
     /* fragment addresses inside a stage */
     const u32 fr = lane & 15, fg = lane >> 4;
-    u32 aoff[H][TI][2];
+    u32 aoff[TI][2];
 #pragma unroll
-    for (int h = 0; h < H; ++h)
-#pragma unroll
-        for (int i = 0; i < TI; ++i) {
-            const u32 r = wm * WTM + 16 * i + fr;
-            aoff[h][i][0] = (r * AG + ((8 * h + 2 * fg) ^ swz_a(r, AG))) * 16;
-            aoff[h][i][1] = (r * AG + ((8 * h + 2 * fg + 1) ^ swz_a(r, AG))) * 16;
-        }
-    u32 boff[H][TJ];
+    for (int i = 0; i < TI; ++i) {
+        const u32 r = wm * WTM + 16 * i + fr;
+        aoff[i][0] = (r * AG + ((2 * fg) ^ swz_a(r))) * 16;
+        aoff[i][1] = (r * AG + ((2 * fg + 1) ^ swz_a(r))) * 16;
+    }
+    u32 boff[TJ];
 #pragma unroll
     for (int j = 0; j < TJ; ++j) {
         u32 n;
         if (GLU) n = j < TJ / 2 ? wn * (WTN / 2) + 16 * j : BN / 2 + wn * (WTN / 2) + 16 * (j - TJ / 2);
         else n = wn * WTN + 16 * j;
         n += fr;
-#pragma unroll
-        for (int h = 0; h < H; ++h)
-            boff[h][j] = A_BYTES + (n * BG + ((4 * h + fg) ^ swz_b(n, BG))) * 16;
+        boff[j] = A_BYTES + (n * BG + (fg ^ swz_b(n))) * 16;
     }
 
     floatx4 acc[TI][TJ];
+    /* EPI 2: sum of the finished K blocks, (((0 + b0) + b1) + ...) */
+    floatx4 tot[EPI == 2 ? TI : 1][EPI == 2 ? TJ : 1];
 #pragma unroll
     for (int i = 0; i < TI; ++i)
 #pragma unroll
         for (int j = 0; j < TJ; ++j) acc[i][j] = (floatx4){ 0.f, 0.f, 0.f, 0.f };
+    if constexpr (EPI == 2)
+#pragma unroll
+        for (int i = 0; i < TI; ++i)
+#pragma unroll
+            for (int j = 0; j < TJ; ++j) tot[i][j] = (floatx4){ 0.f, 0.f, 0.f, 0.f };
 
     /* Every step issues the loads of the step NS-1 ahead, clamped to the last one (the extra
      * copies land in slots nobody reads), so the loads in flight behind step q are always (NS-2)
@@ -144,32 +153,99 @@ __device__ __forceinline__ void mx_impl(const NkGemmArgs &a, lds_char_t *const (
         barrier_mem();
         issue(min(q + NS - 1, nst - 1), (u + NS - 1) % NS);
         const lds_char_t *st = ring[u];
+        uint4 fb[TJ];
 #pragma unroll
-        for (int h = 0; h < H; ++h) {
-            uint4 fb[TJ];
+        for (int j = 0; j < TJ; ++j) fb[j] = *(const __attribute__((address_space(3))) uint4 *)(st + boff[j]);
+        uint4 fh[TI], fl[TI];
 #pragma unroll
-            for (int j = 0; j < TJ; ++j) fb[j] = *(const __attribute__((address_space(3))) uint4 *)(st + boff[h][j]);
-            uint4 fh[TI], fl[TI];
+        for (int i = 0; i < TI; ++i) {
+            const floatx4 x0 = *(const __attribute__((address_space(3))) floatx4 *)(st + aoff[i][0]);
+            const floatx4 x1 = *(const __attribute__((address_space(3))) floatx4 *)(st + aoff[i][1]);
+            const float x[8] = { x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3] };
+            split8(x, fh[i], fl[i]);
+        }
 #pragma unroll
-            for (int i = 0; i < TI; ++i) {
-                const floatx4 x0 = *(const __attribute__((address_space(3))) floatx4 *)(st + aoff[h][i][0]);
-                const floatx4 x1 = *(const __attribute__((address_space(3))) floatx4 *)(st + aoff[h][i][1]);
-                const float x[8] = { x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3] };
-                split8(x, fh[i], fl[i]);
+        for (int i = 0; i < TI; ++i)
+#pragma unroll
+            for (int j = 0; j < TJ; ++j) acc[i][j] = mfma_bf16(fh[i], fb[j], acc[i][j]);
+#pragma unroll
+        for (int i = 0; i < TI; ++i)
+#pragma unroll
+            for (int j = 0; j < TJ; ++j) acc[i][j] = mfma_bf16(fl[i], fb[j], acc[i][j]);
+        if constexpr (EPI == 2) {
+            if ((q + 1) % spb == 0) { /* a K block ends: add its sum, start the next from zero */
+#pragma unroll
+                for (int i = 0; i < TI; ++i)
+#pragma unroll
+                    for (int j = 0; j < TJ; ++j) {
+                        tot[i][j] += acc[i][j];
+                        acc[i][j] = (floatx4){ 0.f, 0.f, 0.f, 0.f };
+                    }
             }
-#pragma unroll
-            for (int i = 0; i < TI; ++i)
-#pragma unroll
-                for (int j = 0; j < TJ; ++j) acc[i][j] = mfma_bf16(fh[i], fb[j], acc[i][j]);
-#pragma unroll
-            for (int i = 0; i < TI; ++i)
-#pragma unroll
-                for (int j = 0; j < TJ; ++j) acc[i][j] = mfma_bf16(fl[i], fb[j], acc[i][j]);
         }
     }
     }
 
     wait_vm_lgkm<0>(); /* no load into LDS may land after the workgroup ends */
+
+    if constexpr (EPI == 2) {
+        /* C[crow(m)][n] += alpha * sum; with K split, block kz's sum goes to the workspace and the
+         * tile's last workgroup adds all blocks in order */
+        constexpr int NV = TI * TJ * 4;
+        const u32 tid256 = threadIdx.x;
+        if (KZ > 1) {
+            float *wsb = a.ws + (u64)tt * KZ * NV * 256;
+#pragma unroll
+            for (int i = 0; i < TI; ++i)
+#pragma unroll
+                for (int j = 0; j < TJ; ++j)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        st_agent(wsb + ((u64)kz * NV + (i * TJ + j) * 4 + e) * 256 + tid256, tot[i][j][e]);
+            wait_stores();
+            __syncthreads();
+            if (tid256 == 0) *flag = arrive_last(a.counters + tt, KZ) ? 1u : 0u;
+            __syncthreads();
+            if (!*flag) return;
+#pragma unroll
+            for (int i = 0; i < TI; ++i)
+#pragma unroll
+                for (int j = 0; j < TJ; ++j)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        float t = 0.0f;
+                        for (u32 b = 0; b < KZ; ++b)
+                            t += b == kz ? tot[i][j][e] : ld_agent(wsb + ((u64)b * NV + (i * TJ + j) * 4 + e) * 256 + tid256);
+                        tot[i][j][e] = t;
+                    }
+        }
+        u32 orow[TI][4];
+#pragma unroll
+        for (int i = 0; i < TI; ++i)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const u32 r = min(m0 + wm * WTM + 16 * i + 4 * fg + e, M - 1);
+                orow[i][e] = a.crow ? (u32)a.crow[r] : r;
+            }
+        float cv[TJ][TI][4];
+#pragma unroll
+        for (int j = 0; j < TJ; ++j)
+#pragma unroll
+            for (int i = 0; i < TI; ++i)
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    cv[j][i][e] = a.C[(u64)orow[i][e] * a.ldc + c0 + wn * WTN + 16 * j + fr];
+#pragma unroll
+        for (int j = 0; j < TJ; ++j)
+#pragma unroll
+            for (int i = 0; i < TI; ++i)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    if (m0 + wm * WTM + 16 * i + 4 * fg + e >= M) continue;
+                    a.C[(u64)orow[i][e] * a.ldc + c0 + wn * WTN + 16 * j + fr] = cv[j][i][e] + tot[i][j][e] * a.alpha;
+                }
+        return;
+    }
 
     if constexpr (EPI == 1) {
         /* argmax partials: per row, the best (score + bias, lowest column) over this wavefront's
@@ -227,7 +303,7 @@ __device__ __forceinline__ void mx_impl(const NkGemmArgs &a, lds_char_t *const (
         ba[j] = a.bias ? a.bias[ocol[j]] : 0.0f;
         bb[j] = (GLU && a.bias) ? a.bias[ocol[j] + a.N / 2] : 0.0f;
     }
-    const bool rmw = a.accumulate && KZ == 1;
+    const bool rmw = a.accumulate;
     float cv[TO][TI][4];
 #pragma unroll
     for (int j = 0; j < TO; ++j)
@@ -243,10 +319,6 @@ __device__ __forceinline__ void mx_impl(const NkGemmArgs &a, lds_char_t *const (
             for (int e = 0; e < 4; ++e) {
                 if (m0 + wm * WTM + 16 * i + 4 * fg + e >= M) continue;
                 float *dst = a.C + (u64)orow[i][e] * a.ldc + ocol[j];
-                if (KZ > 1) {
-                    atomicAdd(dst, acc[i][j][e] * a.alpha);
-                    continue;
-                }
                 float v;
                 if constexpr (GLU) {
                     v = (acc[i][j][e] + ba[j]) * sigmoid_f(acc[i][j + TJ / 2][e] + bb[j]) * a.alpha;
@@ -261,30 +333,27 @@ __device__ __forceinline__ void mx_impl(const NkGemmArgs &a, lds_char_t *const (
     }
 }
 
-/* NS ring stages of KS-wide K steps: (BM*4 + BN*2)*KS bytes each, sized so that two workgroups fit
+/* NS ring stages of 32-wide K steps: (BM*4 + BN*2)*32 bytes each, sized so that two workgroups fit
  * a CU's 160 KB of LDS (measured: the second workgroup overlaps one's loads and barriers with the
- * other's MFMAs; 3584 rows, 128x128: 117 -> 79 us with the swizzles).  K % 32 kernels: 3 x 24 KB
- * for 128x128, 4 x 16 KB for 64x128, 4 x 12 KB for 64x64; K % 64 kernels (suffix _k64, half the
- * barriers per MFMA): 2 x 48 KB, 2 x 32 KB, 3 x 24 KB */
-#define GEMM_MX(NAME, BM, BN, WGM, NS, KS, GLU, EPI)                                                      \
+ * other's MFMAs; 3584 rows, 128x128: 117 -> 79 us with the swizzles): 3 x 24 KB for 128x128,
+ * 4 x 16 KB for 64x128, 4 x 12 KB for 64x64 */
+#define GEMM_MX(NAME, BM, BN, WGM, NS, GLU, EPI)                                                          \
     extern "C" __global__ __launch_bounds__(256) void NAME(const NkGemmArgs a) {                          \
-        __shared__ uint4 ring_mem[NS][(BM * 4 + BN * 2) * KS / 16];                                      \
+        __shared__ uint4 ring_mem[NS][(BM * 4 + BN * 2) * 32 / 16];                                      \
+        __shared__ u32 flag;                                                                              \
         lds_char_t *ring[NS];                                                                             \
         _Pragma("unroll") for (int i = 0; i < NS; ++i) ring[i] = (lds_char_t *)ring_mem[i];               \
-        mx_impl<BM, BN, WGM, NS, KS, GLU, EPI>(a, ring);                                                  \
+        mx_impl<BM, BN, WGM, NS, GLU, EPI>(a, ring, &flag);                                               \
     }
-GEMM_MX(gemm_mx128x128, 128, 128, 2, 3, 32, false, 0)
-GEMM_MX(gemm_mx64x128, 64, 128, 2, 4, 32, false, 0)
-GEMM_MX(gemm_mx64x64, 64, 64, 2, 4, 32, false, 0)
-GEMM_MX(gemm_mx128x128_glu, 128, 128, 2, 3, 32, true, 0)
-GEMM_MX(gemm_mx64x128_glu, 64, 128, 2, 4, 32, true, 0)
-GEMM_MX(gemm_mx64x64_glu, 64, 64, 2, 4, 32, true, 0)
-GEMM_MX(gemm_mx128x128_k64, 128, 128, 2, 2, 64, false, 0)
-GEMM_MX(gemm_mx64x128_k64, 64, 128, 2, 2, 64, false, 0)
-GEMM_MX(gemm_mx64x64_k64, 64, 64, 2, 3, 64, false, 0)
-GEMM_MX(gemm_mx128x128_glu_k64, 128, 128, 2, 2, 64, true, 0)
-GEMM_MX(gemm_mx64x128_glu_k64, 64, 128, 2, 2, 64, true, 0)
-GEMM_MX(gemm_mx64x64_glu_k64, 64, 64, 2, 3, 64, true, 0)
+GEMM_MX(gemm_mx128x128, 128, 128, 2, 3, false, 0)
+GEMM_MX(gemm_mx64x128, 64, 128, 2, 4, false, 0)
+GEMM_MX(gemm_mx64x64, 64, 64, 2, 4, false, 0)
+GEMM_MX(gemm_mx128x128_glu, 128, 128, 2, 3, true, 0)
+GEMM_MX(gemm_mx64x128_glu, 64, 128, 2, 4, true, 0)
+GEMM_MX(gemm_mx64x64_glu, 64, 64, 2, 4, true, 0)
+/* residual updates: blocked K, optional ordered split */
+GEMM_MX(gemm_mx128x128_acc, 128, 128, 2, 3, false, 2)
+GEMM_MX(gemm_mx64x128_acc, 64, 128, 2, 4, false, 2)
+GEMM_MX(gemm_mx64x64_acc, 64, 64, 2, 4, false, 2)
 /* joint scores -> argmax partials (keys), 64x64 tiles: two keys per row per column tile */
-GEMM_MX(gemm_mx64x64_argmax, 64, 64, 2, 4, 32, false, 1)
-GEMM_MX(gemm_mx64x64_argmax_k64, 64, 64, 2, 3, 64, false, 1)
+GEMM_MX(gemm_mx64x64_argmax, 64, 64, 2, 4, false, 1)

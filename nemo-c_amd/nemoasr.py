@@ -104,7 +104,7 @@ API = {
     "nk_gemm_ln": (C.c_int, [_vp, _vp, _u32, _vp, _u32, _vp, _vp, _u32, _vp, _u32, _u32, _u32, C.c_int, C.c_int,
                              C.c_float, C.c_int, _vp, _vp, _vp, _vp, _vp, _vp, C.c_float]),
     "nk_gemm_force": (C.c_int, [C.c_int]),
-    "nk_gemm_mx_k64": (C.c_int, [C.c_int]),
+    "nk_gemm_split": (C.c_int, [C.c_int]),
     "nk_gemm_argmax": (C.c_int, [_vp, _vp, _u32, _vp, _u32, _vp, _vp, _u32, _u32, _u32, _u32, _u32]),
     "nk_gemm_argmax_rows": (C.c_int, [_vp, _vp, _u32, _vp, _u32, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _vp, _u32]),
     "nk_gemm_kernel_name": (C.c_char_p, [_u32, _u32, _u32, C.c_int]),

@@ -7,7 +7,7 @@ It joins two pieces of the reference's parity tooling:
     the emitted token ids.  `run` produces the same three artefacts through the public C API of
     this library (nemoasr_open / nemoasr_feed) and its dump hooks, feeding the file the way the
     CLI does (src/main.c:230-252): pieces of one chunk of audio, the last one final;
-  - the comparison of those dumps with the MLX reference directory (tools/compare.py:1-53),
+  - the comparison of those dumps with the MLX reference directory (tools/compare.py:1-45),
     with the same gates: log-mel max |diff| < 1e-3 with equal shapes, encoder rows
     max |diff| / max |ref| < 1e-2 with equal shapes, token ids identical.
 
@@ -136,7 +136,7 @@ def write_dumps(out_dir: str, mel: np.ndarray, enc: np.ndarray, tokens: list[int
             f.write(f"{int(t)}\n")
 
 
-# ---- comparison (tools/compare.py:1-53) -------------------------------------------------------
+# ---- comparison (tools/compare.py:1-45) -------------------------------------------------------
 
 def _load(path: str, cols: int) -> np.ndarray:
     a = np.fromfile(path, dtype=np.float32)

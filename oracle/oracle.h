@@ -100,6 +100,9 @@ const float *or_session_dump_joint_enc(const or_session_t *s);
 const int *or_session_dump_chunk_rows(const or_session_t *s);
 /* joint evaluation log: for every joint evaluation, best index and top-2 margin */
 size_t or_session_joint_log(const or_session_t *s, const int **best, const float **margin);
+/* per emitted token, the smallest top-2 joint margin of the decisions that produced it; *tail is the
+ * smallest margin of the decisions after the last token (INFINITY when there are none) */
+size_t or_session_token_margins(const or_session_t *s, const float **margin, float *tail);
 /* For tests of compaction-independence: the epoch length in chunks (reference CACHE_EPOCH_CHUNKS). */
 const char *or_session_error(const or_session_t *s);
 

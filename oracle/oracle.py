@@ -107,6 +107,8 @@ def lib() -> C.CDLL:
         L.or_session_dump_chunk_rows.restype = _i32p
         L.or_session_joint_log.argtypes = [C.c_void_p, C.POINTER(_i32p), C.POINTER(_f32p)]
         L.or_session_joint_log.restype = C.c_size_t
+        L.or_session_token_margins.argtypes = [C.c_void_p, C.POINTER(_f32p), C.POINTER(C.c_float)]
+        L.or_session_token_margins.restype = C.c_size_t
         L.or_session_error.argtypes = [C.c_void_p]
         L.or_session_error.restype = C.c_char_p
         L.or_enc_plan.argtypes = [C.POINTER(EncBook), C.c_int, C.c_int, C.c_int, C.c_int]
@@ -407,6 +409,15 @@ class Session:
         if n == 0:
             return np.zeros(0, np.int32), np.zeros(0, np.float32)
         return (np.ctypeslib.as_array(b, shape=(n,)).copy(), np.ctypeslib.as_array(m, shape=(n,)).copy())
+
+    def token_margins(self) -> np.ndarray:
+        """Per emitted token k, the smallest top-2 joint margin over the greedy decisions that
+        produced it (blank frames since token k-1, then the emitting frame); one extra last entry
+        for the decisions after the last token (inf when there are none)."""
+        m, tail = _f32p(), C.c_float()
+        n = lib().or_session_token_margins(self.h, C.byref(m), C.byref(tail))
+        head = np.ctypeslib.as_array(m, shape=(n,)).copy() if n else np.zeros(0, np.float32)
+        return np.append(head, np.float32(tail.value))
 
     def __del__(self):
         if getattr(self, "h", None):

@@ -1,9 +1,10 @@
 /* ORACLE — test infrastructure only (see oracle.h).
  *
  * CPU restatement of the streaming bookkeeping of nemoasr-c:
- *   encoder: src/encoder.c (window/lo/hi rule :242-280, pre-encode :150-171, blocks :174-226);
- *   decoder: src/decoder.c (prediction net :370-389, joint batch :393-402, greedy loop :404-439);
- *   model:   src/model.c (prompt fold :390-400, ptab :364-384).
+ *   encoder: src/encoder.c (window/lo/hi rule :213-267, pre-encode :120-142, blocks :144-197,
+ *            compaction :199-211);
+ *   decoder: src/decoder.c (prediction net :57-77, joint batch :79-90, greedy loop :92-127);
+ *   model:   src/model.c (prompt fold :312-322, ptab :286-306).
  *
  * The attention and convolution histories are kept here as explicit sliding windows (the last
  * min(L, att_left) K/V rows and the last conv_kernel-1 GLU rows), not as the reference's
@@ -153,6 +154,12 @@ struct or_session {
     int *jl_best;
     float *jl_margin;
     size_t jl_n, jl_cap;
+    /* per emitted token: the smallest top-2 margin over the decisions that produced it (the blank
+     * frames passed since the previous token, then the emitting frame); seg_min is the running
+     * minimum of the decisions since the last emitted token */
+    float *tk_margin;
+    size_t tk_n, tk_cap;
+    float seg_min;
     char err[256];
 };
 
@@ -192,7 +199,7 @@ void or_session_free(or_session_t *s) {
     free(s->pred_out);
     free(s->pending);
     free(s->d_layers); free(s->d_prompted); free(s->d_joint); free(s->d_rows);
-    free(s->jl_best); free(s->jl_margin);
+    free(s->jl_best); free(s->jl_margin); free(s->tk_margin);
     free(s);
 }
 
@@ -212,6 +219,8 @@ void or_session_reset(or_session_t *s) {
     s->chunks = s->frames = s->joint_steps = 0;
     s->d_nchunks = 0;
     s->jl_n = 0;
+    s->tk_n = 0;
+    s->seg_min = INFINITY;
 }
 
 void or_session_set_dump(or_session_t *s, int on) { s->dump = on; }
@@ -227,6 +236,11 @@ size_t or_session_joint_log(const or_session_t *s, const int **best, const float
     *best = s->jl_best;
     *margin = s->jl_margin;
     return s->jl_n;
+}
+size_t or_session_token_margins(const or_session_t *s, const float **margin, float *tail) {
+    *margin = s->tk_margin;
+    *tail = s->seg_min;
+    return s->tk_n;
 }
 
 static int sub_len(int n) { return n / 2 + 1; } /* src/encoder.c:118 */
@@ -426,7 +440,15 @@ static int decode(or_session_t *s, const float *joint_enc, int frames, int *out,
         int i = 0;
         for (; i < rows; ++i) {
             const int pred = res[i];
+            const float mg = s->jl_margin[s->jl_n - (size_t)rows + (size_t)i];
+            if (mg < s->seg_min) s->seg_min = mg;
             if (pred == d->blank_id) { symbols = 0; continue; }
+            if (s->tk_n == s->tk_cap) {
+                s->tk_cap = s->tk_cap ? 2 * s->tk_cap : 1024;
+                s->tk_margin = realloc(s->tk_margin, s->tk_cap * sizeof(float));
+            }
+            s->tk_margin[s->tk_n++] = s->seg_min;
+            s->seg_min = INFINITY;
             if (n < max_out) out[n++] = pred;
             s->last_token = pred;
             for (int l = 0; l < 2; ++l) {

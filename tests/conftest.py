@@ -17,6 +17,43 @@ def pytest_configure(config):
     config.addinivalue_line("markers", "slow: full-size model on the CPU oracle")
 
 
+# GPU files in the order their evidence builds on each other: per-kernel parity first, then the
+# single stream end to end, then the multi-stream batch (built from the same kernels), then the
+# allocation-free entry point; so that under -x a failure in a later layer cannot hide the
+# foundational results.  Files not listed keep their place ahead of these.
+_FILE_ORDER = {"test_golden.py": 0, "test_gpu_kernels.py": 1, "test_gpu_stream.py": 2, "test_gpu_determinism.py": 3,
+               "test_gpu_batch.py": 4, "test_zz_no_alloc.py": 5}
+
+
+def pytest_collection_modifyitems(session, config, items):
+    items.sort(key=lambda it: _FILE_ORDER.get(os.path.basename(str(it.fspath)), -1))
+
+
+# Greedy decisions whose top-2 joint margin in the oracle is below TOKEN_TIE (absolute logit units)
+# are float ties: the GPU sums in another order (MFMA blocks, wavefront reductions), so the winner of
+# such a decision may differ.  Measured oracle margins: median 0.1 (tiny model) / 0.5 (full), 1% below
+# 2e-3; the two flips seen on the GPU were at 3.9e-6 and 2.8e-6.
+TOKEN_TIE = 1e-4
+
+
+def check_tokens(got, ref, margins, what=""):
+    """Token ids must equal the oracle's.  The only exception is a float tie: at the first differing
+    position k the oracle's decisions that produced its token k (the blank frames since token k-1 and
+    the emitting frame; past the last token, the trailing decisions) must include one with a top-2
+    margin below TOKEN_TIE.  After such a tie the two decodes legitimately diverge, so the comparison
+    stops there.  Returns k, or None when the sequences are identical."""
+    got, ref = list(got), list(ref)
+    if got == ref:
+        return None
+    k = next(i for i, (a, b) in enumerate(zip(got + [-1], ref + [-2])) if a != b)
+    m = float(margins[min(k, len(margins) - 1)])
+    msg = (f"{what}tokens differ at {k} of {len(ref)} (gpu {got[k] if k < len(got) else 'end'}, "
+           f"oracle {ref[k] if k < len(ref) else 'end'}); oracle decision margin {m:.3g}, tie bound {TOKEN_TIE:g}")
+    print(msg, flush=True)
+    assert m < TOKEN_TIE, msg
+    return k
+
+
 def model_dir(kind: str, seed: int = 0, blank_bias: float = 0.0) -> str:
     import synth
 

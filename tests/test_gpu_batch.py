@@ -2,9 +2,10 @@
 
 Every stream of a batch must emit exactly the tokens that the oracle's single-stream session emits
 for that stream's audio, whatever the other streams do: different lengths, staggered starts,
-streams ending while others continue, a slot reused after reset.  The joint.enc rows of each stream
-(the joint's encoder input) are held to the encoder gate of the single-stream tests (1e-3
-relative).
+streams ending while others continue, a slot reused after reset (conftest.check_tokens: the only
+exception is a float tie of the oracle's greedy decision, after which the comparison stops).  The
+joint.enc rows of each stream (the joint's encoder input) are held to the encoder gate of the
+single-stream tests (1e-3 relative).
 """
 import numpy as np
 import pytest
@@ -12,7 +13,7 @@ import pytest
 import mel_ref
 import oracle
 import synth
-from conftest import model_dir, rel_err
+from conftest import check_tokens, model_dir, rel_err
 
 pytestmark = pytest.mark.gpu
 
@@ -23,16 +24,18 @@ _ORACLE = {}
 
 
 def oracle_run(om, latency, mel, key=None):
-    """Oracle tokens and joint.enc rows of one stream (cached by key across parametrizations)."""
+    """Oracle tokens, joint.enc rows and per-token decision margins of one stream (cached by key
+    across parametrizations)."""
     if key is not None and key in _ORACLE:
         return _ORACLE[key]
     o = oracle.Session(om, LAT_RIGHT[latency], dump=True)
     o.feed_mel(mel, final=True)
     _, _, oj, _ = o.dumps()
+    res = (list(o.tokens), oj, o.token_margins())
     if key is not None:
-        _ORACLE[key] = (list(o.tokens), oj)
+        _ORACLE[key] = res
     print(f"  oracle {key or ''}: {mel.shape[0]} mel rows, {len(o.tokens)} tokens", flush=True)
-    return list(o.tokens), oj
+    return res
 
 
 def drive(b, mels, starts, piece):
@@ -53,12 +56,12 @@ def drive(b, mels, starts, piece):
 
 def check_streams(b, om, latency, mels, J, tag=None):
     for s, m in enumerate(mels):
-        toks, oj = oracle_run(om, latency, m, None if tag is None else (tag, s))
+        toks, oj, margins = oracle_run(om, latency, m, None if tag is None else (tag, s))
         gj = b.joint_enc(s, J)
         assert gj.shape == oj.shape, (s, gj.shape, oj.shape)
         err = rel_err(gj, oj)
         assert err <= 1e-3, (s, err)
-        assert b.tokens(s) == toks, f"stream {s}: {len(b.tokens(s))} tokens vs oracle {len(toks)}"
+        check_tokens(b.tokens(s), toks, margins, f"stream {s}: ")
 
 
 @pytest.mark.parametrize("device_loop", [True, False])
@@ -101,10 +104,12 @@ def test_full_batch_matches_oracle(graphs):
 
 
 def test_batch_matches_sessions_full():
-    """Sixteen streams at 560 ms against sixteen single-stream sessions (GPU against GPU)."""
+    """Sixteen streams at 560 ms and sixteen single-stream sessions (different kernels: many-row
+    MFMA tiles against weight-streaming GEMVs), both against the oracle."""
     import nemoasr
 
     mdir = model_dir("full")
+    om = oracle.Model(mdir, "en-US")
     mels = [mel_ref.logmel(synth.make_audio(1.5 + 0.1 * (i % 5), seed=80 + i)) for i in range(16)]
     b = nemoasr.Batch(mdir, "en-US", 560, streams=16)
     for s, m in enumerate(mels):
@@ -112,9 +117,11 @@ def test_batch_matches_sessions_full():
     b.run()
     sess = nemoasr.Session(mdir, "en-US", 560)
     for s, m in enumerate(mels):
+        toks, _, margins = oracle_run(om, 560, m)
         sess.reset("en-US", 560)
         sess.feed_mel(m, final=True)
-        assert b.tokens(s) == sess.tokens(), s
+        check_tokens(b.tokens(s), toks, margins, f"batch stream {s}: ")
+        check_tokens(sess.tokens(), toks, margins, f"session {s}: ")
     sess.close()
     b.close()
 
@@ -124,19 +131,25 @@ def test_batch_many_streams_compacted(latency):
     """130 streams, three row blocks of the greedy loop's GEMMs: the compacted step rows, the row
     blocks past the live count that return at once and the joint GEMM's device-side row count,
     with streams of different lengths and starts (so the live count changes from step to step),
-    against single-stream sessions."""
+    against the oracle (and single-stream sessions, also against the oracle).  Streams 93 and 121
+    carry float ties of the oracle (top-2 margins 3.9e-6 and 2.8e-6 at tokens 59 and 52)."""
     import nemoasr
 
     mdir = model_dir("tiny")
+    om = oracle.Model(mdir, "en-US")
     S = 130
     mels = [mel_ref.logmel(synth.make_audio(0.4 + 0.07 * (i % 23), seed=300 + i)) for i in range(S)]
     b = nemoasr.Batch(mdir, "en-US", latency, streams=S)
     drive(b, mels, [i % 5 for i in range(S)], piece=8 * (LAT_RIGHT[latency] + 1))
     sess = nemoasr.Session(mdir, "en-US", latency)
+    ties = 0
     for s, m in enumerate(mels):
+        toks, _, margins = oracle_run(om, latency, m, ("many", latency, s))
         sess.reset("en-US", latency)
         sess.feed_mel(m, final=True)
-        assert b.tokens(s) == sess.tokens(), s
+        ties += check_tokens(b.tokens(s), toks, margins, f"batch stream {s}: ") is not None
+        ties += check_tokens(sess.tokens(), toks, margins, f"session {s}: ") is not None
+    print(f"  {ties} float ties among {2 * S} decodes", flush=True)
     sess.close()
     b.close()
 
@@ -144,21 +157,18 @@ def test_batch_many_streams_compacted(latency):
 @pytest.mark.parametrize("latency", [80, 560])
 def test_batch_cache_compaction(latency):
     """Streams long enough that their K/V and conv cache regions (56 + 8 x cmax rows) fill and
-    are compacted at least once, next to a short stream, with staggered starts, against
-    single-stream sessions."""
+    are compacted at least once, next to a short stream, with staggered starts, against the
+    oracle (whose histories are plain sliding windows: compaction must be invisible)."""
     import nemoasr
 
     mdir = model_dir("tiny")
+    om = oracle.Model(mdir, "en-US")
     secs = [9.5, 8.8, 10.2, 2.0] if latency == 80 else [24.0, 22.5, 25.0, 6.0]
     mels = [mel_ref.logmel(synth.make_audio(t, seed=500 + i)) for i, t in enumerate(secs)]
     b = nemoasr.Batch(mdir, "en-US", latency, streams=len(mels))
+    b.set_dump(True)
     drive(b, mels, [0, 3, 1, 7], piece=8 * (LAT_RIGHT[latency] + 1))
-    sess = nemoasr.Session(mdir, "en-US", latency)
-    for s, m in enumerate(mels):
-        sess.reset("en-US", latency)
-        sess.feed_mel(m, final=True)
-        assert b.tokens(s) == sess.tokens(), s
-    sess.close()
+    check_streams(b, om, latency, mels, om.dims.joint_hidden)
     b.close()
 
 
@@ -180,8 +190,8 @@ def test_batch_audio_and_reset(gpu_fe):
         b.step()
     b.run()
     for s, a in enumerate(audios):
-        toks, _ = oracle_run(om, 560, mel_ref.logmel(a))
-        assert b.tokens(s) == toks, s
+        toks, _, margins = oracle_run(om, 560, mel_ref.logmel(a))
+        check_tokens(b.tokens(s), toks, margins, f"stream {s}: ")
         b.text(s)
     first = b.tokens(1)
     b.reset_stream(1)
@@ -221,10 +231,10 @@ def test_batch_gpu_frontend_matches_host(latency):
         b.close()
     for s, a in enumerate(audios):
         (tg, jg), (th, jh) = out[0][s], out[1][s]
-        assert tg == th, s
         assert rel_err(jg, jh) < 1e-4, s
-        toks, _ = oracle_run(om, latency, mel_ref.logmel(a))
-        assert tg == toks, s
+        toks, _, margins = oracle_run(om, latency, mel_ref.logmel(a))
+        check_tokens(tg, toks, margins, f"gpu front end, stream {s}: ")
+        check_tokens(th, toks, margins, f"host front end, stream {s}: ")
 
 
 def test_batch_mixed_input_rejected():
@@ -243,4 +253,43 @@ def test_batch_mixed_input_rejected():
         b.gpu_frontend(False)
     b.reset_stream(1)
     b.push(1, np.zeros(1600, np.float32))
+    b.close()
+
+
+@pytest.mark.parametrize("device_loop", [True, False])
+@pytest.mark.parametrize("bias,lang,latency", [(0.7, "en-US", 560), (0.6, "auto", 160), (0.7, "auto", 1120)])
+def test_batch_blank_biased(bias, lang, latency, device_loop):
+    """Blank-biased tiny models (the settings of the r6_blank07 / r1_blank06 fixtures): both batched
+    greedy loops must take the blank branches (symbol reset, first non-blank frame wins, later
+    frames redone, a prediction carried into the next chunk) and give the oracle's tokens."""
+    import nemoasr
+
+    mdir = model_dir("tiny", 0, bias)
+    om = oracle.Model(mdir, lang)
+    secs = [2.0, 1.5, 2.6, 0.9, 1.8]
+    mels = [mel_ref.logmel(synth.make_audio(t, seed=14 + 7 * i)) for i, t in enumerate(secs)]
+    b = nemoasr.Batch(mdir, lang, latency, streams=len(mels))
+    b.device_decoder(device_loop)
+    b.set_dump(True)
+    drive(b, mels, [0, 1, 0, 2, 1], piece=8 * (LAT_RIGHT[latency] + 1))
+    check_streams(b, om, latency, mels, om.dims.joint_hidden, tag=("blank", bias, lang, latency))
+    st = b.stats()
+    assert 0 < st["tokens"] < st["rows"] * om.dims.max_symbols, st
+    b.close()
+
+
+@pytest.mark.parametrize("latency", [1120, 560])
+def test_batch_auto_prompt_full(latency):
+    """Full model with the language auto-detect prompt (the one-hot folded into the first prompt
+    layer's bias, src/model.c:312-322), staggered streams, against the oracle."""
+    import nemoasr
+
+    mdir = model_dir("full")
+    om = oracle.Model(mdir, "auto")
+    secs = [2.5, 1.6, 2.9]
+    mels = [mel_ref.logmel(synth.make_audio(t, seed=900 + i)) for i, t in enumerate(secs)]
+    b = nemoasr.Batch(mdir, "auto", latency, streams=len(mels))
+    b.set_dump(True)
+    drive(b, mels, [0, 2, 1], piece=8 * (LAT_RIGHT[latency] + 1))
+    check_streams(b, om, latency, mels, om.dims.joint_hidden, tag=("auto", latency))
     b.close()

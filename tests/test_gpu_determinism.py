@@ -1,0 +1,106 @@
+"""Run-to-run and batch-composition determinism of the HIP path.
+
+Every reduction on the token path has a fixed order: wavefront and workgroup sums in index order,
+split-K partials combined in split order by the last workgroup to arrive (no float atomics), the
+batched residual updates' K summed in blocks fixed by K alone.  So:
+  - the same input gives the same bits twice (single stream and batch);
+  - a stream's joint.enc rows and tokens in a batch do not depend on the other streams of the batch
+    (their number, lengths, starts), because every batched kernel computes a row the same way
+    whatever the number of rows in the launch.
+"""
+import numpy as np
+import pytest
+
+import mel_ref
+import oracle
+import synth
+from conftest import model_dir
+
+pytestmark = pytest.mark.gpu
+
+LAT_RIGHT = {80: 0, 160: 1, 320: 3, 560: 6, 1120: 13}
+
+
+def bits(a):
+    return np.ascontiguousarray(a, np.float32).view(np.uint32)
+
+
+@pytest.mark.parametrize("latency", [80, 560, 1120])
+def test_session_repeatable(latency):
+    """Two sessions on the same audio: identical per-layer rows, joint.enc rows and tokens (80 ms
+    covers the fused attention + out_proj combine, 560 / 1120 ms the few-row K split)."""
+    import nemoasr
+
+    mdir = model_dir("full")
+    d = oracle.Model(mdir, "en-US").dims
+    mel = mel_ref.logmel(synth.make_audio(2.0, seed=31))
+    out = []
+    for _ in range(2):
+        s = nemoasr.Session(mdir, "en-US", latency)
+        s.set_dump(True)
+        s.feed_mel(mel, final=True)
+        out.append((s.tokens(), s.dumps(d.n_layers, d.d_model, d.joint_hidden)))
+        s.close()
+    (t0, (l0, p0, j0)), (t1, (l1, p1, j1)) = out
+    assert t0 == t1
+    assert np.array_equal(bits(l0), bits(l1)) and np.array_equal(bits(j0), bits(j1))
+
+
+def test_session_graphs_repeatable():
+    """Graph replay twice from a fresh session: the same tokens."""
+    import nemoasr
+
+    mdir = model_dir("full")
+    mel = mel_ref.logmel(synth.make_audio(3.0, seed=32))
+    toks = []
+    for _ in range(2):
+        s = nemoasr.Session(mdir, "en-US", 80)
+        s.use_graphs(True)
+        s.feed_mel(mel, final=True)
+        toks.append(s.tokens())
+        s.close()
+    assert toks[0] == toks[1]
+
+
+def drive(b, mels, starts, piece):
+    pos = [0] * len(mels)
+    tick = 0
+    while any(p < m.shape[0] for p, m in zip(pos, mels)):
+        for s, m in enumerate(mels):
+            if tick < starts[s] or pos[s] >= m.shape[0]:
+                continue
+            end = min(pos[s] + piece, m.shape[0])
+            b.push_mel(s, m[pos[s]:end], final=end >= m.shape[0])
+            pos[s] = end
+        b.step()
+        tick += 1
+    b.run()
+
+
+@pytest.mark.parametrize("latency", [560, 1120])
+def test_batch_composition_independent(latency):
+    """Full model: a batch of nine streams (different lengths, staggered starts) run twice, and the
+    same stream alone in a batch of one and in a batch of three.  The stream's joint.enc rows must be
+    bit-identical in all four runs and its tokens identical; the nine streams identical between the
+    two full runs."""
+    import nemoasr
+
+    mdir = model_dir("full")
+    J = oracle.Model(mdir, "en-US").dims.joint_hidden
+    secs = [2.4, 1.1, 3.0, 2.2, 0.6, 2.8, 1.7, 2.5, 1.9]
+    mels = [mel_ref.logmel(synth.make_audio(t, seed=700 + i)) for i, t in enumerate(secs)]
+    starts = [0, 1, 0, 3, 2, 0, 5, 1, 4]
+    piece = 8 * (LAT_RIGHT[latency] + 1)
+    runs = []
+    for sel in (list(range(9)), list(range(9)), [2], [7, 2, 4]):
+        b = nemoasr.Batch(mdir, "en-US", latency, streams=len(sel))
+        b.set_dump(True)
+        drive(b, [mels[i] for i in sel], [starts[i] if len(sel) > 1 else 0 for i in sel], piece)
+        runs.append({i: (b.tokens(k), b.joint_enc(k, J)) for k, i in enumerate(sel)})
+        b.close()
+    for i in range(9):
+        assert runs[0][i][0] == runs[1][i][0], i
+        assert np.array_equal(bits(runs[0][i][1]), bits(runs[1][i][1])), i
+    for r in runs[2:]:
+        assert r[2][0] == runs[0][2][0]
+        assert np.array_equal(bits(r[2][1]), bits(runs[0][2][1]))

@@ -100,8 +100,9 @@ def test_gemm_many_rows(gpu, M, N, K, act):
 
 
 # batched multi-stream shapes (64 streams x 7 rows, 256 x 14) through the many-row MFMA kernels:
-# each tile shape (128x128, 64x128, 64x64, plain and GLU), K split over workgroups with atomic
-# accumulation, row counts that are not tile multiples, K of one or two steps, row maps
+# each tile shape (128x128, 64x128, 64x64, plain and GLU), the residual updates' K split over
+# workgroups (by tile count, never, always), row counts that are not tile multiples, K of one or
+# two steps, row maps
 @pytest.mark.parametrize("M,N,K,act,acc,bias", [
     (448, 4096, 1024, 1, 0, False), (448, 1024, 4096, 0, 1, False), (448, 3072, 1024, 0, 0, False),
     (448, 2048, 1024, 3, 0, False), (448, 1024, 1024, 0, 1, False), (448, 640, 1024, 0, 0, True),
@@ -111,11 +112,11 @@ def test_gemm_many_rows(gpu, M, N, K, act):
     (20, 3072, 1024, 0, 0, False), (448, 2560, 1280, 0, 0, True), (1024, 1088, 640, 0, 0, True),
     (64, 256, 32, 2, 0, True), (96, 128, 64, 0, 1, False), (64, 1024, 1024, 0, 1, False),
     (64, 2560, 1280, 0, 1, False), (224, 1024, 1024, 0, 1, False), (896, 1024, 4096, 0, 1, False)])
-@pytest.mark.parametrize("k64", [1, 0])
-def test_gemm_batched_rows(gpu, M, N, K, act, acc, bias, k64):
+@pytest.mark.parametrize("split", [-1, 0, 1])
+def test_gemm_batched_rows(gpu, M, N, K, act, acc, bias, split):
     import nemoasr
 
-    prev = nemoasr.lib().nk_gemm_mx_k64(k64)
+    prev = nemoasr.lib().nk_gemm_split(split)
     rng = np.random.default_rng([M, N, K, act])
     W = _w(rng, N, K)
     A = rng.standard_normal((M, K)).astype(np.float32)
@@ -125,9 +126,52 @@ def test_gemm_batched_rows(gpu, M, N, K, act, acc, bias, k64):
     try:
         got = run_gemm(gpu, A, W, b, act, acc, 0.5 if acc else 1.0, C0=C0)
     finally:
-        nemoasr.lib().nk_gemm_mx_k64(prev)
+        nemoasr.lib().nk_gemm_split(prev)
     ref = oracle.gemm(A, W, b, act, acc, 0.5 if acc else 1.0, C0=C0)
     assert rel_err(got, ref) < GEMM_TOL, (M, N, K, act)
+
+
+@pytest.mark.parametrize("N,K", [(1024, 1024), (1024, 4096), (1024, 2048)])
+def test_gemm_residual_bits(gpu, N, K):
+    """The many-row residual update (C += alpha A W^T) gives the same bits whether its K is split
+    over workgroups or not, from one launch to the next, and whatever the number of rows in the
+    launch (a row computed alone equals the same row in a launch of 3584): the property that makes
+    a stream's results independent of the other streams of a batch step."""
+    import nemoasr
+
+    L = nemoasr.lib()
+    rng = np.random.default_rng([N, K])
+    W = _w(rng, N, K)
+    A = rng.standard_normal((3584, K)).astype(np.float32)
+    C0 = rng.standard_normal((3584, N)).astype(np.float32)
+    outs = {}
+    try:
+        for M in (3584, 448, 64, 17):
+            for split in (0, 1, -1, -1):
+                L.nk_gemm_split(split)
+                outs.setdefault(M, []).append(run_gemm(gpu, A[:M], W, None, 0, True, 0.5, C0=C0[:M].copy()))
+    finally:
+        L.nk_gemm_split(-1)
+    for M, runs in outs.items():
+        for r in runs[1:]:
+            assert np.array_equal(r.view(np.uint32), runs[0].view(np.uint32)), M
+        assert np.array_equal(runs[0].view(np.uint32), outs[3584][0][:M].view(np.uint32)), M
+    ref = oracle.gemm(A[:448], W, None, 0, True, 0.5, C0=C0[:448])
+    assert rel_err(outs[448][0], ref) < GEMM_TOL
+
+
+@pytest.mark.parametrize("M,N,K", [(7, 1024, 4096), (14, 1024, 1024), (10, 1024, 4096)])
+def test_gemm_few_rows_split_repeatable(gpu, M, N, K):
+    """The few-row residual update splits K over four workgroups; their partials are combined in a
+    fixed order, so repeated launches give the same bits (and the oracle's values)."""
+    rng = np.random.default_rng([M, N, K, 5])
+    W = _w(rng, N, K)
+    A = rng.standard_normal((M, K)).astype(np.float32)
+    C0 = rng.standard_normal((M, N)).astype(np.float32)
+    runs = [run_gemm(gpu, A, W, None, 0, True, 0.5, C0=C0.copy()) for _ in range(4)]
+    for r in runs[1:]:
+        assert np.array_equal(r.view(np.uint32), runs[0].view(np.uint32))
+    assert rel_err(runs[0], oracle.gemm(A, W, None, 0, True, 0.5, C0=C0)) < GEMM_TOL
 
 
 @pytest.mark.parametrize("M,V", [(576, 1025), (64, 1025), (100, 97), (4096, 1025)])

@@ -5,7 +5,8 @@ on seeded random-init checkpoints and seeded synthetic audio; the oracle runs th
 through its CPU restatement.  Gates (from the scope of this path):
   - per-layer encoder activations: max|gpu - oracle| / max|oracle| <= 2e-3 for every layer;
   - joint.enc rows (the joint's encoder input): <= 1e-3; joint logits are checked per kernel;
-  - emitted token ids: identical.
+  - emitted token ids: identical, except at a float tie of the oracle's greedy decision
+    (conftest.check_tokens: top-2 joint margin below TOKEN_TIE), where the comparison stops.
 """
 import os
 import wave
@@ -16,7 +17,7 @@ import pytest
 import mel_ref
 import oracle
 import synth
-from conftest import model_dir, rel_err
+from conftest import check_tokens, model_dir, rel_err
 
 pytestmark = pytest.mark.gpu
 
@@ -54,10 +55,7 @@ def check_parity(om, o, s, d, check_dumps=True):
         assert max(errs) <= 2e-3, errs
         assert rel_err(gp, op) <= 2e-3
         assert rel_err(gj, oj) <= 1e-3
-    if toks_g != o.tokens:
-        first = next(i for i, (a, b) in enumerate(zip(toks_g + [-1], o.tokens + [-2])) if a != b)
-        _, margin = o.joint_log()
-        pytest.fail(f"tokens differ at {first} of {len(o.tokens)}; oracle min top-2 margin {margin.min():.3g}")
+    check_tokens(toks_g, o.tokens, o.token_margins())
 
 
 @pytest.mark.parametrize("latency", [80, 560, 1120])
@@ -88,12 +86,15 @@ def test_graph_replay_matches(latency):
 @pytest.mark.parametrize("latency", [80, 160])
 def test_fused_launches_match_separate(latency):
     """The one- and two-row chunks' fused launches (attention + out_proj, dwconv + pw2) against the
-    separate launches: every layer's activations within float rounding, identical tokens."""
+    separate launches: every layer's activations within float rounding, the oracle's tokens."""
     import nemoasr
 
     mdir = model_dir("full")
-    d = oracle.Model(mdir, "en-US").dims
+    om = oracle.Model(mdir, "en-US")
+    d = om.dims
     mel = mel_ref.logmel(synth.make_audio(1.5, seed=21))
+    o = oracle.Session(om, LAT_RIGHT[latency])
+    o.feed_mel(mel, final=True)
     out = []
     for fuse in (True, False):
         s = nemoasr.Session(mdir, "en-US", latency)
@@ -103,7 +104,8 @@ def test_fused_launches_match_separate(latency):
         out.append((s.tokens(), s.dumps(d.n_layers, d.d_model, d.joint_hidden)))
         s.close()
     (tf, (lf, pf, jf)), (ts, (ls, ps, js)) = out
-    assert tf == ts
+    check_tokens(tf, o.tokens, o.token_margins(), "fused: ")
+    check_tokens(ts, o.tokens, o.token_margins(), "separate: ")
     assert rel_err(lf, ls) < 1e-5 and rel_err(jf, js) < 1e-5
 
 
@@ -121,9 +123,9 @@ def test_audio_api_tiny():
     text = ""
     for i in range(0, audio.size, 1600):
         text += s.feed(audio[i:i + 1600], final=i + 1600 >= audio.size)
-    assert s.tokens() == o.tokens
-    st = s.stats()
-    assert st["tokens"] == len(o.tokens) and st["chunks"] == o.chunks
+    if check_tokens(s.tokens(), o.tokens, o.token_margins()) is None:
+        assert s.stats()["tokens"] == len(o.tokens)
+    assert s.stats()["chunks"] == o.chunks
     s.close()
 
 
@@ -143,7 +145,7 @@ def test_reset_replays_identically():
     o = oracle.Session(om, 0)
     o.feed_mel(mel, final=True)
     s.feed_mel(mel, final=True)
-    assert s.tokens() == o.tokens
+    check_tokens(s.tokens(), o.tokens, o.token_margins())
     s.close()
 
 
@@ -182,3 +184,62 @@ def test_parity_harness_end_to_end(tmp_path, latency):
     print("\n".join(rep))
     assert ok, rep
     assert res["mel"].shape == mel.shape and len(o.tokens) > 0
+
+
+def _golden_cases():
+    import json
+
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "tiny_tokens.json")
+    with open(path) as f:
+        return json.load(f)["cases"]
+
+
+RIGHT_LAT = {v: k for k, v in LAT_RIGHT.items()}
+
+
+@pytest.mark.parametrize("case", _golden_cases(), ids=lambda c: c["name"])
+def test_golden_token_cases(case):
+    """The committed token fixtures (tests/golden/tiny_tokens.json: right contexts 0/6/13, en-US
+    and auto prompts, blank-biased models) through the public API.  The blank-biased cases must
+    actually take the blank branches of the greedy rule (symbol reset on a blank frame, first
+    non-blank frame wins, later frames redone): fewer tokens than frames x max_symbols."""
+    import nemoasr
+
+    mdir = model_dir("tiny", case["model_seed"], case["blank_bias"])
+    lat = RIGHT_LAT[case["right"]]
+    mel = mel_ref.logmel(synth.make_audio(case["seconds"], seed=case["audio_seed"]))
+    om = oracle.Model(mdir, case["language"])
+    o = oracle.Session(om, case["right"])
+    o.feed_mel(mel, final=True)
+    assert o.tokens == case["tokens"]
+    for graphs in (False, True):
+        s = nemoasr.Session(mdir, case["language"], lat)
+        s.use_graphs(graphs)
+        s.feed_mel(mel, final=True)
+        check_tokens(s.tokens(), case["tokens"], o.token_margins(), f"graphs {graphs}: ")
+        assert s.stats()["chunks"] == case["chunks"]
+        s.close()
+    if case["blank_bias"] > 0:
+        assert len(case["tokens"]) < case["frames"] * om.dims.max_symbols
+
+
+@pytest.mark.parametrize("latency,seconds", [(80, 20.0), (560, 24.0)])
+def test_stream_cache_compaction(latency, seconds):
+    """A single stream long enough that its append-only K/V and conv caches (56 + 8 x 16 rows) are
+    compacted at least once (past 184 encoder rows: ~15 s of audio), against the oracle, whose
+    histories are plain sliding windows: compaction must be invisible in every layer's rows and in
+    the tokens (the reference's epoch rule, src/encoder.c:199-211, :256)."""
+    mdir = model_dir("tiny")
+    om, o, s, d = run_pair(mdir, latency, seconds, seed=17, graphs=False)
+    assert o.frames > 56 + 8 * 16
+    check_parity(om, o, s, d)
+    s.close()
+
+
+@pytest.mark.parametrize("latency,seconds", [(80, 20.0), (560, 24.0)])
+def test_stream_cache_compaction_graphs(latency, seconds):
+    """The same through captured chunk graphs (compaction is a launch outside the chunk graph)."""
+    mdir = model_dir("tiny")
+    om, o, s, d = run_pair(mdir, latency, seconds, seed=17, graphs=True)
+    check_parity(om, o, s, d, check_dumps=False)
+    s.close()

@@ -205,3 +205,46 @@ def test_golden_tokens():
         s = oracle.Session(om, case["right"])
         s.feed_mel(mel, final=True)
         assert s.tokens == case["tokens"], case["name"]
+
+
+@pytest.mark.parametrize("language", ["en-US", "auto"])
+def test_prompt_fold_equals_one_hot_concat(language):
+    """Pins the oracle's prompt fold (b_eff = b0 + W0[:, D + idx] in f32, src/model.c:312-322)
+    against the unfolded layer it stands for: prompted = ReLU([h | one-hot(idx)] W0^T + b0) W2^T + b2
+    in float64 over the full D + num_prompts columns of W0, with idx the language's entry in
+    config.json's prompt_dictionary and h the last block's output rows of the same stream.  A wrong
+    prompt index, a dropped one-hot term or a one-hot placed at column idx instead of D + idx all fail."""
+    mdir = model_dir("tiny")
+    cfg = json.load(open(os.path.join(mdir, "config.json")))
+    dic = cfg["prompt"]["prompt_dictionary"]
+    idx = dic[language]
+    om = oracle.Model(mdir, language)
+    d = om.dims
+    o = oracle.Session(om, 6, dump=True)
+    o.feed_mel(mel_ref.logmel(synth.make_audio(1.5, seed=41)), final=True)
+    lay, prompted, _, _ = o.dumps()
+    h = lay[:, -1].astype(np.float64)
+    t = synth.load_safetensors(os.path.join(mdir, "model.safetensors"))
+
+    def w(name):
+        raw, shape = t[name]
+        return oracle.bf16_to_f32(np.asarray(raw)).reshape(shape).astype(np.float64)
+
+    W0, b0, W2, b2 = (w(n) for n in ("prompt_kernel.0.weight", "prompt_kernel.0.bias", "prompt_kernel.2.weight",
+                                      "prompt_kernel.2.bias"))
+    D, NP = d.d_model, d.num_prompts
+    assert W0.shape == (d.prompt_hidden, D + NP)
+
+    def unfolded(col):
+        x = np.zeros((h.shape[0], D + NP))
+        x[:, :D] = h
+        if col is not None:
+            x[:, col] = 1.0
+        return np.maximum(x @ W0.T + b0, 0.0) @ W2.T + b2
+
+    ref = unfolded(D + idx)
+    err = float(np.max(np.abs(prompted - ref)) / np.max(np.abs(ref)))
+    assert err < 1e-5, err
+    other = next(v for k, v in dic.items() if v != idx)
+    for wrong in (unfolded(D + other), unfolded(None), unfolded(idx)):
+        assert float(np.max(np.abs(prompted - wrong)) / np.max(np.abs(ref))) > 1e-2
