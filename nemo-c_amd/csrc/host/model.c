@@ -1,9 +1,10 @@
 #include "model.h"
 #include "nemo_kernels.h"
-#include "safetensors.h"
+#include "ckpt.h"
 #include "../kernel_params.h"
 #include <fcntl.h>
 #include <math.h>
+#include <stddef.h>
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
@@ -30,55 +31,91 @@ static char *slurp(const char *path, size_t *len) {
     return b;
 }
 
-/* src/model.c:125-172: configuration keys, defaults and the supported-architecture checks */
-static int parse_cfg(model_t *m, char *err, size_t errlen) {
-    const jn_t *c = m->config, *enc = jn_get(c, "encoder"), *pre = jn_get(c, "preprocessor");
-    const jn_t *pr = jn_get(c, "prompt"), *dec = jn_get(c, "decoder"), *jo = jn_get(c, "joint");
-    if (!enc || !pre || !pr || !dec || !jo) { snprintf(err, errlen, "config.json missing sections"); return -1; }
+/* config.json: the keys the reference reads and its defaults for absent ones (src/model.c:125-172),
+ * as a table of (section, key, default) -> integer field. */
+typedef struct { const char *section, *key; int dflt; size_t field; } cfg_key_t;
+#define CFG_FIELD(f) offsetof(model_cfg_t, f)
+static const cfg_key_t k_cfg_keys[] = {
+    { "encoder", "feat_in", 128, CFG_FIELD(feat_in) },
+    { "encoder", "n_layers", 24, CFG_FIELD(n_layers) },
+    { "encoder", "d_model", 1024, CFG_FIELD(d_model) },
+    { "encoder", "n_heads", 8, CFG_FIELD(n_heads) },
+    { "encoder", "ff_expansion_factor", 4, CFG_FIELD(d_ff) },          /* scaled by d_model below */
+    { "encoder", "subsampling_factor", 8, CFG_FIELD(subsampling) },
+    { "encoder", "subsampling_conv_channels", 256, CFG_FIELD(sub_channels) },
+    { "encoder", "conv_kernel_size", 9, CFG_FIELD(conv_kernel) },
+    { "prompt", "num_prompts", 128, CFG_FIELD(num_prompts) },
+    { "prompt", "prompt_hidden", 2048, CFG_FIELD(prompt_hidden) },
+    { "decoder", "pred_hidden", 640, CFG_FIELD(pred_hidden) },
+    { "decoder", "pred_rnn_layers", 2, CFG_FIELD(pred_layers) },
+    { "decoder", "vocab_size", 13087, CFG_FIELD(vocab_size) },
+    { "joint", "joint_hidden", 640, CFG_FIELD(joint_hidden) },
+    { "joint", "num_classes", 13087, CFG_FIELD(num_classes) },         /* + 1 (blank) below */
+    { NULL, "max_symbols", 10, CFG_FIELD(max_symbols) },                /* top level */
+};
+
+static int cfg_int(const jn_t *sec, const char *key, int dflt) { return (int)jn_num(jn_get(sec, key), dflt); }
+
+/* The shapes the kernels and launch plans are written for; anything else is refused at load. */
+static const char *unsupported(const model_cfg_t *g) {
+    if (g->pred_layers != 2) return "a prediction network of other than 2 LSTM layers";
+    if (g->head_dim != 128) return "an attention head width other than 128";
+    if (g->conv_kernel != 9 || g->subsampling != 8) return "a conv kernel other than 9 or subsampling other than 8";
+    if (g->d_model % 32 || g->d_model > NK_ROW_MAX || g->prompt_hidden % 32 || g->sub_channels % 32)
+        return "model widths that are not multiples of 32 (or above the row limit)";
+    if (g->pred_hidden % 8 || g->joint_hidden % 8 || g->joint_hidden > NK_JOINT_MAX_H) return "decoder widths";
+    if (g->num_classes > NK_JOINT_GROUPS * NK_JOINT_WAVES * 1024) return "a vocabulary above the joint kernel's limit";
+    return NULL;
+}
+
+static int read_config(model_t *m, char *err, size_t errlen) {
+    const jn_t *root = m->config, *pre = jn_get(root, "preprocessor"), *enc = jn_get(root, "encoder");
+    const jn_t *prm = jn_get(root, "prompt");
+    if (!pre || !enc || !prm || !jn_get(root, "decoder") || !jn_get(root, "joint")) {
+        snprintf(err, errlen, "config.json: need the preprocessor, encoder, prompt, decoder and joint sections");
+        return -1;
+    }
     model_cfg_t *g = &m->cfg;
-    g->feat_in = (int)jn_num(jn_get(enc, "feat_in"), 128);
-    g->n_layers = (int)jn_num(jn_get(enc, "n_layers"), 24);
-    g->d_model = (int)jn_num(jn_get(enc, "d_model"), 1024);
-    g->n_heads = (int)jn_num(jn_get(enc, "n_heads"), 8);
-    g->head_dim = g->n_heads ? g->d_model / g->n_heads : 0;
-    g->d_ff = g->d_model * (int)jn_num(jn_get(enc, "ff_expansion_factor"), 4);
-    g->subsampling = (int)jn_num(jn_get(enc, "subsampling_factor"), 8);
-    g->sub_channels = (int)jn_num(jn_get(enc, "subsampling_conv_channels"), 256);
-    g->conv_kernel = (int)jn_num(jn_get(enc, "conv_kernel_size"), 9);
-    g->num_prompts = (int)jn_num(jn_get(pr, "num_prompts"), 128);
-    g->prompt_hidden = (int)jn_num(jn_get(pr, "prompt_hidden"), 2048);
-    g->pred_hidden = (int)jn_num(jn_get(dec, "pred_hidden"), 640);
-    g->pred_layers = (int)jn_num(jn_get(dec, "pred_rnn_layers"), 2);
-    g->vocab_size = (int)jn_num(jn_get(dec, "vocab_size"), 13087);
+    for (size_t i = 0; i < sizeof k_cfg_keys / sizeof k_cfg_keys[0]; ++i) {
+        const cfg_key_t *k = &k_cfg_keys[i];
+        *(int *)((char *)g + k->field) = cfg_int(k->section ? jn_get(root, k->section) : root, k->key, k->dflt);
+    }
+    g->d_ff *= g->d_model;
+    g->head_dim = g->n_heads > 0 ? g->d_model / g->n_heads : 0;
     g->blank_id = g->vocab_size;
-    g->joint_hidden = (int)jn_num(jn_get(jo, "joint_hidden"), 640);
-    g->num_classes = (int)jn_num(jn_get(jo, "num_classes"), 13087) + 1;
-    g->max_symbols = (int)jn_num(jn_get(c, "max_symbols"), 10);
+    g->num_classes += 1;
     g->ln_eps = 1e-5f;
-    const jn_t *acs = jn_get(enc, "att_context_size");
+    /* att_context_size: [[left, right], ...], the trained (left, right) pairs */
+    const jn_t *ctx = jn_get(enc, "att_context_size");
     g->n_trained = 0;
-    for (size_t i = 0; i < jn_len(acs) && i < 8; ++i) {
-        g->att_left = (int)jn_num(jn_at(jn_at(acs, i), 0), 56);
-        g->trained_right[g->n_trained++] = (int)jn_num(jn_at(jn_at(acs, i), 1), 13);
+    for (size_t i = 0; i < jn_len(ctx) && g->n_trained < 8; ++i) {
+        g->att_left = (int)jn_num(jn_at(jn_at(ctx, i), 0), 56);
+        g->trained_right[g->n_trained++] = (int)jn_num(jn_at(jn_at(ctx, i), 1), 13);
     }
-    g->att_right_default = (int)jn_num(jn_at(jn_get(c, "default_att_context_size"), 1), 13);
-    if (g->pred_layers != 2) { snprintf(err, errlen, "only 2 LSTM layers supported"); return -1; }
-    if (g->head_dim != 128 || g->joint_hidden > NK_JOINT_MAX_H || g->conv_kernel != 9 || g->subsampling != 8 ||
-        g->d_model % 32 || g->d_model > NK_ROW_MAX || g->prompt_hidden % 32 || g->sub_channels % 32 ||
-        g->pred_hidden % 8 || g->joint_hidden % 8 || g->num_classes > NK_JOINT_GROUPS * NK_JOINT_WAVES * 1024) {
-        snprintf(err, errlen, "unexpected architecture dims");
+    g->att_right_default = (int)jn_num(jn_at(jn_get(root, "default_att_context_size"), 1), 13);
+    const char *why = unsupported(g);
+    if (why) {
+        snprintf(err, errlen, "config.json: unsupported architecture (%s)", why);
         return -1;
     }
-    if ((int)jn_num(jn_get(pre, "sample_rate"), 16000) != 16000 || (int)jn_num(jn_get(pre, "features"), 128) != 128) {
-        snprintf(err, errlen, "unexpected preprocessor config");
+    if (cfg_int(pre, "sample_rate", 16000) != 16000 || cfg_int(pre, "features", 128) != 128) {
+        snprintf(err, errlen, "config.json: the front end must be 16 kHz, 128 mel bins");
         return -1;
     }
-    int maxr = 0;
-    for (int i = 0; i < g->n_trained; ++i) if (g->trained_right[i] > maxr) maxr = g->trained_right[i];
-    m->Lmax = g->att_left + maxr + 1 + 2; /* a final boundary window can yield up to chunk + 2 rows */
-    if (m->Lmax > NK_ATT_MAX_L) { snprintf(err, errlen, "attention window %d exceeds %d", m->Lmax, NK_ATT_MAX_L); return -1; }
-    m->prompt_dict = jn_get(pr, "prompt_dictionary");
-    if (vocab_load(jn_get(c, "vocabulary"), &m->vocab)) { snprintf(err, errlen, "vocabulary missing"); return -1; }
+    /* attention window: left context + the widest trained chunk + the two extra rows a final
+     * boundary window can yield */
+    int widest = 0;
+    for (int i = 0; i < g->n_trained; ++i) widest = g->trained_right[i] > widest ? g->trained_right[i] : widest;
+    m->Lmax = g->att_left + widest + 1 + 2;
+    if (m->Lmax > NK_ATT_MAX_L) {
+        snprintf(err, errlen, "config.json: attention window of %d rows, the kernels take %d", m->Lmax, NK_ATT_MAX_L);
+        return -1;
+    }
+    m->prompt_dict = jn_get(prm, "prompt_dictionary");
+    if (vocab_load(jn_get(root, "vocabulary"), &m->vocab)) {
+        snprintf(err, errlen, "config.json: no vocabulary");
+        return -1;
+    }
     return 0;
 }
 
@@ -114,13 +151,24 @@ static void addf(reqs_t *r, const char *name, size_t numel, const float **dst) {
     r->nf++;
 }
 
-/* src/model.c:41-47: tensor present, BF16, and (if given) with the expected element count */
-static const st_entry_t *need(const st_map_t *st, const char *name, size_t numel, char *err, size_t errlen) {
-    const st_entry_t *t = st_lookup(st, name);
-    if (!t) { snprintf(err, errlen, "missing tensor %s", name); return NULL; }
-    if (t->dtype != STD_BF16) { snprintf(err, errlen, "tensor %s is not bf16", name); return NULL; }
-    if (numel && t->numel != numel) { snprintf(err, errlen, "tensor %s has %zu elements, expected %zu", name, t->numel, numel); return NULL; }
-    return t;
+/* Every tensor the model reads must be present, bf16 and of the expected element count (the
+ * reference's checks, src/model.c:41-47). */
+static const ck_tensor_t *need(const ckpt_t *ck, const char *name, size_t numel, char *err, size_t errlen) {
+    const ck_tensor_t *t = ckpt_find(ck, name);
+    if (!t) snprintf(err, errlen, "checkpoint has no tensor %s", name);
+    else if (t->dtype != CK_BF16) snprintf(err, errlen, "checkpoint tensor %s: expected bf16", name);
+    else if (numel && t->numel != numel) snprintf(err, errlen, "checkpoint tensor %s: %zu elements, expected %zu", name, t->numel, numel);
+    else return t;
+    return NULL;
+}
+
+/* a bf16 tensor widened to f32 on the host */
+static int read_widened(const ckpt_t *ck, const ck_tensor_t *t, float *dst) {
+    uint16_t *raw = malloc(t->bytes ? t->bytes : 2);
+    if (!raw || ckpt_read(ck, t, raw)) { free(raw); return -1; }
+    for (size_t k = 0; k < t->numel; ++k) dst[k] = ck_bf16(raw[k]);
+    free(raw);
+    return 0;
 }
 
 #define WALIGN 4096
@@ -139,13 +187,13 @@ model_t *model_load(const char *dir, char *err, size_t errlen) {
     m->config = jn_parse(txt, len, jerr, sizeof jerr);
     free(txt);
     if (!m->config) { snprintf(err, errlen, "config.json: %s", jerr); free(m); return NULL; }
-    if (parse_cfg(m, err, errlen)) { model_free(m); return NULL; }
-    st_map_t st;
+    if (read_config(m, err, errlen)) { model_free(m); return NULL; }
     gpu_buf_t *wpos_d = NULL;
     snprintf(path, sizeof path, "%s/model.safetensors", dir);
-    if (st_map(path, &st, err, errlen)) { model_free(m); return NULL; }
+    ckpt_t *st = ckpt_open(path, err, errlen);
+    if (!st) { model_free(m); return NULL; }
     m->gpu = gpu_create(err, errlen);
-    if (!m->gpu) { st_unmap(&st); model_free(m); return NULL; }
+    if (!m->gpu) { ckpt_close(st); model_free(m); return NULL; }
 
     const model_cfg_t *g = &m->cfg;
     const size_t D = (size_t)g->d_model, CH = (size_t)g->sub_channels, FF = (size_t)g->d_ff, nl = (size_t)g->n_layers;
@@ -154,7 +202,7 @@ model_t *model_load(const char *dir, char *err, size_t errlen) {
     int freq = g->feat_in;
     for (int i = 0; i < 3; ++i) freq = freq / 2 + 1;
     m->sub_freq_out = freq;
-    if ((CH * (size_t)freq) % 32) { snprintf(err, errlen, "unexpected subsampling width"); st_unmap(&st); model_free(m); return NULL; }
+    if ((CH * (size_t)freq) % 32) { snprintf(err, errlen, "unsupported subsampling output width"); ckpt_close(st); model_free(m); return NULL; }
     m->L = calloc(nl, sizeof *m->L);
 
     reqs_t r = { 0 };
@@ -212,24 +260,24 @@ model_t *model_load(const char *dir, char *err, size_t errlen) {
 
     /* validate every tensor, size the arenas */
     size_t wbytes = 0, fcount = 0;
-    const st_entry_t **bt = calloc(r.nb, sizeof *bt), **ft = calloc(r.nf, sizeof *ft);
+    const ck_tensor_t **bt = calloc(r.nb, sizeof *bt), **ft = calloc(r.nf, sizeof *ft);
     int ok = 1;
     for (size_t i = 0; i < r.nb && ok; ++i) {
-        if (!(bt[i] = need(&st, r.b[i].name, r.b[i].numel, err, errlen))) ok = 0;
+        if (!(bt[i] = need(st, r.b[i].name, r.b[i].numel, err, errlen))) ok = 0;
         else {
             /* q|k|v pack tightly so the three form one matrix */
             const int packed = strstr(r.b[i].name, "linear_k.weight") || strstr(r.b[i].name, "linear_v.weight");
-            wbytes = (packed ? wbytes : up_to(wbytes, WALIGN)) + bt[i]->nbytes;
+            wbytes = (packed ? wbytes : up_to(wbytes, WALIGN)) + bt[i]->bytes;
         }
     }
     for (size_t i = 0; i < r.nf && ok; ++i) {
-        if (!(ft[i] = need(&st, r.f[i].name, r.f[i].numel, err, errlen))) ok = 0;
+        if (!(ft[i] = need(st, r.f[i].name, r.f[i].numel, err, errlen))) ok = 0;
         else fcount += up_to(ft[i]->numel, 64);
     }
-    const st_entry_t *emb = ok ? need(&st, "decoder.prediction.embed.weight", (size_t)(g->vocab_size + 1) * P, err, errlen) : NULL;
-    const st_entry_t *w0 = ok ? need(&st, "prompt_kernel.0.weight", PH * (D + NP), err, errlen) : NULL;
-    const st_entry_t *b0 = ok ? need(&st, "prompt_kernel.0.bias", PH, err, errlen) : NULL;
-    const st_entry_t *wpos0 = ok ? need(&st, "encoder.layers.0.self_attn.linear_pos.weight", D * D, err, errlen) : NULL;
+    const ck_tensor_t *emb = ok ? need(st, "decoder.prediction.embed.weight", (size_t)(g->vocab_size + 1) * P, err, errlen) : NULL;
+    const ck_tensor_t *w0 = ok ? need(st, "prompt_kernel.0.weight", PH * (D + NP), err, errlen) : NULL;
+    const ck_tensor_t *b0 = ok ? need(st, "prompt_kernel.0.bias", PH, err, errlen) : NULL;
+    const ck_tensor_t *wpos0 = ok ? need(st, "encoder.layers.0.self_attn.linear_pos.weight", D * D, err, errlen) : NULL;
     if (!ok || !emb || !w0 || !b0 || !wpos0) goto fail;
     m->warena = gpu_buf_alloc(m->gpu, wbytes);
     m->farena = gpu_buf_alloc(m->gpu, fcount * sizeof(float));
@@ -246,50 +294,49 @@ model_t *model_load(const char *dir, char *err, size_t errlen) {
         for (size_t i = 0; i < r.nb; ++i) {
             const int packed = strstr(r.b[i].name, "linear_k.weight") || strstr(r.b[i].name, "linear_v.weight");
             if (!packed) off = up_to(off, WALIGN);
-            rg[i] = (gpu_file_range_t){ bt[i]->offset, bt[i]->nbytes, wbase + off };
+            rg[i] = (gpu_file_range_t){ bt[i]->at, bt[i]->bytes, wbase + off };
             *r.b[i].dst = (const uint16_t *)(wbase + off);
-            off += bt[i]->nbytes;
+            off += bt[i]->bytes;
         }
         int urc = 0;
         for (size_t l = 0; l < nl && !urc; ++l) {
             snprintf(n, sizeof n, "encoder.layers.%zu.self_attn.linear_pos.weight", l);
-            const st_entry_t *t = need(&st, n, D * D, err, errlen);
+            const ck_tensor_t *t = need(st, n, D * D, err, errlen);
             if (!t) urc = -2;
-            else rg[r.nb + l] = (gpu_file_range_t){ t->offset, t->nbytes, (uint16_t *)gpu_buf_dptr(wpos_d) + l * D * D };
+            else rg[r.nb + l] = (gpu_file_range_t){ t->at, t->bytes, (uint16_t *)gpu_buf_dptr(wpos_d) + l * D * D };
         }
         if (!urc) {
-            const int fd = open(path, O_RDONLY);
-            urc = fd < 0 ? -3 : gpu_upload_file(m->gpu, fd, rg, r.nb + nl);
-            if (fd >= 0) close(fd);
-            if (urc == -3) snprintf(err, errlen, "cannot open %s", path);
-            else if (urc) snprintf(err, errlen, "weight upload: %s", gpu_last_error(m->gpu));
+            urc = gpu_upload_file(m->gpu, ckpt_fd(st), rg, r.nb + nl);
+            if (urc) snprintf(err, errlen, "weight upload: %s", gpu_last_error(m->gpu));
         }
         free(rg);
         if (urc) goto fail;
         float *fh = calloc(fcount ? fcount : 1, sizeof(float));
         float *fbase = gpu_buf_dptr(m->farena);
         size_t fo = 0;
-        for (size_t i = 0; i < r.nf; ++i) {
-            const uint16_t *src = st_ptr(&st, ft[i]);
-            for (size_t k = 0; k < ft[i]->numel; ++k) fh[fo + k] = st_bf16(src[k]);
+        int rrc = !fh;
+        for (size_t i = 0; i < r.nf && !rrc; ++i) {
+            rrc = read_widened(st, ft[i], fh + fo);
             *r.f[i].dst = fbase + fo;
             fo += up_to(ft[i]->numel, 64);
         }
-        const int rc = gpu_upload(m->gpu, fbase, fh, fcount * sizeof(float));
+        const int rc = rrc ? -1 : gpu_upload(m->gpu, fbase, fh, fcount * sizeof(float));
         free(fh);
+        if (rrc) { snprintf(err, errlen, "%s: reading the small tensors failed", path); goto fail; }
         if (rc) { snprintf(err, errlen, "param upload: %s", gpu_last_error(m->gpu)); goto fail; }
     }
     /* host copies: embedding rows (read per emitted token) and the prompt fold inputs */
-    m->embed_host = malloc(emb->nbytes);
-    memcpy(m->embed_host, st_ptr(&st, emb), emb->nbytes);
+    m->embed_host = malloc(emb->bytes);
     m->b0_host = malloc(PH * sizeof(float));
     m->w0_prompt_host = malloc(PH * NP * sizeof(float));
     {
-        const uint16_t *w = st_ptr(&st, w0), *b = st_ptr(&st, b0);
-        for (size_t i = 0; i < PH; ++i) {
-            m->b0_host[i] = st_bf16(b[i]);
-            for (size_t p = 0; p < NP; ++p) m->w0_prompt_host[i * NP + p] = st_bf16(w[i * (D + NP) + D + p]);
-        }
+        uint16_t *w = malloc(w0->bytes);
+        int rrc = !m->embed_host || !m->b0_host || !m->w0_prompt_host || !w;
+        if (!rrc) rrc = ckpt_read(st, emb, m->embed_host) || ckpt_read(st, w0, w) || read_widened(st, b0, m->b0_host);
+        for (size_t i = 0; i < PH && !rrc; ++i)
+            for (size_t p = 0; p < NP; ++p) m->w0_prompt_host[i * NP + p] = ck_bf16(w[i * (D + NP) + D + p]);
+        free(w);
+        if (rrc) { snprintf(err, errlen, "%s: reading the embedding and prompt tensors failed", path); goto fail; }
     }
     m->b0_eff_buf = gpu_buf_alloc(m->gpu, PH * sizeof(float));
     m->prompt_b0_eff = gpu_buf_dptr(m->b0_eff_buf);
@@ -333,7 +380,7 @@ model_t *model_load(const char *dir, char *err, size_t errlen) {
     free(ft);
     free(r.b);
     free(r.f);
-    st_unmap(&st);
+    ckpt_close(st);
     m->load_ms = now_ms() - t0;
     return m;
 fail:
@@ -342,7 +389,7 @@ fail:
     free(ft);
     free(r.b);
     free(r.f);
-    st_unmap(&st);
+    ckpt_close(st);
     model_free(m);
     return NULL;
 }

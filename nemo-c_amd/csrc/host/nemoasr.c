@@ -1,5 +1,14 @@
-/* Library API (include/nemoasr.h): the reference's src/nemoasr.c:1-202 behaviour on the HIP
- * backend, plus the test hooks of include/nemoasr_debug.h. */
+/* Public session API (include/nemoasr.h) on the HIP backend, plus the test hooks of
+ * include/nemoasr_debug.h.
+ *
+ * A session moves audio through three stages:
+ *   input   the caller's samples, resampled to 16 kHz when the caller's rate differs (rsmp_*);
+ *   frames  streaming log-mel rows (melfe_*), queued as the encoder's pending rows;
+ *   chunks  every encoder step that is ready, whose joint.enc rows the greedy loop decodes.
+ * Token text collects in an output buffer whose ownership passes to the caller on each feed.
+ * The observable behaviour is the reference's (src/nemoasr.c:58-196): the latency -> right context
+ * table, language prompt, warm-up at open, feed / final flush, reset, leading spaces dropped from
+ * the stream's first text. */
 #include "nemoasr.h"
 #include "nemoasr_debug.h"
 #include "decoder.h"
@@ -7,320 +16,374 @@
 #include "mel.h"
 #include "model.h"
 #include "resample.h"
-#include <dirent.h>
+#include <glob.h>
+#include <stdarg.h>
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
-#include <sys/stat.h>
 #include <time.h>
 
-static double now_ms(void) {
-    struct timespec ts;
-    clock_gettime(CLOCK_MONOTONIC, &ts);
-    return ts.tv_sec * 1e3 + ts.tv_nsec / 1e6;
+#define TOKENS_PER_CHUNK_MAX 4096
+
+static double clock_ms(void) {
+    struct timespec t;
+    clock_gettime(CLOCK_MONOTONIC, &t);
+    return 1e3 * (double)t.tv_sec + 1e-6 * (double)t.tv_nsec;
+}
+
+/* Grow *buf (element size esz) to hold at least `need` elements; 0 on success. */
+static int reserve(void **buf, size_t *cap, size_t need, size_t esz) {
+    if (need <= *cap) return 0;
+    size_t n = *cap ? *cap : 64;
+    while (n < need) n *= 2;
+    void *p = realloc(*buf, n * esz);
+    if (!p) return -1;
+    *buf = p;
+    *cap = n;
+    return 0;
+}
+
+static void set_err(char *err, size_t errlen, const char *fmt, ...) {
+    if (!errlen) return;
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(err, errlen, fmt, ap);
+    va_end(ap);
+}
+
+/* chunk latency -> attention right context, the checkpoint's trained settings */
+static const struct { int ms, right; } k_latency[] = { { 80, 0 }, { 160, 1 }, { 320, 3 }, { 560, 6 }, { 1120, 13 } };
+
+static int latency_right(int ms) {
+    for (size_t i = 0; i < sizeof k_latency / sizeof k_latency[0]; ++i)
+        if (k_latency[i].ms == ms) return k_latency[i].right;
+    return -1;
+}
+
+/* A latency the session can run: a known setting that the checkpoint was trained for. */
+static int check_latency(const model_t *m, int ms, char *err, size_t errlen) {
+    const int r = latency_right(ms);
+    if (r < 0) {
+        set_err(err, errlen, "unsupported latency %d ms (one of 80, 160, 320, 560, 1120)", ms);
+        return -1;
+    }
+    if (m && !model_right_context_trained(m, r)) {
+        set_err(err, errlen, "the checkpoint has no trained context for %d ms chunks", ms);
+        return -1;
+    }
+    return r;
 }
 
 struct nemoasr {
     model_t *m;
     encoder_t *enc;
     decoder_t *dec;
-    melfe_t *mel;
-    rsmp_t *rs;
-    int input_rate, latency_ms, finished, printed_any;
-    unsigned warmed;
-    float *tmp;
-    size_t tmp_cap;
-    char *text;
-    size_t text_len, text_cap;
-    int tokbuf[4096];
-    int *all_tok;
-    size_t n_tok, cap_tok;
-    double *chunk_ms;
-    size_t n_chunk, cap_chunk;
-    size_t joint_steps;
-    double enc_gpu_ms;
-    double load_ms;
+    struct { /* input stage */
+        int rate;
+        rsmp_t *rs;  /* NULL at 16 kHz */
+        float *buf;  /* resampled samples of one feed */
+        size_t cap;
+        melfe_t *mel;
+    } in;
+    struct { /* text handed out by the next feed */
+        char *p;
+        size_t len, cap;
+        int started; /* a non-space character has been emitted since open / reset */
+    } out;
+    struct { /* records since open / reset (stats and test hooks) */
+        int *ids;
+        size_t nids, capids;
+        double *chunk_ms;
+        size_t nchunk, capchunk;
+        size_t joint_steps;
+        double enc_gpu_ms;
+        float *mel;
+        size_t nmel, capmel;
+    } rec;
     nemoasr_stats_t stats;
-    /* test hook: the front end's log-mel frames since open/reset, kept while dumps are on */
-    int dump;
-    float *mel_dump;
-    size_t n_mel_dump, cap_mel_dump;
+    int latency_ms, done, dump;
+    unsigned warm; /* bit r: chunk shapes of right context r have run once */
+    double open_ms;
+    int ids[TOKENS_PER_CHUNK_MAX];
 };
 
+/* The mlx-community/nemotron-3.5-asr-streaming-0.6b snapshot in the Hugging Face cache: the first
+ * snapshot directory (in name order) that holds model.safetensors. */
 int nemoasr_default_model_dir(char *out, size_t n) {
     const char *home = getenv("HOME");
-    char snaps[1024];
-    snprintf(snaps, sizeof snaps, "%s/.cache/huggingface/hub/models--mlx-community--nemotron-3.5-asr-streaming-0.6b/snapshots",
+    char pat[1200];
+    snprintf(pat, sizeof pat,
+             "%s/.cache/huggingface/hub/models--mlx-community--nemotron-3.5-asr-streaming-0.6b/snapshots/*/model.safetensors",
              home ? home : ".");
-    DIR *d = opendir(snaps);
-    if (!d) return -1;
-    struct dirent *ent;
-    int found = 0;
-    while (!found && (ent = readdir(d))) {
-        if (ent->d_name[0] == '.') continue;
-        snprintf(out, n, "%s/%s", snaps, ent->d_name);
-        char probe[1400];
-        snprintf(probe, sizeof probe, "%s/model.safetensors", out);
-        struct stat sb;
-        found = stat(probe, &sb) == 0;
+    glob_t g;
+    if (glob(pat, 0, NULL, &g) != 0 || g.gl_pathc == 0) {
+        globfree(&g);
+        return -1;
     }
-    closedir(d);
-    return found ? 0 : -1;
+    const char *hit = g.gl_pathv[0];
+    const size_t dirlen = strlen(hit) - strlen("/model.safetensors");
+    const int ok = dirlen < n;
+    if (ok) snprintf(out, n, "%.*s", (int)dirlen, hit);
+    globfree(&g);
+    return ok ? 0 : -1;
 }
 
-/* latency -> right context (src/nemoasr.c:58-64) */
-static int right_for(int latency_ms) {
-    static const int ms[] = { 80, 160, 320, 560, 1120 }, r[] = { 0, 1, 3, 6, 13 };
-    for (size_t i = 0; i < sizeof ms / sizeof *ms; ++i)
-        if (ms[i] == latency_ms) return r[i];
-    return -1;
-}
-
-/* Run zeros through a throwaway encoder/decoder so the first real chunk finds every kernel
- * loaded and the split-K scratch allocated (the reference's asr_warmup, src/warmup.c:23-42). */
-static void warmup(model_t *m, int right, char *err, size_t errlen) {
+/* Warm-up: 1.5 s of silence through a throwaway encoder and decoder of this right context, so the
+ * session's first chunks find every kernel loaded, the graph shapes seen and the scratch sized
+ * (the reference warms its pipelines the same way, src/warmup.c:23-42).  Errors are not fatal. */
+static void warm_up(model_t *m, int right) {
     encoder_t *e = encoder_create(m, right);
     decoder_t *d = decoder_create(m);
-    if (!e || !d) {
-        decoder_destroy(d);
-        encoder_destroy(e);
-        return;
+    melfe_t *fe = melfe_create();
+    if (e && d && fe) {
+        float *silence = calloc(24000, sizeof(float));
+        const float *rows;
+        size_t nrows;
+        char scratch[256];
+        int ids[256];
+        if (silence) {
+            melfe_push(fe, silence, 24000, 1, &rows, &nrows);
+            encoder_push(e, rows, nrows);
+            enc_out_t o;
+            while (encoder_step(e, 1, &o, scratch, sizeof scratch) == 1)
+                if (o.frames > 0 && decoder_run(d, o.joint_enc, o.frames, ids, 256, scratch, sizeof scratch) < 0) break;
+        }
+        free(silence);
     }
-    melfe_t *ms = melfe_create();
-    static const float zeros[1600];
-    int tok[64];
-    for (int i = 0; i < 15; ++i) {
-        const float *fr;
-        size_t nf;
-        melfe_push(ms, zeros, 1600, i == 14, &fr, &nf);
-        encoder_push(e, fr, nf);
-        enc_out_t out;
-        while (encoder_step(e, i == 14, &out, err, errlen) == 1)
-            if (out.frames > 0) decoder_run(d, out.joint_enc, out.frames, tok, 64, err, errlen);
-    }
-    melfe_destroy(ms);
+    melfe_destroy(fe);
     decoder_destroy(d);
     encoder_destroy(e);
 }
 
-nemoasr_t *nemoasr_open(const char *model_dir, const char *language, int latency_ms, int input_rate, char *err, size_t errlen) {
-    if (errlen) err[0] = 0;
-    const int right = right_for(latency_ms);
-    if (right < 0) { snprintf(err, errlen, "latency must be one of 80, 160, 320, 560, 1120 ms"); return NULL; }
-    if (input_rate <= 0) { snprintf(err, errlen, "input_rate must be positive"); return NULL; }
-    const double t0 = now_ms();
+/* Fresh front end and empty records (open and reset). */
+static int begin_stream(nemoasr_t *s) {
+    melfe_destroy(s->in.mel);
+    rsmp_destroy(s->in.rs);
+    s->in.mel = melfe_create();
+    s->in.rs = s->in.rate != MEL_SR ? rsmp_create(s->in.rate, MEL_SR) : NULL;
+    free(s->out.p);
+    s->out.p = NULL;
+    s->out.len = s->out.cap = 0;
+    s->out.started = 0;
+    s->rec.nids = s->rec.nchunk = s->rec.nmel = 0;
+    s->rec.joint_steps = 0;
+    s->rec.enc_gpu_ms = 0.0;
+    memset(&s->stats, 0, sizeof s->stats);
+    s->done = 0;
+    return s->in.mel && (s->in.rate == MEL_SR || s->in.rs) ? 0 : -1;
+}
+
+nemoasr_t *nemoasr_open(const char *model_dir, const char *language, int latency_ms, int input_rate, char *err,
+                        size_t errlen) {
+    set_err(err, errlen, "%s", "");
+    const double t0 = clock_ms();
+    if (check_latency(NULL, latency_ms, err, errlen) < 0) return NULL;
+    if (input_rate <= 0) {
+        set_err(err, errlen, "input_rate must be > 0 (got %d)", input_rate);
+        return NULL;
+    }
     nemoasr_t *s = calloc(1, sizeof *s);
-    s->m = model_load(model_dir, err, errlen);
-    if (!s->m) { free(s); return NULL; }
-    if (!model_right_context_trained(s->m, right)) {
-        snprintf(err, errlen, "latency %d ms not trained for this checkpoint", latency_ms);
+    if (!s) {
+        set_err(err, errlen, "out of memory");
+        return NULL;
+    }
+    s->in.rate = input_rate;
+    s->latency_ms = latency_ms;
+    if (!(s->m = model_load(model_dir, err, errlen))) {
+        free(s);
+        return NULL;
+    }
+    const int right = check_latency(s->m, latency_ms, err, errlen);
+    if (right < 0 || model_set_language(s->m, language ? language : "auto", err, errlen)) {
         nemoasr_close(s);
         return NULL;
     }
-    if (model_set_language(s->m, language ? language : "auto", err, errlen)) { nemoasr_close(s); return NULL; }
-    warmup(s->m, right, err, errlen);
-    if (errlen) err[0] = 0;
-    s->warmed = 1u << right;
+    warm_up(s->m, right);
+    s->warm = 1u << right;
     s->enc = encoder_create(s->m, right);
     s->dec = decoder_create(s->m);
-    s->mel = melfe_create();
-    if (!s->enc || !s->dec) {
-        snprintf(err, errlen, "nemoasr_open: GPU setup failed: %s", gpu_last_error(s->m->gpu));
+    if (!s->enc || !s->dec || begin_stream(s)) {
+        set_err(err, errlen, "session setup on the GPU failed: %s", gpu_last_error(s->m->gpu));
         nemoasr_close(s);
         return NULL;
     }
-    s->input_rate = input_rate;
-    s->latency_ms = latency_ms;
-    if (input_rate != MEL_SR) s->rs = rsmp_create(input_rate, MEL_SR);
-    s->load_ms = now_ms() - t0;
+    set_err(err, errlen, "%s", "");
+    s->open_ms = clock_ms() - t0;
     return s;
 }
 
 void nemoasr_close(nemoasr_t *s) {
     if (!s) return;
-    melfe_destroy(s->mel);
-    decoder_destroy(s->dec);
     encoder_destroy(s->enc);
-    rsmp_destroy(s->rs);
+    decoder_destroy(s->dec);
+    melfe_destroy(s->in.mel);
+    rsmp_destroy(s->in.rs);
     model_free(s->m);
-    free(s->tmp);
-    free(s->text);
-    free(s->all_tok);
-    free(s->chunk_ms);
-    free(s->mel_dump);
+    free(s->in.buf);
+    free(s->out.p);
+    free(s->rec.ids);
+    free(s->rec.chunk_ms);
+    free(s->rec.mel);
     free(s);
 }
 
-static void append_text(nemoasr_t *s, const char *t) {
+/* Token text into the output buffer; the stream's first text loses its leading spaces. */
+static int emit_text(nemoasr_t *s, int id) {
+    char *piece = piece_text(&s->m->vocab, id);
+    if (!piece) return -1;
+    const char *t = piece;
+    if (!s->out.started) t += strspn(t, " ");
     const size_t n = strlen(t);
-    if (!n) return;
-    if (s->text_len + n + 1 > s->text_cap) {
-        s->text_cap = (s->text_len + n + 1) * 2;
-        s->text = realloc(s->text, s->text_cap);
-    }
-    memcpy(s->text + s->text_len, t, n + 1);
-    s->text_len += n;
-}
-
-static void keep_tokens(nemoasr_t *s, const int *t, int n) {
-    if (s->n_tok + (size_t)n > s->cap_tok) {
-        s->cap_tok = (s->n_tok + (size_t)n) * 2 + 256;
-        s->all_tok = realloc(s->all_tok, s->cap_tok * sizeof(int));
-    }
-    memcpy(s->all_tok + s->n_tok, t, (size_t)n * sizeof(int));
-    s->n_tok += (size_t)n;
-}
-
-/* every ready chunk: encoder step, then the decoder over its frames (src/nemoasr.c:112-132) */
-static int run_pending(nemoasr_t *s, int final, int *new_tokens, char *err, size_t errlen) {
-    enc_out_t out;
-    int rc, total = 0;
-    while ((rc = encoder_step(s->enc, final, &out, err, errlen)) == 1) {
-        if (out.frames <= 0) continue;
-        const double t0 = now_ms();
-        s->stats.chunks++;
-        s->stats.encoder_ms += out.wall_ms;
-        s->enc_gpu_ms += out.gpu_ms;
-        const int n = decoder_run(s->dec, out.joint_enc, out.frames, s->tokbuf, 4096, err, errlen);
-        if (n < 0) return -1;
-        s->stats.decoder_ms += decoder_last_ms(s->dec);
-        s->joint_steps += (size_t)decoder_last_steps(s->dec);
-        s->stats.tokens += (size_t)n;
-        keep_tokens(s, s->tokbuf, n);
-        total += n;
-        for (int i = 0; i < n; ++i) {
-            char *txt = piece_text(&s->m->vocab, s->tokbuf[i]);
-            const char *p = txt;
-            if (!s->printed_any) while (*p == ' ') p++;
-            if (*p) { append_text(s, p); s->printed_any = 1; }
-            free(txt);
+    int rc = 0;
+    if (n) {
+        if (reserve((void **)&s->out.p, &s->out.cap, s->out.len + n + 1, 1)) rc = -1;
+        else {
+            memcpy(s->out.p + s->out.len, t, n + 1);
+            s->out.len += n;
+            s->out.started = 1;
         }
-        if (s->n_chunk == s->cap_chunk) {
-            s->cap_chunk = s->cap_chunk ? 2 * s->cap_chunk : 256;
-            s->chunk_ms = realloc(s->chunk_ms, s->cap_chunk * sizeof(double));
-        }
-        s->chunk_ms[s->n_chunk++] = out.wall_ms + (now_ms() - t0);
     }
-    if (new_tokens) *new_tokens = total;
+    free(piece);
     return rc;
 }
 
-char *nemoasr_feed(nemoasr_t *s, const float *samples, size_t n, int final, char *err, size_t errlen) {
-    if (errlen) err[0] = 0;
-    if (s->finished) return NULL;
-    const float *in = samples;
-    size_t count = n;
-    if (s->rs) {
-        const size_t need = (size_t)((double)n * MEL_SR / s->input_rate) + 4096;
-        if (need > s->tmp_cap) {
-            s->tmp_cap = need * 2;
-            s->tmp = realloc(s->tmp, s->tmp_cap * sizeof(float));
+/* Run every encoder step that is ready (all remaining ones when final) and decode each chunk's
+ * frames.  Returns the number of new tokens, or -1 with err set. */
+static int drain_chunks(nemoasr_t *s, int final, char *err, size_t errlen) {
+    int fresh = 0;
+    for (;;) {
+        enc_out_t o;
+        const int rc = encoder_step(s->enc, final, &o, err, errlen);
+        if (rc < 0) return -1;
+        if (rc == 0) return fresh;
+        if (o.frames <= 0) continue;
+        const double t0 = clock_ms();
+        const int n = decoder_run(s->dec, o.joint_enc, o.frames, s->ids, TOKENS_PER_CHUNK_MAX, err, errlen);
+        if (n < 0) return -1;
+        if (reserve((void **)&s->rec.ids, &s->rec.capids, s->rec.nids + (size_t)n, sizeof(int)) ||
+            reserve((void **)&s->rec.chunk_ms, &s->rec.capchunk, s->rec.nchunk + 1, sizeof(double))) {
+            set_err(err, errlen, "out of memory");
+            return -1;
         }
-        count = n ? rsmp_process(s->rs, samples, n, s->tmp, s->tmp_cap) : 0;
-        if (final) count += rsmp_flush(s->rs, s->tmp + count, s->tmp_cap - count);
-        in = s->tmp;
-    }
-    s->stats.audio_seconds += (double)count / MEL_SR;
-    if (!(final && count == 0 && melfe_samples(s->mel) == 0)) {
-        const float *frames;
-        size_t nf;
-        melfe_push(s->mel, in, count, final, &frames, &nf);
-        if (nf && s->dump) {
-            if (s->n_mel_dump + nf > s->cap_mel_dump) {
-                s->cap_mel_dump = (s->n_mel_dump + nf) * 2;
-                s->mel_dump = realloc(s->mel_dump, s->cap_mel_dump * MEL_NMEL * sizeof(float));
+        for (int i = 0; i < n; ++i)
+            if (emit_text(s, s->ids[i])) {
+                set_err(err, errlen, "out of memory");
+                return -1;
             }
-            memcpy(s->mel_dump + s->n_mel_dump * MEL_NMEL, frames, nf * MEL_NMEL * sizeof(float));
-            s->n_mel_dump += nf;
-        }
-        if (nf) encoder_push(s->enc, frames, nf);
-        if (run_pending(s, final, NULL, err, errlen) < 0) return NULL;
+        memcpy(s->rec.ids + s->rec.nids, s->ids, (size_t)n * sizeof(int));
+        s->rec.nids += (size_t)n;
+        s->rec.chunk_ms[s->rec.nchunk++] = o.wall_ms + (clock_ms() - t0);
+        s->rec.joint_steps += (size_t)decoder_last_steps(s->dec);
+        s->rec.enc_gpu_ms += o.gpu_ms;
+        s->stats.chunks += 1;
+        s->stats.tokens += (size_t)n;
+        s->stats.encoder_ms += o.wall_ms;
+        s->stats.decoder_ms += decoder_last_ms(s->dec);
+        fresh += n;
     }
-    if (final) s->finished = 1;
-    if (!s->text_len) return NULL;
-    char *out = s->text;
-    s->text = NULL;
-    s->text_len = s->text_cap = 0;
-    return out;
 }
 
-int nemoasr_prepare_latency(nemoasr_t *s, int latency_ms, char *err, size_t errlen) {
-    if (errlen) err[0] = 0;
-    const int right = right_for(latency_ms);
-    if (right < 0) { snprintf(err, errlen, "latency must be one of 80, 160, 320, 560, 1120 ms"); return -1; }
-    if (!model_right_context_trained(s->m, right)) {
-        snprintf(err, errlen, "latency %d ms not trained for this checkpoint", latency_ms);
-        return -1;
+char *nemoasr_feed(nemoasr_t *s, const float *samples, size_t n, int final, char *err, size_t errlen) {
+    set_err(err, errlen, "%s", "");
+    if (s->done) return NULL;
+    const float *x = samples;
+    size_t cnt = n;
+    if (s->in.rs) { /* to 16 kHz, plus the filter's tail when the stream ends */
+        const size_t most = (size_t)((double)n * MEL_SR / s->in.rate) + 4096;
+        if (reserve((void **)&s->in.buf, &s->in.cap, most, sizeof(float))) {
+            set_err(err, errlen, "out of memory");
+            return NULL;
+        }
+        cnt = n ? rsmp_process(s->in.rs, samples, n, s->in.buf, s->in.cap) : 0;
+        if (final) cnt += rsmp_flush(s->in.rs, s->in.buf + cnt, s->in.cap - cnt);
+        x = s->in.buf;
     }
-    if (!(s->warmed & (1u << right))) {
-        warmup(s->m, right, err, errlen);
-        if (errlen) err[0] = 0;
-        s->warmed |= 1u << right;
+    s->stats.audio_seconds += (double)cnt / MEL_SR;
+    /* a final call on a stream that never received a sample has nothing to flush */
+    const int nothing = final && cnt == 0 && melfe_samples(s->in.mel) == 0;
+    if (!nothing) {
+        const float *rows;
+        size_t nrows;
+        melfe_push(s->in.mel, x, cnt, final, &rows, &nrows);
+        if (nrows && s->dump) {
+            if (reserve((void **)&s->rec.mel, &s->rec.capmel, (s->rec.nmel + nrows) * MEL_NMEL, sizeof(float))) {
+                set_err(err, errlen, "out of memory");
+                return NULL;
+            }
+            memcpy(s->rec.mel + s->rec.nmel * MEL_NMEL, rows, nrows * MEL_NMEL * sizeof(float));
+            s->rec.nmel += nrows;
+        }
+        if (nrows) encoder_push(s->enc, rows, nrows);
+        if (drain_chunks(s, final, err, errlen) < 0) return NULL;
+    }
+    if (final) s->done = 1;
+    if (!s->out.len) return NULL;
+    char *text = s->out.p; /* ownership moves to the caller */
+    s->out.p = NULL;
+    s->out.len = s->out.cap = 0;
+    return text;
+}
+
+void nemoasr_free(char *text) { free(text); }
+
+int nemoasr_prepare_latency(nemoasr_t *s, int latency_ms, char *err, size_t errlen) {
+    set_err(err, errlen, "%s", "");
+    const int right = check_latency(s->m, latency_ms, err, errlen);
+    if (right < 0) return -1;
+    if (!(s->warm & (1u << right))) {
+        warm_up(s->m, right);
+        s->warm |= 1u << right;
     }
     return 0;
 }
 
 int nemoasr_reset(nemoasr_t *s, const char *language, int latency_ms, char *err, size_t errlen) {
-    if (errlen) err[0] = 0;
     if (nemoasr_prepare_latency(s, latency_ms, err, errlen)) return -1;
     if (language && model_set_language(s->m, language, err, errlen)) return -1;
-    const int right = right_for(latency_ms);
-    if (encoder_right(s->enc) == right) {
-        encoder_reset(s->enc);
-    } else {
+    const int right = latency_right(latency_ms);
+    if (encoder_right(s->enc) != right) { /* another chunk shape: a new encoder */
         encoder_destroy(s->enc);
-        s->enc = encoder_create(s->m, right);
-        if (!s->enc) {
-            snprintf(err, errlen, "nemoasr_reset: GPU setup failed: %s", gpu_last_error(s->m->gpu));
-            s->finished = 1;
+        if (!(s->enc = encoder_create(s->m, right))) {
+            set_err(err, errlen, "encoder setup on the GPU failed: %s", gpu_last_error(s->m->gpu));
+            s->done = 1;
             return -1;
         }
         encoder_set_dump(s->enc, s->dump);
+    } else {
+        encoder_reset(s->enc);
     }
-    melfe_destroy(s->mel);
-    s->mel = melfe_create();
     decoder_reset(s->dec);
-    if (s->rs) { rsmp_destroy(s->rs); s->rs = rsmp_create(s->input_rate, MEL_SR); }
-    free(s->text);
-    s->text = NULL;
-    s->text_len = s->text_cap = 0;
-    s->finished = 0;
-    s->printed_any = 0;
     s->latency_ms = latency_ms;
-    s->n_tok = 0;
-    s->n_chunk = 0;
-    s->n_mel_dump = 0;
-    s->joint_steps = 0;
-    s->enc_gpu_ms = 0;
-    memset(&s->stats, 0, sizeof s->stats);
+    if (begin_stream(s)) {
+        set_err(err, errlen, "out of memory");
+        s->done = 1;
+        return -1;
+    }
     return 0;
 }
 
-void nemoasr_free(char *text) { free(text); }
-double nemoasr_load_ms(const nemoasr_t *s) { return s->load_ms; }
+double nemoasr_load_ms(const nemoasr_t *s) { return s->open_ms; }
 const char *nemoasr_gpu_name(const nemoasr_t *s) { return gpu_device_name(s->m->gpu); }
 int nemoasr_latency_ms(const nemoasr_t *s) { return s->latency_ms; }
 void nemoasr_stats(const nemoasr_t *s, nemoasr_stats_t *out) { *out = s->stats; }
 
 /* ---- test hooks ---------------------------------------------------------------------------- */
 int nemoasr_debug_feed_mel(nemoasr_t *s, const float *mel, size_t nframes, int final, char *err, size_t errlen) {
-    if (errlen) err[0] = 0;
+    set_err(err, errlen, "%s", "");
     if (nframes) encoder_push(s->enc, mel, nframes);
-    int n = 0;
-    if (run_pending(s, final, &n, err, errlen) < 0) return -1;
-    return n;
+    return drain_chunks(s, final, err, errlen);
 }
 const int *nemoasr_debug_tokens(const nemoasr_t *s, size_t *n) {
-    *n = s->n_tok;
-    return s->all_tok;
+    *n = s->rec.nids;
+    return s->rec.ids;
 }
 void nemoasr_debug_set_dump(nemoasr_t *s, int on) {
     s->dump = on;
     encoder_set_dump(s->enc, on);
 }
 const float *nemoasr_debug_dump_mel(const nemoasr_t *s, size_t *nframes) {
-    *nframes = s->n_mel_dump;
-    return s->mel_dump;
+    *nframes = s->rec.nmel;
+    return s->rec.mel;
 }
 size_t nemoasr_debug_frames(const nemoasr_t *s) { return encoder_dump_frames(s->enc); }
 const float *nemoasr_debug_dump_layers(const nemoasr_t *s) { return encoder_dump_layers(s->enc); }
@@ -331,11 +394,11 @@ void nemoasr_debug_use_graphs(nemoasr_t *s, int on) {
     decoder_use_graphs(s->dec, on);
 }
 void nemoasr_debug_fuse(nemoasr_t *s, int on) { encoder_fuse(s->enc, on); }
-size_t nemoasr_debug_joint_steps(const nemoasr_t *s) { return s->joint_steps; }
-double nemoasr_debug_encoder_gpu_ms(const nemoasr_t *s) { return s->enc_gpu_ms; }
+size_t nemoasr_debug_joint_steps(const nemoasr_t *s) { return s->rec.joint_steps; }
+double nemoasr_debug_encoder_gpu_ms(const nemoasr_t *s) { return s->rec.enc_gpu_ms; }
 const double *nemoasr_debug_chunk_ms(const nemoasr_t *s, size_t *n) {
-    *n = s->n_chunk;
-    return s->chunk_ms;
+    *n = s->rec.nchunk;
+    return s->rec.chunk_ms;
 }
 int nemoasr_debug_time_kernel(nemoasr_t *s, const char *kernel, int max_launches) {
     return gpu_timing_set(s->m->gpu, kernel, max_launches);

@@ -3,8 +3,11 @@
 The checkpoint follows the tensor names, shapes and dtype (BF16) that the loader enforces
 (reference: src/model.c:41-47 `need`, src/model.c:215-282 tensor list) and the
 config.json keys it reads (src/model.c:125-172).  Weights are random: matrices
-N(0, 1/fan_in), LayerNorm gamma ~1 / beta ~0, small biases.  The joint output bias of the
-blank class can be raised to give a chosen blank probability.
+N(0, 1/fan_in), LayerNorm gamma ~1 / beta ~0, small biases.  The joint output bias can be
+skewed toward the blank class to give a chosen blank probability: blank_bias is added to the blank
+class's bias and label_shift subtracted from every other class's bias.  The biases are stored as
+bf16, whose spacing near a skew of 2 is 2^-6; splitting the skew between a bf16-exact blank_bias
+and a small label_shift (spacing ~2^-11 near 0.1) sets it about 30 times more finely.
 
 Audio is 16 kHz float32: pink noise at -20 dBFS RMS plus random linear sine chirps.
 Every array is a pure function of (seed, tensor name), so a model or clip is bit-identical on
@@ -154,10 +157,12 @@ def make_config(d: dict) -> dict:
     }
 
 
-def write_model(out_dir: str, dims: dict | None = None, seed: int = 0, blank_bias: float = 0.0) -> str:
+def write_model(out_dir: str, dims: dict | None = None, seed: int = 0, blank_bias: float = 0.0,
+                label_shift: float = 0.0) -> str:
     """Write config.json + model.safetensors into out_dir (skipped if an identical one is there)."""
     d = dict(FULL_DIMS if dims is None else dims)
-    tag = hashlib.sha1(json.dumps([d, seed, blank_bias], sort_keys=True).encode()).hexdigest()[:16]
+    key = [d, seed, blank_bias] + ([label_shift] if label_shift else [])
+    tag = hashlib.sha1(json.dumps(key, sort_keys=True).encode()).hexdigest()[:16]
     os.makedirs(out_dir, exist_ok=True)
     stamp = os.path.join(out_dir, "synth.tag")
     if os.path.exists(stamp) and open(stamp).read() == tag and os.path.exists(os.path.join(out_dir, "model.safetensors")):
@@ -179,6 +184,7 @@ def write_model(out_dir: str, dims: dict | None = None, seed: int = 0, blank_bia
             x = make_tensor(seed, name, shape, kind, scale)
             if name == "joint.joint_net.2.bias":
                 x[blank] += np.float32(blank_bias)
+                x[:blank] -= np.float32(label_shift)
             f.write(f32_to_bf16(x).tobytes())
     os.replace(tmp, os.path.join(out_dir, "model.safetensors"))
     with open(os.path.join(out_dir, "config.json"), "w") as f:

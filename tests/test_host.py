@@ -260,3 +260,100 @@ def test_enc_plan_product_vs_oracle(chunk_mel):
                         break
                 if final and b.closed:
                     break
+
+
+class _CkTensor(C.Structure):
+    _fields_ = [("name", C.c_char_p), ("dtype", C.c_int), ("numel", C.c_size_t), ("at", C.c_uint64),
+                ("bytes", C.c_uint64)]
+
+
+def _ckpt_lib():
+    L = product()
+    L.ckpt_open.restype = C.c_void_p
+    L.ckpt_open.argtypes = [C.c_char_p, C.c_char_p, C.c_size_t]
+    L.ckpt_close.argtypes = [C.c_void_p]
+    L.ckpt_count.restype = C.c_size_t
+    L.ckpt_count.argtypes = [C.c_void_p]
+    L.ckpt_find.restype = C.POINTER(_CkTensor)
+    L.ckpt_find.argtypes = [C.c_void_p, C.c_char_p]
+    L.ckpt_read.argtypes = [C.c_void_p, C.POINTER(_CkTensor), C.c_void_p]
+    return L
+
+
+def _write_st(path, header: dict, payload: bytes):
+    import json
+    import struct
+
+    hj = json.dumps(header).encode()
+    with open(path, "wb") as f:
+        f.write(struct.pack("<Q", len(hj)) + hj + payload)
+
+
+def test_checkpoint_index_reads_tensors(tmp_path):
+    """The product's checkpoint index (pread, sorted lookup) gives every tensor of a synthetic
+    checkpoint with the shape, dtype and bytes a plain reader finds."""
+    from conftest import model_dir
+
+    L = _ckpt_lib()
+    path = os.path.join(model_dir("tiny"), "model.safetensors")
+    ref = synth.load_safetensors(path)
+    err = C.create_string_buffer(256)
+    h = L.ckpt_open(path.encode(), err, 256)
+    assert h, err.value
+    try:
+        assert L.ckpt_count(h) == len(ref)
+        for name in sorted(ref)[::7] + ["prompt_kernel.0.weight", "joint.joint_net.2.bias"]:
+            raw, shape = ref[name]
+            t = L.ckpt_find(h, name.encode())
+            assert t and t.contents.dtype == 0 and t.contents.numel == int(np.prod(shape))
+            out = np.empty(raw.size, np.uint16)
+            assert L.ckpt_read(h, t, out.ctypes.data) == 0
+            np.testing.assert_array_equal(out, raw)
+        assert not L.ckpt_find(h, b"no.such.tensor")
+        assert not L.ckpt_find(h, b"")
+    finally:
+        L.ckpt_close(h)
+
+
+@pytest.mark.parametrize("case", ["past_end", "length_mismatch", "header_length", "duplicate", "not_object"])
+def test_checkpoint_index_rejects_bad_files(tmp_path, case):
+    L = _ckpt_lib()
+    p = str(tmp_path / "bad.safetensors")
+    ok = {"dtype": "BF16", "shape": [2, 3], "data_offsets": [0, 12]}
+    if case == "past_end":
+        _write_st(p, {"a": {"dtype": "BF16", "shape": [2, 3], "data_offsets": [0, 12]}}, b"\0" * 8)
+    elif case == "length_mismatch":
+        _write_st(p, {"a": {"dtype": "F32", "shape": [2, 3], "data_offsets": [0, 12]}}, b"\0" * 12)
+    elif case == "header_length":
+        with open(p, "wb") as f:
+            f.write((1 << 40).to_bytes(8, "little") + b"{}")
+    elif case == "duplicate":
+        import struct
+
+        hj = b'{"a": ' + str(ok).replace("'", '"').encode() + b', "a": ' + str(ok).replace("'", '"').encode() + b"}"
+        with open(p, "wb") as f:
+            f.write(struct.pack("<Q", len(hj)) + hj + b"\0" * 12)
+    else:
+        with open(p, "wb") as f:
+            f.write((2).to_bytes(8, "little") + b"[]")
+    err = C.create_string_buffer(256)
+    assert not L.ckpt_open(p.encode(), err, 256)
+    assert err.value, case
+
+
+def test_default_model_dir(tmp_path, monkeypatch):
+    """nemoasr_default_model_dir: the Hugging Face cache snapshot that holds model.safetensors
+    (src/nemoasr.h:23-25), -1 when there is none."""
+    L = product()
+    L.nemoasr_default_model_dir.restype = C.c_int
+    L.nemoasr_default_model_dir.argtypes = [C.c_char_p, C.c_size_t]
+    monkeypatch.setenv("HOME", str(tmp_path))
+    out = C.create_string_buffer(4096)
+    assert L.nemoasr_default_model_dir(out, 4096) == -1
+    snaps = tmp_path / ".cache/huggingface/hub/models--mlx-community--nemotron-3.5-asr-streaming-0.6b/snapshots"
+    (snaps / "aaa").mkdir(parents=True)  # a snapshot without the weights is skipped
+    (snaps / "bbb").mkdir()
+    (snaps / "bbb" / "model.safetensors").write_bytes(b"")
+    assert L.nemoasr_default_model_dir(out, 4096) == 0
+    assert out.value.decode() == str(snaps / "bbb")
+    assert L.nemoasr_default_model_dir(out, 8) == -1  # does not fit
