@@ -1,28 +1,35 @@
 #!/usr/bin/env python3
 """Streaming ASR benchmark on one MI355X.
 
-Workload (default): one stream at 80 ms latency (1 encoder frame per chunk, every GEMM an M=1
+Headline (value): one stream at 80 ms latency (1 encoder frame per chunk, every GEMM an M=1
 weight-streaming GEMV) over 10 s of seeded 16 kHz synthetic audio, FastConformer 0.6B + RNNT with
 seeded random-init bf16 weights.  A step is one pass of that clip through the public C API
 (nemoasr_reset + nemoasr_feed in chunk-sized pieces, like the reference's file mode,
 src/main.c:234-246); value = RTFx = audio seconds / wall seconds over the timed steps.
 
-A second leg runs the batched multi-stream path (include/nemoasr_batch.h): by default 64 streams
-at 560 ms (M = 448 encoder rows per step), each stream with its own seeded 20 s clip and a start
-offset of 0-7 chunks of pre-filled caches; it reports aggregate RTFx, p50 step latency (one chunk of
-every stream, from the step's start to its tokens: front end + encoder + RNNT loop), the step period
-(the RNNT loop of a step overlaps the next step's front end and encoder, so steps start faster than
-they finish), the encoder's GEMM TFLOP/s per step and the MFMA roofline of the many-row GEMM kernels.
+Legs in the same JSON line (each with its own roofline of its dominant kernel):
+  S560   one stream, 560 ms, 10 s, en-US;
+  S1120  one stream, 1120 ms, 30 s, en-US, joint bias skewed to P(blank) ~ 0.5 (the token loop);
+  B64    64 streams, 560 ms, 20 s each, start offsets 0-7 chunks of pre-filled caches;
+  B256   256 streams, 1120 ms, 60 s each, prompt auto, offsets 0-4 chunks, P(blank) ~ 0.7.
+P(blank) is measured and reported as blank decisions / all greedy decisions, counted as
+frames / (frames + tokens) (a frame ends on a blank unless it reaches max_symbols).
 
-Also reported: p50 chunk latency (encoder step + its decoder round trips), the per-chunk HBM rate
-of the encoder (1,176,502,272 bytes of bf16 weights streamed per chunk / chunk GPU time), the
-roofline of the dominant kernel (algorithmic bytes / mean launch time, hipEvents around every
-launch of that kernel on its stream during a direct-launch replay of the same clip), and the CPU
-baseline: the oracle's C restatement on a bounded sample of the same clip on this host's cores.
+Per single-stream leg: RTFx, p50/p90 chunk latency (encoder step + its decoder round trips), the
+encoder's HBM rate (1,176,502,272 bytes of bf16 weights streamed per chunk / chunk GPU time) and the
+roofline of the dominant kernel class (algorithmic bytes / mean launch duration from hipEvents
+stamped by the dispatch itself around every launch of the class on the library's stream, during a
+direct-launch replay of the same clip).  Per batch leg: aggregate RTFx, p50 step latency (one chunk
+of every stream, from the step's start to its tokens), the step period, and the MFMA roofline of the
+many-row GEMM kernels (algorithmic 2*M*N*K flops / dispatch-stamped durations).
+
+CPU baseline: the oracle's C restatement (log-mel + encoder + greedy RNNT) on bounded samples of the
+headline clip on this host's cores, at one thread and at all threads given to this process.
 """
 import argparse
 import json
 import os
+import re
 import sys
 import time
 
@@ -37,6 +44,14 @@ HBM_PEAK_GBS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0
 LAT_RIGHT = {80: 0, 160: 1, 320: 3, 560: 6, 1120: 13}
 DOMINANT = {80: "gemv_*", 160: "gemv_*", 320: "gemm_fr*", 560: "gemm_fr*", 1120: "gemm_fr*"}
+# joint-bias skews (blank_bias, label_shift) of the checkpoints for the skewed legs, calibrated on
+# those legs' own workloads by bisection on label_shift (MI355X): S1120 gives P(blank) 0.500
+# (376 tokens over 376 frames), B256 0.701
+SKEW_S1120 = (2.0, 0.0188)
+SKEW_B256 = (2.0, 0.0619)
+# HBM traffic per launch of the headline's dominant kernel class, from rocprofv3 FETCH_SIZE and
+# WRITE_SIZE runs of this benchmark's headline workload (profiles/stream80_hbm_traffic.md)
+TRAFFIC_FILE = os.path.join(REPO, "profiles", "stream80_hbm_traffic.md")
 
 
 def weight_bytes_per_chunk(cfg: dict) -> int:
@@ -60,15 +75,102 @@ def gemm_params_per_row(cfg: dict) -> int:
     return nl * layer + 2 * p["prompt_hidden"] * D + j["joint_hidden"] * D
 
 
-def batch_leg(a, nemoasr, synth, mdir, cfg):
-    """Many streams through the batch API; see the module docstring."""
-    S, lat, right = a.batch_streams, a.batch_latency, LAT_RIGHT[a.batch_latency]
+def model(synth, skew=(0.0, 0.0)):
+    cache = os.environ.get("NEMO_MODEL_CACHE", "/tmp/nemo_models")
+    bb, ls = skew
+    tag = f"full_s0_b{bb:g}" + (f"_l{ls:g}" if ls else "")
+    return synth.write_model(os.path.join(cache, tag), synth.FULL_DIMS, 0, bb, ls)
+
+
+def p_blank(frames, tokens):
+    return round(frames / (frames + tokens), 4) if frames + tokens else None
+
+
+def traffic_from_profile(kernel: str):
+    """HBM bytes per launch (FETCH + WRITE, scaled by the copy calibration) that the committed PMC
+    summary records for this kernel class, or None."""
+    try:
+        text = open(TRAFFIC_FILE).read()
+    except OSError:
+        return None
+    m = re.search(r"traffic_bytes_per_launch\[" + re.escape(kernel) + r"\]\s*=\s*([0-9.eE+]+)", text)
+    return float(m.group(1)) if m else None
+
+
+def single_leg(a, nemoasr, synth, mdir, cfg, latency, seconds, lang="en-US", steps=None, warmup=None, frames_fn=None):
+    """One stream through the public API: see the module docstring."""
+    steps = a.steps if steps is None else steps
+    warmup = a.warmup if warmup is None else warmup
+    audio = synth.make_audio(seconds, seed=0)
+    audio_s = audio.size / 16000.0
+    right = LAT_RIGHT[latency]
     piece = (right + 1) * 8 * 160
-    nsamp = int(round(a.batch_seconds * 16000))
-    clips = [synth.make_audio(a.batch_seconds, seed=1000 + s) for s in range(S)]
-    offs = [s % (a.batch_offsets + 1) for s in range(S)]
+    s = nemoasr.Session(mdir, lang, latency)
+
+    def clip():
+        s.reset(lang, latency)
+        s.use_graphs(not a.no_graphs)
+        t0 = time.perf_counter()
+        for i in range(0, audio.size, piece):
+            s.feed(audio[i:i + piece], final=i + piece >= audio.size)
+        return time.perf_counter() - t0
+
+    for _ in range(warmup):
+        clip()
+    times, chunk_ms, enc_gpu, chunks, toks, trips = [], [], 0.0, 0, 0, 0
+    for _ in range(steps):
+        times.append(clip())
+        chunk_ms.append(s.chunk_ms())
+        st = s.stats()
+        enc_gpu += nemoasr.lib().nemoasr_debug_encoder_gpu_ms(s.h)
+        chunks += st["chunks"]
+        toks += st["tokens"]
+        trips += s.joint_steps
+    wall = sum(times)
+    cms = np.concatenate(chunk_ms)
+    wb = weight_bytes_per_chunk(cfg)
+    enc_ms = enc_gpu / max(chunks, 1)
+    # dominant kernel class: hipEvents around each of its launches during a direct-launch replay
+    kname = DOMINANT.get(latency, "gemm_fr*")
+    s.reset(lang, latency)
+    s.use_graphs(False)
+    s.time_kernel(kname, 32768)
+    for i in range(0, audio.size, piece):
+        s.feed(audio[i:i + piece], final=i + piece >= audio.size)
+    kms, kn, kbytes = s.kernel_ms()
+    s.time_kernel(None, 0)
+    achieved = (kbytes / max(kn, 1)) / (kms * 1e-3) / 1e9 if kn and kms > 0 else 0.0
+    gpu_name = s.gpu_name
+    s.close()
+    frames = frames_fn(audio.size)
+    return {
+        "workload": f"1 stream, {latency} ms latency ({right + 1} encoder frame(s)/chunk), {audio_s:g} s of 16 kHz "
+                    f"audio, prompt {lang}",
+        "latency_ms": latency, "audio_s": audio_s, "rtfx": round(steps * audio_s / wall, 3),
+        "ms_per_pass": round(1e3 * wall / steps, 3),
+        "chunks_per_clip": int(chunks / steps), "frames_per_clip": frames, "tokens_per_clip": int(toks / steps),
+        "p_blank": p_blank(frames, toks / steps),
+        "joint_round_trips_per_clip": int(trips / steps),
+        "p50_chunk_ms": round(float(np.median(cms)), 4), "p90_chunk_ms": round(float(np.percentile(cms, 90)), 4),
+        "encoder_gpu_ms_per_chunk": round(enc_ms, 4), "encoder_weight_bytes_per_chunk": wb,
+        "encoder_chunk_hbm_gbs": round(wb / (enc_ms * 1e-3) / 1e9, 1) if enc_ms > 0 else None,
+        "graphs": not a.no_graphs, "gpu": gpu_name,
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_from_profile(kname)
+                     if latency == 80 else None, "kernel": kname, "launches": kn,
+                     "mean_launch_us": round(kms * 1e3, 3), "bytes_per_launch": round(kbytes / max(kn, 1))},
+    }
+
+
+def batch_leg(a, nemoasr, synth, mdir, cfg, S, lat, seconds, offsets, lang):
+    """Many streams through the batch API; see the module docstring."""
+    right = LAT_RIGHT[lat]
+    piece = (right + 1) * 8 * 160
+    nsamp = int(round(seconds * 16000))
+    clips = [synth.make_audio(seconds, seed=1000 + s) for s in range(S)]
+    offs = [s % (offsets + 1) for s in range(S)]
     pre = [synth.make_audio(max(o, 1) * piece / 16000.0, seed=2000 + s)[: o * piece] for s, o in enumerate(offs)]
-    b = nemoasr.Batch(mdir, a.batch_lang, lat, S)
+    b = nemoasr.Batch(mdir, lang, lat, S)
     b.use_graphs(not a.no_graphs)
 
     def run_once():
@@ -87,8 +189,7 @@ def batch_leg(a, nemoasr, synth, mdir, cfg):
         b.run()
         wall = time.perf_counter() - t0
         st1 = b.stats()
-        d = {k: st1[k] - st0[k] for k in st1}
-        return wall, b.step_ms()[n0:], d
+        return wall, b.step_ms()[n0:], {k: st1[k] - st0[k] for k in st1}
 
     for _ in range(a.warmup):
         run_once()
@@ -103,7 +204,6 @@ def batch_leg(a, nemoasr, synth, mdir, cfg):
     rtfx = a.steps * S * nsamp / 16000.0 / wall
     flops_rows = 2.0 * gemm_params_per_row(cfg) * tot["rows"]
     enc_tflops = flops_rows / (tot["encoder_gpu_ms"] * 1e-3) / 1e12 if tot["encoder_gpu_ms"] > 0 else 0.0
-
     # many-row GEMM kernels timed one by one during a direct-launch pass of the same workload
     b.use_graphs(False)
     b.time_kernel("gemm_m*", 32768)
@@ -115,8 +215,8 @@ def batch_leg(a, nemoasr, synth, mdir, cfg):
     steps = max(int(tot["steps"]), 1)
     return {
         "workload": f"{S} streams, {lat} ms latency ({right + 1} encoder frames/chunk/stream, M = {S * (right + 1)} rows "
-                    f"per steady step), {a.batch_seconds:g} s of 16 kHz audio per stream (own seed), start offsets "
-                    f"0-{a.batch_offsets} chunks of pre-filled caches, prompt {a.batch_lang}",
+                    f"per steady step), {seconds:g} s of 16 kHz audio per stream (own seed), start offsets "
+                    f"0-{offsets} chunks of pre-filled caches, prompt {lang}",
         "streams": S, "latency_ms": lat, "rtfx": round(rtfx, 2), "audio_s_per_pass": S * nsamp / 16000.0,
         "wall_s_per_pass": round(wall / a.steps, 4),
         "p50_step_ms": round(float(np.median(sm)), 3), "p90_step_ms": round(float(np.percentile(sm, 90)), 3),
@@ -128,6 +228,7 @@ def batch_leg(a, nemoasr, synth, mdir, cfg):
         "decoder_ms_per_step": round(tot["decoder_ms"] / steps, 3),
         "joint_round_trips_per_step": round(tot["joint_steps"] / steps, 2),
         "tokens_per_pass": int(tot["tokens"] / a.steps),
+        "p_blank": p_blank(tot["rows"], tot["tokens"]),
         "encoder_gemm_tflops": round(enc_tflops, 1),
         "encoder_gemm_frac_of_bf16_peak": round(enc_tflops / MFMA_BF16_PEAK_TFLOPS, 4),
         "graphs": not a.no_graphs,
@@ -140,11 +241,40 @@ def batch_leg(a, nemoasr, synth, mdir, cfg):
 
 
 def cpu_threads() -> int:
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    if env.isdigit() and int(env) > 0:
+        return int(env)
     try:
-        n = len(os.sched_getaffinity(0))
+        return max(1, len(os.sched_getaffinity(0)))
     except AttributeError:
-        n = os.cpu_count() or 1
-    return max(1, min(16, n))
+        return os.cpu_count() or 1
+
+
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_leg(mdir, audio, right, latency, threads, sample_s):
+    import mel_ref
+    import oracle
+
+    oracle.lib().or_set_threads(threads)
+    om = oracle.Model(mdir, "en-US")
+    sample = audio[: int(sample_s * 16000)]
+    t0 = time.perf_counter()
+    o = oracle.Session(om, right)
+    o.feed_mel(mel_ref.logmel(sample), final=True)
+    dt = time.perf_counter() - t0
+    return {"value": round(sample.size / 16000.0 / dt, 4), "unit": "audio-s/s", "cores": threads, "kind": "port",
+            "sample": f"first {sample_s:g} s of the headline clip at {latency} ms latency through the oracle's C "
+                      f"restatement (log-mel + encoder + greedy RNNT), {threads} thread(s), {o.chunks} chunks, "
+                      f"{dt:.1f} s", "seconds": round(dt, 2)}
 
 
 def main():
@@ -154,20 +284,11 @@ def main():
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--latency", type=int, default=80, choices=sorted(LAT_RIGHT))
     ap.add_argument("--seconds", type=float, default=10.0)
-    ap.add_argument("--cpu-sample-s", type=float, default=10.0)
+    ap.add_argument("--cpu-sample-s", type=float, default=6.0, help="audio seconds of the all-threads CPU sample")
+    ap.add_argument("--cpu1-sample-s", type=float, default=1.0, help="audio seconds of the one-thread CPU sample")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-graphs", action="store_true")
-    ap.add_argument("--kernel", default=None, help="kernel whose launches are timed for the roofline")
-    ap.add_argument("--batch-streams", type=int, default=64, help="0 skips the multi-stream leg")
-    ap.add_argument("--batch-latency", type=int, default=560, choices=sorted(LAT_RIGHT))
-    ap.add_argument("--batch-seconds", type=float, default=20.0)
-    ap.add_argument("--batch-offsets", type=int, default=7, help="start offsets 0..this many chunks")
-    ap.add_argument("--batch-lang", default="en-US")
-    ap.add_argument("--batch-blank-bias", type=float, default=0.0,
-                    help="added to the blank logit's bias of the checkpoint for the multi-stream leg")
-    ap.add_argument("--batch-only", action="store_true")
-    ap.add_argument("--copy-calib-mib", type=int, default=0,
-                    help="first run one device copy of this many MiB (a known-size reference for HBM counters)")
+    ap.add_argument("--legs", default="S560,S1120,B64,B256", help="comma list of extra legs (empty: none)")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py: this build runs one stream set on one GPU; --gpus {a.gpus} is not supported "
@@ -177,117 +298,51 @@ def main():
     import nemoasr
     import synth
 
-    cache = os.environ.get("NEMO_MODEL_CACHE", "/tmp/nemo_models")
-    mdir = synth.write_model(os.path.join(cache, "full_s0_b0"), synth.FULL_DIMS, 0, 0.0)
+    def sub3(nsamp):  # encoder frames of a clip: mel frames (centred, 10 ms hop) subsampled x8
+        n = nsamp // 160 + 1
+        for _ in range(3):
+            n = n // 2 + 1
+        return n
+
+    mdir = model(synth)
     cfg = json.load(open(os.path.join(mdir, "config.json")))
-
-    def run_batch():
-        bb = a.batch_blank_bias
-        bdir = mdir if bb == 0 else synth.write_model(os.path.join(cache, f"full_s0_b{bb:g}"), synth.FULL_DIMS, 0, bb)
-        r = batch_leg(a, nemoasr, synth, bdir, cfg)
-        r["blank_bias"] = bb
-        return r
-
-    if a.batch_only:
-        print(json.dumps({"batch": run_batch()}), flush=True)
-        return
-    audio = synth.make_audio(a.seconds, seed=0)
-    audio_s = audio.size / 16000.0
-    right = LAT_RIGHT[a.latency]
-    piece = (right + 1) * 8 * 160
-
-    s = nemoasr.Session(mdir, "en-US", a.latency)
-    s.use_graphs(not a.no_graphs)
-    if a.copy_calib_mib:
-        g = nemoasr.Gpu()
-        nb = a.copy_calib_mib << 20
-        src, dst = g.alloc(nb), g.alloc(nb)
-        g.begin()
-        g.check(nemoasr.lib().nk_copy(g.h, src.ptr, dst.ptr, nb // 4))
-        g.end()
-        g.close()
-
-    def clip():
-        s.reset("en-US", a.latency)
-        s.use_graphs(not a.no_graphs)
-        t0 = time.perf_counter()
-        for i in range(0, audio.size, piece):
-            s.feed(audio[i:i + piece], final=i + piece >= audio.size)
-        return time.perf_counter() - t0
-
-    for _ in range(a.warmup):
-        clip()
-    times, chunk_ms, enc_gpu, chunks, toks, steps = [], [], 0.0, 0, 0, 0
-    for _ in range(a.steps):
-        times.append(clip())
-        chunk_ms.append(s.chunk_ms())
-        st = s.stats()
-        enc_gpu += nemoasr.lib().nemoasr_debug_encoder_gpu_ms(s.h)
-        chunks += st["chunks"]
-        toks += st["tokens"]
-        steps += s.joint_steps
-    wall = sum(times)
-    rtfx = a.steps * audio_s / wall
-    cms = np.concatenate(chunk_ms)
-    wb = weight_bytes_per_chunk(cfg)
-    enc_ms_per_chunk = enc_gpu / max(chunks, 1)
-
-    # dominant kernel: hipEvents around each of its launches during a direct-launch replay
-    kname = a.kernel or DOMINANT.get(a.latency, "gemm_fr*")
-    s.reset("en-US", a.latency)
-    s.use_graphs(False)
-    s.time_kernel(kname, 32768)
-    for i in range(0, audio.size, piece):
-        s.feed(audio[i:i + piece], final=i + piece >= audio.size)
-    kms, kn, kbytes = s.kernel_ms()
-    s.time_kernel(None, 0)
-    achieved = (kbytes / max(kn, 1)) / (kms * 1e-3) / 1e9 if kn and kms > 0 else 0.0
-    gpu_name = s.gpu_name
-    s.close()
-    batch = run_batch() if a.batch_streams > 0 else None
+    head = single_leg(a, nemoasr, synth, mdir, cfg, a.latency, a.seconds, frames_fn=sub3)
+    legs = {}
+    want = [x for x in a.legs.split(",") if x]
+    if "S560" in want:
+        legs["S560"] = single_leg(a, nemoasr, synth, mdir, cfg, 560, 10.0, frames_fn=sub3)
+    if "S1120" in want:
+        legs["S1120"] = single_leg(a, nemoasr, synth, model(synth, SKEW_S1120), cfg, 1120, 30.0, frames_fn=sub3)
+        legs["S1120"]["skew"] = {"blank_bias": SKEW_S1120[0], "label_shift": SKEW_S1120[1]}
+    if "B64" in want:
+        legs["B64"] = batch_leg(a, nemoasr, synth, mdir, cfg, 64, 560, 20.0, 7, "en-US")
+    if "B256" in want:
+        legs["B256"] = batch_leg(a, nemoasr, synth, model(synth, SKEW_B256), cfg, 256, 1120, 60.0, 4, "auto")
+        legs["B256"]["skew"] = {"blank_bias": SKEW_B256[0], "label_shift": SKEW_B256[1]}
 
     cpu = None
     if not a.no_cpu:
-        import mel_ref
-        import oracle
-
+        audio = synth.make_audio(a.seconds, seed=0)
+        right = LAT_RIGHT[a.latency]
         n = cpu_threads()
-        oracle.lib().or_set_threads(n)
-        om = oracle.Model(mdir, "en-US")
-        sample = audio[: int(a.cpu_sample_s * 16000)]
-        t0 = time.perf_counter()
-        o = oracle.Session(om, right)
-        o.feed_mel(mel_ref.logmel(sample), final=True)
-        dt = time.perf_counter() - t0
-        cpu = {"value": round(sample.size / 16000.0 / dt, 4), "unit": "audio-s/s", "cores": n, "kind": "port",
-               "sample": f"first {a.cpu_sample_s:g} s of the same clip at {a.latency} ms latency through the oracle's "
-                         f"C restatement (log-mel + encoder + greedy RNNT), {n} threads, {o.chunks} chunks"}
+        cpu = cpu_leg(mdir, audio, right, a.latency, n, a.cpu_sample_s)
+        cpu["cpu_model"] = cpu_model()
+        cpu["nproc"] = os.cpu_count()
+        cpu["single_thread"] = cpu_leg(mdir, audio, right, a.latency, 1, a.cpu1_sample_s)
 
     out = {
-        "metric": METRIC, "value": round(rtfx, 3), "unit": "audio-s/s", "n_gpus": 1, "steps": a.steps,
-        "warmup": a.warmup, "ms_per_step": round(1e3 * wall / a.steps, 3), "higher_is_better": True,
+        "metric": METRIC, "value": head["rtfx"], "unit": "audio-s/s", "n_gpus": 1, "steps": a.steps,
+        "warmup": a.warmup, "ms_per_step": head["ms_per_pass"], "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "f32",
         "data": "synthetic: seeded random-init bf16 weights (seed 0), seeded pink noise -20 dBFS + sine chirps",
-        "config": {
-            "workload": f"1 stream, {a.latency} ms latency ({right + 1} encoder frame(s)/chunk), {audio_s:g} s of 16 kHz "
-                        "audio, FastConformer 0.6B (24 x d1024, FF 4096, 8 heads) + RNNT (2 x LSTM 640, vocab 1024+blank)",
-            "latency_ms": a.latency, "streams": 1, "audio_s": audio_s, "graphs": not a.no_graphs,
-            "weights": "bf16", "activations": "f32",
-            "chunks_per_clip": int(chunks / a.steps), "tokens_per_clip": int(toks / a.steps),
-            "joint_round_trips_per_clip": int(steps / a.steps),
-            "p50_chunk_ms": round(float(np.median(cms)), 4), "p90_chunk_ms": round(float(np.percentile(cms, 90)), 4),
-            "encoder_gpu_ms_per_chunk": round(enc_ms_per_chunk, 4),
-            "encoder_weight_bytes_per_chunk": wb,
-            "encoder_chunk_hbm_gbs": round(wb / (enc_ms_per_chunk * 1e-3) / 1e9, 1) if enc_ms_per_chunk > 0 else None,
-            "gpu": gpu_name,
-        },
-        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "kernel": kname,
-                     "launches": kn, "mean_launch_us": round(kms * 1e3, 3),
-                     "bytes_per_launch": round(kbytes / max(kn, 1))},
+        "config": dict(head, workload=head["workload"] + ", FastConformer 0.6B (24 x d1024, FF 4096, 8 heads) + RNNT "
+                                                         "(2 x LSTM 640, vocab 1024+blank)",
+                       streams=1, weights="bf16", activations="f32"),
+        "roofline": head["roofline"],
         "cpu_baseline": cpu,
-        "batch": batch,
+        "legs": legs,
     }
+    out["config"].pop("roofline")
     print(json.dumps(out), flush=True)
 
 

@@ -15,7 +15,21 @@
  *   nk_compact          compact_caches               src/encoder.c:199-211 (one launch for all layers)
  *   nk_lstm_cell        lstm_cell dispatch           src/decoder.c:71-73
  *   nk_joint_argmax     joint_partial + argmax_reduce src/decoder.c:79-90
- * and the GPU runtime of src/gpu.h:20-41 (gpu_* below).
+ *
+ * The GPU runtime (gpu_* below) is a re-design of src/gpu.h:20-41, not the same interface: the
+ * host here is this library's own (the launchers compute their grids from the shapes), so the
+ * reference's dispatch forms were folded into one launch call:
+ *   gpu_create(metal_source)          -> gpu_create(): loads the gfx950 code object linked into
+ *                                        the library (hipModuleLoadData)
+ *   gpu_buf_alloc (shared storage)    -> gpu_buf_alloc (device memory, zero-filled)
+ *   gpu_buf_ptr (host address)        -> gpu_buf_dptr (device address) + gpu_upload / gpu_download
+ *   GPU_BUF(b, off) / GPU_BYTES(p)    -> device pointers and sizes inside one by-value argument struct
+ *   gpu_dispatch (total threads),     -> gpu_launch (workgroup counts and sizes)
+ *   gpu_dispatch_groups (groups)
+ *   gpu_dispatch_groups_fc (function -> one kernel symbol per specialisation, looked up by name
+ *     constants, cached per value set)   (e.g. gemv_r1_n4_k2, gemm_fr_w16s8)
+ *   gpu_begin / gpu_end / gpu_last_ms -> same roles (one stream, hipEvents)
+ * The kernel argument structs are likewise re-designed (nemo-c_amd/csrc/kernel_params.h).
  */
 #ifndef NEMO_KERNELS_H
 #define NEMO_KERNELS_H
@@ -86,12 +100,44 @@ int nk_gemm_argmax_rows(gpu_t *g, const float *A, uint32_t lda, const uint16_t *
 /* K split of the many-row residual updates (accumulate, no bias, no activation): -1 (default) by
  * tile count, 0 never, 1 always where K has more than one block.  All three give the same bits.
  * Returns the previous setting. */
-int nk_gemm_split(int mode);
+int nk_gemm_ksplit(int mode);
+/* Few-row residual updates (5..16 rows): 1 (default) splits K over four workgroups with an ordered
+ * combine, 0 keeps K in one workgroup (more wavefronts).  Returns the previous setting. */
+int nk_gemm_fr_ksplit(int on);
 /* Kernel selection: 0 automatic (by row count), 1 first-generation VALU GEMV (M <= 4),
  * 2 few-row MFMA (M <= 16), 3 many-row MFMA, 4 weight-streaming GEMV (M <= 4),
  * 5 first-generation many-row MFMA (register-staged).
  * Returns the previous setting. */
 int nk_gemm_force(int kind);
+/* Split rows: a row of K activations stored as K bf16 hi = RNE(a) then K bf16 lo = RNE(a - hi),
+ * the operand form the many-row MFMA kernels multiply (hi and lo each against the bf16 weights).
+ * A producer that writes them saves every consumer GEMM the split (its K loop then has no vector
+ * work) and gives the same bits.  The batched encoder keeps the activations between its kernels in
+ * this form.  nk_gemm_split: the many-row GEMM with exactly one of A (f32 rows) / A2 (split rows,
+ * lda in bf16 elements >= 2K) and one of C (f32) / C2 (split rows of the nout outputs, ldc >= 2 nout;
+ * no accumulate, row map or GLU). */
+int nk_gemm_split(gpu_t *g, const float *A, const uint16_t *A2, uint32_t lda, const uint16_t *W, uint32_t ldw,
+                  const float *bias, float *C, uint16_t *C2, uint32_t ldc, const int *crow, uint32_t M, uint32_t N,
+                  uint32_t K, int act, int accumulate, float alpha);
+/* A many-row residual update left pending: C += alpha * A W^T is computed as nparts partial rows
+ * (the K blocks' sums) in the context's scratch and applied later, in block order, by the kernel
+ * that reads C next: nk_layernorm2_split (the batched encoder: every residual update is followed by
+ * a LayerNorm of the residual) or nk_resid_fold.  The same bits as nk_gemm_split's update.  The
+ * scratch holds one pending update at a time. */
+typedef struct {
+    const float *parts;
+    uint32_t nparts;
+    float alpha;
+} nk_resid_t;
+int nk_gemm_resid(gpu_t *g, const float *A, const uint16_t *A2, uint32_t lda, const uint16_t *W, uint32_t ldw, float *C,
+                  uint32_t ldc, uint32_t M, uint32_t N, uint32_t K, float alpha, nk_resid_t *pend);
+int nk_resid_fold(gpu_t *g, float *C, uint32_t ldc, uint32_t M, uint32_t N, const nk_resid_t *pend);
+/* LayerNorm of M rows (D <= 1024, one wavefront per row) whose GEMM-feeding output goes to Ys as
+ * split rows (row stride 2D): the single LayerNorm (g2 NULL) writes only Ys; the pair writes
+ * LN(X; g1, b1) to Y1 (f32) and LN(Y1; g2, b2) to Ys.  With pend (from nk_gemm_resid, may be NULL)
+ * the pending residual update is applied to X first and X is written back. */
+int nk_layernorm2_split(gpu_t *g, float *X, const nk_resid_t *pend, const float *g1, const float *b1, const float *g2,
+                        const float *b2, float *Y1, uint16_t *Ys, uint32_t M, uint32_t D, float eps);
 /* Name of the kernel nk_gemm would launch for these shapes (for profiling and tests). */
 const char *nk_gemm_kernel_name(uint32_t M, uint32_t N, uint32_t K, int act);
 
@@ -140,8 +186,16 @@ int nk_attention_rel_rows(gpu_t *g, const float *kv, uint32_t ld, const int *row
 int nk_attention_rel_chunks(gpu_t *g, const float *kv, uint32_t ld, const int *chunks, uint32_t nchunks, const float *P,
                             const float *bias_u, const float *bias_v, float *O, uint32_t Lmax, uint32_t H, uint32_t dh,
                             uint32_t D, float scale);
+/* Same, output as split rows (row stride 2D) to Os. */
+int nk_attention_rel_chunks_split(gpu_t *g, const float *kv, uint32_t ld, const int *chunks, uint32_t nchunks,
+                                  const float *P, const float *bias_u, const float *bias_v, uint16_t *Os, uint32_t Lmax,
+                                  uint32_t H, uint32_t dh, uint32_t D, float scale);
 int nk_dwconv_ln_silu_rows(gpu_t *g, const float *din_base, const int *rows, uint32_t M, const float *W,
                            const float *gamma, const float *beta, float *Y, uint32_t D, uint32_t taps, float eps);
+/* Same, output as split rows (row stride 2D) to Ys (Y NULL) or f32 to Y (Ys NULL). */
+int nk_dwconv_ln_silu_rows_split(gpu_t *g, const float *din_base, const int *rows, uint32_t M, const float *W,
+                                 const float *gamma, const float *beta, float *Y, uint16_t *Ys, uint32_t D, uint32_t taps,
+                                 float eps);
 int nk_conv2d_c1_s2_relu(gpu_t *g, const float *X, const float *W, const float *bias, float *Y, uint32_t T,
                          uint32_t F, uint32_t T1, uint32_t F1, uint32_t C);
 int nk_dwconv2d_s2(gpu_t *g, const float *X, const float *W, const float *bias, float *Y, uint32_t T, uint32_t F,

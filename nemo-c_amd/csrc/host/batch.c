@@ -464,6 +464,17 @@ nemoasr_batch_t *nemoasr_batch_open(const char *model_dir, const char *language,
     b->c4 = gpu_buf_alloc(g, S * (size_t)b->T3max * b->F3 * CH * fs);
     b->flat = gpu_buf_alloc(g, S * (size_t)b->T3max * b->F3 * CH * fs);
     b->pre_out = gpu_buf_alloc(g, S * (size_t)b->T3max * D * fs);
+    /* the residual updates' partial rows (at most one part per 1024 of K, the feed-forward width)
+     * live in the context's scratch: sized now, before any step is captured */
+    {
+        size_t parts = (size_t)c->d_ff / 1024;
+        parts = parts < 2 ? 2 : parts > 8 ? 8 : parts;
+        if (!gpu_scratch_ws(g, parts * Mm * D)) {
+            snprintf(err, errlen, "batch: cannot allocate the residual-update scratch");
+            nemoasr_batch_close(b);
+            return NULL;
+        }
+    }
     b->h = gpu_buf_alloc(g, Mm * D * fs);
     b->tmp = gpu_buf_alloc(g, Mm * D * fs);
     b->lnb = gpu_buf_alloc(g, Mm * D * fs);
@@ -893,57 +904,75 @@ static void launch_pre_encode(nemoasr_batch_t *b, const float *win, int nwin, in
 
 /* conformer blocks + prompt + joint projection on the M rows in h (src/encoder.c:144-197).
  * The order of operations and the LayerNorm placement are those of the single-stream encoder;
- * crow maps every row to its stream's cache row, rows is the attention/conv row table. */
+ * crow maps every row to its stream's cache row, rows is the attention/conv row table.
+ * Activations that only feed a GEMM (LayerNorm outputs, the feed-forward hidden rows, attention
+ * and conv module outputs, the prompt's hidden rows) are kept as split rows (nk_gemm_split): their
+ * producers write bf16 hi / lo once, in the buffers that hold the f32 rows otherwise (a split row
+ * of K values takes the bytes of K floats).  The residual stream, the caches and the rows that are
+ * dumped stay f32.  Each residual update (FF down, out_proj, pw2) is left pending (nk_gemm_resid)
+ * and applied by the LayerNorm that follows it, which reads the residual rows anyway. */
 static void launch_blocks(nemoasr_batch_t *b, uint32_t M, const int *crow, const int *rows, const int *chunks,
                           uint32_t nchunks) {
     model_t *m = b->m;
     gpu_t *g = b->g;
     const model_cfg_t *cf = &m->cfg;
     const uint32_t D = (uint32_t)cf->d_model, FF = (uint32_t)cf->d_ff, H = (uint32_t)cf->n_heads,
-                   dh = (uint32_t)cf->head_dim, nl = (uint32_t)cf->n_layers;
+                   dh = (uint32_t)cf->head_dim, nl = (uint32_t)cf->n_layers, taps = (uint32_t)cf->conv_kernel;
     const float eps = cf->ln_eps, scale = 1.0f / sqrtf((float)dh);
     float *R[2] = { gpu_buf_dptr(b->h), gpu_buf_dptr(b->tmp) };
-    float *lnbuf = gpu_buf_dptr(b->lnb), *ff = gpu_buf_dptr(b->ff), *att = gpu_buf_dptr(b->att), *y = gpu_buf_dptr(b->y);
+    uint16_t *lns = gpu_buf_dptr(b->lnb), *ffs = gpu_buf_dptr(b->ff), *ys = gpu_buf_dptr(b->y);
+    float *att = gpu_buf_dptr(b->att);
+    uint16_t *atts = (uint16_t *)att;
     int cur = 0;
+    nk_resid_t pend = { 0 }; /* the residual update the next LayerNorm applies */
     for (uint32_t l = 0; l < nl; ++l) {
         const layer_dev_t *W = &m->L[l];
         float *kv = (float *)gpu_buf_dptr(b->kv) + (size_t)l * b->kv_lstride;
         float *din = (float *)gpu_buf_dptr(b->din) + (size_t)l * b->din_lstride;
+        /* FF1 half step: LN (paired with the previous block's output norm), up + SiLU, down */
         if (l == 0) {
-            nk_gemm_ln(g, R[0], D, W->ff1_w1, D, NULL, ff, FF, NULL, M, FF, D, NK_ACT_SILU, 0, 1.0f, 1, W->ln_ff1_g,
-                       W->ln_ff1_b, NULL, NULL, NULL, lnbuf, eps);
+            nk_layernorm2_split(g, R[0], NULL, W->ln_ff1_g, W->ln_ff1_b, NULL, NULL, NULL, lns, M, D, eps);
         } else {
             const layer_dev_t *Wp = &m->L[l - 1];
             const int prev = cur;
             cur ^= 1;
-            nk_gemm_ln(g, R[prev], D, W->ff1_w1, D, NULL, ff, FF, NULL, M, FF, D, NK_ACT_SILU, 0, 1.0f, 2, Wp->ln_out_g,
-                       Wp->ln_out_b, W->ln_ff1_g, W->ln_ff1_b, R[cur], lnbuf, eps);
+            nk_layernorm2_split(g, R[prev], &pend, Wp->ln_out_g, Wp->ln_out_b, W->ln_ff1_g, W->ln_ff1_b, R[cur], lns, M,
+                                D, eps);
         }
         float *res = R[cur];
-        nk_gemm(g, ff, FF, W->ff1_w2, FF, NULL, res, D, M, D, FF, NK_ACT_NONE, 1, 0.5f);
-        nk_gemm_ln(g, res, D, W->wqkv, D, NULL, kv, 3 * D, crow, M, 3 * D, D, NK_ACT_NONE, 0, 1.0f, 1, W->ln_att_g,
-                   W->ln_att_b, NULL, NULL, NULL, lnbuf, eps);
-        if (b->chunk_attn)
-            nk_attention_rel_chunks(g, kv, 3 * D, chunks, nchunks, W->ptab, W->bias_u, W->bias_v, att, (uint32_t)b->Lmax, H,
-                                    dh, D, scale);
-        else
+        nk_gemm_split(g, NULL, lns, 2 * D, W->ff1_w1, D, NULL, NULL, ffs, 2 * FF, NULL, M, FF, D, NK_ACT_SILU, 0, 1.0f);
+        nk_gemm_resid(g, NULL, ffs, 2 * FF, W->ff1_w2, FF, res, D, M, D, FF, 0.5f, &pend);
+        /* attention: LN, QKV into the cache rows, attention, out_proj into the residual */
+        nk_layernorm2_split(g, res, &pend, W->ln_att_g, W->ln_att_b, NULL, NULL, NULL, lns, M, D, eps);
+        nk_gemm_split(g, NULL, lns, 2 * D, W->wqkv, D, NULL, kv, NULL, 3 * D, crow, M, 3 * D, D, NK_ACT_NONE, 0, 1.0f);
+        if (b->chunk_attn) {
+            nk_attention_rel_chunks_split(g, kv, 3 * D, chunks, nchunks, W->ptab, W->bias_u, W->bias_v, atts,
+                                          (uint32_t)b->Lmax, H, dh, D, scale);
+            nk_gemm_resid(g, NULL, atts, 2 * D, W->wo, D, res, D, M, D, D, 1.0f, &pend);
+        } else {
             nk_attention_rel_rows(g, kv, 3 * D, rows, M, W->ptab, W->bias_u, W->bias_v, att, (uint32_t)b->Lmax, H, dh, D,
                                   scale);
-        nk_gemm(g, att, D, W->wo, D, NULL, res, D, M, D, D, NK_ACT_NONE, 1, 1.0f);
-        nk_gemm_ln(g, res, D, W->pw1, D, NULL, din, D, crow, M, 2 * D, D, NK_ACT_GLU, 0, 1.0f, 1, W->ln_conv_g,
-                   W->ln_conv_b, NULL, NULL, NULL, lnbuf, eps);
-        nk_dwconv_ln_silu_rows(g, din, rows, M, W->dw_w, W->bn_g, W->bn_b, y, D, (uint32_t)cf->conv_kernel, eps);
-        nk_gemm(g, y, D, W->pw2, D, NULL, res, D, M, D, D, NK_ACT_NONE, 1, 1.0f);
-        nk_gemm_ln(g, res, D, W->ff2_w1, D, NULL, ff, FF, NULL, M, FF, D, NK_ACT_SILU, 0, 1.0f, 1, W->ln_ff2_g,
-                   W->ln_ff2_b, NULL, NULL, NULL, lnbuf, eps);
-        nk_gemm(g, ff, FF, W->ff2_w2, FF, NULL, res, D, M, D, FF, NK_ACT_NONE, 1, 0.5f);
+            nk_gemm_resid(g, att, NULL, D, W->wo, D, res, D, M, D, D, 1.0f, &pend);
+        }
+        /* conv module: LN, pw1 + GLU into the conv cache rows, depthwise conv + LN + SiLU, pw2 */
+        nk_layernorm2_split(g, res, &pend, W->ln_conv_g, W->ln_conv_b, NULL, NULL, NULL, lns, M, D, eps);
+        nk_gemm_split(g, NULL, lns, 2 * D, W->pw1, D, NULL, din, NULL, D, crow, M, 2 * D, D, NK_ACT_GLU, 0, 1.0f);
+        nk_dwconv_ln_silu_rows_split(g, din, rows, M, W->dw_w, W->bn_g, W->bn_b, NULL, ys, D, taps, eps);
+        nk_gemm_resid(g, NULL, ys, 2 * D, W->pw2, D, res, D, M, D, D, 1.0f, &pend);
+        /* FF2 half step */
+        nk_layernorm2_split(g, res, &pend, W->ln_ff2_g, W->ln_ff2_b, NULL, NULL, NULL, lns, M, D, eps);
+        nk_gemm_split(g, NULL, lns, 2 * D, W->ff2_w1, D, NULL, NULL, ffs, 2 * FF, NULL, M, FF, D, NK_ACT_SILU, 0, 1.0f);
+        nk_gemm_resid(g, NULL, ffs, 2 * FF, W->ff2_w2, FF, res, D, M, D, FF, 0.5f, &pend);
     }
+    /* last output norm, prompt (W0 + ReLU, W2) and joint.enc (src/encoder.c:189-194) */
     const layer_dev_t *Wl = &m->L[nl - 1];
     const uint32_t PH = (uint32_t)cf->prompt_hidden, NP = (uint32_t)cf->num_prompts, JH = (uint32_t)b->J;
-    float *ph = gpu_buf_dptr(b->ph), *pr = gpu_buf_dptr(b->prompted);
-    nk_gemm_ln(g, R[cur], D, m->prompt_w0, D + NP, m->prompt_b0_eff, ph, PH, NULL, M, PH, D, NK_ACT_RELU, 0, 1.0f, 1,
-               Wl->ln_out_g, Wl->ln_out_b, NULL, NULL, NULL, lnbuf, eps);
-    nk_gemm(g, ph, PH, m->prompt_w2, PH, m->prompt_b2, pr, D, M, D, PH, NK_ACT_NONE, 0, 1.0f);
+    uint16_t *phs = gpu_buf_dptr(b->ph);
+    float *pr = gpu_buf_dptr(b->prompted);
+    nk_layernorm2_split(g, R[cur], &pend, Wl->ln_out_g, Wl->ln_out_b, NULL, NULL, NULL, lns, M, D, eps);
+    nk_gemm_split(g, NULL, lns, 2 * D, m->prompt_w0, D + NP, m->prompt_b0_eff, NULL, phs, 2 * PH, NULL, M, PH, D,
+                  NK_ACT_RELU, 0, 1.0f);
+    nk_gemm_split(g, NULL, phs, 2 * PH, m->prompt_w2, PH, m->prompt_b2, pr, NULL, D, NULL, M, D, PH, NK_ACT_NONE, 0, 1.0f);
     nk_gemm(g, pr, D, m->joint_enc_w, D, m->joint_enc_b, gpu_buf_dptr(b->joint_enc), JH, M, JH, D, NK_ACT_NONE, 0, 1.0f);
 }
 

@@ -104,6 +104,8 @@ const float *gpu_zeros(gpu_t *g);
  * row count; 1 always uses the many-row kernels (batched streams: every row's arithmetic is then
  * the same whatever the number of rows in the launch). */
 void gpu_set_many_rows(gpu_t *g, int on);
+/* HIP device index the context runs on. */
+int gpu_device_index(const gpu_t *g);
 int gpu_many_rows(const gpu_t *g);
 
 /* Number of kernel launches issued since creation (for tests and the launch-count check). */

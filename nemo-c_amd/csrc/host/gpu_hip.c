@@ -122,6 +122,7 @@ gpu_t *gpu_create(char *err, size_t errlen) {
 const int *gpu_iota(gpu_t *g) { return g->iota; }
 void gpu_set_many_rows(gpu_t *g, int on) { g->many_rows = on != 0; }
 int gpu_many_rows(const gpu_t *g) { return g->many_rows; }
+int gpu_device_index(const gpu_t *g) { return g->dev; }
 const float *gpu_zeros(gpu_t *g) { return g->zeros; }
 
 void gpu_destroy(gpu_t *g) {

@@ -10,7 +10,7 @@
 static int g_force = 0;
 static int g_split = -1; /* many-row residual updates: -1 K split chosen by tile count, 0 never, 1 always */
 
-int nk_gemm_split(int mode) {
+int nk_gemm_ksplit(int mode) {
     const int prev = g_split;
     g_split = mode < 0 ? -1 : mode > 0 ? 1 : 0;
     return prev;
@@ -48,11 +48,20 @@ static int fr_ok(uint32_t M, uint32_t K, int act) {
     return M <= NK_FEW_ROWS && K % 32 == 0 && K <= 4608 && (act != NK_ACT_GLU || K <= 1024);
 }
 
+static int g_fr_ksplit = 1; /* few-row residual updates: K split over four workgroups (1) or not (0) */
+
+int nk_gemm_fr_ksplit(int on) {
+    const int prev = g_fr_ksplit;
+    g_fr_ksplit = on != 0;
+    return prev;
+}
+
 static fr_plan_t fr_plan(uint32_t nout, uint32_t K, int act, int accumulate, int has_bias, int ln) {
     const uint32_t S = K / 32;
     fr_plan_t p = { 4, 8, 1 };
     if (ln || act == NK_ACT_GLU) return p;
-    if (accumulate && act == NK_ACT_NONE && !has_bias && (nout + 15) / 16 < 128 && S % 4 == 0 && S / 4 <= 32) {
+    if (g_fr_ksplit && accumulate && act == NK_ACT_NONE && !has_bias && (nout + 15) / 16 < 128 && S % 4 == 0 &&
+        S / 4 <= 32) {
         p.KS = 4;
         p.SPW = S / 4 <= 8 ? 2 : 8;
         return p;
@@ -111,12 +120,21 @@ typedef struct {
 
 /* Many-row GEMM on the direct-to-LDS MFMA kernels (kernels/nk_mx.hip).  Tile choice: the largest
  * of 128x128, 64x128, 64x64 whose tile count reaches about 400 workgroups; otherwise the smallest
- * tile that divides the output columns.  Residual updates (accumulate, no bias, no activation) run
- * on the _acc kernels, whose K sum is blocked (mx_kblocks); below ~400 tiles their K is split one
- * block per workgroup, combined in block order by the tile's last workgroup (same bits as
- * unsplit).  Returns 1 when no tile divides the output columns (the caller falls back), else the
- * launch status. */
-static int launch_mx(gpu_t *g, NkGemmArgs *a, uint32_t M, uint32_t nout, uint32_t K, int glu, int resid) {
+ * tile that divides the output columns.  Residual updates (accumulate, no bias, no activation, no
+ * row map) run on the _acc kernels: their K sum is blocked (mx_kblocks), below ~400 tiles K is
+ * split one block per workgroup, and the sums go to partial rows in the scratch (nparts of them,
+ * same bits either way); *pend then describes the update still to apply (NkFoldArgs).
+ * Returns 1 when no tile divides the output columns (the caller falls back), -2 when a fixed
+ * scratch region is too small, else the launch status. */
+typedef struct {
+    float *ws; /* fixed region (no allocation; a launch that needs more is refused), or NULL */
+    size_t ws_floats;
+} mx_scratch_t;
+
+static int launch_mx_s(gpu_t *g, NkGemmArgs *a, uint32_t M, uint32_t nout, uint32_t K, int glu, int resid,
+                       const mx_scratch_t *sc, nk_resid_t *pend) {
+    /* split-row A (_s) and split-row outputs (_so) variants */
+    const char *sfx = a->A2 ? (a->C2 ? "_s_so" : "_s") : (a->C2 ? "_so" : "");
     static const struct { const char *name, *glu_name, *acc_name; uint32_t bm, bn; } cfg[] = {
         { "gemm_mx128x128", "gemm_mx128x128_glu", "gemm_mx128x128_acc", 128, 128 },
         { "gemm_mx64x128", "gemm_mx64x128_glu", "gemm_mx64x128_acc", 64, 128 },
@@ -146,19 +164,94 @@ static int launch_mx(gpu_t *g, NkGemmArgs *a, uint32_t M, uint32_t nout, uint32_
         a->kblocks = mx_kblocks(K);
         /* split below ~400 tiles (measured on 64 x 64 tiles: about 448 workgroups at 448 rows) */
         if (a->kblocks > 1 && (g_split == 1 || (g_split < 0 && tiles < 400))) kz = a->kblocks;
-        if (kz > 1) {
-            a->ws = gpu_scratch_ws(g, (size_t)tiles * kz * cfg[pick_i].bm * cfg[pick_i].bn);
-            a->counters = gpu_scratch_counters(g, tiles);
-            /* no scratch (a capture that cannot grow it): unsplit gives the same bits */
-            if (!a->ws || !a->counters) kz = 1;
+        const size_t need = (size_t)kz * M * nout;
+        if (sc && sc->ws) {
+            if (need > sc->ws_floats) return -2;
+            a->ws = sc->ws;
+        } else {
+            a->ws = gpu_scratch_ws(g, need);
+            if (!a->ws && kz > 1) { /* a capture that cannot grow the scratch: unsplit, same bits */
+                kz = 1;
+                a->ws = gpu_scratch_ws(g, (size_t)M * nout);
+            }
+            if (!a->ws) return bad(g, "gemm: residual-update scratch unavailable (size it before capture)");
         }
+        pend->parts = a->ws;
+        pend->nparts = kz;
+        pend->alpha = a->alpha;
     }
     const uint32_t tm = (M + cfg[pick_i].bm - 1) / cfg[pick_i].bm;
     a->splits = kz;
     a->group_m = tm <= 8 ? tm : (tm + 3) / 4;
     const uint32_t total = tiles * kz, per = (total + 7) / 8;
-    const char *name = resid ? cfg[pick_i].acc_name : glu ? cfg[pick_i].glu_name : cfg[pick_i].name;
+    char name[40];
+    snprintf(name, sizeof name, "%s%s", resid ? cfg[pick_i].acc_name : glu ? cfg[pick_i].glu_name : cfg[pick_i].name, sfx);
     return gpu_launch(g, name, a, sizeof *a, 8 * per, 1, 1, 256, 1, 1);
+}
+
+static int launch_mx(gpu_t *g, NkGemmArgs *a, uint32_t M, uint32_t nout, uint32_t K, int glu, int resid) {
+    nk_resid_t pend = { 0 };
+    const int rc = launch_mx_s(g, a, M, nout, K, glu, resid, NULL, &pend);
+    if (rc || !resid) return rc;
+    return nk_resid_fold(g, a->C, a->ldc, M, nout, &pend);
+}
+
+int nk_resid_fold(gpu_t *g, float *C, uint32_t ldc, uint32_t M, uint32_t N, const nk_resid_t *pend) {
+    if (!M || !pend || !pend->nparts) return 0;
+    if (N % 4 || ldc % 4 || (uintptr_t)C % 16) return bad(g, "resid_fold: N, ldc multiples of 4, C 16-byte aligned");
+    NkFoldArgs f = { C, pend->parts, M, N, ldc, pend->nparts, pend->alpha, 0 };
+    return gpu_launch(g, "resid_fold", &f, sizeof f, (uint32_t)(((uint64_t)M * (N / 4) + 255) / 256), 1, 1, 256, 1, 1);
+}
+
+/* The many-row GEMM with split-row operands (the batched encoder's activations between kernels):
+ * exactly one of A (f32 rows of lda floats) and A2 (split rows, lda bf16 elements, K hi then K lo)
+ * and one of C (f32, += when accumulating, row map crow) and C2 (split rows of the nout outputs,
+ * ldc bf16 elements; no accumulate, no row map, no GLU).  With pend set, a residual update
+ * (accumulate, no bias, no activation, no row map) leaves C untouched and returns the update in
+ * *pend for the next LayerNorm (nk_layernorm2_split) or nk_resid_fold to apply; otherwise C is
+ * updated by the call. */
+static int gemm_split_core(gpu_t *g, const float *A, const uint16_t *A2, uint32_t lda, const uint16_t *W, uint32_t ldw,
+                           const float *bias, float *C, uint16_t *C2, uint32_t ldc, const int *crow, uint32_t M,
+                           uint32_t N, uint32_t K, int act, int accumulate, float alpha, const mx_scratch_t *sc,
+                           nk_resid_t *pend) {
+    if (pend) memset(pend, 0, sizeof *pend);
+    if (!M) return 0;
+    const int glu = act == NK_ACT_GLU;
+    const uint32_t nout = glu ? N / 2 : N;
+    if (!N || !K || (glu && (N & 1)) || K % 32 || !A == !A2 || !C == !C2)
+        return bad(g, "gemm_split: one A form, one C form, K % 32 == 0");
+    if (!aligned16(W) || ldw % 8 || K > ldw) return bad(g, "gemm_split: W 16-byte aligned, ldw % 8 == 0, K <= ldw");
+    if (A ? (!aligned16(A) || lda % 4 || K > lda) : (!aligned16(A2) || lda % 8 || 2 * K > lda))
+        return bad(g, "gemm_split: A 16-byte aligned rows of at least K values (split: 2K, lda % 8 == 0)");
+    if (C2 && (glu || accumulate || crow || ldc < 2 * nout || ldc % 4 || (uintptr_t)C2 % 8))
+        return bad(g, "gemm_split: split outputs take no GLU, accumulate or row map; ldc >= 2 nout");
+    if (C && ldc < nout) return bad(g, "gemm_split: ldc < output width");
+    const int resid = accumulate && !bias && act == NK_ACT_NONE && !crow && nout % 4 == 0;
+    if (pend && !resid) return bad(g, "gemm_split: a deferred update needs accumulate, no bias, activation or row map");
+    NkGemmArgs a;
+    memset(&a, 0, sizeof a);
+    a.A = A; a.A2 = A2; a.W = W; a.bias = bias; a.C = C; a.C2 = C2; a.crow = crow;
+    a.M = M; a.N = N; a.K = K; a.lda = lda; a.ldw = ldw; a.ldc = ldc;
+    a.act = (uint32_t)act; a.accumulate = (uint32_t)(accumulate != 0); a.alpha = alpha; a.splits = 1;
+    gpu_next_bytes(g, 2.0 * N * K + 4.0 * M * K + 4.0 * M * nout * (accumulate ? 2 : 1) + (bias ? 4.0 * N : 0.0));
+    gpu_next_flops(g, 2.0 * M * N * K);
+    nk_resid_t local;
+    const int rc = launch_mx_s(g, &a, M, nout, K, glu, resid, sc, pend ? pend : &local);
+    if (rc == -2) return bad(g, "gemm_split: the K split of this shape needs more than the fixed scratch holds");
+    if (rc == 1) return bad(g, "gemm_split: no tile divides the output columns");
+    if (rc || !resid || pend) return rc;
+    return nk_resid_fold(g, C, ldc, M, nout, &local);
+}
+
+int nk_gemm_split(gpu_t *g, const float *A, const uint16_t *A2, uint32_t lda, const uint16_t *W, uint32_t ldw,
+                  const float *bias, float *C, uint16_t *C2, uint32_t ldc, const int *crow, uint32_t M, uint32_t N,
+                  uint32_t K, int act, int accumulate, float alpha) {
+    return gemm_split_core(g, A, A2, lda, W, ldw, bias, C, C2, ldc, crow, M, N, K, act, accumulate, alpha, NULL, NULL);
+}
+
+int nk_gemm_resid(gpu_t *g, const float *A, const uint16_t *A2, uint32_t lda, const uint16_t *W, uint32_t ldw, float *C,
+                  uint32_t ldc, uint32_t M, uint32_t N, uint32_t K, float alpha, nk_resid_t *pend) {
+    return gemm_split_core(g, A, A2, lda, W, ldw, NULL, C, NULL, ldc, NULL, M, N, K, NK_ACT_NONE, 1, alpha, NULL, pend);
 }
 
 int nk_gemm_argmax(gpu_t *g, const float *A, uint32_t lda, const uint16_t *W, uint32_t ldw, const float *bias,
@@ -296,7 +389,7 @@ int nk_layernorm2(gpu_t *g, const float *X, const float *g1, const float *b1, co
                   float *Y1, float *Y2, uint32_t M, uint32_t D, float eps) {
     if (!M) return 0;
     if (D > NK_ROW_MAX || D % 4) return bad(g, "layernorm: D must be a multiple of 4, at most 4096");
-    NkLnArgs a = { X, g1, b1, g2, b2, Y1, Y2, M, D, eps, 0 };
+    NkLnArgs a = { X, g1, b1, g2, b2, Y1, Y2, M, D, eps, 0, NULL, NULL, 0, 0.0f };
     /* many rows: a wavefront per row (D <= 1024), no barriers; 2 or 4 rows per wavefront from
      * 1024 / 2048 rows */
     if ((M > 16 || gpu_many_rows(g)) && D <= 1024) {
@@ -305,6 +398,23 @@ int nk_layernorm2(gpu_t *g, const float *X, const float *g1, const float *b1, co
                           sizeof a, (W + 3) / 4, 1, 1, 256, 1, 1);
     }
     return gpu_launch(g, "layernorm", &a, sizeof a, M, 1, 1, NK_LN_THREADS, 1, 1);
+}
+
+int nk_layernorm2_split(gpu_t *g, float *X, const nk_resid_t *pend, const float *g1, const float *b1, const float *g2,
+                        const float *b2, float *Y1, uint16_t *Ys, uint32_t M, uint32_t D, float eps) {
+    if (!M) return 0;
+    if (D > 1024 || D % 4 || !Ys || (uintptr_t)Ys % 8 || (g2 && !Y1))
+        return bad(g, "layernorm_split: D a multiple of 4, at most 1024, a split output (and Y1 when paired)");
+    NkLnArgs a = { X, g1, b1, g2, b2, g2 ? Y1 : NULL, NULL, M, D, eps, 0, Ys, NULL, 0, 0.0f };
+    if (g2) a.Y2 = Y1; /* any non-NULL Y2 selects the pair; its rows go to Ys */
+    if (pend && pend->nparts) {
+        a.P = pend->parts;
+        a.nparts = pend->nparts;
+        a.palpha = pend->alpha;
+    }
+    const uint32_t R = M >= 2048 ? 4 : M >= 1024 ? 2 : 1, W = (M + R - 1) / R;
+    return gpu_launch(g, R == 4 ? "layernorm_rows_r4" : R == 2 ? "layernorm_rows_r2" : "layernorm_rows", &a, sizeof a,
+                      (W + 3) / 4, 1, 1, 256, 1, 1);
 }
 
 int nk_layernorm(gpu_t *g, const float *X, const float *gamma, const float *beta, float *Y, uint32_t M, uint32_t D,
@@ -428,15 +538,32 @@ int nk_attention_rel_chunks(gpu_t *g, const float *kv, uint32_t ld, const int *c
     if (!nchunks) return 0;
     if (dh != 128 || H * dh != D) return bad(g, "attention: head_dim must be 128");
     if ((uintptr_t)kv % 16 || ld % 4 || (uintptr_t)P % 16 || D % 4) return bad(g, "attention: cache must be 16-byte aligned");
-    NkAttnChunkArgs a = { kv, P, bias_u, bias_v, O, chunks, H, dh, D, ld, Lmax, scale };
+    NkAttnChunkArgs a = { kv, P, bias_u, bias_v, O, chunks, H, dh, D, ld, Lmax, scale, NULL };
+    return gpu_launch(g, "attention_rel_chunks", &a, sizeof a, H, nchunks, 1, 256, 1, 1);
+}
+
+int nk_attention_rel_chunks_split(gpu_t *g, const float *kv, uint32_t ld, const int *chunks, uint32_t nchunks,
+                                  const float *P, const float *bias_u, const float *bias_v, uint16_t *Os, uint32_t Lmax,
+                                  uint32_t H, uint32_t dh, uint32_t D, float scale) {
+    if (!nchunks) return 0;
+    if (dh != 128 || H * dh != D) return bad(g, "attention: head_dim must be 128");
+    if ((uintptr_t)kv % 16 || ld % 4 || (uintptr_t)P % 16 || D % 4 || !Os) return bad(g, "attention: cache must be 16-byte aligned");
+    NkAttnChunkArgs a = { kv, P, bias_u, bias_v, NULL, chunks, H, dh, D, ld, Lmax, scale, Os };
     return gpu_launch(g, "attention_rel_chunks", &a, sizeof a, H, nchunks, 1, 256, 1, 1);
 }
 
 int nk_dwconv_ln_silu_rows(gpu_t *g, const float *din_base, const int *rows, uint32_t M, const float *W,
                            const float *gamma, const float *beta, float *Y, uint32_t D, uint32_t taps, float eps) {
+    return nk_dwconv_ln_silu_rows_split(g, din_base, rows, M, W, gamma, beta, Y, NULL, D, taps, eps);
+}
+
+int nk_dwconv_ln_silu_rows_split(gpu_t *g, const float *din_base, const int *rows, uint32_t M, const float *W,
+                                 const float *gamma, const float *beta, float *Y, uint16_t *Ys, uint32_t D, uint32_t taps,
+                                 float eps) {
     if (!M) return 0;
     if (D > NK_ROW_MAX || D % 4 || taps != NK_CONV_TAPS) return bad(g, "dwconv: 9 taps, D a multiple of 4, at most 4096");
-    NkDwArgs a = { din_base, W, gamma, beta, Y, NULL, rows, M, D, taps, eps };
+    if (!Y == !Ys || (uintptr_t)Ys % 8) return bad(g, "dwconv: one output form");
+    NkDwArgs a = { din_base, W, gamma, beta, Y, NULL, rows, M, D, taps, eps, Ys };
     return gpu_launch(g, "dwconv_ln_silu", &a, sizeof a, M, 1, 1, NK_LN_THREADS, 1, 1);
 }
 

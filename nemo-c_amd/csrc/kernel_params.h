@@ -2,9 +2,17 @@
  *
  * Every kernel takes exactly one of these structs by value; the host passes its bytes through
  * hipModuleLaunchKernel's argument buffer, so the struct layout is the kernel ABI.  Pointers are
- * device addresses.  This replaces the Metal parameter blocks of the reference
- * (src/kernel_params.h:22-32) with the same meaning per field, plus the device pointers that
- * Metal bound as separate buffer arguments.
+ * device addresses.  This is a re-design of the reference's Metal parameter blocks
+ * (src/kernel_params.h:22-32), which carried only scalars, with the buffers bound separately at
+ * argument index i (src/gpu.m:98-101).  Here each struct carries the scalars of the reference's
+ * block (same meaning) and the device pointers of its buffers:
+ *   GemmParams   -> NkGemmArgs (+ row map, split-K scratch, LayerNorm prologue, argmax keys)
+ *   LnParams     -> NkLnArgs (both outputs of the paired LayerNorm in one launch)
+ *   AttnParams   -> NkAttnArgs (+ the chunk descriptor or per-row stream table), NkAttnChunksArgs,
+ *                   NkAttnOutArgs (attention fused with the output projection)
+ *   DwParams     -> NkDwArgs;  Conv2dParams / FlatParams -> the subsampling structs below
+ *   GluParams    -> none (GLU is the GEMM epilogue, act 3, as in the reference's GEMMs)
+ *   LstmParams, JointParams, CountParams, FillParams -> the decoder and copy structs below
  */
 #ifndef NEMO_KERNEL_PARAMS_H
 #define NEMO_KERNEL_PARAMS_H
@@ -43,14 +51,15 @@ typedef struct {
     const float *bias;
     float *C;
     const int *crow;
-    float *ws;      /* split-K partials, stored agent-coherent          */
-    u32 *counters;  /* split-K arrival counters, one per output tile; the last arrival resets it */
+    float *ws;      /* split-K partials (few-row kernels: stored agent-coherent; many-row residual
+                     * updates: the deferred partial rows) */
+    u32 *counters;  /* few-row split-K arrival counters, one per output tile; the last arrival resets it */
     u32 M, N, K, lda, ldw, ldc;
     u32 act, accumulate, splits, group_m; /* group_m: row tiles per group of the many-row tile order */
     float alpha;
-    /* many-row accumulating kernels: K is summed in kblocks equal blocks, each block from zero,
-     * the block sums added in order; splits is 1 or kblocks (one block per workgroup) and gives
-     * the same bits either way */
+    /* many-row residual updates: K is summed in kblocks equal blocks, each block from zero, the
+     * block sums added in order; splits is 1 or kblocks (one block per workgroup) and gives the same
+     * bits either way; the sums go to partial rows at ws (NkFoldArgs) */
     u32 kblocks;
     /* LayerNorm prologue on A (weight-streaming GEMV): ln_mode 0 none, 1 LN(g1,b1),
      * 2 LN(LN(g1,b1); g2,b2); ln_out (optional) receives LN(A; g1,b1), rows of lda floats */
@@ -66,6 +75,12 @@ typedef struct {
      * (a row count known on the device only; the grid covers M) */
     const int *mrows;
     u32 mrows_mul, pad2;
+    /* split activations (many-row kernels): a row of K values is stored as K bf16 hi = RNE(a) then
+     * K bf16 lo = RNE(a - hi), lda / ldc in bf16 elements.  A2 set: A is read from A2 (split by its
+     * producer, the same hi / lo the kernel would form itself); C2 set: the outputs are written as
+     * split rows of nout values to C2 instead of f32 to C (no accumulate, no row map). */
+    const u16 *A2;
+    u16 *C2;
 } NkGemmArgs;
 
 typedef struct {
@@ -75,7 +90,26 @@ typedef struct {
     u32 M, D;
     float eps;
     u32 pad;
+    /* set: the LayerNorm that feeds the next GEMM (Y2 when paired, else Y1) is written as split
+     * rows (D bf16 hi, D bf16 lo; row stride 2D) here instead (see NkGemmArgs.A2) */
+    u16 *Ys;
+    /* set: a pending residual update is applied to X first (and X written back):
+     * X[r] = X[r] + palpha * (((0 + P[0][r]) + P[1][r]) + ...), nparts rows of D floats per part
+     * (part stride M * D) */
+    const float *P;
+    u32 nparts;
+    float palpha;
 } NkLnArgs;
+
+/* C[r][n] = C[r][n] + alpha * (((0 + P[0][r][n]) + P[1][r][n]) + ...): a pending residual update
+ * of the many-row GEMM (parts of M rows of N floats, part stride M * N) applied to C. */
+typedef struct {
+    float *C;
+    const float *P;
+    u32 M, N, ldc, nparts;
+    float alpha;
+    u32 pad;
+} NkFoldArgs;
 
 /* Chunk descriptor in device memory, written by the host before each chunk so that a captured
  * graph can replay a chunk at any cache position:
@@ -122,6 +156,7 @@ typedef struct {
     const int *chunks;
     u32 H, dh, D, ld, Lmax;
     float scale;
+    u16 *Os; /* set: O written as split rows (row stride 2D) here instead */
 } NkAttnChunkArgs;
 
 /* Causal depthwise conv + LN + SiLU. din: [(taps-1) + c][D]; W: [D][taps].
@@ -135,6 +170,7 @@ typedef struct {
     const int *rows;
     u32 c, D, taps;
     float eps;
+    u16 *Ys; /* set: Y written as split rows (row stride 2D) here instead */
 } NkDwArgs;
 
 /* Attention fused with its output projection (single stream, window from the descriptor):

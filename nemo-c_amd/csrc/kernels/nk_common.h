@@ -143,6 +143,30 @@ __device__ __forceinline__ void split8(const float (&x)[8], uint4 &hi, uint4 &lo
     lo = make_uint4(l[0], l[1], l[2], l[3]);
 }
 
+/* two f32 -> their bf16 hi (RNE) and lo = RNE(x - hi), each pair packed element 0 in the low half:
+ * the same rounding as split8 */
+__device__ __forceinline__ void split2(float x0, float x1, u32 &hi, u32 &lo) {
+    const floatx2 v = { x0, x1 };
+    hi = __builtin_bit_cast(u32, __builtin_convertvector(v, bf16x2));
+    const floatx2 hv = { __uint_as_float(hi << 16), __uint_as_float(hi & 0xffff0000u) };
+    lo = __builtin_bit_cast(u32, __builtin_convertvector(v - hv, bf16x2));
+}
+
+/* Split-row stores: element i of a row of D values goes to row[i] (hi) and row[D + i] (lo). */
+__device__ __forceinline__ void store_split4(u16 *row, u32 D, u32 i, float4 v) {
+    uint2 h, l;
+    split2(v.x, v.y, h.x, l.x);
+    split2(v.z, v.w, h.y, l.y);
+    *(uint2 *)(row + i) = h;
+    *(uint2 *)(row + D + i) = l;
+}
+__device__ __forceinline__ void store_split1(u16 *row, u32 D, u32 i, float v) {
+    u32 h, l;
+    split2(v, 0.0f, h, l);
+    row[i] = (u16)h;
+    row[D + i] = (u16)l;
+}
+
 __device__ __forceinline__ bf16x8 as_bf16x8(uint4 v) {
     union { uint4 u; bf16x8 b; } c;
     c.u = v;

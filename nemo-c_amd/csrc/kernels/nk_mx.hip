@@ -14,11 +14,16 @@
  * that granule g of row r holds K-granule (g ^ swizzle(r)), which makes the 16-row fragment reads
  * (ds_read_b128) hit distinct banks (swz_a / swz_b below).
  *
- * A is f32 in memory and in LDS; each fragment (8 consecutive K of one row per lane) is split in
- * registers into bf16 hi = RNE(a) and lo = RNE(a - hi) (v_cvt_pk_bf16_f32), and every K step
- * issues the hi and the lo product: 16 significant bits of A against exact bf16 weights, f32
- * accumulation.  The reference's many-row path multiplies f32 A by bf16 W in f32
- * (src/kernels.metal:120-208, simdgroup_float8x8).
+ * A enters the MFMAs as bf16 hi = RNE(a) and lo = RNE(a - hi), and every K step issues the hi and
+ * the lo product: 16 significant bits of A against exact bf16 weights, f32 accumulation.  The
+ * reference's many-row path multiplies f32 A by bf16 W in f32 (src/kernels.metal:120-208,
+ * simdgroup_float8x8).  Two A forms:
+ *   - f32 rows (AS = false): each fragment (8 consecutive K of one row per lane) is split in
+ *     registers (v_cvt_pk_bf16_f32) after its LDS read;
+ *   - split rows (AS = true, NkGemmArgs.A2): the producer stored hi and lo (the same values), so
+ *     both planes stream into LDS like the weights and the fragments feed the MFMAs directly, with
+ *     no VALU work in the K loop.
+ * A kernel that produces the next GEMM's A can write split rows itself (OS, NkGemmArgs.C2).
  *
  * Tile order: the grid is 8 x (tiles per XCD); workgroup b runs on XCD b % 8 and takes tile
  * (b % 8) * per + b / 8 of an order that walks groups of group_m row tiles across all column tiles
@@ -27,11 +32,12 @@
  *
  * Accumulating GEMMs without bias or activation (the residual updates: C += alpha * A W^T) run on
  * the _acc kernels.  They sum K in kblocks equal blocks, each from zero, and add the block sums in
- * block order; with splits = kblocks every workgroup computes one block, stores it agent-coherent
- * and the last workgroup of the tile to arrive adds them in the same order (nk_common.h).  The two
- * forms give the same bits, so the host may split K or not by the row count (how many other
+ * block order; with splits = kblocks every workgroup computes one block.  Either way the kernel
+ * only writes partial rows (one per split), and the update C + alpha * (((0 + p0) + p1) + ...) is
+ * applied by the next kernel that reads C (the batched encoder's LayerNorms) or by resid_fold.
+ * Both forms give the same bits, so the host may split K or not by the row count (how many other
  * streams share the step) without changing any row's result, and no result depends on which
- * workgroup finishes first. */
+ * workgroup finishes first; no workgroup waits for or communicates with another. */
 #include "nk_common.h"
 
 /* LDS granule swizzles: granule g of row r lives in slot g ^ swz(r).  A fragment read is one
@@ -45,10 +51,11 @@ __device__ __forceinline__ u32 swz_a(u32 r) { return (r & 7) ^ ((r >> 3) & 1); }
 __device__ __forceinline__ u32 swz_b(u32 n) { return (n >> 1) & 3; }
 
 /* EPI: 0 bias / activation / GLU / accumulate epilogue; 1 argmax keys; 2 blocked-K residual
- * update with the ordered split combine (flag: LDS word for the arrival result) */
-template <int BM, int BN, int WGM, int NS, bool GLU, int EPI = 0>
-__device__ __forceinline__ void mx_impl(const NkGemmArgs &a, lds_char_t *const (&ring)[NS], u32 *flag) {
+ * update into partial rows.  AS: A as split rows; OS: outputs as split rows (EPI 0 without GLU). */
+template <int BM, int BN, int WGM, int NS, bool GLU, int EPI = 0, bool AS = false, bool OS = false>
+__device__ __forceinline__ void mx_impl(const NkGemmArgs &a, lds_char_t *const (&ring)[NS]) {
     constexpr int KS = 32;
+    static_assert(!OS || (EPI == 0 && !GLU), "split outputs from the plain epilogue only");
     constexpr int WGN = 4 / WGM;
     constexpr int WTM = BM / WGM, WTN = BN / WGN;
     constexpr int TI = WTM / 16, TJ = WTN / 16;
@@ -81,13 +88,21 @@ __device__ __forceinline__ void mx_impl(const NkGemmArgs &a, lds_char_t *const (
     const u32 spb = EPI == 2 ? S / a.kblocks : nst;
 
     /* DMA sources: granule p of a stage region is written by lane p % 64 of instruction p / 64
-     * (instruction j of wavefront w covers p in [(4j + w) * 64, +64)) */
-    const float *asrc[AI];
+     * (instruction j of wavefront w covers p in [(4j + w) * 64, +64)).  Split A: the stage's A region
+     * is the hi plane (BM rows of BG granules, laid out like the weights) then the lo plane. */
+    const char *asrc[AI];
 #pragma unroll
     for (int j = 0; j < AI; ++j) {
-        const u32 p = (4 * j + wave) * 64 + lane, r = p / AG, kg = (p % AG) ^ swz_a(r);
-        asrc[j] = a.A + (u64)min(m0 + r, M - 1) * a.lda + 4 * kg + (u64)s_begin * KS;
+        const u32 p = (4 * j + wave) * 64 + lane;
+        if constexpr (AS) {
+            const u32 plane = p / (BM * BG), q = p % (BM * BG), r = q / BG, kg = (q % BG) ^ swz_b(r);
+            asrc[j] = (const char *)(a.A2 + (u64)min(m0 + r, M - 1) * a.lda + plane * a.K + 8 * kg + (u64)s_begin * KS);
+        } else {
+            const u32 r = p / AG, kg = (p % AG) ^ swz_a(r);
+            asrc[j] = (const char *)(a.A + (u64)min(m0 + r, M - 1) * a.lda + 4 * kg + (u64)s_begin * KS);
+        }
     }
+    constexpr u32 A_STEP = AS ? KS * 2 : KS * 4; /* bytes of one K step of one A row (per plane) */
     const u16 *bsrc[BI];
 #pragma unroll
     for (int j = 0; j < BI; ++j) {
@@ -100,19 +115,24 @@ __device__ __forceinline__ void mx_impl(const NkGemmArgs &a, lds_char_t *const (
     auto issue = [&](u32 q, int slot) { /* loads of local step q into ring slot `slot` */
         lds_char_t *st = ring[slot];
 #pragma unroll
-        for (int j = 0; j < AI; ++j) dma16(asrc[j] + (u64)q * KS, st + (4 * j + wave) * 1024);
+        for (int j = 0; j < AI; ++j) dma16(asrc[j] + (u64)q * A_STEP, st + (4 * j + wave) * 1024);
 #pragma unroll
         for (int j = 0; j < BI; ++j) dma16(bsrc[j] + (u64)q * KS, st + A_BYTES + (4 * j + wave) * 1024);
     };
 
     /* fragment addresses inside a stage */
     const u32 fr = lane & 15, fg = lane >> 4;
-    u32 aoff[TI][2];
+    u32 aoff[TI][2]; /* f32 A: the two halves of the 8 K; split A: the hi and the lo fragment */
 #pragma unroll
     for (int i = 0; i < TI; ++i) {
         const u32 r = wm * WTM + 16 * i + fr;
-        aoff[i][0] = (r * AG + ((2 * fg) ^ swz_a(r))) * 16;
-        aoff[i][1] = (r * AG + ((2 * fg + 1) ^ swz_a(r))) * 16;
+        if constexpr (AS) {
+            aoff[i][0] = (r * BG + (fg ^ swz_b(r))) * 16;
+            aoff[i][1] = aoff[i][0] + BM * BG * 16;
+        } else {
+            aoff[i][0] = (r * AG + ((2 * fg) ^ swz_a(r))) * 16;
+            aoff[i][1] = (r * AG + ((2 * fg + 1) ^ swz_a(r))) * 16;
+        }
     }
     u32 boff[TJ];
 #pragma unroll
@@ -159,10 +179,15 @@ __device__ __forceinline__ void mx_impl(const NkGemmArgs &a, lds_char_t *const (
         uint4 fh[TI], fl[TI];
 #pragma unroll
         for (int i = 0; i < TI; ++i) {
-            const floatx4 x0 = *(const __attribute__((address_space(3))) floatx4 *)(st + aoff[i][0]);
-            const floatx4 x1 = *(const __attribute__((address_space(3))) floatx4 *)(st + aoff[i][1]);
-            const float x[8] = { x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3] };
-            split8(x, fh[i], fl[i]);
+            if constexpr (AS) {
+                fh[i] = *(const __attribute__((address_space(3))) uint4 *)(st + aoff[i][0]);
+                fl[i] = *(const __attribute__((address_space(3))) uint4 *)(st + aoff[i][1]);
+            } else {
+                const floatx4 x0 = *(const __attribute__((address_space(3))) floatx4 *)(st + aoff[i][0]);
+                const floatx4 x1 = *(const __attribute__((address_space(3))) floatx4 *)(st + aoff[i][1]);
+                const float x[8] = { x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3] };
+                split8(x, fh[i], fl[i]);
+            }
         }
 #pragma unroll
         for (int i = 0; i < TI; ++i)
@@ -189,60 +214,19 @@ __device__ __forceinline__ void mx_impl(const NkGemmArgs &a, lds_char_t *const (
     wait_vm_lgkm<0>(); /* no load into LDS may land after the workgroup ends */
 
     if constexpr (EPI == 2) {
-        /* C[crow(m)][n] += alpha * sum; with K split, block kz's sum goes to the workspace and the
-         * tile's last workgroup adds all blocks in order */
-        constexpr int NV = TI * TJ * 4;
-        const u32 tid256 = threadIdx.x;
-        if (KZ > 1) {
-            float *wsb = a.ws + (u64)tt * KZ * NV * 256;
-#pragma unroll
-            for (int i = 0; i < TI; ++i)
-#pragma unroll
-                for (int j = 0; j < TJ; ++j)
-#pragma unroll
-                    for (int e = 0; e < 4; ++e)
-                        st_agent(wsb + ((u64)kz * NV + (i * TJ + j) * 4 + e) * 256 + tid256, tot[i][j][e]);
-            wait_stores();
-            __syncthreads();
-            if (tid256 == 0) *flag = arrive_last(a.counters + tt, KZ) ? 1u : 0u;
-            __syncthreads();
-            if (!*flag) return;
-#pragma unroll
-            for (int i = 0; i < TI; ++i)
-#pragma unroll
-                for (int j = 0; j < TJ; ++j)
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        float t = 0.0f;
-                        for (u32 b = 0; b < KZ; ++b)
-                            t += b == kz ? tot[i][j][e] : ld_agent(wsb + ((u64)b * NV + (i * TJ + j) * 4 + e) * 256 + tid256);
-                        tot[i][j][e] = t;
-                    }
-        }
-        u32 orow[TI][4];
-#pragma unroll
-        for (int i = 0; i < TI; ++i)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const u32 r = min(m0 + wm * WTM + 16 * i + 4 * fg + e, M - 1);
-                orow[i][e] = a.crow ? (u32)a.crow[r] : r;
-            }
-        float cv[TJ][TI][4];
-#pragma unroll
-        for (int j = 0; j < TJ; ++j)
-#pragma unroll
-            for (int i = 0; i < TI; ++i)
-#pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    cv[j][i][e] = a.C[(u64)orow[i][e] * a.ldc + c0 + wn * WTN + 16 * j + fr];
+        /* residual update, deferred: block kz's sum (all blocks' ordered sum when K is not split)
+         * goes to partials[kz][row][n] (rows of N floats); C is not touched.  The rows are folded
+         * into C in block order afterwards, by the LayerNorm that reads them next or by
+         * resid_fold: C + alpha * (((0 + p0) + p1) + ...), the unsplit epilogue's bits. */
+        float *P = a.ws + (u64)kz * a.M * a.N;
 #pragma unroll
         for (int j = 0; j < TJ; ++j)
 #pragma unroll
             for (int i = 0; i < TI; ++i)
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    if (m0 + wm * WTM + 16 * i + 4 * fg + e >= M) continue;
-                    a.C[(u64)orow[i][e] * a.ldc + c0 + wn * WTN + 16 * j + fr] = cv[j][i][e] + tot[i][j][e] * a.alpha;
+                    const u32 r = m0 + wm * WTM + 16 * i + 4 * fg + e;
+                    if (r < M) P[(u64)r * a.N + c0 + wn * WTN + 16 * j + fr] = tot[i][j][e];
                 }
         return;
     }
@@ -303,6 +287,35 @@ __device__ __forceinline__ void mx_impl(const NkGemmArgs &a, lds_char_t *const (
         ba[j] = a.bias ? a.bias[ocol[j]] : 0.0f;
         bb[j] = (GLU && a.bias) ? a.bias[ocol[j] + a.N / 2] : 0.0f;
     }
+    if constexpr (OS) {
+        /* split rows of nout values: hi at C2[row * ldc + n], lo at + nout */
+#pragma unroll
+        for (int j = 0; j < TO; ++j)
+#pragma unroll
+            for (int i = 0; i < TI; ++i)
+#pragma unroll
+                for (int e = 0; e < 4; e += 2) {
+                    float v[2];
+#pragma unroll
+                    for (int d = 0; d < 2; ++d) {
+                        v[d] = acc[i][j][e + d] + ba[j];
+                        if (a.act == NK_ACT_SILU) v[d] = silu_f(v[d]);
+                        else if (a.act == NK_ACT_RELU) v[d] = fmaxf(v[d], 0.0f);
+                        v[d] *= a.alpha;
+                    }
+                    u32 hi, lo;
+                    split2(v[0], v[1], hi, lo);
+#pragma unroll
+                    for (int d = 0; d < 2; ++d) {
+                        const u32 r = m0 + wm * WTM + 16 * i + 4 * fg + e + d;
+                        if (r >= M) continue;
+                        u16 *dst = a.C2 + (u64)r * a.ldc + ocol[j];
+                        dst[0] = (u16)(hi >> (16 * d));
+                        dst[nout] = (u16)(lo >> (16 * d));
+                    }
+                }
+        return;
+    }
     const bool rmw = a.accumulate;
     float cv[TO][TI][4];
 #pragma unroll
@@ -337,14 +350,14 @@ __device__ __forceinline__ void mx_impl(const NkGemmArgs &a, lds_char_t *const (
  * a CU's 160 KB of LDS (measured: the second workgroup overlaps one's loads and barriers with the
  * other's MFMAs; 3584 rows, 128x128: 117 -> 79 us with the swizzles): 3 x 24 KB for 128x128,
  * 4 x 16 KB for 64x128, 4 x 12 KB for 64x64 */
-#define GEMM_MX(NAME, BM, BN, WGM, NS, GLU, EPI)                                                          \
+#define GEMM_MX_T(NAME, BM, BN, WGM, NS, GLU, EPI, AS, OS)                                              \
     extern "C" __global__ __launch_bounds__(256) void NAME(const NkGemmArgs a) {                          \
         __shared__ uint4 ring_mem[NS][(BM * 4 + BN * 2) * 32 / 16];                                      \
-        __shared__ u32 flag;                                                                              \
         lds_char_t *ring[NS];                                                                             \
         _Pragma("unroll") for (int i = 0; i < NS; ++i) ring[i] = (lds_char_t *)ring_mem[i];               \
-        mx_impl<BM, BN, WGM, NS, GLU, EPI>(a, ring, &flag);                                               \
+        mx_impl<BM, BN, WGM, NS, GLU, EPI, AS, OS>(a, ring);                                              \
     }
+#define GEMM_MX(NAME, BM, BN, WGM, NS, GLU, EPI) GEMM_MX_T(NAME, BM, BN, WGM, NS, GLU, EPI, false, false)
 GEMM_MX(gemm_mx128x128, 128, 128, 2, 3, false, 0)
 GEMM_MX(gemm_mx64x128, 64, 128, 2, 4, false, 0)
 GEMM_MX(gemm_mx64x64, 64, 64, 2, 4, false, 0)
@@ -357,3 +370,19 @@ GEMM_MX(gemm_mx64x128_acc, 64, 128, 2, 4, false, 2)
 GEMM_MX(gemm_mx64x64_acc, 64, 64, 2, 4, false, 2)
 /* joint scores -> argmax partials (keys), 64x64 tiles: two keys per row per column tile */
 GEMM_MX(gemm_mx64x64_argmax, 64, 64, 2, 4, false, 1)
+/* split-row A (suffix _s), split-row outputs (suffix _so) */
+GEMM_MX_T(gemm_mx128x128_s, 128, 128, 2, 3, false, 0, true, false)
+GEMM_MX_T(gemm_mx64x128_s, 64, 128, 2, 4, false, 0, true, false)
+GEMM_MX_T(gemm_mx64x64_s, 64, 64, 2, 4, false, 0, true, false)
+GEMM_MX_T(gemm_mx128x128_glu_s, 128, 128, 2, 3, true, 0, true, false)
+GEMM_MX_T(gemm_mx64x128_glu_s, 64, 128, 2, 4, true, 0, true, false)
+GEMM_MX_T(gemm_mx64x64_glu_s, 64, 64, 2, 4, true, 0, true, false)
+GEMM_MX_T(gemm_mx128x128_acc_s, 128, 128, 2, 3, false, 2, true, false)
+GEMM_MX_T(gemm_mx64x128_acc_s, 64, 128, 2, 4, false, 2, true, false)
+GEMM_MX_T(gemm_mx64x64_acc_s, 64, 64, 2, 4, false, 2, true, false)
+GEMM_MX_T(gemm_mx128x128_so, 128, 128, 2, 3, false, 0, false, true)
+GEMM_MX_T(gemm_mx64x128_so, 64, 128, 2, 4, false, 0, false, true)
+GEMM_MX_T(gemm_mx64x64_so, 64, 64, 2, 4, false, 0, false, true)
+GEMM_MX_T(gemm_mx128x128_s_so, 128, 128, 2, 3, false, 0, true, true)
+GEMM_MX_T(gemm_mx64x128_s_so, 64, 128, 2, 4, false, 0, true, true)
+GEMM_MX_T(gemm_mx64x64_s_so, 64, 64, 2, 4, false, 0, true, true)

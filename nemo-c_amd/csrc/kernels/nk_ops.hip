@@ -206,6 +206,23 @@ extern "C" __global__ __launch_bounds__(256) void copy_f32(const NkCopyArgs a) {
     if (i < a.n) a.dst[i] = a.src[i];
 }
 
+/* Pending residual update of the many-row GEMM (NkFoldArgs): one thread per 4 consecutive values
+ * of a row, the parts added in order from zero, then C + alpha * sum. */
+extern "C" __global__ __launch_bounds__(256) void resid_fold(const NkFoldArgs a) {
+    const u32 n4 = a.N >> 2, i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= a.M * n4) return;
+    const u32 r = i / n4, c = 4 * (i % n4);
+    float4 t = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (u32 b = 0; b < a.nparts; ++b) {
+        const float4 q = *(const float4 *)(a.P + ((u64)b * a.M + r) * a.N + c);
+        t.x += q.x; t.y += q.y; t.z += q.z; t.w += q.w;
+    }
+    float4 *dst = (float4 *)(a.C + (u64)r * a.ldc + c);
+    float4 v = *dst;
+    v.x = v.x + t.x * a.alpha; v.y = v.y + t.y * a.alpha; v.z = v.z + t.z * a.alpha; v.w = v.w + t.w * a.alpha;
+    *dst = v;
+}
+
 extern "C" __global__ __launch_bounds__(256) void fill_f32(const NkFillArgs a) {
     const u32 i = blockIdx.x * 256 + threadIdx.x;
     if (i < a.n) a.dst[i] = a.value;

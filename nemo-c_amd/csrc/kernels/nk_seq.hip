@@ -117,6 +117,37 @@ __device__ __forceinline__ void layernorm_rows_impl(const NkLnArgs &a) {
 #pragma unroll
         for (int k = 0; k < 4; ++k) v[r][k] = lane + 64 * k < D4 ? x[lane + 64 * k] : z;
     }
+    if (a.P) {
+        /* pending residual update: x + palpha * (((0 + p0) + p1) + ...), written back to X (this
+         * wavefront owns its rows) */
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const u32 row = min(r0 + r, a.M - 1);
+            float4 t[4] = { z, z, z, z };
+            for (u32 b = 0; b < a.nparts; ++b) {
+                const float4 *p = (const float4 *)(a.P + ((u64)b * a.M + row) * a.D);
+#pragma unroll
+                for (int k = 0; k < 4; ++k)
+                    if (lane + 64 * k < D4) {
+                        const float4 q = p[lane + 64 * k];
+                        t[k].x += q.x; t[k].y += q.y; t[k].z += q.z; t[k].w += q.w;
+                    }
+            }
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                v[r][k].x = v[r][k].x + t[k].x * a.palpha;
+                v[r][k].y = v[r][k].y + t[k].y * a.palpha;
+                v[r][k].z = v[r][k].z + t[k].z * a.palpha;
+                v[r][k].w = v[r][k].w + t[k].w * a.palpha;
+            }
+            if (r0 + r < a.M) {
+                float4 *x = (float4 *)(a.X + (u64)row * a.D);
+#pragma unroll
+                for (int k = 0; k < 4; ++k)
+                    if (lane + 64 * k < D4) x[lane + 64 * k] = v[r][k];
+            }
+        }
+    }
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
         const u32 i = lane + 64 * k;
@@ -131,12 +162,25 @@ __device__ __forceinline__ void layernorm_rows_impl(const NkLnArgs &a) {
         const u32 row = r0 + r;
         if (row >= a.M) break;
         ln_row64(v[r], g1, b1, lane, D4, a.D, a.eps);
+        u16 *ys = a.Ys ? a.Ys + (u64)row * 2 * a.D : nullptr;
+        if (!a.Y2 && ys) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                if (lane + 64 * k < D4) store_split4(ys, a.D, 4 * (lane + 64 * k), v[r][k]);
+            continue;
+        }
         float4 *y1 = (float4 *)(a.Y1 + (u64)row * a.D);
 #pragma unroll
         for (int k = 0; k < 4; ++k)
             if (lane + 64 * k < D4) y1[lane + 64 * k] = v[r][k];
         if (!a.Y2) continue;
         ln_row64(v[r], g2, b2, lane, D4, a.D, a.eps);
+        if (ys) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                if (lane + 64 * k < D4) store_split4(ys, a.D, 4 * (lane + 64 * k), v[r][k]);
+            continue;
+        }
         float4 *y2 = (float4 *)(a.Y2 + (u64)row * a.D);
 #pragma unroll
         for (int k = 0; k < 4; ++k)
@@ -381,7 +425,10 @@ extern "C" __global__ __launch_bounds__(256) void attention_rel_chunks(const NkA
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const u32 i = 4 * kq + r;
-            if (i < c) a.O[(u64)(m0 + i) * a.D + off + d] = acc[r];
+            if (i < c) {
+                if (a.Os) store_split1(a.Os + (u64)(m0 + i) * 2 * a.D, a.D, off + d, acc[r]);
+                else a.O[(u64)(m0 + i) * a.D + off + d] = acc[r];
+            }
         }
     }
 }
@@ -426,6 +473,9 @@ extern "C" __global__ __launch_bounds__(256) void dwconv_ln_silu(const NkDwArgs 
     float4 *y = (float4 *)(a.Y + (u64)t * a.D);
 #pragma unroll
     for (int k = 0; k < LN_VEC; ++k)
-        if (tid + k * 256 < D4)
-            y[tid + k * 256] = make_float4(silu_f(v[k].x), silu_f(v[k].y), silu_f(v[k].z), silu_f(v[k].w));
+        if (tid + k * 256 < D4) {
+            const float4 o = make_float4(silu_f(v[k].x), silu_f(v[k].y), silu_f(v[k].z), silu_f(v[k].w));
+            if (a.Ys) store_split4(a.Ys + (u64)t * 2 * a.D, a.D, 4 * (tid + k * 256), o);
+            else y[tid + k * 256] = o;
+        }
 }

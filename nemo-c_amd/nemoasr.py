@@ -104,7 +104,16 @@ API = {
     "nk_gemm_ln": (C.c_int, [_vp, _vp, _u32, _vp, _u32, _vp, _vp, _u32, _vp, _u32, _u32, _u32, C.c_int, C.c_int,
                              C.c_float, C.c_int, _vp, _vp, _vp, _vp, _vp, _vp, C.c_float]),
     "nk_gemm_force": (C.c_int, [C.c_int]),
-    "nk_gemm_split": (C.c_int, [C.c_int]),
+    "nk_gemm_ksplit": (C.c_int, [C.c_int]),
+    "nk_gemm_fr_ksplit": (C.c_int, [C.c_int]),
+    "nk_gemm_split": (C.c_int, [_vp, _vp, _vp, _u32, _vp, _u32, _vp, _vp, _vp, _u32, _vp, _u32, _u32, _u32, C.c_int,
+                                C.c_int, C.c_float]),
+    "nk_layernorm2_split": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32, C.c_float]),
+    "nk_gemm_resid": (C.c_int, [_vp, _vp, _vp, _u32, _vp, _u32, _vp, _u32, _u32, _u32, _u32, C.c_float, _vp]),
+    "nk_resid_fold": (C.c_int, [_vp, _vp, _u32, _u32, _u32, _vp]),
+    "nk_attention_rel_chunks_split": (C.c_int, [_vp, _vp, _u32, _vp, _u32, _vp, _vp, _vp, _vp, _u32, _u32, _u32,
+                                                _u32, C.c_float]),
+    "nk_dwconv_ln_silu_rows_split": (C.c_int, [_vp, _vp, _vp, _u32, _vp, _vp, _vp, _vp, _vp, _u32, _u32, C.c_float]),
     "nk_gemm_argmax": (C.c_int, [_vp, _vp, _u32, _vp, _u32, _vp, _vp, _u32, _u32, _u32, _u32, _u32]),
     "nk_gemm_argmax_rows": (C.c_int, [_vp, _vp, _u32, _vp, _u32, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _vp, _u32]),
     "nk_gemm_kernel_name": (C.c_char_p, [_u32, _u32, _u32, C.c_int]),
@@ -178,6 +187,11 @@ def lib() -> C.CDLL:
 
 def fp(a: np.ndarray):
     return a.ctypes.data_as(_f32p)
+
+
+class Resid(C.Structure):
+    """nk_resid_t: a pending residual update (partial rows in the context's scratch)."""
+    _fields_ = [("parts", C.c_void_p), ("nparts", C.c_uint32), ("alpha", C.c_float)]
 
 
 class Gpu:

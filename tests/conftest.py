@@ -21,7 +21,7 @@ def pytest_configure(config):
 # single stream end to end, then the multi-stream batch (built from the same kernels), then the
 # allocation-free entry point; so that under -x a failure in a later layer cannot hide the
 # foundational results.  Files not listed keep their place ahead of these.
-_FILE_ORDER = {"test_golden.py": 0, "test_gpu_kernels.py": 1, "test_gpu_stream.py": 2, "test_gpu_determinism.py": 3,
+_FILE_ORDER = {"test_golden.py": 0, "test_gpu_kernels.py": 1, "test_gpu_split.py": 1, "test_gpu_stream.py": 2, "test_gpu_determinism.py": 3,
                "test_gpu_batch.py": 4, "test_zz_no_alloc.py": 5}
 
 
@@ -54,13 +54,19 @@ def check_tokens(got, ref, margins, what=""):
     return k
 
 
-def model_dir(kind: str, seed: int = 0, blank_bias: float = 0.0) -> str:
+def model_dir(kind: str, seed: int = 0, blank_bias: float = 0.0, label_shift: float = 0.0) -> str:
     import synth
 
     dims = synth.TINY_DIMS if kind == "tiny" else synth.FULL_DIMS
-    d = os.path.join(MODEL_CACHE, f"{kind}_s{seed}_b{blank_bias:g}")
-    synth.write_model(d, dims, seed, blank_bias)
+    d = os.path.join(MODEL_CACHE, f"{kind}_s{seed}_b{blank_bias:g}" + (f"_l{label_shift:g}" if label_shift else ""))
+    synth.write_model(d, dims, seed, blank_bias, label_shift)
     return d
+
+
+# joint-bias skews of the skewed benchmark workloads (bench.py): one stream at 1120 ms with
+# P(blank) ~ 0.5, and 256 streams with the auto prompt at P(blank) ~ 0.7
+SKEW_S1120 = (2.0, 0.0188)
+SKEW_B256 = (2.0, 0.0619)
 
 
 @pytest.fixture(scope="session")

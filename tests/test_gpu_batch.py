@@ -293,3 +293,22 @@ def test_batch_auto_prompt_full(latency):
     drive(b, mels, [0, 2, 1], piece=8 * (LAT_RIGHT[latency] + 1))
     check_streams(b, om, latency, mels, om.dims.joint_hidden, tag=("auto", latency))
     b.close()
+
+
+def test_batch_skewed_auto_full():
+    """The full model skewed as in the 256-stream benchmark workload (auto prompt, P(blank) ~ 0.7),
+    five staggered streams at 1120 ms through the device-resident batched loop, against the oracle."""
+    import nemoasr
+    from conftest import SKEW_B256
+
+    mdir = model_dir("full", 0, *SKEW_B256)
+    om = oracle.Model(mdir, "auto")
+    secs = [3.0, 2.2, 3.4, 1.5, 2.8]
+    mels = [mel_ref.logmel(synth.make_audio(t, seed=1000 + i)) for i, t in enumerate(secs)]
+    b = nemoasr.Batch(mdir, "auto", 1120, streams=len(mels))
+    b.set_dump(True)
+    drive(b, mels, [0, 1, 2, 0, 3], piece=8 * 14)
+    check_streams(b, om, 1120, mels, om.dims.joint_hidden, tag=("skew256",))
+    st = b.stats()
+    assert 0 < st["tokens"] < st["rows"] * om.dims.max_symbols, st
+    b.close()

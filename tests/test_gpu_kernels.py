@@ -116,7 +116,7 @@ def test_gemm_many_rows(gpu, M, N, K, act):
 def test_gemm_batched_rows(gpu, M, N, K, act, acc, bias, split):
     import nemoasr
 
-    prev = nemoasr.lib().nk_gemm_split(split)
+    prev = nemoasr.lib().nk_gemm_ksplit(split)
     rng = np.random.default_rng([M, N, K, act])
     W = _w(rng, N, K)
     A = rng.standard_normal((M, K)).astype(np.float32)
@@ -126,7 +126,7 @@ def test_gemm_batched_rows(gpu, M, N, K, act, acc, bias, split):
     try:
         got = run_gemm(gpu, A, W, b, act, acc, 0.5 if acc else 1.0, C0=C0)
     finally:
-        nemoasr.lib().nk_gemm_split(prev)
+        nemoasr.lib().nk_gemm_ksplit(prev)
     ref = oracle.gemm(A, W, b, act, acc, 0.5 if acc else 1.0, C0=C0)
     assert rel_err(got, ref) < GEMM_TOL, (M, N, K, act)
 
@@ -148,10 +148,10 @@ def test_gemm_residual_bits(gpu, N, K):
     try:
         for M in (3584, 448, 64, 17):
             for split in (0, 1, -1, -1):
-                L.nk_gemm_split(split)
+                L.nk_gemm_ksplit(split)
                 outs.setdefault(M, []).append(run_gemm(gpu, A[:M], W, None, 0, True, 0.5, C0=C0[:M].copy()))
     finally:
-        L.nk_gemm_split(-1)
+        L.nk_gemm_ksplit(-1)
     for M, runs in outs.items():
         for r in runs[1:]:
             assert np.array_equal(r.view(np.uint32), runs[0].view(np.uint32)), M

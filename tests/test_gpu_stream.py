@@ -243,3 +243,19 @@ def test_stream_cache_compaction_graphs(latency, seconds):
     om, o, s, d = run_pair(mdir, latency, seconds, seed=17, graphs=True)
     check_parity(om, o, s, d, check_dumps=False)
     s.close()
+
+
+@pytest.mark.parametrize("graphs", [False, True])
+def test_full_skewed_stream_1120(graphs):
+    """The full model with the joint bias skewed as in the 1120 ms benchmark workload
+    (P(blank) ~ 0.5 over the benchmark's 30 s clip), on a 4 s clip whose frames mix blank frames,
+    emits and redone frames (the oracle: 170 tokens over 51 frames; with random weights a stretch
+    of audio tends to decode either to blanks only or to max_symbols per frame), against the oracle."""
+    from conftest import SKEW_S1120
+
+    mdir = model_dir("full", 0, *SKEW_S1120)
+    om, o, s, d = run_pair(mdir, 1120, 4.0, seed=6, graphs=graphs)
+    check_parity(om, o, s, d, check_dumps=not graphs)
+    frames, toks = o.frames, len(o.tokens)
+    assert 0 < toks < frames * om.dims.max_symbols, (frames, toks)
+    s.close()
