@@ -74,14 +74,11 @@ int gpu_graph_launch(gpu_t *g, gpu_graph_t *gr);
 void gpu_graph_free(gpu_graph_t *gr);
 int gpu_capturing(const gpu_t *g);
 
-/* Scratch of the ordered split-K combines: partial sums and arrival counters (zero between launches:
- * every launch's last arrivals reset theirs).  GPU_SCRATCH_FLOATS / GPU_SCRATCH_COUNTERS are
- * allocated at creation; larger requests grow the scratch outside a capture and return NULL (no
- * error recorded) inside one.  Launches on one gpu_t run in stream order, so they may share it. */
+/* Scratch of the split-K partial rows (GPU_SCRATCH_FLOATS allocated at creation): a larger request
+ * grows it outside a capture and returns NULL (no error recorded) inside one.  Launches on one
+ * gpu_t run in stream order, so they share it; it holds one pending residual update at a time. */
 #define GPU_SCRATCH_FLOATS (1u << 20)
-#define GPU_SCRATCH_COUNTERS 4096u
 float *gpu_scratch_ws(gpu_t *g, size_t floats_needed);
-uint32_t *gpu_scratch_counters(gpu_t *g, size_t n_needed);
 
 /* Per-kernel timing on the launch stream: when a name is set, every launch of that kernel is
  * bracketed by a pair of hipEvents; gpu_timing_collect returns the mean duration in ms. */

@@ -35,8 +35,6 @@ struct gpu {
     int nfn;
     float *ws;
     size_t ws_floats;
-    uint32_t *counters;
-    size_t ncounters;
     uint64_t launches;
     /* constant tables for kernels that take no optional pointers: rows 0..GPU_IOTA_N-1 and zeros */
     int *iota;
@@ -105,9 +103,7 @@ gpu_t *gpu_create(char *err, size_t errlen) {
         (e = hipMemcpy(g->iota, iota, GPU_IOTA_N * sizeof(int), hipMemcpyHostToDevice)) != hipSuccess ||
         (e = hipMalloc((void **)&g->zeros, GPU_ZEROS_N * sizeof(float))) != hipSuccess ||
         (e = hipMemset(g->zeros, 0, GPU_ZEROS_N * sizeof(float))) != hipSuccess ||
-        (e = hipMalloc((void **)&g->ws, GPU_SCRATCH_FLOATS * sizeof(float))) != hipSuccess ||
-        (e = hipMalloc((void **)&g->counters, GPU_SCRATCH_COUNTERS * sizeof(uint32_t))) != hipSuccess ||
-        (e = hipMemset(g->counters, 0, GPU_SCRATCH_COUNTERS * sizeof(uint32_t))) != hipSuccess) {
+        (e = hipMalloc((void **)&g->ws, GPU_SCRATCH_FLOATS * sizeof(float))) != hipSuccess) {
         snprintf(err, errlen, "constant tables: %s", hipGetErrorString(e));
         free(iota);
         gpu_destroy(g);
@@ -115,7 +111,6 @@ gpu_t *gpu_create(char *err, size_t errlen) {
     }
     free(iota);
     g->ws_floats = GPU_SCRATCH_FLOATS;
-    g->ncounters = GPU_SCRATCH_COUNTERS;
     return g;
 }
 
@@ -134,7 +129,6 @@ void gpu_destroy(gpu_t *g) {
         free(g->tbytes);
     }
     if (g->ws) hipFree(g->ws);
-    if (g->counters) hipFree(g->counters);
     if (g->iota) hipFree(g->iota);
     if (g->zeros) hipFree(g->zeros);
     hipEventDestroy(g->ev0);
@@ -444,20 +438,6 @@ float *gpu_scratch_ws(gpu_t *g, size_t floats) {
         g->ws_floats = floats;
     }
     return g->ws;
-}
-
-uint32_t *gpu_scratch_counters(gpu_t *g, size_t n) {
-    if (n > g->ncounters) {
-        if (g->capturing) return NULL;
-        hipStreamSynchronize(g->stream);
-        uint32_t *p = NULL;
-        if (hipMalloc((void **)&p, n * sizeof(uint32_t)) != hipSuccess) return NULL;
-        if (hipMemset(p, 0, n * sizeof(uint32_t)) != hipSuccess) { hipFree(p); return NULL; }
-        if (g->counters) hipFree(g->counters);
-        g->counters = p;
-        g->ncounters = n;
-    }
-    return g->counters;
 }
 
 int gpu_timing_set(gpu_t *g, const char *kernel, int max_launches) {

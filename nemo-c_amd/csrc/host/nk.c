@@ -334,15 +334,18 @@ static int gemm_core(gpu_t *g, const float *A, uint32_t lda, const uint16_t *W, 
     if (kind == K_FR) {
         /* the few-row kernel reads bias and the row map unconditionally */
         if (N > GPU_ZEROS_N) return bad(g, "gemm: N too large for the few-row kernel");
-        const fr_plan_t p = fr_plan(nout, K, act, accumulate, bias != NULL, ln_fused);
+        const fr_plan_t p = fr_plan(nout, K, act, accumulate && !crow && nout % 4 == 0 && ldc % 4 == 0 &&
+                                    ((uintptr_t)C & 15) == 0, bias != NULL, ln_fused);
         if (!a.bias) a.bias = gpu_zeros(g);
         if (!a.crow) a.crow = gpu_iota(g);
         const uint32_t tiles = (nout + 15) / 16;
         if (p.KS > 1) {
-            /* partial tiles of 16 x 16 floats per K share, one arrival counter per column tile */
-            a.ws = gpu_scratch_ws(g, (size_t)tiles * p.KS * 256);
-            a.counters = gpu_scratch_counters(g, tiles);
-            if (!a.ws || !a.counters) return bad(g, "gemm: split-K scratch unavailable");
+            /* the K shares' partial rows, folded into C in share order by a second launch */
+            a.ws = gpu_scratch_ws(g, (size_t)p.KS * M * nout);
+            if (!a.ws) return bad(g, "gemm: split-K scratch unavailable (size it before capture)");
+            if (gpu_launch(g, fr_name(p, act, ln_fused), &a, sizeof a, tiles, p.KS, 1, 64 * p.W, 1, 1)) return -1;
+            const nk_resid_t pend = { a.ws, p.KS, alpha };
+            return nk_resid_fold(g, C, ldc, M, nout, &pend);
         }
         return gpu_launch(g, fr_name(p, act, ln_fused), &a, sizeof a, tiles, p.KS, 1, 64 * p.W, 1, 1);
     }
@@ -485,10 +488,10 @@ int nk_attention_out_desc(gpu_t *g, const float *kv, uint32_t ld, const int *des
     p.at = (NkAttnArgs){ kv, kv + D, kv + 2 * D, P, bias_u, bias_v, NULL, desc, NULL, c, 0, Lmax, H, dh, D, ld, ld, scale, 0 };
     p.Wo = Wo;
     p.C = C;
-    /* per-head partials [c][column tiles][H][columns], one arrival counter per (row, column tile) */
+    /* per-head partial rows [H][c][D], folded into C in head order by a second launch */
     p.ws = gpu_scratch_ws(g, (size_t)c * D * H);
-    p.counters = gpu_scratch_counters(g, (size_t)c * (D / (8u * (uint32_t)g_attn_cpw)));
-    if (!p.ws || !p.counters) return bad(g, "attention_out: scratch unavailable");
+    if (!p.ws) return bad(g, "attention_out: scratch unavailable (size it before capture)");
+    if (ldc % 4 || (uintptr_t)C % 16) return bad(g, "attention_out: C 16-byte aligned, ldc % 4 == 0");
     p.ldw = ldw;
     p.ldc = ldc;
     p.alpha = alpha;
@@ -497,7 +500,9 @@ int nk_attention_out_desc(gpu_t *g, const float *kv, uint32_t ld, const int *des
     const uint32_t cols = 8u * (uint32_t)g_attn_cpw;
     char name[32];
     snprintf(name, sizeof name, "attention_rel_out_c%d", g_attn_cpw);
-    return gpu_launch(g, name, &p, sizeof p, H, D / cols, c, 512, 1, 1);
+    if (gpu_launch(g, name, &p, sizeof p, H, D / cols, c, 512, 1, 1)) return -1;
+    const nk_resid_t pend = { p.ws, H, alpha };
+    return nk_resid_fold(g, C, ldc, c, D, &pend);
 }
 
 int nk_dwconv_pw_desc(gpu_t *g, const float *din_base, const int *desc, const float *dw_w, const float *gamma,

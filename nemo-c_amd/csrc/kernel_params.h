@@ -51,9 +51,7 @@ typedef struct {
     const float *bias;
     float *C;
     const int *crow;
-    float *ws;      /* split-K partials (few-row kernels: stored agent-coherent; many-row residual
-                     * updates: the deferred partial rows) */
-    u32 *counters;  /* few-row split-K arrival counters, one per output tile; the last arrival resets it */
+    float *ws;      /* split-K residual updates: partial rows [split][M][nout], folded by resid_fold */
     u32 M, N, K, lda, ldw, ldc;
     u32 act, accumulate, splits, group_m; /* group_m: row tiles per group of the many-row tile order */
     float alpha;
@@ -179,8 +177,7 @@ typedef struct {
     NkAttnArgs at;
     const u16 *Wo;
     float *C;
-    float *ws;     /* per-head partial products, [row][column tile][head][columns] */
-    u32 *counters; /* one per (row, column tile); the last of the H heads to arrive resets it */
+    float *ws;     /* per-head partial rows [head][row][D], folded into C by resid_fold */
     u32 ldw, ldc;
     float alpha;
     u32 pad;

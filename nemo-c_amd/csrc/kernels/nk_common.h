@@ -210,30 +210,4 @@ template <int N> __device__ __forceinline__ void wait_vm_lgkm() {
 
 __device__ __forceinline__ void barrier_mem() { asm volatile("s_barrier" ::: "memory"); }
 
-/* ---- ordered cross-workgroup combine (split K without float atomics) ----------------------------
- * The workgroups that share one output tile each store their partial with agent-coherent stores
- * (relaxed atomics at agent scope: global_store / global_load with sc1, which write through and
- * read past this XCD's L2, so another XCD sees the values without a writeback or invalidate of
- * the whole cache), wait until those stores have completed, and then count in on the tile's
- * counter.  The workgroup that arrives last reads the other partials and sums all of them in
- * split order, so the result does not depend on which workgroup finishes first; it resets the
- * counter to zero for the next launch.  No workgroup ever waits for another. */
-__device__ __forceinline__ void st_agent(float *p, float v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float ld_agent(const float *p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-/* every store of this wavefront has completed (vmcnt counts stores on gfx9) */
-__device__ __forceinline__ void wait_stores() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
-
-/* Called by one lane after its workgroup's partial stores completed: true in the last of `parts`
- * arrivals at *cnt, which also resets the counter. */
-__device__ __forceinline__ bool arrive_last(u32 *cnt, u32 parts) {
-    const u32 old = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (old != parts - 1) return false;
-    __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    return true;
-}
-
 #endif

@@ -6,10 +6,10 @@
  *   C[row] += alpha * O[row] . Wo^T,  O[row] = [head 0 | ... | head H-1] attention outputs.
  * Workgroup (head h, column tile, row) computes its head's output (the heads' shares of the
  * product are independent: K of the projection is split by head) and multiplies it by its columns'
- * 128-wide slice of Wo.  The H workgroups of one (column tile, row) store their partial sums
- * agent-coherent; the last of them to arrive adds the H partials in head order into C
- * (nk_common.h), so the sum does not depend on which head finishes first.  Its Wo loads are issued
- * with the attention's own loads.  CPW output columns per wavefront, 8 wavefronts.
+ * 128-wide slice of Wo, writing its head's partial row P[h][row][n]; the host folds the H partial
+ * rows into C in head order with one more launch (resid_fold), so the sum does not depend on which
+ * head finishes first.  Its Wo loads are issued with the attention's own loads.  CPW output columns
+ * per wavefront, 8 wavefronts.
  *
  * gemv_dw_r<R>_n<NC>_k<KCH>: the causal depthwise conv + LayerNorm + SiLU of the convolution module
  * (the math of dwconv_ln_silu) as the prologue of the pointwise conv GEMV that consumes it
@@ -23,7 +23,6 @@ template <int CPW>
 __device__ __forceinline__ void attn_out_impl(const NkAttnOutArgs &p) {
     __shared__ AttnShared sh;
     __shared__ float oh[128];
-    __shared__ u32 last;
     constexpr int LPC = 64 / CPW, DPL = 128 / LPC, LD = DPL / 8; /* lanes per column, dims per lane */
     const u32 h = blockIdx.x, orow = blockIdx.z, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const u32 n = blockIdx.y * (8 * CPW) + wave * CPW + lane / LPC, kq = (lane % LPC) * DPL;
@@ -39,19 +38,8 @@ __device__ __forceinline__ void attn_out_impl(const NkAttnOutArgs &p) {
     for (int i = 0; i < LD; ++i) acc = dot8(&oh[kq + 8 * i], w[i], acc);
 #pragma unroll
     for (int m = 1; m < LPC; m <<= 1) acc += __shfl_xor(acc, m, 64);
-    /* partials [row][column tile][head][8 CPW columns]; column n is slot n - tile * 8 CPW */
-    const u32 H = gridDim.x, cols = 8 * CPW, slot = n - blockIdx.y * cols, tile = orow * gridDim.y + blockIdx.y;
-    float *wsb = p.ws + (u64)tile * H * cols;
-    if (lane % LPC == 0) st_agent(wsb + h * cols + slot, acc);
-    wait_stores();
-    __syncthreads();
-    if (tid == 0) last = arrive_last(p.counters + tile, H) ? 1u : 0u;
-    __syncthreads();
-    if (!last || lane % LPC != 0) return;
-    float t = 0.0f;
-    for (u32 hh = 0; hh < H; ++hh) t += hh == h ? acc : ld_agent(wsb + hh * cols + slot);
-    float *dst = p.C + (u64)orow * p.ldc + n;
-    *dst = *dst + p.alpha * t;
+    /* partial rows [head][row][D] */
+    if (lane % LPC == 0) p.ws[((u64)h * gridDim.z + orow) * p.at.D + n] = acc;
 }
 
 extern "C" __global__ __launch_bounds__(512) void attention_rel_out_c16(const NkAttnOutArgs p) { attn_out_impl<16>(p); }

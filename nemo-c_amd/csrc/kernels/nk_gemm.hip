@@ -22,7 +22,7 @@
  *      LayerNorm (the _ln kernels, K <= 1024) or straight from global memory;
  *   3. per step two MFMAs, A = hi + lo bf16 split of the f32 activations (16 significant bits);
  *   4. the W partial tiles are summed in wavefront order through LDS; wavefront 0 applies the
- *      epilogue (after the ordered combine of the K split, when there is one).
+ *      epilogue (or, with K split over workgroups, writes its share's partial rows).
  * MFMA 16x16x32 bf16 lane layouts (lane l, element i):
  *   A: row l % 16, k 8*(l/16) + i;  B: k 8*(l/16) + i, column l % 16;
  *   D: row 4*(l/16) + i, column l % 16. */
@@ -50,9 +50,9 @@ __device__ __forceinline__ void ln_wave4(floatx4 (&v)[4], const floatx4 (&g)[4],
 
 /* grid = (ceil(nout/16), KS): workgroup (tile, ks) takes the K steps [ks*S/KS, (ks+1)*S/KS) of the
  * S = K/32 steps, wavefront w the SPW steps from w*SPW within them.  With KS > 1 (the host uses it
- * only for accumulating GEMMs with no bias and no activation) every workgroup stores its partial
- * tile agent-coherent and the tile's last workgroup to arrive adds the KS partials in ks order
- * and updates C (nk_common.h), so the result does not depend on arrival order. */
+ * only for residual updates: accumulate, no bias, no activation, identity rows) every workgroup
+ * writes its share as partial rows and the host folds them into C in share order with one more
+ * launch (resid_fold), so no result depends on which workgroup finishes first. */
 template <int W, int SPW, bool LNA, bool GLU>
 __device__ __forceinline__ void fr_impl(const NkGemmArgs &a, float *sA, floatx4 *sred) {
     const u32 tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -186,20 +186,17 @@ __device__ __forceinline__ void fr_impl(const NkGemmArgs &a, float *sA, floatx4 
         ta += sred[w * 64 + lane];
         if constexpr (GLU) tb += sred[(W + w) * 64 + lane];
     }
-    if (KS > 1) { /* K split over workgroups: no bias, no activation, accumulate */
-        float *wsb = a.ws + (u64)blockIdx.x * KS * 256;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) st_agent(wsb + (blockIdx.y * 4 + i) * 64 + lane, ta[i]);
-        wait_stores();
-        u32 last = 0;
-        if (lane == 0) last = arrive_last(a.counters + blockIdx.x, KS) ? 1u : 0u;
-        if (!__builtin_amdgcn_readfirstlane(last)) return;
+    if (KS > 1) {
+        /* K split over workgroups (residual updates: no bias, no activation, identity rows): this
+         * share's sums go to partial rows P[ks][row][n] (rows of nout floats); the host folds them
+         * into C in ks order afterwards (resid_fold) */
+        if (n0 + (lane & 15) >= nout) return;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            float t = 0.0f;
-            for (u32 ks = 0; ks < KS; ++ks) t += ks == blockIdx.y ? ta[i] : ld_agent(wsb + (ks * 4 + i) * 64 + lane);
-            ta[i] = t;
+            const u32 r = 4 * (lane >> 4) + i;
+            if (r < M) a.ws[((u64)blockIdx.y * M + r) * nout + col] = ta[i];
         }
+        return;
     }
     if (n0 + (lane & 15) >= nout) return;
 #pragma unroll
