@@ -132,6 +132,18 @@ typedef struct {
 int nk_gemm_resid(gpu_t *g, const float *A, const uint16_t *A2, uint32_t lda, const uint16_t *W, uint32_t ldw, float *C,
                   uint32_t ldc, uint32_t M, uint32_t N, uint32_t K, float alpha, nk_resid_t *pend);
 int nk_resid_fold(gpu_t *g, float *C, uint32_t ldc, uint32_t M, uint32_t N, const nk_resid_t *pend);
+/* nk_gemm_split without any allocation.  No counterpart in the reference: it is for callers that
+ * cannot allocate device memory (code under hipGraph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  The split-K partial sums and arrival counters live in a static device array
+ * of NK_NOALLOC_WS_FLOATS floats per GPU (held until the process ends): the partial rows of a
+ * residual update (at most NK_NOALLOC_WS_FLOATS = parts x M x N floats; a larger one is refused with
+ * an error before any launch).  Every call on a GPU shares its array and overwrites what the last
+ * call left there (nothing in it needs to start at zero): calls that overlap on one GPU race.  Same
+ * arguments and results (bit for bit) as nk_gemm_split. */
+#define NK_NOALLOC_WS_FLOATS (4u << 20)
+int nk_gemm_split_noalloc(gpu_t *g, const float *A, const uint16_t *A2, uint32_t lda, const uint16_t *W, uint32_t ldw,
+                          const float *bias, float *C, uint16_t *C2, uint32_t ldc, const int *crow, uint32_t M,
+                          uint32_t N, uint32_t K, int act, int accumulate, float alpha);
 /* LayerNorm of M rows (D <= 1024, one wavefront per row) whose GEMM-feeding output goes to Ys as
  * split rows (row stride 2D): the single LayerNorm (g2 NULL) writes only Ys; the pair writes
  * LN(X; g1, b1) to Y1 (f32) and LN(Y1; g2, b2) to Ys.  With pend (from nk_gemm_resid, may be NULL)

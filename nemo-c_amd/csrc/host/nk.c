@@ -254,6 +254,16 @@ int nk_gemm_resid(gpu_t *g, const float *A, const uint16_t *A2, uint32_t lda, co
     return gemm_split_core(g, A, A2, lda, W, ldw, NULL, C, NULL, ldc, NULL, M, N, K, NK_ACT_NONE, 1, alpha, NULL, pend);
 }
 
+/* nk_gemm_split on a fixed scratch region the caller provides (the allocation-free entry point,
+ * noalloc.hip): a residual update whose partial rows need more than the region holds is refused
+ * before anything is launched. */
+int nk_gemm_split_scratch(gpu_t *g, const float *A, const uint16_t *A2, uint32_t lda, const uint16_t *W, uint32_t ldw,
+                          const float *bias, float *C, uint16_t *C2, uint32_t ldc, const int *crow, uint32_t M,
+                          uint32_t N, uint32_t K, int act, int accumulate, float alpha, float *ws, size_t ws_floats) {
+    const mx_scratch_t sc = { ws, ws_floats };
+    return gemm_split_core(g, A, A2, lda, W, ldw, bias, C, C2, ldc, crow, M, N, K, act, accumulate, alpha, &sc, NULL);
+}
+
 int nk_gemm_argmax(gpu_t *g, const float *A, uint32_t lda, const uint16_t *W, uint32_t ldw, const float *bias,
                    unsigned long long *keys, uint32_t keys_ld, uint32_t M, uint32_t N, uint32_t K, uint32_t V) {
     return nk_gemm_argmax_rows(g, A, lda, W, ldw, bias, keys, keys_ld, M, N, K, V, NULL, 0);

@@ -108,6 +108,8 @@ API = {
     "nk_gemm_fr_ksplit": (C.c_int, [C.c_int]),
     "nk_gemm_split": (C.c_int, [_vp, _vp, _vp, _u32, _vp, _u32, _vp, _vp, _vp, _u32, _vp, _u32, _u32, _u32, C.c_int,
                                 C.c_int, C.c_float]),
+    "nk_gemm_split_noalloc": (C.c_int, [_vp, _vp, _vp, _u32, _vp, _u32, _vp, _vp, _vp, _u32, _vp, _u32, _u32, _u32,
+                                        C.c_int, C.c_int, C.c_float]),
     "nk_layernorm2_split": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32, C.c_float]),
     "nk_gemm_resid": (C.c_int, [_vp, _vp, _vp, _u32, _vp, _u32, _vp, _u32, _u32, _u32, _u32, C.c_float, _vp]),
     "nk_resid_fold": (C.c_int, [_vp, _vp, _u32, _u32, _u32, _vp]),
