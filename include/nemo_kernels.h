@@ -101,6 +101,9 @@ int nk_gemm_argmax_rows(gpu_t *g, const float *A, uint32_t lda, const uint16_t *
  * tile count, 0 never, 1 always where K has more than one block.  All three give the same bits.
  * Returns the previous setting. */
 int nk_gemm_ksplit(int mode);
+/* Many-row tile: -1 (default) by tile count, else 0 128x128, 1 64x128, 2 64x64 where it divides
+ * the output columns.  Returns the previous setting. */
+int nk_gemm_mx_tile(int t);
 /* Few-row residual updates (5..16 rows): 1 (default) splits K over four workgroups with an ordered
  * combine, 0 keeps K in one workgroup (more wavefronts).  Returns the previous setting. */
 int nk_gemm_fr_ksplit(int on);

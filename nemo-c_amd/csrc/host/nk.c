@@ -9,6 +9,13 @@
 
 static int g_force = 0;
 static int g_split = -1; /* many-row residual updates: -1 K split chosen by tile count, 0 never, 1 always */
+static int g_mx_tile = -1; /* many-row tile: -1 by tile count, else 0 128x128, 1 64x128, 2 64x64 where it divides */
+
+int nk_gemm_mx_tile(int t) {
+    const int prev = g_mx_tile;
+    g_mx_tile = t < 0 || t > 2 ? -1 : t;
+    return prev;
+}
 
 int nk_gemm_ksplit(int mode) {
     const int prev = g_split;
@@ -142,17 +149,24 @@ static int launch_mx_s(gpu_t *g, NkGemmArgs *a, uint32_t M, uint32_t nout, uint3
     };
     int pick_i = -1, last_ok = -1;
     uint32_t tiles = 0;
+    const uint32_t kb = resid ? mx_kblocks(K) : 1;
     for (int i = 0; i < 3; ++i) {
         const uint32_t cols = glu ? cfg[i].bn / 2 : cfg[i].bn;
         if (nout % cols) continue;
         const uint32_t t = ((M + cfg[i].bm - 1) / cfg[i].bm) * (nout / cols);
-        if (cfg[i].bm == 128 && M < 512) continue;
+        if (cfg[i].bm == 128 && (M < 512 || a->A2)) continue; /* split rows: one workgroup per CU */
         last_ok = i;
-        /* two workgroups per CU: the largest tile with at least ~400 tiles was the fastest at every
-         * measured shape (448 to 3584 rows, N 1024 to 4096, K 1024 and 4096) */
-        if (t >= 400) { pick_i = i; tiles = t; break; }
+        /* two workgroups per CU: the largest tile with at least ~400 workgroups (residual updates:
+         * tiles x K blocks, the split below) was the fastest at every measured shape (448 to 3584
+         * rows, N 1024 to 4096, K 1024 and 4096) */
+        if ((a->A2 ? t * kb : t) >= 400) { pick_i = i; tiles = t; break; }
     }
     if (last_ok < 0) return 1;
+    if (g_mx_tile >= 0 && nout % (glu ? cfg[g_mx_tile].bn / 2 : cfg[g_mx_tile].bn) == 0) pick_i = g_mx_tile;
+    if (pick_i >= 0) {
+        const uint32_t cols = glu ? cfg[pick_i].bn / 2 : cfg[pick_i].bn;
+        tiles = ((M + cfg[pick_i].bm - 1) / cfg[pick_i].bm) * (nout / cols);
+    }
     if (pick_i < 0) {
         pick_i = last_ok;
         const uint32_t cols = glu ? cfg[pick_i].bn / 2 : cfg[pick_i].bn;
@@ -218,8 +232,8 @@ static int gemm_split_core(gpu_t *g, const float *A, const uint16_t *A2, uint32_
     if (!M) return 0;
     const int glu = act == NK_ACT_GLU;
     const uint32_t nout = glu ? N / 2 : N;
-    if (!N || !K || (glu && (N & 1)) || K % 32 || !A == !A2 || !C == !C2)
-        return bad(g, "gemm_split: one A form, one C form, K % 32 == 0");
+    if (!N || !K || (glu && (N & 1)) || K % 32 || (A2 && K % NK_MX_KS_SPLIT) || !A == !A2 || !C == !C2)
+        return bad(g, "gemm_split: one A form, one C form, K % 32 == 0 (K % 64 == 0 with split-row A)");
     if (!aligned16(W) || ldw % 8 || K > ldw) return bad(g, "gemm_split: W 16-byte aligned, ldw % 8 == 0, K <= ldw");
     if (A ? (!aligned16(A) || lda % 4 || K > lda) : (!aligned16(A2) || lda % 8 || 2 * K > lda))
         return bad(g, "gemm_split: A 16-byte aligned rows of at least K values (split: 2K, lda % 8 == 0)");

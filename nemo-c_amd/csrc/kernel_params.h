@@ -28,6 +28,7 @@ typedef uint16_t u16;
 
 /* Row and chunk limits.  One wavefront is 64 lanes on CDNA4. */
 #define NK_WAVE 64
+#define NK_MX_KS_SPLIT 64       /* K step of the many-row kernels on split-row A (K % this == 0)  */
 #define NK_FEW_ROWS 16          /* GEMMs with M <= 16 use the weight-streaming kernels            */
 #define NK_ATT_MAX_L 128        /* attention window limit (reference ATT_MAX_L 80; 56 + 16 + 2)    */
 #define NK_DEC_MAX_BATCH 16     /* joint rows per decoder round trip (reference DEC_MAX_BATCH)    */

@@ -49,12 +49,17 @@
  * 3584 rows. */
 __device__ __forceinline__ u32 swz_a(u32 r) { return (r & 7) ^ ((r >> 3) & 1); }
 __device__ __forceinline__ u32 swz_b(u32 n) { return (n >> 1) & 3; }
+/* bf16 rows of G granules (4: 32 K, 8: 64 K; the 128-byte rows have the f32 rows' geometry) */
+template <int G> __device__ __forceinline__ u32 swz_h(u32 r) { return G == 4 ? swz_b(r) : swz_a(r); }
+
 
 /* EPI: 0 bias / activation / GLU / accumulate epilogue; 1 argmax keys; 2 blocked-K residual
  * update into partial rows.  AS: A as split rows; OS: outputs as split rows (EPI 0 without GLU). */
 template <int BM, int BN, int WGM, int NS, bool GLU, int EPI = 0, bool AS = false, bool OS = false>
 __device__ __forceinline__ void mx_impl(const NkGemmArgs &a, lds_char_t *const (&ring)[NS]) {
-    constexpr int KS = 32;
+    /* K step: 64 for split-row A (128-byte row segments, whole cache lines, per operand row), 32 for
+     * f32 A */
+    constexpr int KS = AS ? NK_MX_KS_SPLIT : 32, KSUB = KS / 32;
     static_assert(!OS || (EPI == 0 && !GLU), "split outputs from the plain epilogue only");
     constexpr int WGN = 4 / WGM;
     constexpr int WTM = BM / WGM, WTN = BN / WGN;
@@ -95,7 +100,7 @@ __device__ __forceinline__ void mx_impl(const NkGemmArgs &a, lds_char_t *const (
     for (int j = 0; j < AI; ++j) {
         const u32 p = (4 * j + wave) * 64 + lane;
         if constexpr (AS) {
-            const u32 plane = p / (BM * BG), q = p % (BM * BG), r = q / BG, kg = (q % BG) ^ swz_b(r);
+            const u32 plane = p / (BM * BG), q = p % (BM * BG), r = q / BG, kg = (q % BG) ^ swz_h<BG>(r);
             asrc[j] = (const char *)(a.A2 + (u64)min(m0 + r, M - 1) * a.lda + plane * a.K + 8 * kg + (u64)s_begin * KS);
         } else {
             const u32 r = p / AG, kg = (p % AG) ^ swz_a(r);
@@ -106,7 +111,7 @@ __device__ __forceinline__ void mx_impl(const NkGemmArgs &a, lds_char_t *const (
     const u16 *bsrc[BI];
 #pragma unroll
     for (int j = 0; j < BI; ++j) {
-        const u32 p = (4 * j + wave) * 64 + lane, n = p / BG, kg = (p % BG) ^ swz_b(n);
+        const u32 p = (4 * j + wave) * 64 + lane, n = p / BG, kg = (p % BG) ^ swz_h<BG>(n);
         u32 col;
         if (GLU) col = n < BN / 2 ? c0 + n : a.N / 2 + c0 + (n - BN / 2);
         else col = c0 + n;
@@ -122,26 +127,31 @@ __device__ __forceinline__ void mx_impl(const NkGemmArgs &a, lds_char_t *const (
 
     /* fragment addresses inside a stage */
     const u32 fr = lane & 15, fg = lane >> 4;
-    u32 aoff[TI][2]; /* f32 A: the two halves of the 8 K; split A: the hi and the lo fragment */
+    /* f32 A: the two halves of the 8 K; split A: the hi and the lo fragment of each 32-K substep */
+    u32 aoff[TI][KSUB][2];
 #pragma unroll
     for (int i = 0; i < TI; ++i) {
         const u32 r = wm * WTM + 16 * i + fr;
         if constexpr (AS) {
-            aoff[i][0] = (r * BG + (fg ^ swz_b(r))) * 16;
-            aoff[i][1] = aoff[i][0] + BM * BG * 16;
+#pragma unroll
+            for (int h = 0; h < KSUB; ++h) {
+                aoff[i][h][0] = (r * BG + ((4 * h + fg) ^ swz_h<BG>(r))) * 16;
+                aoff[i][h][1] = aoff[i][h][0] + BM * BG * 16;
+            }
         } else {
-            aoff[i][0] = (r * AG + ((2 * fg) ^ swz_a(r))) * 16;
-            aoff[i][1] = (r * AG + ((2 * fg + 1) ^ swz_a(r))) * 16;
+            aoff[i][0][0] = (r * AG + ((2 * fg) ^ swz_a(r))) * 16;
+            aoff[i][0][1] = (r * AG + ((2 * fg + 1) ^ swz_a(r))) * 16;
         }
     }
-    u32 boff[TJ];
+    u32 boff[TJ][KSUB];
 #pragma unroll
     for (int j = 0; j < TJ; ++j) {
         u32 n;
         if (GLU) n = j < TJ / 2 ? wn * (WTN / 2) + 16 * j : BN / 2 + wn * (WTN / 2) + 16 * (j - TJ / 2);
         else n = wn * WTN + 16 * j;
         n += fr;
-        boff[j] = A_BYTES + (n * BG + (fg ^ swz_b(n))) * 16;
+#pragma unroll
+        for (int h = 0; h < KSUB; ++h) boff[j][h] = A_BYTES + (n * BG + ((4 * h + fg) ^ swz_h<BG>(n))) * 16;
     }
 
     floatx4 acc[TI][TJ];
@@ -173,30 +183,37 @@ __device__ __forceinline__ void mx_impl(const NkGemmArgs &a, lds_char_t *const (
         barrier_mem();
         issue(min(q + NS - 1, nst - 1), (u + NS - 1) % NS);
         const lds_char_t *st = ring[u];
-        uint4 fb[TJ];
+        uint4 fb[KSUB][TJ], fh[KSUB][TI], fl[KSUB][TI];
 #pragma unroll
-        for (int j = 0; j < TJ; ++j) fb[j] = *(const __attribute__((address_space(3))) uint4 *)(st + boff[j]);
-        uint4 fh[TI], fl[TI];
+        for (int h = 0; h < KSUB; ++h) {
 #pragma unroll
-        for (int i = 0; i < TI; ++i) {
-            if constexpr (AS) {
-                fh[i] = *(const __attribute__((address_space(3))) uint4 *)(st + aoff[i][0]);
-                fl[i] = *(const __attribute__((address_space(3))) uint4 *)(st + aoff[i][1]);
-            } else {
-                const floatx4 x0 = *(const __attribute__((address_space(3))) floatx4 *)(st + aoff[i][0]);
-                const floatx4 x1 = *(const __attribute__((address_space(3))) floatx4 *)(st + aoff[i][1]);
-                const float x[8] = { x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3] };
-                split8(x, fh[i], fl[i]);
+            for (int j = 0; j < TJ; ++j) fb[h][j] = *(const __attribute__((address_space(3))) uint4 *)(st + boff[j][h]);
+#pragma unroll
+            for (int i = 0; i < TI; ++i) {
+                if constexpr (AS) {
+                    fh[h][i] = *(const __attribute__((address_space(3))) uint4 *)(st + aoff[i][h][0]);
+                    fl[h][i] = *(const __attribute__((address_space(3))) uint4 *)(st + aoff[i][h][1]);
+                } else {
+                    const floatx4 x0 = *(const __attribute__((address_space(3))) floatx4 *)(st + aoff[i][0][0]);
+                    const floatx4 x1 = *(const __attribute__((address_space(3))) floatx4 *)(st + aoff[i][0][1]);
+                    const float x[8] = { x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3] };
+                    split8(x, fh[h][i], fl[h][i]);
+                }
             }
         }
+        /* per 32-K substep: every hi product, then every lo product (the same order at every K step
+         * size, so every tile and step size gives the same bits) */
 #pragma unroll
-        for (int i = 0; i < TI; ++i)
+        for (int h = 0; h < KSUB; ++h) {
 #pragma unroll
-            for (int j = 0; j < TJ; ++j) acc[i][j] = mfma_bf16(fh[i], fb[j], acc[i][j]);
+            for (int i = 0; i < TI; ++i)
 #pragma unroll
-        for (int i = 0; i < TI; ++i)
+                for (int j = 0; j < TJ; ++j) acc[i][j] = mfma_bf16(fh[h][i], fb[h][j], acc[i][j]);
 #pragma unroll
-            for (int j = 0; j < TJ; ++j) acc[i][j] = mfma_bf16(fl[i], fb[j], acc[i][j]);
+            for (int i = 0; i < TI; ++i)
+#pragma unroll
+                for (int j = 0; j < TJ; ++j) acc[i][j] = mfma_bf16(fl[h][i], fb[h][j], acc[i][j]);
+        }
         if constexpr (EPI == 2) {
             if ((q + 1) % spb == 0) { /* a K block ends: add its sum, start the next from zero */
 #pragma unroll
@@ -346,43 +363,66 @@ __device__ __forceinline__ void mx_impl(const NkGemmArgs &a, lds_char_t *const (
     }
 }
 
-/* NS ring stages of 32-wide K steps: (BM*4 + BN*2)*32 bytes each, sized so that two workgroups fit
- * a CU's 160 KB of LDS (measured: the second workgroup overlaps one's loads and barriers with the
- * other's MFMAs; 3584 rows, 128x128: 117 -> 79 us with the swizzles): 3 x 24 KB for 128x128,
- * 4 x 16 KB for 64x128, 4 x 12 KB for 64x64 */
+/* Ring depth NS.  Stages are (BM*4 + BN*2)*KS bytes, and the depth is chosen so that two
+ * workgroups fit a CU's 160 KB of LDS: the second workgroup's MFMAs run while the first waits at
+ * its barrier.  Measured on gfx950 (3584 rows, 128x128: 117 -> 79 us), and again with deeper rings
+ * at one workgroup per CU, which were slower at every shape from 448 to 3584 rows.
+ *   f32 A, KS 32:        3 x 24 KB for 128x128, 4 x 16 KB for 64x128, 4 x 12 KB for 64x64;
+ *   split-row A, KS 64:  2 x 32 KB for 64x128, 3 x 24 KB for 64x64 (2 x 48 KB for 128x128, one
+ *                        workgroup per CU, which the host does not pick for split rows).
+ * The 64-wide K step reads whole 128-byte row segments and halves the barriers: 10-15% faster
+ * than 32 at 448 and 1792 rows. */
+#ifndef MX_NS_L
+#define MX_NS_L 3
+#endif
+#ifndef MX_NS_M
+#define MX_NS_M 4
+#endif
+#ifndef MX_NS_S
+#define MX_NS_S 4
+#endif
+#ifndef MX_NS_LS
+#define MX_NS_LS 2
+#endif
+#ifndef MX_NS_MS
+#define MX_NS_MS 2
+#endif
+#ifndef MX_NS_SS
+#define MX_NS_SS 3
+#endif
 #define GEMM_MX_T(NAME, BM, BN, WGM, NS, GLU, EPI, AS, OS)                                              \
     extern "C" __global__ __launch_bounds__(256) void NAME(const NkGemmArgs a) {                          \
-        __shared__ uint4 ring_mem[NS][(BM * 4 + BN * 2) * 32 / 16];                                      \
+        __shared__ uint4 ring_mem[NS][(BM * 4 + BN * 2) * (AS ? NK_MX_KS_SPLIT : 32) / 16];                    \
         lds_char_t *ring[NS];                                                                             \
         _Pragma("unroll") for (int i = 0; i < NS; ++i) ring[i] = (lds_char_t *)ring_mem[i];               \
         mx_impl<BM, BN, WGM, NS, GLU, EPI, AS, OS>(a, ring);                                              \
     }
 #define GEMM_MX(NAME, BM, BN, WGM, NS, GLU, EPI) GEMM_MX_T(NAME, BM, BN, WGM, NS, GLU, EPI, false, false)
-GEMM_MX(gemm_mx128x128, 128, 128, 2, 3, false, 0)
-GEMM_MX(gemm_mx64x128, 64, 128, 2, 4, false, 0)
-GEMM_MX(gemm_mx64x64, 64, 64, 2, 4, false, 0)
-GEMM_MX(gemm_mx128x128_glu, 128, 128, 2, 3, true, 0)
-GEMM_MX(gemm_mx64x128_glu, 64, 128, 2, 4, true, 0)
-GEMM_MX(gemm_mx64x64_glu, 64, 64, 2, 4, true, 0)
+GEMM_MX(gemm_mx128x128, 128, 128, 2, MX_NS_L, false, 0)
+GEMM_MX(gemm_mx64x128, 64, 128, 2, MX_NS_M, false, 0)
+GEMM_MX(gemm_mx64x64, 64, 64, 2, MX_NS_S, false, 0)
+GEMM_MX(gemm_mx128x128_glu, 128, 128, 2, MX_NS_L, true, 0)
+GEMM_MX(gemm_mx64x128_glu, 64, 128, 2, MX_NS_M, true, 0)
+GEMM_MX(gemm_mx64x64_glu, 64, 64, 2, MX_NS_S, true, 0)
 /* residual updates: blocked K, optional ordered split */
-GEMM_MX(gemm_mx128x128_acc, 128, 128, 2, 3, false, 2)
-GEMM_MX(gemm_mx64x128_acc, 64, 128, 2, 4, false, 2)
-GEMM_MX(gemm_mx64x64_acc, 64, 64, 2, 4, false, 2)
+GEMM_MX(gemm_mx128x128_acc, 128, 128, 2, MX_NS_L, false, 2)
+GEMM_MX(gemm_mx64x128_acc, 64, 128, 2, MX_NS_M, false, 2)
+GEMM_MX(gemm_mx64x64_acc, 64, 64, 2, MX_NS_S, false, 2)
 /* joint scores -> argmax partials (keys), 64x64 tiles: two keys per row per column tile */
-GEMM_MX(gemm_mx64x64_argmax, 64, 64, 2, 4, false, 1)
+GEMM_MX(gemm_mx64x64_argmax, 64, 64, 2, MX_NS_S, false, 1)
 /* split-row A (suffix _s), split-row outputs (suffix _so) */
-GEMM_MX_T(gemm_mx128x128_s, 128, 128, 2, 3, false, 0, true, false)
-GEMM_MX_T(gemm_mx64x128_s, 64, 128, 2, 4, false, 0, true, false)
-GEMM_MX_T(gemm_mx64x64_s, 64, 64, 2, 4, false, 0, true, false)
-GEMM_MX_T(gemm_mx128x128_glu_s, 128, 128, 2, 3, true, 0, true, false)
-GEMM_MX_T(gemm_mx64x128_glu_s, 64, 128, 2, 4, true, 0, true, false)
-GEMM_MX_T(gemm_mx64x64_glu_s, 64, 64, 2, 4, true, 0, true, false)
-GEMM_MX_T(gemm_mx128x128_acc_s, 128, 128, 2, 3, false, 2, true, false)
-GEMM_MX_T(gemm_mx64x128_acc_s, 64, 128, 2, 4, false, 2, true, false)
-GEMM_MX_T(gemm_mx64x64_acc_s, 64, 64, 2, 4, false, 2, true, false)
-GEMM_MX_T(gemm_mx128x128_so, 128, 128, 2, 3, false, 0, false, true)
-GEMM_MX_T(gemm_mx64x128_so, 64, 128, 2, 4, false, 0, false, true)
-GEMM_MX_T(gemm_mx64x64_so, 64, 64, 2, 4, false, 0, false, true)
-GEMM_MX_T(gemm_mx128x128_s_so, 128, 128, 2, 3, false, 0, true, true)
-GEMM_MX_T(gemm_mx64x128_s_so, 64, 128, 2, 4, false, 0, true, true)
-GEMM_MX_T(gemm_mx64x64_s_so, 64, 64, 2, 4, false, 0, true, true)
+GEMM_MX_T(gemm_mx128x128_s, 128, 128, 2, MX_NS_LS, false, 0, true, false)
+GEMM_MX_T(gemm_mx64x128_s, 64, 128, 2, MX_NS_MS, false, 0, true, false)
+GEMM_MX_T(gemm_mx64x64_s, 64, 64, 2, MX_NS_SS, false, 0, true, false)
+GEMM_MX_T(gemm_mx128x128_glu_s, 128, 128, 2, MX_NS_LS, true, 0, true, false)
+GEMM_MX_T(gemm_mx64x128_glu_s, 64, 128, 2, MX_NS_MS, true, 0, true, false)
+GEMM_MX_T(gemm_mx64x64_glu_s, 64, 64, 2, MX_NS_SS, true, 0, true, false)
+GEMM_MX_T(gemm_mx128x128_acc_s, 128, 128, 2, MX_NS_LS, false, 2, true, false)
+GEMM_MX_T(gemm_mx64x128_acc_s, 64, 128, 2, MX_NS_MS, false, 2, true, false)
+GEMM_MX_T(gemm_mx64x64_acc_s, 64, 64, 2, MX_NS_SS, false, 2, true, false)
+GEMM_MX_T(gemm_mx128x128_so, 128, 128, 2, MX_NS_L, false, 0, false, true)
+GEMM_MX_T(gemm_mx64x128_so, 64, 128, 2, MX_NS_M, false, 0, false, true)
+GEMM_MX_T(gemm_mx64x64_so, 64, 64, 2, MX_NS_S, false, 0, false, true)
+GEMM_MX_T(gemm_mx128x128_s_so, 128, 128, 2, MX_NS_LS, false, 0, true, true)
+GEMM_MX_T(gemm_mx64x128_s_so, 64, 128, 2, MX_NS_MS, false, 0, true, true)
+GEMM_MX_T(gemm_mx64x64_s_so, 64, 64, 2, MX_NS_SS, false, 0, true, true)

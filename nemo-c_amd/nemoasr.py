@@ -93,6 +93,7 @@ API = {
     "gpu_last_error": (C.c_char_p, [_vp]),
     "gpu_timing_set": (C.c_int, [_vp, C.c_char_p, C.c_int]),
     "gpu_timing_collect": (C.c_int, [_vp, C.POINTER(C.c_double), C.POINTER(C.c_int), C.POINTER(C.c_double)]),
+    "gpu_timing_last_flops": (C.c_double, [_vp]),
     "gpu_launch_count": (C.c_uint64, [_vp]),
     "gpu_capture_begin": (C.c_int, [_vp]),
     "gpu_capture_end": (_vp, [_vp]),
@@ -105,6 +106,7 @@ API = {
                              C.c_float, C.c_int, _vp, _vp, _vp, _vp, _vp, _vp, C.c_float]),
     "nk_gemm_force": (C.c_int, [C.c_int]),
     "nk_gemm_ksplit": (C.c_int, [C.c_int]),
+    "nk_gemm_mx_tile": (C.c_int, [C.c_int]),
     "nk_gemm_fr_ksplit": (C.c_int, [C.c_int]),
     "nk_gemm_split": (C.c_int, [_vp, _vp, _vp, _u32, _vp, _u32, _vp, _vp, _vp, _u32, _vp, _u32, _u32, _u32, C.c_int,
                                 C.c_int, C.c_float]),
