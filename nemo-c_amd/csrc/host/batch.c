@@ -64,7 +64,13 @@ typedef struct {
     size_t consumed, emitted;
     int closed, final;
     int pos, cache_len;                 /* cache rows of this stream */
-    int last_token, pred_valid, cur;    /* decoder; cur = committed LSTM slot set */
+    /* Decoder fields (through cap_tok).  Ownership between the caller's thread and the greedy-loop
+     * worker: while a loop is queued or running (dstate != 0) only the worker touches them; the
+     * caller's thread sets frames..erow0 for the next loop, and reads or resets any of them, only
+     * after dec_drain() has returned (worker idle).  The encoder part of a step touches none of
+     * them.  The same rule holds for the stats fields the worker adds to (decoder_ms, tokens,
+     * joint_steps). */
+    int last_token, pred_valid, cur;    /* cur = committed LSTM slot set */
     int frames, t, symbols, erow0;      /* the chunk in the decoder */
     int *tok;
     size_t n_tok, cap_tok, n_text;
@@ -348,9 +354,14 @@ static int mel_gpu_setup(nemoasr_batch_t *b) {
     const int rc = gpu_upload(g, gpu_buf_dptr(b->meltab), h, MT_BYTES);
     free(h);
     melfe_destroy(mf);
+    /* every staging buffer sized at open for one window per stream per step (host mel rows
+     * included), so a step allocates nothing while the worker thread may be capturing; growth stays
+     * only for a stream that consumes several row-less chunks in one step */
     const size_t fr = S * (size_t)b->nwin_max;
     if (grow_stage(g, (void **)&b->stage_span, &b->span_dev, &b->span_cap, fr * MEL_HOP + S * MEL_NFFT, 0, sizeof(float)) ||
-        grow_stage(g, (void **)&b->stage_ftab, &b->ftab_dev, &b->ftab_cap, 2 * fr, 0, sizeof(int)))
+        grow_stage(g, (void **)&b->stage_ftab, &b->ftab_dev, &b->ftab_cap, 2 * fr, 0, sizeof(int)) ||
+        grow_stage(g, (void **)&b->stage_hrow, &b->hrow_dev, &b->hrow_cap, fr * MEL_NMEL, 0, sizeof(float)) ||
+        grow_stage(g, (void **)&b->stage_hmap, &b->hmap_dev, &b->hmap_cap, fr, 0, sizeof(int)))
         return -1;
     return rc;
 }

@@ -49,8 +49,10 @@
  * 3584 rows. */
 __device__ __forceinline__ u32 swz_a(u32 r) { return (r & 7) ^ ((r >> 3) & 1); }
 __device__ __forceinline__ u32 swz_b(u32 n) { return (n >> 1) & 3; }
-/* bf16 rows of G granules (4: 32 K, 8: 64 K; the 128-byte rows have the f32 rows' geometry) */
-template <int G> __device__ __forceinline__ u32 swz_h(u32 r) { return G == 4 ? swz_b(r) : swz_a(r); }
+/* bf16 rows of G granules (4: 32 K, 8: 64 K).  The 8-granule rows have the f32 rows' geometry but
+ * another read pattern (lane group f reads granule 4h + f, not 2f and 2f + 1): swz_a costs a 2-way
+ * conflict on every read there, (r >> 1) & 7 none (SQ_LDS_BANK_CONFLICT over candidates on gfx950) */
+template <int G> __device__ __forceinline__ u32 swz_h(u32 r) { return G == 4 ? swz_b(r) : (r >> 1) & 7; }
 
 
 /* EPI: 0 bias / activation / GLU / accumulate epilogue; 1 argmax keys; 2 blocked-K residual

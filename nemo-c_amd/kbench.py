@@ -12,6 +12,7 @@ For each shape it reports
 Plus a large device copy (HBM read + write bandwidth reference) and the per-row kernels.
 
 Usage: python kbench.py [--rows 1,7,14] [--reps 3] [--json out.json]
+       python kbench.py --no-gemm --rows 0 --split-rows 448,1792,3584 --tiles=-1,2,1 --ksplits=-1,0,1
 """
 import argparse
 import ctypes as C
@@ -167,6 +168,54 @@ def bench_dwconv(gpu, c, use_desc, copies, reps):
     return us
 
 
+# the batched encoder's many-row GEMMs on split-row activations (K bf16 hi then K lo per row), as
+# batch.c calls them: (label, N, K, act, kind) with kind "so" split-row output, "f" f32 output,
+# "r" residual update left pending (nk_gemm_resid)
+SPLIT_SHAPES = [("ff_up", 4096, 1024, 1, "so"), ("ff_down", 1024, 4096, 0, "r"), ("qkv", 3072, 1024, 0, "f"),
+                ("pw1_glu", 2048, 1024, 3, "f"), ("out/pw2", 1024, 1024, 0, "r")]
+
+
+def split_rows(x):
+    """f32 rows -> split rows (RNE bf16 hi, then RNE bf16 of the remainder)."""
+    u = np.ascontiguousarray(x, np.float32).view(np.uint32)
+    hi = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    r = (x - (hi.astype(np.uint32) << 16).view(np.float32)).astype(np.float32).view(np.uint32)
+    lo = ((r + 0x7FFF + ((r >> 16) & 1)) >> 16).astype(np.uint16)
+    return np.concatenate([hi, lo], axis=1)
+
+
+def bench_split(gpu, M, N, K, act, kind, copies, launches):
+    """Mean kernel time (dispatch-stamped events, direct launches) and total flops of `launches`
+    launches cycling `copies` weight matrices."""
+    L = nemoasr.lib()
+    rng = np.random.default_rng(1)
+    A2 = gpu.put(split_rows(rng.standard_normal((M, K)).astype(np.float32)))
+    Ws = [gpu.put(((rng.standard_normal((N, K)) * 0.03).astype(np.float32).view(np.uint32) >> 16).astype(np.uint16))
+          for _ in range(copies)]
+    nout = N // 2 if act == 3 else N
+    Cb = gpu.alloc(M * nout * 4 * (2 if kind == "so" else 1))
+    pend = nemoasr.Resid()
+    L.gpu_timing_set(gpu.h, b"gemm_mx*", launches)
+    gpu.begin()
+    for r in range(launches):
+        W = Ws[r % copies].ptr
+        if kind == "so":
+            rc = L.nk_gemm_split(gpu.h, None, A2.ptr, 2 * K, W, K, None, None, Cb.ptr, 2 * nout, None, M, N, K, act, 0, 1.0)
+        elif kind == "f":
+            rc = L.nk_gemm_split(gpu.h, None, A2.ptr, 2 * K, W, K, None, Cb.ptr, None, nout, None, M, N, K, act, 0, 1.0)
+        else:
+            rc = L.nk_gemm_resid(gpu.h, None, A2.ptr, 2 * K, W, K, Cb.ptr, N, M, N, K, 1.0, C.byref(pend))
+        gpu.check(rc)
+    gpu.end()
+    ms, cnt, by = C.c_double(), C.c_int(), C.c_double()
+    L.gpu_timing_collect(gpu.h, C.byref(ms), C.byref(cnt), C.byref(by))
+    fl = L.gpu_timing_last_flops(gpu.h)
+    for b in Ws + [A2, Cb]:
+        b.free()
+    gpu._bufs = []
+    return ms.value * 1e3, fl / max(cnt.value, 1)
+
+
 def bench_copy(gpu, nbytes, reps):
     L = nemoasr.lib()
     n = nbytes // 4
@@ -190,6 +239,10 @@ def main():
     ap.add_argument("--no-gemm", action="store_true")
     ap.add_argument("--batch-rows", default="", help="many-row (batched streams) GEMM sizes, e.g. 448,3584")
     ap.add_argument("--batch-force", default="0", help="kernel selections to compare (nk_gemm_force), e.g. 0,5")
+    ap.add_argument("--split-rows", default="", help="many-row GEMMs on split-row activations, e.g. 448,1792,3584")
+    ap.add_argument("--tiles", default="-1", help="many-row tiles to compare (nk_gemm_mx_tile: -1 policy, "
+                                                  "0 128x128, 1 64x128, 2 64x64), e.g. -1,2,1")
+    ap.add_argument("--ksplits", default="-1", help="residual K split modes to compare (nk_gemm_ksplit), e.g. -1,0,1")
     a = ap.parse_args()
     gpu = nemoasr.Gpu()
     print(f"device: {gpu.name}", flush=True)
@@ -232,8 +285,24 @@ def main():
         nemoasr.lib().nk_gemm_force(0)
         print(f"M={M:5d} f{force} chunk GEMMs (24 layers + prompt + joint.enc, no LN launches): {tot_us / 1e3:.3f} ms, "
               f"{tot_fl / (tot_us * 1e-6) / 1e12:.1f} TFLOP/s = {tot_fl / (tot_us * 1e-6) / 2.5e15:.3f} of peak", flush=True)
+    out["split"] = []
+    L = nemoasr.lib()
+    for M in [int(x) for x in a.split_rows.split(",") if x]:
+        for (label, N, K, act, kind) in SPLIT_SHAPES:
+            for tile in [int(t) for t in a.tiles.split(",")]:
+                for ks in ([int(k) for k in a.ksplits.split(",")] if kind == "r" else [-1]):
+                    L.nk_gemm_mx_tile(tile)
+                    L.nk_gemm_ksplit(ks)
+                    us, fl = bench_split(gpu, M, N, K, act, kind, 8, 64)
+                    tf = fl / (us * 1e-6) / 1e12
+                    out["split"].append({"M": M, "shape": label, "N": N, "K": K, "tile": tile, "ksplit": ks,
+                                         "kernel_us": round(us, 3), "tflops": round(tf, 1)})
+                    print(f"M={M:5d} {label:8s} tile {tile:2d} ksplit {ks:2d}  kernel {us:7.2f} us  {tf:6.1f} TFLOP/s "
+                          f"({tf / 2500:.3f} of 2.5 PF bf16)", flush=True)
+            L.nk_gemm_mx_tile(-1)
+            L.nk_gemm_ksplit(-1)
     out["rows"] = []
-    for c in [int(x) for x in a.rows.split(",") if int(x) <= 16]:
+    for c in [int(x) for x in a.rows.split(",") if 0 < int(x) <= 16]:
         for desc in (0, 1):
             us = bench_attention(gpu, c, 56, desc, 24, a.reps)
             out["rows"].append({"kernel": "attention_rel", "c": c, "cache": 56, "desc": desc, "graph_us": round(us, 3)})
