@@ -135,9 +135,19 @@ typedef struct {
 int nk_gemm_resid(gpu_t *g, const float *A, const uint16_t *A2, uint32_t lda, const uint16_t *W, uint32_t ldw, float *C,
                   uint32_t ldc, uint32_t M, uint32_t N, uint32_t K, float alpha, nk_resid_t *pend);
 int nk_resid_fold(gpu_t *g, float *C, uint32_t ldc, uint32_t M, uint32_t N, const nk_resid_t *pend);
+/* nk_gemm_ln on A with a pending residual update (pend, may be NULL or empty) applied first:
+ * Xf = A + alpha * (((0 + p0) + p1) + ...) (the bits of nk_resid_fold), and the GEMM's LayerNorm
+ * prologue reads Xf.  Xf (rows of lda floats, not A) receives the updated rows: the residual
+ * stream after the update.  The weight-streaming GEMV (M <= 4, K <= 1024) applies the update in its
+ * prologue, no extra launch; other kernels get a copy and an nk_resid_fold first.  Parts are
+ * [nparts][M][K] (part stride M * K). */
+int nk_gemm_ln_pend(gpu_t *g, const float *A, uint32_t lda, const uint16_t *W, uint32_t ldw, const float *bias,
+                    float *C, uint32_t ldc, const int *crow, uint32_t M, uint32_t N, uint32_t K, int act, int accumulate,
+                    float alpha, int ln_mode, const float *g1, const float *b1, const float *g2, const float *b2,
+                    float *ln_out, float *tmp, float eps, const nk_resid_t *pend, float *Xf);
 /* nk_gemm_split without any allocation.  No counterpart in the reference: it is for callers that
  * cannot allocate device memory (code under hipGraph capture, tight serving loops, harnesses that
- * forbid hipMalloc).  The split-K partial sums and arrival counters live in a static device array
+ * forbid hipMalloc).  The split-K partial sums live in a static device array
  * of NK_NOALLOC_WS_FLOATS floats per GPU (held until the process ends): the partial rows of a
  * residual update (at most NK_NOALLOC_WS_FLOATS = parts x M x N floats; a larger one is refused with
  * an error before any launch).  Every call on a GPU shares its array and overwrites what the last
@@ -175,12 +185,18 @@ int nk_attention_rel_desc(gpu_t *g, const float *kv, uint32_t ld, const int *des
 int nk_dwconv_ln_silu_desc(gpu_t *g, const float *din_base, const int *desc, const float *W, const float *gamma,
                            const float *beta, float *Y, uint32_t c, uint32_t D, uint32_t taps, float eps);
 /* Launch fusions of the single-stream chunk (descriptor window, c <= 4 rows):
- * C[i] += alpha * attention_i . Wo^T for the c rows (attention as nk_attention_rel_desc; each head's
- * share of the product is added atomically, so the sum order of the H shares varies); Wo [D][ldw]
- * bf16, D % 128 == 0.  Replaces nk_attention_rel_desc + nk_gemm(O, Wo, accumulate). */
+ * C[i] += alpha * attention_i . Wo^T for the c rows (attention as nk_attention_rel_desc); Wo [D][ldw]
+ * bf16, D % 128 == 0.  Each head's share of the product is written as a partial row and the H rows
+ * are added in head order: by an nk_resid_fold launch (nk_attention_out_desc), or left pending in
+ * *pend for the next LayerNorm-fused GEMM (nk_attention_out_desc_pend + nk_gemm_ln_pend).
+ * Replaces nk_attention_rel_desc + nk_gemm(O, Wo, accumulate). */
 int nk_attention_out_desc(gpu_t *g, const float *kv, uint32_t ld, const int *desc, const float *P, const float *bias_u,
                           const float *bias_v, uint32_t c, uint32_t Lmax, uint32_t H, uint32_t dh, uint32_t D,
                           float scale, const uint16_t *Wo, uint32_t ldw, float *C, uint32_t ldc, float alpha);
+int nk_attention_out_desc_pend(gpu_t *g, const float *kv, uint32_t ld, const int *desc, const float *P,
+                               const float *bias_u, const float *bias_v, uint32_t c, uint32_t Lmax, uint32_t H,
+                               uint32_t dh, uint32_t D, float scale, const uint16_t *Wo, uint32_t ldw, float alpha,
+                               nk_resid_t *pend);
 /* C[i][n] (= or +=) alpha * sum_k y_i[k] W[n][k] with y = SiLU(LN(dwconv(din))) of the c <= 2 rows
  * (as nk_dwconv_ln_silu_desc; 9 taps, D <= 1024, D % 8 == 0).  Bit-identical to that launch
  * followed by nk_gemm(y, W, no bias, no activation). */

@@ -287,16 +287,23 @@ static void run_blocks(encoder_t *e, int c) {
         nk_gemm_ln(g, res, D, W->wqkv, D, NULL, kv, 3 * D, rows, uc, 3 * D, D, NK_ACT_NONE, 0, 1.0f, 1, W->ln_att_g,
                    W->ln_att_b, NULL, NULL, NULL, lnbuf, eps);
         if (fuse_att) {
-            nk_attention_out_desc(g, kv, 3 * D, desc, W->ptab, W->bias_u, W->bias_v, uc, (uint32_t)e->Lmax, H, dh, D,
-                                  scale, W->wo, D, res, D, 1.0f);
+            /* the heads' partial rows stay pending; the conv module's LN-fused pw1 adds them to the
+             * residual in head order and writes the updated residual to the other buffer */
+            nk_resid_t pend;
+            nk_attention_out_desc_pend(g, kv, 3 * D, desc, W->ptab, W->bias_u, W->bias_v, uc, (uint32_t)e->Lmax, H, dh,
+                                       D, scale, W->wo, D, 1.0f, &pend);
+            cur ^= 1;
+            nk_gemm_ln_pend(g, res, D, W->pw1, D, NULL, din, D, rows, uc, 2 * D, D, NK_ACT_GLU, 0, 1.0f, 1,
+                            W->ln_conv_g, W->ln_conv_b, NULL, NULL, NULL, lnbuf, eps, &pend, R[cur]);
+            res = R[cur];
         } else {
             nk_attention_rel_desc(g, kv, 3 * D, desc, W->ptab, W->bias_u, W->bias_v, att, uc, (uint32_t)e->Lmax, H, dh,
                                   D, scale);
             nk_gemm(g, att, D, W->wo, D, NULL, res, D, uc, D, D, NK_ACT_NONE, 1, 1.0f);
+            /* convolution module: GLU output appended to the conv history, causal depthwise conv over it */
+            nk_gemm_ln(g, res, D, W->pw1, D, NULL, din, D, rows, uc, 2 * D, D, NK_ACT_GLU, 0, 1.0f, 1, W->ln_conv_g,
+                       W->ln_conv_b, NULL, NULL, NULL, lnbuf, eps);
         }
-        /* convolution module: GLU output appended to the conv history, causal depthwise conv over it */
-        nk_gemm_ln(g, res, D, W->pw1, D, NULL, din, D, rows, uc, 2 * D, D, NK_ACT_GLU, 0, 1.0f, 1, W->ln_conv_g,
-                   W->ln_conv_b, NULL, NULL, NULL, lnbuf, eps);
         if (fuse_conv) {
             nk_dwconv_pw_desc(g, din, desc, W->dw_w, W->bn_g, W->bn_b, eps, W->pw2, D, res, D, uc, D, D, 1, 1.0f);
         } else {

@@ -123,6 +123,8 @@ typedef struct {
     const float *g1, *b1, *g2, *b2;
     float *out, *tmp;
     float eps;
+    const nk_resid_t *pend; /* a pending residual update applied to A first (may be NULL) */
+    float *fold_out;        /* receives A with the update applied */
 } ln_pro_t;
 
 /* Many-row GEMM on the direct-to-LDS MFMA kernels (kernels/nk_mx.hip).  Tile choice: the largest
@@ -316,6 +318,19 @@ static int gemm_core(gpu_t *g, const float *A, uint32_t lda, const uint16_t *W, 
     const int kind = gpu_many_rows(g) && !g_force && K % 32 == 0 ? K_MR : pick(M, K, act);
     const int ln_fused = ln && ln->mode && K == lda &&
                          ((kind == K_GEMV && K <= 1024) || (kind == K_FR && K == 1024 && M <= 16));
+    const int fold = ln && ln->mode && ln->pend && ln->pend->nparts;
+    if (fold) {
+        if (!ln->fold_out || ln->fold_out == A || lda % 4) return bad(g, "gemm: a pending update needs its own output rows");
+        if (!(kind == K_GEMV && ln_fused && K % 4 == 0 && M <= 4)) {
+            /* kernels without the fold prologue: apply the update to a copy of A, then as usual */
+            if (nk_copy2d(g, A, lda, ln->fold_out, lda, M, K)) return -1;
+            if (nk_resid_fold(g, ln->fold_out, lda, M, K, ln->pend)) return -1;
+            ln_pro_t plain = *ln;
+            plain.pend = NULL;
+            plain.fold_out = NULL;
+            return gemm_core(g, ln->fold_out, lda, W, ldw, bias, C, ldc, crow, M, N, K, act, accumulate, alpha, &plain);
+        }
+    }
     if (ln && ln->mode && !ln_fused) {
         /* unfused LayerNorm: out = LN1(A) (if requested), tmp = LN(...) feeds the GEMM */
         if (!ln->tmp || K != lda) return bad(g, "gemm: LayerNorm prologue needs a scratch buffer");
@@ -351,7 +366,14 @@ static int gemm_core(gpu_t *g, const float *A, uint32_t lda, const uint16_t *W, 
         gemv_shape(N, K, act, &kch, &nc);
         const uint32_t per_wave = act == NK_ACT_GLU ? nc / 2 : nc;
         const uint32_t waves = (nout + per_wave - 1) / per_wave;
-        snprintf(name, sizeof name, "gemv_r%u_n%u_k%u", M, nc, kch);
+        if (fold) {
+            /* the workgroups apply the pending update to A in their prologue (gemv_*_f) */
+            a.fold = ln->pend->parts;
+            a.fold_n = ln->pend->nparts;
+            a.fold_alpha = ln->pend->alpha;
+            a.fold_out = ln->fold_out;
+        }
+        snprintf(name, sizeof name, "gemv_r%u_n%u_k%u%s", M, nc, kch, fold ? "_f" : "");
         return gpu_launch(g, name, &a, sizeof a, (waves + 3) / 4, 1, 1, 256, 1, 1);
     }
     if (K % 32) return bad(g, "gemm: K % 32 != 0 for the MFMA kernels");
@@ -407,8 +429,17 @@ int nk_gemm_ln(gpu_t *g, const float *A, uint32_t lda, const uint16_t *W, uint32
                uint32_t ldc, const int *crow, uint32_t M, uint32_t N, uint32_t K, int act, int accumulate, float alpha,
                int ln_mode, const float *g1, const float *b1, const float *g2, const float *b2, float *ln_out,
                float *tmp, float eps) {
-    const ln_pro_t ln = { ln_mode, g1, b1, g2, b2, ln_out, tmp, eps };
+    const ln_pro_t ln = { ln_mode, g1, b1, g2, b2, ln_out, tmp, eps, NULL, NULL };
     if (ln_mode < 0 || ln_mode > 2) return bad(g, "gemm: ln_mode must be 0, 1 or 2");
+    return gemm_core(g, A, lda, W, ldw, bias, C, ldc, crow, M, N, K, act, accumulate, alpha, &ln);
+}
+
+int nk_gemm_ln_pend(gpu_t *g, const float *A, uint32_t lda, const uint16_t *W, uint32_t ldw, const float *bias,
+                    float *C, uint32_t ldc, const int *crow, uint32_t M, uint32_t N, uint32_t K, int act, int accumulate,
+                    float alpha, int ln_mode, const float *g1, const float *b1, const float *g2, const float *b2,
+                    float *ln_out, float *tmp, float eps, const nk_resid_t *pend, float *Xf) {
+    const ln_pro_t ln = { ln_mode, g1, b1, g2, b2, ln_out, tmp, eps, pend, Xf };
+    if (ln_mode < 1 || ln_mode > 2) return bad(g, "gemm: a pending update needs a LayerNorm prologue (ln_mode 1 or 2)");
     return gemm_core(g, A, lda, W, ldw, bias, C, ldc, crow, M, N, K, act, accumulate, alpha, &ln);
 }
 
@@ -503,21 +534,32 @@ int nk_attention_out_desc(gpu_t *g, const float *kv, uint32_t ld, const int *des
                           const float *bias_v, uint32_t c, uint32_t Lmax, uint32_t H, uint32_t dh, uint32_t D,
                           float scale, const uint16_t *Wo, uint32_t ldw, float *C, uint32_t ldc, float alpha) {
     if (!c) return 0;
+    if (ldc % 4 || (uintptr_t)C % 16) return bad(g, "attention_out: C 16-byte aligned, ldc % 4 == 0");
+    nk_resid_t pend;
+    if (nk_attention_out_desc_pend(g, kv, ld, desc, P, bias_u, bias_v, c, Lmax, H, dh, D, scale, Wo, ldw, alpha, &pend))
+        return -1;
+    return nk_resid_fold(g, C, ldc, c, D, &pend);
+}
+
+int nk_attention_out_desc_pend(gpu_t *g, const float *kv, uint32_t ld, const int *desc, const float *P,
+                               const float *bias_u, const float *bias_v, uint32_t c, uint32_t Lmax, uint32_t H,
+                               uint32_t dh, uint32_t D, float scale, const uint16_t *Wo, uint32_t ldw, float alpha,
+                               nk_resid_t *pend) {
+    memset(pend, 0, sizeof *pend);
+    if (!c) return 0;
     if (dh != 128 || H * dh != D || c > 4 || c > Lmax || Lmax > NK_ATT_MAX_L || D % (8u * (uint32_t)g_attn_cpw))
         return bad(g, "attention_out: head_dim 128, c <= 4, D a multiple of the column tile");
-    if ((uintptr_t)kv % 16 || ld % 4 || !aligned16(Wo) || ldw % 8 || ldw < D || ldc < D)
-        return bad(g, "attention_out: aligned cache and weights, ldw and ldc >= D");
+    if ((uintptr_t)kv % 16 || ld % 4 || !aligned16(Wo) || ldw % 8 || ldw < D)
+        return bad(g, "attention_out: aligned cache and weights, ldw >= D");
     NkAttnOutArgs p;
     memset(&p, 0, sizeof p);
     p.at = (NkAttnArgs){ kv, kv + D, kv + 2 * D, P, bias_u, bias_v, NULL, desc, NULL, c, 0, Lmax, H, dh, D, ld, ld, scale, 0 };
     p.Wo = Wo;
-    p.C = C;
-    /* per-head partial rows [H][c][D], folded into C in head order by a second launch */
+    /* per-head partial rows [H][c][D]: the update C + alpha * (((0 + h0) + h1) + ...) is left pending */
     p.ws = gpu_scratch_ws(g, (size_t)c * D * H);
     if (!p.ws) return bad(g, "attention_out: scratch unavailable (size it before capture)");
-    if (ldc % 4 || (uintptr_t)C % 16) return bad(g, "attention_out: C 16-byte aligned, ldc % 4 == 0");
     p.ldw = ldw;
-    p.ldc = ldc;
+    p.ldc = D;
     p.alpha = alpha;
     gpu_next_bytes(g, 2.0 * D * D + 4.0 * 2 * c * D);
     gpu_next_flops(g, 2.0 * c * D * D);
@@ -525,8 +567,10 @@ int nk_attention_out_desc(gpu_t *g, const float *kv, uint32_t ld, const int *des
     char name[32];
     snprintf(name, sizeof name, "attention_rel_out_c%d", g_attn_cpw);
     if (gpu_launch(g, name, &p, sizeof p, H, D / cols, c, 512, 1, 1)) return -1;
-    const nk_resid_t pend = { p.ws, H, alpha };
-    return nk_resid_fold(g, C, ldc, c, D, &pend);
+    pend->parts = p.ws;
+    pend->nparts = H;
+    pend->alpha = alpha;
+    return 0;
 }
 
 int nk_dwconv_pw_desc(gpu_t *g, const float *din_base, const int *desc, const float *dw_w, const float *gamma,

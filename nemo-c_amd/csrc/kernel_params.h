@@ -80,6 +80,14 @@ typedef struct {
      * split rows of nout values to C2 instead of f32 to C (no accumulate, no row map). */
     const u16 *A2;
     u16 *C2;
+    /* weight-streaming GEMV with a LayerNorm prologue: with fold set, a pending residual update is
+     * applied to A first, x = A + fold_alpha * (((0 + P[0]) + P[1]) + ...) (fold_n parts of M rows of
+     * K floats, part stride M * K), by every workgroup into LDS; workgroup 0 also writes x to
+     * fold_out (rows of lda floats), the residual stream after the update */
+    const float *fold;
+    float *fold_out;
+    u32 fold_n;
+    float fold_alpha;
 } NkGemmArgs;
 
 typedef struct {

@@ -53,8 +53,11 @@ __device__ __forceinline__ void ld8(float (&d)[8], const float *p) {
     d[0] = x[0]; d[1] = x[1]; d[2] = x[2]; d[3] = x[3]; d[4] = y[0]; d[5] = y[1]; d[6] = y[2]; d[7] = y[3];
 }
 
-template <int R, int NC, int KCH>
-__device__ __forceinline__ void gemv_impl(const NkGemmArgs &a) {
+/* FOLD (K <= 1024, LayerNorm prologue): the activation rows are A plus a pending residual update,
+ * formed by the workgroup in xs (R rows of K floats) before the LayerNorm; the partial rows are
+ * loaded ahead of the weight stream, the sums finished after it is issued, one barrier. */
+template <int R, int NC, int KCH, bool FOLD = false>
+__device__ __forceinline__ void gemv_impl(const NkGemmArgs &a, float *xs = nullptr) {
     const u32 lane = threadIdx.x & 63;
     const u32 gw = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
     const bool glu = a.act == NK_ACT_GLU;
@@ -62,8 +65,27 @@ __device__ __forceinline__ void gemv_impl(const NkGemmArgs &a) {
     constexpr int NP = NC / 2 > 0 ? NC / 2 : 1; /* GLU output pairs per wavefront */
     const u32 per_wave = glu ? (u32)NP : (u32)NC;
     const u32 j0 = gw * per_wave;
-    if (j0 >= nout) return; /* uniform per wavefront; the kernel has no barriers */
+    /* uniform per wavefront; without FOLD the kernel has no barriers, with it the wavefronts past
+     * the end leave after the fold's barrier */
+    const bool live = j0 < nout;
+    if (!FOLD && !live) return;
     const u32 nch = a.K >> 3, M = a.M;
+
+    /* 0. FOLD: this thread's float4 column c4 = tid (K <= 1024) of every row: A and the parts */
+    constexpr int FP = 8; /* parts held in registers per pass */
+    floatx4 fa[FOLD ? R : 1], fp[FOLD ? R : 1][FOLD ? FP : 1];
+    const u32 c4 = threadIdx.x, k4 = a.K >> 2;
+    if constexpr (FOLD) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const u32 rr = (u32)r < M ? r : 0, cc = c4 < k4 ? c4 : 0;
+            fa[r] = ((const floatx4 *)(a.A + (u64)rr * a.lda))[cc];
+#pragma unroll
+            for (int h = 0; h < FP; ++h)
+                fp[r][h] = (u32)h < a.fold_n ? ((const floatx4 *)(a.fold + ((u64)h * M + rr) * a.K))[cc]
+                                            : (floatx4){ 0.f, 0.f, 0.f, 0.f };
+        }
+    }
 
     /* 1. epilogue row map and bias: lane e < M*outputs owns output (r = e / per_wave, column
      *    j0 + e % per_wave); other lanes read a clamped (valid) entry and store nothing */
@@ -76,13 +98,15 @@ __device__ __forceinline__ void gemv_impl(const NkGemmArgs &a) {
 
     /* 2. activation chunks (rows past M read row 0) and LayerNorm parameters */
     float x[R][KCH][8];
+    if constexpr (!FOLD) {
 #pragma unroll
-    for (int r = 0; r < R; ++r)
+        for (int r = 0; r < R; ++r)
 #pragma unroll
-        for (int q = 0; q < KCH; ++q) {
-            const u32 j = min(lane + 64 * q, nch - 1);
-            ld8(x[r][q], a.A + (u64)((u32)r < M ? r : 0) * a.lda + 8 * j);
-        }
+            for (int q = 0; q < KCH; ++q) {
+                const u32 j = min(lane + 64 * q, nch - 1);
+                ld8(x[r][q], a.A + (u64)((u32)r < M ? r : 0) * a.lda + 8 * j);
+            }
+    }
     float g1[KCH <= 2 ? KCH : 1][8], b1[KCH <= 2 ? KCH : 1][8], g2[KCH <= 2 ? KCH : 1][8], b2[KCH <= 2 ? KCH : 1][8];
     if constexpr (KCH <= 2) {
         if (a.ln_mode) {
@@ -103,6 +127,7 @@ __device__ __forceinline__ void gemv_impl(const NkGemmArgs &a) {
     uint4 w[NC][KCH];
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
+        if (FOLD && !live) break;
         u32 row;
         if (glu) row = (c < NP) ? j0 + c : j0 + (c - NP) + a.N / 2;
         else row = j0 + c;
@@ -116,7 +141,40 @@ __device__ __forceinline__ void gemv_impl(const NkGemmArgs &a) {
 
     /* 4. the C value to accumulate into */
     float *e_dst = a.C + (u64)(u32)e_row * a.ldc + ecol_c;
-    const float e_c = a.accumulate ? *e_dst : 0.0f;
+    const float e_c = a.accumulate && live ? *e_dst : 0.0f;
+
+    if constexpr (FOLD) {
+        /* x = A + alpha * (((0 + p0) + p1) + ...), the order and form of resid_fold; parts past
+         * FP are read here (after the weight stream is issued) */
+        if (c4 < k4) {
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                if ((u32)r >= M) break;
+                floatx4 t = { 0.f, 0.f, 0.f, 0.f };
+#pragma unroll
+                for (int h = 0; h < FP; ++h)
+                    if ((u32)h < a.fold_n) { t.x += fp[r][h].x; t.y += fp[r][h].y; t.z += fp[r][h].z; t.w += fp[r][h].w; }
+                for (u32 h = FP; h < a.fold_n; ++h) {
+                    const floatx4 q = ((const floatx4 *)(a.fold + ((u64)h * M + r) * a.K))[c4];
+                    t.x += q.x; t.y += q.y; t.z += q.z; t.w += q.w;
+                }
+                floatx4 v = fa[r];
+                v.x = v.x + t.x * a.fold_alpha; v.y = v.y + t.y * a.fold_alpha;
+                v.z = v.z + t.z * a.fold_alpha; v.w = v.w + t.w * a.fold_alpha;
+                ((floatx4 *)(xs + r * 1024))[c4] = v;
+                if (blockIdx.x == 0) ((floatx4 *)(a.fold_out + (u64)r * a.lda))[c4] = v;
+            }
+        }
+        __syncthreads();
+        if (!live) return;
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int q = 0; q < KCH; ++q) {
+                const u32 j = min(lane + 64 * q, nch - 1);
+                ld8(x[r][q], xs + ((u32)r < M ? r : 0) * 1024 + 8 * j);
+            }
+    }
 
     /* chunks past the row contribute nothing (selects, so no register is rewritten while its
      * load is in flight) */
@@ -217,3 +275,15 @@ GEMV2_R(1)
 GEMV2_R(2)
 GEMV2_SMALLK(3)
 GEMV2_SMALLK(4)
+
+/* the FOLD variants (suffix _f): K <= 1024 with the LayerNorm prologue */
+#define GEMV2F(R, NC, KCH)                                                                              \
+    extern "C" __global__ __launch_bounds__(256) void gemv_r##R##_n##NC##_k##KCH##_f(const NkGemmArgs a) { \
+        __shared__ float xs[R * 1024];                                                                  \
+        gemv_impl<R, NC, KCH, true>(a, xs);                                                             \
+    }
+#define GEMV2F_R(R) GEMV2F(R, 1, 1) GEMV2F(R, 2, 1) GEMV2F(R, 4, 1) GEMV2F(R, 1, 2) GEMV2F(R, 2, 2) GEMV2F(R, 4, 2)
+GEMV2F_R(1)
+GEMV2F_R(2)
+GEMV2F_R(3)
+GEMV2F_R(4)

@@ -241,3 +241,52 @@ def test_resid_pending_folded_by_layernorm(gpu, M, K, split_in, paired):
             assert np.array_equal(bits(y1), bits(out[2][2]))
     ref = oracle.gemm(A, W, None, 0, True, 0.5, C0=X)
     assert rel_err(out[2][0], ref) < 2e-5
+
+
+@pytest.mark.parametrize("M,nparts,N,act,mode", [(1, 8, 2048, 3, 1), (2, 8, 2048, 3, 1), (4, 8, 2048, 3, 1),
+                                                 (3, 3, 4096, 1, 2), (1, 11, 3072, 0, 1), (7, 8, 2048, 3, 1)])
+def test_gemm_ln_pending_fold_bits(gpu, M, nparts, N, act, mode):
+    """A pending residual update (partial rows, e.g. the fused attention's eight heads) applied by the
+    LayerNorm-fused GEMM that reads the residual next (nk_gemm_ln_pend: inside the GEMV prologue for
+    M <= 4; a copy and nk_resid_fold first otherwise) gives, bit for bit, the updated residual and
+    the outputs of nk_resid_fold followed by nk_gemm_ln; the input rows are left as they were."""
+    import ctypes as C
+
+    import nemoasr
+
+    L = nemoasr.lib()
+    K = 1024
+    rng = np.random.default_rng([M, nparts, N, 31])
+    X = rng.standard_normal((M, K)).astype(np.float32)
+    P = (0.3 * rng.standard_normal((nparts, M, K))).astype(np.float32)
+    W = w_bf16(rng, N, K)
+    g1, g2 = [(1 + 0.1 * rng.standard_normal(K)).astype(np.float32) for _ in range(2)]
+    b1, b2 = [(0.1 * rng.standard_normal(K)).astype(np.float32) for _ in range(2)]
+    nout = N // 2 if act == 3 else N
+    dW, dP, dg1, db1, dg2, db2 = (gpu.put(a) for a in (W, P, g1, b1, g2, b2))
+    tmp = gpu.alloc(M * K * 4)
+    pend = nemoasr.Resid(dP.ptr, nparts, 0.75)
+    ln2 = (dg2.ptr, db2.ptr) if mode == 2 else (None, None)
+    outs = []
+    for fused in (False, True):
+        dX, dXf, dC, dL1 = gpu.put(X), gpu.alloc(M * K * 4), gpu.alloc(M * nout * 4), gpu.alloc(M * K * 4)
+        gpu.begin()
+        if fused:
+            gpu.check(L.nk_gemm_ln_pend(gpu.h, dX.ptr, K, dW.ptr, K, None, dC.ptr, nout, None, M, N, K, act, 0, 1.0,
+                                        mode, dg1.ptr, db1.ptr, *ln2, dL1.ptr if mode == 2 else None, tmp.ptr, 1e-5,
+                                        C.byref(pend), dXf.ptr))
+        else:
+            gpu.check(L.nk_copy(gpu.h, dX.ptr, dXf.ptr, M * K))
+            gpu.check(L.nk_resid_fold(gpu.h, dXf.ptr, K, M, K, C.byref(pend)))
+            gpu.check(L.nk_gemm_ln(gpu.h, dXf.ptr, K, dW.ptr, K, None, dC.ptr, nout, None, M, N, K, act, 0, 1.0, mode,
+                                   dg1.ptr, db1.ptr, *ln2, dL1.ptr if mode == 2 else None, tmp.ptr, 1e-5))
+        gpu.end()
+        outs.append((dX.read((M, K)), dXf.read((M, K)), dC.read((M, nout)), dL1.read((M, K)) if mode == 2 else None))
+    (x0, xf0, c0, l0), (x1, xf1, c1, l1) = outs
+    assert np.array_equal(bits(x1), bits(X))
+    assert np.array_equal(bits(xf1), bits(xf0))
+    assert np.array_equal(bits(c1), bits(c0))
+    if mode == 2:
+        assert np.array_equal(bits(l1), bits(l0))
+    ref = X + np.float32(0.75) * P.sum(axis=0, dtype=np.float64).astype(np.float32)
+    assert rel_err(xf1, ref) < 1e-6
