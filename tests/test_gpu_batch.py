@@ -312,3 +312,22 @@ def test_batch_skewed_auto_full():
     st = b.stats()
     assert 0 < st["tokens"] < st["rows"] * om.dims.max_symbols, st
     b.close()
+
+
+def test_batch_single_stream_and_empty_steps():
+    """A batch of one stream equals the oracle; steps with nothing ready (before any push, after
+    the end) run nothing and return 0."""
+    import nemoasr
+
+    mdir = model_dir("tiny")
+    b = nemoasr.Batch(mdir, "en-US", 560, 1)
+    assert b.step() == 0 and b.run() == 0
+    audio = synth.make_audio(2.0, seed=47)
+    om = oracle.Model(mdir, "en-US")
+    o = oracle.Session(om, 6)
+    o.feed_mel(mel_ref.logmel(audio), final=True)
+    b.push(0, audio, final=True)
+    b.run()
+    check_tokens(b.tokens(0), o.tokens, o.token_margins())
+    assert b.step() == 0 and b.stats()["chunks"] == o.chunks
+    b.close()

@@ -259,3 +259,93 @@ def test_full_skewed_stream_1120(graphs):
     frames, toks = o.frames, len(o.tokens)
     assert 0 < toks < frames * om.dims.max_symbols, (frames, toks)
     s.close()
+
+
+def _oracle_audio_tokens(mdir, audio16, latency):
+    om = oracle.Model(mdir, "en-US")
+    o = oracle.Session(om, LAT_RIGHT[latency])
+    o.feed_mel(mel_ref.logmel(audio16), final=True)
+    return o
+
+
+@pytest.mark.parametrize("latency", [80, 560])
+def test_api_ragged_and_empty_feeds(latency):
+    """nemoasr_feed with empty calls (before, between, and as the final flush) and ragged piece sizes
+    (1 sample up to several chunks) decodes exactly what one whole-clip call decodes, and the
+    oracle's tokens (src/nemoasr.c:134-160: audio is queued and every ready chunk runs)."""
+    import nemoasr
+
+    mdir = model_dir("tiny")
+    audio = synth.make_audio(2.3, seed=41)
+    o = _oracle_audio_tokens(mdir, audio, latency)
+    whole = nemoasr.Session(mdir, "en-US", latency)
+    whole.feed(audio, final=True)
+    rng = np.random.default_rng(latency)
+    s = nemoasr.Session(mdir, "en-US", latency)
+    assert s.feed(np.zeros(0, np.float32)) in ("", None)
+    assert s.stats()["chunks"] == 0 and s.tokens() == []
+    pos = 0
+    while pos < audio.size:
+        n = int(rng.choice([1, 7, 160, 1279, 1280, 1281, 4000, 17000]))
+        s.feed(audio[pos:pos + n])
+        if rng.random() < 0.2:
+            s.feed(np.zeros(0, np.float32))
+        pos += n
+    s.feed(np.zeros(0, np.float32), final=True)  # the final flush carries no samples
+    assert s.tokens() == whole.tokens()
+    assert s.stats()["chunks"] == whole.stats()["chunks"] == o.chunks
+    check_tokens(s.tokens(), o.tokens, o.token_margins())
+    s.close()
+    whole.close()
+
+
+@pytest.mark.parametrize("seconds", [0.05, 0.2, 0.6])
+def test_api_clip_shorter_than_a_chunk(seconds):
+    """Clips shorter than one 560 ms chunk: the final flush runs the partial window (the
+    boundary rule of src/encoder.c) and decodes what the oracle decodes, including nothing."""
+    import nemoasr
+
+    mdir = model_dir("tiny")
+    audio = synth.make_audio(seconds, seed=43)
+    o = _oracle_audio_tokens(mdir, audio, 560)
+    s = nemoasr.Session(mdir, "en-US", 560)
+    s.feed(audio, final=True)
+    check_tokens(s.tokens(), o.tokens, o.token_margins())
+    assert s.stats()["chunks"] == o.chunks
+    s.close()
+
+
+def _product_resample(x, rate):
+    """The library's streaming resampler (pinned against the reference's src/resample.c on the CPU)."""
+    import ctypes as C
+
+    import nemoasr
+
+    L = nemoasr.lib()
+    r = L.rsmp_create(rate, 16000)
+    buf = np.zeros(x.size * 16000 // rate + 4096, np.float32)
+    x = np.ascontiguousarray(x, np.float32)
+    fp = C.POINTER(C.c_float)
+    k = L.rsmp_process(r, x.ctypes.data_as(fp), x.size, buf.ctypes.data_as(fp), buf.size)
+    k2 = L.rsmp_flush(r, buf[k:].ctypes.data_as(fp), buf.size - k)
+    L.rsmp_destroy(r)
+    return buf[:k + k2].copy()
+
+
+@pytest.mark.parametrize("rate", [8000, 48000])
+def test_api_input_rate(rate):
+    """A session opened at another input rate resamples to 16 kHz on the host (src/nemoasr.c:66-87
+    and :134-160) and decodes what the oracle decodes from the resampled samples."""
+    import nemoasr
+
+    mdir = model_dir("tiny")
+    t = np.arange(int(2.0 * rate)) / rate
+    audio = (0.05 * np.sin(2 * np.pi * 440 * t) + 0.02 * np.random.default_rng(rate).standard_normal(t.size))
+    audio = audio.astype(np.float32)
+    o = _oracle_audio_tokens(mdir, _product_resample(audio, rate), 560)
+    s = nemoasr.Session(mdir, "en-US", 560, input_rate=rate)
+    for i in range(0, audio.size, rate // 10):
+        s.feed(audio[i:i + rate // 10], final=i + rate // 10 >= audio.size)
+    check_tokens(s.tokens(), o.tokens, o.token_margins())
+    assert s.stats()["chunks"] == o.chunks
+    s.close()
