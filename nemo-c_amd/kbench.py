@@ -216,6 +216,26 @@ def bench_split(gpu, M, N, K, act, kind, copies, launches):
     return ms.value * 1e3, fl / max(cnt.value, 1)
 
 
+def bench_floor(gpu, copies, reps):
+    """The launch floor under both timings: a 256-float copy (one workgroup) replayed in a graph
+    (graph_us) and timed by dispatch-stamped events around each direct launch (kernel_us), the
+    method of bench.py's roofline; the fixed cost every GEMV measurement above includes."""
+    L = nemoasr.lib()
+    src, dst = gpu.alloc(1024 * copies), gpu.alloc(1024 * copies)
+    gus = graph_us(gpu, lambda i: L.nk_copy(gpu.h, src.at(1024 * i), dst.at(1024 * i), 256), copies, reps)
+    L.gpu_timing_set(gpu.h, b"copy_f32", 4096)
+    gpu.begin()
+    for i in range(copies * 4):
+        gpu.check(L.nk_copy(gpu.h, src.at(1024 * (i % copies)), dst.at(1024 * (i % copies)), 256))
+    gpu.end()
+    ms, cnt, by = C.c_double(), C.c_int(), C.c_double()
+    L.gpu_timing_collect(gpu.h, C.byref(ms), C.byref(cnt), C.byref(by))
+    L.gpu_timing_set(gpu.h, None, 0)
+    src.free()
+    dst.free()
+    return gus, ms.value * 1e3
+
+
 def bench_copy(gpu, nbytes, reps):
     L = nemoasr.lib()
     n = nbytes // 4
@@ -251,6 +271,9 @@ def main():
     cu = bench_copy(gpu, cb, a.reps)
     out["copy"] = {"bytes": cb, "us": cu, "gbs_rw": 2 * cb / (cu * 1e-6) / 1e9}
     print(f"copy {cb >> 20} MiB: {cu:.1f} us, {2 * cb / (cu * 1e-6) / 1e9:.0f} GB/s read+write", flush=True)
+    fg, fk = bench_floor(gpu, 48, a.reps)
+    out["floor"] = {"graph_us": round(fg, 3), "kernel_us": round(fk, 3)}
+    print(f"launch floor (1 KB copy): graph {fg:7.2f} us  kernel {fk:7.2f} us", flush=True)
     for M in ([] if a.no_gemm else [int(x) for x in a.rows.split(",")]):
         for (label, N, K, act, acc, alpha, ln, ldw, hb) in SHAPES:
             if label == "lstm" and M > 1:
