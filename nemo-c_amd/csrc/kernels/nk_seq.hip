@@ -107,7 +107,8 @@ __device__ __forceinline__ void ln_row64(float4 (&v)[4], const float4 (&g)[4], c
  * row's arithmetic is ln_row64's, so every R gives the same bits. */
 template <int R>
 __device__ __forceinline__ void layernorm_rows_impl(const NkLnArgs &a) {
-    const u32 lane = threadIdx.x & 63, r0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * R, D4 = a.D >> 2;
+    const u32 lane = threadIdx.x & 63, D4 = a.D >> 2;
+    const u32 r0 = (blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6)) * R;
     if (r0 >= a.M) return; /* uniform per wavefront; no barriers */
     float4 v[R][4], g1[4], b1[4], g2[4], b2[4];
     const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
