@@ -104,8 +104,9 @@ int nk_gemm_ksplit(int mode);
 /* Many-row tile: -1 (default) by tile count, else 0 128x128, 1 64x128, 2 64x64 where it divides
  * the output columns.  Returns the previous setting. */
 int nk_gemm_mx_tile(int t);
-/* Few-row residual updates (5..16 rows): 1 (default) splits K over four workgroups with an ordered
- * combine, 0 keeps K in one workgroup (more wavefronts).  Returns the previous setting. */
+/* Few-row residual updates (5..16 rows): 1 (default) splits K over four workgroups whose partial
+ * rows are added in split order by a second launch, 0 keeps K in one workgroup (more wavefronts).
+ * Returns the previous setting. */
 int nk_gemm_fr_ksplit(int on);
 /* Kernel selection: 0 automatic (by row count), 1 first-generation VALU GEMV (M <= 4),
  * 2 few-row MFMA (M <= 16), 3 many-row MFMA, 4 weight-streaming GEMV (M <= 4),

@@ -46,9 +46,9 @@ static int aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 enum { K_FR = 2, K_MR = 3, K_GEMV = 4, K_MM_OLD = 5 };
 
 /* few-row MFMA kernel plan: W wavefronts of SPW K steps (32 wide) per workgroup, K split over KS
- * workgroups (KS > 1 only for accumulating GEMMs with no bias and no activation, whose partial
- * products are added into C atomically; it puts four times as many workgroups on the small-N
- * matrices). */
+ * workgroups (KS > 1 only for accumulating GEMMs with no bias and no activation, whose shares are
+ * written as partial rows and added into C in share order by resid_fold; it puts four times as
+ * many workgroups on the small-N matrices). */
 typedef struct { uint32_t W, SPW, KS; } fr_plan_t;
 
 static int fr_ok(uint32_t M, uint32_t K, int act) {
