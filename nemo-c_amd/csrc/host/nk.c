@@ -319,6 +319,14 @@ static int gemm_core(gpu_t *g, const float *A, uint32_t lda, const uint16_t *W, 
     const int ln_fused = ln && ln->mode && K == lda &&
                          ((kind == K_GEMV && K <= 1024) || (kind == K_FR && K == 1024 && M <= 16));
     const int fold = ln && ln->mode && ln->pend && ln->pend->nparts;
+    if (ln && ln->mode && ln->fold_out && !fold) {
+        /* nothing pending: the output rows are A itself */
+        if (ln->fold_out == A || lda % 4) return bad(g, "gemm: a pending update needs its own output rows");
+        if (nk_copy2d(g, A, lda, ln->fold_out, lda, M, K)) return -1;
+        ln_pro_t plain = *ln;
+        plain.fold_out = NULL;
+        return gemm_core(g, ln->fold_out, lda, W, ldw, bias, C, ldc, crow, M, N, K, act, accumulate, alpha, &plain);
+    }
     if (fold) {
         if (!ln->fold_out || ln->fold_out == A || lda % 4) return bad(g, "gemm: a pending update needs its own output rows");
         if (!(kind == K_GEMV && ln_fused && K % 4 == 0 && M <= 4)) {
