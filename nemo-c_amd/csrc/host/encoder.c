@@ -370,6 +370,8 @@ int encoder_step(encoder_t *e, int final, enc_out_t *out, char *err, size_t errl
     e->closed = b.closed;
     if (!p.ran) return 0;
     const double t0 = now_ms();
+    /* the previous step's uploads read the pinned staging: wait for them before rewriting it */
+    gpu_wait_deferred(e->g);
     /* window = mel cache ++ the consumed rows, written into pinned staging */
     float *w = e->stage_win;
     memcpy(w, e->mel_cache, (size_t)cache_before * MEL_NMEL * sizeof(float));
@@ -421,7 +423,7 @@ int encoder_step(encoder_t *e, int final, enc_out_t *out, char *err, size_t errl
     }
     e->pos += c;
     e->cache_len = L < e->left ? L : e->left;
-    if (gpu_end(g, err, errlen)) return -1;
+    if (e->dump ? gpu_end(g, err, errlen) : gpu_end_nowait(g, err, errlen)) return -1;
     if (e->dump) {
         const model_cfg_t *cf = &e->m->cfg;
         const size_t D = (size_t)cf->d_model, nl = (size_t)cf->n_layers, J = (size_t)cf->joint_hidden;
@@ -439,7 +441,9 @@ int encoder_step(encoder_t *e, int final, enc_out_t *out, char *err, size_t errl
     out->frames = c;
     out->prompted = gpu_buf_dptr(e->prompted);
     out->joint_enc = gpu_buf_dptr(e->joint_enc);
-    out->gpu_ms = gpu_last_ms(g);
+    out->gpu_ms = e->dump ? gpu_last_ms(g) : 0.0;
     out->wall_ms = now_ms() - t0;
     return 1;
 }
+
+double encoder_take_gpu_ms(encoder_t *e) { return gpu_wait_deferred(e->g); }

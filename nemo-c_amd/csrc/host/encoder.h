@@ -20,8 +20,12 @@ int encoder_right(const encoder_t *e);
 int encoder_chunk_frames(const encoder_t *e);
 int encoder_chunk_mel(const encoder_t *e);
 void encoder_push(encoder_t *e, const float *mel, size_t nframes);
-/* 1: a piece was consumed (out->frames may be 0); 0: nothing to do; -1: error in err */
+/* 1: a piece was consumed (out->frames may be 0); 0: nothing to do; -1: error in err.
+ * Unless dumps are on, the step's GPU work is queued without waiting for it (the decoder's work
+ * queues behind it on the same stream): out->gpu_ms is then 0 and encoder_take_gpu_ms returns the
+ * step's GPU time, waiting for it. */
 int encoder_step(encoder_t *e, int final, enc_out_t *out, char *err, size_t errlen);
+double encoder_take_gpu_ms(encoder_t *e);
 
 /* Replay each chunk shape as a captured hipGraph (default on). */
 void encoder_use_graphs(encoder_t *e, int on);

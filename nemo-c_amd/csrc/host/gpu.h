@@ -61,6 +61,12 @@ int gpu_begin(gpu_t *g);
 int gpu_launch(gpu_t *g, const char *kernel, const void *args, size_t args_size,
                uint32_t gx, uint32_t gy, uint32_t gz, uint32_t bx, uint32_t by, uint32_t bz);
 int gpu_end(gpu_t *g, char *err, size_t errlen);
+/* End the batch without waiting for it: later work on the stream queues behind it at once.  The
+ * host must not reuse what the batch reads from host memory (pinned staging) before
+ * gpu_wait_deferred, which waits for that batch and returns its GPU time in ms (0 when none is
+ * pending).  Launch errors already recorded are reported here, execution errors by the next end. */
+int gpu_end_nowait(gpu_t *g, char *err, size_t errlen);
+double gpu_wait_deferred(gpu_t *g);
 double gpu_last_ms(gpu_t *g);
 const char *gpu_last_error(gpu_t *g);
 int gpu_sync(gpu_t *g);

@@ -26,6 +26,8 @@ struct gpu {
     hipModule_t mod;
     hipStream_t stream;
     hipEvent_t ev0, ev1;
+    hipEvent_t evd0, evd1; /* the bracket of a batch ended without waiting (gpu_end_nowait) */
+    int deferred;
     double last_ms;
     int in_batch, capturing, failed;
     int many_rows;
@@ -91,7 +93,8 @@ gpu_t *gpu_create(char *err, size_t errlen) {
         return NULL;
     }
     if ((e = hipStreamCreateWithFlags(&g->stream, hipStreamNonBlocking)) != hipSuccess ||
-        (e = hipEventCreate(&g->ev0)) != hipSuccess || (e = hipEventCreate(&g->ev1)) != hipSuccess) {
+        (e = hipEventCreate(&g->ev0)) != hipSuccess || (e = hipEventCreate(&g->ev1)) != hipSuccess ||
+        (e = hipEventCreate(&g->evd0)) != hipSuccess || (e = hipEventCreate(&g->evd1)) != hipSuccess) {
         snprintf(err, errlen, "stream/event: %s", hipGetErrorString(e));
         hipModuleUnload(g->mod);
         free(g);
@@ -133,6 +136,8 @@ void gpu_destroy(gpu_t *g) {
     if (g->zeros) hipFree(g->zeros);
     hipEventDestroy(g->ev0);
     hipEventDestroy(g->ev1);
+    hipEventDestroy(g->evd0);
+    hipEventDestroy(g->evd1);
     hipStreamDestroy(g->stream);
     hipModuleUnload(g->mod);
     free(g);
@@ -395,6 +400,32 @@ int gpu_end(gpu_t *g, char *err, size_t errlen) {
         return -1;
     }
     return 0;
+}
+
+int gpu_end_nowait(gpu_t *g, char *err, size_t errlen) {
+    if (g->deferred) gpu_wait_deferred(g); /* one deferred bracket at a time */
+    hipError_t e = hipEventRecord(g->ev1, g->stream);
+    if (e != hipSuccess) fail(g, "end", e);
+    g->in_batch = 0;
+    if (g->failed) {
+        if (errlen) snprintf(err, errlen, "gpu: %s", g->err);
+        return -1;
+    }
+    hipEvent_t t0 = g->evd0, t1 = g->evd1;
+    g->evd0 = g->ev0;
+    g->evd1 = g->ev1;
+    g->ev0 = t0;
+    g->ev1 = t1;
+    g->deferred = 1;
+    return 0;
+}
+
+double gpu_wait_deferred(gpu_t *g) {
+    if (!g->deferred) return 0.0;
+    g->deferred = 0;
+    float ms = 0.0f;
+    if (hipEventSynchronize(g->evd1) != hipSuccess || hipEventElapsedTime(&ms, g->evd0, g->evd1) != hipSuccess) return 0.0;
+    return ms;
 }
 
 int gpu_capture_begin(gpu_t *g) {

@@ -256,9 +256,16 @@ static int drain_chunks(nemoasr_t *s, int final, char *err, size_t errlen) {
         const int rc = encoder_step(s->enc, final, &o, err, errlen);
         if (rc < 0) return -1;
         if (rc == 0) return fresh;
-        if (o.frames <= 0) continue;
+        if (o.frames <= 0) {
+            o.gpu_ms += encoder_take_gpu_ms(s->enc);
+            continue;
+        }
+        /* the decoder's work queues behind the encoder's on the stream; its wall time includes
+         * the wait for the encoder, whose GPU time is moved to the encoder's account */
         const double t0 = clock_ms();
         const int n = decoder_run(s->dec, o.joint_enc, o.frames, s->ids, TOKENS_PER_CHUNK_MAX, err, errlen);
+        const double enc_gpu = encoder_take_gpu_ms(s->enc);
+        o.gpu_ms += enc_gpu;
         if (n < 0) return -1;
         if (reserve((void **)&s->rec.ids, &s->rec.capids, s->rec.nids + (size_t)n, sizeof(int)) ||
             reserve((void **)&s->rec.chunk_ms, &s->rec.capchunk, s->rec.nchunk + 1, sizeof(double))) {
@@ -277,8 +284,9 @@ static int drain_chunks(nemoasr_t *s, int final, char *err, size_t errlen) {
         s->rec.enc_gpu_ms += o.gpu_ms;
         s->stats.chunks += 1;
         s->stats.tokens += (size_t)n;
-        s->stats.encoder_ms += o.wall_ms;
-        s->stats.decoder_ms += decoder_last_ms(s->dec);
+        const double dec_ms = decoder_last_ms(s->dec);
+        s->stats.encoder_ms += o.wall_ms + (enc_gpu < dec_ms ? enc_gpu : dec_ms);
+        s->stats.decoder_ms += dec_ms > enc_gpu ? dec_ms - enc_gpu : 0.0;
         fresh += n;
     }
 }
