@@ -3,7 +3,7 @@
  * The loop is the reference's (src/decoder.c:92-127): committed and provisional LSTM states, the
  * joint evaluated for up to 16 remaining frames per step with the current prediction (speculating
  * blank), and on the first non-blank: emit, commit the provisional state, redo the later frames.
- * It runs on the device (kernels/nk_dec.hip): one step is four launches, a graph holds a run of
+ * It runs on the device (kernels/nk_dec.hip): one step is three launches, a graph holds a run of
  * steps, and the host replays graphs until the device state says the chunk is done.  The host
  * reads back the state and the emitted tokens once per graph, not once per joint evaluation. */
 #include "decoder.h"
@@ -32,7 +32,7 @@ typedef struct {
 struct decoder {
     model_t *m;
     gpu_t *g;
-    gpu_buf_t *st, *part, *tokens, *hc, *pred, *tx;
+    gpu_buf_t *st, *part, *tokens, *hc, *pre0, *pred, *tx;
     NkDecState *host_st; /* pinned: chunk fields in, final state out */
     int *host_tok;       /* pinned: tokens of the chunk               */
     dgraph_t gr[2];
@@ -51,6 +51,7 @@ decoder_t *decoder_create(model_t *m) {
     d->part = gpu_buf_alloc(d->g, 2 * NK_DEC_MAX_BATCH * NK_DEC_GROUPS * sizeof(unsigned long long));
     d->tokens = gpu_buf_alloc(d->g, NK_DEC_MAX_TOKENS * sizeof(int));
     d->hc = gpu_buf_alloc(d->g, 2 * 4 * P * sizeof(float));
+    d->pre0 = gpu_buf_alloc(d->g, 2 * 4 * P * sizeof(float));
     d->pred = gpu_buf_alloc(d->g, J * sizeof(float));
     d->host_st = gpu_host_alloc(d->g, sizeof(NkDecState));
     d->host_tok = gpu_host_alloc(d->g, NK_DEC_MAX_TOKENS * sizeof(int));
@@ -81,18 +82,20 @@ static void free_graphs(decoder_t *d) {
 void decoder_destroy(decoder_t *d) {
     if (!d) return;
     free_graphs(d);
-    gpu_buf_t *bufs[] = { d->st, d->part, d->tokens, d->hc, d->pred, d->tx };
+    gpu_buf_t *bufs[] = { d->st, d->part, d->tokens, d->hc, d->pre0, d->pred, d->tx };
     for (size_t i = 0; i < sizeof bufs / sizeof *bufs; ++i) gpu_buf_free(bufs[i]);
     gpu_host_free(d->host_st);
     gpu_host_free(d->host_tok);
     free(d);
 }
 
-/* src/decoder.c:48-53: zero LSTM state, last token blank, no valid prediction */
+/* src/decoder.c:48-53: zero LSTM state (so Wh0 . h0 is zero too), last token blank, no valid
+ * prediction */
 void decoder_reset(decoder_t *d) {
     const size_t P = (size_t)d->m->cfg.pred_hidden;
     float *z = calloc(2 * 4 * P, sizeof(float));
     gpu_upload(d->g, gpu_buf_dptr(d->hc), z, 2 * 4 * P * sizeof(float));
+    gpu_upload(d->g, gpu_buf_dptr(d->pre0), z, 2 * 4 * P * sizeof(float));
     free(z);
     NkDecState s[2];
     memset(s, 0, sizeof s);
@@ -118,6 +121,7 @@ static NkDecArgs dec_args(decoder_t *d, const float *enc, uint32_t parity, uint3
     a.wx0 = m->lstm_wx[0]; a.wh0 = m->lstm_wh[0]; a.wx1 = m->lstm_wx[1]; a.wh1 = m->lstm_wh[1];
     a.b0 = m->lstm_b[0]; a.b1 = m->lstm_b[1];
     a.hc = gpu_buf_dptr(d->hc);
+    a.pre0 = gpu_buf_dptr(d->pre0);
     a.wjp = m->joint_pred_w; a.bjp = m->joint_pred_b;
     a.pred = gpu_buf_dptr(d->pred);
     a.wout = m->joint_out_w; a.bout = m->joint_out_b;
@@ -140,9 +144,8 @@ static int launch_steps(decoder_t *d, const float *enc, int steps) {
     const uint32_t P = (uint32_t)d->m->cfg.pred_hidden, J = (uint32_t)d->m->cfg.joint_hidden;
     for (int j = 0; j <= steps; ++j) {
         const NkDecArgs a = dec_args(d, enc, (uint32_t)j & 1u, j == steps);
-        if (gpu_launch(g, "dec_lstm0", &a, sizeof a, (P + 3) / 4, 1, 1, 256, 1, 1)) return -1;
+        if (gpu_launch(g, "dec_step", &a, sizeof a, (P + 3) / 4, 1, 1, 256, 1, 1)) return -1;
         if (j == steps) break;
-        if (gpu_launch(g, "dec_lstm1", &a, sizeof a, (P + 3) / 4, 1, 1, 256, 1, 1)) return -1;
         if (gpu_launch(g, "dec_pred", &a, sizeof a, (J + 3) / 4, 1, 1, 256, 1, 1)) return -1;
         if (gpu_launch(g, "dec_joint", &a, sizeof a, NK_DEC_GROUPS, NK_DEC_MAX_BATCH, 1, 256, 1, 1)) return -1;
     }

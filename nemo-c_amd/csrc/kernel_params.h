@@ -320,7 +320,8 @@ typedef struct {
     const u16 *wout;          /* joint output [V][J]                                                */
     const float *bout;        /* [V]                                                               */
     float *tx;                /* [blank + 1][4P] layer-0 input gates Wx0 . embed(v) + b0 (zero input
-                                 for the blank row): read by dec_lstm0, written by dec_tx_build    */
+                                 for the blank row): read by dec_step, written by dec_tx_build     */
+    float *pre0;              /* [2 slots][4P] Wh0 . h0 of each slot's layer-0 state (gate-major)   */
     u32 P, J, V, blank, max_symbols, parity, enc_ld, decide_only;
 } NkDecArgs;
 

@@ -1,17 +1,17 @@
 /* Device-resident greedy RNNT loop for gfx950: the reference's decoder_run (src/decoder.c:92-127)
  * without a host round trip per joint evaluation.
  *
- * One iteration of the loop is four launches, captured into a graph that holds a run of
+ * One iteration of the loop is three launches, captured into a graph that holds a run of
  * iterations (the host replays it until the chunk is done):
- *   dec_lstm0  every wavefront first takes the decision of the previous iteration's joint (the
+ *   dec_step   every wavefront first takes the decision of the previous iteration's joint (the
  *              greedy rule of src/decoder.c:107-122: first non-blank row wins; blank rows reset
  *              the symbol count; max_symbols moves past the frame) from the packed per-workgroup
  *              argmax keys, workgroup 0 records it (next state copy, emitted token); then, when the
- *              prediction must be recomputed, LSTM layer 0 from embed(last token)
- *              (src/decoder.c:57-77; zeros for blank); its input half Wx0 . embed(v) + b0 is a
- *              per-token table built once by dec_tx_build with this kernel's own lane layout and
- *              sums, so the gates are the same bits while only Wh0 is streamed;
- *   dec_lstm1  LSTM layer 1;
+ *              prediction must be recomputed, both LSTM layers from embed(last token)
+ *              (src/decoder.c:57-77; zeros for blank).  Layer 0's input half Wx0 . embed(v) + b0
+ *              is a per-token table built once by dec_tx_build, and its hidden half Wh0 . h0 was
+ *              taken by the launch that made h0, so layer 0 is a cell over stored gate sums and
+ *              the launch streams Wx1, Wh1 and Wh0 (for the next step) once;
  *   dec_pred   joint.pred projection of the new hidden state;
  *   dec_joint  joint scores relu(enc[t + r] + pred) . W_out + b for up to 16 remaining frames
  *              with one prediction (speculating blank, src/decoder.c:79-90); each workgroup
@@ -22,23 +22,33 @@
  * (lane l reads the 16-byte chunks l and l + 64 of every row). */
 #include "nk_common.h"
 
+/* The previous joint's argmax keys this lane reduces: lane l takes groups l/16, l/16 + 4, ... of
+ * row l % 16 (they do not depend on the state, so they load beside it) */
+struct DecKeys {
+    unsigned long long k[NK_DEC_GROUPS / 4];
+};
+__device__ __forceinline__ DecKeys dec_keys(const NkDecArgs &a) {
+    const u32 lane = threadIdx.x & 63;
+    const unsigned long long *pp = a.part + (u64)(a.parity ^ 1) * NK_DEC_MAX_BATCH * NK_DEC_GROUPS;
+    DecKeys ks;
+#pragma unroll
+    for (int q = 0; q < NK_DEC_GROUPS / 4; ++q) ks.k[q] = pp[(lane & 15) * NK_DEC_GROUPS + (lane >> 4) + 4 * q];
+    return ks;
+}
+
 /* The decision of the previous joint, taken by one wavefront (every wavefront gets the same
  * answer).  Returns the new state; *tok = emitted token or -1. */
-__device__ __forceinline__ NkDecState dec_decide(const NkDecArgs &a, const NkDecState s, int *tok) {
+__device__ __forceinline__ NkDecState dec_decide(const NkDecArgs &a, const NkDecState s, const DecKeys &ks, int *tok) {
     NkDecState d = s;
     *tok = -1;
     if (!s.pending) return d;
     const u32 lane = threadIdx.x & 63;
     const int rows = min(NK_DEC_MAX_BATCH, s.frames - s.t);
-    /* lane l reduces groups l/16, l/16 + 4, ... of row l % 16; then the four lanes of a row combine */
-    const unsigned long long *pp = a.part + (u64)(a.parity ^ 1) * NK_DEC_MAX_BATCH * NK_DEC_GROUPS;
+    /* lane l reduces its groups of row l % 16; then the four lanes of a row combine */
     const u32 r = lane & 15;
     unsigned long long best = 0;
 #pragma unroll
-    for (int q = 0; q < NK_DEC_GROUPS / 4; ++q) {
-        const unsigned long long k = pp[r * NK_DEC_GROUPS + (lane >> 4) + 4 * q];
-        best = k > best ? k : best;
-    }
+    for (int q = 0; q < NK_DEC_GROUPS / 4; ++q) best = ks.k[q] > best ? ks.k[q] : best;
     unsigned long long o = shfl_xor_u64(best, 16);
     best = o > best ? o : best;
     o = shfl_xor_u64(best, 32);
@@ -95,56 +105,8 @@ __device__ __forceinline__ void dec_gate_dots(float (&out)[4], float (&x)[2][8],
     }
 }
 
-/* One LSTM layer for unit j = global wavefront index: four gate rows of Wx and Wh (K = P <= 1024,
- * two 16-byte chunks per lane per row), then the cell.  x_f32 (or x_bf16 for the embedding row,
- * or zeros when x_zero) is the layer input; with tx_row set, the input half Wx.x + b of the gates
- * comes from that table row instead (no Wx stream). */
-__device__ __forceinline__ void dec_lstm_unit(const NkDecArgs &a, u32 j, const float *x_f32, const u16 *x_bf16,
-                                              bool x_zero, const u16 *Wx, const u16 *Wh, const float *bias,
-                                              const float *tx_row, const float *h_in, const float *c_in,
-                                              float *h_out, float *c_out) {
-    const u32 lane = threadIdx.x & 63, P = a.P, nch = P >> 3;
-    float x[2][8], h[2][8];
-    if (!tx_row) dec_row_chunks(x, x_f32, x_bf16, x_zero, lane, nch);
-    dec_row_chunks(h, h_in, nullptr, false, lane, nch);
-    float bg[4];
-#pragma unroll
-    for (int g = 0; g < 4; ++g) bg[g] = tx_row ? tx_row[g * P + j] : bias[g * P + j];
-    const float c0 = c_in[j];
-    __builtin_amdgcn_sched_barrier(0);
-    uint4 wx[4][2], wh[4][2];
-#pragma unroll
-    for (int g = 0; g < 4; ++g)
-#pragma unroll
-        for (int q = 0; q < 2; ++q) {
-            const u64 off = (u64)(g * P + j) * P + 8 * min(lane + 64 * q, nch - 1);
-            if (!tx_row) wx[g][q] = ld_nt16(Wx + off);
-            wh[g][q] = ld_nt16(Wh + off);
-        }
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int q = 0; q < 2; ++q) {
-        const bool ok = lane + 64 * q < nch;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            if (!tx_row) x[q][e] = ok && !x_zero ? x[q][e] : 0.0f;
-            h[q][e] = ok ? h[q][e] : 0.0f;
-        }
-    }
-    float sxg[4], shg[4], gate[4];
-    if (!tx_row) dec_gate_dots(sxg, x, wx);
-    dec_gate_dots(shg, h, wh);
-#pragma unroll
-    for (int g = 0; g < 4; ++g) gate[g] = (tx_row ? bg[g] : sxg[g] + bg[g]) + shg[g];
-    if (lane != 0) return;
-    const float ig = sigmoid_f(gate[0]), fg = sigmoid_f(gate[1]), gg = tanhf(gate[2]), og = sigmoid_f(gate[3]);
-    const float c = fg * c0 + ig * gg;
-    c_out[j] = c;
-    h_out[j] = og * tanhf(c);
-}
-
 /* the layer-0 input table: row v = Wx0 . embed(v) + b0 (the blank row: b0), gate-major [4P], in
- * dec_lstm_unit's lane layout and summation order.  grid = ceil(P/4) x (blank + 1), block 256. */
+ * dec_step's lane layout and summation order.  grid = ceil(P/4) x (blank + 1), block 256. */
 extern "C" __global__ __launch_bounds__(256) void dec_tx_build(const NkDecArgs a) {
     const u32 j = blockIdx.x * 4 + (threadIdx.x >> 6), v = blockIdx.y, lane = threadIdx.x & 63, P = a.P, nch = P >> 3;
     if (j >= P) return;
@@ -169,40 +131,113 @@ extern "C" __global__ __launch_bounds__(256) void dec_tx_build(const NkDecArgs a
     for (int g = 0; g < 4; ++g) a.tx[(u64)v * 4 * P + g * P + j] = sx[g] + a.b0[g * P + j];
 }
 
-/* decision + LSTM layer 0.  grid = ceil(P/4) x 1, block 256 (one unit per wavefront). */
-extern "C" __global__ __launch_bounds__(256) void dec_lstm0(const NkDecArgs a) {
+/* One step of the loop up to the new hidden state, in one launch: the decision of the previous
+ * joint, the layer-0 cell, LSTM layer 1, and layer 0's hidden product for the step after.
+ * Layer 0's gates are tx[last token] + Wh0 . h0 with h0 the committed layer-0 state.  That state is
+ * always the provisional state of the last launch that ran the cell (the decision that emits commits
+ * it), so Wh0 . h0 is taken by that launch, against the h0 it has just made, and kept per state
+ * slot in pre0: then the cell needs no GEMV of its own and a step is one dependent phase shorter.
+ * grid = ceil(P/4), block 256.  Every workgroup takes the decision (the same answer) and computes
+ * the whole layer-0 cell into LDS from pre0 and the table row; wavefront j then runs layer-1 unit j
+ * and the four Wh0 rows of unit j against the new h0.  Workgroup 0 writes the state, the token and
+ * the new layer-0 state. */
+extern "C" __global__ __launch_bounds__(256) void dec_step(const NkDecArgs a) {
+    __shared__ float h0s[1024];
+    const u32 tid = threadIdx.x, lane = tid & 63, j = blockIdx.x * 4 + (tid >> 6), P = a.P;
+    /* loaded together: the state, the joint's keys, and the layer-0 gate sums and cell states of
+     * both slots (the decision picks the slot) for this thread's units tid, tid + 256, ... */
     const NkDecState s = a.st[a.parity];
+    const DecKeys ks = dec_keys(a);
+    constexpr int UPT = 4; /* units per thread: P <= 1024 */
+    float pre2[2][UPT][4], c02[2][UPT];
+#pragma unroll
+    for (int sl = 0; sl < 2; ++sl)
+#pragma unroll
+        for (int i = 0; i < UPT; ++i) {
+            const u32 u = min(tid + 256 * i, P - 1);
+#pragma unroll
+            for (int g = 0; g < 4; ++g) pre2[sl][i][g] = a.pre0[(u64)sl * 4 * P + g * P + u];
+            c02[sl][i] = a.hc[(u64)sl * 4 * P + 2 * P + u];
+        }
     int tok;
-    NkDecState d = dec_decide(a, s, &tok);
+    NkDecState d = dec_decide(a, s, ks, &tok);
     d.done = d.t >= d.frames;
     d.need_pred = !d.done && !d.pred_valid && !a.decide_only;
-    const u32 j = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (j == 0 && (threadIdx.x & 63) == 0) {
+    if (blockIdx.x == 0 && tid == 0) {
         NkDecState ns = d;
         if (d.need_pred) ns.pred_valid = 1;
         ns.pending = !d.done && !a.decide_only;
         a.st[a.parity ^ 1] = ns;
         if (tok >= 0 && d.n_out <= NK_DEC_MAX_TOKENS) a.tokens[d.n_out - 1] = tok;
     }
-    if (!d.need_pred || j >= a.P) return;
-    const u32 P = a.P, cm = (u32)d.cur, pv = cm ^ 1u;
-    const float *hc_c = a.hc + (u64)cm * 4 * P, *none = nullptr;
-    float *hc_p = a.hc + (u64)pv * 4 * P;
-    const bool blank = d.last_token == (int)a.blank || d.last_token < 0;
-    const float *tx_row = a.tx + (u64)(blank ? a.blank : (u32)d.last_token) * 4 * P;
-    dec_lstm_unit(a, j, none, nullptr, blank, a.wx0, a.wh0, a.b0, tx_row, hc_c, hc_c + 2 * P, hc_p, hc_p + 2 * P);
-}
-
-/* LSTM layer 1 from the new layer-0 state */
-extern "C" __global__ __launch_bounds__(256) void dec_lstm1(const NkDecArgs a) {
-    const NkDecState s = a.st[a.parity ^ 1];
-    const u32 j = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (!s.need_pred || j >= a.P) return;
-    const u32 P = a.P, cm = (u32)s.cur, pv = cm ^ 1u;
+    if (!d.need_pred) return; /* the same for every thread of the grid */
+    const u32 nch = P >> 3, cm = (u32)d.cur, pv = cm ^ 1u, jj = min(j, P - 1);
     const float *hc_c = a.hc + (u64)cm * 4 * P;
     float *hc_p = a.hc + (u64)pv * 4 * P;
-    dec_lstm_unit(a, j, hc_p, nullptr, false, a.wx1, a.wh1, a.b1, nullptr, hc_c + P, hc_c + 3 * P, hc_p + P,
-                  hc_p + 3 * P);
+    /* this wavefront's weight rows first (they do not wait for the cell), then its state operands */
+    uint4 wx[4][2], wh[4][2], w0[4][2];
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            const u64 off = (u64)(g * P + jj) * P + 8 * min(lane + 64 * q, nch - 1);
+            wx[g][q] = ld_nt16(a.wx1 + off);
+            wh[g][q] = ld_nt16(a.wh1 + off);
+            w0[g][q] = ld_nt16(a.wh0 + off);
+        }
+    float h1[2][8];
+    dec_row_chunks(h1, hc_c + P, nullptr, false, lane, nch);
+    float b1[4];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) b1[g] = a.b1[g * P + jj];
+    const float c1 = hc_c[3 * P + jj];
+    /* the layer-0 cell of every unit: gates = tx[last token] + Wh0 . h0 (input zero for blank) */
+    const bool blank = d.last_token == (int)a.blank || d.last_token < 0;
+    const float *tx_row = a.tx + (u64)(blank ? a.blank : (u32)d.last_token) * 4 * P;
+#pragma unroll
+    for (int i = 0; i < UPT; ++i) {
+        const u32 u = tid + 256 * i;
+        if (u >= P) break;
+        float gate[4];
+#pragma unroll
+        for (int g = 0; g < 4; ++g) gate[g] = tx_row[g * P + u] + (cm ? pre2[1][i][g] : pre2[0][i][g]);
+        const float ig = sigmoid_f(gate[0]), fg = sigmoid_f(gate[1]), gg = tanhf(gate[2]), og = sigmoid_f(gate[3]);
+        const float c = fg * (cm ? c02[1][i] : c02[0][i]) + ig * gg;
+        const float h = og * tanhf(c);
+        h0s[u] = h;
+        if (blockIdx.x == 0) {
+            hc_p[u] = h;
+            hc_p[2 * P + u] = c;
+        }
+    }
+    __syncthreads();
+    if (j >= P) return;
+    float x[2][8];
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+        const bool ok = lane + 64 * q < nch;
+        const u32 k = 8 * min(lane + 64 * q, nch - 1);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            x[q][e] = ok ? h0s[k + e] : 0.0f;
+            h1[q][e] = ok ? h1[q][e] : 0.0f;
+        }
+    }
+    float sx[4], sh[4], s0[4];
+    dec_gate_dots(sx, x, wx);
+    dec_gate_dots(sh, h1, wh);
+    dec_gate_dots(s0, x, w0);
+    if (lane != 0) return;
+    float gate[4];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) gate[g] = (sx[g] + b1[g]) + sh[g];
+    const float ig = sigmoid_f(gate[0]), fg = sigmoid_f(gate[1]), gg = tanhf(gate[2]), og = sigmoid_f(gate[3]);
+    const float c = fg * c1 + ig * gg;
+    hc_p[3 * P + j] = c;
+    hc_p[P + j] = og * tanhf(c);
+    float *pre_p = a.pre0 + (u64)pv * 4 * P;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) pre_p[g * P + j] = s0[g];
 }
 
 /* pred = joint.pred . h1' + b; one output per wavefront (K = P <= 1024) */
