@@ -13,8 +13,11 @@
  *   nk_dwconv_ln_silu   dwconv_ln_silu dispatch      src/encoder.c:172-174
  *   nk_conv2d_c1_s2_relu, nk_dwconv2d_s2, nk_flatten_cf   subsampling dispatches src/encoder.c:120-142
  *   nk_compact          compact_caches               src/encoder.c:199-211 (one launch for all layers)
- *   nk_lstm_cell        lstm_cell dispatch           src/decoder.c:71-73
- *   nk_joint_argmax     joint_partial + argmax_reduce src/decoder.c:79-90
+ *   nk_lstm_cell_rows   lstm_cell dispatch           src/decoder.c:71-73 (rows of many streams)
+ *   nk_joint_in_rows + nk_gemm_argmax_rows (or nk_gemm + nk_argmax_rows)
+ *                       joint + argmax dispatches    src/decoder.c:79-90 (rows of many streams)
+ * The single stream's LSTM, joint and argmax run inside the device-resident greedy loop
+ * (csrc/host/decoder.c, kernels dec_step / dec_pred / dec_joint), which has no per-kernel launcher.
  *
  * The GPU runtime (gpu_* below) is a re-design of src/gpu.h:20-41, not the same interface: the
  * host here is this library's own (the launchers compute their grids from the shapes), so the
@@ -266,7 +269,6 @@ int nk_compact(gpu_t *g, float *base, uint64_t stride, uint32_t nbuf, uint32_t r
                uint32_t src_row, uint32_t dst_row);
 
 /* ---- RNNT decoder ------------------------------------------------------------------------------ */
-int nk_lstm_cell(gpu_t *g, const float *gates, const float *c_in, float *c_out, float *h_out, uint32_t H);
 /* Batched decoder pieces (rows of many streams; see kernel_params.h for the layouts):
  * LSTM input rows [x | h], the LSTM cell on rows, joint input rows relu(enc + pred), row argmax. */
 int nk_lstm_input_rows(gpu_t *g, const uint16_t *embed, const int *tok, const float *xsrc, const float *hc,
@@ -276,12 +278,6 @@ int nk_lstm_cell_rows(gpu_t *g, const float *gates, float *hc, const int *crow_i
 int nk_joint_in_rows(gpu_t *g, const float *enc, const float *pred, const int *erow, const int *prow, float *jin,
                      uint32_t rows, uint32_t J);
 int nk_argmax_rows(gpu_t *g, const float *logits, uint32_t ld, uint32_t rows, uint32_t V, int *out);
-/* argmax over V classes of W . relu(enc[enc_row + r] + pred) + bias for r < rows (<= 16);
- * out[2r] = index (lowest on ties), out[2r+1] = value bits.  part_v/part_i: scratch of
- * rows * 256 entries. */
-int nk_joint_argmax(gpu_t *g, const float *enc, uint32_t enc_row, uint32_t enc_ld, uint32_t rows, const float *pred,
-                    const uint16_t *W, const float *bias, uint32_t V, uint32_t H, float *part_v, int *part_i,
-                    int *out);
 
 #ifdef __cplusplus
 }

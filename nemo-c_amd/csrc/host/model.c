@@ -64,7 +64,7 @@ static const char *unsupported(const model_cfg_t *g) {
     if (g->d_model % 32 || g->d_model > NK_ROW_MAX || g->prompt_hidden % 32 || g->sub_channels % 32)
         return "model widths that are not multiples of 32 (or above the row limit)";
     if (g->pred_hidden % 8 || g->joint_hidden % 8 || g->joint_hidden > NK_JOINT_MAX_H) return "decoder widths";
-    if (g->num_classes > NK_JOINT_GROUPS * NK_JOINT_WAVES * 1024) return "a vocabulary above the joint kernel's limit";
+    if (g->num_classes > 32 * NK_DEC_GROUPS) return "a vocabulary above the joint kernels' limit";
     return NULL;
 }
 

@@ -780,19 +780,3 @@ int nk_compact(gpu_t *g, float *base, uint64_t stride, uint32_t nbuf, uint32_t r
     return gpu_launch(g, "compact_rows", &a, sizeof a, blocks_for((uint64_t)rows * cols), nbuf, 1, 256, 1, 1);
 }
 
-int nk_lstm_cell(gpu_t *g, const float *gates, const float *c_in, float *c_out, float *h_out, uint32_t H) {
-    NkLstmArgs a = { gates, c_in, c_out, h_out, H, 0 };
-    return gpu_launch(g, "lstm_cell", &a, sizeof a, blocks_for(H), 1, 1, 256, 1, 1);
-}
-
-int nk_joint_argmax(gpu_t *g, const float *enc, uint32_t enc_row, uint32_t enc_ld, uint32_t rows, const float *pred,
-                    const uint16_t *W, const float *bias, uint32_t V, uint32_t H, float *part_v, int *part_i,
-                    int *out) {
-    if (!rows) return 0;
-    if (rows > NK_DEC_MAX_BATCH || H > NK_JOINT_MAX_H || (H & 1) || ((uintptr_t)W & 3))
-        return bad(g, "joint: rows <= 16, even H <= 1024, 4-byte aligned W");
-    NkJointArgs j = { enc, pred, W, bias, part_v, part_i, V, H, enc_row, enc_ld };
-    if (gpu_launch(g, "joint_partial", &j, sizeof j, NK_JOINT_GROUPS, rows, 1, 256, 1, 1)) return -1;
-    NkArgmaxArgs r = { part_v, part_i, out, NK_JOINT_GROUPS * NK_JOINT_WAVES, 0 };
-    return gpu_launch(g, "argmax_reduce", &r, sizeof r, rows, 1, 1, 256, 1, 1);
-}

@@ -32,9 +32,7 @@ typedef uint16_t u16;
 #define NK_FEW_ROWS 16          /* GEMMs with M <= 16 use the weight-streaming kernels            */
 #define NK_ATT_MAX_L 128        /* attention window limit (reference ATT_MAX_L 80; 56 + 16 + 2)    */
 #define NK_DEC_MAX_BATCH 16     /* joint rows per decoder round trip (reference DEC_MAX_BATCH)    */
-#define NK_JOINT_GROUPS 64      /* workgroups of the joint scoring kernel                          */
-#define NK_JOINT_WAVES 4        /* waves per joint workgroup                                       */
-#define NK_JOINT_MAX_H 1024     /* joint hidden size limit (LDS staging)                           */
+#define NK_JOINT_MAX_H 1024     /* joint hidden size limit (16 floats per lane of a wavefront)     */
 #define NK_CACHE_EPOCH_CHUNKS 8 /* K/V and conv caches compacted once per this many chunks         */
 #define NK_LN_THREADS 256
 #define NK_ROW_MAX 4096         /* row width limit of the per-row kernels (4 float4 per thread)    */
@@ -267,30 +265,6 @@ typedef struct {
     unsigned long long stride;
     u32 nbuf, rows, cols, src_row, dst_row, pad;
 } NkCompactArgs;
-
-typedef struct {
-    const float *gates, *c_in;
-    float *c_out, *h_out;
-    u32 H, pad;
-} NkLstmArgs;
-
-/* Joint scoring of `rows` encoder frames with one prediction vector.
- * part_v / part_i: [rows][NK_JOINT_GROUPS * NK_JOINT_WAVES]. */
-typedef struct {
-    const float *enc, *pred;
-    const u16 *W;
-    const float *bias;
-    float *part_v;
-    int *part_i;
-    u32 V, H, enc_row, enc_ld;
-} NkJointArgs;
-
-typedef struct {
-    const float *part_v;
-    const int *part_i;
-    int *out; /* out[2*row] = index, out[2*row+1] = value bits */
-    u32 n, pad;
-} NkArgmaxArgs;
 
 /* ---- device-resident greedy RNNT loop -------------------------------------------------------- */
 #define NK_DEC_MAX_TOKENS 256 /* tokens per chunk: at most 16 frames x max_symbols                  */

@@ -238,79 +238,6 @@ extern "C" __global__ __launch_bounds__(256) void compact_rows(const NkCompactAr
     b[(u64)a.dst_row * a.cols + idx] = b[(u64)a.src_row * a.cols + idx];
 }
 
-/* LSTM cell, gates [4H] in order i, f, g, o: reference src/kernels.metal:474-486. */
-extern "C" __global__ __launch_bounds__(256) void lstm_cell(const NkLstmArgs a) {
-    const u32 i = blockIdx.x * 256 + threadIdx.x;
-    if (i >= a.H) return;
-    const float ig = sigmoid_f(a.gates[i]);
-    const float fg = sigmoid_f(a.gates[a.H + i]);
-    const float gg = tanhf(a.gates[2 * a.H + i]);
-    const float og = sigmoid_f(a.gates[3 * a.H + i]);
-    const float c = fg * a.c_in[i] + ig * gg;
-    a.c_out[i] = c;
-    a.h_out[i] = og * tanhf(c);
-}
-
-/* RNNT joint, stage 1 (reference src/kernels.metal:488-519): r = relu(enc[row] + pred) in LDS;
- * wavefront w of workgroup g scores vocabulary rows n = g*4 + w (mod G*4) and keeps the best,
- * lowest index on ties.  grid = (NK_JOINT_GROUPS, rows), block = 256. */
-extern "C" __global__ __launch_bounds__(256) void joint_partial(const NkJointArgs a) {
-    __shared__ float r[NK_JOINT_MAX_H];
-    const u32 g = blockIdx.x, G = gridDim.x, row = blockIdx.y, tid = threadIdx.x;
-    const int lane = tid & 63, wave = tid >> 6;
-    const float *e = a.enc + (u64)(a.enc_row + row) * a.enc_ld;
-    for (u32 i = tid; i < a.H; i += 256) r[i] = fmaxf(e[i] + a.pred[i], 0.0f);
-    __syncthreads();
-    float bv = -INFINITY;
-    int bi = 0x7fffffff;
-    const u32 npair = a.H >> 1;
-    for (u32 n = g * NK_JOINT_WAVES + wave; n < a.V; n += G * NK_JOINT_WAVES) {
-        const u32 *w2 = (const u32 *)(a.W + (u64)n * a.H);
-        float acc = 0.0f;
-        for (u32 k = lane; k < npair; k += 64) {
-            const u32 w = w2[k];
-            acc += r[2 * k] * bf_lo(w);
-            acc += r[2 * k + 1] * bf_hi(w);
-        }
-        acc = wave_sum(acc) + a.bias[n];
-        if (acc > bv || (acc == bv && (int)n < bi)) { bv = acc; bi = (int)n; }
-    }
-    if (lane == 0) {
-        const u32 slot = row * G * NK_JOINT_WAVES + g * NK_JOINT_WAVES + wave;
-        a.part_v[slot] = bv;
-        a.part_i[slot] = bi;
-    }
-}
-
-/* RNNT joint, stage 2 (reference src/kernels.metal:521-550): reduce n partial bests of one row,
- * same tie rule; out[2*row] = index, out[2*row+1] = value bits.  grid = rows, block = 256. */
-extern "C" __global__ __launch_bounds__(256) void argmax_reduce(const NkArgmaxArgs a) {
-    __shared__ float bestv[256];
-    __shared__ int besti[256];
-    const u32 row = blockIdx.x, tid = threadIdx.x;
-    const float *pv = a.part_v + (u64)row * a.n;
-    const int *pi = a.part_i + (u64)row * a.n;
-    float bv = -INFINITY;
-    int bi = 0x7fffffff;
-    for (u32 i = tid; i < a.n; i += 256)
-        if (pv[i] > bv || (pv[i] == bv && pi[i] < bi)) { bv = pv[i]; bi = pi[i]; }
-    bestv[tid] = bv;
-    besti[tid] = bi;
-    __syncthreads();
-    for (u32 st = 128; st > 0; st >>= 1) {
-        if (tid < st) {
-            const float ov = bestv[tid + st];
-            const int oi = besti[tid + st];
-            if (ov > bestv[tid] || (ov == bestv[tid] && oi < besti[tid])) { bestv[tid] = ov; besti[tid] = oi; }
-        }
-        __syncthreads();
-    }
-    if (tid == 0) {
-        a.out[2 * row] = besti[0];
-        a.out[2 * row + 1] = __float_as_int(bestv[0]);
-    }
-}
-
 /* Strided row copy: rows x cols floats from src (row stride src_ld) to dst (row stride dst_ld).
  * Used for the row select of the subsampled window and for activation dumps. */
 extern "C" __global__ __launch_bounds__(256) void copy2d_f32(const NkCopy2dArgs a) {

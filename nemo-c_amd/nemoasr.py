@@ -157,12 +157,10 @@ API = {
     "nk_conv2d_c1_dw_s2_b": (C.c_int, [_vp] * 7 + [_u32] * 8),
     "nk_flatten_cf_b": (C.c_int, [_vp, _vp, _vp, _u32, _u32, _u32, _u32]),
     "nk_gather_rows": (C.c_int, [_vp, _vp, _u32, _vp, _vp, _u32, _u32, _u32]),
-    "nk_lstm_cell": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _u32]),
     "nk_lstm_input_rows": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32]),
     "nk_lstm_cell_rows": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32]),
     "nk_joint_in_rows": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32]),
     "nk_argmax_rows": (C.c_int, [_vp, _vp, _u32, _u32, _u32, _vp]),
-    "nk_joint_argmax": (C.c_int, [_vp, _vp, _u32, _u32, _u32, _vp, _vp, _vp, _u32, _u32, _vp, _vp, _vp]),
     # include/nemoasr_host.h
     "melfe_create": (_vp, []),
     "melfe_destroy": (None, [_vp]),

@@ -101,3 +101,73 @@ def rel_err(a: np.ndarray, b: np.ndarray) -> float:
     b = np.asarray(b, dtype=np.float64)
     den = max(float(np.max(np.abs(b))) if b.size else 0.0, 1e-30)
     return float(np.max(np.abs(a - b))) / den if b.size else 0.0
+
+
+# ---- the product's decoder pieces, driven one kernel at a time ---------------------------------
+def lstm_cell_rows(gpu, gates: np.ndarray, c_in: np.ndarray):
+    """The LSTM cell of the batched greedy loop (nk_lstm_cell_rows, kernel lstm_cell_rows) on one
+    row: gates [4H] (i, f, g, o), c_in [H] -> (c_out, h_out)."""
+    import nemoasr
+
+    L = nemoasr.lib()
+    H = c_in.size
+    hc = np.zeros((3, H), np.float32)
+    hc[0] = c_in
+    dg, dhc, dout = gpu.put(np.ascontiguousarray(gates, np.float32)), gpu.put(hc), gpu.alloc(H * 4)
+    rows = [gpu.put(np.array([i], np.int32)) for i in (0, 1, 2)]
+    gpu.begin()
+    gpu.check(L.nk_lstm_cell_rows(gpu.h, dg.ptr, dhc.ptr, rows[0].ptr, rows[1].ptr, rows[2].ptr, dout.ptr, 1, H))
+    gpu.end()
+    out = dhc.read((3, H))
+    np.testing.assert_array_equal(dout.read(H), out[2])
+    return out[1], out[2]
+
+
+def joint_argmax_rows(gpu, enc: np.ndarray, pred: np.ndarray, W: np.ndarray, bias: np.ndarray, device_loop: bool):
+    """argmax_n W[n] . relu(enc[r] + pred) + bias[n] for every row r of enc, through the batched
+    loop's kernels: joint_in_rows, then either the joint GEMM with the argmax-key epilogue
+    (gemm_mx64x64_argmax, the device loop; the keys of each row reduced here) or the joint GEMM into
+    logits and argmax_rows (the host loop).  Operands are zero-padded to the kernels' multiples,
+    which changes no score.  Returns [(index, value)] per row."""
+    import nemoasr
+
+    L = nemoasr.lib()
+    R, J = enc.shape
+    V = W.shape[0]
+    Jp, N = -(-J // 32) * 32, -(-V // 64) * 64
+    Wp = np.zeros((N, Jp), np.uint16)
+    Wp[:V, :J] = W
+    bp = np.zeros(N, np.float32)
+    bp[:V] = bias
+    ep = np.zeros((R, Jp), np.float32)
+    ep[:, :J] = enc
+    pp = np.zeros((1, Jp), np.float32)
+    pp[0, :J] = pred
+    de, dp, dW, db = gpu.put(ep), gpu.put(pp), gpu.put(Wp), gpu.put(bp)
+    erow, prow = gpu.put(np.arange(R, dtype=np.int32)), gpu.put(np.zeros(R, np.int32))
+    jin = gpu.alloc(R * Jp * 4)
+    gpu.begin()
+    gpu.check(L.nk_joint_in_rows(gpu.h, de.ptr, dp.ptr, erow.ptr, prow.ptr, jin.ptr, R, Jp))
+    if device_loop:
+        parts = N // 32
+        keys = gpu.alloc(R * parts * 8)
+        gpu.check(L.nk_gemm_argmax(gpu.h, jin.ptr, Jp, dW.ptr, Jp, db.ptr, keys.ptr, parts, R, N, Jp, V))
+    else:
+        logits, out = gpu.alloc(R * N * 4), gpu.alloc(2 * R * 4)
+        gpu.check(L.nk_gemm(gpu.h, jin.ptr, Jp, dW.ptr, Jp, db.ptr, logits.ptr, N, R, N, Jp, 0, 0, 1.0))
+        gpu.check(L.nk_argmax_rows(gpu.h, logits.ptr, N, R, V, out.ptr))
+    gpu.end()
+    res = []
+    if device_loop:
+        k = keys.read((R, parts), np.uint64).max(axis=1)
+        for best in k:
+            best = int(best)
+            idx = 0xFFFFFFFF - (best & 0xFFFFFFFF)
+            ordv = best >> 32
+            bits = ordv & 0x7FFFFFFF if ordv & 0x80000000 else (~ordv) & 0xFFFFFFFF
+            res.append((idx, float(np.array([bits], np.uint32).view(np.float32)[0])))
+    else:
+        o = out.read(2 * R, np.int32)
+        for r in range(R):
+            res.append((int(o[2 * r]), float(o[2 * r + 1:2 * r + 2].view(np.float32)[0])))
+    return res

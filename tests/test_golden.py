@@ -127,26 +127,19 @@ def test_gpu_golden_dwconv(gpu, gold):
 
 
 @pytest.mark.gpu
-def test_gpu_golden_decoder_kernels(gpu, gold):
-    import nemoasr
+@pytest.mark.parametrize("device_loop", [True, False])
+def test_gpu_golden_decoder_kernels(gpu, gold, device_loop):
+    """The LSTM cell and the joint argmax kernels the batched greedy loop launches (the device loop's
+    argmax-key GEMM, or logits + argmax_rows in the host loop), on the golden cases, including the
+    planted exact tie (lowest index wins)."""
+    from conftest import joint_argmax_rows, lstm_cell_rows
 
-    L = nemoasr.lib()
     c = case(gold, "lstm")
-    H = c["c_in"].size
-    dg, dc, dco, dho = gpu.put(c["gates"]), gpu.put(c["c_in"]), gpu.alloc(H * 4), gpu.alloc(H * 4)
-    gpu.begin()
-    gpu.check(L.nk_lstm_cell(gpu.h, dg.ptr, dc.ptr, dco.ptr, dho.ptr, H))
-    gpu.end()
-    assert rel_err(dco.read(H), c["c_out"]) < 1e-6
-    assert rel_err(dho.read(H), c["h_out"]) < 1e-6
+    co, ho = lstm_cell_rows(gpu, c["gates"], c["c_in"])
+    assert rel_err(co, c["c_out"]) < 1e-6
+    assert rel_err(ho, c["h_out"]) < 1e-6
     for name in ("joint", "joint_tie"):
         c = case(gold, name)
-        V, Hj = c["W"].shape
-        de, dp, dW, db = gpu.put(c["enc"][None]), gpu.put(c["pred"]), gpu.put(c["W"]), gpu.put(c["bias"])
-        pv, pi, out = gpu.alloc(16 * 256 * 4), gpu.alloc(16 * 256 * 4), gpu.alloc(32 * 4)
-        gpu.begin()
-        gpu.check(L.nk_joint_argmax(gpu.h, de.ptr, 0, Hj, 1, dp.ptr, dW.ptr, db.ptr, V, Hj, pv.ptr, pi.ptr, out.ptr))
-        gpu.end()
-        res = out.read(2, np.int32)
-        assert res[0] == int(c["idx"]), name
-        assert abs(res[1:2].view(np.float32)[0] - float(c["val"])) <= 1e-5 * max(1.0, abs(float(c["val"])))
+        (idx, val), = joint_argmax_rows(gpu, c["enc"][None], c["pred"], c["W"], c["bias"], device_loop)
+        assert idx == int(c["idx"]), name
+        assert abs(val - float(c["val"])) <= 1e-5 * max(1.0, abs(float(c["val"]))), name

@@ -624,63 +624,50 @@ def test_subsampling_conv02_fused(gpu, nwin, batch, F, C):
         assert rel_err(fused[w], ref) < 1e-6
 
 
-def test_lstm_cell(gpu):
-    import nemoasr
+def test_lstm_cell_rows(gpu):
+    from conftest import lstm_cell_rows
 
-    lib = nemoasr.lib()
     H = 640
     rng = np.random.default_rng(7)
     gates = (2 * rng.standard_normal(4 * H)).astype(np.float32)
     c_in = rng.standard_normal(H).astype(np.float32)
     rc, rh = oracle.lstm_cell(gates, c_in)
-    dg, dc, dco, dho = gpu.put(gates), gpu.put(c_in), gpu.alloc(H * 4), gpu.alloc(H * 4)
-    gpu.begin()
-    gpu.check(lib.nk_lstm_cell(gpu.h, dg.ptr, dc.ptr, dco.ptr, dho.ptr, H))
-    gpu.end()
-    assert rel_err(dco.read(H), rc) < 1e-6
-    assert rel_err(dho.read(H), rh) < 1e-6
+    co, ho = lstm_cell_rows(gpu, gates, c_in)
+    assert rel_err(co, rc) < 1e-6
+    assert rel_err(ho, rh) < 1e-6
 
 
+@pytest.mark.parametrize("device_loop", [True, False])
 @pytest.mark.parametrize("rows", [1, 5, 16])
-def test_joint_argmax(gpu, rows):
-    import nemoasr
+def test_joint_argmax(gpu, rows, device_loop):
+    """The full-size joint (V = 1025 classes, 640 wide) through the batched loop's kernels."""
+    from conftest import joint_argmax_rows
 
-    lib = nemoasr.lib()
     V, H = 1025, 640
     rng = np.random.default_rng(rows)
     W = _w(rng, V, H)
     bias = (0.1 * rng.standard_normal(V)).astype(np.float32)
-    enc = rng.standard_normal((rows + 3, H)).astype(np.float32)
+    enc = rng.standard_normal((rows, H)).astype(np.float32)
     pred = rng.standard_normal(H).astype(np.float32)
-    dW, db, de, dp = gpu.put(W), gpu.put(bias), gpu.put(enc), gpu.put(pred)
-    pv, pi, out = gpu.alloc(16 * 256 * 4), gpu.alloc(16 * 256 * 4), gpu.alloc(32 * 4)
-    gpu.begin()
-    gpu.check(lib.nk_joint_argmax(gpu.h, de.ptr, 2, H, rows, dp.ptr, dW.ptr, db.ptr, V, H, pv.ptr, pi.ptr, out.ptr))
-    gpu.end()
-    res = out.read(2 * rows, np.int32)
+    got = joint_argmax_rows(gpu, enc, pred, W, bias, device_loop)
     for r in range(rows):
-        i, v, logits = oracle.joint_argmax(enc[2 + r], pred, W, bias)
-        assert res[2 * r] == i
-        assert abs(res[2 * r + 1:2 * r + 2].view(np.float32)[0] - v) <= 1e-5 * max(1.0, abs(v))
+        i, v, logits = oracle.joint_argmax(enc[r], pred, W, bias)
+        assert got[r][0] == i
+        assert abs(got[r][1] - v) <= 1e-5 * max(1.0, abs(v))
 
 
-def test_joint_argmax_tie_lowest_index(gpu):
+@pytest.mark.parametrize("device_loop", [True, False])
+def test_joint_argmax_tie_lowest_index(gpu, device_loop):
     """Exact ties resolve to the lowest class index (src/kernels.metal:516, :545)."""
-    import nemoasr
+    from conftest import joint_argmax_rows
 
-    lib = nemoasr.lib()
     V, H = 1025, 640
     W = np.zeros((V, H), np.uint16)
     bias = np.zeros(V, np.float32)
     bias[[17, 300, 999]] = 1.0
     enc = np.ones((1, H), np.float32)
     pred = np.zeros(H, np.float32)
-    dW, db, de, dp = gpu.put(W), gpu.put(bias), gpu.put(enc), gpu.put(pred)
-    pv, pi, out = gpu.alloc(16 * 256 * 4), gpu.alloc(16 * 256 * 4), gpu.alloc(32 * 4)
-    gpu.begin()
-    gpu.check(lib.nk_joint_argmax(gpu.h, de.ptr, 0, H, 1, dp.ptr, dW.ptr, db.ptr, V, H, pv.ptr, pi.ptr, out.ptr))
-    gpu.end()
-    assert out.read(2, np.int32)[0] == 17
+    assert joint_argmax_rows(gpu, enc, pred, W, bias, device_loop)[0][0] == 17
 
 
 def test_compact_rows(gpu):
