@@ -139,12 +139,21 @@ typedef struct {
 int nk_gemm_resid(gpu_t *g, const float *A, const uint16_t *A2, uint32_t lda, const uint16_t *W, uint32_t ldw, float *C,
                   uint32_t ldc, uint32_t M, uint32_t N, uint32_t K, float alpha, nk_resid_t *pend);
 int nk_resid_fold(gpu_t *g, float *C, uint32_t ldc, uint32_t M, uint32_t N, const nk_resid_t *pend);
+/* A few-row residual update C += alpha * A W^T (no bias, activation or row map) whose kernel may
+ * split K (the few-row MFMA kernel, 5-16 rows): its partial rows are returned in *pend and C is not
+ * touched, for the next nk_gemm_ln_pend on C to add in share order; when the kernel does not split
+ * K, C is updated and *pend is empty.  The partial rows live in the context's scratch, which holds
+ * one pending update at a time. */
+int nk_gemm_pend(gpu_t *g, const float *A, uint32_t lda, const uint16_t *W, uint32_t ldw, float *C, uint32_t ldc,
+                 uint32_t M, uint32_t N, uint32_t K, float alpha, nk_resid_t *pend);
 /* nk_gemm_ln on A with a pending residual update (pend, may be NULL or empty) applied first:
  * Xf = A + alpha * (((0 + p0) + p1) + ...) (the bits of nk_resid_fold), and the GEMM's LayerNorm
  * prologue reads Xf.  Xf (rows of lda floats, not A) receives the updated rows: the residual
- * stream after the update.  The weight-streaming GEMV (M <= 4, K <= 1024) applies the update in its
- * prologue, no extra launch; other kernels get a copy and an nk_resid_fold first.  Parts are
- * [nparts][M][K] (part stride M * K). */
+ * stream after the update; it may be NULL when they are not needed (the LayerNorm output carries
+ * the stream on) and the kernel folds in its prologue.  The weight-streaming GEMV (M <= 4,
+ * K <= 1024) and the few-row MFMA kernel (M <= 16, K == 1024, at most 4 parts) apply the update in
+ * their prologue, no extra launch; other kernels get a copy into Xf and an nk_resid_fold first.
+ * Parts are [nparts][M][K] (part stride M * K). */
 int nk_gemm_ln_pend(gpu_t *g, const float *A, uint32_t lda, const uint16_t *W, uint32_t ldw, const float *bias,
                     float *C, uint32_t ldc, const int *crow, uint32_t M, uint32_t N, uint32_t K, int act, int accumulate,
                     float alpha, int ln_mode, const float *g1, const float *b1, const float *g2, const float *b2,

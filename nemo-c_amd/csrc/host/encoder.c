@@ -47,7 +47,7 @@ struct encoder {
     int closed;
     /* device buffers */
     gpu_buf_t *win, *c1, *c2, *c3, *c4, *flat;
-    gpu_buf_t *h, *tmp, *t2, *ff, *att, *y, *ph, *prompted, *joint_enc;
+    gpu_buf_t *h, *tmp, *t2, *xf, *ff, *att, *y, *ph, *prompted, *joint_enc;
     gpu_buf_t *kv, *din, *desc;
     size_t kv_stride, din_stride; /* floats per layer */
     int cap_rows, pos, cache_len;
@@ -95,6 +95,7 @@ encoder_t *encoder_create(model_t *m, int right) {
     e->h = gpu_buf_alloc(g, cm * D * fs);
     e->tmp = gpu_buf_alloc(g, cm * D * fs);
     e->t2 = gpu_buf_alloc(g, cm * D * fs);
+    e->xf = gpu_buf_alloc(g, cm * D * fs);
     e->ff = gpu_buf_alloc(g, cm * (size_t)c->d_ff * fs);
     e->att = gpu_buf_alloc(g, cm * D * fs);
     e->y = gpu_buf_alloc(g, cm * D * fs);
@@ -125,7 +126,7 @@ static void drop_graphs(encoder_t *e) {
 void encoder_destroy(encoder_t *e) {
     if (!e) return;
     drop_graphs(e);
-    gpu_buf_t *bufs[] = { e->win, e->c1, e->c2, e->c3, e->c4, e->flat, e->h, e->tmp, e->t2, e->ff,
+    gpu_buf_t *bufs[] = { e->win, e->c1, e->c2, e->c3, e->c4, e->flat, e->h, e->tmp, e->t2, e->xf, e->ff,
                           e->att, e->y, e->ph, e->prompted, e->joint_enc, e->kv, e->din, e->desc, e->dump_dev };
     for (size_t i = 0; i < sizeof bufs / sizeof *bufs; ++i) gpu_buf_free(bufs[i]);
     gpu_host_free(e->stage_win);
@@ -259,17 +260,31 @@ static void run_blocks(encoder_t *e, int c) {
     const int *rows = desc + NK_DESC_ROWS;
     float *R[2] = { gpu_buf_dptr(e->h), gpu_buf_dptr(e->tmp) };
     float *lnbuf = gpu_buf_dptr(e->t2); /* LayerNorm output when the GEMM cannot take it as a prologue */
+    float *xdead = gpu_buf_dptr(e->xf);  /* residual rows after a pending update that nothing reads again */
     float *ff = gpu_buf_dptr(e->ff), *att = gpu_buf_dptr(e->att), *y = gpu_buf_dptr(e->y);
     float *dump = e->dump ? gpu_buf_dptr(e->dump_dev) : NULL;
     /* one or two rows per chunk: attention + out_proj and dwconv + pw2 as one launch each */
     const int fuse_att = e->fuse && uc <= 4 && dh == 128 && D % 128 == 0;
     const int fuse_conv = e->fuse && uc <= 2 && D <= 1024 && D % 8 == 0 && cf->conv_kernel == NK_CONV_TAPS;
     int cur = 0;
+    /* A residual update may stay pending (its partial rows in the context's scratch: the few-row
+     * kernel's K shares, or the fused attention's heads) until the next LayerNorm-fused GEMM, which
+     * adds it to the residual in its prologue and writes the updated rows to the other buffer. */
+    nk_resid_t pend = { 0 };
+#define LN_GEMM(Wt, C, ldc, crow, N, act, g1, b1)                                                          \
+    do {                                                                                                   \
+        float *xf = pend.nparts ? R[cur ^ 1] : NULL;                                                       \
+        nk_gemm_ln_pend(g, R[cur], D, Wt, D, NULL, C, ldc, crow, uc, N, D, act, 0, 1.0f, 1, g1, b1, NULL, NULL, NULL, \
+                        lnbuf, eps, &pend, xf);                                                            \
+        if (xf) cur ^= 1;                                                                                  \
+        pend.nparts = 0;                                                                                   \
+    } while (0)
     for (uint32_t l = 0; l < nl; ++l) {
         const layer_dev_t *W = &m->L[l];
         float *kv = (float *)gpu_buf_dptr(e->kv) + (size_t)l * e->kv_stride;
         float *din = (float *)gpu_buf_dptr(e->din) + (size_t)l * e->din_stride;
-        /* FF1 half step (LN of block l-1's output, then this block's FF1 norm) */
+        /* FF1 half step (LN of block l-1's output, then this block's FF1 norm; block l-1's last
+         * update added first) */
         if (l == 0) {
             nk_gemm_ln(g, R[0], D, W->ff1_w1, D, NULL, ff, FF, NULL, uc, FF, D, NK_ACT_SILU, 0, 1.0f, 1, W->ln_ff1_g,
                        W->ln_ff1_b, NULL, NULL, NULL, lnbuf, eps);
@@ -277,52 +292,46 @@ static void run_blocks(encoder_t *e, int c) {
             const layer_dev_t *Wp = &m->L[l - 1];
             const int prev = cur;
             cur ^= 1;
-            nk_gemm_ln(g, R[prev], D, W->ff1_w1, D, NULL, ff, FF, NULL, uc, FF, D, NK_ACT_SILU, 0, 1.0f, 2, Wp->ln_out_g,
-                       Wp->ln_out_b, W->ln_ff1_g, W->ln_ff1_b, R[cur], lnbuf, eps);
+            nk_gemm_ln_pend(g, R[prev], D, W->ff1_w1, D, NULL, ff, FF, NULL, uc, FF, D, NK_ACT_SILU, 0, 1.0f, 2,
+                            Wp->ln_out_g, Wp->ln_out_b, W->ln_ff1_g, W->ln_ff1_b, R[cur], lnbuf, eps, &pend,
+                            pend.nparts ? xdead : NULL);
+            pend.nparts = 0;
             if (dump) nk_copy2d(g, R[cur], D, dump + (size_t)(l - 1) * D, D * nl, uc, D);
         }
-        float *res = R[cur];
-        nk_gemm(g, ff, FF, W->ff1_w2, FF, NULL, res, D, uc, D, FF, NK_ACT_NONE, 1, 0.5f);
+        nk_gemm_pend(g, ff, FF, W->ff1_w2, FF, R[cur], D, uc, D, FF, 0.5f, &pend);
         /* attention: fused q|k|v projection written into cache rows pos .. pos+c-1 */
-        nk_gemm_ln(g, res, D, W->wqkv, D, NULL, kv, 3 * D, rows, uc, 3 * D, D, NK_ACT_NONE, 0, 1.0f, 1, W->ln_att_g,
-                   W->ln_att_b, NULL, NULL, NULL, lnbuf, eps);
+        LN_GEMM(W->wqkv, kv, 3 * D, rows, 3 * D, NK_ACT_NONE, W->ln_att_g, W->ln_att_b);
         if (fuse_att) {
-            /* the heads' partial rows stay pending; the conv module's LN-fused pw1 adds them to the
-             * residual in head order and writes the updated residual to the other buffer */
-            nk_resid_t pend;
+            /* the heads' partial rows stay pending for the conv module's LN-fused pw1 */
             nk_attention_out_desc_pend(g, kv, 3 * D, desc, W->ptab, W->bias_u, W->bias_v, uc, (uint32_t)e->Lmax, H, dh,
                                        D, scale, W->wo, D, 1.0f, &pend);
-            cur ^= 1;
-            nk_gemm_ln_pend(g, res, D, W->pw1, D, NULL, din, D, rows, uc, 2 * D, D, NK_ACT_GLU, 0, 1.0f, 1,
-                            W->ln_conv_g, W->ln_conv_b, NULL, NULL, NULL, lnbuf, eps, &pend, R[cur]);
-            res = R[cur];
         } else {
             nk_attention_rel_desc(g, kv, 3 * D, desc, W->ptab, W->bias_u, W->bias_v, att, uc, (uint32_t)e->Lmax, H, dh,
                                   D, scale);
-            nk_gemm(g, att, D, W->wo, D, NULL, res, D, uc, D, D, NK_ACT_NONE, 1, 1.0f);
-            /* convolution module: GLU output appended to the conv history, causal depthwise conv over it */
-            nk_gemm_ln(g, res, D, W->pw1, D, NULL, din, D, rows, uc, 2 * D, D, NK_ACT_GLU, 0, 1.0f, 1, W->ln_conv_g,
-                       W->ln_conv_b, NULL, NULL, NULL, lnbuf, eps);
+            nk_gemm_pend(g, att, D, W->wo, D, R[cur], D, uc, D, D, 1.0f, &pend);
         }
+        /* convolution module: GLU output appended to the conv history, causal depthwise conv over it */
+        LN_GEMM(W->pw1, din, D, rows, 2 * D, NK_ACT_GLU, W->ln_conv_g, W->ln_conv_b);
         if (fuse_conv) {
-            nk_dwconv_pw_desc(g, din, desc, W->dw_w, W->bn_g, W->bn_b, eps, W->pw2, D, res, D, uc, D, D, 1, 1.0f);
+            nk_dwconv_pw_desc(g, din, desc, W->dw_w, W->bn_g, W->bn_b, eps, W->pw2, D, R[cur], D, uc, D, D, 1, 1.0f);
         } else {
             nk_dwconv_ln_silu_desc(g, din, desc, W->dw_w, W->bn_g, W->bn_b, y, uc, D, (uint32_t)cf->conv_kernel, eps);
-            nk_gemm(g, y, D, W->pw2, D, NULL, res, D, uc, D, D, NK_ACT_NONE, 1, 1.0f);
+            nk_gemm_pend(g, y, D, W->pw2, D, R[cur], D, uc, D, D, 1.0f, &pend);
         }
-        /* FF2 half step */
-        nk_gemm_ln(g, res, D, W->ff2_w1, D, NULL, ff, FF, NULL, uc, FF, D, NK_ACT_SILU, 0, 1.0f, 1, W->ln_ff2_g,
-                   W->ln_ff2_b, NULL, NULL, NULL, lnbuf, eps);
-        nk_gemm(g, ff, FF, W->ff2_w2, FF, NULL, res, D, uc, D, FF, NK_ACT_NONE, 1, 0.5f);
+        /* FF2 half step; its update stays pending for the next block's (or the prompt's) LayerNorm */
+        LN_GEMM(W->ff2_w1, ff, FF, NULL, FF, NK_ACT_SILU, W->ln_ff2_g, W->ln_ff2_b);
+        nk_gemm_pend(g, ff, FF, W->ff2_w2, FF, R[cur], D, uc, D, FF, 0.5f, &pend);
     }
+#undef LN_GEMM
     /* last output norm in the prompt GEMM's prologue, language prompt (one-hot folded into the
      * bias) and joint encoder projection */
     const layer_dev_t *Wl = &m->L[nl - 1];
     const uint32_t PH = (uint32_t)cf->prompt_hidden, NP = (uint32_t)cf->num_prompts, JH = (uint32_t)cf->joint_hidden;
     float *ph = gpu_buf_dptr(e->ph), *pr = gpu_buf_dptr(e->prompted);
     float *hn = dump ? R[cur ^ 1] : NULL;
-    nk_gemm_ln(g, R[cur], D, m->prompt_w0, D + NP, m->prompt_b0_eff, ph, PH, NULL, uc, PH, D, NK_ACT_RELU, 0, 1.0f, 1,
-               Wl->ln_out_g, Wl->ln_out_b, NULL, NULL, hn, lnbuf, eps);
+    nk_gemm_ln_pend(g, R[cur], D, m->prompt_w0, D + NP, m->prompt_b0_eff, ph, PH, NULL, uc, PH, D, NK_ACT_RELU, 0, 1.0f,
+                    1, Wl->ln_out_g, Wl->ln_out_b, NULL, NULL, hn, lnbuf, eps, &pend,
+                    pend.nparts ? xdead : NULL);
     if (dump) nk_copy2d(g, hn, D, dump + (size_t)(nl - 1) * D, D * nl, uc, D);
     nk_gemm(g, ph, PH, m->prompt_w2, PH, m->prompt_b2, pr, D, uc, D, PH, NK_ACT_NONE, 0, 1.0f);
     nk_gemm(g, pr, D, m->joint_enc_w, D, m->joint_enc_b, gpu_buf_dptr(e->joint_enc), JH, uc, JH, D, NK_ACT_NONE, 0, 1.0f);

@@ -66,7 +66,12 @@ int nk_gemm_fr_ksplit(int on) {
 static fr_plan_t fr_plan(uint32_t nout, uint32_t K, int act, int accumulate, int has_bias, int ln) {
     const uint32_t S = K / 32;
     fr_plan_t p = { 4, 8, 1 };
-    if (ln || act == NK_ACT_GLU) return p;
+    if (ln) { /* K == 1024: eight wavefronts of four K steps (two LayerNorm rows each) */
+        p.W = 8;
+        p.SPW = 4;
+        return p;
+    }
+    if (act == NK_ACT_GLU) return p;
     if (g_fr_ksplit && accumulate && act == NK_ACT_NONE && !has_bias && (nout + 15) / 16 < 128 && S % 4 == 0 &&
         S / 4 <= 32) {
         p.KS = 4;
@@ -80,9 +85,10 @@ static fr_plan_t fr_plan(uint32_t nout, uint32_t K, int act, int accumulate, int
     return p;
 }
 
-static const char *fr_name(fr_plan_t p, int act, int ln) {
+static const char *fr_name(fr_plan_t p, int act, int ln, int fold) {
     static char buf[40];
-    snprintf(buf, sizeof buf, "gemm_fr%s%s_w%us%u", ln ? "_ln" : "", act == NK_ACT_GLU ? "_glu" : "", p.W, p.SPW);
+    snprintf(buf, sizeof buf, "gemm_fr%s%s_w%us%u%s", ln ? "_ln" : "", act == NK_ACT_GLU ? "_glu" : "", p.W, p.SPW,
+             fold ? "_f" : "");
     return buf;
 }
 
@@ -113,7 +119,7 @@ const char *nk_gemm_kernel_name(uint32_t M, uint32_t N, uint32_t K, int act) {
         gemv_shape(N, K, act, &kch, &nc);
         snprintf(buf, sizeof buf, "gemv_r%u_n%u_k%u", M, nc, kch);
         return buf;
-    case K_FR: return fr_name(fr_plan(act == NK_ACT_GLU ? N / 2 : N, K, act, 0, 1, 0), act, 0);
+    case K_FR: return fr_name(fr_plan(act == NK_ACT_GLU ? N / 2 : N, K, act, 0, 1, 0), act, 0, 0);
     default: return "gemm_m*";
     }
 }
@@ -302,11 +308,24 @@ int nk_gemm_argmax_rows(gpu_t *g, const float *A, uint32_t lda, const uint16_t *
     return gpu_launch(g, "gemm_mx64x64_argmax", &a, sizeof a, 8 * per, 1, 1, 256, 1, 1);
 }
 
-/* The GEMM with an optional LayerNorm prologue on A.  The weight-streaming GEMV applies it in
- * registers; the MFMA kernels get it from separate LayerNorm launches into ln.tmp. */
+/* The GEMM with an optional LayerNorm prologue on A.  The weight-streaming GEMV (K <= 1024) and the
+ * few-row MFMA kernel (K == 1024) apply it in their prologue; other kernels get it from separate
+ * LayerNorm launches into ln.tmp.  With pend_out set, a residual update whose kernel splits K
+ * (the few-row kernel) is left pending: its partial rows are returned in *pend_out and C is not
+ * touched; otherwise *pend_out is emptied and C updated. */
+#define FR_FOLD_PARTS 4 /* partial rows the few-row kernel's fold prologue takes */
+static int gemm_core_p(gpu_t *g, const float *A, uint32_t lda, const uint16_t *W, uint32_t ldw, const float *bias,
+                       float *C, uint32_t ldc, const int *crow, uint32_t M, uint32_t N, uint32_t K, int act,
+                       int accumulate, float alpha, const ln_pro_t *ln, nk_resid_t *pend_out);
 static int gemm_core(gpu_t *g, const float *A, uint32_t lda, const uint16_t *W, uint32_t ldw, const float *bias,
                      float *C, uint32_t ldc, const int *crow, uint32_t M, uint32_t N, uint32_t K, int act,
                      int accumulate, float alpha, const ln_pro_t *ln) {
+    return gemm_core_p(g, A, lda, W, ldw, bias, C, ldc, crow, M, N, K, act, accumulate, alpha, ln, NULL);
+}
+static int gemm_core_p(gpu_t *g, const float *A, uint32_t lda, const uint16_t *W, uint32_t ldw, const float *bias,
+                       float *C, uint32_t ldc, const int *crow, uint32_t M, uint32_t N, uint32_t K, int act,
+                       int accumulate, float alpha, const ln_pro_t *ln, nk_resid_t *pend_out) {
+    if (pend_out) memset(pend_out, 0, sizeof *pend_out);
     if (!M) return 0;
     if (!N || !K || (act == NK_ACT_GLU && (N & 1))) return bad(g, "gemm: bad shape");
     if (!aligned16(A) || !aligned16(W) || lda % 4 || ldw % 8 || K % 8 || K > lda || K > ldw)
@@ -327,10 +346,13 @@ static int gemm_core(gpu_t *g, const float *A, uint32_t lda, const uint16_t *W, 
         plain.fold_out = NULL;
         return gemm_core(g, ln->fold_out, lda, W, ldw, bias, C, ldc, crow, M, N, K, act, accumulate, alpha, &plain);
     }
+    const int fold_fused = fold && ln_fused &&
+                           ((kind == K_GEMV && K % 4 == 0 && M <= 4) || (kind == K_FR && ln->pend->nparts <= FR_FOLD_PARTS));
     if (fold) {
-        if (!ln->fold_out || ln->fold_out == A || lda % 4) return bad(g, "gemm: a pending update needs its own output rows");
-        if (!(kind == K_GEMV && ln_fused && K % 4 == 0 && M <= 4)) {
+        if (ln->fold_out && (ln->fold_out == A || lda % 4)) return bad(g, "gemm: a pending update needs its own output rows");
+        if (!fold_fused) {
             /* kernels without the fold prologue: apply the update to a copy of A, then as usual */
+            if (!ln->fold_out) return bad(g, "gemm: this kernel applies a pending update only through output rows (Xf)");
             if (nk_copy2d(g, A, lda, ln->fold_out, lda, M, K)) return -1;
             if (nk_resid_fold(g, ln->fold_out, lda, M, K, ln->pend)) return -1;
             ln_pro_t plain = *ln;
@@ -393,15 +415,27 @@ static int gemm_core(gpu_t *g, const float *A, uint32_t lda, const uint16_t *W, 
         if (!a.bias) a.bias = gpu_zeros(g);
         if (!a.crow) a.crow = gpu_iota(g);
         const uint32_t tiles = (nout + 15) / 16;
+        if (fold) {
+            /* the LayerNorm prologue adds the pending update to A first (gemm_fr_ln*_f) */
+            a.fold = ln->pend->parts;
+            a.fold_n = ln->pend->nparts;
+            a.fold_alpha = ln->pend->alpha;
+            a.fold_out = ln->fold_out;
+        }
         if (p.KS > 1) {
-            /* the K shares' partial rows, folded into C in share order by a second launch */
+            /* the K shares' partial rows: left pending for the caller, or folded into C in share
+             * order by a second launch */
             a.ws = gpu_scratch_ws(g, (size_t)p.KS * M * nout);
             if (!a.ws) return bad(g, "gemm: split-K scratch unavailable (size it before capture)");
-            if (gpu_launch(g, fr_name(p, act, ln_fused), &a, sizeof a, tiles, p.KS, 1, 64 * p.W, 1, 1)) return -1;
+            if (gpu_launch(g, fr_name(p, act, ln_fused, 0), &a, sizeof a, tiles, p.KS, 1, 64 * p.W, 1, 1)) return -1;
             const nk_resid_t pend = { a.ws, p.KS, alpha };
+            if (pend_out) {
+                *pend_out = pend;
+                return 0;
+            }
             return nk_resid_fold(g, C, ldc, M, nout, &pend);
         }
-        return gpu_launch(g, fr_name(p, act, ln_fused), &a, sizeof a, tiles, p.KS, 1, 64 * p.W, 1, 1);
+        return gpu_launch(g, fr_name(p, act, ln_fused, fold), &a, sizeof a, tiles, p.KS, 1, 64 * p.W, 1, 1);
     }
     const int glu = act == NK_ACT_GLU;
     if (g_force != K_MM_OLD) {
@@ -440,6 +474,12 @@ int nk_gemm_ln(gpu_t *g, const float *A, uint32_t lda, const uint16_t *W, uint32
     const ln_pro_t ln = { ln_mode, g1, b1, g2, b2, ln_out, tmp, eps, NULL, NULL };
     if (ln_mode < 0 || ln_mode > 2) return bad(g, "gemm: ln_mode must be 0, 1 or 2");
     return gemm_core(g, A, lda, W, ldw, bias, C, ldc, crow, M, N, K, act, accumulate, alpha, &ln);
+}
+
+int nk_gemm_pend(gpu_t *g, const float *A, uint32_t lda, const uint16_t *W, uint32_t ldw, float *C, uint32_t ldc,
+                 uint32_t M, uint32_t N, uint32_t K, float alpha, nk_resid_t *pend) {
+    if (!pend) return bad(g, "gemm_pend: pend is required");
+    return gemm_core_p(g, A, lda, W, ldw, NULL, C, ldc, NULL, M, N, K, NK_ACT_NONE, 1, alpha, NULL, pend);
 }
 
 int nk_gemm_ln_pend(gpu_t *g, const float *A, uint32_t lda, const uint16_t *W, uint32_t ldw, const float *bias,

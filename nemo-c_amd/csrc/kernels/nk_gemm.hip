@@ -51,10 +51,19 @@ __device__ __forceinline__ void ln_wave4(floatx4 (&v)[4], const floatx4 (&g)[4],
 /* grid = (ceil(nout/16), KS): workgroup (tile, ks) takes the K steps [ks*S/KS, (ks+1)*S/KS) of the
  * S = K/32 steps, wavefront w the SPW steps from w*SPW within them.  With KS > 1 (the host uses it
  * only for residual updates: accumulate, no bias, no activation, identity rows) every workgroup
- * writes its share as partial rows and the host folds them into C in share order with one more
- * launch (resid_fold), so no result depends on which workgroup finishes first. */
-template <int W, int SPW, bool LNA, bool GLU>
-__device__ __forceinline__ void fr_impl(const NkGemmArgs &a, float *sA, floatx4 *sred) {
+ * writes its share as partial rows, which are added to C in share order afterwards (by resid_fold,
+ * or by the LayerNorm prologue of the GEMM that reads C next), so no result depends on which
+ * workgroup finishes first.
+ * FOLD (with LNA): the activation rows are A plus a pending residual update,
+ * A + alpha * (((0 + p0) + p1) + ...) with at most FR_FOLD_PARTS partial rows, formed by each
+ * wavefront for the rows it normalises (the order and form of resid_fold); workgroup (0, 0) writes
+ * them to fold_out when it is set.  The LayerNorm parameters then pass through LDS (sP), so that
+ * they load with the rows and the parts without holding registers through the fold. */
+#define FR_FOLD_PARTS 4
+template <int W, int SPW, bool LNA, bool GLU, bool FOLD = false>
+__device__ __forceinline__ void fr_impl(const NkGemmArgs &a, float *sA, floatx4 *sred, floatx4 *sP = nullptr) {
+    static_assert(!FOLD || LNA, "the fold feeds the LayerNorm prologue");
+    constexpr int RPW = 16 / W; /* LayerNorm rows per wavefront: wave, wave + W, ... */
     const u32 tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const u32 nout = GLU ? a.N / 2 : a.N;
     const u32 n0 = blockIdx.x * 16;
@@ -66,21 +75,49 @@ __device__ __forceinline__ void fr_impl(const NkGemmArgs &a, float *sA, floatx4 
     const u32 m = lane & 15, kq = 8 * (lane >> 4);
     const bool mrow = m < M;
 
-    /* LayerNorm variant: wavefront w normalises rows w, w+4, w+8, w+12 (those below M) */
-    floatx4 v[LNA ? 4 : 1][4], g1[4], b1[4], g2[4], b2[4];
-    if constexpr (LNA) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const u32 r = min(wave + 4 * i, M - 1);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) v[i][j] = ((const floatx4 *)(a.A + (u64)r * a.lda))[lane + 64 * j];
-        }
+    /* LayerNorm variant: wavefront w normalises rows w, w + W, ... (those below M).  Its parameters
+     * load with the rows, or, with FOLD, once the partial rows are summed (so the registers of
+     * the two are never live together) */
+    floatx4 v[LNA ? RPW : 1][4], g1[4], b1[4], g2[4], b2[4];
+    floatx4 fp[FOLD ? RPW : 1][FOLD ? FR_FOLD_PARTS : 1][4];
+    auto ln_params = [&]() {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             g1[j] = ((const floatx4 *)a.ln_g1)[lane + 64 * j];
             b1[j] = ((const floatx4 *)a.ln_b1)[lane + 64 * j];
             g2[j] = ((const floatx4 *)(a.ln_mode == 2 ? a.ln_g2 : a.ln_g1))[lane + 64 * j];
             b2[j] = ((const floatx4 *)(a.ln_mode == 2 ? a.ln_b2 : a.ln_b1))[lane + 64 * j];
+        }
+    };
+    if constexpr (LNA) {
+#pragma unroll
+        for (int i = 0; i < RPW; ++i) {
+            const u32 r = min(wave + W * i, M - 1);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) v[i][j] = ((const floatx4 *)(a.A + (u64)r * a.lda))[lane + 64 * j];
+            if constexpr (FOLD) {
+#pragma unroll
+                for (int h = 0; h < FR_FOLD_PARTS; ++h)
+                    if ((u32)h < a.fold_n)
+#pragma unroll
+                        for (int j = 0; j < 4; ++j)
+                            fp[i][h][j] = ((const floatx4 *)(a.fold + ((u64)h * M + r) * a.K))[lane + 64 * j];
+            }
+        }
+        if constexpr (!FOLD) ln_params();
+    }
+    /* FOLD: this thread's float4 c = tid % 256 of two parameters: g1 and g2 (wavefronts 0-3) or b1
+     * and b2 (wavefronts 4-7); the choice is per wavefront (a scalar branch) */
+    floatx4 pq[FOLD ? 2 : 1];
+    if constexpr (FOLD) {
+        const u32 c = tid & 255;
+        const bool two = a.ln_mode == 2;
+        if (wave < 4) {
+            pq[0] = ((const floatx4 *)a.ln_g1)[c];
+            pq[1] = ((const floatx4 *)(two ? a.ln_g2 : a.ln_g1))[c];
+        } else {
+            pq[0] = ((const floatx4 *)a.ln_b1)[c];
+            pq[1] = ((const floatx4 *)(two ? a.ln_b2 : a.ln_b1))[c];
         }
     }
 
@@ -132,12 +169,49 @@ __device__ __forceinline__ void fr_impl(const NkGemmArgs &a, float *sA, floatx4 
     for (int i = 0; i < 4; ++i) ec[i] = a.C[(u64)(u32)erow[i] * a.ldc + col];
 
     /* 2. LayerNorm of the activation rows into LDS while the weights stream in */
+    if constexpr (FOLD) {
+        static_assert(W == 8, "the parameter staging assumes 512 threads");
+        /* sP: g1 [0, 256), b1 [256, 512), g2 [512, 768), b2 [768, 1024) */
+        sP[tid] = pq[0];
+        sP[(tid & 255) + (wave < 4 ? 512 : 768)] = pq[1];
+        __syncthreads();
+    }
     if constexpr (LNA) {
         const float D = (float)a.K;
         const bool write1 = a.ln_out && blockIdx.x == 0 && blockIdx.y == 0;
+        if constexpr (FOLD) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const u32 r = wave + 4 * i;
+            for (int i = 0; i < RPW; ++i) {
+                const u32 r = wave + W * i;
+                if (r >= M) continue;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    floatx4 t = { 0.f, 0.f, 0.f, 0.f };
+#pragma unroll
+                    for (int h = 0; h < FR_FOLD_PARTS; ++h)
+                        if ((u32)h < a.fold_n) {
+                            t.x += fp[i][h][j].x; t.y += fp[i][h][j].y; t.z += fp[i][h][j].z; t.w += fp[i][h][j].w;
+                        }
+                    floatx4 x = v[i][j];
+                    x.x = x.x + t.x * a.fold_alpha; x.y = x.y + t.y * a.fold_alpha;
+                    x.z = x.z + t.z * a.fold_alpha; x.w = x.w + t.w * a.fold_alpha;
+                    v[i][j] = x;
+                }
+                if (a.fold_out && blockIdx.x == 0 && blockIdx.y == 0)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) ((floatx4 *)(a.fold_out + (u64)r * a.lda))[lane + 64 * j] = v[i][j];
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                g1[j] = sP[lane + 64 * j];
+                b1[j] = sP[256 + lane + 64 * j];
+                g2[j] = sP[512 + lane + 64 * j];
+                b2[j] = sP[768 + lane + 64 * j];
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < RPW; ++i) {
+            const u32 r = wave + W * i;
             if (r < M) {
                 ln_wave4(v[i], g1, b1, D, a.ln_eps);
                 if (write1)
@@ -230,15 +304,19 @@ GEMM_FR(gemm_fr_w16s8, 16, 8, false)
 GEMM_FR(gemm_fr_w16s9, 16, 9, false)
 GEMM_FR(gemm_fr_glu_w4s8, 4, 8, true)
 
-/* LayerNorm prologue variants: K == 1024, M <= 16 */
-#define GEMM_FR_LN(NAME, GLU)                                                                            \
-    extern "C" __global__ __launch_bounds__(256) void NAME(const NkGemmArgs a) {                         \
+/* LayerNorm prologue variants: K == 1024, M <= 16; 8 wavefronts (two rows each for the LayerNorm
+ * and the fold), four K steps each; _f: with the pending-update fold */
+#define GEMM_FR_LN(NAME, GLU, FOLD)                                                                      \
+    extern "C" __global__ __launch_bounds__(512) void NAME(const NkGemmArgs a) {                         \
         __shared__ float sA[16 * 1024];                                                                  \
-        __shared__ floatx4 sred[2 * 4 * 64];                                                             \
-        fr_impl<4, 8, true, GLU>(a, sA, sred);                                                           \
+        __shared__ floatx4 sred[2 * 8 * 64];                                                             \
+        __shared__ floatx4 sP[FOLD ? 1024 : 1];                                                          \
+        fr_impl<8, 4, true, GLU, FOLD>(a, sA, sred, sP);                                                 \
     }
-GEMM_FR_LN(gemm_fr_ln_w4s8, false)
-GEMM_FR_LN(gemm_fr_ln_glu_w4s8, true)
+GEMM_FR_LN(gemm_fr_ln_w8s4, false, false)
+GEMM_FR_LN(gemm_fr_ln_glu_w8s4, true, false)
+GEMM_FR_LN(gemm_fr_ln_w8s4_f, false, true)
+GEMM_FR_LN(gemm_fr_ln_glu_w8s4_f, true, true)
 
 /* ---- many-row MFMA GEMM ---------------------------------------------------------------------
  * grid = (ceil(N / 64), ceil(M / 64)), block = 256 (2 x 2 wavefronts, 32 x 32 outputs each).

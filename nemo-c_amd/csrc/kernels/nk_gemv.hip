@@ -162,7 +162,7 @@ __device__ __forceinline__ void gemv_impl(const NkGemmArgs &a, float *xs = nullp
                 v.x = v.x + t.x * a.fold_alpha; v.y = v.y + t.y * a.fold_alpha;
                 v.z = v.z + t.z * a.fold_alpha; v.w = v.w + t.w * a.fold_alpha;
                 ((floatx4 *)(xs + r * 1024))[c4] = v;
-                if (blockIdx.x == 0) ((floatx4 *)(a.fold_out + (u64)r * a.lda))[c4] = v;
+                if (blockIdx.x == 0 && a.fold_out) ((floatx4 *)(a.fold_out + (u64)r * a.lda))[c4] = v;
             }
         }
         __syncthreads();

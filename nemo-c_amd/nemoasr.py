@@ -115,6 +115,7 @@ API = {
     "nk_layernorm2_split": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32, C.c_float]),
     "nk_gemm_resid": (C.c_int, [_vp, _vp, _vp, _u32, _vp, _u32, _vp, _u32, _u32, _u32, _u32, C.c_float, _vp]),
     "nk_resid_fold": (C.c_int, [_vp, _vp, _u32, _u32, _u32, _vp]),
+    "nk_gemm_pend": (C.c_int, [_vp, _vp, _u32, _vp, _u32, _vp, _u32, _u32, _u32, _u32, C.c_float, _vp]),
     "nk_gemm_ln_pend": (C.c_int, [_vp, _vp, _u32, _vp, _u32, _vp, _vp, _u32, _vp, _u32, _u32, _u32, C.c_int, C.c_int,
                                   C.c_float, C.c_int, _vp, _vp, _vp, _vp, _vp, _vp, C.c_float, _vp, _vp]),
     "nk_attention_out_desc_pend": (C.c_int, [_vp, _vp, _u32, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, C.c_float,

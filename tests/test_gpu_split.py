@@ -243,14 +243,18 @@ def test_resid_pending_folded_by_layernorm(gpu, M, K, split_in, paired):
     assert rel_err(out[2][0], ref) < 2e-5
 
 
-@pytest.mark.parametrize("M,nparts,N,act,mode", [(1, 8, 2048, 3, 1), (2, 8, 2048, 3, 1), (4, 8, 2048, 3, 1),
-                                                 (3, 3, 4096, 1, 2), (1, 11, 3072, 0, 1), (7, 8, 2048, 3, 1),
-                                                 (1, 0, 2048, 3, 1)])
-def test_gemm_ln_pending_fold_bits(gpu, M, nparts, N, act, mode):
-    """A pending residual update (partial rows, e.g. the fused attention's eight heads) applied by the
-    LayerNorm-fused GEMM that reads the residual next (nk_gemm_ln_pend: inside the GEMV prologue for
-    M <= 4; a copy and nk_resid_fold first otherwise) gives, bit for bit, the updated residual and
-    the outputs of nk_resid_fold followed by nk_gemm_ln; the input rows are left as they were."""
+@pytest.mark.parametrize("M,nparts,N,act,mode,xf", [
+    (1, 8, 2048, 3, 1, True), (2, 8, 2048, 3, 1, True), (4, 8, 2048, 3, 1, True), (3, 3, 4096, 1, 2, True),
+    (1, 11, 3072, 0, 1, True), (7, 8, 2048, 3, 1, True), (1, 0, 2048, 3, 1, True), (2, 3, 4096, 1, 2, False),
+    (7, 4, 3072, 0, 1, True), (7, 4, 2048, 3, 1, True), (14, 4, 4096, 1, 1, True), (14, 4, 4096, 1, 2, False),
+    (16, 2, 2048, 3, 2, True), (5, 1, 1024, 0, 1, True), (7, 0, 3072, 0, 1, True)])
+def test_gemm_ln_pending_fold_bits(gpu, M, nparts, N, act, mode, xf):
+    """A pending residual update (partial rows: the fused attention's eight heads, the few-row
+    kernel's four K shares) applied by the LayerNorm-fused GEMM that reads the residual next
+    (nk_gemm_ln_pend: inside the prologue of the GEMV for M <= 4 and of the few-row kernel for
+    M <= 16 with at most four parts; a copy and nk_resid_fold first otherwise) gives, bit for bit,
+    the updated residual (when asked for) and the outputs of nk_resid_fold followed by nk_gemm_ln;
+    the input rows are left as they were."""
     import ctypes as C
 
     import nemoasr
@@ -275,7 +279,7 @@ def test_gemm_ln_pending_fold_bits(gpu, M, nparts, N, act, mode):
         if fused:
             gpu.check(L.nk_gemm_ln_pend(gpu.h, dX.ptr, K, dW.ptr, K, None, dC.ptr, nout, None, M, N, K, act, 0, 1.0,
                                         mode, dg1.ptr, db1.ptr, *ln2, dL1.ptr if mode == 2 else None, tmp.ptr, 1e-5,
-                                        C.byref(pend), dXf.ptr))
+                                        C.byref(pend), dXf.ptr if xf else None))
         else:
             gpu.check(L.nk_copy(gpu.h, dX.ptr, dXf.ptr, M * K))
             gpu.check(L.nk_resid_fold(gpu.h, dXf.ptr, K, M, K, C.byref(pend)))
@@ -285,9 +289,61 @@ def test_gemm_ln_pending_fold_bits(gpu, M, nparts, N, act, mode):
         outs.append((dX.read((M, K)), dXf.read((M, K)), dC.read((M, nout)), dL1.read((M, K)) if mode == 2 else None))
     (x0, xf0, c0, l0), (x1, xf1, c1, l1) = outs
     assert np.array_equal(bits(x1), bits(X))
-    assert np.array_equal(bits(xf1), bits(xf0))
     assert np.array_equal(bits(c1), bits(c0))
     if mode == 2:
         assert np.array_equal(bits(l1), bits(l0))
     ref = X + np.float32(0.75) * P[:nparts].sum(axis=0, dtype=np.float64).astype(np.float32)
-    assert rel_err(xf1, ref) < 1e-6
+    assert rel_err(xf0, ref) < 1e-6
+    if xf:
+        assert np.array_equal(bits(xf1), bits(xf0))
+    else:
+        assert not np.any(xf1)
+
+
+@pytest.mark.parametrize("M,N,K", [(7, 1024, 4096), (14, 1024, 1024), (16, 1024, 4096), (1, 1024, 4096),
+                                   (3, 1024, 4096)])
+def test_gemm_pend_then_fold_bits(gpu, M, N, K):
+    """A few-row residual update left pending (nk_gemm_pend: the few-row kernel's K shares, C
+    untouched) and applied by the next LayerNorm-fused GEMM gives, bit for bit, what the update
+    applied at once (nk_gemm with accumulate) followed by nk_gemm_ln gives; a kernel that does not
+    split K updates C itself and leaves nothing pending."""
+    import ctypes as C
+
+    import nemoasr
+
+    L = nemoasr.lib()
+    D, NQ = 1024, 3072
+    rng = np.random.default_rng([M, N, K, 5])
+    A = rng.standard_normal((M, K)).astype(np.float32)
+    X = rng.standard_normal((M, N)).astype(np.float32)
+    W = w_bf16(rng, N, K)
+    Wq = w_bf16(rng, NQ, D)
+    g1 = (1 + 0.1 * rng.standard_normal(D)).astype(np.float32)
+    b1 = (0.1 * rng.standard_normal(D)).astype(np.float32)
+    dA, dW, dWq, dg1, db1 = (gpu.put(a) for a in (A, W, Wq, g1, b1))
+    tmp = gpu.alloc(M * D * 4)
+    outs = []
+    for pending in (False, True):
+        dX, dXf, dQ = gpu.put(X), gpu.alloc(M * D * 4), gpu.alloc(M * NQ * 4)
+        pend = nemoasr.Resid()
+        gpu.begin()
+        if pending:
+            gpu.check(L.nk_gemm_pend(gpu.h, dA.ptr, K, dW.ptr, K, dX.ptr, N, M, N, K, 0.5, C.byref(pend)))
+            xf = dXf.ptr if pend.nparts else None
+            gpu.check(L.nk_gemm_ln_pend(gpu.h, dX.ptr, D, dWq.ptr, D, None, dQ.ptr, NQ, None, M, NQ, D, 0, 0, 1.0, 1,
+                                        dg1.ptr, db1.ptr, None, None, None, tmp.ptr, 1e-5, C.byref(pend), xf))
+        else:
+            gpu.check(L.nk_gemm(gpu.h, dA.ptr, K, dW.ptr, K, None, dX.ptr, N, M, N, K, 0, 1, 0.5))
+            gpu.check(L.nk_gemm_ln(gpu.h, dX.ptr, D, dWq.ptr, D, None, dQ.ptr, NQ, None, M, NQ, D, 0, 0, 1.0, 1,
+                                   dg1.ptr, db1.ptr, None, None, None, tmp.ptr, 1e-5))
+        gpu.end()
+        res = (dXf if pending and pend.nparts else dX).read((M, D))
+        outs.append((res, dQ.read((M, NQ)), pend.nparts, dX.read((M, D))))
+    (r0, q0, _, _), (r1, q1, nparts, x1) = outs
+    assert np.array_equal(bits(r1), bits(r0))
+    assert np.array_equal(bits(q1), bits(q0))
+    if nparts:
+        assert nparts == 4
+        assert np.array_equal(bits(x1), bits(X))
+    ref = oracle.gemm(A, W, None, 0, True, 0.5, C0=X)
+    assert rel_err(r1, ref) < 2e-5
