@@ -62,6 +62,8 @@ def bench_gemm(gpu, M, N, K, act, acc, alpha, ln_mode, ldw, has_bias, copies, re
                             dT.ptr, 1e-5)
 
     name = L.nk_gemm_kernel_name(M, N, K, act).decode()
+    if ln_mode and name.startswith("gemm_fr") and K == 1024:
+        name = "gemm_fr_ln*"  # the LayerNorm-fused few-row kernels (nk_gemm_kernel_name names the plain GEMM's)
     # graph replay
     gpu.begin()
     gpu.check(L.gpu_capture_begin(gpu.h))
