@@ -92,11 +92,15 @@ static const char *fr_name(fr_plan_t p, int act, int ln, int fold) {
     return buf;
 }
 
-static int pick(uint32_t M, uint32_t K, int act) {
+static int pick(uint32_t M, uint32_t N, uint32_t K, int act) {
     const int gemv_ok = (M <= 2 && K <= 64 * 8 * 9) || (M <= 4 && K <= 64 * 8 * 2);
     if ((g_force == K_GEMV || g_force == 1) && gemv_ok) return K_GEMV;
     if (g_force == K_FR && fr_ok(M, K, act)) return K_FR;
     if ((g_force == K_MR || g_force == K_MM_OLD) && K % 32 == 0) return K_MR;
+    /* 3-4 rows of the wide matrices (N >= 3072: QKV, FF up): the few-row MFMA kernel, measured
+     * faster than the GEMV there (QKV at 4 rows 6.1 against 10.1 us, FF up 6.5 against 8.2 us);
+     * the narrower ones stay on the GEMV (pw1 5.9 against 7.1 us, out 3.7 against 5.9 us) */
+    if (gemv_ok && M >= 3 && N >= 3072 && fr_ok(M, K, act)) return K_FR;
     if (gemv_ok) return K_GEMV;
     if (fr_ok(M, K, act)) return K_FR;
     return K_MR;
@@ -114,7 +118,7 @@ static void gemv_shape(uint32_t N, uint32_t K, int act, uint32_t *kch, uint32_t 
 const char *nk_gemm_kernel_name(uint32_t M, uint32_t N, uint32_t K, int act) {
     static char buf[32];
     uint32_t kch, nc;
-    switch (pick(M, K, act)) {
+    switch (pick(M, N, K, act)) {
     case K_GEMV:
         gemv_shape(N, K, act, &kch, &nc);
         snprintf(buf, sizeof buf, "gemv_r%u_n%u_k%u", M, nc, kch);
@@ -334,7 +338,7 @@ static int gemm_core_p(gpu_t *g, const float *A, uint32_t lda, const uint16_t *W
     if (ldc < nout) return bad(g, "gemm: ldc < output width");
     /* batched streams: always the many-row kernels (a row's result then does not depend on how many
      * other rows share the launch) */
-    const int kind = gpu_many_rows(g) && !g_force && K % 32 == 0 ? K_MR : pick(M, K, act);
+    const int kind = gpu_many_rows(g) && !g_force && K % 32 == 0 ? K_MR : pick(M, N, K, act);
     const int ln_fused = ln && ln->mode && K == lda &&
                          ((kind == K_GEMV && K <= 1024) || (kind == K_FR && K == 1024 && M <= 16));
     const int fold = ln && ln->mode && ln->pend && ln->pend->nparts;

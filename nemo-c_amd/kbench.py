@@ -255,6 +255,8 @@ def bench_copy(gpu, nbytes, reps):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--rows", default="1,7,14")
+    ap.add_argument("--rows-force", default="0", help="few-row kernel selections to compare (nk_gemm_force: 0 policy, "
+                    "2 few-row MFMA, 4 weight-streaming GEMV where it applies), e.g. 0,2")
     ap.add_argument("--reps", type=int, default=3)
     ap.add_argument("--copies", type=int, default=48, help="distinct weight matrices cycled per replay")
     ap.add_argument("--json", default=None)
@@ -276,11 +278,13 @@ def main():
     fg, fk = bench_floor(gpu, 48, a.reps)
     out["floor"] = {"graph_us": round(fg, 3), "kernel_us": round(fk, 3)}
     print(f"launch floor (1 KB copy): graph {fg:7.2f} us  kernel {fk:7.2f} us", flush=True)
-    for M in ([] if a.no_gemm else [int(x) for x in a.rows.split(",")]):
+    for M, force in ([] if a.no_gemm else [(int(x), int(f)) for x in a.rows.split(",") for f in a.rows_force.split(",")]):
         for (label, N, K, act, acc, alpha, ln, ldw, hb) in SHAPES:
             if label == "lstm" and M > 1:
                 continue
+            nemoasr.lib().nk_gemm_force(force)
             name, gus, kus, cnt = bench_gemm(gpu, M, N, K, act, acc, alpha, ln, ldw, hb, a.copies, a.reps)
+            nemoasr.lib().nk_gemm_force(0)
             wb = 2.0 * N * K
             rec = {"M": M, "shape": label, "N": N, "K": K, "kernel": name, "graph_us": round(gus, 3),
                    "kernel_us": round(kus, 3), "weight_bytes": wb, "gbs_kernel": round(wb / (kus * 1e-6) / 1e9, 1),

@@ -66,7 +66,7 @@ def test_tiny_stream_parity(latency):
     s.close()
 
 
-@pytest.mark.parametrize("latency,seconds", [(80, 2.0), (560, 3.0), (1120, 4.0)])
+@pytest.mark.parametrize("latency,seconds", [(80, 2.0), (320, 2.0), (560, 3.0), (1120, 4.0)])
 def test_full_stream_parity(latency, seconds):
     mdir = model_dir("full")
     om, o, s, d = run_pair(mdir, latency, seconds, seed=3, graphs=False)
