@@ -93,7 +93,11 @@ static const char *fr_name(fr_plan_t p, int act, int ln, int fold) {
 }
 
 static int pick(uint32_t M, uint32_t N, uint32_t K, int act) {
-    const int gemv_ok = (M <= 2 && K <= 64 * 8 * 9) || (M <= 4 && K <= 64 * 8 * 2);
+    /* 5-8 rows: the 1024-row matrices (one weight row per wavefront, 256 workgroups: one per CU),
+     * measured faster than the few-row MFMA kernel there (out / pw2 at 7 rows 5.0 against 5.9 us);
+     * 640 rows (160 workgroups) were not */
+    const int gemv_ok = (M <= 2 && K <= 64 * 8 * 9) || (M <= 4 && K <= 64 * 8 * 2) ||
+                        (M <= 8 && K <= 64 * 8 * 2 && N == 1024 && act != NK_ACT_GLU);
     if ((g_force == K_GEMV || g_force == 1) && gemv_ok) return K_GEMV;
     if (g_force == K_FR && fr_ok(M, K, act)) return K_FR;
     if ((g_force == K_MR || g_force == K_MM_OLD) && K % 32 == 0) return K_MR;

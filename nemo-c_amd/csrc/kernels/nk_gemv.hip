@@ -18,7 +18,8 @@
  * (reference src/encoder.c:180-187).  Dot products are finished with DPP row rotations plus four
  * lane reads, and lanes 0..M*outputs-1 each store one output.
  *
- * Instantiated for R <= 2 at every K up to 4608 and for R = 3, 4 at K <= 1024.
+ * Instantiated for R <= 2 at every K up to 4608, for R = 3, 4 at K <= 1024, and for R = 5..8 with
+ * one weight row per wavefront at K <= 1024 (the 1024-row matrices of 7-row chunks).
  * Replaces gemm_spec (reference src/kernels.metal:51-118) plus the layernorm / layernorm2
  * launches in front of it (src/encoder.c:155, :159, :169, :177, :180-186). */
 #include "nk_common.h"
@@ -275,6 +276,11 @@ GEMV2_R(1)
 GEMV2_R(2)
 GEMV2_SMALLK(3)
 GEMV2_SMALLK(4)
+#define GEMV2_NARROW(R) GEMV2(R, 1, 1) GEMV2(R, 1, 2)
+GEMV2_NARROW(5)
+GEMV2_NARROW(6)
+GEMV2_NARROW(7)
+GEMV2_NARROW(8)
 
 /* the FOLD variants (suffix _f): K <= 1024 with the LayerNorm prologue */
 #define GEMV2F(R, NC, KCH)                                                                              \
