@@ -140,7 +140,7 @@ struct nemoasr_batch {
     int *stage_dtab, *stage_amax;
     /* device-resident loop (kernels/nk_bdec.hip) */
     int device_dec, W, tok_ld;
-    gpu_buf_t *bst, *bsetup, *btok, *lin1, *tx, *wcati[2], *bi[2], *keys, *brows, *bcnt;
+    gpu_buf_t *bst, *bsetup, *btok, *lin1, *tx, *wcati[2], *bi[2], *keys, *brows, *bcnt, *pre0;
     int nkeys;
     NkBDecStream *stage_bst;
     int *stage_bsetup, *stage_btok;
@@ -401,12 +401,14 @@ static int bdec_state_reset(nemoasr_batch_t *b, int s) {
     return gpu_upload(b->g, (NkBDecStream *)gpu_buf_dptr(b->bst) + s, &x, sizeof x);
 }
 
-/* device state of one stream back to that after open: zero LSTM states and conv history */
+/* device state of one stream back to that after open: zero LSTM states (and so zero hidden halves
+ * of layer 0) and conv history */
 static int stream_zero_device(nemoasr_batch_t *b, int s) {
     const size_t D = (size_t)b->m->cfg.d_model, P = (size_t)b->P;
     const size_t n = (size_t)b->conv_left * D > 8 * P ? (size_t)b->conv_left * D : 8 * P;
     float *z = calloc(n, sizeof(float));
     int rc = gpu_upload(b->g, (float *)gpu_buf_dptr(b->hc) + (size_t)s * 8 * P, z, 8 * P * sizeof(float));
+    rc |= gpu_upload(b->g, (float *)gpu_buf_dptr(b->pre0) + (size_t)s * 8 * P, z, 8 * P * sizeof(float));
     for (int l = 0; l < b->m->cfg.n_layers; ++l)
         rc |= gpu_upload(b->g, (float *)gpu_buf_dptr(b->din) + (size_t)l * b->din_lstride + (size_t)s * b->cap_rows * D, z,
                          (size_t)b->conv_left * D * sizeof(float));
@@ -526,6 +528,7 @@ nemoasr_batch_t *nemoasr_batch_open(const char *model_dir, const char *language,
     b->bcnt = gpu_buf_alloc(g, 2 * sizeof(int));
     b->btok = gpu_buf_alloc(g, S * (size_t)b->tok_ld * sizeof(int));
     b->lin1 = gpu_buf_alloc(g, S * 2 * P * fs);
+    b->pre0 = gpu_buf_alloc(g, S * 2 * 4 * P * fs); /* zero: the hidden half of layer 0 at h0 = 0 */
     b->stage_bst = gpu_host_alloc(g, S * sizeof(NkBDecStream));
     b->stage_bsetup = gpu_host_alloc(g, (2 * S + 2) * sizeof(int));
     b->stage_btok = gpu_host_alloc(g, S * (size_t)b->tok_ld * sizeof(int));
@@ -593,7 +596,7 @@ void nemoasr_batch_close(nemoasr_batch_t *b) {
     gpu_buf_t *bufs[] = { b->win, b->c1, b->c2, b->c3, b->c4, b->flat, b->pre_out, b->h, b->tmp, b->lnb,
                           b->ff, b->att, b->y, b->ph, b->prompted, b->joint_enc, b->kv, b->din, b->etab, b->wcat[0],
                           b->wcat[1], b->wout, b->bout, b->hc, b->lin, b->gates, b->hout, b->hout2, b->pred,
-                          b->jin, b->logits, b->amax, b->dtab, b->bst, b->bsetup, b->btok, b->lin1, b->tx,
+                          b->jin, b->logits, b->amax, b->dtab, b->bst, b->bsetup, b->btok, b->lin1, b->pre0, b->tx,
                           b->wcati[0], b->wcati[1], b->bi[0], b->bi[1], b->keys, b->ring, b->meltab, b->span_dev,
                           b->ftab_dev, b->wmap_dev, b->hrow_dev, b->hmap_dev, b->jdec[0], b->jdec[1], b->brows,
                           b->bcnt };
@@ -1289,7 +1292,9 @@ static NkBDecArgs bdec_args(nemoasr_batch_t *b) {
     a.enc = gpu_buf_dptr(b->jdec[b->dbuf]);
     a.tx = gpu_buf_dptr(b->tx);
     a.hc = gpu_buf_dptr(b->hc);
-    a.A0 = gpu_buf_dptr(b->lin);
+    a.pre0 = gpu_buf_dptr(b->pre0);
+    a.wh0 = (const uint16_t *)gpu_buf_dptr(b->wcati[0]) + b->P; /* the Wh0 half of [Wx0 | Wh0] */
+    a.wh0_ld = (uint32_t)(2 * b->P);
     a.A1 = gpu_buf_dptr(b->lin1);
     a.hout = gpu_buf_dptr(b->hout);
     a.pred = gpu_buf_dptr(b->pred);
@@ -1312,8 +1317,10 @@ typedef struct {
     NkBDecArgs d;
 } bdec_launch_t;
 
+/* grid: N / 16 column workgroups (plus gx_more) by row blocks of 64 */
 static int launch_bdec_gemm(nemoasr_batch_t *b, uint32_t par, const char *kernel, const float *A, uint32_t lda,
-                            const uint16_t *W, uint32_t ldw, const float *bias, uint32_t N, uint32_t K, uint32_t waves) {
+                            const uint16_t *W, uint32_t ldw, const float *bias, uint32_t N, uint32_t K, uint32_t waves,
+                            uint32_t gx_more) {
     bdec_launch_t x;
     memset(&x, 0, sizeof x);
     x.g.A = A;
@@ -1326,7 +1333,7 @@ static int launch_bdec_gemm(nemoasr_batch_t *b, uint32_t par, const char *kernel
     x.g.K = K;
     x.d = bdec_args(b);
     x.d.par = par;
-    return gpu_launch(b->gd, kernel, &x, sizeof x, N / 16, ((uint32_t)b->S + 63) / 64, 1, 64 * waves, 1, 1);
+    return gpu_launch(b->gd, kernel, &x, sizeof x, N / 16 + gx_more, ((uint32_t)b->S + 63) / 64, 1, 64 * waves, 1, 1);
 }
 
 static void launch_bdec_steps(nemoasr_batch_t *b, int steps) {
@@ -1337,16 +1344,15 @@ static void launch_bdec_steps(nemoasr_batch_t *b, int steps) {
         /* step parity: the rows come from counter par ^ 1, the decisions append to counter par */
         const uint32_t par = (uint32_t)k & 1u;
         a.par = par;
-        /* layer 0: the Wh0 half of the interleaved [Wx0 | Wh0] rows (row stride 2P) */
-        launch_bdec_gemm(b, par, "bdec_lstm0_w4s5", a.A0, P, (const uint16_t *)gpu_buf_dptr(b->wcati[0]) + P, 2 * P,
-                         NULL, 4 * P, P, 4);
         launch_bdec_gemm(b, par, "bdec_lstm1_w8s5", a.A1, 2 * P, gpu_buf_dptr(b->wcati[1]), 2 * P,
-                         gpu_buf_dptr(b->bi[1]), 4 * P, 2 * P, 8);
-        launch_bdec_gemm(b, par, "bdec_pred_w4s5", a.hout, P, b->m->joint_pred_w, P, b->m->joint_pred_b, J, P, 4);
+                         gpu_buf_dptr(b->bi[1]), 4 * P, 2 * P, 8, 0);
+        /* joint.pred, and the hidden half of the next step's layer 0 (4P/16 more workgroups) */
+        launch_bdec_gemm(b, par, "bdec_pred_w4s5", a.hout, P, b->m->joint_pred_w, P, b->m->joint_pred_b, J, P, 4,
+                         4 * P / 16);
         /* more than one row block: only the step's rows are scored */
         nk_gemm_argmax_rows(g, a.jin, J, gpu_buf_dptr(b->wout), J, gpu_buf_dptr(b->bout), gpu_buf_dptr(b->keys),
                             (uint32_t)b->nkeys, R, Vp, J, (uint32_t)b->V, S > 64 ? a.cnt + (par ^ 1u) : NULL, a.W);
-        gpu_launch(g, "bdec_decide", &a, sizeof a, S, 1, 1, 64, 1, 1);
+        gpu_launch(g, "bdec_decide", &a, sizeof a, S, 1, 1, 256, 1, 1);
     }
 }
 
@@ -1648,7 +1654,17 @@ int nemoasr_batch_debug_gpu_frontend(nemoasr_batch_t *b, int on) {
 
 void nemoasr_batch_debug_device_decoder(nemoasr_batch_t *b, int on) {
     dec_drain(b, NULL, 0);
+    const int was = b->device_dec;
     b->device_dec = on && b->gd && device_dec_ok(b);
+    if (b->device_dec && !was) {
+        /* the host-driven loop keeps no hidden halves of layer 0: take them from the LSTM states
+         * (h0 of every stream's two slot sets, rows 4P apart) */
+        const uint32_t P = (uint32_t)b->P, S2 = 2u * (uint32_t)b->S;
+        gpu_begin(b->gd);
+        nk_gemm(b->gd, gpu_buf_dptr(b->hc), 4 * P, (const uint16_t *)gpu_buf_dptr(b->wcati[0]) + P, 2 * P, NULL,
+                gpu_buf_dptr(b->pre0), 4 * P, S2, 4 * P, P, NK_ACT_NONE, 0, 1.0f);
+        gpu_end(b->gd, NULL, 0);
+    }
 }
 
 void nemoasr_batch_debug_set_dump(nemoasr_batch_t *b, int on) {

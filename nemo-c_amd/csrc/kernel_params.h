@@ -373,7 +373,10 @@ typedef struct {
     const float *enc;      /* joint.enc rows [*][J]                                        */
     const float *tx;       /* [blank + 1][4P] embed . Wx0^T + b0, rows interleaved by unit */
     float *hc;             /* [S][2 slot sets][h0, c0, h1, c1][P]                          */
-    float *A0;             /* [S][P] layer-0 input h0, by row                              */
+    float *pre0;           /* [S][2 slot sets][4P] Wh0 . h0 of each slot set's h0, interleaved
+                              by unit like tx                                               */
+    const u16 *wh0;        /* Wh0 rows interleaved by unit, row stride wh0_ld               */
+    u32 wh0_ld, pad3;
     float *A1;             /* [S][2P] layer-1 input [h0' | h1], by row                     */
     float *hout;           /* [S][P] new layer-1 state, input of joint.pred, by row        */
     float *pred;           /* [S][J] current prediction                                    */

@@ -1,22 +1,25 @@
 /* Device-resident greedy RNNT loop of many streams at once (the batched decoder): the reference's
  * decoder_run (src/decoder.c:92-127) for every stream of a batch, one joint evaluation per step,
- * with no host round trip per step.  A step is five launches:
- *   bdec_lstm<0>  gates = Tx[last token] + h0 . Wh0^T for all S streams, where Tx = embed . Wx0^T + b0
- *                 is a table built once per model (the embedding half of layer 0's input is one of
- *                 V rows, so its product is looked up instead of recomputed), with the LSTM cell in
- *                 the epilogue (weight rows interleaved by unit: row 4u + q is gate q of unit u, so
- *                 a 16-column tile holds the four gates of four units); streams whose prediction is
- *                 stale write their provisional layer-0 state and the layer-1 input [h0' | h1];
- *   bdec_lstm<1>  gates = [h0' | h1] . [Wx1 | Wh1]^T + b1, the same cell; writes h1' (the joint.pred
- *                 input);
+ * with no host round trip per step.  A step is four launches:
+ *   bdec_lstm1    gates = [h0' | h1] . [Wx1 | Wh1]^T + b1 with the LSTM cell in the epilogue (weight
+ *                 rows interleaved by unit: row 4u + q is gate q of unit u, so a 16-column tile
+ *                 holds the four gates of four units); writes h1' (the joint.pred input);
  *   bdec_pred     pred = h1' . Wjp^T + bjp for the streams that recomputed it, and their joint inputs
- *                 relu(enc[t + k] + pred) for the frames k of the chunk after the stream's t;
+ *                 relu(enc[t + k] + pred) for the frames k of the chunk after the stream's t.  A
+ *                 second range of workgroups takes h0' . Wh0^T, the hidden half of layer 0's gates
+ *                 for the step after, into pre0 of the provisional slot set (which the emitting
+ *                 decision commits);
  *   gemm_mx64x64_argmax  joint scores with an argmax epilogue: per row, the best (score, lowest
  *                 index) of each wavefront's 32 columns as a packed key;
- *   bdec_decide   per stream: the best key of each scored frame, the greedy rule (first non-blank
+ *   bdec_decide   per stream (four wavefronts: the first decides): the best key of each scored
+ *                 frame, the greedy rule (first non-blank
  *                 frame wins: emit, commit the provisional LSTM state, the prediction becomes stale;
- *                 blank frames reset the symbol count; max_symbols moves past the frame), then the
- *                 next step's layer-0 input h0.
+ *                 blank frames reset the symbol count; max_symbols moves past the frame), then, for
+ *                 a stream whose prediction must be recomputed, layer 0: gates = Tx[last token] +
+ *                 pre0 of the committed slot set, where Tx = embed . Wx0^T + b0 is a table built
+ *                 once per model (the embedding half of layer 0's input is one of V rows), and the
+ *                 cell, which writes the provisional layer-0 state and the layer-1 input
+ *                 [h0' | h1] of the stream's next step row.
  * After a decision every stream still inside its chunk has emitted a token, so its prediction is
  * recomputed by the next step, which also writes its joint inputs; a prediction carried over from
  * the previous chunk gets its joint inputs from bdec_setup.  The GEMM rows of a step are the
@@ -27,7 +30,7 @@
  * position.  LSTM states live in two slot sets per stream; committing a token flips the committed
  * set (the reference swaps its h/hp and c/cp buffers).
  *
- * bdec_lstm / bdec_pred are GEMMs over at most 64 rows per workgroup (grid.y = row blocks of 64):
+ * bdec_lstm1 / bdec_pred are GEMMs over at most 64 rows per workgroup (grid.y = row blocks of 64):
  * a workgroup owns 16 columns; its W wavefronts split K (SPW steps of 32 each), issue every load
  * (activations of four 16-row tiles in the MFMA A layout, weights in the B layout) before the first
  * MFMA, multiply with A split into bf16 hi + lo, and leave their partial tiles in LDS; the epilogue
@@ -133,44 +136,34 @@ __device__ __forceinline__ int append_row(const NkBDecArgs &d, u32 par, int s, i
     return slot;
 }
 
-/* LSTM layer L (0 or 1) on all streams; grid (4P/16, ceil(S/64)), 64 W threads.  Layer 0: a.A = h0
- * [S][P], a.W = Wh0 rows interleaved by unit, gates start from the table row d.tx[tok] (bias
- * included); layer 1: a.A = [h0' | h1] [S][2P], a.W = [Wx1 | Wh1] interleaved, a.bias interleaved.
- * Epilogue: thread t < 256 runs the cell of row t / 4, unit 4 blockIdx.x + t % 4. */
-template <int W, int SPW, int L>
+/* LSTM layer 1 on all streams; grid (4P/16, ceil(S/64)), 64 W threads: a.A = [h0' | h1] [S][2P],
+ * a.W = [Wx1 | Wh1] interleaved, a.bias interleaved; epilogue: thread t < 256 runs the cell of row
+ * t / 4, unit 4 blockIdx.x + t % 4. */
+template <int W, int SPW>
 __device__ __forceinline__ void bdec_lstm_impl(const NkGemmArgs &a, const NkBDecArgs &d, floatx4 *sred,
                                                BDecStage &ss) {
     static_assert(W >= 4, "the cell epilogue uses 256 threads");
-    const u32 lane = threadIdx.x & 63, r0 = blockIdx.y * 64, col = blockIdx.x * 16 + (lane & 15);
-    if (L == 0 && blockIdx.x == 0 && threadIdx.x == 0) d.cnt[d.par] = 0; /* this step's decisions append here */
+    const u32 P = d.P, lane = threadIdx.x & 63, r0 = blockIdx.y * 64, col = blockIdx.x * 16 + (lane & 15);
+    if (blockIdx.x == 0 && threadIdx.x == 0) d.cnt[d.par] = 0; /* this step's decisions append here */
     if (gridDim.y > 1 && (int)r0 >= step_rows(d)) return; /* no rows in this block */
     stage_state(d, r0, ss);
     fr64_partials<W, SPW>(a.A, a.lda, a.W + (u64)col * a.ldw, a.M, a.K, r0, sred);
     const u32 t = threadIdx.x;
     if (t >= 256) return;
-    const u32 rl = t >> 2, j = t & 3, r = r0 + rl, P = d.P, u = blockIdx.x * 4 + j;
+    const u32 rl = t >> 2, j = t & 3, r = r0 + rl, u = blockIdx.x * 4 + j;
     if (!ss.need[rl]) return;
     const u32 s = (u32)ss.s[rl];
-    const u32 kc = (u32)ss.cur[rl];
-    constexpr u32 CI = L == 0 ? 1 : 3, HI = L == 0 ? 0 : 2;
-    const float c_in = d.hc[(u64)hc_row(s, kc, CI) * P + u];
-    const float h1c = L == 0 ? d.hc[(u64)hc_row(s, kc, 2) * P + u] : 0.0f;
-    const floatx4 g0 = L == 0 ? *(const floatx4 *)(d.tx + (u64)ss.tok[rl] * 4 * P + 4 * u)
-                              : *(const floatx4 *)(a.bias + 4 * u);
+    const u32 kc = (u32)ss.cur[rl], kp = kc ^ 1u;
+    const float c_in = d.hc[(u64)hc_row(s, kc, 3) * P + u];
+    const floatx4 g0 = *(const floatx4 *)(a.bias + 4 * u);
     float g[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q) g[q] = g0[q] + tile_at<W>(sred, rl, 4 * j + q);
-    const u32 kp = kc ^ 1u;
     const float c = sigmoid_f(g[1]) * c_in + sigmoid_f(g[0]) * tanhf(g[2]);
     const float h = sigmoid_f(g[3]) * tanhf(c);
-    d.hc[(u64)hc_row(s, kp, CI) * P + u] = c;
-    d.hc[(u64)hc_row(s, kp, HI) * P + u] = h;
-    if (L == 0) {
-        d.A1[(u64)r * 2 * P + u] = h;
-        d.A1[(u64)r * 2 * P + P + u] = h1c;
-    } else {
-        d.hout[(u64)r * P + u] = h;
-    }
+    d.hc[(u64)hc_row(s, kp, 3) * P + u] = c;
+    d.hc[(u64)hc_row(s, kp, 2) * P + u] = h;
+    d.hout[(u64)r * P + u] = h;
 }
 
 /* joint inputs of step row r at column j: rows r W + k for the lim >= 1 frames after its t (loads
@@ -185,13 +178,30 @@ __device__ __forceinline__ void write_jin(const NkBDecArgs &d, u32 r, u32 j, flo
 }
 
 /* joint.pred for the streams that recompute their prediction, and their joint inputs; grid
- * (J/16, ceil(S/64)), 64 W threads; thread t handles column t % 16 of rows t / 16 + 16 i */
+ * (J/16 + 4P/16, ceil(S/64)), 64 W threads.  Workgroups x < J/16: thread t handles column t % 16 of
+ * rows t / 16 + 16 i.  Workgroups x >= J/16: h0' (the first P columns of the layer-1 input rows) .
+ * Wh0^T for columns 16 (x - J/16) + [0, 16) into pre0 of the row's provisional slot set. */
 template <int W, int SPW>
 __device__ __forceinline__ void bdec_pred_impl(const NkGemmArgs &a, const NkBDecArgs &d, floatx4 *sred,
                                                BDecStage &ss) {
-    const u32 lane = threadIdx.x & 63, r0 = blockIdx.y * 64, col = blockIdx.x * 16 + (lane & 15);
+    const u32 nb = d.J / 16, hid = blockIdx.x >= nb, bx = hid ? blockIdx.x - nb : blockIdx.x;
+    const u32 lane = threadIdx.x & 63, r0 = blockIdx.y * 64, col = bx * 16 + (lane & 15);
     if (gridDim.y > 1 && (int)r0 >= step_rows(d)) return; /* no rows in this block */
     stage_state(d, r0, ss);
+    if (hid) {
+        const u32 P = d.P;
+        fr64_partials<W, SPW>(d.A1, 2 * P, d.wh0 + (u64)col * d.wh0_ld, a.M, P, r0, sred);
+        for (u32 t = threadIdx.x; t < 256; t += 64 * W) {
+            const u32 rl = t >> 2, j = t & 3, u = bx * 4 + j;
+            if (!ss.need[rl]) continue;
+            const u32 s = (u32)ss.s[rl], kp = (u32)ss.cur[rl] ^ 1u;
+            floatx4 v;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) v[q] = tile_at<W>(sred, rl, 4 * j + q);
+            *(floatx4 *)(d.pre0 + ((u64)s * 2 + kp) * 4 * P + 4 * u) = v;
+        }
+        return;
+    }
     fr64_partials<W, SPW>(a.A, a.lda, a.W + (u64)col * a.ldw, a.M, a.K, r0, sred);
     const u32 c = threadIdx.x & 15, j = blockIdx.x * 16 + c;
     const float bias = a.bias[j];
@@ -210,24 +220,49 @@ __device__ __forceinline__ void bdec_pred_impl(const NkGemmArgs &a, const NkBDec
         __shared__ BDecStage ss;                                                                          \
         IMPL(a, d, sred, ss);                                                                             \
     }
-/* layer 0: K = P <= 640 (20 steps): 4 wavefronts x 5 steps; layer 1: K = 2P <= 1280: 8 x 5;
- * joint.pred: K = P: 4 x 5 */
-BDEC_GEMM(bdec_lstm0_w4s5, (bdec_lstm_impl<4, 5, 0>), 4, 5)
-BDEC_GEMM(bdec_lstm1_w8s5, (bdec_lstm_impl<8, 5, 1>), 8, 5)
+/* layer 1: K = 2P <= 1280: 8 wavefronts x 5 steps; joint.pred and Wh0: K = P: 4 x 5 */
+BDEC_GEMM(bdec_lstm1_w8s5, (bdec_lstm_impl<8, 5>), 8, 5)
 BDEC_GEMM(bdec_pred_w4s5, (bdec_pred_impl<4, 5>), 4, 5)
 
-/* next step's layer-0 input of stream s at step row r (one wavefront): its committed h0 (slot set
- * cur), P / 4 <= 192 float4 */
-__device__ __forceinline__ void bdec_prepare(const NkBDecArgs &a, u32 r, u32 s, int cur) {
-    const u32 n4 = a.P >> 2, lane = threadIdx.x;
-    const floatx4 *h0 = (const floatx4 *)(a.hc + (u64)hc_row(s, (u32)cur, 0) * a.P);
-    floatx4 *A = (floatx4 *)(a.A0 + (u64)r * a.P);
-    floatx4 v[3];
+/* layer 0 of stream s for its next step row r (NT threads, unit u = thread + NT i): gates =
+ * Tx[tok] + pre0 of the committed slot set cur (the table row and the hidden product in that order,
+ * as a GEMM epilogue adding its tile to the table row would), the cell, the provisional layer-0
+ * state (slot set cur ^ 1) and the layer-1 input row [h0' | h1 of slot set cur].  P <= 640. */
+template <int NT>
+__device__ __forceinline__ void bdec_cell0(const NkBDecArgs &a, u32 r, u32 s, int cur, int tok) {
+    const u32 P = a.P, lane = threadIdx.x, kc = (u32)cur, kp = kc ^ 1u;
+    const float *tx = a.tx + (u64)(u32)tok * 4 * P;
+    const float *pre = a.pre0 + ((u64)s * 2 + kc) * 4 * P;
+    constexpr int UPL = (640 + NT - 1) / NT; /* units per thread */
+    floatx4 tv[UPL], pv[UPL];
+    float cv[UPL], h1[UPL];
 #pragma unroll
-    for (int i = 0; i < 3; ++i) v[i] = h0[min(lane + 64 * i, n4 - 1)];
+    for (int i = 0; i < UPL; ++i) {
+        const u32 u = min(lane + NT * i, P - 1);
+        tv[i] = *(const floatx4 *)(tx + 4 * u);
+        pv[i] = *(const floatx4 *)(pre + 4 * u);
+        cv[i] = a.hc[(u64)hc_row(s, kc, 1) * P + u];
+        h1[i] = a.hc[(u64)hc_row(s, kc, 2) * P + u];
+    }
 #pragma unroll
-    for (int i = 0; i < 3; ++i)
-        if (lane + 64 * i < n4) A[lane + 64 * i] = v[i];
+    for (int i = 0; i < UPL; ++i) {
+        const u32 u = lane + NT * i;
+        if (u >= P) break;
+        float g[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) g[q] = tv[i][q] + pv[i][q];
+        const float c = sigmoid_f(g[1]) * cv[i] + sigmoid_f(g[0]) * tanhf(g[2]);
+        const float h = sigmoid_f(g[3]) * tanhf(c);
+        a.hc[(u64)hc_row(s, kp, 1) * P + u] = c;
+        a.hc[(u64)hc_row(s, kp, 0) * P + u] = h;
+        a.A1[(u64)r * 2 * P + u] = h;
+        a.A1[(u64)r * 2 * P + P + u] = h1[i];
+    }
+}
+
+/* the layer-0 table row of a stream's last token (the blank's row, zero input, when none) */
+__device__ __forceinline__ int tx_row_of(const NkBDecArgs &a, int last) {
+    return last >= 0 && last < (int)a.blank ? last : (int)a.blank;
 }
 
 /* new chunk: frames and first joint.enc row from the host, fresh frame position and counters; the
@@ -250,7 +285,7 @@ extern "C" __global__ __launch_bounds__(64) void bdec_setup(const NkBDecArgs a) 
         sp->need = need;
         sp->slot = slot;
     }
-    if (need) bdec_prepare(a, (u32)slot, s, cur);
+    if (need) bdec_cell0<64>(a, (u32)slot, s, cur, tx_row_of(a, last));
     if (0 < frames && pred_valid) {
         const int lim = min((int)a.W, frames);
         for (u32 j = threadIdx.x; j < a.J; j += 64) write_jin(a, (u32)slot, j, a.pred[(u64)s * a.J + j], 0, lim, erow0);
@@ -261,56 +296,64 @@ extern "C" __global__ __launch_bounds__(64) void bdec_setup(const NkBDecArgs a) 
  * (at most 16 frames, nkeys <= 64; the stream's key rows follow its step row), two exchanges finish
  * each frame's maximum, a ballot finds the first non-blank frame; then the greedy rule, and a
  * stream still inside its chunk is appended to the next step's rows with its layer-0 input. */
-extern "C" __global__ __launch_bounds__(64) void bdec_decide(const NkBDecArgs a) {
+extern "C" __global__ __launch_bounds__(256) void bdec_decide(const NkBDecArgs a) {
+    __shared__ int dres[4]; /* need, slot, cur, last of the decision, for the four wavefronts */
     const u32 s = blockIdx.x, lane = threadIdx.x, row = lane >> 2, part = lane & 3;
     NkBDecStream *sp = a.st + s;
     const int frames = sp->frames, t = sp->t;
-    if (t >= frames) return;
-    int symbols = sp->symbols, cur = sp->cur, last = sp->last_token, n_out = sp->n_out, pred_valid = 1;
-    const int rows = min(min((int)a.W, frames - t), NK_ATTC_MAX_C);
-    const bool live = (int)row < rows;
-    const unsigned long long *kr = a.keys + (u64)((u32)sp->slot * a.W + min((int)row, rows - 1)) * a.nkeys;
-    unsigned long long kv[16];
+    if (t >= frames) return; /* the same for the whole workgroup */
+    if (threadIdx.x < 64) {
+        int symbols = sp->symbols, cur = sp->cur, last = sp->last_token, n_out = sp->n_out, pred_valid = 1;
+        const int rows = min(min((int)a.W, frames - t), NK_ATTC_MAX_C);
+        const bool live = (int)row < rows;
+        const unsigned long long *kr = a.keys + (u64)((u32)sp->slot * a.W + min((int)row, rows - 1)) * a.nkeys;
+        unsigned long long kv[16];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) kv[i] = kr[min(part + 4 * i, a.nkeys - 1)]; /* repeats change no maximum */
+        for (int i = 0; i < 16; ++i) kv[i] = kr[min(part + 4 * i, a.nkeys - 1)]; /* repeats change no maximum */
 #pragma unroll
-    for (int w = 8; w >= 1; w >>= 1)
+        for (int w = 8; w >= 1; w >>= 1)
 #pragma unroll
-        for (int i = 0; i < w; ++i) kv[i] = kv[i + w] > kv[i] ? kv[i + w] : kv[i];
-    unsigned long long kb = kv[0];
+            for (int i = 0; i < w; ++i) kv[i] = kv[i + w] > kv[i] ? kv[i + w] : kv[i];
+        unsigned long long kb = kv[0];
 #pragma unroll
-    for (int msk = 1; msk < 4; msk <<= 1) {
-        const unsigned long long o = shfl_xor_u64(kb, msk);
-        kb = o > kb ? o : kb;
+        for (int msk = 1; msk < 4; msk <<= 1) {
+            const unsigned long long o = shfl_xor_u64(kb, msk);
+            kb = o > kb ? o : kb;
+        }
+        const int idx = (int)dec_key_index(kb);
+        const unsigned long long nb = __ballot(part == 0 && live && idx != (int)a.blank);
+        const int f = nb ? (__ffsll((long long)nb) - 1) >> 2 : rows; /* first non-blank frame */
+        const int emitted = __shfl(idx, 4 * min(f, NK_ATTC_MAX_C - 1), 64);
+        int k = f;
+        if (f > 0) symbols = 0;
+        if (f < rows) {
+            if (lane == 0 && n_out < (int)a.tok_ld) a.tokens[(u64)s * a.tok_ld + (u32)n_out] = emitted;
+            n_out++;
+            last = emitted;
+            cur ^= 1;
+            pred_valid = 0;
+            symbols++;
+            if (symbols >= (int)a.max_symbols) { symbols = 0; k++; }
+        }
+        const int nt = t + k, need = nt < frames && !pred_valid;
+        int slot = 0;
+        if (nt < frames && lane == 0) slot = append_row(a, a.par, (int)s, need, cur, last, nt, frames, sp->erow0);
+        slot = __shfl(slot, 0, 64);
+        if (lane == 0) {
+            sp->t = nt;
+            sp->symbols = symbols;
+            sp->pred_valid = pred_valid;
+            sp->cur = cur;
+            sp->last_token = last;
+            sp->n_out = n_out;
+            sp->need = need;
+            sp->slot = slot;
+            dres[0] = need;
+            dres[1] = slot;
+            dres[2] = cur;
+            dres[3] = last;
+        }
     }
-    const int idx = (int)dec_key_index(kb);
-    const unsigned long long nb = __ballot(part == 0 && live && idx != (int)a.blank);
-    const int f = nb ? (__ffsll((long long)nb) - 1) >> 2 : rows; /* first non-blank frame */
-    const int emitted = __shfl(idx, 4 * min(f, NK_ATTC_MAX_C - 1), 64);
-    int k = f;
-    if (f > 0) symbols = 0;
-    if (f < rows) {
-        if (lane == 0 && n_out < (int)a.tok_ld) a.tokens[(u64)s * a.tok_ld + (u32)n_out] = emitted;
-        n_out++;
-        last = emitted;
-        cur ^= 1;
-        pred_valid = 0;
-        symbols++;
-        if (symbols >= (int)a.max_symbols) { symbols = 0; k++; }
-    }
-    const int nt = t + k, need = nt < frames && !pred_valid;
-    int slot = 0;
-    if (nt < frames && lane == 0) slot = append_row(a, a.par, (int)s, need, cur, last, nt, frames, sp->erow0);
-    slot = __shfl(slot, 0, 64);
-    if (lane == 0) {
-        sp->t = nt;
-        sp->symbols = symbols;
-        sp->pred_valid = pred_valid;
-        sp->cur = cur;
-        sp->last_token = last;
-        sp->n_out = n_out;
-        sp->need = need;
-        sp->slot = slot;
-    }
-    if (need) bdec_prepare(a, (u32)slot, s, cur);
+    __syncthreads();
+    if (dres[0]) bdec_cell0<256>(a, (u32)dres[1], s, dres[2], tx_row_of(a, dres[3]));
 }
