@@ -66,8 +66,9 @@ const double *nemoasr_batch_step_ms(const nemoasr_batch_t *b, size_t *n);
 void nemoasr_batch_debug_use_graphs(nemoasr_batch_t *b, int on);
 void nemoasr_batch_debug_set_dump(nemoasr_batch_t *b, int on);
 /* 1 (default): the greedy loop runs on the device, graph-replayed runs of steps; 0: one host round
-   trip per joint evaluation.  Select before the first step of a batch. */
-void nemoasr_batch_debug_device_decoder(nemoasr_batch_t *b, int on);
+   trip per joint evaluation.  The two keep their greedy state apart, so only before any input;
+   returns -1 afterwards. */
+int nemoasr_batch_debug_device_decoder(nemoasr_batch_t *b, int on);
 /* 1 (default): log-mel on the GPU (frames computed when a window takes them, kept in per-stream
    device rings; within one stream audio and mel input cannot be mixed); 0: on the host's threads.
    Only before any input; returns -1 afterwards. */

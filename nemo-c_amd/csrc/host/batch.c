@@ -1652,19 +1652,16 @@ int nemoasr_batch_debug_gpu_frontend(nemoasr_batch_t *b, int on) {
     return 0;
 }
 
-void nemoasr_batch_debug_device_decoder(nemoasr_batch_t *b, int on) {
-    dec_drain(b, NULL, 0);
-    const int was = b->device_dec;
-    b->device_dec = on && b->gd && device_dec_ok(b);
-    if (b->device_dec && !was) {
-        /* the host-driven loop keeps no hidden halves of layer 0: take them from the LSTM states
-         * (h0 of every stream's two slot sets, rows 4P apart) */
-        const uint32_t P = (uint32_t)b->P, S2 = 2u * (uint32_t)b->S;
-        gpu_begin(b->gd);
-        nk_gemm(b->gd, gpu_buf_dptr(b->hc), 4 * P, (const uint16_t *)gpu_buf_dptr(b->wcati[0]) + P, 2 * P, NULL,
-                gpu_buf_dptr(b->pre0), 4 * P, S2, 4 * P, P, NK_ACT_NONE, 0, 1.0f);
-        gpu_end(b->gd, NULL, 0);
+int nemoasr_batch_debug_device_decoder(nemoasr_batch_t *b, int on) {
+    /* the two loops keep their greedy state apart (the device loop's stream records, its stored
+     * hidden halves of layer 0): the choice is made before any input */
+    for (int s = 0; s < b->S; ++s) {
+        const bstream_t *x = &b->st[s];
+        if (x->src || x->pending_n || x->aq_n || x->consumed) return -1;
     }
+    dec_drain(b, NULL, 0);
+    b->device_dec = on && b->gd && device_dec_ok(b);
+    return 0;
 }
 
 void nemoasr_batch_debug_set_dump(nemoasr_batch_t *b, int on) {

@@ -54,7 +54,7 @@ API = {
     "nemoasr_batch_debug_use_graphs": (None, [_vp, C.c_int]),
     "nemoasr_batch_debug_gpu_frontend": (C.c_int, [_vp, C.c_int]),
     "nemoasr_batch_debug_set_dump": (None, [_vp, C.c_int]),
-    "nemoasr_batch_debug_device_decoder": (None, [_vp, C.c_int]),
+    "nemoasr_batch_debug_device_decoder": (C.c_int, [_vp, C.c_int]),
     "nemoasr_batch_debug_joint_enc": (_f32p, [_vp, C.c_int, C.POINTER(C.c_size_t)]),
     "nemoasr_batch_debug_time_kernel": (C.c_int, [_vp, C.c_char_p, C.c_int]),
     "nemoasr_batch_debug_kernel_ms": (C.c_int, [_vp, C.POINTER(C.c_double), C.POINTER(C.c_int),
@@ -465,7 +465,8 @@ class Batch:
         lib().nemoasr_batch_debug_set_dump(self.h, int(on))
 
     def device_decoder(self, on: bool):
-        lib().nemoasr_batch_debug_device_decoder(self.h, int(on))
+        if lib().nemoasr_batch_debug_device_decoder(self.h, int(on)):
+            raise RuntimeError("greedy loop can only be chosen before any input")
 
     def joint_enc(self, stream: int, joint_hidden: int) -> np.ndarray:
         n = C.c_size_t()

@@ -85,6 +85,28 @@ def test_tiny_batch_matches_oracle(latency, device_loop):
     b.close()
 
 
+def test_batch_loop_choice_only_before_input():
+    """The greedy loop (device-resident or host-driven) is chosen before any input: the two keep
+    their greedy state apart, so a later switch is refused and the batch decodes on as it was."""
+    import nemoasr
+
+    mdir = model_dir("tiny")
+    om = oracle.Model(mdir, "en-US")
+    mels = [mel_ref.logmel(synth.make_audio(t, seed=70 + i)) for i, t in enumerate([1.5, 0.9])]
+    b = nemoasr.Batch(mdir, "en-US", 80, streams=len(mels))
+    b.device_decoder(False)
+    b.device_decoder(True)
+    b.set_dump(True)
+    b.push_mel(0, mels[0][:16])
+    with pytest.raises(RuntimeError):
+        b.device_decoder(False)
+    b.push_mel(0, mels[0][16:], final=True)
+    b.push_mel(1, mels[1], final=True)
+    b.run()
+    check_streams(b, om, 80, mels, om.dims.joint_hidden, tag=("tiny-choice", 80))
+    b.close()
+
+
 @pytest.mark.parametrize("graphs", [False, True])
 def test_full_batch_matches_oracle(graphs):
     """Full-size model, 560 ms, four streams in lockstep (graph replay of the steady step) and
