@@ -14,8 +14,12 @@
 #include <string.h>
 #include <time.h>
 
-#define STEPS_FIRST 11 /* steps in the first graph of a chunk (odd: see below)        */
-#define STEPS_MORE 15  /* steps in each further graph                                  */
+/* Steps per graph run (odd: see launch_steps): the first run of a chunk, then runs sized from an
+ * estimate of the steps still to go, so that a long chunk (560 ms with every frame emitting
+ * max_symbols: ~70 steps) takes two or three runs instead of five; an overestimate costs steps
+ * whose kernels return at once, an underestimate one more host round trip. */
+static const int k_run_steps[] = { 11, 3, 7, 15, 31, 63 };
+#define N_RUN_SIZES (int)(sizeof k_run_steps / sizeof k_run_steps[0])
 #define MAX_GRAPHS_PER_CHUNK 64
 
 static double now_ms(void) {
@@ -26,7 +30,7 @@ static double now_ms(void) {
 
 typedef struct {
     const float *enc;
-    gpu_graph_t *g[2]; /* first, more */
+    gpu_graph_t *g[N_RUN_SIZES]; /* by k_run_steps index */
 } dgraph_t;
 
 struct decoder {
@@ -71,10 +75,8 @@ decoder_t *decoder_create(model_t *m) {
 }
 
 static void free_graphs(decoder_t *d) {
-    for (int i = 0; i < d->ngr; ++i) {
-        gpu_graph_free(d->gr[i].g[0]);
-        gpu_graph_free(d->gr[i].g[1]);
-    }
+    for (int i = 0; i < d->ngr; ++i)
+        for (int k = 0; k < N_RUN_SIZES; ++k) gpu_graph_free(d->gr[i].g[k]);
     memset(d->gr, 0, sizeof d->gr);
     d->ngr = 0;
 }
@@ -181,17 +183,25 @@ int decoder_run(decoder_t *d, const float *joint_enc, int frames, int *out, int 
     int n = 0;
     for (int run = 0;; ++run) {
         if (run >= MAX_GRAPHS_PER_CHUNK) { snprintf(err, errlen, "decoder: no progress"); return -1; }
-        const int which = run ? 1 : 0;
+        int which = 0;
+        if (run) {
+            /* steps still to go, from the chunk's pace so far (decisions per finished frame) */
+            const int left = h->frames - h->t;
+            const int est = h->t > 0 ? (h->joints * left + h->t - 1) / h->t + 1 : (h->joints + 1) * left;
+            which = N_RUN_SIZES - 1;
+            for (int k = 1; k < N_RUN_SIZES; ++k)
+                if (k_run_steps[k] >= est) { which = k; break; }
+        }
         gpu_begin(g);
         if (!run) gpu_upload_async(g, gpu_buf_dptr(d->st), h, 6 * sizeof(int));
         if (d->use_graphs && !gr->g[which]) {
             if (!gpu_capture_begin(g)) {
-                launch_steps(d, joint_enc, which ? STEPS_MORE : STEPS_FIRST);
+                launch_steps(d, joint_enc, k_run_steps[which]);
                 gr->g[which] = gpu_capture_end(g);
             }
         }
         if (gr->g[which]) gpu_graph_launch(g, gr->g[which]);
-        else launch_steps(d, joint_enc, which ? STEPS_MORE : STEPS_FIRST);
+        else launch_steps(d, joint_enc, k_run_steps[which]);
         gpu_download_async(g, h, gpu_buf_dptr(d->st), sizeof *h);
         gpu_download_async(g, d->host_tok, gpu_buf_dptr(d->tokens), NK_DEC_MAX_TOKENS * sizeof(int));
         if (gpu_end(g, err, errlen)) return -1;
