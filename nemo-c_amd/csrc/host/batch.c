@@ -144,7 +144,7 @@ struct nemoasr_batch {
     int nkeys;
     NkBDecStream *stage_bst;
     int *stage_bsetup, *stage_btok;
-    gpu_graph_t *dgraph[2];        /* one per joint.enc buffer */
+    gpu_graph_t *dgraph[2][6];     /* per joint.enc buffer, per run size (k_brun_steps) */
     /* pipelined greedy loop: a worker thread runs each step's loop on its own GPU context (its own
      * stream) while the caller's next step runs its front end and encoder; the step's joint.enc
      * rows are copied to jdec[parity] for it.  The queue holds one step: the next hand-off waits
@@ -616,7 +616,8 @@ void nemoasr_batch_close(nemoasr_batch_t *b) {
     free(b->dorder);
     free(b->dc);
     free(b->drow0);
-    for (int i = 0; i < 2; ++i) gpu_graph_free(b->dgraph[i]);
+    for (int i = 0; i < 2; ++i)
+        for (int k = 0; k < 6; ++k) gpu_graph_free(b->dgraph[i][k]);
     if (b->st)
         for (int s = 0; s < b->S; ++s) {
             melfe_destroy(b->st[s].mel);
@@ -1278,7 +1279,12 @@ static int decoder_batch_run(nemoasr_batch_t *b, int nact, char *err, size_t err
 }
 
 /* ---- device-resident batched greedy loop (kernels/nk_bdec.hip) --------------------------------- */
-#define BDEC_STEPS 10 /* steps per graph run (even: step parities repeat); the host reads the state back once per run */
+/* Steps per graph run (even: step parities repeat; the host reads the state back once per run):
+ * the first run of a batch step, then runs sized from an estimate of the steps still to go (each
+ * stream's decisions per finished frame times its frames left), so that a step whose streams all
+ * emit max_symbols per frame takes two runs instead of seven; steps past a stream's end return at
+ * once. */
+static const int k_brun_steps[6] = { 10, 2, 6, 14, 30, 62 };
 
 static NkBDecArgs bdec_args(nemoasr_batch_t *b) {
     model_t *m = b->m;
@@ -1357,7 +1363,7 @@ static void launch_bdec_steps(nemoasr_batch_t *b, int steps) {
 }
 
 /* the chunks of order[0..nact) through the device loop: one setup launch, then graph runs of
- * BDEC_STEPS steps until every chunk is done */
+ * k_brun_steps steps until every chunk is done */
 static int decoder_batch_device(nemoasr_batch_t *b, char *err, size_t errlen) {
     gpu_t *g = b->gd;
     const int S = b->S, nact = b->dnact;
@@ -1371,29 +1377,43 @@ static int decoder_batch_device(nemoasr_batch_t *b, char *err, size_t errlen) {
     }
     if (maxc > b->W) { snprintf(err, errlen, "decoder: chunk of %d frames exceeds %d", maxc, b->W); return -1; }
     const NkBDecArgs a = bdec_args(b);
-    const int max_runs = (maxc * b->m->cfg.max_symbols + maxc) / BDEC_STEPS + 3;
+    const int max_runs = (maxc * b->m->cfg.max_symbols + maxc) / k_brun_steps[1] + 3;
     for (int run = 0;; ++run) {
         if (run >= max_runs) { snprintf(err, errlen, "decoder: no progress"); return -1; }
+        int which = 0;
+        if (run) {
+            int est = 0;
+            for (int i = 0; i < nact; ++i) {
+                const NkBDecStream *x = &b->stage_bst[b->dorder[i]];
+                const int left = x->frames - x->t;
+                if (left <= 0) continue;
+                const int e = x->t > 0 ? (x->joints * left + x->t - 1) / x->t + 1 : (x->joints + 1) * left;
+                if (e > est) est = e;
+            }
+            which = 5;
+            for (int k = 1; k < 6; ++k)
+                if (k_brun_steps[k] >= est) { which = k; break; }
+        }
         gpu_begin(g);
         if (run == 0) {
             gpu_upload_async(g, gpu_buf_dptr(b->bsetup), su, (size_t)2 * S * sizeof(int));
             gpu_upload_async(g, gpu_buf_dptr(b->bcnt), su + 2 * S, 2 * sizeof(int)); /* zero row counters */
             gpu_launch(g, "bdec_setup", &a, sizeof a, (uint32_t)S, 1, 1, 64, 1, 1);
         }
-        if (b->use_graphs && !b->dgraph[b->dbuf]) {
+        gpu_graph_t **gslot = &b->dgraph[b->dbuf][which];
+        if (b->use_graphs && !*gslot) {
             if (b->dstarted) pthread_mutex_lock(&b->cmu);
             if (!gpu_capture_begin(g)) {
-                launch_bdec_steps(b, BDEC_STEPS);
-                b->dgraph[b->dbuf] = gpu_capture_end(g);
+                launch_bdec_steps(b, k_brun_steps[which]);
+                *gslot = gpu_capture_end(g);
             }
             if (b->dstarted) pthread_mutex_unlock(&b->cmu);
         }
-        if (b->dgraph[b->dbuf]) gpu_graph_launch(g, b->dgraph[b->dbuf]);
-        else launch_bdec_steps(b, BDEC_STEPS);
+        if (*gslot) gpu_graph_launch(g, *gslot);
+        else launch_bdec_steps(b, k_brun_steps[which]);
         gpu_download_async(g, b->stage_bst, gpu_buf_dptr(b->bst), (size_t)S * sizeof(NkBDecStream));
         gpu_download_async(g, b->stage_btok, gpu_buf_dptr(b->btok), (size_t)S * b->tok_ld * sizeof(int));
         if (gpu_end(g, err, errlen)) return -1;
-        b->stats.joint_steps += BDEC_STEPS;
         int done = 1;
         for (int i = 0; i < nact && done; ++i) {
             const NkBDecStream *x = &b->stage_bst[b->dorder[i]];
@@ -1401,6 +1421,11 @@ static int decoder_batch_device(nemoasr_batch_t *b, char *err, size_t errlen) {
         }
         if (done) break;
     }
+    /* the batched joint evaluations: the steps in which some stream was still inside its chunk */
+    int live = 0;
+    for (int i = 0; i < nact; ++i)
+        if (b->stage_bst[b->dorder[i]].joints > live) live = b->stage_bst[b->dorder[i]].joints;
+    b->stats.joint_steps += (size_t)live;
     for (int i = 0; i < nact; ++i) {
         const int s = b->dorder[i];
         const int n = b->stage_bst[s].n_out;
@@ -1636,10 +1661,11 @@ void nemoasr_batch_debug_use_graphs(nemoasr_batch_t *b, int on) {
     b->use_graphs = on;
     if (!on) {
         drop_graphs(b);
-        for (int i = 0; i < 2; ++i) {
-            gpu_graph_free(b->dgraph[i]);
-            b->dgraph[i] = NULL;
-        }
+        for (int i = 0; i < 2; ++i)
+            for (int k = 0; k < 6; ++k) {
+                gpu_graph_free(b->dgraph[i][k]);
+                b->dgraph[i][k] = NULL;
+            }
     }
 }
 

@@ -354,7 +354,7 @@ typedef struct {
  * joint.enc row, and whether this step recomputes the prediction. */
 typedef struct {
     int frames, t, symbols, pred_valid, cur, last_token, n_out, erow0;
-    int need, slot, pad[6];
+    int need, slot, joints, pad[5]; /* joints: decisions taken in the current chunk */
 } NkBDecStream;
 
 /* One row of a decoder step: the streams still inside their chunk, in the order their previous

@@ -284,6 +284,7 @@ extern "C" __global__ __launch_bounds__(64) void bdec_setup(const NkBDecArgs a) 
         sp->n_out = 0;
         sp->need = need;
         sp->slot = slot;
+        sp->joints = 0;
     }
     if (need) bdec_cell0<64>(a, (u32)slot, s, cur, tx_row_of(a, last));
     if (0 < frames && pred_valid) {
@@ -348,6 +349,7 @@ extern "C" __global__ __launch_bounds__(256) void bdec_decide(const NkBDecArgs a
             sp->n_out = n_out;
             sp->need = need;
             sp->slot = slot;
+            sp->joints = sp->joints + 1;
             dres[0] = need;
             dres[1] = slot;
             dres[2] = cur;
