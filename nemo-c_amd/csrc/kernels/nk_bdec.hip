@@ -55,7 +55,7 @@ __device__ __forceinline__ void fr64_partials(const float *A, u32 lda, const u16
     const u32 m = lane & 15, kq = 8 * (lane >> 4);
     uint4 fw[SPW];
 #pragma unroll
-    for (int s = 0; s < SPW; ++s) fw[s] = ld_nt16(Wt + (u64)(min(sb + s, S - 1) * 32 + kq));
+    for (int s = 0; s < SPW; ++s) fw[s] = ld_c16(Wt + (u64)(min(sb + s, S - 1) * 32 + kq));
     float x[SPW][4][8];
 #pragma unroll
     for (int s = 0; s < SPW; ++s)

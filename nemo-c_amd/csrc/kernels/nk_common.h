@@ -17,6 +17,11 @@ __device__ __forceinline__ uint4 ld_nt16(const u16 *p) {
     const u32x4 v = __builtin_nontemporal_load((const u32x4 *)p);
     return make_uint4(v.x, v.y, v.z, v.w);
 }
+/* 16 bytes with the default cache policy: weights read again by every step of a loop */
+__device__ __forceinline__ uint4 ld_c16(const u16 *p) {
+    const u32x4 v = *(const u32x4 *)p;
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
 
 /* bf16 bits -> f32: the upper half of the f32 pattern (exact). */
 __device__ __forceinline__ float bf2f(u32 bits16) { return __uint_as_float(bits16 << 16); }

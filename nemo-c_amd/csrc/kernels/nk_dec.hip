@@ -117,7 +117,7 @@ extern "C" __global__ __launch_bounds__(256) void dec_tx_build(const NkDecArgs a
 #pragma unroll
     for (int g = 0; g < 4; ++g)
 #pragma unroll
-        for (int q = 0; q < 2; ++q) wx[g][q] = ld_nt16(a.wx0 + (u64)(g * P + j) * P + 8 * min(lane + 64 * q, nch - 1));
+        for (int q = 0; q < 2; ++q) wx[g][q] = ld_c16(a.wx0 + (u64)(g * P + j) * P + 8 * min(lane + 64 * q, nch - 1));
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
         const bool ok = lane + 64 * q < nch;
@@ -181,9 +181,9 @@ extern "C" __global__ __launch_bounds__(256) void dec_step(const NkDecArgs a) {
 #pragma unroll
         for (int q = 0; q < 2; ++q) {
             const u64 off = (u64)(g * P + jj) * P + 8 * min(lane + 64 * q, nch - 1);
-            wx[g][q] = ld_nt16(a.wx1 + off);
-            wh[g][q] = ld_nt16(a.wh1 + off);
-            w0[g][q] = ld_nt16(a.wh0 + off);
+            wx[g][q] = ld_c16(a.wx1 + off);
+            wh[g][q] = ld_c16(a.wh1 + off);
+            w0[g][q] = ld_c16(a.wh0 + off);
         }
     float h1[2][8];
     dec_row_chunks(h1, hc_c + P, nullptr, false, lane, nch);
@@ -259,7 +259,7 @@ extern "C" __global__ __launch_bounds__(256) void dec_pred(const NkDecArgs a) {
     __builtin_amdgcn_sched_barrier(0);
     uint4 w[2];
 #pragma unroll
-    for (int q = 0; q < 2; ++q) w[q] = ld_nt16(a.wjp + (u64)j * P + 8 * min(lane + 64 * q, nch - 1));
+    for (int q = 0; q < 2; ++q) w[q] = ld_c16(a.wjp + (u64)j * P + 8 * min(lane + 64 * q, nch - 1));
     __builtin_amdgcn_sched_barrier(0);
     float acc = 0.0f;
 #pragma unroll
@@ -302,7 +302,7 @@ extern "C" __global__ __launch_bounds__(256) void dec_joint(const NkDecArgs a) {
 #pragma unroll
     for (int i = 0; i < 8; ++i)
 #pragma unroll
-        for (int q = 0; q < 2; ++q) w[i][q] = ld_nt16(a.wout + (u64)min(n0 + i, a.V - 1) * J + 8 * min(lane + 64 * q, nch - 1));
+        for (int q = 0; q < 2; ++q) w[i][q] = ld_c16(a.wout + (u64)min(n0 + i, a.V - 1) * J + 8 * min(lane + 64 * q, nch - 1));
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
