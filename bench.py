@@ -29,6 +29,7 @@ CPU baseline: the oracle's C restatement (log-mel + encoder + greedy RNNT) on bo
 headline clip on this host's cores, at one thread and at all threads given to this process.
 """
 import argparse
+import glob
 import json
 import os
 import re
@@ -53,7 +54,7 @@ SKEW_S1120 = (2.0, 0.0188)
 SKEW_B256 = (2.0, 0.0619)
 # HBM traffic per launch of the headline's dominant kernel class, from rocprofv3 FETCH_SIZE and
 # WRITE_SIZE runs of this benchmark's headline workload (profiles/stream80_hbm_traffic.md)
-TRAFFIC_FILE = os.path.join(REPO, "profiles", "stream80_hbm_traffic.md")
+PROFILES = os.path.join(REPO, "profiles")
 
 
 def weight_bytes_per_chunk(cfg: dict) -> int:
@@ -88,15 +89,20 @@ def p_blank(frames, tokens):
     return round(frames / (frames + tokens), 4) if frames + tokens else None
 
 
-def traffic_from_profile(kernel: str):
-    """HBM bytes per launch (FETCH + WRITE, scaled by the copy calibration) that the committed PMC
-    summary records for this kernel class, or None."""
-    try:
-        text = open(TRAFFIC_FILE).read()
-    except OSError:
-        return None
-    m = re.search(r"traffic_bytes_per_launch\[" + re.escape(kernel) + r"\]\s*=\s*([0-9.eE+]+)", text)
-    return float(m.group(1)) if m else None
+def traffic_from_profile(kernel: str, leg: str = ""):
+    """HBM bytes per launch (FETCH + WRITE, scaled by the copy calibration) that a committed PMC
+    summary under profiles/ records for this kernel class (key "leg:class" for the extra legs,
+    the class alone for the headline stream), or None."""
+    key = f"{leg}:{kernel}" if leg else kernel
+    pat = re.compile(r"traffic_bytes_per_launch\[" + re.escape(key) + r"\]\s*=\s*([0-9.eE+]+)")
+    for path in sorted(glob.glob(os.path.join(PROFILES, "*.md"))):
+        try:
+            m = pat.search(open(path).read())
+        except OSError:
+            continue
+        if m:
+            return float(m.group(1))
+    return None
 
 
 def single_leg(a, nemoasr, synth, mdir, cfg, latency, seconds, lang="en-US", steps=None, warmup=None, frames_fn=None):
@@ -158,8 +164,9 @@ def single_leg(a, nemoasr, synth, mdir, cfg, latency, seconds, lang="en-US", ste
         "encoder_chunk_hbm_gbs": round(wb / (enc_ms * 1e-3) / 1e9, 1) if enc_ms > 0 else None,
         "graphs": not a.no_graphs, "gpu": gpu_name,
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_from_profile(kname)
-                     if latency == 80 else None, "kernel": kname, "launches": kn,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": traffic_from_profile(kname, "" if latency == 80 else f"S{latency}"), "kernel": kname,
+                     "launches": kn,
                      "mean_launch_us": round(kms * 1e3, 3), "bytes_per_launch": round(kbytes / max(kn, 1))},
     }
 
@@ -239,7 +246,8 @@ def batch_leg(a, nemoasr, synth, mdir, cfg, S, lat, seconds, offsets, lang):
         "encoder_gemm_frac_of_bf16_peak": round(enc_tflops / MFMA_BF16_PEAK_TFLOPS, 4),
         "graphs": not a.no_graphs,
         "roofline": {"bound": "mfma", "achieved": round(achieved, 1), "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": None, "kernel": "gemm_m*",
+                     "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": traffic_from_profile("gemm_m*", f"B{S}"),
+                     "kernel": "gemm_m*",
                      "launches": kn, "mean_launch_us": round(kms * 1e3, 3),
                      "note": "algorithmic 2*M*N*K flops; the f32 activations enter the MFMAs as bf16 hi + lo "
                              "halves, so the kernels issue twice these MFMA flops"},
