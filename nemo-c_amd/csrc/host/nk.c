@@ -87,8 +87,9 @@ static fr_plan_t fr_plan(uint32_t nout, uint32_t K, int act, int accumulate, int
 
 static const char *fr_name(fr_plan_t p, int act, int ln, int fold) {
     static char buf[40];
-    snprintf(buf, sizeof buf, "gemm_fr%s%s_w%us%u%s", ln ? "_ln" : "", act == NK_ACT_GLU ? "_glu" : "", p.W, p.SPW,
-             fold ? "_f" : "");
+    /* the LayerNorm-fused GLU kernels pack 8 value / gate row pairs into one MFMA operand */
+    snprintf(buf, sizeof buf, "gemm_fr%s%s_w%us%u%s", ln ? "_ln" : "",
+             act == NK_ACT_GLU ? (ln ? "_glu8" : "_glu") : "", p.W, p.SPW, fold ? "_f" : "");
     return buf;
 }
 
@@ -425,7 +426,8 @@ static int gemm_core_p(gpu_t *g, const float *A, uint32_t lda, const uint16_t *W
                                     ((uintptr_t)C & 15) == 0, bias != NULL, ln_fused);
         if (!a.bias) a.bias = gpu_zeros(g);
         if (!a.crow) a.crow = gpu_iota(g);
-        const uint32_t tiles = (nout + 15) / 16;
+        const uint32_t tc = ln_fused && act == NK_ACT_GLU ? 8 : 16; /* output columns per workgroup */
+        const uint32_t tiles = (nout + tc - 1) / tc;
         if (fold) {
             /* the LayerNorm prologue adds the pending update to A first (gemm_fr_ln*_f) */
             a.fold = ln->pend->parts;

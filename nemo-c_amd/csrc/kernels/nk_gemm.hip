@@ -60,13 +60,19 @@ __device__ __forceinline__ void ln_wave4(floatx4 (&v)[4], const floatx4 (&g)[4],
  * them to fold_out when it is set.  The LayerNorm parameters then pass through LDS (sP), so that
  * they load with the rows and the parts without holding registers through the fold. */
 #define FR_FOLD_PARTS 4
-template <int W, int SPW, bool LNA, bool GLU, bool FOLD = false>
+/* PK (GLU only): a workgroup owns 8 output pairs, whose value and gate weight rows share one
+ * 16-column B operand (columns 0-7 values, 8-15 gates), so there is one MFMA pair per step and
+ * twice the workgroups; the epilogue takes each gate sum from lane ^ 8.  Every output's value and
+ * gate sums are the same expressions in the same order as with 16 pairs in two operands. */
+template <int W, int SPW, bool LNA, bool GLU, bool FOLD = false, bool PK = false>
 __device__ __forceinline__ void fr_impl(const NkGemmArgs &a, float *sA, floatx4 *sred, floatx4 *sP = nullptr) {
     static_assert(!FOLD || LNA, "the fold feeds the LayerNorm prologue");
+    static_assert(!PK || GLU, "packed pairs are a GLU layout");
+    constexpr bool G2 = GLU && !PK; /* value and gate rows in two B operands */
     constexpr int RPW = 16 / W; /* LayerNorm rows per wavefront: wave, wave + W, ... */
     const u32 tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const u32 nout = GLU ? a.N / 2 : a.N;
-    const u32 n0 = blockIdx.x * 16;
+    const u32 n0 = blockIdx.x * (PK ? 8 : 16);
     const u32 S = a.K >> 5, M = a.M, KS = gridDim.y;
     const u32 Sw = S / KS, s0 = blockIdx.y * Sw;
     /* this wavefront's K steps: [sb, sb + ns), ns <= SPW (wave-uniform) */
@@ -139,8 +145,11 @@ __device__ __forceinline__ void fr_impl(const NkGemmArgs &a, float *sA, floatx4 
 
     /* epilogue operands (the host always passes bias and the row map), loaded by every
      * wavefront: lane l owns output rows 4*(l/16)+i, column n0 + l%16 */
-    u32 col = n0 + (lane & 15);
+    const u32 c16 = lane & 15;
+    u32 col = n0 + (PK ? (c16 & 7) : c16);
     if (col >= nout) col = nout - 1;
+    const bool gate_lane = PK && c16 >= 8;
+    const u32 wrow = gate_lane ? col + a.N / 2 : col; /* this lane's B column's weight row */
     const float eba = a.bias[col];
     const float ebb = GLU ? a.bias[col + a.N / 2] : 0.0f;
     int erow[4];
@@ -152,14 +161,14 @@ __device__ __forceinline__ void fr_impl(const NkGemmArgs &a, float *sA, floatx4 
     __builtin_amdgcn_sched_barrier(0); /* keep the small loads ahead of the weight stream */
 
     /* 1. weights: every step of this wavefront (steps past K re-read the last one) */
-    const u16 *wa = a.W + (u64)col * a.ldw + kq;
-    const u16 *wb = GLU ? a.W + (u64)(col + a.N / 2) * a.ldw + kq : wa;
-    uint4 fa[SPW], fb[GLU ? SPW : 1];
+    const u16 *wa = a.W + (u64)wrow * a.ldw + kq;
+    const u16 *wb = G2 ? a.W + (u64)(col + a.N / 2) * a.ldw + kq : wa;
+    uint4 fa[SPW], fb[G2 ? SPW : 1];
 #pragma unroll
     for (int s = 0; s < SPW; ++s) {
         const u32 t = min(sb + s, S - 1);
         fa[s] = ld_nt16(wa + (u64)t * 32);
-        if constexpr (GLU) fb[s] = ld_nt16(wb + (u64)t * 32);
+        if constexpr (G2) fb[s] = ld_nt16(wb + (u64)t * 32);
     }
     __builtin_amdgcn_sched_barrier(0);
 
@@ -242,7 +251,7 @@ __device__ __forceinline__ void fr_impl(const NkGemmArgs &a, float *sA, floatx4 
             if (!mrow) ah = al = make_uint4(0, 0, 0, 0);
             acc_a = mfma_bf16(ah, fa[s], acc_a);
             acc_a = mfma_bf16(al, fa[s], acc_a);
-            if constexpr (GLU) {
+            if constexpr (G2) {
                 acc_b = mfma_bf16(ah, fb[s], acc_b);
                 acc_b = mfma_bf16(al, fb[s], acc_b);
             }
@@ -251,14 +260,16 @@ __device__ __forceinline__ void fr_impl(const NkGemmArgs &a, float *sA, floatx4 
 
     /* 4. wavefront partials summed in order; epilogue on wavefront 0 */
     sred[wave * 64 + lane] = acc_a;
-    if constexpr (GLU) sred[(W + wave) * 64 + lane] = acc_b;
+    if constexpr (G2) sred[(W + wave) * 64 + lane] = acc_b;
     __syncthreads();
     if (wave != 0) return;
-    floatx4 ta = sred[lane], tb = GLU ? sred[W * 64 + lane] : acc_b;
+    /* the gate sums: the second operand's partials, or (PK) lane ^ 8's column of the same ones */
+    const u32 goff = PK ? (lane ^ 8u) : W * 64 + lane;
+    floatx4 ta = sred[lane], tb = GLU ? sred[goff] : acc_b;
 #pragma unroll
     for (int w = 1; w < W; ++w) {
         ta += sred[w * 64 + lane];
-        if constexpr (GLU) tb += sred[(W + w) * 64 + lane];
+        if constexpr (GLU) tb += sred[w * 64 + goff];
     }
     if (KS > 1) {
         /* K split over workgroups (residual updates: no bias, no activation, identity rows): this
@@ -272,7 +283,7 @@ __device__ __forceinline__ void fr_impl(const NkGemmArgs &a, float *sA, floatx4 
         }
         return;
     }
-    if (n0 + (lane & 15) >= nout) return;
+    if (gate_lane || n0 + (PK ? c16 : (lane & 15)) >= nout) return;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const u32 r = 4 * (lane >> 4) + i;
@@ -305,18 +316,19 @@ GEMM_FR(gemm_fr_w16s9, 16, 9, false)
 GEMM_FR(gemm_fr_glu_w4s8, 4, 8, true)
 
 /* LayerNorm prologue variants: K == 1024, M <= 16; 8 wavefronts (two rows each for the LayerNorm
- * and the fold), four K steps each; _f: with the pending-update fold */
+ * and the fold), four K steps each; _glu8: GLU with packed pairs (8 outputs per workgroup); _f:
+ * with the pending-update fold */
 #define GEMM_FR_LN(NAME, GLU, FOLD)                                                                      \
     extern "C" __global__ __launch_bounds__(512) void NAME(const NkGemmArgs a) {                         \
         __shared__ float sA[16 * 1024];                                                                  \
-        __shared__ floatx4 sred[2 * 8 * 64];                                                             \
+        __shared__ floatx4 sred[8 * 64];                                                                 \
         __shared__ floatx4 sP[FOLD ? 1024 : 1];                                                          \
-        fr_impl<8, 4, true, GLU, FOLD>(a, sA, sred, sP);                                                 \
+        fr_impl<8, 4, true, GLU, FOLD, GLU>(a, sA, sred, sP);                                            \
     }
 GEMM_FR_LN(gemm_fr_ln_w8s4, false, false)
-GEMM_FR_LN(gemm_fr_ln_glu_w8s4, true, false)
+GEMM_FR_LN(gemm_fr_ln_glu8_w8s4, true, false)
 GEMM_FR_LN(gemm_fr_ln_w8s4_f, false, true)
-GEMM_FR_LN(gemm_fr_ln_glu_w8s4_f, true, true)
+GEMM_FR_LN(gemm_fr_ln_glu8_w8s4_f, true, true)
 
 /* ---- many-row MFMA GEMM ---------------------------------------------------------------------
  * grid = (ceil(N / 64), ceil(M / 64)), block = 256 (2 x 2 wavefronts, 32 x 32 outputs each).
