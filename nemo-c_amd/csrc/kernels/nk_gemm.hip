@@ -14,7 +14,7 @@
 
 /* ---- few-row MFMA GEMM ---------------------------------------------------------------------
  * grid = ceil(nout / 16) workgroups of W wavefronts; a workgroup owns 16 output columns (GLU: 16
- * output pairs) and all of K.  Wavefront w takes the K steps [S*w/W, S*(w+1)/W) of the S = K/32
+ * output pairs; the LayerNorm-fused GLU kernels 8 pairs, grid ceil(nout / 8)) and all of K.  Wavefront w takes the K steps [S*w/W, S*(w+1)/W) of the S = K/32
  * steps (at most FR_SPW).  Order of work:
  *   1. every weight load of the wavefront is issued (16 bytes per lane per step, straight into the
  *      B operand layout);
