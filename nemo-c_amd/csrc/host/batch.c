@@ -1318,10 +1318,7 @@ static NkBDecArgs bdec_args(nemoasr_batch_t *b) {
 }
 
 /* `steps` decoder steps over all streams (fixed shapes: one graph serves every run) */
-typedef struct {
-    NkGemmArgs g;
-    NkBDecArgs d;
-} bdec_launch_t;
+typedef NkBDecGemmArgs bdec_launch_t;
 
 /* grid: N / 16 column workgroups (plus gx_more) by row blocks of 64 */
 static int launch_bdec_gemm(nemoasr_batch_t *b, uint32_t par, const char *kernel, const float *A, uint32_t lda,

@@ -357,20 +357,22 @@ int gpu_launch(gpu_t *g, const char *kernel, const void *args, size_t args_size,
     if (!gx || !gy || !gz) return 0;
     hipFunction_t f = lookup(g, kernel);
     if (!f) return -1;
-    size_t sz = args_size;
-    void *config[] = { HIP_LAUNCH_PARAM_BUFFER_POINTER, (void *)args, HIP_LAUNCH_PARAM_BUFFER_SIZE, &sz,
-                       HIP_LAUNCH_PARAM_END };
+    /* Every kernel takes one by-value struct: its address is the one entry of kernelParams.  The
+     * runtime copies the argument block into the launch (and into the graph node when the stream
+     * is being captured), so the caller's struct may go out of scope right after this call. */
+    (void)args_size;
+    void *kp[] = { (void *)args };
     const int timed = !g->capturing && g->tev && g->tn < g->tmax && timed_name(g->timed, kernel);
     hipError_t e;
     if (timed) {
         /* the start / stop events are stamped by the dispatch itself: the kernel's execution time */
-        e = hipExtModuleLaunchKernel(f, gx * bx, gy * by, gz * bz, bx, by, bz, 0, g->stream, NULL, config,
+        e = hipExtModuleLaunchKernel(f, gx * bx, gy * by, gz * bz, bx, by, bz, 0, g->stream, kp, NULL,
                                      g->tev[2 * g->tn], g->tev[2 * g->tn + 1], 0);
         g->tbytes[g->tn] = g->next_bytes;
         g->tflops[g->tn] = g->next_flops;
         g->tn++;
     } else {
-        e = hipModuleLaunchKernel(f, gx, gy, gz, bx, by, bz, 0, g->stream, NULL, config);
+        e = hipModuleLaunchKernel(f, gx, gy, gz, bx, by, bz, 0, g->stream, kp, NULL);
     }
     g->next_bytes = 0.0;
     g->next_flops = 0.0;

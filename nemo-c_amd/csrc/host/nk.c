@@ -197,7 +197,10 @@ static int launch_mx_s(gpu_t *g, NkGemmArgs *a, uint32_t M, uint32_t nout, uint3
         if (a->kblocks > 1 && (g_split == 1 || (g_split < 0 && tiles < 400))) kz = a->kblocks;
         const size_t need = (size_t)kz * M * nout;
         if (sc && sc->ws) {
-            if (need > sc->ws_floats) return -2;
+            /* a fixed region too small for the split may still hold the unsplit partial rows (same
+             * bits: the K blocks are summed in the same order either way) */
+            if (need > sc->ws_floats && kz > 1 && (size_t)M * nout <= sc->ws_floats) kz = 1;
+            if ((size_t)kz * M * nout > sc->ws_floats) return -2;
             a->ws = sc->ws;
         } else {
             a->ws = gpu_scratch_ws(g, need);
@@ -452,7 +455,11 @@ static int gemm_core_p(gpu_t *g, const float *A, uint32_t lda, const uint16_t *W
     }
     const int glu = act == NK_ACT_GLU;
     if (g_force != K_MM_OLD) {
-        const int rc = launch_mx(g, &a, M, nout, K, glu, accumulate && !bias && act == NK_ACT_NONE);
+        /* the deferred (partial-row) residual update writes rows 0..M-1 of C through resid_fold: only
+         * without a row map and on the layout the fold takes; otherwise the plain add-into-C epilogue */
+        const int resid = accumulate && !bias && act == NK_ACT_NONE && !crow && nout % 4 == 0 && ldc % 4 == 0 &&
+                          ((uintptr_t)C & 15) == 0;
+        const int rc = launch_mx(g, &a, M, nout, K, glu, resid);
         if (rc <= 0) return rc;
     }
     /* many rows, first-generation kernels: 128 x 128 tiles when they fill the GPU, else 64 x 64 */

@@ -386,4 +386,11 @@ typedef struct {
     u32 S, W, P, J, blank, max_symbols, tok_ld, par;
 } NkBDecArgs;
 
+/* The batched loop's GEMM kernels (bdec_lstm1_*, bdec_pred_*): the GEMM operands and the loop
+ * state in one argument block, like every other kernel (one by-value struct per kernel). */
+typedef struct {
+    NkGemmArgs g;
+    NkBDecArgs d;
+} NkBDecGemmArgs;
+
 #endif

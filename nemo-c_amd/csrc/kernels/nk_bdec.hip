@@ -215,10 +215,10 @@ __device__ __forceinline__ void bdec_pred_impl(const NkGemmArgs &a, const NkBDec
 }
 
 #define BDEC_GEMM(NAME, IMPL, W, SPW)                                                                     \
-    extern "C" __global__ __launch_bounds__(64 * W) void NAME(const NkGemmArgs a, const NkBDecArgs d) {   \
+    extern "C" __global__ __launch_bounds__(64 * W) void NAME(const NkBDecGemmArgs x) {                   \
         __shared__ floatx4 sred[W * 4 * 64];                                                              \
         __shared__ BDecStage ss;                                                                          \
-        IMPL(a, d, sred, ss);                                                                             \
+        IMPL(x.g, x.d, sred, ss);                                                                         \
     }
 /* layer 1: K = 2P <= 1280: 8 wavefronts x 5 steps; joint.pred and Wh0: K = P: 4 x 5 */
 BDEC_GEMM(bdec_lstm1_w8s5, (bdec_lstm_impl<8, 5>), 8, 5)

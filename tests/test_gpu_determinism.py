@@ -1,7 +1,7 @@
 """Run-to-run and batch-composition determinism of the HIP path.
 
 Every reduction on the token path has a fixed order: wavefront and workgroup sums in index order,
-split-K partials combined in split order by the last workgroup to arrive (no float atomics), the
+split-K partial rows added in split order by the kernel that consumes them (no float atomics), the
 batched residual updates' K summed in blocks fixed by K alone.  So:
   - the same input gives the same bits twice (single stream and batch);
   - a stream's joint.enc rows and tokens in a batch do not depend on the other streams of the batch

@@ -69,6 +69,32 @@ def test_library_exports_every_declared_function():
     assert not missing, missing
 
 
+def test_every_kernel_takes_one_argument_block():
+    """gpu_launch hands each kernel one by-value argument block (kernelParams = { &block }), so every
+    kernel in the gfx950 code object must declare exactly one explicit argument; a second one would
+    be read from an unset pointer.  Read from the metadata of the code object built here."""
+    import shutil
+    import subprocess
+    import yaml
+
+    co = os.path.join(REPO, "nemo-c_amd", "build", "nk_all.hsaco")
+    llvm = "/opt/rocm/llvm/bin"
+    if not os.path.exists(co) or not shutil.which(os.path.join(llvm, "llvm-readelf")):
+        pytest.skip("code object or LLVM tools not present")
+    elf = os.path.join(REPO, "nemo-c_amd", "build", "nk_all.gfx950.elf")
+    subprocess.run([os.path.join(llvm, "clang-offload-bundler"), "--unbundle", "--type=o", f"--input={co}",
+                    "--targets=hipv4-amdgcn-amd-amdhsa--gfx950", f"--output={elf}"], check=True)
+    notes = subprocess.run([os.path.join(llvm, "llvm-readelf"), "--notes", elf], check=True, capture_output=True,
+                           text=True).stdout
+    meta = yaml.safe_load(notes[notes.index("---"):notes.index("\n...", notes.index("---"))])
+    kernels = meta["amdhsa.kernels"]
+    assert len(kernels) > 100
+    bad = {k[".name"]: len([a for a in k.get(".args", []) if not a[".value_kind"].startswith("hidden")])
+           for k in kernels}
+    bad = {n: c for n, c in bad.items() if c != 1}
+    assert not bad, bad
+
+
 def test_open_without_gpu_fails_loudly(tiny_model_dir):
     import torch
 

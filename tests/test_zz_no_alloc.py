@@ -34,7 +34,7 @@ def run(gpu, fn, A, W, C0, K_split, alpha=0.5):
     return rc, out, err
 
 
-@pytest.mark.parametrize("ksplit", [1, -1])
+@pytest.mark.parametrize("ksplit", [1, 0, -1])
 def test_noalloc_matches_gemm_split(gpu, ksplit):
     rng = np.random.default_rng([ksplit + 1, 77])
     W = oracle.f32_to_bf16((rng.standard_normal((1024, 4096)) / 64).astype(np.float32))
@@ -46,6 +46,62 @@ def test_noalloc_matches_gemm_split(gpu, ksplit):
         assert rc1 == 0 and rc2 == 0, err
         assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), M
         assert rel_err(got, oracle.gemm(A, W, None, 0, True, 0.5, C0=C0)) < 2e-5
+
+
+def test_noalloc_unsplit_when_split_does_not_fit(gpu):
+    """1536 x 1024 outputs with K = 4096 are split four ways by default below ~400 tiles (6M floats
+    of partial rows, more than the array); the unsplit partial rows (1.5M floats) fit, so the call
+    succeeds with the bits of nk_gemm_split."""
+    rng = np.random.default_rng(1536)
+    M, N, K = 1536, 1024, 4096
+    W = oracle.f32_to_bf16((rng.standard_normal((N, K)) / 64).astype(np.float32))
+    A = rng.standard_normal((M, K)).astype(np.float32)
+    C0 = rng.standard_normal((M, N)).astype(np.float32)
+    rc1, ref, _ = run(gpu, "nk_gemm_split", A, W, C0.copy(), -1)
+    rc2, got, err = run(gpu, "nk_gemm_split_noalloc", A, W, C0.copy(), -1)
+    assert rc1 == 0 and rc2 == 0, err
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+def test_noalloc_in_graph_capture(gpu):
+    """The entry point recorded into a hipGraph (where the library could not grow its own scratch)
+    and replayed three times, with eager launches of the allocating form and host synchronisation
+    between the replays: every replay gives the allocating form's bits."""
+    import nemoasr
+
+    L = nemoasr.lib()
+    rng = np.random.default_rng(4481)
+    M, N, K = 448, 1024, 4096
+    W = oracle.f32_to_bf16((rng.standard_normal((N, K)) / 64).astype(np.float32))
+    A = rng.standard_normal((M, K)).astype(np.float32)
+    C0 = rng.standard_normal((M, N)).astype(np.float32)
+    rc, ref, err = run(gpu, "nk_gemm_split", A, W, C0.copy(), 1)
+    assert rc == 0, err
+    dA, dW, dC = gpu.put(A), gpu.put(W), gpu.put(C0)
+    prev = L.nk_gemm_ksplit(1)
+    graph = None
+    try:
+        gpu.begin()
+        gpu.check(L.gpu_capture_begin(gpu.h))
+        rc = L.nk_gemm_split_noalloc(gpu.h, dA.ptr, None, K, dW.ptr, K, None, dC.ptr, None, N, None, M, N, K, 0, 1, 0.5)
+        graph = L.gpu_capture_end(gpu.h)
+        gpu.end()
+        assert rc == 0 and graph, L.gpu_last_error(gpu.h).decode()
+        for rep in range(3):
+            dC.write(C0)
+            gpu.begin()
+            gpu.check(L.gpu_graph_launch(gpu.h, graph))
+            gpu.end()
+            got = dC.read((M, N))
+            assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), rep
+            rc_e, ref_e, _ = run(gpu, "nk_gemm_split", A, W, C0.copy(), 1)  # eager work between replays
+            assert rc_e == 0 and np.array_equal(ref_e.view(np.uint32), ref.view(np.uint32))
+    finally:
+        L.nk_gemm_ksplit(prev)
+        if graph:
+            L.gpu_graph_free(graph)
+        for b in (dA, dW, dC):
+            b.free()
 
 
 def test_noalloc_refuses_oversized_split(gpu):
