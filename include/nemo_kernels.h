@@ -19,20 +19,14 @@
  * The single stream's LSTM, joint and argmax run inside the device-resident greedy loop
  * (csrc/host/decoder.c, kernels dec_step / dec_pred / dec_joint), which has no per-kernel launcher.
  *
- * The GPU runtime (gpu_* below) is a re-design of src/gpu.h:20-41, not the same interface: the
- * host here is this library's own (the launchers compute their grids from the shapes), so the
- * reference's dispatch forms were folded into one launch call:
- *   gpu_create(metal_source)          -> gpu_create(): loads the gfx950 code object linked into
- *                                        the library (hipModuleLoadData)
- *   gpu_buf_alloc (shared storage)    -> gpu_buf_alloc (device memory, zero-filled)
- *   gpu_buf_ptr (host address)        -> gpu_buf_dptr (device address) + gpu_upload / gpu_download
- *   GPU_BUF(b, off) / GPU_BYTES(p)    -> device pointers and sizes inside one by-value argument struct
- *   gpu_dispatch (total threads),     -> gpu_launch (workgroup counts and sizes)
- *   gpu_dispatch_groups (groups)
- *   gpu_dispatch_groups_fc (function -> one kernel symbol per specialisation, looked up by name
- *     constants, cached per value set)   (e.g. gemv_r1_n4_k2, gemm_fr_w16s8)
- *   gpu_begin / gpu_end / gpu_last_ms -> same roles (one stream, hipEvents)
- * The kernel argument structs are likewise re-designed (nemo-c_amd/csrc/kernel_params.h).
+ * The GPU runtime has two faces.  This library's own host uses the one below: one launch call with
+ * workgroup counts and one by-value argument struct of device pointers per kernel
+ * (nemo-c_amd/csrc/kernel_params.h), device addresses from gpu_buf_dptr, explicit uploads and
+ * downloads, hipGraph capture.  A host written against the reference's runtime (src/gpu.h:7-41:
+ * buffers bound by index, GPU_BUF / GPU_BYTES arguments, dispatch by total threads, by groups or
+ * by groups with function constants, host-addressable buffers) uses include/nemo_gpu.h and the
+ * reference's parameter blocks in include/nemo_kernel_params.h; both faces share gpu_create,
+ * gpu_buf_alloc, gpu_begin / gpu_end and the kernels.
  */
 #ifndef NEMO_KERNELS_H
 #define NEMO_KERNELS_H
@@ -47,7 +41,7 @@ typedef struct gpu gpu_t;
 typedef struct gpu_buf gpu_buf_t;
 
 /* ---- runtime (src/gpu.h:20-41) ---------------------------------------------------------------- */
-gpu_t *gpu_create(char *err, size_t errlen);
+gpu_t *gpu_create(const char *source, char *err, size_t errlen);
 void gpu_destroy(gpu_t *g);
 const char *gpu_device_name(gpu_t *g);
 gpu_buf_t *gpu_buf_alloc(gpu_t *g, size_t bytes);
@@ -287,6 +281,19 @@ int nk_lstm_cell_rows(gpu_t *g, const float *gates, float *hc, const int *crow_i
 int nk_joint_in_rows(gpu_t *g, const float *enc, const float *pred, const int *erow, const int *prow, float *jin,
                      uint32_t rows, uint32_t J);
 int nk_argmax_rows(gpu_t *g, const float *logits, uint32_t ld, uint32_t rows, uint32_t V, int *out);
+
+/* ---- dispatches of the reference that this library's own path fuses away -------------------------
+ * Served for hosts driving include/nemo_gpu.h (reference kernels glu, lstm_cell, joint_partial,
+ * argmax_reduce: src/kernels.metal:349-356, :474-550; dispatch sites src/decoder.c:71-73, :79-90). */
+int nk_glu(gpu_t *g, const float *X, float *Y, uint32_t M, uint32_t D);
+int nk_lstm_cell(gpu_t *g, const float *gates, const float *c_in, float *c_out, float *h_out, uint32_t H);
+/* per row r < rows: slot s < 8 groups keeps the best of n = s, s + 8 groups, ... < V of
+ * W[n] . relu(enc[enc_row + r] + pred) + bias[n] in part_v / part_i[r][s] */
+int nk_joint_partial(gpu_t *g, const float *enc, const float *pred, const uint16_t *W, const float *bias,
+                     float *part_v, int *part_i, uint32_t V, uint32_t H, uint32_t enc_row, uint32_t enc_ld,
+                     uint32_t groups, uint32_t rows);
+/* out[2 r], out[2 r + 1] = index and value bits of the best of row r's n partials (lowest index on ties) */
+int nk_argmax_reduce(gpu_t *g, const float *part_v, const int *part_i, int *out, uint32_t n, uint32_t rows);
 
 #ifdef __cplusplus
 }

@@ -561,7 +561,7 @@ nemoasr_batch_t *nemoasr_batch_open(const char *model_dir, const char *language,
     b->device_dec = device_dec_ok(b);
     if (b->device_dec) {
         /* the greedy loop's own GPU context and worker thread */
-        b->gd = gpu_create(err, errlen);
+        b->gd = gpu_create(NULL, err, errlen);
         if (b->gd) gpu_set_many_rows(b->gd, 1);
         b->jdec[0] = gpu_buf_alloc(g, Mm * (size_t)b->J * fs);
         b->jdec[1] = gpu_buf_alloc(g, Mm * (size_t)b->J * fs);

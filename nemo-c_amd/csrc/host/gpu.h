@@ -25,7 +25,9 @@ typedef struct gpu gpu_t;
 typedef struct gpu_buf gpu_buf_t;
 typedef struct gpu_graph gpu_graph_t;
 
-gpu_t *gpu_create(char *err, size_t errlen);
+/* `source`: the reference passes its Metal source text here (src/gpu.h:20); the gfx950 code
+ * object linked into this library is used instead and the argument is not read (NULL is fine). */
+gpu_t *gpu_create(const char *source, char *err, size_t errlen);
 void gpu_destroy(gpu_t *g);
 const char *gpu_device_name(gpu_t *g);
 
@@ -33,6 +35,9 @@ gpu_buf_t *gpu_buf_alloc(gpu_t *g, size_t bytes); /* device memory, zero-filled;
 void gpu_buf_free(gpu_buf_t *b);
 void *gpu_buf_dptr(gpu_buf_t *b);                 /* device address */
 size_t gpu_buf_len(gpu_buf_t *b);
+/* Host address of a pinned mirror of the buffer (src/gpu.h:26), coherent at batch edges: refreshed
+ * from the device when a batch has ended since, uploaded by the next gpu_begin. */
+void *gpu_buf_ptr(gpu_buf_t *b);
 
 /* pinned host memory for the host<->device staging on the hot path */
 void *gpu_host_alloc(gpu_t *g, size_t bytes);

@@ -46,10 +46,18 @@ struct gpu {
     hipEvent_t *tev;
     double *tbytes, next_bytes, *tflops, next_flops, last_flops;
     int tmax, tn;
+    /* buffers with a host mirror (gpu_buf_ptr): uploaded at gpu_begin when the host may have
+     * written them, marked device-newer at gpu_end */
+    gpu_buf_t *mirrored;
 };
 struct gpu_buf {
     void *d;
     size_t len;
+    gpu_t *g;
+    void *host;           /* pinned mirror, allocated by the first gpu_buf_ptr */
+    int host_dirty;       /* the host may have written the mirror since the last upload */
+    int dev_newer;        /* a batch ended after the last download: the device copy may be newer */
+    gpu_buf_t *next_mirrored;
 };
 struct gpu_graph {
     hipGraph_t graph;
@@ -68,7 +76,10 @@ int gpu_fail(gpu_t *g, const char *msg) {
     return -1;
 }
 
-gpu_t *gpu_create(char *err, size_t errlen) {
+gpu_t *gpu_create(const char *source, char *err, size_t errlen) {
+    /* `source` is the reference's Metal source text (src/model.c:202); this library runs the gfx950
+     * code object linked into it, so the argument is accepted and not compiled */
+    (void)source;
     int n = 0;
     hipError_t e = hipGetDeviceCount(&n);
     if (e != hipSuccess || n <= 0) {
@@ -152,15 +163,66 @@ int gpu_capturing(const gpu_t *g) { return g->capturing; }
 gpu_buf_t *gpu_buf_alloc(gpu_t *g, size_t bytes) {
     gpu_buf_t *b = calloc(1, sizeof *b);
     b->len = bytes ? bytes : 256;
+    b->g = g;
     if (hipMalloc(&b->d, b->len) != hipSuccess) { free(b); return NULL; }
     if (hipMemset(b->d, 0, b->len) != hipSuccess) { hipFree(b->d); free(b); return NULL; }
-    (void)g;
     return b;
 }
 void gpu_buf_free(gpu_buf_t *b) {
     if (!b) return;
+    if (b->host) {
+        for (gpu_buf_t **p = &b->g->mirrored; *p; p = &(*p)->next_mirrored)
+            if (*p == b) { *p = b->next_mirrored; break; }
+        hipHostFree(b->host);
+    }
     hipFree(b->d);
     free(b);
+}
+
+/* Host address of a buffer, as src/gpu.h:26 gives for Metal's shared storage.  Here the buffer
+ * lives in device memory and the address is a pinned mirror of it, kept coherent at batch edges:
+ *   - the mirror is refreshed from the device when a batch has ended since the last refresh;
+ *   - every call marks the mirror as possibly written, and gpu_begin uploads such mirrors before
+ *     the batch's first launch.
+ * So the host reads results and writes inputs between batches through a pointer taken after the
+ * last gpu_end (the reference's own discipline: no command buffer is in flight while the host
+ * touches shared buffers).  Writes through a pointer taken before a later gpu_end are not seen.
+ * The product path never calls this (it uses gpu_upload / gpu_download on device addresses). */
+void *gpu_buf_ptr(gpu_buf_t *b) {
+    if (!b) return NULL;
+    gpu_t *g = b->g;
+    if (!b->host) {
+        if (hipHostMalloc(&b->host, b->len, hipHostMallocDefault) != hipSuccess) {
+            b->host = NULL;
+            gpu_fail(g, "gpu_buf_ptr: pinned host mirror unavailable");
+            return NULL;
+        }
+        b->dev_newer = 1;
+        b->next_mirrored = g->mirrored;
+        g->mirrored = b;
+    }
+    if (b->dev_newer) {
+        hipError_t e = hipStreamSynchronize(g->stream);
+        if (e == hipSuccess) e = hipMemcpy(b->host, b->d, b->len, hipMemcpyDeviceToHost);
+        if (e != hipSuccess) { fail(g, "gpu_buf_ptr refresh", e); return NULL; }
+        b->dev_newer = 0;
+    }
+    b->host_dirty = 1;
+    return b->host;
+}
+
+/* before a batch: device copies of the mirrors the host may have written */
+static int upload_mirrors(gpu_t *g) {
+    for (gpu_buf_t *b = g->mirrored; b; b = b->next_mirrored) {
+        if (!b->host_dirty) continue;
+        hipError_t e = hipMemcpyAsync(b->d, b->host, b->len, hipMemcpyHostToDevice, g->stream);
+        if (e != hipSuccess) return fail(g, "gpu_begin: mirror upload", e);
+        b->host_dirty = 0;
+    }
+    return 0;
+}
+static void mirrors_dev_newer(gpu_t *g) {
+    for (gpu_buf_t *b = g->mirrored; b; b = b->next_mirrored) b->dev_newer = 1;
 }
 void *gpu_buf_dptr(gpu_buf_t *b) { return b ? b->d : NULL; }
 size_t gpu_buf_len(gpu_buf_t *b) { return b->len; }
@@ -348,6 +410,7 @@ int gpu_begin(gpu_t *g) {
     g->failed = 0;
     g->err[0] = 0;
     g->in_batch = 1;
+    if (g->mirrored && upload_mirrors(g)) return -1;
     hipError_t e = hipEventRecord(g->ev0, g->stream);
     return e == hipSuccess ? 0 : fail(g, "begin", e);
 }
@@ -397,6 +460,7 @@ int gpu_end(gpu_t *g, char *err, size_t errlen) {
     float ms = 0.0f;
     if (!g->failed && hipEventElapsedTime(&ms, g->ev0, g->ev1) == hipSuccess) g->last_ms = ms;
     g->in_batch = 0;
+    mirrors_dev_newer(g);
     if (g->failed) {
         if (errlen) snprintf(err, errlen, "gpu: %s", g->err);
         return -1;
@@ -409,6 +473,7 @@ int gpu_end_nowait(gpu_t *g, char *err, size_t errlen) {
     hipError_t e = hipEventRecord(g->ev1, g->stream);
     if (e != hipSuccess) fail(g, "end", e);
     g->in_batch = 0;
+    mirrors_dev_newer(g);
     if (g->failed) {
         if (errlen) snprintf(err, errlen, "gpu: %s", g->err);
         return -1;

@@ -192,7 +192,7 @@ model_t *model_load(const char *dir, char *err, size_t errlen) {
     snprintf(path, sizeof path, "%s/model.safetensors", dir);
     ckpt_t *st = ckpt_open(path, err, errlen);
     if (!st) { model_free(m); return NULL; }
-    m->gpu = gpu_create(err, errlen);
+    m->gpu = gpu_create(NULL, err, errlen);
     if (!m->gpu) { ckpt_close(st); model_free(m); return NULL; }
 
     const model_cfg_t *g = &m->cfg;

@@ -840,3 +840,32 @@ int nk_compact(gpu_t *g, float *base, uint64_t stride, uint32_t nbuf, uint32_t r
     return gpu_launch(g, "compact_rows", &a, sizeof a, blocks_for((uint64_t)rows * cols), nbuf, 1, 256, 1, 1);
 }
 
+
+/* ---- kernels of the reference-shaped dispatch only (gpu_ref.c) -------------------------------- */
+int nk_glu(gpu_t *g, const float *X, float *Y, uint32_t M, uint32_t D) {
+    if (!M || !D) return 0;
+    NkGluArgs a = { X, Y, M, D };
+    return gpu_launch(g, "glu_rows", &a, sizeof a, blocks_for(D), M, 1, 256, 1, 1);
+}
+
+int nk_lstm_cell(gpu_t *g, const float *gates, const float *c_in, float *c_out, float *h_out, uint32_t H) {
+    if (!H) return 0;
+    NkLstmCellArgs a = { gates, c_in, c_out, h_out, H };
+    return gpu_launch(g, "lstm_cell_vec", &a, sizeof a, blocks_for(H), 1, 1, 256, 1, 1);
+}
+
+int nk_joint_partial(gpu_t *g, const float *enc, const float *pred, const uint16_t *W, const float *bias,
+                     float *part_v, int *part_i, uint32_t V, uint32_t H, uint32_t enc_row, uint32_t enc_ld,
+                     uint32_t groups, uint32_t rows) {
+    if (!rows || !groups) return 0;
+    if (H % 4 || H > NK_JOINT_MAX_H || ((uintptr_t)W & 7))
+        return bad(g, "joint_partial: H % 4 == 0, H <= 1024, W 8-byte aligned");
+    NkJointPartArgs a = { enc, pred, W, bias, part_v, part_i, V, H, enc_row, enc_ld, groups };
+    return gpu_launch(g, "joint_partial_groups", &a, sizeof a, groups, rows, 1, 512, 1, 1);
+}
+
+int nk_argmax_reduce(gpu_t *g, const float *part_v, const int *part_i, int *out, uint32_t n, uint32_t rows) {
+    if (!rows) return 0;
+    NkArgmaxPartArgs a = { part_v, part_i, out, n };
+    return gpu_launch(g, "argmax_partials", &a, sizeof a, rows, 1, 1, 256, 1, 1);
+}

@@ -386,6 +386,37 @@ typedef struct {
     u32 S, W, P, J, blank, max_symbols, tok_ld, par;
 } NkBDecArgs;
 
+/* Kernels of the reference-shaped dispatch (include/nemo_gpu.h) with no counterpart in this
+ * library's own path: the standalone GLU, a one-vector LSTM cell with separate input and output
+ * state buffers, and the two-stage joint argmax with the reference's partial-best layout
+ * (src/kernels.metal:349-356, :474-550). */
+typedef struct {
+    const float *X; /* [M][2D]: value half then gate half */
+    float *Y;       /* [M][D] */
+    u32 M, D;
+} NkGluArgs;
+typedef struct {
+    const float *gates; /* [4H] i, f, g, o */
+    const float *c_in;
+    float *c_out, *h_out;
+    u32 H;
+} NkLstmCellArgs;
+typedef struct {
+    const float *enc;   /* joint.enc rows; row enc_row + r of stride enc_ld */
+    const float *pred;  /* [H] */
+    const u16 *W;       /* [V][H] bf16 */
+    const float *bias;  /* [V] */
+    float *part_v;      /* [rows][groups * 8] best score per slot */
+    int *part_i;        /* [rows][groups * 8] its index (lowest on ties) */
+    u32 V, H, enc_row, enc_ld, groups;
+} NkJointPartArgs;
+typedef struct {
+    const float *part_v;
+    const int *part_i;
+    int *out; /* [rows][2]: index, value bits */
+    u32 n;    /* partials per row */
+} NkArgmaxPartArgs;
+
 /* The batched loop's GEMM kernels (bdec_lstm1_*, bdec_pred_*): the GEMM operands and the loop
  * state in one argument block, like every other kernel (one by-value struct per kernel). */
 typedef struct {

@@ -78,7 +78,7 @@ API = {
     "nemoasr_debug_weight_bytes": (C.c_size_t, [_vp]),
     "nemoasr_debug_launches": (C.c_uint64, [_vp]),
     # include/nemo_kernels.h
-    "gpu_create": (_vp, [C.c_char_p, C.c_size_t]),
+    "gpu_create": (_vp, [C.c_char_p, C.c_char_p, C.c_size_t]),
     "gpu_destroy": (None, [_vp]),
     "gpu_device_name": (C.c_char_p, [_vp]),
     "gpu_buf_alloc": (_vp, [_vp, C.c_size_t]),
@@ -162,6 +162,15 @@ API = {
     "nk_lstm_cell_rows": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32]),
     "nk_joint_in_rows": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32]),
     "nk_argmax_rows": (C.c_int, [_vp, _vp, _u32, _u32, _u32, _vp]),
+    "nk_glu": (C.c_int, [_vp, _vp, _vp, _u32, _u32]),
+    "nk_lstm_cell": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _u32]),
+    "nk_joint_partial": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _u32]),
+    "nk_argmax_reduce": (C.c_int, [_vp, _vp, _vp, _vp, _u32, _u32]),
+    # include/nemo_gpu.h (the reference's runtime interface; gpu_arg_t arrays are GpuArg below)
+    "gpu_buf_ptr": (_vp, [_vp]),
+    "gpu_dispatch": (C.c_int, [_vp, C.c_char_p, _vp, C.c_int] + [_u32] * 6),
+    "gpu_dispatch_groups": (C.c_int, [_vp, C.c_char_p, _vp, C.c_int] + [_u32] * 6),
+    "gpu_dispatch_groups_fc": (C.c_int, [_vp, C.c_char_p, _vp, C.c_int, _vp, C.c_int] + [_u32] * 6),
     # include/nemoasr_host.h
     "melfe_create": (_vp, []),
     "melfe_destroy": (None, [_vp]),
@@ -196,6 +205,25 @@ def fp(a: np.ndarray):
     return a.ctypes.data_as(_f32p)
 
 
+class GpuArg(C.Structure):
+    """gpu_arg_t of include/nemo_gpu.h (src/gpu.h:10-15): a buffer + byte offset, or inline bytes."""
+    _fields_ = [("buf", C.c_void_p), ("offset", C.c_size_t), ("bytes", C.c_void_p), ("size", C.c_size_t)]
+
+
+def gpu_args(*items):
+    """A gpu_arg_t array from (buffer handle, byte offset) pairs and ctypes parameter blocks (kept
+    alive by the returned tuple's second element)."""
+    arr = (GpuArg * len(items))()
+    keep = []
+    for i, it in enumerate(items):
+        if isinstance(it, tuple):
+            arr[i].buf, arr[i].offset = it[0], it[1]
+        else:
+            keep.append(it)
+            arr[i].bytes, arr[i].size = C.cast(C.pointer(it), C.c_void_p), C.sizeof(it)
+    return arr, keep
+
+
 class Resid(C.Structure):
     """nk_resid_t: a pending residual update (partial rows in the context's scratch)."""
     _fields_ = [("parts", C.c_void_p), ("nparts", C.c_uint32), ("alpha", C.c_float)]
@@ -206,7 +234,7 @@ class Gpu:
 
     def __init__(self):
         err = C.create_string_buffer(512)
-        self.h = lib().gpu_create(err, 512)
+        self.h = lib().gpu_create(None, err, 512)
         if not self.h:
             raise RuntimeError("gpu_create: " + err.value.decode())
         self._bufs = []

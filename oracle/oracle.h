@@ -103,6 +103,10 @@ size_t or_session_joint_log(const or_session_t *s, const int **best, const float
 /* per emitted token, the smallest top-2 joint margin of the decisions that produced it; *tail is the
  * smallest margin of the decisions after the last token (INFINITY when there are none) */
 size_t or_session_token_margins(const or_session_t *s, const float **margin, float *tail);
+/* committed greedy decisions of the decodes since reset: outcome, runner-up index, top-2 margin */
+size_t or_session_decisions(const or_session_t *s, const int **best, const int **second, const float **margin);
+/* force committed decision at[i] to token tok[i] in the following decodes (test hook) */
+void or_session_force(or_session_t *s, const size_t *at, const int *tok, size_t n);
 /* For tests of compaction-independence: the epoch length in chunks (reference CACHE_EPOCH_CHUNKS). */
 const char *or_session_error(const or_session_t *s);
 

@@ -109,6 +109,10 @@ def lib() -> C.CDLL:
         L.or_session_joint_log.restype = C.c_size_t
         L.or_session_token_margins.argtypes = [C.c_void_p, C.POINTER(_f32p), C.POINTER(C.c_float)]
         L.or_session_token_margins.restype = C.c_size_t
+        L.or_session_decisions.argtypes = [C.c_void_p, C.POINTER(_i32p), C.POINTER(_i32p), C.POINTER(_f32p)]
+        L.or_session_decisions.restype = C.c_size_t
+        L.or_session_force.argtypes = [C.c_void_p, C.POINTER(C.c_size_t), _i32p, C.c_size_t]
+        L.or_session_force.restype = None
         L.or_session_error.argtypes = [C.c_void_p]
         L.or_session_error.restype = C.c_char_p
         L.or_enc_plan.argtypes = [C.POINTER(EncBook), C.c_int, C.c_int, C.c_int, C.c_int]
@@ -361,12 +365,15 @@ class Session:
 
     def __init__(self, model: Model, right: int, dump: bool = False):
         self.model = model
+        self.right = right
         self.h = lib().or_session_create(model.handle, right)
         lib().or_session_set_dump(self.h, int(dump))
         self.tokens: list[int] = []
+        self._mel: list[np.ndarray] = []
 
     def feed_mel(self, mel: np.ndarray, final: bool = False) -> list[int]:
         mel = f32(mel).reshape(-1, self.model.dims.feat_in)
+        self._mel.append(mel.copy())
         buf = np.zeros(1 << 20, np.int32)
         n = lib().or_session_feed_mel(self.h, fp(mel), mel.shape[0], int(final), buf.ctypes.data_as(_i32p), buf.size)
         if n < 0:
@@ -378,6 +385,25 @@ class Session:
     def reset(self):
         lib().or_session_reset(self.h)
         self.tokens = []
+        self._mel = []
+
+    def replayer(self):
+        """rerun(forced) for the tests' token check: a fresh session of the same model and latency
+        decodes the mel rows fed since reset in one piece (feed granularity does not change the
+        decode) with committed decisions forced; returns (tokens, outcomes, runner-ups, margins,
+        blank id)."""
+        nm = self.model.dims.feat_in
+        mel = np.concatenate(self._mel) if self._mel else np.zeros((0, nm), np.float32)
+        model, right = self.model, self.right
+
+        def run(forced):
+            o = Session(model, right)
+            o.force(forced)
+            o.feed_mel(mel, final=True)
+            best, second, margin = o.decisions()
+            return list(o.tokens), best, second, margin, model.dims.blank_id
+
+        return run
 
     @property
     def frames(self) -> int:
@@ -418,6 +444,24 @@ class Session:
         n = lib().or_session_token_margins(self.h, C.byref(m), C.byref(tail))
         head = np.ctypeslib.as_array(m, shape=(n,)).copy() if n else np.zeros(0, np.float32)
         return np.append(head, np.float32(tail.value))
+
+    def decisions(self):
+        """Committed greedy decisions since reset: (outcome, runner-up index, top-2 margin) arrays.
+        A decision is one frame's blank or one emitted token (src/decoder.c:107-123)."""
+        b, s2, m = _i32p(), _i32p(), _f32p()
+        n = lib().or_session_decisions(self.h, C.byref(b), C.byref(s2), C.byref(m))
+        if n == 0:
+            return np.zeros(0, np.int32), np.zeros(0, np.int32), np.zeros(0, np.float32)
+        return (np.ctypeslib.as_array(b, shape=(n,)).copy(), np.ctypeslib.as_array(s2, shape=(n,)).copy(),
+                np.ctypeslib.as_array(m, shape=(n,)).copy())
+
+    def force(self, forced: dict):
+        """Force committed decision j to token forced[j] in the following decodes (the other side of
+        a float tie)."""
+        at = sorted(forced)
+        arr_at = (C.c_size_t * max(1, len(at)))(*at)
+        arr_tok = np.array([forced[j] for j in at] or [0], np.int32)
+        lib().or_session_force(self.h, arr_at, arr_tok.ctypes.data_as(_i32p), len(at))
 
     def __del__(self):
         if getattr(self, "h", None):

@@ -160,6 +160,16 @@ struct or_session {
     float *tk_margin;
     size_t tk_n, tk_cap;
     float seg_min;
+    /* committed greedy decisions (a blank frame or an emitted token; speculative scores of frames
+     * redone after an emission are not counted): outcome, runner-up index, top-2 margin */
+    int *cd_best, *cd_second;
+    float *cd_margin;
+    size_t cd_n, cd_cap;
+    /* forced outcomes: committed decision force_at[i] takes token force_tok[i] (test hook: replays a
+     * decode that took the other side of a float tie) */
+    size_t *force_at;
+    int *force_tok;
+    size_t nforce;
     char err[256];
 };
 
@@ -200,6 +210,8 @@ void or_session_free(or_session_t *s) {
     free(s->pending);
     free(s->d_layers); free(s->d_prompted); free(s->d_joint); free(s->d_rows);
     free(s->jl_best); free(s->jl_margin); free(s->tk_margin);
+    free(s->cd_best); free(s->cd_second); free(s->cd_margin);
+    free(s->force_at); free(s->force_tok);
     free(s);
 }
 
@@ -220,7 +232,26 @@ void or_session_reset(or_session_t *s) {
     s->d_nchunks = 0;
     s->jl_n = 0;
     s->tk_n = 0;
+    s->cd_n = 0;
     s->seg_min = INFINITY;
+}
+
+/* The decisions to force in the next decodes of this session (committed decision index, token);
+ * kept across reset.  n = 0 clears them. */
+void or_session_force(or_session_t *s, const size_t *at, const int *tok, size_t n) {
+    free(s->force_at);
+    free(s->force_tok);
+    s->force_at = n ? malloc(n * sizeof *s->force_at) : NULL;
+    s->force_tok = n ? malloc(n * sizeof *s->force_tok) : NULL;
+    for (size_t i = 0; i < n; ++i) { s->force_at[i] = at[i]; s->force_tok[i] = tok[i]; }
+    s->nforce = n;
+}
+
+size_t or_session_decisions(const or_session_t *s, const int **best, const int **second, const float **margin) {
+    *best = s->cd_best;
+    *second = s->cd_second;
+    *margin = s->cd_margin;
+    return s->cd_n;
 }
 
 void or_session_set_dump(or_session_t *s, int on) { s->dump = on; }
@@ -426,21 +457,35 @@ static int decode(or_session_t *s, const float *joint_enc, int frames, int *out,
         int rows = frames - t;
         if (rows > OR_DEC_MAX_BATCH) rows = OR_DEC_MAX_BATCH;
         if (!s->pred_valid) encode_pred(s);
-        int res[OR_DEC_MAX_BATCH];
+        int res[OR_DEC_MAX_BATCH], res2[OR_DEC_MAX_BATCH];
         for (int i = 0; i < rows; ++i) {
             float bv;
             res[i] = or_joint_argmax(joint_enc + (size_t)(t + i) * J, s->pred_out, m->g.joint_out_w, m->joint_out_b, V, J,
                                      &bv, logits);
             float second = -INFINITY;
-            for (int k = 0; k < V; ++k) if (k != res[i] && logits[k] > second) second = logits[k];
+            res2[i] = -1;
+            for (int k = 0; k < V; ++k)
+                if (k != res[i] && logits[k] > second) { second = logits[k]; res2[i] = k; }
             jlog(s, res[i], bv - second);
         }
         s->joint_steps++;
         s->pred_valid = 1;
         int i = 0;
         for (; i < rows; ++i) {
-            const int pred = res[i];
+            int pred = res[i];
             const float mg = s->jl_margin[s->jl_n - (size_t)rows + (size_t)i];
+            for (size_t f = 0; f < s->nforce; ++f)
+                if (s->force_at[f] == s->cd_n) pred = s->force_tok[f];
+            if (s->cd_n == s->cd_cap) {
+                s->cd_cap = s->cd_cap ? 2 * s->cd_cap : 1024;
+                s->cd_best = realloc(s->cd_best, s->cd_cap * sizeof(int));
+                s->cd_second = realloc(s->cd_second, s->cd_cap * sizeof(int));
+                s->cd_margin = realloc(s->cd_margin, s->cd_cap * sizeof(float));
+            }
+            s->cd_best[s->cd_n] = pred;
+            s->cd_second[s->cd_n] = res2[i];
+            s->cd_margin[s->cd_n] = mg;
+            s->cd_n++;
             if (mg < s->seg_min) s->seg_min = mg;
             if (pred == d->blank_id) { symbols = 0; continue; }
             if (s->tk_n == s->tk_cap) {

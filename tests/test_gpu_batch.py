@@ -2,8 +2,9 @@
 
 Every stream of a batch must emit exactly the tokens that the oracle's single-stream session emits
 for that stream's audio, whatever the other streams do: different lengths, staggered starts,
-streams ending while others continue, a slot reused after reset (conftest.check_tokens: the only
-exception is a float tie of the oracle's greedy decision, after which the comparison stops).  The
+streams ending while others continue, a slot reused after reset (conftest.check_tokens: at a float
+tie of the oracle's greedy decision the oracle is replayed with that decision taken the GPU's way,
+and the comparison goes on to the end of the stream).  The
 joint.enc rows of each stream (the joint's encoder input) are held to the encoder gate of the
 single-stream tests (1e-3 relative).
 """
@@ -24,14 +25,14 @@ _ORACLE = {}
 
 
 def oracle_run(om, latency, mel, key=None):
-    """Oracle tokens, joint.enc rows and per-token decision margins of one stream (cached by key
-    across parametrizations)."""
+    """Oracle tokens, joint.enc rows, per-token decision margins and the replay for ties
+    (oracle.Session.replayer) of one stream (cached by key across parametrizations)."""
     if key is not None and key in _ORACLE:
         return _ORACLE[key]
     o = oracle.Session(om, LAT_RIGHT[latency], dump=True)
     o.feed_mel(mel, final=True)
     _, _, oj, _ = o.dumps()
-    res = (list(o.tokens), oj, o.token_margins())
+    res = (list(o.tokens), oj, o.token_margins(), o.replayer())
     if key is not None:
         _ORACLE[key] = res
     print(f"  oracle {key or ''}: {mel.shape[0]} mel rows, {len(o.tokens)} tokens", flush=True)
@@ -56,12 +57,12 @@ def drive(b, mels, starts, piece):
 
 def check_streams(b, om, latency, mels, J, tag=None):
     for s, m in enumerate(mels):
-        toks, oj, margins = oracle_run(om, latency, m, None if tag is None else (tag, s))
+        toks, oj, margins, rerun = oracle_run(om, latency, m, None if tag is None else (tag, s))
         gj = b.joint_enc(s, J)
         assert gj.shape == oj.shape, (s, gj.shape, oj.shape)
         err = rel_err(gj, oj)
         assert err <= 1e-3, (s, err)
-        check_tokens(b.tokens(s), toks, margins, f"stream {s}: ")
+        check_tokens(b.tokens(s), toks, margins, f"stream {s}: ", rerun=rerun)
 
 
 @pytest.mark.parametrize("device_loop", [True, False])
@@ -139,11 +140,11 @@ def test_batch_matches_sessions_full():
     b.run()
     sess = nemoasr.Session(mdir, "en-US", 560)
     for s, m in enumerate(mels):
-        toks, _, margins = oracle_run(om, 560, m)
+        toks, _, margins, rerun = oracle_run(om, 560, m)
         sess.reset("en-US", 560)
         sess.feed_mel(m, final=True)
-        check_tokens(b.tokens(s), toks, margins, f"batch stream {s}: ")
-        check_tokens(sess.tokens(), toks, margins, f"session {s}: ")
+        check_tokens(b.tokens(s), toks, margins, f"batch stream {s}: ", rerun=rerun)
+        check_tokens(sess.tokens(), toks, margins, f"session {s}: ", rerun=rerun)
     sess.close()
     b.close()
 
@@ -154,7 +155,8 @@ def test_batch_many_streams_compacted(latency):
     blocks past the live count that return at once and the joint GEMM's device-side row count,
     with streams of different lengths and starts (so the live count changes from step to step),
     against the oracle (and single-stream sessions, also against the oracle).  Streams 93 and 121
-    carry float ties of the oracle (top-2 margins 3.9e-6 and 2.8e-6 at tokens 59 and 52)."""
+    carried float ties of the oracle (top-2 margins 3.9e-6 and 2.8e-6 at tokens 59 and 52) when the
+    GPU still summed with atomics; any tie is followed to the end of its stream."""
     import nemoasr
 
     mdir = model_dir("tiny")
@@ -166,12 +168,12 @@ def test_batch_many_streams_compacted(latency):
     sess = nemoasr.Session(mdir, "en-US", latency)
     ties = 0
     for s, m in enumerate(mels):
-        toks, _, margins = oracle_run(om, latency, m, ("many", latency, s))
+        toks, _, margins, rerun = oracle_run(om, latency, m, ("many", latency, s))
         sess.reset("en-US", latency)
         sess.feed_mel(m, final=True)
-        ties += check_tokens(b.tokens(s), toks, margins, f"batch stream {s}: ") is not None
-        ties += check_tokens(sess.tokens(), toks, margins, f"session {s}: ") is not None
-    print(f"  {ties} float ties among {2 * S} decodes", flush=True)
+        ties += check_tokens(b.tokens(s), toks, margins, f"batch stream {s}: ", rerun=rerun) or 0
+        ties += check_tokens(sess.tokens(), toks, margins, f"session {s}: ", rerun=rerun) or 0
+    print(f"  {ties} float ties among {2 * S} decodes, each followed to the end of its stream", flush=True)
     sess.close()
     b.close()
 
@@ -212,8 +214,8 @@ def test_batch_audio_and_reset(gpu_fe):
         b.step()
     b.run()
     for s, a in enumerate(audios):
-        toks, _, margins = oracle_run(om, 560, mel_ref.logmel(a))
-        check_tokens(b.tokens(s), toks, margins, f"stream {s}: ")
+        toks, _, margins, rerun = oracle_run(om, 560, mel_ref.logmel(a))
+        check_tokens(b.tokens(s), toks, margins, f"stream {s}: ", rerun=rerun)
         b.text(s)
     first = b.tokens(1)
     b.reset_stream(1)
@@ -254,9 +256,9 @@ def test_batch_gpu_frontend_matches_host(latency):
     for s, a in enumerate(audios):
         (tg, jg), (th, jh) = out[0][s], out[1][s]
         assert rel_err(jg, jh) < 1e-4, s
-        toks, _, margins = oracle_run(om, latency, mel_ref.logmel(a))
-        check_tokens(tg, toks, margins, f"gpu front end, stream {s}: ")
-        check_tokens(th, toks, margins, f"host front end, stream {s}: ")
+        toks, _, margins, rerun = oracle_run(om, latency, mel_ref.logmel(a))
+        check_tokens(tg, toks, margins, f"gpu front end, stream {s}: ", rerun=rerun)
+        check_tokens(th, toks, margins, f"host front end, stream {s}: ", rerun=rerun)
 
 
 def test_batch_mixed_input_rejected():
@@ -350,6 +352,60 @@ def test_batch_single_stream_and_empty_steps():
     o.feed_mel(mel_ref.logmel(audio), final=True)
     b.push(0, audio, final=True)
     b.run()
-    check_tokens(b.tokens(0), o.tokens, o.token_margins())
+    check_tokens(b.tokens(0), o.tokens, o.token_margins(), rerun=o.replayer())
     assert b.step() == 0 and b.stats()["chunks"] == o.chunks
+    b.close()
+
+
+def test_batch64_full_model_rows448():
+    """The 64-stream, 560 ms workload at its real row count, end to end with the full model: stream
+    s starts at step s % 8 and takes 8 - s % 8 chunks (tests/golden/make_batch64.py), so at step 7
+    all 64 streams run a chunk in one batched step (448 encoder rows per GEMM) with 0 to 7 chunks
+    of cache history each.  Every stream's tokens against the oracle's (committed fixture, the tie
+    rule replaying the oracle only if a tie occurs) and two joint.enc rows per stream (1e-3)."""
+    import os
+
+    import nemoasr
+
+    g = np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "batch64_560.npz"))
+    mdir = model_dir("full")
+    S, piece = 64, 56
+    mels = [mel_ref.logmel(synth.make_audio((8 - s % 8) * 0.56, seed=6400 + s)) for s in range(S)]
+    b = nemoasr.Batch(mdir, "en-US", 560, streams=S)
+    b.set_dump(True)
+    pos, tick, step_rows = [0] * S, 0, []
+    while any(p < m.shape[0] for p, m in zip(pos, mels)):
+        for s, m in enumerate(mels):
+            if tick < s % 8 or pos[s] >= m.shape[0]:
+                continue
+            end = min(pos[s] + piece, m.shape[0])
+            if m.shape[0] - end < 8:  # the frame left over by the mel framing goes with the last chunk
+                end = m.shape[0]
+            b.push_mel(s, m[pos[s]:end], final=end >= m.shape[0])
+            pos[s] = end
+        rows0 = b.stats()["rows"]
+        n = b.step()
+        step_rows.append((n, b.stats()["rows"] - rows0))
+        tick += 1
+    b.run()
+    print(f"  (streams, rows) per step: {step_rows}", flush=True)
+    assert (64, 448) in step_rows
+    om = None
+    J = 640
+    for s in range(S):
+        toks = g["tokens"][g["offsets"][s]:g["offsets"][s + 1]].astype(int).tolist()
+        margins = g["margins"][g["margin_offsets"][s]:g["margin_offsets"][s + 1]]
+        je = b.joint_enc(s, J)
+        fr = g["joint_enc_frames"][s]
+        assert je.shape[0] == fr[1] + 1, (s, je.shape)
+        assert rel_err(je[fr], g["joint_enc"][s]) <= 1e-3, s
+
+        def rerun(forced, s=s):
+            nonlocal om
+            om = om or oracle.Model(mdir, "en-US")
+            o = oracle.Session(om, LAT_RIGHT[560])
+            o.feed_mel(mels[s], final=True)
+            return o.replayer()(forced)
+
+        check_tokens(b.tokens(s), toks, margins, f"stream {s}: ", rerun=rerun)
     b.close()

@@ -6,7 +6,8 @@ through its CPU restatement.  Gates (from the scope of this path):
   - per-layer encoder activations: max|gpu - oracle| / max|oracle| <= 2e-3 for every layer;
   - joint.enc rows (the joint's encoder input): <= 1e-3; joint logits are checked per kernel;
   - emitted token ids: identical, except at a float tie of the oracle's greedy decision
-    (conftest.check_tokens: top-2 joint margin below TOKEN_TIE), where the comparison stops.
+    (conftest.check_tokens: top-2 joint margin below TOKEN_TIE); there the oracle is replayed with
+    that decision taken the GPU's way and the comparison goes on to the end of the stream.
 """
 import os
 import wave
@@ -17,7 +18,7 @@ import pytest
 import mel_ref
 import oracle
 import synth
-from conftest import check_tokens, model_dir, rel_err
+from conftest import check_oracle, check_tokens, model_dir, rel_err
 
 pytestmark = pytest.mark.gpu
 
@@ -55,7 +56,7 @@ def check_parity(om, o, s, d, check_dumps=True):
         assert max(errs) <= 2e-3, errs
         assert rel_err(gp, op) <= 2e-3
         assert rel_err(gj, oj) <= 1e-3
-    check_tokens(toks_g, o.tokens, o.token_margins())
+    check_oracle(toks_g, o)
 
 
 @pytest.mark.parametrize("latency", [80, 560, 1120])
@@ -104,8 +105,8 @@ def test_fused_launches_match_separate(latency):
         out.append((s.tokens(), s.dumps(d.n_layers, d.d_model, d.joint_hidden)))
         s.close()
     (tf, (lf, pf, jf)), (ts, (ls, ps, js)) = out
-    check_tokens(tf, o.tokens, o.token_margins(), "fused: ")
-    check_tokens(ts, o.tokens, o.token_margins(), "separate: ")
+    check_oracle(tf, o, "fused: ")
+    check_oracle(ts, o, "separate: ")
     assert rel_err(lf, ls) < 1e-5 and rel_err(jf, js) < 1e-5
 
 
@@ -123,7 +124,7 @@ def test_audio_api_tiny():
     text = ""
     for i in range(0, audio.size, 1600):
         text += s.feed(audio[i:i + 1600], final=i + 1600 >= audio.size)
-    if check_tokens(s.tokens(), o.tokens, o.token_margins()) is None:
+    if check_oracle(s.tokens(), o) is None:
         assert s.stats()["tokens"] == len(o.tokens)
     assert s.stats()["chunks"] == o.chunks
     s.close()
@@ -145,7 +146,7 @@ def test_reset_replays_identically():
     o = oracle.Session(om, 0)
     o.feed_mel(mel, final=True)
     s.feed_mel(mel, final=True)
-    check_tokens(s.tokens(), o.tokens, o.token_margins())
+    check_oracle(s.tokens(), o)
     s.close()
 
 
@@ -216,7 +217,7 @@ def test_golden_token_cases(case):
         s = nemoasr.Session(mdir, case["language"], lat)
         s.use_graphs(graphs)
         s.feed_mel(mel, final=True)
-        check_tokens(s.tokens(), case["tokens"], o.token_margins(), f"graphs {graphs}: ")
+        check_tokens(s.tokens(), case["tokens"], o.token_margins(), f"graphs {graphs}: ", rerun=o.replayer())
         assert s.stats()["chunks"] == case["chunks"]
         s.close()
     if case["blank_bias"] > 0:
@@ -294,7 +295,7 @@ def test_api_ragged_and_empty_feeds(latency):
     s.feed(np.zeros(0, np.float32), final=True)  # the final flush carries no samples
     assert s.tokens() == whole.tokens()
     assert s.stats()["chunks"] == whole.stats()["chunks"] == o.chunks
-    check_tokens(s.tokens(), o.tokens, o.token_margins())
+    check_oracle(s.tokens(), o)
     s.close()
     whole.close()
 
@@ -310,7 +311,7 @@ def test_api_clip_shorter_than_a_chunk(seconds):
     o = _oracle_audio_tokens(mdir, audio, 560)
     s = nemoasr.Session(mdir, "en-US", 560)
     s.feed(audio, final=True)
-    check_tokens(s.tokens(), o.tokens, o.token_margins())
+    check_oracle(s.tokens(), o)
     assert s.stats()["chunks"] == o.chunks
     s.close()
 
@@ -346,6 +347,6 @@ def test_api_input_rate(rate):
     s = nemoasr.Session(mdir, "en-US", 560, input_rate=rate)
     for i in range(0, audio.size, rate // 10):
         s.feed(audio[i:i + rate // 10], final=i + rate // 10 >= audio.size)
-    check_tokens(s.tokens(), o.tokens, o.token_margins())
+    check_oracle(s.tokens(), o)
     assert s.stats()["chunks"] == o.chunks
     s.close()

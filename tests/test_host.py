@@ -95,6 +95,54 @@ def test_every_kernel_takes_one_argument_block():
     assert not bad, bad
 
 
+def test_reference_runtime_header_compiles_and_links(tmp_path):
+    """include/nemo_gpu.h and include/nemo_kernel_params.h: a host unit written the way the
+    reference's launchers are (src/model.c:70-111: GemmParams by value, GPU_BUF / GPU_BYTES,
+    gpu_dispatch_groups_fc with function constants) compiles with gcc, the parameter blocks have the
+    reference's layout (src/kernel_params.h:22-32), and the program links against the library and
+    runs (gpu_create takes the reference's source argument and fails cleanly without a GPU)."""
+    import shutil
+    import subprocess
+
+    if not shutil.which("gcc"):
+        pytest.skip("gcc not present")
+    src = tmp_path / "refhost.c"
+    src.write_text(r"""
+#include <stddef.h>
+#include <stdio.h>
+#include "nemo_gpu.h"
+#include "nemo_kernel_params.h"
+_Static_assert(sizeof(GemmParams) == 40 && offsetof(GemmParams, has_bias) == 24 && offsetof(GemmParams, alpha) == 36, "GemmParams");
+_Static_assert(sizeof(LnParams) == 12 && offsetof(LnParams, eps) == 8, "LnParams");
+_Static_assert(sizeof(AttnParams) == 36 && offsetof(AttnParams, ldk) == 28 && offsetof(AttnParams, scale) == 32, "AttnParams");
+_Static_assert(sizeof(GluParams) == 8 && sizeof(DwParams) == 16 && offsetof(DwParams, eps) == 12, "Glu/Dw");
+_Static_assert(sizeof(Conv2dParams) == 20 && sizeof(FlatParams) == 12 && sizeof(CountParams) == 4, "conv");
+_Static_assert(sizeof(FillParams) == 8 && sizeof(LstmParams) == 4 && sizeof(JointParams) == 16, "misc");
+_Static_assert(sizeof(gpu_arg_t) == 4 * sizeof(void *), "gpu_arg_t");
+static int k_gemm_like(gpu_t *g, gpu_buf_t *A, gpu_buf_t *W, gpu_buf_t *C) {
+    GemmParams p = { 7, 4096, 1024, 1024, 1024, 4096, 0, 1, 0, 1.0f };
+    gpu_arg_t args[5] = { GPU_BUF(A, 0), GPU_BUF(W, 0), GPU_BUF(A, 0), GPU_BUF(C, 0), GPU_BYTES(&p) };
+    uint32_t fc[7] = { 7, 0, 0, 1, 2, 8, 32 };
+    return gpu_dispatch_groups_fc(g, "gemm_mma", fc, 7, args, 5, 256, 1, 1, 256, 1, 1);
+}
+int main(void) {
+    char err[256] = "";
+    gpu_t *g = gpu_create("metal source text", err, sizeof err);
+    if (g) { gpu_buf_t *b = gpu_buf_alloc(g, 64); (void)gpu_buf_ptr(b); (void)k_gemm_like; gpu_buf_free(b); gpu_destroy(g); return 2; }
+    printf("%s\n", err);
+    return err[0] ? 0 : 1;
+}
+""")
+    exe = tmp_path / "refhost"
+    pkg = os.path.join(REPO, "nemo-c_amd")
+    subprocess.run(["gcc", "-std=c11", "-Wall", "-Werror", "-I", os.path.join(REPO, "include"), str(src), "-o", str(exe),
+                    "-L", pkg, "-lnemoasr_hip", f"-Wl,-rpath,{pkg}"], check=True)
+    r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=60)
+    if r.returncode == 2:
+        pytest.skip("a GPU is present: the no-device path is not exercised")
+    assert r.returncode == 0, r.stdout + r.stderr
+
+
 def test_open_without_gpu_fails_loudly(tiny_model_dir):
     import torch
 

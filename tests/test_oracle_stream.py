@@ -248,3 +248,37 @@ def test_prompt_fold_equals_one_hot_concat(language):
     other = next(v for k, v in dic.items() if v != idx)
     for wrong in (unfolded(D + other), unfolded(None), unfolded(idx)):
         assert float(np.max(np.abs(prompted - wrong)) / np.max(np.abs(ref))) > 1e-2
+
+
+def test_token_check_follows_a_forced_tie(tiny_model_dir, monkeypatch):
+    """The tie rule of conftest.check_tokens, on the CPU: a decode that took the runner-up at one
+    committed decision (what a GPU does at a float tie) passes when that decision counts as a tie
+    and the replay forced to it matches to the end; with the tie bound at 0 it fails; and a decode
+    with a token changed at no decision of the replay's (a planted error) fails either way."""
+    import conftest
+
+    om = oracle.Model(tiny_model_dir, "en-US")
+    mel = mel_ref.logmel(synth.make_audio(1.2, seed=31))
+    o = oracle.Session(om, 6)
+    o.feed_mel(mel, final=True)
+    best, second, margin = o.decisions()
+    assert len(best) > 10 and len(o.tokens) > 3
+    assert np.all(second != best) and np.all(margin >= 0)
+    j = 2 + int(np.argmin(margin[2:60]))  # the closest of the first decisions: no earlier one is as close
+    forced = oracle.Session(om, 6)
+    forced.force({j: int(second[j])})
+    forced.feed_mel(mel, final=True)
+    assert forced.tokens != o.tokens
+    fb, _, _ = forced.decisions()
+    assert fb[j] == second[j] and np.array_equal(fb[:j], best[:j])
+    monkeypatch.setattr(conftest, "TOKEN_TIE", float(np.nextafter(margin[j], np.float32(np.inf))))
+    assert np.all(margin[:j] >= conftest.TOKEN_TIE)  # so the check picks j
+    assert conftest.check_tokens(forced.tokens, o.tokens, o.token_margins(), rerun=o.replayer()) == 1
+    monkeypatch.setattr(conftest, "TOKEN_TIE", 0.0)
+    with pytest.raises(AssertionError):
+        conftest.check_tokens(forced.tokens, o.tokens, o.token_margins(), rerun=o.replayer())
+    bad = list(o.tokens)
+    bad[-1] = (bad[-1] + 1) % om.dims.vocab_size
+    monkeypatch.setattr(conftest, "TOKEN_TIE", 1e-4)
+    with pytest.raises(AssertionError):
+        conftest.check_tokens(bad, o.tokens, o.token_margins(), rerun=o.replayer())
