@@ -25,6 +25,8 @@ extern "C" {
 /* ---- kernel-level restatements (reference src/kernels.metal) ------------------------------ */
 enum { OR_ACT_NONE = 0, OR_ACT_SILU = 1, OR_ACT_RELU = 2, OR_ACT_GLU = 3 };
 
+/* numerics study switch: GEMM A operand as f32 (0, the reference), bf16 (1), bf16 hi + lo (2) */
+void or_set_gemm_a_mode(int mode);
 void or_gemm(const float *A, long lda, const uint16_t *W, long ldw, const float *bias,
              float *C, long ldc, int M, int N, int K, int act, int accumulate, float alpha);
 void or_layernorm(const float *X, const float *g, const float *b, float *Y, int M, int D, float eps);

@@ -109,6 +109,8 @@ def lib() -> C.CDLL:
         L.or_session_joint_log.restype = C.c_size_t
         L.or_session_token_margins.argtypes = [C.c_void_p, C.POINTER(_f32p), C.POINTER(C.c_float)]
         L.or_session_token_margins.restype = C.c_size_t
+        L.or_set_gemm_a_mode.argtypes = [C.c_int]
+        L.or_set_gemm_a_mode.restype = None
         L.or_session_decisions.argtypes = [C.c_void_p, C.POINTER(_i32p), C.POINTER(_i32p), C.POINTER(_f32p)]
         L.or_session_decisions.restype = C.c_size_t
         L.or_session_force.argtypes = [C.c_void_p, C.POINTER(C.c_size_t), _i32p, C.c_size_t]

@@ -33,10 +33,41 @@ float or_silu(float v) { return v / (1.0f + expf(-v)); }
  *                C[m][j] (=|+=) (sa_j + b_j) * sigmoid(sb_{j+N/2} + b_{j+N/2}) * alpha
  * Each dot product is summed in f32 in increasing k; four columns are interleaved only to break
  * the add dependency chain, which leaves each column's order unchanged. */
+/* Numerics study switch (not the reference's semantics, which is mode 0): the GEMMs' A operand as
+ * f32 (0), rounded to bf16 (1), or as the bf16 pair hi = RNE(a), lo = RNE(a - hi) summed (2; the
+ * split the batched GPU GEMMs feed their bf16 MFMAs).  Used by oracle/study_a_precision.py. */
+static int g_a_mode;
+void or_set_gemm_a_mode(int mode) { g_a_mode = mode; }
+static float rne_bf16(float x) {
+    uint32_t u;
+    memcpy(&u, &x, 4);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    u &= 0xffff0000u;
+    float r;
+    memcpy(&r, &u, 4);
+    return r;
+}
+static float a_val(float a) {
+    if (g_a_mode == 1) return rne_bf16(a);
+    if (g_a_mode == 2) {
+        const float hi = rne_bf16(a);
+        return hi + rne_bf16(a - hi);
+    }
+    return a;
+}
+
 void or_gemm(const float *A, long lda, const uint16_t *W, long ldw, const float *bias,
              float *C, long ldc, int M, int N, int K, int act, int accumulate, float alpha) {
     const int glu = act == OR_ACT_GLU;
     const int nout = glu ? N / 2 : N;
+    float *Ar = NULL;
+    if (g_a_mode) {
+        Ar = malloc(sizeof(float) * (size_t)M * (size_t)K);
+        for (int m = 0; m < M; ++m)
+            for (int k = 0; k < K; ++k) Ar[(size_t)m * K + k] = a_val(A[(size_t)m * lda + k]);
+        A = Ar;
+        lda = K;
+    }
 #pragma omp parallel
     {
         float *w = malloc(sizeof(float) * (size_t)K * 2);
@@ -75,6 +106,7 @@ void or_gemm(const float *A, long lda, const uint16_t *W, long ldw, const float 
         free(w);
         free(acc);
     }
+    free(Ar);
 }
 
 /* One LayerNorm row: src/kernels.metal:257-288.  mean = sum/D; var = sum((x-mean)^2)/D (biased);
