@@ -26,7 +26,9 @@ direct-launch pass in which each step's greedy loop is drained before the next s
 the durations are the kernels' own and not shared with the overlapping loop of the timed passes).
 
 CPU baseline: the oracle's C restatement (log-mel + encoder + greedy RNNT) on bounded samples of the
-headline clip on this host's cores, at one thread and at all threads given to this process.
+headline clip and of every leg's workload on this host's cores, at one thread and at all threads
+given to this process: RTFx and the median chunk time (batch legs: streams one after another, the
+step time being the stream count times the chunk time).
 """
 import argparse
 import glob
@@ -150,6 +152,14 @@ def single_leg(a, nemoasr, synth, mdir, cfg, latency, seconds, lang="en-US", ste
     achieved = (kbytes / max(kn, 1)) / (kms * 1e-3) / 1e9 if kn and kms > 0 else 0.0
     gpu_name = s.gpu_name
     s.close()
+    # a freshly opened session: open time (model load + warm-up, which captures the session's chunk
+    # and decoder graphs) and its first chunk's latency
+    s = nemoasr.Session(mdir, lang, latency)
+    open_ms = s.load_ms
+    for i in range(0, min(audio.size, 4 * piece), piece):
+        s.feed(audio[i:i + piece])
+    first = s.chunk_ms()
+    s.close()
     frames = frames_fn(audio.size)
     return {
         "workload": f"1 stream, {latency} ms latency ({right + 1} encoder frame(s)/chunk), {audio_s:g} s of 16 kHz "
@@ -160,6 +170,7 @@ def single_leg(a, nemoasr, synth, mdir, cfg, latency, seconds, lang="en-US", ste
         "p_blank": p_blank(frames, toks / steps),
         "joint_round_trips_per_clip": int(trips / steps),
         "p50_chunk_ms": round(float(np.median(cms)), 4), "p90_chunk_ms": round(float(np.percentile(cms, 90)), 4),
+        "first_chunk_ms": round(float(first[0]), 4) if first.size else None, "open_ms": round(open_ms, 1),
         "encoder_gpu_ms_per_chunk": round(enc_ms, 4), "encoder_weight_bytes_per_chunk": wb,
         "encoder_chunk_hbm_gbs": round(wb / (enc_ms * 1e-3) / 1e9, 1) if enc_ms > 0 else None,
         "graphs": not a.no_graphs, "gpu": gpu_name,
@@ -274,21 +285,87 @@ def cpu_model() -> str:
     return "unknown"
 
 
-def cpu_leg(mdir, audio, right, latency, threads, sample_s):
+_ORACLE_MODELS = {}
+
+
+def cpu_sample(mdir, lang, latency, clips, threads, what):
+    """The oracle's C restatement (log-mel + encoder + greedy RNNT) on `clips` (one stream after
+    another, each fed one chunk of mel rows at a time) with `threads` threads: RTFx over the sample
+    and the median chunk time (one chunk's encoder step and its greedy decode)."""
     import mel_ref
     import oracle
 
     oracle.lib().or_set_threads(threads)
-    om = oracle.Model(mdir, "en-US")
-    sample = audio[: int(sample_s * 16000)]
-    t0 = time.perf_counter()
-    o = oracle.Session(om, right)
-    o.feed_mel(mel_ref.logmel(sample), final=True)
-    dt = time.perf_counter() - t0
-    return {"value": round(sample.size / 16000.0 / dt, 4), "unit": "audio-s/s", "cores": threads, "kind": "port",
-            "sample": f"first {sample_s:g} s of the headline clip at {latency} ms latency through the oracle's C "
-                      f"restatement (log-mel + encoder + greedy RNNT), {threads} thread(s), {o.chunks} chunks, "
-                      f"{dt:.1f} s", "seconds": round(dt, 2)}
+    key = (mdir, lang)
+    if key not in _ORACLE_MODELS:
+        _ORACLE_MODELS[key] = oracle.Model(mdir, lang)
+    om = _ORACLE_MODELS[key]
+    right = LAT_RIGHT[latency]
+    cm = 8 * (right + 1)
+    chunk_ms, wall, chunks = [], 0.0, 0
+    for clip in clips:
+        t0 = time.perf_counter()
+        mel = mel_ref.logmel(clip)
+        o = oracle.Session(om, right)
+        for i in range(0, mel.shape[0], cm):
+            tc = time.perf_counter()
+            o.feed_mel(mel[i:i + cm], final=i + cm >= mel.shape[0])
+            if i + cm <= mel.shape[0]:
+                chunk_ms.append(1e3 * (time.perf_counter() - tc))
+        wall += time.perf_counter() - t0
+        chunks += o.chunks
+    audio_s = sum(c.size for c in clips) / 16000.0
+    return {"value": round(audio_s / wall, 4), "unit": "audio-s/s", "cores": threads, "kind": "port",
+            "p50_chunk_ms": round(float(np.median(chunk_ms)), 2) if chunk_ms else None,
+            "sample": f"{what}: {audio_s:g} s of audio through the oracle's C restatement (log-mel + encoder + greedy "
+                      f"RNNT) at {latency} ms latency, {threads} thread(s), {chunks} chunks, {wall:.1f} s",
+            "seconds": round(wall, 2)}
+
+
+def cpu_baselines(synth, mdir, a, want):
+    """Bounded CPU samples of the headline and of every leg, at all threads given to this process
+    and at one thread (a few seconds of CPU work each).  Batch legs: streams one after another (the
+    oracle has no batching); their p50 step is the stream count times the median chunk time."""
+    n = cpu_threads()
+    out = {}
+    head_audio = synth.make_audio(a.seconds, seed=0)
+    chunk_s = {80: 0.08, 560: 0.56, 1120: 1.12}
+    cases = {"S80": (mdir, "en-US", a.latency, [head_audio[: int(a.cpu_sample_s * 16000)]],
+                     [head_audio[: int(a.cpu1_sample_s * 16000)]], "first %s s of the headline clip" % a.cpu_sample_s,
+                     1)}
+    if "S560" in want:
+        clip = synth.make_audio(10.0, seed=0)
+        cases["S560"] = (mdir, "en-US", 560, [clip[:int(3.4 * 16000)]], [clip[:int(0.6 * 16000)]],
+                         "first seconds of the 560 ms leg's clip", 1)
+    if "S1120" in want:
+        clip = synth.make_audio(30.0, seed=0)
+        cases["S1120"] = (model(synth, SKEW_S1120), "en-US", 1120, [clip[:int(3.4 * 16000)]],
+                          [clip[:int(1.2 * 16000)]], "first seconds of the 1120 ms leg's clip (P(blank) 0.5 model)", 1)
+    if "B64" in want:
+        clips = [synth.make_audio(20.0, seed=1000 + s) for s in range(2)]
+        cases["B64"] = (mdir, "en-US", 560, [c[:int(1.2 * 16000)] for c in clips], [clips[0][:int(0.6 * 16000)]],
+                        "first seconds of streams 0-1 of the 64-stream leg", 64)
+    if "B256" in want:
+        clips = [synth.make_audio(60.0, seed=1000 + s) for s in range(2)]
+        cases["B256"] = (model(synth, SKEW_B256), "auto", 1120, [c[:int(2.3 * 16000)] for c in clips],
+                         [clips[0][:int(1.2 * 16000)]], "first seconds of streams 0-1 of the 256-stream leg (auto, "
+                                                        "P(blank) 0.7 model)", 256)
+    # a batch leg's one-thread chunk costs what the single-stream leg of its latency and model size
+    # costs, whose one-thread sample it reuses
+    same = {"B64": "S560", "B256": "S1120"}
+    for leg, (md, lang, lat, many, one, what, streams) in cases.items():
+        full = cpu_sample(md, lang, lat, many, n, what)
+        if leg in same and same[leg] in out:
+            single = dict(out[same[leg]]["single_thread"])
+            single["sample"] = f"the {same[leg]} leg's one-thread sample (same latency and model size): " + single["sample"]
+        else:
+            single = cpu_sample(md, lang, lat, one, 1, what)
+        for r in (full, single):
+            if streams > 1 and r["p50_chunk_ms"] is not None:
+                r["p50_step_ms"] = round(streams * r["p50_chunk_ms"], 1)
+        full["single_thread"] = single
+        out[leg] = full
+    return out
 
 
 def main():
@@ -353,13 +430,12 @@ def main():
 
     cpu = None
     if not a.no_cpu:
-        audio = synth.make_audio(a.seconds, seed=0)
-        right = LAT_RIGHT[a.latency]
-        n = cpu_threads()
-        cpu = cpu_leg(mdir, audio, right, a.latency, n, a.cpu_sample_s)
+        base = cpu_baselines(synth, mdir, a, want)
+        cpu = base.pop("S80")
         cpu["cpu_model"] = cpu_model()
         cpu["nproc"] = os.cpu_count()
-        cpu["single_thread"] = cpu_leg(mdir, audio, right, a.latency, 1, a.cpu1_sample_s)
+        for leg, b in base.items():
+            legs[leg]["cpu_baseline"] = b
 
     out = {
         "metric": METRIC, "value": head["rtfx"], "unit": "audio-s/s", "n_gpus": 1, "steps": a.steps,

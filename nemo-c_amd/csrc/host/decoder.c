@@ -21,6 +21,8 @@
 static const int k_run_steps[] = { 11, 3, 7, 15, 31, 63 };
 #define N_RUN_SIZES (int)(sizeof k_run_steps / sizeof k_run_steps[0])
 #define MAX_GRAPHS_PER_CHUNK 64
+/* graph sets kept, one per joint.enc buffer (a session keeps one encoder per prepared latency) */
+#define DEC_GRAPH_SETS 5
 
 static double now_ms(void) {
     struct timespec ts;
@@ -39,7 +41,7 @@ struct decoder {
     gpu_buf_t *st, *part, *tokens, *hc, *pre0, *pred, *tx;
     NkDecState *host_st; /* pinned: chunk fields in, final state out */
     int *host_tok;       /* pinned: tokens of the chunk               */
-    dgraph_t gr[2];
+    dgraph_t gr[DEC_GRAPH_SETS];
     int ngr, last_steps, use_graphs;
     double last_ms;
 };
@@ -111,6 +113,8 @@ void decoder_use_graphs(decoder_t *d, int on) {
 }
 int decoder_last_steps(const decoder_t *d) { return d->last_steps; }
 
+
+
 static NkDecArgs dec_args(decoder_t *d, const float *enc, uint32_t parity, uint32_t decide_only) {
     const model_t *m = d->m;
     NkDecArgs a;
@@ -157,7 +161,7 @@ static int launch_steps(decoder_t *d, const float *enc, int steps) {
 static dgraph_t *graphs_for(decoder_t *d, const float *enc) {
     for (int i = 0; i < d->ngr; ++i)
         if (d->gr[i].enc == enc) return &d->gr[i];
-    if (d->ngr == 2) free_graphs(d);
+    if (d->ngr == DEC_GRAPH_SETS) free_graphs(d);
     dgraph_t *x = &d->gr[d->ngr++];
     x->enc = enc;
     return x;
@@ -212,5 +216,26 @@ int decoder_run(decoder_t *d, const float *joint_enc, int frames, int *out, int 
         if (n < max_out) out[n++] = d->host_tok[i];
     d->last_steps = h->joints;
     d->last_ms = now_ms() - t0;
+    return n;
+}
+
+/* Capture the graph of every run size for chunks whose joint.enc rows live at joint_enc, without
+ * running them (warm-up: the first chunks of a session then replay graphs from their first step).
+ * Returns the number of graphs held for that buffer. */
+int decoder_prepare_graphs(decoder_t *d, const float *joint_enc) {
+    if (!d->use_graphs) return 0;
+    dgraph_t *gr = graphs_for(d, joint_enc);
+    int n = 0;
+    for (int k = 0; k < N_RUN_SIZES; ++k) {
+        if (!gr->g[k]) {
+            gpu_begin(d->g);
+            if (!gpu_capture_begin(d->g)) {
+                launch_steps(d, joint_enc, k_run_steps[k]);
+                gr->g[k] = gpu_capture_end(d->g);
+            }
+            if (gpu_end(d->g, NULL, 0)) break;
+        }
+        n += gr->g[k] != NULL;
+    }
     return n;
 }

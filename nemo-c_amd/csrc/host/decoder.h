@@ -16,5 +16,8 @@ double decoder_last_ms(const decoder_t *d);
 /* 1 (default): replay each run of steps from a captured hipGraph; 0: launch every kernel directly */
 void decoder_use_graphs(decoder_t *d, int on);
 int decoder_last_steps(const decoder_t *d); /* joint evaluations (round trips) in the last run */
+/* Capture (without running) the graphs of every run size for joint.enc rows at joint_enc; returns
+ * the number of graphs held for it. */
+int decoder_prepare_graphs(decoder_t *d, const float *joint_enc);
 
 #endif

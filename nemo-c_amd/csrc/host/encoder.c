@@ -55,7 +55,7 @@ struct encoder {
     float *stage_win;
     int *stage_desc;
     /* graphs */
-    int use_graphs;
+    int use_graphs, capture_first;
     int fuse; /* single-stream launch fusions (kernels/nk_fuse.hip) */
     gslot_t gs[MAX_GRAPHS];
     unsigned long long tick;
@@ -160,6 +160,13 @@ int encoder_chunk_mel(const encoder_t *e) { return e->chunk_mel; }
 void encoder_use_graphs(encoder_t *e, int on) {
     e->use_graphs = on;
     if (!on) drop_graphs(e);
+}
+
+void encoder_capture_first(encoder_t *e, int on) { e->capture_first = on != 0; }
+int encoder_graphs(const encoder_t *e) {
+    int n = 0;
+    for (int i = 0; i < MAX_GRAPHS; ++i) n += e->gs[i].graph != NULL;
+    return n;
 }
 
 void encoder_fuse(encoder_t *e, int on) {
@@ -417,8 +424,8 @@ int encoder_step(encoder_t *e, int final, enc_out_t *out, char *err, size_t errl
     if (e->use_graphs && !e->dump) {
         gslot_t *s = graph_slot(e, c, p.nwin, p.lo);
         s->last_use = ++e->tick;
-        if (!s->graph && s->seen >= 1) {
-            /* second chunk of this shape: capture it once, replay from now on */
+        if (!s->graph && (s->seen >= 1 || e->capture_first)) {
+            /* second chunk of this shape (first, during warm-up): capture it once, replay from now on */
             if (!gpu_capture_begin(g)) {
                 launch_chunk(e, p.nwin, p.lo, c);
                 s->graph = gpu_capture_end(g);

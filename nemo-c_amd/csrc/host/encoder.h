@@ -29,6 +29,11 @@ double encoder_take_gpu_ms(encoder_t *e);
 
 /* Replay each chunk shape as a captured hipGraph (default on). */
 void encoder_use_graphs(encoder_t *e, int on);
+/* 1: capture a chunk shape's graph on its first chunk (warm-up); 0 (default): on its second, so a
+ * shape seen once (a stream's last, boundary chunk) costs no capture. */
+void encoder_capture_first(encoder_t *e, int on);
+/* Chunk shapes with a captured graph. */
+int encoder_graphs(const encoder_t *e);
 /* 1 (default): fused attention + out_proj and dwconv + pw2 launches for chunks of few rows. */
 void encoder_fuse(encoder_t *e, int on);
 /* Keep per-layer block outputs of every chunk (test hook). */

@@ -74,9 +74,12 @@ static int check_latency(const model_t *m, int ms, char *err, size_t errlen) {
     return r;
 }
 
+#define N_LATENCIES (int)(sizeof k_latency / sizeof k_latency[0])
+
 struct nemoasr {
     model_t *m;
-    encoder_t *enc;
+    encoder_t *enc;               /* the current latency's, one of encs  */
+    encoder_t *encs[N_LATENCIES]; /* by latency index: prepared encoders */
     decoder_t *dec;
     struct { /* input stage */
         int rate;
@@ -101,7 +104,7 @@ struct nemoasr {
         size_t nmel, capmel;
     } rec;
     nemoasr_stats_t stats;
-    int latency_ms, done, dump;
+    int latency_ms, done, dump, graphs, fuse;
     unsigned warm; /* bit r: chunk shapes of right context r have run once */
     double open_ms;
     int ids[TOKENS_PER_CHUNK_MAX];
@@ -128,31 +131,65 @@ int nemoasr_default_model_dir(char *out, size_t n) {
     return ok ? 0 : -1;
 }
 
-/* Warm-up: 1.5 s of silence through a throwaway encoder and decoder of this right context, so the
- * session's first chunks find every kernel loaded, the graph shapes seen and the scratch sized
- * (the reference warms its pipelines the same way, src/warmup.c:23-42).  Errors are not fatal. */
-static void warm_up(model_t *m, int right) {
-    encoder_t *e = encoder_create(m, right);
-    decoder_t *d = decoder_create(m);
+static int latency_index(int right) {
+    for (int i = 0; i < N_LATENCIES; ++i)
+        if (k_latency[i].right == right) return i;
+    return -1;
+}
+
+/* The session's encoder for a right context (created on first use), with the session's settings. */
+static encoder_t *encoder_for(nemoasr_t *s, int right) {
+    const int i = latency_index(right);
+    if (i < 0) return NULL;
+    if (!s->encs[i]) s->encs[i] = encoder_create(s->m, right);
+    encoder_t *e = s->encs[i];
+    if (e) {
+        encoder_set_dump(e, s->dump);
+        encoder_use_graphs(e, s->graphs);
+        encoder_fuse(e, s->fuse);
+    }
+    return e;
+}
+
+/* Warm-up, as the reference's (src/warmup.c:23-42): silence through an encoder of this right
+ * context and a throwaway decoder, so that every kernel is loaded and the scratch sized.  Here the
+ * encoder is the session's own for that right context (kept for later resets to it), which
+ * captures each chunk shape's hipGraph on first sight (the first chunk's window and the steady
+ * window: at least 1.5 s and three chunks of zeros), and the session's decoder captures, without
+ * running them, its graphs of every run size for that encoder's joint.enc rows.  The encoder then
+ * returns to its start state; the session's decoder state is not touched (a stream in progress at
+ * another latency goes on undisturbed).  Errors are not fatal. */
+static void warm_up(nemoasr_t *s, int right) {
+    encoder_t *e = encoder_for(s, right);
+    decoder_t *d = decoder_create(s->m);
     melfe_t *fe = melfe_create();
     if (e && d && fe) {
-        float *silence = calloc(24000, sizeof(float));
-        const float *rows;
+        const size_t need = (size_t)(3 * encoder_chunk_mel(e) + 32) * 160, n = need > 24000 ? need : 24000;
+        float *silence = calloc(n, sizeof(float));
+        const float *rows, *joint_enc = NULL;
         size_t nrows;
         char scratch[256];
         int ids[256];
         if (silence) {
-            melfe_push(fe, silence, 24000, 1, &rows, &nrows);
+            encoder_capture_first(e, 1);
+            melfe_push(fe, silence, n, 1, &rows, &nrows);
             encoder_push(e, rows, nrows);
             enc_out_t o;
-            while (encoder_step(e, 1, &o, scratch, sizeof scratch) == 1)
-                if (o.frames > 0 && decoder_run(d, o.joint_enc, o.frames, ids, 256, scratch, sizeof scratch) < 0) break;
+            while (encoder_step(e, 1, &o, scratch, sizeof scratch) == 1) {
+                if (o.frames > 0) {
+                    joint_enc = o.joint_enc;
+                    if (decoder_run(d, o.joint_enc, o.frames, ids, 256, scratch, sizeof scratch) < 0) break;
+                }
+                encoder_take_gpu_ms(e);
+            }
+            encoder_capture_first(e, 0);
+            if (joint_enc && s->dec) decoder_prepare_graphs(s->dec, joint_enc);
         }
         free(silence);
     }
     melfe_destroy(fe);
     decoder_destroy(d);
-    encoder_destroy(e);
+    if (e) encoder_reset(e);
 }
 
 /* Fresh front end and empty records (open and reset). */
@@ -198,10 +235,12 @@ nemoasr_t *nemoasr_open(const char *model_dir, const char *language, int latency
         nemoasr_close(s);
         return NULL;
     }
-    warm_up(s->m, right);
-    s->warm = 1u << right;
-    s->enc = encoder_create(s->m, right);
+    s->graphs = 1;
+    s->fuse = 1;
     s->dec = decoder_create(s->m);
+    if (s->dec) warm_up(s, right);
+    s->warm = 1u << right;
+    s->enc = encoder_for(s, right);
     if (!s->enc || !s->dec || begin_stream(s)) {
         set_err(err, errlen, "session setup on the GPU failed: %s", gpu_last_error(s->m->gpu));
         nemoasr_close(s);
@@ -214,7 +253,7 @@ nemoasr_t *nemoasr_open(const char *model_dir, const char *language, int latency
 
 void nemoasr_close(nemoasr_t *s) {
     if (!s) return;
-    encoder_destroy(s->enc);
+    for (int i = 0; i < N_LATENCIES; ++i) encoder_destroy(s->encs[i]);
     decoder_destroy(s->dec);
     melfe_destroy(s->in.mel);
     rsmp_destroy(s->in.rs);
@@ -339,8 +378,12 @@ int nemoasr_prepare_latency(nemoasr_t *s, int latency_ms, char *err, size_t errl
     const int right = check_latency(s->m, latency_ms, err, errlen);
     if (right < 0) return -1;
     if (!(s->warm & (1u << right))) {
-        warm_up(s->m, right);
+        warm_up(s, right);
         s->warm |= 1u << right;
+        if (!s->encs[latency_index(right)]) {
+            set_err(err, errlen, "encoder setup on the GPU failed: %s", gpu_last_error(s->m->gpu));
+            return -1;
+        }
     }
     return 0;
 }
@@ -349,17 +392,12 @@ int nemoasr_reset(nemoasr_t *s, const char *language, int latency_ms, char *err,
     if (nemoasr_prepare_latency(s, latency_ms, err, errlen)) return -1;
     if (language && model_set_language(s->m, language, err, errlen)) return -1;
     const int right = latency_right(latency_ms);
-    if (encoder_right(s->enc) != right) { /* another chunk shape: a new encoder */
-        encoder_destroy(s->enc);
-        if (!(s->enc = encoder_create(s->m, right))) {
-            set_err(err, errlen, "encoder setup on the GPU failed: %s", gpu_last_error(s->m->gpu));
-            s->done = 1;
-            return -1;
-        }
-        encoder_set_dump(s->enc, s->dump);
-    } else {
-        encoder_reset(s->enc);
+    if (!(s->enc = encoder_for(s, right))) { /* the prepared encoder of this chunk shape */
+        set_err(err, errlen, "encoder setup on the GPU failed: %s", gpu_last_error(s->m->gpu));
+        s->done = 1;
+        return -1;
     }
+    encoder_reset(s->enc);
     decoder_reset(s->dec);
     s->latency_ms = latency_ms;
     if (begin_stream(s)) {
@@ -398,10 +436,14 @@ const float *nemoasr_debug_dump_layers(const nemoasr_t *s) { return encoder_dump
 const float *nemoasr_debug_dump_prompted(const nemoasr_t *s) { return encoder_dump_prompted(s->enc); }
 const float *nemoasr_debug_dump_joint_enc(const nemoasr_t *s) { return encoder_dump_joint(s->enc); }
 void nemoasr_debug_use_graphs(nemoasr_t *s, int on) {
+    s->graphs = on != 0;
     encoder_use_graphs(s->enc, on);
     decoder_use_graphs(s->dec, on);
 }
-void nemoasr_debug_fuse(nemoasr_t *s, int on) { encoder_fuse(s->enc, on); }
+void nemoasr_debug_fuse(nemoasr_t *s, int on) {
+    s->fuse = on != 0;
+    encoder_fuse(s->enc, on);
+}
 size_t nemoasr_debug_joint_steps(const nemoasr_t *s) { return s->rec.joint_steps; }
 double nemoasr_debug_encoder_gpu_ms(const nemoasr_t *s) { return s->rec.enc_gpu_ms; }
 const double *nemoasr_debug_chunk_ms(const nemoasr_t *s, size_t *n) {

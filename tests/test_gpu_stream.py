@@ -350,3 +350,37 @@ def test_api_input_rate(rate):
     check_oracle(s.tokens(), o)
     assert s.stats()["chunks"] == o.chunks
     s.close()
+
+
+@pytest.mark.parametrize("latency", [80, 560, 1120])
+def test_first_chunks_replay_prepared_graphs(latency):
+    """The warm-up at open runs silence through the session's own encoder, capturing each chunk
+    shape's graph on first sight, and captures the decoder's graphs of every run size (the
+    reference warms its pipelines the same way, src/warmup.c:7-42): the stream's first three chunks
+    then issue no direct kernel launch.  The same holds after nemoasr_prepare_latency of another
+    latency and a reset to it (the prepared encoder is kept), and the decode is the oracle's."""
+    import ctypes as C
+
+    import nemoasr
+
+    mdir = model_dir("tiny")
+    L = nemoasr.lib()
+    other = 560 if latency != 560 else 1120
+    s = nemoasr.Session(mdir, "en-US", latency)
+    err = C.create_string_buffer(256)
+    for lat in (latency, other):
+        chunk = 8 * (LAT_RIGHT[lat] + 1)
+        mel = mel_ref.logmel(synth.make_audio(4.0 * chunk * 0.01 + 0.3, seed=50 + lat))
+        if lat != latency:
+            assert L.nemoasr_prepare_latency(s.h, lat, err, 256) == 0, err.value
+            s.reset("en-US", lat)
+        n0 = L.nemoasr_debug_launches(s.h)
+        s.feed_mel(mel[:3 * chunk], final=False)
+        assert s.stats()["chunks"] == 3
+        assert L.nemoasr_debug_launches(s.h) == n0, f"{lat} ms: direct launches in the first chunks"
+        s.feed_mel(mel[3 * chunk:], final=True)
+        om = oracle.Model(mdir, "en-US")
+        o = oracle.Session(om, LAT_RIGHT[lat])
+        o.feed_mel(mel, final=True)
+        check_oracle(s.tokens(), o, f"{lat} ms: ")
+    s.close()
