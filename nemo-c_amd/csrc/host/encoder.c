@@ -57,6 +57,11 @@ struct encoder {
     /* graphs */
     int use_graphs, capture_first;
     int fuse; /* single-stream launch fusions (kernels/nk_fuse.hip) */
+    /* one-row chunks: all blocks in one persistent launch (kernels/nk_chain.hip) */
+    int chain, chain_ok;
+    gpu_buf_t *ch_layers, *ch_ll, *ch_abort;
+    int *ch_err;        /* pinned host word the chain reports a time-out in */
+    unsigned epoch;     /* per-chunk tag base of the chain's hand-offs */
     gslot_t gs[MAX_GRAPHS];
     unsigned long long tick;
     /* dumps */
@@ -67,6 +72,66 @@ struct encoder {
 };
 
 static int sub_len(int n) { return n / 2 + 1; } /* src/encoder.c:118 */
+
+/* The persistent chain serves one-row chunks of the shape it is built for, on a device with
+ * enough compute units to hold all its workgroups at once; everything else takes the per-kernel
+ * sequence of run_blocks. */
+static void chain_init(encoder_t *e) {
+    const model_cfg_t *c = &e->m->cfg;
+    gpu_t *g = e->g;
+    e->chain_ok = c->d_model == NK_CHAIN_D && c->d_ff == NK_CHAIN_FF && c->n_heads == NK_CHAIN_HEADS &&
+                  c->head_dim * c->n_heads == c->d_model && c->conv_kernel == NK_CONV_TAPS &&
+                  c->n_layers > 0 && c->n_layers * NK_CHAIN_PH < 1024 && e->left + 1 <= NK_CHAIN_MAX_L &&
+                  e->left + 1 <= e->Lmax && gpu_cu_count(g) >= NK_CHAIN_G;
+    e->chain = e->chain_ok;
+    if (!e->chain_ok) return;
+    const int nl = c->n_layers;
+    NkChainLayer *t = calloc((size_t)nl, sizeof *t);
+    for (int l = 0; l < nl; ++l) {
+        const layer_dev_t *W = &e->m->L[l];
+        t[l] = (NkChainLayer){ W->ff1_w1, W->ff1_w2, W->wqkv, W->wo, W->pw1, W->pw2, W->ff2_w1, W->ff2_w2,
+                               W->ln_ff1_g, W->ln_ff1_b, W->ln_att_g, W->ln_att_b, W->ln_conv_g, W->ln_conv_b,
+                               W->ln_ff2_g, W->ln_ff2_b, W->ln_out_g, W->ln_out_b, W->bn_g, W->bn_b, W->dw_w,
+                               W->bias_u, W->bias_v, W->ptab };
+    }
+    e->ch_layers = gpu_buf_alloc(g, (size_t)nl * sizeof *t);
+    e->ch_ll = gpu_buf_alloc(g, (size_t)NK_CHAIN_SLOTS * NK_CHAIN_SLOT * sizeof(unsigned long long));
+    e->ch_abort = gpu_buf_alloc(g, 256);
+    e->ch_err = gpu_host_alloc(g, 64);
+    if (!e->ch_layers || !e->ch_ll || !e->ch_abort || !e->ch_err || !gpu_host_dptr(g, e->ch_err) ||
+        gpu_upload(g, gpu_buf_dptr(e->ch_layers), t, (size_t)nl * sizeof *t))
+        e->chain_ok = e->chain = 0;
+    free(t);
+}
+
+/* all conformer blocks of a one-row chunk: block 0 reads x_in, the last block leaves its residual
+ * row (before its output norm) in x_out */
+static void run_chain(encoder_t *e, const float *x_in, float *x_out) {
+    const model_cfg_t *c = &e->m->cfg;
+    gpu_t *g = e->g;
+    NkChainArgs a;
+    memset(&a, 0, sizeof a);
+    a.L = gpu_buf_dptr(e->ch_layers);
+    a.x_in = x_in;
+    a.x_out = x_out;
+    a.kv = gpu_buf_dptr(e->kv);
+    a.din = gpu_buf_dptr(e->din);
+    a.ll = gpu_buf_dptr(e->ch_ll);
+    a.abort_word = gpu_buf_dptr(e->ch_abort);
+    a.err_word = gpu_host_dptr(g, e->ch_err);
+    a.dump = e->dump ? gpu_buf_dptr(e->dump_dev) : NULL;
+    a.desc = gpu_buf_dptr(e->desc);
+    a.kv_stride = e->kv_stride;
+    a.din_stride = e->din_stride;
+    a.n_layers = (uint32_t)c->n_layers;
+    a.Lmax = (uint32_t)e->Lmax;
+    a.spin_max = 1u << 20;
+    a.eps = c->ln_eps;
+    a.scale = 1.0f / sqrtf((float)c->head_dim);
+    const double D = NK_CHAIN_D, FF = NK_CHAIN_FF;
+    gpu_next_bytes(g, (double)c->n_layers * (4.0 * FF * D + 7.0 * D * D) * 2.0);
+    gpu_launch(g, "enc_chain", &a, sizeof a, NK_CHAIN_G, 1, 1, NK_CHAIN_THREADS, 1, 1);
+}
 
 encoder_t *encoder_create(model_t *m, int right) {
     encoder_t *e = calloc(1, sizeof *e);
@@ -113,6 +178,7 @@ encoder_t *encoder_create(model_t *m, int right) {
     e->use_graphs = 1;
     e->fuse = 1;
     e->pos = e->conv_left; /* rows [0, conv_left) stay zero: the empty conv history */
+    chain_init(e);
     return e;
 }
 
@@ -127,9 +193,11 @@ void encoder_destroy(encoder_t *e) {
     if (!e) return;
     drop_graphs(e);
     gpu_buf_t *bufs[] = { e->win, e->c1, e->c2, e->c3, e->c4, e->flat, e->h, e->tmp, e->t2, e->xf, e->ff,
-                          e->att, e->y, e->ph, e->prompted, e->joint_enc, e->kv, e->din, e->desc, e->dump_dev };
+                          e->att, e->y, e->ph, e->prompted, e->joint_enc, e->kv, e->din, e->desc, e->dump_dev,
+                          e->ch_layers, e->ch_ll, e->ch_abort };
     for (size_t i = 0; i < sizeof bufs / sizeof *bufs; ++i) gpu_buf_free(bufs[i]);
     gpu_host_free(e->stage_win);
+    gpu_host_free(e->ch_err);
     free(e->pending);
     free(e->d_layers);
     free(e->d_prompted);
@@ -172,6 +240,20 @@ int encoder_graphs(const encoder_t *e) {
 void encoder_fuse(encoder_t *e, int on) {
     if (e->fuse != on) drop_graphs(e);
     e->fuse = on;
+}
+
+void encoder_chain(encoder_t *e, int on) {
+    if (e->chain != (on != 0)) drop_graphs(e);
+    e->chain = on != 0;
+}
+int encoder_chain_usable(const encoder_t *e) { return e->chain_ok; }
+
+int encoder_check(encoder_t *e, char *err, size_t errlen) {
+    if (e->ch_err && *(volatile int *)e->ch_err) {
+        snprintf(err, errlen, "encoder chain: hand-off %d timed out", *(volatile int *)e->ch_err - 1);
+        return -1;
+    }
+    return 0;
 }
 
 void encoder_set_dump(encoder_t *e, int on) {
@@ -270,6 +352,20 @@ static void run_blocks(encoder_t *e, int c) {
     float *xdead = gpu_buf_dptr(e->xf);  /* residual rows after a pending update that nothing reads again */
     float *ff = gpu_buf_dptr(e->ff), *att = gpu_buf_dptr(e->att), *y = gpu_buf_dptr(e->y);
     float *dump = e->dump ? gpu_buf_dptr(e->dump_dev) : NULL;
+    if (e->chain && uc == 1) {
+        /* one row: every block in the persistent chain; its output row in R[1] */
+        run_chain(e, R[0], R[1]);
+        const layer_dev_t *Wl = &m->L[nl - 1];
+        const uint32_t PH = (uint32_t)cf->prompt_hidden, NP = (uint32_t)cf->num_prompts, JH = (uint32_t)cf->joint_hidden;
+        float *ph = gpu_buf_dptr(e->ph), *pr = gpu_buf_dptr(e->prompted);
+        float *hn = dump ? R[0] : NULL;
+        nk_gemm_ln(g, R[1], D, m->prompt_w0, D + NP, m->prompt_b0_eff, ph, PH, NULL, uc, PH, D, NK_ACT_RELU, 0, 1.0f, 1,
+                   Wl->ln_out_g, Wl->ln_out_b, NULL, NULL, hn, lnbuf, eps);
+        if (dump) nk_copy2d(g, hn, D, dump + (size_t)(nl - 1) * D, D * nl, uc, D);
+        nk_gemm(g, ph, PH, m->prompt_w2, PH, m->prompt_b2, pr, D, uc, D, PH, NK_ACT_NONE, 0, 1.0f);
+        nk_gemm(g, pr, D, m->joint_enc_w, D, m->joint_enc_b, gpu_buf_dptr(e->joint_enc), JH, uc, JH, D, NK_ACT_NONE, 0, 1.0f);
+        return;
+    }
     /* one or two rows per chunk: attention + out_proj and dwconv + pw2 as one launch each */
     const int fuse_att = e->fuse && uc <= 4 && dh == 128 && D % 128 == 0;
     const int fuse_conv = e->fuse && uc <= 2 && D <= 1024 && D % 8 == 0 && cf->conv_kernel == NK_CONV_TAPS;
@@ -419,6 +515,8 @@ int encoder_step(encoder_t *e, int final, enc_out_t *out, char *err, size_t errl
     d[NK_DESC_L] = L;
     d[NK_DESC_C] = c;
     for (int i = 0; i < NK_FEW_ROWS; ++i) d[NK_DESC_ROWS + i] = e->pos + (i < c ? i : c - 1);
+    e->epoch = e->epoch + 1 < (1u << 22) ? e->epoch + 1 : 1; /* tag base epoch << 10 stays in 32 bits */
+    d[NK_DESC_EPOCH] = (int)e->epoch;
     gpu_upload_async(g, gpu_buf_dptr(e->win), w, (size_t)p.nwin * MEL_NMEL * sizeof(float));
     gpu_upload_async(g, gpu_buf_dptr(e->desc), d, NK_DESC_INTS * sizeof(int));
     if (e->use_graphs && !e->dump) {

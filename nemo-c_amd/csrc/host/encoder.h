@@ -36,6 +36,13 @@ void encoder_capture_first(encoder_t *e, int on);
 int encoder_graphs(const encoder_t *e);
 /* 1 (default): fused attention + out_proj and dwconv + pw2 launches for chunks of few rows. */
 void encoder_fuse(encoder_t *e, int on);
+/* 1 (default where usable): one-row chunks run all conformer blocks as one persistent launch;
+ * 0: the per-kernel sequence.  Usable for the d_model 1024 / d_ff 4096 / 8-head shape on a device
+ * with at least 256 compute units. */
+void encoder_chain(encoder_t *e, int on);
+int encoder_chain_usable(const encoder_t *e);
+/* -1 with err set when a chain launch reported a time-out (checked after the stream has synced). */
+int encoder_check(encoder_t *e, char *err, size_t errlen);
 /* Keep per-layer block outputs of every chunk (test hook). */
 void encoder_set_dump(encoder_t *e, int on);
 size_t encoder_dump_frames(const encoder_t *e);

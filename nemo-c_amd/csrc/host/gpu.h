@@ -114,6 +114,10 @@ const float *gpu_zeros(gpu_t *g);
 void gpu_set_many_rows(gpu_t *g, int on);
 /* HIP device index the context runs on. */
 int gpu_device_index(const gpu_t *g);
+/* Compute units of the device (0 when the query fails). */
+int gpu_cu_count(gpu_t *g);
+/* Device address of pinned host memory from gpu_host_alloc (kernels may store into it). */
+void *gpu_host_dptr(gpu_t *g, void *host);
 int gpu_many_rows(const gpu_t *g);
 
 /* Number of kernel launches issued since creation (for tests and the launch-count check). */

@@ -132,6 +132,19 @@ const int *gpu_iota(gpu_t *g) { return g->iota; }
 void gpu_set_many_rows(gpu_t *g, int on) { g->many_rows = on != 0; }
 int gpu_many_rows(const gpu_t *g) { return g->many_rows; }
 int gpu_device_index(const gpu_t *g) { return g->dev; }
+
+int gpu_cu_count(gpu_t *g) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, g->dev) != hipSuccess) return 0;
+    return n;
+}
+
+void *gpu_host_dptr(gpu_t *g, void *host) {
+    void *d = NULL;
+    (void)g;
+    if (!host || hipHostGetDevicePointer(&d, host, 0) != hipSuccess) return NULL;
+    return d;
+}
 const float *gpu_zeros(gpu_t *g) { return g->zeros; }
 
 void gpu_destroy(gpu_t *g) {

@@ -104,7 +104,7 @@ struct nemoasr {
         size_t nmel, capmel;
     } rec;
     nemoasr_stats_t stats;
-    int latency_ms, done, dump, graphs, fuse;
+    int latency_ms, done, dump, graphs, fuse, chain;
     unsigned warm; /* bit r: chunk shapes of right context r have run once */
     double open_ms;
     int ids[TOKENS_PER_CHUNK_MAX];
@@ -147,6 +147,7 @@ static encoder_t *encoder_for(nemoasr_t *s, int right) {
         encoder_set_dump(e, s->dump);
         encoder_use_graphs(e, s->graphs);
         encoder_fuse(e, s->fuse);
+        encoder_chain(e, s->chain && encoder_chain_usable(e));
     }
     return e;
 }
@@ -237,6 +238,7 @@ nemoasr_t *nemoasr_open(const char *model_dir, const char *language, int latency
     }
     s->graphs = 1;
     s->fuse = 1;
+    s->chain = 0; /* on by nemoasr_debug_chain until it beats the per-kernel graph */
     s->dec = decoder_create(s->m);
     if (s->dec) warm_up(s, right);
     s->warm = 1u << right;
@@ -306,6 +308,7 @@ static int drain_chunks(nemoasr_t *s, int final, char *err, size_t errlen) {
         const double enc_gpu = encoder_take_gpu_ms(s->enc);
         o.gpu_ms += enc_gpu;
         if (n < 0) return -1;
+        if (encoder_check(s->enc, err, errlen)) return -1;
         if (reserve((void **)&s->rec.ids, &s->rec.capids, s->rec.nids + (size_t)n, sizeof(int)) ||
             reserve((void **)&s->rec.chunk_ms, &s->rec.capchunk, s->rec.nchunk + 1, sizeof(double))) {
             set_err(err, errlen, "out of memory");
@@ -444,6 +447,11 @@ void nemoasr_debug_fuse(nemoasr_t *s, int on) {
     s->fuse = on != 0;
     encoder_fuse(s->enc, on);
 }
+void nemoasr_debug_chain(nemoasr_t *s, int on) {
+    s->chain = on != 0;
+    encoder_chain(s->enc, s->chain && encoder_chain_usable(s->enc));
+}
+int nemoasr_debug_chain_usable(const nemoasr_t *s) { return encoder_chain_usable(s->enc); }
 size_t nemoasr_debug_joint_steps(const nemoasr_t *s) { return s->rec.joint_steps; }
 double nemoasr_debug_encoder_gpu_ms(const nemoasr_t *s) { return s->rec.enc_gpu_ms; }
 const double *nemoasr_debug_chunk_ms(const nemoasr_t *s, size_t *n) {

@@ -122,13 +122,16 @@ typedef struct {
  *   [1] cache_len  cached attention rows in front of pos
  *   [2] L          attention window = cache_len + c
  *   [3] c          rows of the chunk
- *   [4 + i]        pos + i, the cache row of chunk row i (GEMM output row map) */
+ *   [4 + i]        pos + i, the cache row of chunk row i (GEMM output row map)
+ *   [4 + 16]       epoch, a per-chunk number that never repeats on consecutive chunks (the
+ *                  tag base of the single-row chain's hand-offs) */
 #define NK_DESC_POS 0
 #define NK_DESC_CACHE 1
 #define NK_DESC_L 2
 #define NK_DESC_C 3
 #define NK_DESC_ROWS 4
-#define NK_DESC_INTS (NK_DESC_ROWS + NK_FEW_ROWS)
+#define NK_DESC_EPOCH (NK_DESC_ROWS + NK_FEW_ROWS)
+#define NK_DESC_INTS (NK_DESC_EPOCH + 1)
 
 /* Relative-position attention for one chunk of one stream.
  * Q: [c][ldq]; K, V: [L][ldk] (the window: cached rows then the chunk's rows);
@@ -423,5 +426,41 @@ typedef struct {
     NkGemmArgs g;
     NkBDecArgs d;
 } NkBDecGemmArgs;
+
+/* Persistent encoder chain for one-row chunks (kernels/nk_chain.hip): all conformer blocks of a
+ * chunk in one launch of NK_CHAIN_G resident workgroups that hand each block's intermediate rows
+ * to one another through tagged entries.  Built for d_model 1024, d_ff 4096, 8 heads of 128 and
+ * a 9-tap depthwise conv; the host uses the per-kernel graph for any other shape. */
+#define NK_CHAIN_G 256       /* workgroups, one per CU; every one must be resident at once      */
+#define NK_CHAIN_THREADS 384 /* 4 compute wavefronts + 2 hand-off wavefronts                      */
+#define NK_CHAIN_D 1024
+#define NK_CHAIN_FF 4096
+#define NK_CHAIN_HEADS 8
+#define NK_CHAIN_MAX_L 64    /* attention window (cached rows + the chunk's row)                 */
+#define NK_CHAIN_SLOT 4096   /* hand-off entries per slot                                        */
+#define NK_CHAIN_SLOTS 3     /* slots in rotation (hand-off i uses slot i mod 3)                 */
+#define NK_CHAIN_PH 9        /* hand-offs per conformer block                                    */
+
+/* device addresses of one block's weights (the layer's tensors in the model arenas) */
+typedef struct {
+    const u16 *ff1_w1, *ff1_w2, *wqkv, *wo, *pw1, *pw2, *ff2_w1, *ff2_w2;
+    const float *ln_ff1_g, *ln_ff1_b, *ln_att_g, *ln_att_b, *ln_conv_g, *ln_conv_b, *ln_ff2_g, *ln_ff2_b;
+    const float *ln_out_g, *ln_out_b, *bn_g, *bn_b, *dw_w, *bias_u, *bias_v, *ptab;
+} NkChainLayer;
+
+typedef struct {
+    const NkChainLayer *L;          /* [n_layers] */
+    const float *x_in;              /* block 0 input row [D] */
+    float *x_out;                   /* last block's residual row [D], before its output norm */
+    float *kv, *din;                /* layer 0's K/V and conv histories; layer l at + l * stride */
+    unsigned long long *ll;         /* hand-off entries [NK_CHAIN_SLOTS][NK_CHAIN_SLOT]: {f32, tag} */
+    u32 *abort_word;                /* epoch of a chunk that gave up waiting */
+    int *err_word;                  /* host-visible: 1 + the hand-off that timed out */
+    float *dump;                    /* optional [n_layers][D]: block outputs 0 .. n_layers-2 */
+    const int *desc;                /* chunk descriptor (position, cache length, epoch) */
+    unsigned long long kv_stride, din_stride; /* floats per layer */
+    u32 n_layers, Lmax, spin_max;
+    float eps, scale;
+} NkChainArgs;
 
 #endif

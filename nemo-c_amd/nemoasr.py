@@ -70,6 +70,8 @@ API = {
     "nemoasr_debug_dump_joint_enc": (_f32p, [_vp]),
     "nemoasr_debug_use_graphs": (None, [_vp, C.c_int]),
     "nemoasr_debug_fuse": (None, [_vp, C.c_int]),
+    "nemoasr_debug_chain": (None, [_vp, C.c_int]),
+    "nemoasr_debug_chain_usable": (C.c_int, [_vp]),
     "nemoasr_debug_joint_steps": (C.c_size_t, [_vp]),
     "nemoasr_debug_encoder_gpu_ms": (C.c_double, [_vp]),
     "nemoasr_debug_chunk_ms": (C.POINTER(C.c_double), [_vp, C.POINTER(C.c_size_t)]),
@@ -356,6 +358,14 @@ class Session:
     def fuse(self, on: bool):
         lib().nemoasr_debug_fuse(self.h, int(on))
 
+    def chain(self, on: bool):
+        """One-row chunks: every conformer block in one persistent launch (default, where usable)
+        or the per-kernel sequence."""
+        lib().nemoasr_debug_chain(self.h, int(on))
+
+    def chain_usable(self) -> bool:
+        return bool(lib().nemoasr_debug_chain_usable(self.h))
+
     def dumps(self, n_layers: int, d_model: int, joint_hidden: int):
         F = lib().nemoasr_debug_frames(self.h)
         if F == 0:
@@ -398,6 +408,10 @@ class Session:
     @property
     def load_ms(self) -> float:
         return lib().nemoasr_load_ms(self.h)
+
+    def launches(self) -> int:
+        """Kernel launches (direct and captured) issued on the session's device so far."""
+        return int(lib().nemoasr_debug_launches(self.h))
 
     def time_kernel(self, name: str | None, max_launches: int = 4096):
         lib().nemoasr_debug_time_kernel(self.h, name.encode() if name else None, max_launches)

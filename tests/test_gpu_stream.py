@@ -99,6 +99,7 @@ def test_fused_launches_match_separate(latency):
     out = []
     for fuse in (True, False):
         s = nemoasr.Session(mdir, "en-US", latency)
+        s.chain(False)  # one-row chunks would otherwise run the persistent chain, fused or not
         s.fuse(fuse)
         s.set_dump(True)
         s.feed_mel(mel, final=True)
