@@ -429,15 +429,17 @@ typedef struct {
 
 /* Persistent encoder chain for one-row chunks (kernels/nk_chain.hip): all conformer blocks of a
  * chunk in one launch of NK_CHAIN_G resident workgroups that hand each block's intermediate rows
- * to one another through tagged entries.  Built for d_model 1024, d_ff 4096, 8 heads of 128 and
- * a 9-tap depthwise conv; the host uses the per-kernel graph for any other shape. */
+ * to one another through tagged entries, while one wavefront per workgroup streams that
+ * workgroup's weight slices into an LDS ring.  Built for d_model 1024, d_ff 4096, 8 heads of 128
+ * and a 9-tap depthwise conv; the host uses the per-kernel graph for any other shape. */
 #define NK_CHAIN_G 256       /* workgroups, one per CU; every one must be resident at once      */
-#define NK_CHAIN_THREADS 384 /* 4 compute wavefronts + 2 hand-off wavefronts                      */
+#define NK_CHAIN_THREADS 448 /* 4 compute, 2 hand-off and 1 weight-streaming wavefronts          */
 #define NK_CHAIN_D 1024
 #define NK_CHAIN_FF 4096
 #define NK_CHAIN_HEADS 8
+#define NK_CHAIN_PARTS 4     /* attention workgroups per head (each a quarter of the window)      */
 #define NK_CHAIN_MAX_L 64    /* attention window (cached rows + the chunk's row)                 */
-#define NK_CHAIN_SLOT 4096   /* hand-off entries per slot                                        */
+#define NK_CHAIN_SLOT 4160   /* hand-off entries per slot (4096 + the heads' 64 softmax terms)    */
 #define NK_CHAIN_SLOTS 3     /* slots in rotation (hand-off i uses slot i mod 3)                 */
 #define NK_CHAIN_PH 9        /* hand-offs per conformer block                                    */
 

@@ -11,15 +11,17 @@
  *   A  LN_out(prev) -> LN_ff1 -> ff1_w1, SiLU          (4096)   src/encoder.c:155-157
  *   B  x + 0.5 * ff1_w2 h                              (1024)
  *   C  LN_att -> q|k|v (also written to the K/V cache)  (3072)   src/encoder.c:159-162
- *   D  relative-position attention, one workgroup per head (1024)  src/encoder.c:163-165
- *   E  x + wo att                                      (1024)
+ *   D  relative-position attention: 4 workgroups per head, each over a quarter of the window,
+ *      hand over their unnormalised outputs with their softmax max and sum  (8 x 4 x 130)
+ *   E  merge of the quarters, x + wo att               (1024)   src/encoder.c:163-165
  *   F  LN_conv -> pw1, GLU (written to the conv history) -> causal depthwise conv  (1024)
  *   G  LN_bn -> SiLU -> x + pw2 y                       (1024)   src/encoder.c:169-175
  *   H  LN_ff2 -> ff2_w1, SiLU                           (4096)   src/encoder.c:177-179
  *   I  x + 0.5 * ff2_w2 h                              (1024)   (LN_out in the next block's A)
  * The math of each operation is that of the per-kernel path (reference src/kernels.metal: GEMMs
  * with bf16 weights and f32 activations :51-118, LayerNorm :211-255, attention :290-348, conv
- * :359-409); only the summation orders differ.
+ * :359-409); only the summation orders differ (the attention's softmax is summed per quarter and
+ * the quarters combined with their max: the same value up to rounding).
  *
  * Hand-off.  An entry is 8 bytes {f32 value, u32 tag}, stored with one agent-coherent (sc1)
  * 8-byte store, so value and tag arrive together: no flag, no fence, no counter.  The reader
@@ -29,40 +31,69 @@
  * match.  Hand-off i uses slot i mod 3: a slot is rewritten three hand-offs later, and by then
  * every reader of its previous contents has finished (a writer of hand-off i + 3 has seen all of
  * hand-off i + 2, whose writers had all seen i + 1, whose writers are, directly or through the
- * attention heads, every workgroup that waits for i).  Two slots would not do: hand-off D -> E
- * is written by the 8 attention workgroups alone, which do not wait for all of C -> D.
+ * attention workgroups, every workgroup that waits for i).  Two slots would not do: hand-off
+ * D -> E is written by the attention workgroups alone, which do not wait for all of C -> D.
  * Every wait is bounded (spin_max polls, and the epoch written to abort_word by any workgroup
  * that gave up ends the others' waits), and a time-out is reported in the host-visible err_word.
  *
- * Roles within a workgroup (6 wavefronts, one LDS barrier per phase):
- *   - wavefronts 0-3 compute: after the barrier of phase p they issue the weight loads of phase
- *     p + 2 into registers, read the phase's input row from LDS, form their dot products (lane l
- *     holds 16-byte chunks l, l + 64, ... of a weight row, 1 KB per load instruction), reduce
- *     them across the wavefront and store the outputs as hand-off entries;
+ * Weight stream.  A CU keeps only so many lines in flight, so a wavefront that issues a burst of
+ * loads stalls until they drain; issued by the wavefronts that compute, the weight loads would
+ * put that stall on every phase's critical path.  Instead one wavefront per workgroup streams the
+ * workgroup's whole sequence of weight slices (with the LayerNorm parameters, the conv taps and
+ * history and, in the attention workgroups, the head's K, V and position rows) into a 120 KB LDS
+ * ring by direct-to-LDS loads, two phases ahead: after the barrier of phase p it issues the
+ * segment of phase p + 2, then waits for the segment of phase p + 1 before the next barrier.
+ * Segment sizes are fixed per phase (SEG_*), so every ring offset is known statically and the
+ * ring holds any three consecutive segments.
+ *
+ * Roles within a workgroup (7 wavefronts, one LDS barrier per phase):
+ *   - wavefronts 0-3 compute: read the phase's input row and their weight rows from LDS (lane l
+ *     holds 16-byte chunks l, l + 64, ... of a weight row), reduce the dot products across the
+ *     wavefront and store the outputs as hand-off entries;
  *   - wavefront 4 waits for the next phase's input while they compute, applies that phase's
- *     LayerNorm (the whole row: every workgroup normalises it itself), keeps the residual row
- *     and writes the input row to LDS for the next barrier; its LayerNorm parameters are loaded
- *     one LayerNorm ahead;
- *   - wavefront 5 shares the waits of the 4096-wide rows and, in the attention workgroups, moves
- *     the head's cached K and V rows and its position rows into LDS by direct-to-LDS loads two
- *     phases before the attention. */
+ *     LayerNorm (the whole row: every workgroup normalises it itself) with parameters from the
+ *     ring, keeps the residual row and writes the input row to LDS for the next barrier;
+ *   - wavefront 5 shares the waits of the 4096-wide rows;
+ *   - wavefront 6 streams the weights. */
 #include "nk_common.h"
 
 namespace chain {
 
 constexpr u32 G = NK_CHAIN_G, D = NK_CHAIN_D, FF = NK_CHAIN_FF, QKV = 3 * NK_CHAIN_D, H = NK_CHAIN_HEADS, DH = 128;
-constexpr u32 SLOT = NK_CHAIN_SLOT, MAXL = NK_CHAIN_MAX_L;
+constexpr u32 NP = NK_CHAIN_PARTS, NATT = H * NP, SLOT = NK_CHAIN_SLOT, MAXL = NK_CHAIN_MAX_L;
+constexpr u32 ML = H * NP * DH; /* E-input entry of the attention quarters' (max, sum) pairs */
+constexpr u32 RING = 120;       /* KB */
+/* Direct-to-LDS loads the streaming wavefront keeps in flight.  The CU's vector memory queue is
+ * shared by all its wavefronts: a deeper stream would hold the hand-off stores and waits of the
+ * other wavefronts behind it. */
+constexpr int STREAM_INFLIGHT = 16;
+/* ring segment of each phase (KB blocks) and its offset within a block's stream */
+constexpr u32 SEG_A = 32, SEG_B = 40, SEG_C = 24, SEG_D = 25, SEG_E = 16, SEG_F = 25, SEG_G = 16, SEG_H = 32, SEG_I = 48;
+constexpr u32 OFF_A = 0, OFF_B = OFF_A + SEG_A, OFF_C = OFF_B + SEG_B, OFF_D = OFF_C + SEG_C, OFF_E = OFF_D + SEG_D,
+              OFF_F = OFF_E + SEG_E, OFF_G = OFF_F + SEG_F, OFF_H = OFF_G + SEG_G, OFF_I = OFF_H + SEG_H,
+              BLOCK_KB = OFF_I + SEG_I;
 static_assert(H * DH == D && G * 4 == D && G * 16 == FF && G * 12 == QKV, "slices assume these shapes");
+static_assert(ML + 2 * NATT <= SLOT && NATT <= G && MAXL % NP == 0 && MAXL / NP <= 16, "attention split");
+static_assert(SEG_I + SEG_A + SEG_B <= RING && SEG_H + SEG_I + SEG_A <= RING && SEG_A + SEG_B + SEG_C <= RING &&
+                  SEG_B + SEG_C + SEG_D <= RING && SEG_G + SEG_H + SEG_I <= RING,
+              "the ring holds any three consecutive segments");
+static_assert(SEG_A >= STREAM_INFLIGHT && SEG_B >= STREAM_INFLIGHT && SEG_C >= STREAM_INFLIGHT &&
+                  SEG_D >= STREAM_INFLIGHT && SEG_E >= STREAM_INFLIGHT && SEG_F >= STREAM_INFLIGHT &&
+                  SEG_G >= STREAM_INFLIGHT && SEG_H >= STREAM_INFLIGHT && SEG_I >= STREAM_INFLIGHT,
+              "a nonempty segment holds more loads than are in flight");
 
 struct Shared {
-    float ib[2][FF];                            /* phase input rows, by phase parity */
-    float xr[2][D];                             /* residual rows (alternating) */
-    float ks[MAXL][DH], vs[MAXL][DH], ps[MAXL][DH]; /* attention: the head's cached K, V rows and position rows */
-    float knew[DH], vnew[DH];                   /* attention: the chunk's own K and V of the head */
-    float lnp[4][D];                            /* LayerNorm parameters of the next LayerNorm(s) */
+    char ring[RING * 1024];
+    float big[FF + 2 * NATT]; /* inputs of B, E (with the quarters' max and sum), I */
+    float sm[2][D];           /* inputs of A, C, F, H (sm[0]) and D, G (sm[1]) */
+    float xr[2][D];           /* residual rows (alternating) */
+    float knew[DH], vnew[DH]; /* attention: the chunk's own K and V of the head */
     floatx4 qu4[32], qv4[32];
     float s[MAXL];
     floatx4 part[8][32];
+    float outv[16], aux[4];   /* the compute wavefronts' outputs of a phase, stored by the last one */
+    float att_out[DH];        /* the attention quarter's output, stored by wavefront 0 */
+    u32 done;                 /* compute wavefronts finished, counted across phases */
     int bad;
 };
 
@@ -85,26 +116,34 @@ struct Ctl {
     __device__ u32 tag(u32 hand) const { return base + hand; }
 };
 
-/* Wavefront-wide wait: load i of this lane covers entries ent[i], ent[i] + 1 of the slot of
- * hand-off `hand`; returns once every entry of the wavefront carries its tag, with the values in
- * v (false after spin_max rounds, or once another workgroup has given up on this epoch). */
+/* Wavefront-wide wait: load i of this lane covers entries e0 + i * es, +1 of the slot of hand-off
+ * `hand`; returns once every entry of the wavefront carries its tag, with the values in v (false
+ * after spin_max rounds, or once another workgroup has given up on this epoch).  Every workgroup
+ * waits at once, so the wait keeps its memory traffic small: after a full pass that finds entries
+ * missing it re-reads only the first incomplete group (one 16-byte load per lane) until that group
+ * is complete, then makes the next full pass. */
 template <int NL>
-__device__ __forceinline__ bool ll_wait(const Ctl &c, u32 hand, const u32 (&ent)[NL], float2 (&v)[NL]) {
+__device__ __forceinline__ bool ll_wait(const Ctl &c, u32 hand, u32 e0, u32 es, float2 (&v)[NL]) {
     const u64 *slot = c.slot(hand);
     const u32 tag = c.tag(hand);
     u32 spins = 0;
     for (;;) {
-        bool ok = true;
+        int first_bad = -1;
 #pragma unroll
         for (int i = 0; i < NL; ++i) {
-            const u32x4 r = ll_load(slot, ent[i]);
+            const u32x4 r = ll_load(slot, e0 + i * es);
             v[i] = make_float2(__uint_as_float(r.x), __uint_as_float(r.z));
-            ok = ok & (r.y == tag) & (r.w == tag);
+            if (!__all((r.y == tag) & (r.w == tag)) && first_bad < 0) first_bad = i;
         }
-        if (__all(ok)) return true;
-        if (++spins > c.spin_max) return false;
-        if ((spins & 255) == 0 && __hip_atomic_load(c.abort_word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == c.epoch)
-            return false;
+        if (first_bad < 0) return true;
+        const u32 eb = e0 + (u32)first_bad * es;
+        for (;;) {
+            if (++spins > c.spin_max) return false;
+            if ((spins & 255) == 0 && __hip_atomic_load(c.abort_word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == c.epoch)
+                return false;
+            const u32x4 r = ll_load(slot, eb);
+            if (__all((r.y == tag) & (r.w == tag))) break;
+        }
     }
 }
 
@@ -117,21 +156,25 @@ __device__ __forceinline__ void give_up(const NkChainArgs &a, const Ctl &c, Shar
     }
 }
 
+/* ring block kb (a KB index of the workgroup's stream) */
+__device__ __forceinline__ const char *rblk(const Shared &sh, u32 kb) { return sh.ring + (kb % RING) * 1024; }
+__device__ __forceinline__ uint4 rw16(const Shared &sh, u32 kb, u32 lane) { return *(const uint4 *)(rblk(sh, kb) + 16 * lane); }
+
 /* LayerNorm of a 1024-row held as float2 pairs by one wavefront (lane l: elements 2(l + 64i),
- * +1): mean, then the centred variance, y = (x - mean) * (1 / sqrt(var + eps)) * g + b. */
+ * +1): mean, then the centred variance (the reference's two passes, summed in another order),
+ * y = (x - mean) * (1 / sqrt(var + eps)) * g + b. */
 __device__ __forceinline__ void ln_pairs(float2 (&v)[8], const float2 (&g)[8], const float2 (&b)[8], float eps) {
-    float s = 0.0f;
+    /* the lane's 16 terms summed as a tree (a short dependent chain), then across the wavefront */
+    float t[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) { s += v[i].x; s += v[i].y; }
-    const float mean = wsum(s) / (float)D;
-    float ss = 0.0f;
+    for (int i = 0; i < 8; ++i) t[i] = v[i].x + v[i].y;
+    const float mean = wsum(((t[0] + t[1]) + (t[2] + t[3])) + ((t[4] + t[5]) + (t[6] + t[7]))) / (float)D;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
         const float d0 = v[i].x - mean, d1 = v[i].y - mean;
-        ss += d0 * d0;
-        ss += d1 * d1;
+        t[i] = d0 * d0 + d1 * d1;
     }
-    const float inv = 1.0f / sqrtf(wsum(ss) / (float)D + eps);
+    const float inv = 1.0f / sqrtf(wsum(((t[0] + t[1]) + (t[2] + t[3])) + ((t[4] + t[5]) + (t[6] + t[7]))) / (float)D + eps);
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
         v[i].x = (v[i].x - mean) * inv * g[i].x + b[i].x;
@@ -139,58 +182,20 @@ __device__ __forceinline__ void ln_pairs(float2 (&v)[8], const float2 (&g)[8], c
     }
 }
 
-__device__ __forceinline__ void ld_pairs(float2 (&p)[8], const float *src, u32 lane) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) p[i] = *(const float2 *)(src + 2 * (lane + 64 * i));
-}
-
-/* LayerNorm parameter vectors (D floats each) into lnp[k], lnp[k + 1] by direct-to-LDS loads of
- * the hand-off wavefront.  They are issued after the LayerNorm that last read those rows (the
- * lgkmcnt wait makes sure its LDS reads are done) and before the next hand-off wait, whose own
- * loads complete after them: the vmcnt(0) that follows that wait covers them. */
-__device__ __forceinline__ void ln_params_to_lds(Shared &sh, u32 k, const float *gam, const float *bet, u32 lane) {
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-#pragma unroll
-    for (int i = 0; i < (int)D / 256; ++i) {
-        dma16(gam + 256 * i + 4 * lane, (lds_char_t *)&sh.lnp[k][256 * i]);
-        dma16(bet + 256 * i + 4 * lane, (lds_char_t *)&sh.lnp[k + 1][256 * i]);
-    }
-}
-
-/* LayerNorm with the parameters in lnp[k], lnp[k + 1] (after the wait that covers their loads) */
-__device__ __forceinline__ void ln_lds(float2 (&v)[8], const Shared &sh, u32 k, float eps, u32 lane) {
+/* LayerNorm with its parameters in the ring: gamma in the 4 blocks from kg, beta from kb */
+__device__ __forceinline__ void ln_ring(float2 (&v)[8], const Shared &sh, u32 kg, u32 kb, float eps, u32 lane) {
     float2 g[8], b[8];
-    ld_pairs(g, sh.lnp[k], lane);
-    ld_pairs(b, sh.lnp[k + 1], lane);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        g[i] = *(const float2 *)(rblk(sh, kg + (i >> 1)) + 8 * lane + 512 * (i & 1));
+        b[i] = *(const float2 *)(rblk(sh, kb + (i >> 1)) + 8 * lane + 512 * (i & 1));
+    }
     ln_pairs(v, g, b, eps);
 }
+
 __device__ __forceinline__ void st_pairs(float *dst, const float2 (&v)[8], u32 lane) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) *(float2 *)(dst + 2 * (lane + 64 * i)) = v[i];
-}
-
-/* Global-memory accesses through pointers read from the layer table.  The compiler cannot tell
- * that such a pointer is global and would emit flat instructions, which also count in lgkmcnt:
- * then every LDS wait (each barrier) would wait for the weight loads in flight as well. */
-typedef __attribute__((address_space(1))) const u32x4 g_u32x4;
-typedef __attribute__((address_space(1))) const float g_float;
-typedef __attribute__((address_space(1))) const floatx4 g_floatx4;
-typedef __attribute__((address_space(1))) float g_float_w;
-__device__ __forceinline__ uint4 ldg_nt16(const u16 *p) {
-    const u32x4 v = __builtin_nontemporal_load((g_u32x4 *)p);
-    return make_uint4(v.x, v.y, v.z, v.w);
-}
-__device__ __forceinline__ float ldg(const float *p) { return *(g_float *)p; }
-__device__ __forceinline__ floatx4 ldg4(const float *p) { return *(g_floatx4 *)p; }
-__device__ __forceinline__ void stg(float *p, float v) { *(g_float_w *)p = v; }
-
-/* weight rows row0 .. row0 + NC - 1 of a [.][K] bf16 matrix, chunks lane + 64 q */
-template <int NC, int KCH>
-__device__ __forceinline__ void ld_rows(uint4 (&w)[NC][KCH], const u16 *W, u32 row0, u32 K, u32 lane) {
-#pragma unroll
-    for (int c = 0; c < NC; ++c)
-#pragma unroll
-        for (int q = 0; q < KCH; ++q) w[c][q] = ldg_nt16(W + (u64)(row0 + c) * K + 8 * (lane + 64 * q));
 }
 
 /* the lane's chunks lane + 64 q of an input row in LDS */
@@ -205,54 +210,56 @@ __device__ __forceinline__ void ld_x(float (&x)[KCH][8], const float *row, u32 l
     }
 }
 
-/* dot product of one weight row with the row held in x, summed over the wavefront (uniform) */
+/* dot product of the weight row in ring blocks kb .. kb + KCH - 1 with the row held in x, summed
+ * over the wavefront (uniform) */
 template <int KCH>
-__device__ __forceinline__ float dot_row(const float (&x)[KCH][8], const uint4 (&w)[KCH]) {
+__device__ __forceinline__ float dot_ring(const float (&x)[KCH][8], const Shared &sh, u32 kb, u32 lane) {
     float s = 0.0f;
 #pragma unroll
-    for (int q = 0; q < KCH; ++q) s = dot8(x[q], w[q], s);
+    for (int q = 0; q < KCH; ++q) s = dot8(x[q], rw16(sh, kb + q, lane), s);
     return wsum(s);
 }
 
-/* the head's cached K and V rows (window rows 0 .. cl-1) and its position rows (0 .. L-1) into
- * LDS: each direct load moves two 512-byte row segments (lanes 0-31, 32-63) */
-__device__ __forceinline__ void kpv_to_lds(const NkChainArgs &a, Shared &sh, u32 l, u32 h, u32 pos, u32 cl, u32 lane) {
-    const float *kvl = a.kv + (u64)l * a.kv_stride;
-    const float *pt = a.L[l].ptab;
-    const u32 L = cl + 1, half = lane >> 5, c4 = lane & 31;
-    for (u32 r = 0; r < cl; r += 2) {
-        const u32 row = r + half;
-        if (row < cl) {
-            const float *src = kvl + (u64)(pos - cl + row) * QKV + h * DH + 4 * c4;
-            dma16(src + D, (lds_char_t *)&sh.ks[r][0]);
-            dma16(src + 2 * D, (lds_char_t *)&sh.vs[r][0]);
-        }
+/* dot products of NR weight rows of K = 1024 (ring blocks kb[k], kb[k] + 1) with the row in x,
+ * each summed over the wavefront (uniform): every LDS read first, then the sums side by side */
+template <int NR>
+__device__ __forceinline__ void dots_ring(float (&sums)[NR], const float (&x)[2][8], const Shared &sh, const u32 (&kb)[NR], u32 lane) {
+    uint4 wv[NR][2];
+#pragma unroll
+    for (int k = 0; k < NR; ++k) {
+        wv[k][0] = rw16(sh, kb[k], lane);
+        wv[k][1] = rw16(sh, kb[k] + 1, lane);
     }
-    for (u32 r = 0; r < L; r += 2) {
-        const u32 row = r + half;
-        if (row < L) dma16(pt + (u64)(a.Lmax - L + row) * D + h * DH + 4 * c4, (lds_char_t *)&sh.ps[r][0]);
-    }
+    float acc[NR];
+#pragma unroll
+    for (int k = 0; k < NR; ++k) acc[k] = dot8(x[1], wv[k][1], dot8(x[0], wv[k][0], 0.0f));
+#pragma unroll
+    for (int k = 0; k < NR; ++k) sums[k] = wsum(acc[k]);
 }
 
-/* Relative-position attention of head h for the chunk's one row (c = 1, i = 0), the math of
- * attention_rel: score_j = ((q + u) . K_j + (q + v) . P[Lmax - L + j]) * scale over the L window
- * rows (cached rows, then the row itself), softmax, O = sum_j p_j V_j.  256 threads: scores by
- * thread quads (key tid / 4, head dims 4 (tid % 4 + 4 t)), softmax on wavefront 0, the output by
- * 8 key groups of 32 threads summed in order.  Four LDS barriers, matched by the hand-off
- * wavefronts.  Returns dims 4 tid .. 4 tid + 3 on threads tid < 32. */
-__device__ __forceinline__ floatx4 attend(Shared &sh, const float *q, floatx4 bu, floatx4 bv, u32 cl, float scale) {
-    const u32 tid = threadIdx.x, L = cl + 1;
+/* The attention quarter of this workgroup: head h's window rows j0 .. j0 + nk - 1 (cached rows,
+ * then the row itself) with the math of attention_rel: score_j = ((q + u) . K_j + (q + v) .
+ * P[Lmax - L + j]) * scale, m = max score, p_j = exp(score_j - m), l = sum p_j, o = sum p_j V_j
+ * (unnormalised; the E phase combines the quarters).  256 threads: scores by thread quads (key
+ * tid / 4, head dims 4 (tid % 4 + 4 t)), the exponentials on wavefront 0, the output by 8 key
+ * groups of 32 threads summed in order.  K, V and P rows are in the ring segment at kd (K rows
+ * 2 per block from kd, V from kd + 8, P from kd + 16, then u | v in kd + 24).  Four LDS barriers,
+ * matched by the other wavefronts.  Returns o[4 tid .. 4 tid + 3] on threads tid < 32. */
+__device__ __forceinline__ floatx4 attend_part(Shared &sh, u32 kd, const float *q, u32 cl, u32 j0, u32 nk, float scale,
+                                               float &m_out, float &l_out) {
+    const u32 tid = threadIdx.x;
+    const float *uv = (const float *)rblk(sh, kd + 24);
     if (tid < 32) {
         const floatx4 qx = *(const floatx4 *)(q + 4 * tid);
-        sh.qu4[tid] = qx + bu;
-        sh.qv4[tid] = qx + bv;
+        sh.qu4[tid] = qx + *(const floatx4 *)(uv + 4 * tid);
+        sh.qv4[tid] = qx + *(const floatx4 *)(uv + DH + 4 * tid);
     }
     lds_barrier();
     const u32 ks = tid >> 2, part4 = tid & 3;
     float acc = 0.0f;
-    if (ks < L) {
-        const floatx4 *kr = (const floatx4 *)(ks < cl ? &sh.ks[ks][0] : sh.knew);
-        const floatx4 *pr = (const floatx4 *)&sh.ps[ks][0];
+    if (ks < nk) {
+        const floatx4 *kr = (const floatx4 *)(j0 + ks < cl ? rblk(sh, kd + (ks >> 1)) + 512 * (ks & 1) : (const char *)sh.knew);
+        const floatx4 *pr = (const floatx4 *)(rblk(sh, kd + 16 + (ks >> 1)) + 512 * (ks & 1));
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
             const u32 cq = part4 + 4 * t;
@@ -263,24 +270,29 @@ __device__ __forceinline__ floatx4 attend(Shared &sh, const float *q, floatx4 bu
     }
     acc += dpp_f<DPP_QUAD_1032>(acc);
     acc += dpp_f<DPP_QUAD_2301>(acc);
-    if (part4 == 0 && ks < L) sh.s[ks] = acc * scale;
+    if (part4 == 0 && ks < nk) sh.s[ks] = acc * scale;
     lds_barrier();
     if (tid < 64) {
-        const float sv = tid < L ? sh.s[tid] : -INFINITY;
+        const float sv = tid < nk ? sh.s[tid] : -INFINITY;
         const float mx = wmax(sv);
-        const float ev = tid < L ? expf(sv - mx) : 0.0f;
+        const float ev = tid < nk ? expf(sv - mx) : 0.0f;
         const float sum = wsum(ev);
-        if (tid < L) sh.s[tid] = ev / sum;
+        if (tid < nk) sh.s[tid] = ev;
+        if (tid == 0) {
+            sh.s[MAXL - 2] = mx;
+            sh.s[MAXL - 1] = sum;
+        }
     }
     lds_barrier();
     const u32 vg = tid >> 5, d4 = tid & 31;
     floatx4 o = { 0.f, 0.f, 0.f, 0.f };
 #pragma unroll
-    for (int t = 0; t < MAXL / 8; ++t) {
-        const u32 j = vg + 8 * t;
-        if (j < L) {
-            const floatx4 *vr = (const floatx4 *)(j < cl ? &sh.vs[j][0] : sh.vnew);
-            o += sh.s[j] * vr[d4];
+    for (int t = 0; t < 2; ++t) {
+        const u32 jj = vg + 8 * t;
+        if (jj < nk) {
+            const floatx4 *vr = (const floatx4 *)(j0 + jj < cl ? rblk(sh, kd + 8 + (jj >> 1)) + 512 * (jj & 1)
+                                                                : (const char *)sh.vnew);
+            o += sh.s[jj] * vr[d4];
         }
     }
     sh.part[vg][d4] = o;
@@ -291,357 +303,390 @@ __device__ __forceinline__ floatx4 attend(Shared &sh, const float *q, floatx4 bu
 #pragma unroll
         for (int gq = 1; gq < 8; ++gq) r += sh.part[gq][tid];
     }
+    m_out = sh.s[MAXL - 2];
+    l_out = sh.s[MAXL - 1];
     return r;
 }
 
+/* The lane's chunks (as ld_x<2>) of the attention output: each head's quarters combined,
+ * att = sum_k (w_k / sum_k' w_k' l_k') o_k, w_k = exp(m_k - max m), quarters in order. */
+__device__ __forceinline__ void ld_att(float (&x)[2][8], const Shared &sh, u32 lane) {
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+        const u32 hh = (lane >> 4) + 4 * q, d0 = 8 * (lane & 15);
+        float m[NP], w[NP];
+        float mx = -INFINITY;
+#pragma unroll
+        for (int k = 0; k < (int)NP; ++k) {
+            m[k] = sh.big[ML + 2 * (hh * NP + k)];
+            mx = fmaxf(mx, m[k]);
+        }
+        float lsum = 0.0f;
+#pragma unroll
+        for (int k = 0; k < (int)NP; ++k) {
+            w[k] = expf(m[k] - mx);
+            lsum += w[k] * sh.big[ML + 2 * (hh * NP + k) + 1];
+        }
+        const float inv = 1.0f / lsum;
+#pragma unroll
+        for (int k = 0; k < (int)NP; ++k) w[k] *= inv;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            float o = 0.0f;
+#pragma unroll
+            for (int k = 0; k < (int)NP; ++k) o += w[k] * sh.big[(hh * NP + k) * DH + d0 + i];
+            x[q][i] = o;
+        }
+    }
+}
+
+/* the window quarter of attention workgroup part k: rows j0 .. j0 + nk - 1 of the L rows */
+struct Quarter {
+    u32 j0, nk;
+};
+__device__ __forceinline__ Quarter quarter(u32 L, u32 k) {
+    const u32 S = (L + NP - 1) / NP, j0 = k * S;
+    return { j0, L > j0 ? min(S, L - j0) : 0u };
+}
+
+/* Phase j = p % 9 of block l = p / 9 reads hand-off p (its input) and writes hand-off p + 1.  The
+ * three loops below run every phase through one copy of their code (the whole kernel must stay
+ * resident in the instruction cache, which the CU pair shares: unrolled per phase, the code of the
+ * seven wavefronts missed it at every phase). */
+constexpr u32 PH_A = 0, PH_B = 1, PH_C = 2, PH_D = 3, PH_E = 4, PH_F = 5, PH_G = 6, PH_H = 7, PH_I = 8;
+
 /* wavefronts 0-3 */
 __device__ __forceinline__ void compute_loop(const NkChainArgs &a, Shared &sh, const Ctl &c, u32 g, u32 w, u32 lane) {
-    const u32 nl = a.n_layers, tid = threadIdx.x;
-    const u32 pos = (u32)a.desc[NK_DESC_POS], cl = (u32)a.desc[NK_DESC_CACHE];
-    const bool attn = g < H;
-    const u32 col1 = 4 * g + w;      /* this wavefront's column of the 1024-wide outputs */
-    const u32 colA = 16 * g + 4 * w; /* first of its 4 columns of the 4096-wide outputs */
-    const u32 colC = 12 * g + 3 * w; /* first of its 3 columns of q|k|v */
-    uint4 wA[4][2], wB[1][8];
-    ld_rows<4, 2>(wA, a.L[0].ff1_w1, colA, D, lane);
-    ld_rows<1, 8>(wB, a.L[0].ff1_w2, col1, FF, lane);
-    for (u32 l = 0; l < nl; ++l) {
-        const NkChainLayer &W = a.L[l];
-        const u32 h0 = 9 * l; /* hand-off index of this block's first input */
-        float *kvl = a.kv + (u64)l * a.kv_stride;
-        float *dinl = a.din + (u64)l * a.din_stride;
-
-        /* A: ff1_w1 (LayerNorms applied by the hand-off wavefront), SiLU */
+    const u32 nl = a.n_layers, tid = threadIdx.x, P = NK_CHAIN_PH * nl;
+    const u32 pos = (u32)a.desc[NK_DESC_POS], cl = (u32)a.desc[NK_DESC_CACHE], L = cl + 1;
+    const bool attn = g < NATT;
+    const Quarter qt = quarter(L, g % NP);
+    const u32 col1 = 4 * g + w; /* this wavefront's column of the 1024-wide outputs */
+#pragma nounroll
+    for (u32 p = 0; p < P; ++p) {
+        const u32 l = p / NK_CHAIN_PH, j = p % NK_CHAIN_PH, kb0 = l * BLOCK_KB;
+        u64 *out = c.slot(p + 1);
+        const u32 tag = c.tag(p + 1);
         lds_barrier();
         if (sh.bad) return;
-        uint4 wC[3][2];
-        ld_rows<3, 2>(wC, W.wqkv, colC, D, lane);
-        {
-            float x[2][8];
-            ld_x<2>(x, sh.ib[h0 & 1], lane);
-            float mine = 0.0f;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const float s = silu_f(dot_row<2>(x, wA[j]));
-                if (lane == (u32)j) mine = s;
+        if (j == PH_D) {
+            /* attention quarter (workgroups 0 .. NATT-1): its unnormalised output and (max, sum),
+             * stored by wavefront 0 as two 512-byte runs of entries and one pair */
+            if (attn) {
+                float m, lsum;
+                const floatx4 r = attend_part(sh, kb0 + OFF_D, sh.sm[1], cl, qt.j0, qt.nk, a.scale, m, lsum);
+                if (tid < 32) *(floatx4 *)&sh.att_out[4 * tid] = r;
+                if (w == 0) {
+                    ll_put(out, g * DH + lane, sh.att_out[lane], tag);
+                    ll_put(out, g * DH + 64 + lane, sh.att_out[64 + lane], tag);
+                    if (lane < 2) ll_put(out, ML + 2 * g + lane, lane ? lsum : m, tag);
+                }
             }
-            if (lane < 4) ll_put(c.slot(h0 + 1), colA + lane, mine, c.tag(h0 + 1));
+            continue;
         }
-
-        /* B: x + 0.5 * ff1_w2 h */
-        lds_barrier();
-        if (sh.bad) return;
-        {
+        /* Each wavefront leaves its outputs in LDS; the last of the four to finish stores the
+         * workgroup's entries with one instruction (entries of one 32-byte run written by four
+         * wavefronts separately reach the other workgroups measurably later). */
+        u32 n_out, e_out; /* entries of the workgroup and the first of them */
+        if (j == PH_B || j == PH_I) {
+            /* x + 0.5 * ff_w2 h: one row of K = 4096 per wavefront */
             float x[8][8];
-            ld_x<8>(x, sh.ib[(h0 + 1) & 1], lane);
-            const float s = dot_row<8>(x, wB[0]);
-            const float v = sh.xr[0][col1] + s * 0.5f;
-            if (lane == 0) ll_put(c.slot(h0 + 2), col1, v, c.tag(h0 + 2));
-        }
-
-        /* C: q|k|v of the normalised row, also written to the cache row */
-        lds_barrier();
-        if (sh.bad) return;
-        uint4 wE[1][2];
-        ld_rows<1, 2>(wE, W.wo, col1, D, lane);
-        floatx4 bu = { 0.f, 0.f, 0.f, 0.f }, bv = bu;
-        if (attn && tid < 32) {
-            bu = ldg4(W.bias_u + g * DH + 4 * tid);
-            bv = ldg4(W.bias_v + g * DH + 4 * tid);
-        }
-        {
+            ld_x<8>(x, sh.big, lane);
+            const float s = dot_ring<8>(x, sh, kb0 + (j == PH_B ? OFF_B : OFF_I) + 8 * w, lane);
+            if (lane == 0) sh.outv[w] = sh.xr[j == PH_B ? 0 : 1][col1] + s * 0.5f;
+            n_out = 4;
+            e_out = 4 * g;
+        } else {
+            /* K = 1024: A, H (4 rows, SiLU), C (3 rows of q|k|v), E (wo on the merged attention),
+             * F (the GLU pair, then the causal depthwise conv), G (pw2) */
             float x[2][8];
-            ld_x<2>(x, sh.ib[(h0 + 2) & 1], lane);
-            float mine = 0.0f;
+            if (j == PH_E) ld_att(x, sh, lane);
+            else ld_x<2>(x, sh.sm[j == PH_G ? 1 : 0], lane);
+            if (j == PH_A || j == PH_H) {
+                const u32 kb = kb0 + (j == PH_A ? OFF_A : OFF_H) + 8 * w; /* rows 4w .. 4w+3 */
+                const u32 kbs[4] = { kb, kb + 2, kb + 4, kb + 6 };
+                float sums[4];
+                dots_ring<4>(sums, x, sh, kbs, lane);
+                const float mine = lane == 0 ? sums[0] : lane == 1 ? sums[1] : lane == 2 ? sums[2] : sums[3];
+                if (lane < 4) sh.outv[4 * w + lane] = silu_f(mine);
+                n_out = 16;
+                e_out = 16 * g;
+            } else if (j == PH_C) {
+                const u32 kb = kb0 + OFF_C + 6 * w; /* rows 3w .. 3w+2 */
+                const u32 kbs[3] = { kb, kb + 2, kb + 4 };
+                float sums[3];
+                dots_ring<3>(sums, x, sh, kbs, lane);
+                if (lane < 3) sh.outv[3 * w + lane] = lane == 0 ? sums[0] : lane == 1 ? sums[1] : sums[2];
+                n_out = 12;
+                e_out = 12 * g;
+            } else if (j == PH_F) {
+                const u32 kbs[2] = { kb0 + OFF_F + 2 * w, kb0 + OFF_F + 2 * (4 + w) }; /* GLU rows w, 4 + w */
+                float sums[2];
+                dots_ring<2>(sums, x, sh, kbs, lane);
+                const float gl = sums[0] * sigmoid_f(sums[1]);
+                const float *th = (const float *)rblk(sh, kb0 + OFF_F + 16); /* taps [4][9], then history [8][4] */
+                float d = 0.0f;
 #pragma unroll
-            for (int j = 0; j < 3; ++j) {
-                const float s = dot_row<2>(x, wC[j]);
-                if (lane == (u32)j) mine = s;
-            }
-            if (lane < 3) {
-                ll_put(c.slot(h0 + 3), colC + lane, mine, c.tag(h0 + 3));
-                stg(kvl + (u64)pos * QKV + colC + lane, mine);
-            }
-        }
-
-        /* D: attention of head g (workgroups 0 .. H-1) */
-        lds_barrier();
-        if (sh.bad) return;
-        uint4 wF[2][2];
-        {
-            uint4 t0[1][2], t1[1][2];
-            ld_rows<1, 2>(t0, W.pw1, col1, D, lane);
-            ld_rows<1, 2>(t1, W.pw1, col1 + D, D, lane);
-            wF[0][0] = t0[0][0]; wF[0][1] = t0[0][1];
-            wF[1][0] = t1[0][0]; wF[1][1] = t1[0][1];
-        }
-        float taps[NK_CONV_TAPS], hist[NK_CONV_TAPS - 1];
-#pragma unroll
-        for (int t = 0; t < NK_CONV_TAPS; ++t) taps[t] = ldg(W.dw_w + col1 * NK_CONV_TAPS + t);
-#pragma unroll
-        for (int t = 0; t < NK_CONV_TAPS - 1; ++t) hist[t] = ldg(dinl + (u64)(pos - (NK_CONV_TAPS - 1) + t) * D + col1);
-        if (attn) {
-            const floatx4 r = attend(sh, sh.ib[(h0 + 3) & 1], bu, bv, cl, a.scale);
-            if (tid < 32) {
-                u64 *sl = c.slot(h0 + 4);
-                const u32 tg = c.tag(h0 + 4), e0 = g * DH + 4 * tid;
-                ll_put(sl, e0, r[0], tg);
-                ll_put(sl, e0 + 1, r[1], tg);
-                ll_put(sl, e0 + 2, r[2], tg);
-                ll_put(sl, e0 + 3, r[3], tg);
+                for (int t = 0; t < NK_CONV_TAPS - 1; ++t) d += th[w * NK_CONV_TAPS + t] * th[4 * NK_CONV_TAPS + 4 * t + w];
+                d += th[w * NK_CONV_TAPS + NK_CONV_TAPS - 1] * gl;
+                if (lane == 0) {
+                    sh.aux[w] = gl;
+                    sh.outv[w] = d;
+                }
+                n_out = 4;
+                e_out = 4 * g;
+            } else {
+                const u32 kbs[1] = { kb0 + (j == PH_E ? OFF_E : OFF_G) + 2 * w };
+                float sums[1];
+                dots_ring<1>(sums, x, sh, kbs, lane);
+                if (lane == 0) sh.outv[w] = sh.xr[j == PH_E ? 1 : 0][col1] + sums[0];
+                n_out = 4;
+                e_out = 4 * g;
             }
         }
-
-        /* E: x + wo att */
-        lds_barrier();
-        if (sh.bad) return;
-        uint4 wG[1][2];
-        ld_rows<1, 2>(wG, W.pw2, col1, D, lane);
-        {
-            float x[2][8];
-            ld_x<2>(x, sh.ib[(h0 + 4) & 1], lane);
-            const float s = dot_row<2>(x, wE[0]);
-            const float v = sh.xr[1][col1] + s;
-            if (lane == 0) ll_put(c.slot(h0 + 5), col1, v, c.tag(h0 + 5));
-        }
-
-        /* F: pw1 GLU channel col1 (into the conv history), then its causal depthwise conv */
-        lds_barrier();
-        if (sh.bad) return;
-        uint4 wH[4][2];
-        ld_rows<4, 2>(wH, W.ff2_w1, colA, D, lane);
-        {
-            float x[2][8];
-            ld_x<2>(x, sh.ib[(h0 + 5) & 1], lane);
-            const float sa = dot_row<2>(x, wF[0]);
-            const float sb = dot_row<2>(x, wF[1]);
-            const float gl = sa * sigmoid_f(sb);
-            float d = 0.0f;
-#pragma unroll
-            for (int t = 0; t < NK_CONV_TAPS - 1; ++t) d += taps[t] * hist[t];
-            d += taps[NK_CONV_TAPS - 1] * gl;
-            if (lane == 0) {
-                stg(dinl + (u64)pos * D + col1, gl);
-                ll_put(c.slot(h0 + 6), col1, d, c.tag(h0 + 6));
-            }
-        }
-
-        /* G: x + pw2 SiLU(LN_bn(conv)) (normalised and activated by the hand-off wavefront) */
-        lds_barrier();
-        if (sh.bad) return;
-        uint4 wI[1][8];
-        ld_rows<1, 8>(wI, W.ff2_w2, col1, FF, lane);
-        {
-            float x[2][8];
-            ld_x<2>(x, sh.ib[(h0 + 6) & 1], lane);
-            const float s = dot_row<2>(x, wG[0]);
-            const float v = sh.xr[0][col1] + s;
-            if (lane == 0) ll_put(c.slot(h0 + 7), col1, v, c.tag(h0 + 7));
-        }
-
-        /* H: ff2_w1, SiLU */
-        lds_barrier();
-        if (sh.bad) return;
-        /* the next block's first weights (the last block reloads its own: unconditional loads
-         * keep the registers of the previous ones from staying live through the loop) */
-        const NkChainLayer &Wn = a.L[l + 1 < nl ? l + 1 : l];
-        ld_rows<4, 2>(wA, Wn.ff1_w1, colA, D, lane);
-        {
-            float x[2][8];
-            ld_x<2>(x, sh.ib[(h0 + 7) & 1], lane);
-            float mine = 0.0f;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const float s = silu_f(dot_row<2>(x, wH[j]));
-                if (lane == (u32)j) mine = s;
-            }
-            if (lane < 4) ll_put(c.slot(h0 + 8), colA + lane, mine, c.tag(h0 + 8));
-        }
-
-        /* I: x + 0.5 * ff2_w2 h: the next block's input, or the chain's output */
-        lds_barrier();
-        if (sh.bad) return;
-        ld_rows<1, 8>(wB, Wn.ff1_w2, col1, FF, lane);
-        {
-            float x[8][8];
-            ld_x<8>(x, sh.ib[(h0 + 8) & 1], lane);
-            const float s = dot_row<8>(x, wI[0]);
-            const float v = sh.xr[1][col1] + s * 0.5f;
-            if (lane == 0) {
-                if (l + 1 < nl) ll_put(c.slot(h0 + 9), col1, v, c.tag(h0 + 9));
-                else stg(a.x_out + col1, v);
+        u32 before = 0;
+        if (lane == 0) before = atomicAdd(&sh.done, 1u);
+        if ((__builtin_amdgcn_readfirstlane(before) & 3) == 3) {
+            /* the last wavefront: the others' LDS writes precede their count */
+            if (lane < n_out) {
+                const float v = sh.outv[lane];
+                if (p + 1 < P) ll_put(out, e_out + lane, v, tag);
+                else a.x_out[e_out + lane] = v;
+                if (j == PH_C) a.kv[(u64)l * a.kv_stride + (u64)pos * QKV + e_out + lane] = v;
+                if (j == PH_F) a.din[(u64)l * a.din_stride + (u64)pos * D + e_out + lane] = sh.aux[lane];
             }
         }
     }
 }
 
-/* wavefronts 4 and 5 */
+/* wavefronts 4 and 5: the input of phase p + 1 while phase p computes */
 __device__ __forceinline__ void handoff_loop(const NkChainArgs &a, Shared &sh, const Ctl &c, u32 g, u32 wave, u32 lane) {
-    const u32 nl = a.n_layers;
-    const u32 pos = (u32)a.desc[NK_DESC_POS], cl = (u32)a.desc[NK_DESC_CACHE];
-    const bool attn = g < H, w4 = wave == 4;
+    const u32 nl = a.n_layers, P = NK_CHAIN_PH * nl;
+    const u32 cl = (u32)a.desc[NK_DESC_CACHE], L = cl + 1;
+    const bool attn = g < NATT, w4 = wave == 4;
+    const u32 head = g / NP;
+    const Quarter qt = quarter(L, g % NP);
+    const bool has_new = qt.j0 + qt.nk == L && qt.nk > 0; /* this quarter holds the chunk's own row */
     const float eps = a.eps;
     const u32 pl = threadIdx.x - 4 * 64; /* 0 .. 127 over both wavefronts */
-    u32 e8[8], e16[16], eq[3];
+    float2 f_g[8], f_b[8];               /* block 0's LN_ff1 (later blocks take it from the ring) */
+    if (w4) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) e8[i] = 2 * (lane + 64 * i);
-#pragma unroll
-    for (int i = 0; i < 16; ++i) e16[i] = 2 * (pl + 128 * i);
-#pragma unroll
-    for (int i = 0; i < 3; ++i) eq[i] = i * D + g * DH + 2 * lane;
-    if (w4) ln_params_to_lds(sh, 2, a.L[0].ln_ff1_g, a.L[0].ln_ff1_b, lane);
-    else if (attn) kpv_to_lds(a, sh, 0, g, pos, cl, lane);
-    for (u32 l = 0; l < nl; ++l) {
-        const NkChainLayer &W = a.L[l];
-        const u32 h0 = 9 * l;
-
-        /* A: LN_out of the previous block (lnp[0..1]) gives the residual row, LN_ff1 (lnp[2..3])
-         * the input of ff1_w1 */
-        if (w4) {
-            float2 v[8];
-            bool ok = true;
-            if (l == 0) {
-#pragma unroll
-                for (int i = 0; i < 8; ++i) v[i] = *(const float2 *)(a.x_in + e8[i]);
-            } else {
-                ok = ll_wait<8>(c, h0, e8, v);
-            }
-            if (!ok) {
-                give_up(a, c, sh, h0);
-            } else {
-                wait_vm_lgkm<0>();
-                if (l > 0) ln_lds(v, sh, 0, eps, lane);
-                st_pairs(sh.xr[0], v, lane);
-                if (l > 0 && a.dump && g == 0) st_pairs(a.dump + (u64)(l - 1) * D, v, lane);
-                ln_lds(v, sh, 2, eps, lane);
-                st_pairs(sh.ib[h0 & 1], v, lane);
-            }
-            ln_params_to_lds(sh, 0, W.ln_att_g, W.ln_att_b, lane);
+        for (int i = 0; i < 8; ++i) {
+            f_g[i] = *(const float2 *)(a.L[0].ln_ff1_g + 2 * (lane + 64 * i));
+            f_b[i] = *(const float2 *)(a.L[0].ln_ff1_b + 2 * (lane + 64 * i));
         }
-        lds_barrier();
-        if (sh.bad) return;
-
-        /* B: the 4096-wide row, both wavefronts */
-        {
+    }
+#pragma nounroll
+    for (u32 p = 0; p < P; ++p) {
+        const u32 l = p / NK_CHAIN_PH, j = p % NK_CHAIN_PH, kb0 = l * BLOCK_KB;
+        bool ok = true;
+        if (j == PH_B || j == PH_E || j == PH_I) {
+            /* the 4096-wide row, both wavefronts (E: the attention quarters' outputs, then their
+             * (max, sum) pairs) */
             float2 v[16];
-            if (!ll_wait<16>(c, h0 + 1, e16, v)) give_up(a, c, sh, h0 + 1);
-            else {
+            ok = ll_wait<16>(c, p, 2 * pl, 256, v);
+            if (ok) {
 #pragma unroll
-                for (int i = 0; i < 16; ++i) *(float2 *)(sh.ib[(h0 + 1) & 1] + e16[i]) = v[i];
-            }
-        }
-        lds_barrier();
-        if (sh.bad) return;
-
-        /* C: LN_att */
-        if (w4) {
-            float2 v[8];
-            if (!ll_wait<8>(c, h0 + 2, e8, v)) give_up(a, c, sh, h0 + 2);
-            else {
-                wait_vm_lgkm<0>();
-                st_pairs(sh.xr[1], v, lane);
-                ln_lds(v, sh, 0, eps, lane);
-                st_pairs(sh.ib[(h0 + 2) & 1], v, lane);
-            }
-            ln_params_to_lds(sh, 0, W.ln_conv_g, W.ln_conv_b, lane);
-        }
-        lds_barrier();
-        if (sh.bad) return;
-
-        /* D: the head's q, k, v (attention workgroups) */
-        if (attn) {
-            if (w4) {
-                float2 v[3];
-                if (!ll_wait<3>(c, h0 + 3, eq, v)) give_up(a, c, sh, h0 + 3);
-                else {
-                    *(float2 *)(sh.ib[(h0 + 3) & 1] + 2 * lane) = v[0];
-                    *(float2 *)(sh.knew + 2 * lane) = v[1];
-                    *(float2 *)(sh.vnew + 2 * lane) = v[2];
+                for (int i = 0; i < 16; ++i) *(float2 *)(sh.big + 2 * (pl + 128 * i)) = v[i];
+                if (j == PH_E && w4) {
+                    float2 u[1];
+                    ok = ll_wait<1>(c, p, ML + 2 * (lane & 31), 0, u);
+                    if (ok && lane < 32) *(float2 *)(sh.big + ML + 2 * lane) = u[0];
                 }
+            }
+        } else if (j == PH_D) {
+            /* the head's q (and k, v in the quarter that holds the chunk's row) */
+            if (attn && w4) {
+                float2 v[3];
+                ok = ll_wait<3>(c, p, head * DH + 2 * lane, has_new ? D : 0, v);
+                if (ok) {
+                    *(float2 *)(sh.sm[1] + 2 * lane) = v[0];
+                    if (has_new) {
+                        *(float2 *)(sh.knew + 2 * lane) = v[1];
+                        *(float2 *)(sh.vnew + 2 * lane) = v[2];
+                    }
+                }
+            }
+        } else if (w4) {
+            /* a 1024-wide row: A (LN_out of the previous block gives the residual row, LN_ff1 the
+             * GEMV input, both from the previous block's I segment; block 0 reads its input row
+             * and keeps LN_ff1 in registers), C (LN_att, B segment), F (LN_conv, E segment),
+             * G (LN_bn then SiLU, F segment), H (LN_ff2, G segment); C, F, H keep the row itself
+             * as the residual */
+            float2 v[8];
+            if (p == 0) {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) v[i] = *(const float2 *)(a.x_in + 2 * (lane + 64 * i));
             } else {
-                wait_vm_lgkm<0>(); /* the K, V and position rows have landed */
+                ok = ll_wait<8>(c, p, 2 * lane, 128, v);
             }
-        }
-        lds_barrier();
-        if (sh.bad) return;
-        if (attn) {
-            lds_barrier();
-            lds_barrier();
-            lds_barrier();
-            lds_barrier();
-        }
-
-        /* E */
-        if (w4) {
-            float2 v[8];
-            if (!ll_wait<8>(c, h0 + 4, e8, v)) give_up(a, c, sh, h0 + 4);
-            else st_pairs(sh.ib[(h0 + 4) & 1], v, lane);
-        }
-        lds_barrier();
-        if (sh.bad) return;
-
-        /* F: LN_conv */
-        if (w4) {
-            float2 v[8];
-            if (!ll_wait<8>(c, h0 + 5, e8, v)) give_up(a, c, sh, h0 + 5);
-            else {
-                wait_vm_lgkm<0>();
-                st_pairs(sh.xr[0], v, lane);
-                ln_lds(v, sh, 0, eps, lane);
-                st_pairs(sh.ib[(h0 + 5) & 1], v, lane);
-            }
-            ln_params_to_lds(sh, 0, W.bn_g, W.bn_b, lane);
-        } else if (attn && l + 1 < nl) {
-            kpv_to_lds(a, sh, l + 1, g, pos, cl, lane); /* this block's attention has read them */
-        }
-        lds_barrier();
-        if (sh.bad) return;
-
-        /* G: SiLU(LN_bn(conv)) */
-        if (w4) {
-            float2 v[8];
-            if (!ll_wait<8>(c, h0 + 6, e8, v)) give_up(a, c, sh, h0 + 6);
-            else {
-                wait_vm_lgkm<0>();
-                ln_lds(v, sh, 0, eps, lane);
+            if (ok) {
+                if (j == PH_A) {
+                    const u32 kp = kb0 - BLOCK_KB + OFF_I;
+                    if (l > 0) ln_ring(v, sh, kp + 32, kp + 36, eps, lane);
+                    st_pairs(sh.xr[0], v, lane);
+                    if (l > 0 && a.dump && g == 0) st_pairs(a.dump + (u64)(l - 1) * D, v, lane);
+                    if (l > 0) ln_ring(v, sh, kp + 40, kp + 44, eps, lane);
+                    else ln_pairs(v, f_g, f_b, eps);
+                } else {
+                    if (j != PH_G) st_pairs(sh.xr[j == PH_F ? 0 : 1], v, lane);
+                    const u32 kg = kb0 + (j == PH_C ? OFF_B + 32 : j == PH_F ? OFF_E + 8 : j == PH_G ? OFF_F + 17 : OFF_G + 8);
+                    ln_ring(v, sh, kg, kg + 4, eps, lane);
+                    if (j == PH_G) {
 #pragma unroll
-                for (int i = 0; i < 8; ++i) { v[i].x = silu_f(v[i].x); v[i].y = silu_f(v[i].y); }
-                st_pairs(sh.ib[(h0 + 6) & 1], v, lane);
+                        for (int i = 0; i < 8; ++i) { v[i].x = silu_f(v[i].x); v[i].y = silu_f(v[i].y); }
+                    }
+                }
+                st_pairs(sh.sm[j == PH_G ? 1 : 0], v, lane);
             }
-            ln_params_to_lds(sh, 0, W.ln_ff2_g, W.ln_ff2_b, lane);
         }
+        if (!ok) give_up(a, c, sh, p);
         lds_barrier();
         if (sh.bad) return;
+        if (j == PH_D && attn) { /* the attention's four barriers */
+            lds_barrier();
+            lds_barrier();
+            lds_barrier();
+            lds_barrier();
+        }
+    }
+}
 
-        /* H: LN_ff2; then the next block's LN_out (this block's) and LN_ff1 */
-        if (w4) {
-            float2 v[8];
-            if (!ll_wait<8>(c, h0 + 7, e8, v)) give_up(a, c, sh, h0 + 7);
-            else {
-                wait_vm_lgkm<0>();
-                st_pairs(sh.xr[1], v, lane);
-                ln_lds(v, sh, 0, eps, lane);
-                st_pairs(sh.ib[(h0 + 7) & 1], v, lane);
-            }
-            if (l + 1 < nl) {
-                ln_params_to_lds(sh, 0, W.ln_out_g, W.ln_out_b, lane);
-                ln_params_to_lds(sh, 2, a.L[l + 1].ln_ff1_g, a.L[l + 1].ln_ff1_b, lane);
-            }
-        }
-        lds_barrier();
-        if (sh.bad) return;
+typedef __attribute__((address_space(4))) const NkChainLayer const_layer_t;
 
-        /* I: the 4096-wide row, both wavefronts */
-        {
-            float2 v[16];
-            if (!ll_wait<16>(c, h0 + 8, e16, v)) give_up(a, c, sh, h0 + 8);
-            else {
-#pragma unroll
-                for (int i = 0; i < 16; ++i) *(float2 *)(sh.ib[(h0 + 8) & 1] + e16[i]) = v[i];
+/* Segment p of the stream (block p / 9, phase p % 9) into the ring: its KB blocks go to ring
+ * blocks (l * BLOCK_KB + OFF_j + i) mod RING, one direct-to-LDS load of 16 bytes per lane each;
+ * the count of loads per segment is fixed (SEG_j; none for D outside the attention workgroups). */
+struct Stream {
+    const_layer_t *Lt; /* constant address space: the pointers are read with scalar loads, which
+                        * do not count in vmcnt (a vector load would need a vmcnt(0) wait, i.e. for
+                        * every segment in flight) */
+    const float *kv, *din;
+    u64 kv_stride, din_stride;
+    lds_char_t *ring; /* the LDS ring as an LDS address (a generic pointer here miscompiles) */
+    u32 g, lane, pos, cl, L, head, Lmax, nl;
+    Quarter qt;
+    bool attn;
+    __device__ void put(u32 kb, const void *src) const {
+        wait_vm_lgkm<STREAM_INFLIGHT - 1>();
+        dma16(src, ring + (kb % RING) * 1024);
+    }
+    /* n rows of nb blocks from src, rows row_bytes apart: block q of row r is bytes
+     * [1024 q, 1024 q + 1024) of that row (16 bytes per lane) */
+    __device__ void blocks(u32 kb, const void *src, u64 row_bytes, u32 n, u32 nb) const {
+        const char *s = (const char *)src + 16 * lane;
+#pragma nounroll
+        for (u32 r = 0; r < n; ++r)
+#pragma nounroll
+            for (u32 q = 0; q < nb; ++q) put(kb + r * nb + q, s + r * row_bytes + 1024 * q);
+    }
+    /* rows r0 .. r0 + n - 1 of a [.][K] bf16 matrix; a D-float vector */
+    __device__ void rows(u32 kb, const u16 *W, u32 r0, u32 n, u32 K) const { blocks(kb, W + (u64)r0 * K, 2ull * K, n, K / 512); }
+    __device__ void vec(u32 kb, const float *p) const { blocks(kb, p, 0, 1, D / 256); }
+    __device__ void seg(u32 p) const {
+        const u32 l = p / NK_CHAIN_PH, j = p % NK_CHAIN_PH, kb = l * BLOCK_KB;
+        const_layer_t &W = Lt[l];
+        if (j == PH_A) {
+            rows(kb + OFF_A, W.ff1_w1, 16 * g, 16, D);
+        } else if (j == PH_B) {
+            rows(kb + OFF_B, W.ff1_w2, 4 * g, 4, FF);
+            vec(kb + OFF_B + 32, W.ln_att_g);
+            vec(kb + OFF_B + 36, W.ln_att_b);
+        } else if (j == PH_C) {
+            rows(kb + OFF_C, W.wqkv, 12 * g, 12, D);
+        } else if (j == PH_D) {
+            if (attn) {
+                /* K, V rows of the quarter's cached window rows, P rows of all its rows (two rows
+                 * of 128 floats per block; rows past the quarter repeat a valid row) */
+                const float *kvl = kv + (u64)l * kv_stride;
+                const u32 half = lane >> 5, c4 = 4 * (lane & 31);
+#pragma nounroll
+                for (u32 b = 0; b < 8; ++b) {
+                    const u32 jr = qt.j0 + 2 * b + half;
+                    const u32 kvrow = cl > 0 ? pos - cl + min(jr, cl - 1) : pos;
+                    const float *src = kvl + (u64)kvrow * QKV + head * DH + c4;
+                    put(kb + OFF_D + b, src + D);
+                    put(kb + OFF_D + 8 + b, src + 2 * D);
+                    put(kb + OFF_D + 16 + b, W.ptab + (u64)(Lmax - L + min(jr, L - 1)) * D + head * DH + c4);
+                }
+                /* u for lanes 0-31, v for 32-63, as an offset from u: a per-lane choice of which
+                 * table entry to read would make the read a vector load (and a vmcnt(0) wait) */
+                const u64 bu = (u64)W.bias_u, dv = (u64)W.bias_v - bu;
+                put(kb + OFF_D + 24, (const float *)(bu + (half ? dv : 0)) + head * DH + c4);
             }
+        } else if (j == PH_E) {
+            rows(kb + OFF_E, W.wo, 4 * g, 4, D);
+            vec(kb + OFF_E + 8, W.ln_conv_g);
+            vec(kb + OFF_E + 12, W.ln_conv_b);
+        } else if (j == PH_F) {
+            rows(kb + OFF_F, W.pw1, 4 * g, 4, D);
+            rows(kb + OFF_F + 8, W.pw1, D + 4 * g, 4, D);
+            /* lanes 0-8: the 36 taps of channels 4g .. 4g+3; lanes 9-16: their 8 history rows */
+            const float *dinl = din + (u64)l * din_stride;
+            const u32 t = lane - 9;
+            const float *src = lane < 9    ? W.dw_w + 4 * g * NK_CONV_TAPS + 4 * lane
+                               : lane < 17 ? dinl + (u64)(pos - (NK_CONV_TAPS - 1) + t) * D + 4 * g
+                                           : W.dw_w + 4 * g * NK_CONV_TAPS;
+            put(kb + OFF_F + 16, src);
+            vec(kb + OFF_F + 17, W.bn_g);
+            vec(kb + OFF_F + 21, W.bn_b);
+        } else if (j == PH_G) {
+            rows(kb + OFF_G, W.pw2, 4 * g, 4, D);
+            vec(kb + OFF_G + 8, W.ln_ff2_g);
+            vec(kb + OFF_G + 12, W.ln_ff2_b);
+        } else if (j == PH_H) {
+            rows(kb + OFF_H, W.ff2_w1, 16 * g, 16, D);
+        } else {
+            rows(kb + OFF_I, W.ff2_w2, 4 * g, 4, FF);
+            vec(kb + OFF_I + 32, W.ln_out_g);
+            vec(kb + OFF_I + 36, W.ln_out_b);
+            const_layer_t &Wn = Lt[l + 1 < nl ? l + 1 : l];
+            vec(kb + OFF_I + 40, Wn.ln_ff1_g);
+            vec(kb + OFF_I + 44, Wn.ln_ff1_b);
         }
+    }
+};
+
+/* wavefront 6: segment p + 2 after the barrier of phase p, then a wait for segment p + 1 before
+ * the barrier of phase p + 1.  The loads complete in order and at most STREAM_INFLIGHT are in
+ * flight, all of them (when it is not empty) from segment p + 2, which holds more than that. */
+__device__ __forceinline__ void stream_loop(const NkChainArgs &a, Shared &sh, u32 g, u32 lane) {
+    const u32 nl = a.n_layers, P = NK_CHAIN_PH * nl;
+    Stream st;
+    st.Lt = (const_layer_t *)a.L;
+    st.kv = a.kv;
+    st.din = a.din;
+    st.kv_stride = a.kv_stride;
+    st.din_stride = a.din_stride;
+    st.Lmax = a.Lmax;
+    st.nl = nl;
+    st.ring = (lds_char_t *)sh.ring;
+    st.g = g;
+    st.lane = lane;
+    st.pos = (u32)a.desc[NK_DESC_POS];
+    st.cl = (u32)a.desc[NK_DESC_CACHE];
+    st.L = st.cl + 1;
+    st.attn = g < NATT;
+    st.head = g / NP;
+    st.qt = quarter(st.L, g % NP);
+    st.seg(0);
+    st.seg(1);
+    wait_vm_lgkm<STREAM_INFLIGHT>();
+#pragma nounroll
+    for (u32 p = 0; p < P; ++p) {
         lds_barrier();
         if (sh.bad) return;
+        if (p % NK_CHAIN_PH == PH_D && st.attn) {
+            lds_barrier();
+            lds_barrier();
+            lds_barrier();
+            lds_barrier();
+        }
+        const u32 q = p + 2;
+        if (q < P) st.seg(q);
+        if (q < P && (q % NK_CHAIN_PH != PH_D || st.attn)) wait_vm_lgkm<STREAM_INFLIGHT>();
+        else wait_vm_lgkm<0>();
     }
 }
 
@@ -657,9 +702,13 @@ extern "C" __global__ __launch_bounds__(NK_CHAIN_THREADS) void enc_chain(const N
     c.epoch = (u32)a.desc[NK_DESC_EPOCH];
     c.base = c.epoch << 10;
     c.spin_max = a.spin_max;
-    if (tid == 0) sh.bad = 0;
+    if (tid == 0) {
+        sh.bad = 0;
+        sh.done = 0;
+    }
     __syncthreads();
     if (wave < 4) chain::compute_loop(a, sh, c, g, wave, lane);
-    else chain::handoff_loop(a, sh, c, g, wave, lane);
+    else if (wave < 6) chain::handoff_loop(a, sh, c, g, wave, lane);
+    else chain::stream_loop(a, sh, g, lane);
     wait_vm_lgkm<0>(); /* no direct-to-LDS load outlives the workgroup */
 }
