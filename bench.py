@@ -48,7 +48,9 @@ METRIC = "RTFx (audio-s/s) + p50 chunk ms at 1 and 64 streams; achieved HBM GB/s
 HBM_PEAK_GBS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0
 LAT_RIGHT = {80: 0, 160: 1, 320: 3, 560: 6, 1120: 13}
-DOMINANT = {80: "gemv_*", 160: "gemv_*", 320: "gemm_fr*", 560: "gemm_fr*", 1120: "gemm_fr*"}
+# dominant kernel class per latency: one-row chunks run every conformer block in one persistent
+# launch (enc_chain); two-row chunks stream each matrix in a GEMV, longer chunks in few-row GEMMs
+DOMINANT = {80: "enc_chain", 160: "gemv_*", 320: "gemm_fr*", 560: "gemm_fr*", 1120: "gemm_fr*"}
 # joint-bias skews (blank_bias, label_shift) of the checkpoints for the skewed legs, calibrated on
 # those legs' own workloads by bisection on label_shift (MI355X): S1120 gives P(blank) 0.500
 # (376 tokens over 376 frames), B256 0.701

@@ -31,8 +31,8 @@ void nemoasr_debug_use_graphs(nemoasr_t *s, int on);
 /* 1 (default): chunks of at most two rows run attention + output projection and depthwise conv +
  * pointwise conv as one launch each; 0: the separate launches. */
 void nemoasr_debug_fuse(nemoasr_t *s, int on);
-/* 1: one-row chunks run every conformer block in one persistent launch, where the
- * model shape and device allow it (nemoasr_debug_chain_usable); 0 (default): the per-kernel sequence. */
+/* 1 (default): one-row chunks run every conformer block in one persistent launch, where the
+ * model shape and device allow it (nemoasr_debug_chain_usable); 0: the per-kernel sequence. */
 void nemoasr_debug_chain(nemoasr_t *s, int on);
 int nemoasr_debug_chain_usable(const nemoasr_t *s);
 /* Round trips of the decoder since open/reset, and GPU time of the encoder chunks (ms). */

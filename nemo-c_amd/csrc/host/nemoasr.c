@@ -238,7 +238,7 @@ nemoasr_t *nemoasr_open(const char *model_dir, const char *language, int latency
     }
     s->graphs = 1;
     s->fuse = 1;
-    s->chain = 0; /* on by nemoasr_debug_chain until it beats the per-kernel graph */
+    s->chain = 1; /* one-row chunks run the persistent chain where the device and model allow it */
     s->dec = decoder_create(s->m);
     if (s->dec) warm_up(s, right);
     s->warm = 1u << right;

@@ -160,9 +160,13 @@ __device__ __forceinline__ void give_up(const NkChainArgs &a, const Ctl &c, Shar
 __device__ __forceinline__ const char *rblk(const Shared &sh, u32 kb) { return sh.ring + (kb % RING) * 1024; }
 __device__ __forceinline__ uint4 rw16(const Shared &sh, u32 kb, u32 lane) { return *(const uint4 *)(rblk(sh, kb) + 16 * lane); }
 
+/* x * sigmoid(x) with the hardware exp2 and reciprocal (about 1 ulp each): one wavefront
+ * evaluates it on a whole 1024-row between a hand-off and the next GEMV */
+__device__ __forceinline__ float silu_fast(float v) { return v * __builtin_amdgcn_rcpf(1.0f + __expf(-v)); }
+
 /* LayerNorm of a 1024-row held as float2 pairs by one wavefront (lane l: elements 2(l + 64i),
  * +1): mean, then the centred variance (the reference's two passes, summed in another order),
- * y = (x - mean) * (1 / sqrt(var + eps)) * g + b. */
+ * y = (x - mean) * rsqrt(var + eps) * g + b (hardware reciprocal square root, about 1 ulp). */
 __device__ __forceinline__ void ln_pairs(float2 (&v)[8], const float2 (&g)[8], const float2 (&b)[8], float eps) {
     /* the lane's 16 terms summed as a tree (a short dependent chain), then across the wavefront */
     float t[8];
@@ -174,7 +178,7 @@ __device__ __forceinline__ void ln_pairs(float2 (&v)[8], const float2 (&g)[8], c
         const float d0 = v[i].x - mean, d1 = v[i].y - mean;
         t[i] = d0 * d0 + d1 * d1;
     }
-    const float inv = 1.0f / sqrtf(wsum(((t[0] + t[1]) + (t[2] + t[3])) + ((t[4] + t[5]) + (t[6] + t[7]))) / (float)D + eps);
+    const float inv = __builtin_amdgcn_rsqf(wsum(((t[0] + t[1]) + (t[2] + t[3])) + ((t[4] + t[5]) + (t[6] + t[7]))) / (float)D + eps);
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
         v[i].x = (v[i].x - mean) * inv * g[i].x + b[i].x;
@@ -535,7 +539,10 @@ __device__ __forceinline__ void handoff_loop(const NkChainArgs &a, Shared &sh, c
                     ln_ring(v, sh, kg, kg + 4, eps, lane);
                     if (j == PH_G) {
 #pragma unroll
-                        for (int i = 0; i < 8; ++i) { v[i].x = silu_f(v[i].x); v[i].y = silu_f(v[i].y); }
+                        for (int i = 0; i < 8; ++i) {
+                            v[i].x = silu_fast(v[i].x);
+                            v[i].y = silu_fast(v[i].y);
+                        }
                     }
                 }
                 st_pairs(sh.sm[j == PH_G ? 1 : 0], v, lane);
