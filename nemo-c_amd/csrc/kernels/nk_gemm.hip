@@ -57,8 +57,9 @@ __device__ __forceinline__ void ln_wave4(floatx4 (&v)[4], const floatx4 (&g)[4],
  * FOLD (with LNA): the activation rows are A plus a pending residual update,
  * A + alpha * (((0 + p0) + p1) + ...) with at most FR_FOLD_PARTS partial rows, formed by each
  * wavefront for the rows it normalises (the order and form of resid_fold); workgroup (0, 0) writes
- * them to fold_out when it is set.  The LayerNorm parameters then pass through LDS (sP), so that
- * they load with the rows and the parts without holding registers through the fold. */
+ * them to fold_out when it is set.  The LayerNorm parameters pass through LDS (sP) in every LNA
+ * variant, so that they load with the rows (and the parts) without holding registers through the
+ * fold. */
 #define FR_FOLD_PARTS 4
 /* PK (GLU only): a workgroup owns 8 output pairs, whose value and gate weight rows share one
  * 16-column B operand (columns 0-7 values, 8-15 gates), so there is one MFMA pair per step and
@@ -82,19 +83,10 @@ __device__ __forceinline__ void fr_impl(const NkGemmArgs &a, float *sA, floatx4 
     const bool mrow = m < M;
 
     /* LayerNorm variant: wavefront w normalises rows w, w + W, ... (those below M).  Its parameters
-     * load with the rows, or, with FOLD, once the partial rows are summed (so the registers of
-     * the two are never live together) */
+     * are loaded once per workgroup and pass through LDS (sP): loaded by every wavefront they were
+     * 128 KB of cache reads per workgroup queued ahead of its weights (0.4 us per launch) */
     floatx4 v[LNA ? RPW : 1][4], g1[4], b1[4], g2[4], b2[4];
     floatx4 fp[FOLD ? RPW : 1][FOLD ? FR_FOLD_PARTS : 1][4];
-    auto ln_params = [&]() {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            g1[j] = ((const floatx4 *)a.ln_g1)[lane + 64 * j];
-            b1[j] = ((const floatx4 *)a.ln_b1)[lane + 64 * j];
-            g2[j] = ((const floatx4 *)(a.ln_mode == 2 ? a.ln_g2 : a.ln_g1))[lane + 64 * j];
-            b2[j] = ((const floatx4 *)(a.ln_mode == 2 ? a.ln_b2 : a.ln_b1))[lane + 64 * j];
-        }
-    };
     if constexpr (LNA) {
 #pragma unroll
         for (int i = 0; i < RPW; ++i) {
@@ -110,12 +102,11 @@ __device__ __forceinline__ void fr_impl(const NkGemmArgs &a, float *sA, floatx4 
                             fp[i][h][j] = ((const floatx4 *)(a.fold + ((u64)h * M + r) * a.K))[lane + 64 * j];
             }
         }
-        if constexpr (!FOLD) ln_params();
     }
-    /* FOLD: this thread's float4 c = tid % 256 of two parameters: g1 and g2 (wavefronts 0-3) or b1
-     * and b2 (wavefronts 4-7); the choice is per wavefront (a scalar branch) */
-    floatx4 pq[FOLD ? 2 : 1];
-    if constexpr (FOLD) {
+    /* this thread's float4 c = tid % 256 of two parameters: g1 and g2 (wavefronts 0-3) or b1 and b2
+     * (wavefronts 4-7); the choice is per wavefront (a scalar branch) */
+    floatx4 pq[LNA ? 2 : 1];
+    if constexpr (LNA) {
         const u32 c = tid & 255;
         const bool two = a.ln_mode == 2;
         if (wave < 4) {
@@ -178,7 +169,7 @@ __device__ __forceinline__ void fr_impl(const NkGemmArgs &a, float *sA, floatx4 
     for (int i = 0; i < 4; ++i) ec[i] = a.C[(u64)(u32)erow[i] * a.ldc + col];
 
     /* 2. LayerNorm of the activation rows into LDS while the weights stream in */
-    if constexpr (FOLD) {
+    if constexpr (LNA) {
         static_assert(W == 8, "the parameter staging assumes 512 threads");
         /* sP: g1 [0, 256), b1 [256, 512), g2 [512, 768), b2 [768, 1024) */
         sP[tid] = pq[0];
@@ -210,13 +201,13 @@ __device__ __forceinline__ void fr_impl(const NkGemmArgs &a, float *sA, floatx4 
 #pragma unroll
                     for (int j = 0; j < 4; ++j) ((floatx4 *)(a.fold_out + (u64)r * a.lda))[lane + 64 * j] = v[i][j];
             }
+        }
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                g1[j] = sP[lane + 64 * j];
-                b1[j] = sP[256 + lane + 64 * j];
-                g2[j] = sP[512 + lane + 64 * j];
-                b2[j] = sP[768 + lane + 64 * j];
-            }
+        for (int j = 0; j < 4; ++j) {
+            g1[j] = sP[lane + 64 * j];
+            b1[j] = sP[256 + lane + 64 * j];
+            g2[j] = sP[512 + lane + 64 * j];
+            b2[j] = sP[768 + lane + 64 * j];
         }
 #pragma unroll
         for (int i = 0; i < RPW; ++i) {
@@ -322,7 +313,7 @@ GEMM_FR(gemm_fr_glu_w4s8, 4, 8, true)
     extern "C" __global__ __launch_bounds__(512) void NAME(const NkGemmArgs a) {                         \
         __shared__ float sA[16 * 1024];                                                                  \
         __shared__ floatx4 sred[8 * 64];                                                                 \
-        __shared__ floatx4 sP[FOLD ? 1024 : 1];                                                          \
+        __shared__ floatx4 sP[1024];                                                                     \
         fr_impl<8, 4, true, GLU, FOLD, GLU>(a, sA, sred, sP);                                            \
     }
 GEMM_FR_LN(gemm_fr_ln_w8s4, false, false)
