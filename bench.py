@@ -395,6 +395,10 @@ def main():
     import nemoasr
     import synth
 
+    if a.no_graphs:
+        # direct launches from each session's open on (its warm-up included)
+        nemoasr.lib().nemoasr_debug_default_graphs(0)
+
     def sub3(nsamp):  # encoder frames of a clip: mel frames (centred, 10 ms hop) subsampled x8
         n = nsamp // 160 + 1
         for _ in range(3):

@@ -28,6 +28,10 @@ const float *nemoasr_debug_dump_joint_enc(const nemoasr_t *s);
 const float *nemoasr_debug_dump_mel(const nemoasr_t *s, size_t *nframes);
 /* 0: launch every kernel directly; 1: replay chunks as hipGraphs (default). */
 void nemoasr_debug_use_graphs(nemoasr_t *s, int on);
+/* The graph setting of sessions opened from now on, their warm-up included (1 by default): 0 makes
+ * every launch of the session a direct launch from its first (profilers that cannot follow graph
+ * launches). */
+void nemoasr_debug_default_graphs(int on);
 /* 1 (default): chunks of at most two rows run attention + output projection and depthwise conv +
  * pointwise conv as one launch each; 0: the separate launches. */
 void nemoasr_debug_fuse(nemoasr_t *s, int on);

@@ -23,6 +23,9 @@
 #include <string.h>
 #include <time.h>
 
+/* graph replay for sessions opened from now on (warm-up included); nemoasr_debug_default_graphs */
+static int g_default_graphs = 1;
+
 #define TOKENS_PER_CHUNK_MAX 4096
 
 static double clock_ms(void) {
@@ -236,10 +239,11 @@ nemoasr_t *nemoasr_open(const char *model_dir, const char *language, int latency
         nemoasr_close(s);
         return NULL;
     }
-    s->graphs = 1;
+    s->graphs = g_default_graphs;
     s->fuse = 1;
     s->chain = 1; /* one-row chunks run the persistent chain where the device and model allow it */
     s->dec = decoder_create(s->m);
+    if (s->dec) decoder_use_graphs(s->dec, s->graphs);
     if (s->dec) warm_up(s, right);
     s->warm = 1u << right;
     s->enc = encoder_for(s, right);
@@ -438,6 +442,7 @@ size_t nemoasr_debug_frames(const nemoasr_t *s) { return encoder_dump_frames(s->
 const float *nemoasr_debug_dump_layers(const nemoasr_t *s) { return encoder_dump_layers(s->enc); }
 const float *nemoasr_debug_dump_prompted(const nemoasr_t *s) { return encoder_dump_prompted(s->enc); }
 const float *nemoasr_debug_dump_joint_enc(const nemoasr_t *s) { return encoder_dump_joint(s->enc); }
+void nemoasr_debug_default_graphs(int on) { g_default_graphs = on != 0; }
 void nemoasr_debug_use_graphs(nemoasr_t *s, int on) {
     s->graphs = on != 0;
     encoder_use_graphs(s->enc, on);

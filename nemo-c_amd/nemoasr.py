@@ -71,6 +71,7 @@ API = {
     "nemoasr_debug_use_graphs": (None, [_vp, C.c_int]),
     "nemoasr_debug_fuse": (None, [_vp, C.c_int]),
     "nemoasr_debug_chain": (None, [_vp, C.c_int]),
+    "nemoasr_debug_default_graphs": (None, [C.c_int]),
     "nemoasr_debug_chain_usable": (C.c_int, [_vp]),
     "nemoasr_debug_joint_steps": (C.c_size_t, [_vp]),
     "nemoasr_debug_encoder_gpu_ms": (C.c_double, [_vp]),
