@@ -41,10 +41,11 @@
  * put that stall on every phase's critical path.  Instead one wavefront per workgroup streams the
  * workgroup's whole sequence of weight slices (with the LayerNorm parameters, the conv taps and
  * history and, in the attention workgroups, the head's K, V and position rows) into a 120 KB LDS
- * ring by direct-to-LDS loads, two phases ahead: after the barrier of phase p it issues the
+ * area by direct-to-LDS loads, two phases ahead: after the barrier of phase p it issues the
  * segment of phase p + 2, then waits for the segment of phase p + 1 before the next barrier.
- * Segment sizes are fixed per phase (SEG_*), so every ring offset is known statically and the
- * ring holds any three consecutive segments.
+ * Each kind of phase has a segment of fixed size (SEG_*) at a fixed place in the area (AT_*),
+ * chosen so that any three consecutive segments are disjoint: every LDS address of a weight block
+ * is a constant of the code that reads it.
  *
  * Roles within a workgroup (7 wavefronts, one LDS barrier per phase):
  *   - wavefronts 0-3 compute: read the phase's input row and their weight rows from LDS (lane l
@@ -67,16 +68,21 @@ constexpr u32 RING = 120;       /* KB */
  * shared by all its wavefronts: a deeper stream would hold the hand-off stores and waits of the
  * other wavefronts behind it. */
 constexpr int STREAM_INFLIGHT = 16;
-/* ring segment of each phase (KB blocks) and its offset within a block's stream */
+/* segment of each kind of phase: its size and its first block in the area (KB blocks) */
 constexpr u32 SEG_A = 32, SEG_B = 40, SEG_C = 24, SEG_D = 25, SEG_E = 16, SEG_F = 25, SEG_G = 16, SEG_H = 32, SEG_I = 48;
-constexpr u32 OFF_A = 0, OFF_B = OFF_A + SEG_A, OFF_C = OFF_B + SEG_B, OFF_D = OFF_C + SEG_C, OFF_E = OFF_D + SEG_D,
-              OFF_F = OFF_E + SEG_E, OFF_G = OFF_F + SEG_F, OFF_H = OFF_G + SEG_G, OFF_I = OFF_H + SEG_H,
-              BLOCK_KB = OFF_I + SEG_I;
+constexpr u32 AT_A = 88, AT_B = 48, AT_C = 0, AT_D = 88, AT_E = 25, AT_F = 0, AT_G = 80, AT_H = 48, AT_I = 0;
+constexpr u32 SEG_N[9] = { SEG_A, SEG_B, SEG_C, SEG_D, SEG_E, SEG_F, SEG_G, SEG_H, SEG_I };
+constexpr u32 SEG_AT[9] = { AT_A, AT_B, AT_C, AT_D, AT_E, AT_F, AT_G, AT_H, AT_I };
+constexpr bool seg_apart(u32 j, u32 k) { return SEG_AT[j] + SEG_N[j] <= SEG_AT[k] || SEG_AT[k] + SEG_N[k] <= SEG_AT[j]; }
+constexpr bool segs_placed() {
+    for (u32 j = 0; j < 9; ++j)
+        if (SEG_AT[j] + SEG_N[j] > RING || !seg_apart(j, (j + 1) % 9) || !seg_apart(j, (j + 2) % 9)) return false;
+    return true;
+}
 static_assert(H * DH == D && G * 4 == D && G * 16 == FF && G * 12 == QKV, "slices assume these shapes");
 static_assert(ML + 2 * NATT <= SLOT && NATT <= G && MAXL % NP == 0 && MAXL / NP <= 16, "attention split");
-static_assert(SEG_I + SEG_A + SEG_B <= RING && SEG_H + SEG_I + SEG_A <= RING && SEG_A + SEG_B + SEG_C <= RING &&
-                  SEG_B + SEG_C + SEG_D <= RING && SEG_G + SEG_H + SEG_I <= RING,
-              "the ring holds any three consecutive segments");
+static_assert(segs_placed(), "every segment lies in the area and apart from the next two (the phase in flight and the one "
+                             "computing)");
 static_assert(SEG_A >= STREAM_INFLIGHT && SEG_B >= STREAM_INFLIGHT && SEG_C >= STREAM_INFLIGHT &&
                   SEG_D >= STREAM_INFLIGHT && SEG_E >= STREAM_INFLIGHT && SEG_F >= STREAM_INFLIGHT &&
                   SEG_G >= STREAM_INFLIGHT && SEG_H >= STREAM_INFLIGHT && SEG_I >= STREAM_INFLIGHT,
@@ -128,21 +134,30 @@ __device__ __forceinline__ bool ll_wait(const Ctl &c, u32 hand, u32 e0, u32 es, 
     const u32 tag = c.tag(hand);
     u32 spins = 0;
     for (;;) {
-        int first_bad = -1;
+        /* the complete pass is the one on the hand-off's critical path: one test per lane for all
+         * its groups (a vector OR of the tag differences), the first incomplete group only
+         * sought after a failed pass */
+        u32x4 r[NL];
+        u32 miss = 0;
+#pragma unroll
+        for (int i = 0; i < NL; ++i) r[i] = ll_load(slot, e0 + i * es);
 #pragma unroll
         for (int i = 0; i < NL; ++i) {
-            const u32x4 r = ll_load(slot, e0 + i * es);
-            v[i] = make_float2(__uint_as_float(r.x), __uint_as_float(r.z));
-            if (!__all((r.y == tag) & (r.w == tag)) && first_bad < 0) first_bad = i;
+            v[i] = make_float2(__uint_as_float(r[i].x), __uint_as_float(r[i].z));
+            miss |= (r[i].y ^ tag) | (r[i].w ^ tag);
         }
-        if (first_bad < 0) return true;
-        const u32 eb = e0 + (u32)first_bad * es;
+        if (__all(miss == 0)) return true;
+        u32 first_bad = NL - 1;
+#pragma unroll
+        for (int i = NL - 2; i >= 0; --i)
+            if (!__all((r[i].y == tag) & (r[i].w == tag))) first_bad = i;
+        const u32 eb = e0 + first_bad * es;
         for (;;) {
             if (++spins > c.spin_max) return false;
             if ((spins & 255) == 0 && __hip_atomic_load(c.abort_word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == c.epoch)
                 return false;
-            const u32x4 r = ll_load(slot, eb);
-            if (__all((r.y == tag) & (r.w == tag))) break;
+            const u32x4 u = ll_load(slot, eb);
+            if (__all((u.y == tag) & (u.w == tag))) break;
         }
     }
 }
@@ -156,8 +171,8 @@ __device__ __forceinline__ void give_up(const NkChainArgs &a, const Ctl &c, Shar
     }
 }
 
-/* ring block kb (a KB index of the workgroup's stream) */
-__device__ __forceinline__ const char *rblk(const Shared &sh, u32 kb) { return sh.ring + (kb % RING) * 1024; }
+/* block kb of the weight area */
+__device__ __forceinline__ const char *rblk(const Shared &sh, u32 kb) { return sh.ring + kb * 1024; }
 __device__ __forceinline__ uint4 rw16(const Shared &sh, u32 kb, u32 lane) { return *(const uint4 *)(rblk(sh, kb) + 16 * lane); }
 
 /* x * sigmoid(x) with the hardware exp2 and reciprocal (about 1 ulp each): one wavefront
@@ -368,7 +383,7 @@ __device__ __forceinline__ void compute_loop(const NkChainArgs &a, Shared &sh, c
     const u32 col1 = 4 * g + w; /* this wavefront's column of the 1024-wide outputs */
 #pragma nounroll
     for (u32 p = 0; p < P; ++p) {
-        const u32 l = p / NK_CHAIN_PH, j = p % NK_CHAIN_PH, kb0 = l * BLOCK_KB;
+        const u32 l = p / NK_CHAIN_PH, j = p % NK_CHAIN_PH;
         u64 *out = c.slot(p + 1);
         const u32 tag = c.tag(p + 1);
         lds_barrier();
@@ -378,7 +393,7 @@ __device__ __forceinline__ void compute_loop(const NkChainArgs &a, Shared &sh, c
              * stored by wavefront 0 as two 512-byte runs of entries and one pair */
             if (attn) {
                 float m, lsum;
-                const floatx4 r = attend_part(sh, kb0 + OFF_D, sh.sm[1], cl, qt.j0, qt.nk, a.scale, m, lsum);
+                const floatx4 r = attend_part(sh, AT_D, sh.sm[1], cl, qt.j0, qt.nk, a.scale, m, lsum);
                 if (tid < 32) *(floatx4 *)&sh.att_out[4 * tid] = r;
                 if (w == 0) {
                     ll_put(out, g * DH + lane, sh.att_out[lane], tag);
@@ -396,7 +411,7 @@ __device__ __forceinline__ void compute_loop(const NkChainArgs &a, Shared &sh, c
             /* x + 0.5 * ff_w2 h: one row of K = 4096 per wavefront */
             float x[8][8];
             ld_x<8>(x, sh.big, lane);
-            const float s = dot_ring<8>(x, sh, kb0 + (j == PH_B ? OFF_B : OFF_I) + 8 * w, lane);
+            const float s = dot_ring<8>(x, sh, (j == PH_B ? AT_B : AT_I) + 8 * w, lane);
             if (lane == 0) sh.outv[w] = sh.xr[j == PH_B ? 0 : 1][col1] + s * 0.5f;
             n_out = 4;
             e_out = 4 * g;
@@ -407,7 +422,7 @@ __device__ __forceinline__ void compute_loop(const NkChainArgs &a, Shared &sh, c
             if (j == PH_E) ld_att(x, sh, lane);
             else ld_x<2>(x, sh.sm[j == PH_G ? 1 : 0], lane);
             if (j == PH_A || j == PH_H) {
-                const u32 kb = kb0 + (j == PH_A ? OFF_A : OFF_H) + 8 * w; /* rows 4w .. 4w+3 */
+                const u32 kb = (j == PH_A ? AT_A : AT_H) + 8 * w; /* rows 4w .. 4w+3 */
                 const u32 kbs[4] = { kb, kb + 2, kb + 4, kb + 6 };
                 float sums[4];
                 dots_ring<4>(sums, x, sh, kbs, lane);
@@ -416,7 +431,7 @@ __device__ __forceinline__ void compute_loop(const NkChainArgs &a, Shared &sh, c
                 n_out = 16;
                 e_out = 16 * g;
             } else if (j == PH_C) {
-                const u32 kb = kb0 + OFF_C + 6 * w; /* rows 3w .. 3w+2 */
+                const u32 kb = AT_C + 6 * w; /* rows 3w .. 3w+2 */
                 const u32 kbs[3] = { kb, kb + 2, kb + 4 };
                 float sums[3];
                 dots_ring<3>(sums, x, sh, kbs, lane);
@@ -424,11 +439,11 @@ __device__ __forceinline__ void compute_loop(const NkChainArgs &a, Shared &sh, c
                 n_out = 12;
                 e_out = 12 * g;
             } else if (j == PH_F) {
-                const u32 kbs[2] = { kb0 + OFF_F + 2 * w, kb0 + OFF_F + 2 * (4 + w) }; /* GLU rows w, 4 + w */
+                const u32 kbs[2] = { AT_F + 2 * w, AT_F + 2 * (4 + w) }; /* GLU rows w, 4 + w */
                 float sums[2];
                 dots_ring<2>(sums, x, sh, kbs, lane);
                 const float gl = sums[0] * sigmoid_f(sums[1]);
-                const float *th = (const float *)rblk(sh, kb0 + OFF_F + 16); /* taps [4][9], then history [8][4] */
+                const float *th = (const float *)rblk(sh, AT_F + 16); /* taps [4][9], then history [8][4] */
                 float d = 0.0f;
 #pragma unroll
                 for (int t = 0; t < NK_CONV_TAPS - 1; ++t) d += th[w * NK_CONV_TAPS + t] * th[4 * NK_CONV_TAPS + 4 * t + w];
@@ -440,7 +455,7 @@ __device__ __forceinline__ void compute_loop(const NkChainArgs &a, Shared &sh, c
                 n_out = 4;
                 e_out = 4 * g;
             } else {
-                const u32 kbs[1] = { kb0 + (j == PH_E ? OFF_E : OFF_G) + 2 * w };
+                const u32 kbs[1] = { (j == PH_E ? AT_E : AT_G) + 2 * w };
                 float sums[1];
                 dots_ring<1>(sums, x, sh, kbs, lane);
                 if (lane == 0) sh.outv[w] = sh.xr[j == PH_E ? 1 : 0][col1] + sums[0];
@@ -483,7 +498,7 @@ __device__ __forceinline__ void handoff_loop(const NkChainArgs &a, Shared &sh, c
     }
 #pragma nounroll
     for (u32 p = 0; p < P; ++p) {
-        const u32 l = p / NK_CHAIN_PH, j = p % NK_CHAIN_PH, kb0 = l * BLOCK_KB;
+        const u32 l = p / NK_CHAIN_PH, j = p % NK_CHAIN_PH;
         bool ok = true;
         if (j == PH_B || j == PH_E || j == PH_I) {
             /* the 4096-wide row, both wavefronts (E: the attention quarters' outputs, then their
@@ -527,15 +542,14 @@ __device__ __forceinline__ void handoff_loop(const NkChainArgs &a, Shared &sh, c
             }
             if (ok) {
                 if (j == PH_A) {
-                    const u32 kp = kb0 - BLOCK_KB + OFF_I;
-                    if (l > 0) ln_ring(v, sh, kp + 32, kp + 36, eps, lane);
+                    if (l > 0) ln_ring(v, sh, AT_I + 32, AT_I + 36, eps, lane);
                     st_pairs(sh.xr[0], v, lane);
                     if (l > 0 && a.dump && g == 0) st_pairs(a.dump + (u64)(l - 1) * D, v, lane);
-                    if (l > 0) ln_ring(v, sh, kp + 40, kp + 44, eps, lane);
+                    if (l > 0) ln_ring(v, sh, AT_I + 40, AT_I + 44, eps, lane);
                     else ln_pairs(v, f_g, f_b, eps);
                 } else {
                     if (j != PH_G) st_pairs(sh.xr[j == PH_F ? 0 : 1], v, lane);
-                    const u32 kg = kb0 + (j == PH_C ? OFF_B + 32 : j == PH_F ? OFF_E + 8 : j == PH_G ? OFF_F + 17 : OFF_G + 8);
+                    const u32 kg = j == PH_C ? AT_B + 32 : j == PH_F ? AT_E + 8 : j == PH_G ? AT_F + 17 : AT_G + 8;
                     ln_ring(v, sh, kg, kg + 4, eps, lane);
                     if (j == PH_G) {
 #pragma unroll
@@ -562,9 +576,9 @@ __device__ __forceinline__ void handoff_loop(const NkChainArgs &a, Shared &sh, c
 
 typedef __attribute__((address_space(4))) const NkChainLayer const_layer_t;
 
-/* Segment p of the stream (block p / 9, phase p % 9) into the ring: its KB blocks go to ring
- * blocks (l * BLOCK_KB + OFF_j + i) mod RING, one direct-to-LDS load of 16 bytes per lane each;
- * the count of loads per segment is fixed (SEG_j; none for D outside the attention workgroups). */
+/* Segment p of the stream (block p / 9, phase j = p % 9) into the weight area: its KB blocks go
+ * to blocks AT_j + i, one direct-to-LDS load of 16 bytes per lane each; the count of loads per
+ * segment is fixed (SEG_j; none for D outside the attention workgroups). */
 struct Stream {
     const_layer_t *Lt; /* constant address space: the pointers are read with scalar loads, which
                         * do not count in vmcnt (a vector load would need a vmcnt(0) wait, i.e. for
@@ -577,7 +591,7 @@ struct Stream {
     bool attn;
     __device__ void put(u32 kb, const void *src) const {
         wait_vm_lgkm<STREAM_INFLIGHT - 1>();
-        dma16(src, ring + (kb % RING) * 1024);
+        dma16(src, ring + kb * 1024);
     }
     /* n rows of nb blocks from src, rows row_bytes apart: block q of row r is bytes
      * [1024 q, 1024 q + 1024) of that row (16 bytes per lane) */
@@ -592,16 +606,16 @@ struct Stream {
     __device__ void rows(u32 kb, const u16 *W, u32 r0, u32 n, u32 K) const { blocks(kb, W + (u64)r0 * K, 2ull * K, n, K / 512); }
     __device__ void vec(u32 kb, const float *p) const { blocks(kb, p, 0, 1, D / 256); }
     __device__ void seg(u32 p) const {
-        const u32 l = p / NK_CHAIN_PH, j = p % NK_CHAIN_PH, kb = l * BLOCK_KB;
+        const u32 l = p / NK_CHAIN_PH, j = p % NK_CHAIN_PH;
         const_layer_t &W = Lt[l];
         if (j == PH_A) {
-            rows(kb + OFF_A, W.ff1_w1, 16 * g, 16, D);
+            rows(AT_A, W.ff1_w1, 16 * g, 16, D);
         } else if (j == PH_B) {
-            rows(kb + OFF_B, W.ff1_w2, 4 * g, 4, FF);
-            vec(kb + OFF_B + 32, W.ln_att_g);
-            vec(kb + OFF_B + 36, W.ln_att_b);
+            rows(AT_B, W.ff1_w2, 4 * g, 4, FF);
+            vec(AT_B + 32, W.ln_att_g);
+            vec(AT_B + 36, W.ln_att_b);
         } else if (j == PH_C) {
-            rows(kb + OFF_C, W.wqkv, 12 * g, 12, D);
+            rows(AT_C, W.wqkv, 12 * g, 12, D);
         } else if (j == PH_D) {
             if (attn) {
                 /* K, V rows of the quarter's cached window rows, P rows of all its rows (two rows
@@ -613,44 +627,44 @@ struct Stream {
                     const u32 jr = qt.j0 + 2 * b + half;
                     const u32 kvrow = cl > 0 ? pos - cl + min(jr, cl - 1) : pos;
                     const float *src = kvl + (u64)kvrow * QKV + head * DH + c4;
-                    put(kb + OFF_D + b, src + D);
-                    put(kb + OFF_D + 8 + b, src + 2 * D);
-                    put(kb + OFF_D + 16 + b, W.ptab + (u64)(Lmax - L + min(jr, L - 1)) * D + head * DH + c4);
+                    put(AT_D + b, src + D);
+                    put(AT_D + 8 + b, src + 2 * D);
+                    put(AT_D + 16 + b, W.ptab + (u64)(Lmax - L + min(jr, L - 1)) * D + head * DH + c4);
                 }
                 /* u for lanes 0-31, v for 32-63, as an offset from u: a per-lane choice of which
                  * table entry to read would make the read a vector load (and a vmcnt(0) wait) */
                 const u64 bu = (u64)W.bias_u, dv = (u64)W.bias_v - bu;
-                put(kb + OFF_D + 24, (const float *)(bu + (half ? dv : 0)) + head * DH + c4);
+                put(AT_D + 24, (const float *)(bu + (half ? dv : 0)) + head * DH + c4);
             }
         } else if (j == PH_E) {
-            rows(kb + OFF_E, W.wo, 4 * g, 4, D);
-            vec(kb + OFF_E + 8, W.ln_conv_g);
-            vec(kb + OFF_E + 12, W.ln_conv_b);
+            rows(AT_E, W.wo, 4 * g, 4, D);
+            vec(AT_E + 8, W.ln_conv_g);
+            vec(AT_E + 12, W.ln_conv_b);
         } else if (j == PH_F) {
-            rows(kb + OFF_F, W.pw1, 4 * g, 4, D);
-            rows(kb + OFF_F + 8, W.pw1, D + 4 * g, 4, D);
+            rows(AT_F, W.pw1, 4 * g, 4, D);
+            rows(AT_F + 8, W.pw1, D + 4 * g, 4, D);
             /* lanes 0-8: the 36 taps of channels 4g .. 4g+3; lanes 9-16: their 8 history rows */
             const float *dinl = din + (u64)l * din_stride;
             const u32 t = lane - 9;
             const float *src = lane < 9    ? W.dw_w + 4 * g * NK_CONV_TAPS + 4 * lane
                                : lane < 17 ? dinl + (u64)(pos - (NK_CONV_TAPS - 1) + t) * D + 4 * g
                                            : W.dw_w + 4 * g * NK_CONV_TAPS;
-            put(kb + OFF_F + 16, src);
-            vec(kb + OFF_F + 17, W.bn_g);
-            vec(kb + OFF_F + 21, W.bn_b);
+            put(AT_F + 16, src);
+            vec(AT_F + 17, W.bn_g);
+            vec(AT_F + 21, W.bn_b);
         } else if (j == PH_G) {
-            rows(kb + OFF_G, W.pw2, 4 * g, 4, D);
-            vec(kb + OFF_G + 8, W.ln_ff2_g);
-            vec(kb + OFF_G + 12, W.ln_ff2_b);
+            rows(AT_G, W.pw2, 4 * g, 4, D);
+            vec(AT_G + 8, W.ln_ff2_g);
+            vec(AT_G + 12, W.ln_ff2_b);
         } else if (j == PH_H) {
-            rows(kb + OFF_H, W.ff2_w1, 16 * g, 16, D);
+            rows(AT_H, W.ff2_w1, 16 * g, 16, D);
         } else {
-            rows(kb + OFF_I, W.ff2_w2, 4 * g, 4, FF);
-            vec(kb + OFF_I + 32, W.ln_out_g);
-            vec(kb + OFF_I + 36, W.ln_out_b);
+            rows(AT_I, W.ff2_w2, 4 * g, 4, FF);
+            vec(AT_I + 32, W.ln_out_g);
+            vec(AT_I + 36, W.ln_out_b);
             const_layer_t &Wn = Lt[l + 1 < nl ? l + 1 : l];
-            vec(kb + OFF_I + 40, Wn.ln_ff1_g);
-            vec(kb + OFF_I + 44, Wn.ln_ff1_b);
+            vec(AT_I + 40, Wn.ln_ff1_g);
+            vec(AT_I + 44, Wn.ln_ff1_b);
         }
     }
 };
