@@ -90,7 +90,7 @@ static_assert(SEG_A >= STREAM_INFLIGHT && SEG_B >= STREAM_INFLIGHT && SEG_C >= S
 
 struct Shared {
     char ring[RING * 1024];
-    float big[FF + 2 * NATT]; /* inputs of B, E (with the quarters' max and sum), I */
+    float big[FF + 2 * NATT]; /* inputs of B, E (with the heads' merge weights), I */
     float sm[2][D];           /* inputs of A, C, F, H (sm[0]) and D, G (sm[1]) */
     float xr[2][D];           /* residual rows (alternating) */
     float knew[DH], vnew[DH]; /* attention: the chunk's own K and V of the head */
@@ -328,27 +328,14 @@ __device__ __forceinline__ floatx4 attend_part(Shared &sh, u32 kd, const float *
 }
 
 /* The lane's chunks (as ld_x<2>) of the attention output: each head's quarters combined,
- * att = sum_k (w_k / sum_k' w_k' l_k') o_k, w_k = exp(m_k - max m), quarters in order. */
+ * att = sum_k w_k o_k in quarter order, with the merge weights w_k = exp(m_k - max m) /
+ * sum_k' exp(m_k' - max m) l_k' that the hand-off wavefront left after the quarters' outputs. */
 __device__ __forceinline__ void ld_att(float (&x)[2][8], const Shared &sh, u32 lane) {
+    static_assert(NP == 4, "one floatx4 of merge weights per head");
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
         const u32 hh = (lane >> 4) + 4 * q, d0 = 8 * (lane & 15);
-        float m[NP], w[NP];
-        float mx = -INFINITY;
-#pragma unroll
-        for (int k = 0; k < (int)NP; ++k) {
-            m[k] = sh.big[ML + 2 * (hh * NP + k)];
-            mx = fmaxf(mx, m[k]);
-        }
-        float lsum = 0.0f;
-#pragma unroll
-        for (int k = 0; k < (int)NP; ++k) {
-            w[k] = expf(m[k] - mx);
-            lsum += w[k] * sh.big[ML + 2 * (hh * NP + k) + 1];
-        }
-        const float inv = 1.0f / lsum;
-#pragma unroll
-        for (int k = 0; k < (int)NP; ++k) w[k] *= inv;
+        const floatx4 w = *(const floatx4 *)(sh.big + ML + NP * hh);
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             float o = 0.0f;
@@ -509,9 +496,21 @@ __device__ __forceinline__ void handoff_loop(const NkChainArgs &a, Shared &sh, c
 #pragma unroll
                 for (int i = 0; i < 16; ++i) *(float2 *)(sh.big + 2 * (pl + 128 * i)) = v[i];
                 if (j == PH_E && w4) {
+                    /* lane g (and g + 32): quarter g's (max, sum); its weight in the merge of its
+                     * head (quarters 4h .. 4h + 3 in lanes 4h .. 4h + 3), in ld_att's order:
+                     * w = exp(m - max m) / ((e0 l0 + e1 l1) + e2 l2) + e3 l3 */
                     float2 u[1];
                     ok = ll_wait<1>(c, p, ML + 2 * (lane & 31), 0, u);
-                    if (ok && lane < 32) *(float2 *)(sh.big + ML + 2 * lane) = u[0];
+                    if (ok) {
+                        const float m = u[0].x;
+                        const float mx = fmaxf(fmaxf(fmaxf(fmaxf(-INFINITY, dpp_f<DPP_QUAD_0000>(m)), dpp_f<DPP_QUAD_1111>(m)),
+                                                     dpp_f<DPP_QUAD_2222>(m)),
+                                               dpp_f<DPP_QUAD_3333>(m));
+                        const float e = expf(m - mx), el = e * u[0].y;
+                        const float lsum = ((dpp_f<DPP_QUAD_0000>(el) + dpp_f<DPP_QUAD_1111>(el)) + dpp_f<DPP_QUAD_2222>(el)) +
+                                           dpp_f<DPP_QUAD_3333>(el);
+                        if (lane < 32) sh.big[ML + lane] = e * (1.0f / lsum);
+                    }
                 }
             }
         } else if (j == PH_D) {

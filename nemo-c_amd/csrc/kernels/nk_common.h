@@ -56,6 +56,10 @@ __device__ __forceinline__ float dpp_f(float v) {
 }
 #define DPP_QUAD_1032 0xB1 /* quad_perm(1,0,3,2) */
 #define DPP_QUAD_2301 0x4E /* quad_perm(2,3,0,1) */
+#define DPP_QUAD_0000 0x00 /* quad_perm(0,0,0,0): lane 0 of the quad to all four */
+#define DPP_QUAD_1111 0x55
+#define DPP_QUAD_2222 0xAA
+#define DPP_QUAD_3333 0xFF
 #define DPP_ROW_ROR4 0x124
 #define DPP_ROW_ROR8 0x128
 
