@@ -39,6 +39,11 @@ void nemoasr_debug_fuse(nemoasr_t *s, int on);
  * model shape and device allow it (nemoasr_debug_chain_usable); 0: the per-kernel sequence. */
 void nemoasr_debug_chain(nemoasr_t *s, int on);
 int nemoasr_debug_chain_usable(const nemoasr_t *s);
+/* Polls a hand-off of the chain may spend before the launch gives up (0: the default, 2^20, about
+ * half a second).  A launch that gives up ends every workgroup at its next barrier or wait and
+ * leaves the session in error ("encoder chain: hand-off N timed out"); a tiny bound forces that
+ * path (the failure-handling test).  Applies to the session's current latency. */
+void nemoasr_debug_chain_spin(nemoasr_t *s, unsigned spin_max);
 /* Round trips of the decoder since open/reset, and GPU time of the encoder chunks (ms). */
 size_t nemoasr_debug_joint_steps(const nemoasr_t *s);
 double nemoasr_debug_encoder_gpu_ms(const nemoasr_t *s);

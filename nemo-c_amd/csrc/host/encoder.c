@@ -22,6 +22,7 @@
 
 #define MEL_CACHE 16 /* src/encoder.c:10 */
 #define MAX_GRAPHS 8
+#define CHAIN_SPIN_DEFAULT (1u << 20) /* polls before a chain hand-off gives up: about half a second */
 
 static double now_ms(void) {
     struct timespec ts;
@@ -59,6 +60,7 @@ struct encoder {
     int fuse; /* single-stream launch fusions (kernels/nk_fuse.hip) */
     /* one-row chunks: all blocks in one persistent launch (kernels/nk_chain.hip) */
     int chain, chain_ok;
+    uint32_t chain_spin; /* 0: CHAIN_SPIN_DEFAULT */
     gpu_buf_t *ch_layers, *ch_ll, *ch_abort;
     int *ch_err;        /* pinned host word the chain reports a time-out in */
     unsigned epoch;     /* per-chunk tag base of the chain's hand-offs */
@@ -125,7 +127,7 @@ static void run_chain(encoder_t *e, const float *x_in, float *x_out) {
     a.din_stride = e->din_stride;
     a.n_layers = (uint32_t)c->n_layers;
     a.Lmax = (uint32_t)e->Lmax;
-    a.spin_max = 1u << 20;
+    a.spin_max = e->chain_spin ? e->chain_spin : CHAIN_SPIN_DEFAULT;
     a.eps = c->ln_eps;
     a.scale = 1.0f / sqrtf((float)c->head_dim);
     const double D = NK_CHAIN_D, FF = NK_CHAIN_FF;
@@ -247,6 +249,10 @@ void encoder_chain(encoder_t *e, int on) {
     e->chain = on != 0;
 }
 int encoder_chain_usable(const encoder_t *e) { return e->chain_ok; }
+void encoder_chain_spin(encoder_t *e, uint32_t spin_max) {
+    if (e->chain_spin != spin_max) drop_graphs(e); /* captured launches hold the old bound */
+    e->chain_spin = spin_max;
+}
 
 int encoder_check(encoder_t *e, char *err, size_t errlen) {
     if (e->ch_err && *(volatile int *)e->ch_err) {

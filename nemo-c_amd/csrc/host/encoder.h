@@ -41,6 +41,8 @@ void encoder_fuse(encoder_t *e, int on);
  * with at least 256 compute units. */
 void encoder_chain(encoder_t *e, int on);
 int encoder_chain_usable(const encoder_t *e);
+/* Polls a chain hand-off may spend before it gives up (0: the default, 2^20, about half a second). */
+void encoder_chain_spin(encoder_t *e, uint32_t spin_max);
 /* -1 with err set when a chain launch reported a time-out (checked after the stream has synced). */
 int encoder_check(encoder_t *e, char *err, size_t errlen);
 /* Keep per-layer block outputs of every chunk (test hook). */

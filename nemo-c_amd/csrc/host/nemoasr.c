@@ -457,6 +457,7 @@ void nemoasr_debug_chain(nemoasr_t *s, int on) {
     encoder_chain(s->enc, s->chain && encoder_chain_usable(s->enc));
 }
 int nemoasr_debug_chain_usable(const nemoasr_t *s) { return encoder_chain_usable(s->enc); }
+void nemoasr_debug_chain_spin(nemoasr_t *s, unsigned spin_max) { encoder_chain_spin(s->enc, spin_max); }
 size_t nemoasr_debug_joint_steps(const nemoasr_t *s) { return s->rec.joint_steps; }
 double nemoasr_debug_encoder_gpu_ms(const nemoasr_t *s) { return s->rec.enc_gpu_ms; }
 const double *nemoasr_debug_chunk_ms(const nemoasr_t *s, size_t *n) {

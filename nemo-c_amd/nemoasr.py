@@ -73,6 +73,7 @@ API = {
     "nemoasr_debug_chain": (None, [_vp, C.c_int]),
     "nemoasr_debug_default_graphs": (None, [C.c_int]),
     "nemoasr_debug_chain_usable": (C.c_int, [_vp]),
+    "nemoasr_debug_chain_spin": (None, [_vp, C.c_uint]),
     "nemoasr_debug_joint_steps": (C.c_size_t, [_vp]),
     "nemoasr_debug_encoder_gpu_ms": (C.c_double, [_vp]),
     "nemoasr_debug_chunk_ms": (C.POINTER(C.c_double), [_vp, C.POINTER(C.c_size_t)]),
@@ -366,6 +367,10 @@ class Session:
 
     def chain_usable(self) -> bool:
         return bool(lib().nemoasr_debug_chain_usable(self.h))
+
+    def chain_spin(self, spin_max: int):
+        """Polls a chain hand-off may spend before the launch gives up (0: the default)."""
+        lib().nemoasr_debug_chain_spin(self.h, int(spin_max))
 
     def dumps(self, n_layers: int, d_model: int, joint_hidden: int):
         F = lib().nemoasr_debug_frames(self.h)

@@ -121,3 +121,29 @@ def test_chain_repeatable():
         res.append(s.dumps(d.n_layers, d.d_model, d.joint_hidden)[0].copy())
         s.close()
     assert np.array_equal(res[0], res[1])
+
+
+def test_chain_timeout_is_an_error():
+    """The failure path of the chain's bounded waits, forced from the host: with a hand-off bound
+    of one poll the first launch gives up (every workgroup leaves at its next barrier or wait, no
+    wait is unbounded) and the session reports the time-out as an error; a session opened after
+    it computes the same block outputs as one that never timed out."""
+    import nemoasr
+
+    mdir = model_dir("full")
+    om = oracle.Model(mdir, "en-US")
+    d = om.dims
+    mel = mel_ref.logmel(synth.make_audio(1.0, seed=13))
+    s = nemoasr.Session(mdir, "en-US", 80)
+    s.chain(True)
+    s.use_graphs(False)
+    s.chain_spin(1)
+    with pytest.raises(RuntimeError, match="encoder chain: hand-off [0-9]+ timed out"):
+        s.feed_mel(mel, final=True)
+    s.close()
+    outs = []
+    for _ in range(2):
+        t, _ = run_session(mdir, mel, chain=True)
+        outs.append(t.dumps(d.n_layers, d.d_model, d.joint_hidden)[0].copy())
+        t.close()
+    assert np.array_equal(outs[0], outs[1])
