@@ -53,7 +53,7 @@
  *     wavefront and store the outputs as hand-off entries;
  *   - wavefront 4 waits for the next phase's input while they compute, applies that phase's
  *     LayerNorm (the whole row: every workgroup normalises it itself) with parameters from the
- *     ring, keeps the residual row and writes the input row to LDS for the next barrier;
+ *     weight area, keeps the residual row and writes the input row to LDS for the next barrier;
  *   - wavefront 5 shares the waits of the 4096-wide rows;
  *   - wavefront 6 streams the weights. */
 #include "nk_common.h"
@@ -89,7 +89,7 @@ static_assert(SEG_A >= STREAM_INFLIGHT && SEG_B >= STREAM_INFLIGHT && SEG_C >= S
               "a nonempty segment holds more loads than are in flight");
 
 struct Shared {
-    char ring[RING * 1024];
+    char ring[RING * 1024]; /* the weight area: each kind of phase's segment at its fixed place */
     float big[FF + 2 * NATT]; /* inputs of B, E (with the heads' merge weights), I */
     float sm[2][D];           /* inputs of A, C, F, H (sm[0]) and D, G (sm[1]) */
     float xr[2][D];           /* residual rows (alternating) */
@@ -201,7 +201,7 @@ __device__ __forceinline__ void ln_pairs(float2 (&v)[8], const float2 (&g)[8], c
     }
 }
 
-/* LayerNorm with its parameters in the ring: gamma in the 4 blocks from kg, beta from kb */
+/* LayerNorm with its parameters in the weight area: gamma in the 4 blocks from kg, beta from kb */
 __device__ __forceinline__ void ln_ring(float2 (&v)[8], const Shared &sh, u32 kg, u32 kb, float eps, u32 lane) {
     float2 g[8], b[8];
 #pragma unroll
@@ -229,7 +229,7 @@ __device__ __forceinline__ void ld_x(float (&x)[KCH][8], const float *row, u32 l
     }
 }
 
-/* dot product of the weight row in ring blocks kb .. kb + KCH - 1 with the row held in x, summed
+/* dot product of the weight row in blocks kb .. kb + KCH - 1 with the row held in x, summed
  * over the wavefront (uniform) */
 template <int KCH>
 __device__ __forceinline__ float dot_ring(const float (&x)[KCH][8], const Shared &sh, u32 kb, u32 lane) {
@@ -239,7 +239,7 @@ __device__ __forceinline__ float dot_ring(const float (&x)[KCH][8], const Shared
     return wsum(s);
 }
 
-/* dot products of NR weight rows of K = 1024 (ring blocks kb[k], kb[k] + 1) with the row in x,
+/* dot products of NR weight rows of K = 1024 (blocks kb[k], kb[k] + 1) with the row in x,
  * each summed over the wavefront (uniform): every LDS read first, then the sums side by side */
 template <int NR>
 __device__ __forceinline__ void dots_ring(float (&sums)[NR], const float (&x)[2][8], const Shared &sh, const u32 (&kb)[NR], u32 lane) {
@@ -261,7 +261,7 @@ __device__ __forceinline__ void dots_ring(float (&sums)[NR], const float (&x)[2]
  * P[Lmax - L + j]) * scale, m = max score, p_j = exp(score_j - m), l = sum p_j, o = sum p_j V_j
  * (unnormalised; the E phase combines the quarters).  256 threads: scores by thread quads (key
  * tid / 4, head dims 4 (tid % 4 + 4 t)), the exponentials on wavefront 0, the output by 8 key
- * groups of 32 threads summed in order.  K, V and P rows are in the ring segment at kd (K rows
+ * groups of 32 threads summed in order.  K, V and P rows are in the segment at block kd (K rows
  * 2 per block from kd, V from kd + 8, P from kd + 16, then u | v in kd + 24).  Four LDS barriers,
  * matched by the other wavefronts.  Returns o[4 tid .. 4 tid + 3] on threads tid < 32. */
 __device__ __forceinline__ floatx4 attend_part(Shared &sh, u32 kd, const float *q, u32 cl, u32 j0, u32 nk, float scale,
@@ -475,7 +475,7 @@ __device__ __forceinline__ void handoff_loop(const NkChainArgs &a, Shared &sh, c
     const bool has_new = qt.j0 + qt.nk == L && qt.nk > 0; /* this quarter holds the chunk's own row */
     const float eps = a.eps;
     const u32 pl = threadIdx.x - 4 * 64; /* 0 .. 127 over both wavefronts */
-    float2 f_g[8], f_b[8];               /* block 0's LN_ff1 (later blocks take it from the ring) */
+    float2 f_g[8], f_b[8];               /* block 0's LN_ff1 (later blocks take it from the weight area) */
     if (w4) {
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
