@@ -837,6 +837,8 @@ int nk_compact(gpu_t *g, float *base, uint64_t stride, uint32_t nbuf, uint32_t r
     if (!rows || !nbuf) return 0;
     if (src_row < dst_row + rows && dst_row < src_row + rows) return bad(g, "compact: overlapping rows");
     NkCompactArgs a = { base, stride, nbuf, rows, cols, src_row, dst_row, 0 };
+    if (cols % 4 == 0 && stride % 4 == 0 && (uintptr_t)base % 16 == 0)
+        return gpu_launch(g, "compact_rows4", &a, sizeof a, blocks_for((uint64_t)rows * cols / 4), nbuf, 1, 256, 1, 1);
     return gpu_launch(g, "compact_rows", &a, sizeof a, blocks_for((uint64_t)rows * cols), nbuf, 1, 256, 1, 1);
 }
 

@@ -23,6 +23,14 @@ __device__ __forceinline__ uint4 ld_c16(const u16 *p) {
     return make_uint4(v.x, v.y, v.z, v.w);
 }
 
+/* float4 i of an n-float4 array, or zeros for i >= n (n >= 1).  The load itself is unconditional
+ * (index clamped into the array) and only the result is selected: written as `i < n ? p[i] : 0`,
+ * the compiler splits the 16-byte load into four exec-masked 4-byte loads, each behind a branch. */
+__device__ __forceinline__ float4 ld4z(const float4 *p, u32 i, u32 n) {
+    const float4 v = p[min(i, n - 1)];
+    return i < n ? v : make_float4(0.f, 0.f, 0.f, 0.f);
+}
+
 /* bf16 bits -> f32: the upper half of the f32 pattern (exact). */
 __device__ __forceinline__ float bf2f(u32 bits16) { return __uint_as_float(bits16 << 16); }
 __device__ __forceinline__ float bf_lo(u32 pair) { return __uint_as_float(pair << 16); }

@@ -237,6 +237,14 @@ extern "C" __global__ __launch_bounds__(256) void compact_rows(const NkCompactAr
     float *b = a.base + (u64)blockIdx.y * a.stride;
     b[(u64)a.dst_row * a.cols + idx] = b[(u64)a.src_row * a.cols + idx];
 }
+/* The same copy 16 bytes per thread, when cols, the buffer stride and the base are multiples of 4
+ * floats (every cache of the model: rows of 1024 or 3072 floats).  grid = (ceil(rows*cols/1024), nbuf). */
+extern "C" __global__ __launch_bounds__(256) void compact_rows4(const NkCompactArgs a) {
+    const u64 idx = (u64)blockIdx.x * 256 + threadIdx.x, n4 = (u64)a.rows * a.cols / 4;
+    if (idx >= n4) return;
+    float4 *b = (float4 *)(a.base + (u64)blockIdx.y * a.stride);
+    b[(u64)a.dst_row * (a.cols / 4) + idx] = b[(u64)a.src_row * (a.cols / 4) + idx];
+}
 
 /* Strided row copy: rows x cols floats from src (row stride src_ld) to dst (row stride dst_ld).
  * Used for the row select of the subsampled window and for activation dumps. */

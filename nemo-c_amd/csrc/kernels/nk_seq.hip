@@ -16,6 +16,9 @@ __device__ __forceinline__ float block_sum256(float v, float *red) {
 }
 
 #define LN_VEC 4 /* float4 per thread: D <= 4096 */
+#ifndef LN_PARTS_AHEAD
+#define LN_PARTS_AHEAD 4 /* pending parts whose loads layernorm_rows issues together */
+#endif
 
 /* LayerNorm of a row held as float4s (reference src/kernels.metal:257-288):
  * mean = sum/D, var = sum((x-mean)^2)/D, inv = 1/sqrt(var + eps), y = (x-mean)*inv*g + b. */
@@ -55,12 +58,11 @@ extern "C" __global__ __launch_bounds__(256) void layernorm(const NkLnArgs a) {
 #pragma unroll
     for (int k = 0; k < LN_VEC; ++k) {
         const u32 i = tid + k * 256;
-        const bool ok = i < D4;
-        v[k] = ok ? x[i] : z;
-        g1[k] = ok ? ((const float4 *)a.g1)[i] : z;
-        b1[k] = ok ? ((const float4 *)a.b1)[i] : z;
-        g2[k] = ok && a.Y2 ? ((const float4 *)a.g2)[i] : z;
-        b2[k] = ok && a.Y2 ? ((const float4 *)a.b2)[i] : z;
+        v[k] = ld4z(x, i, D4);
+        g1[k] = ld4z((const float4 *)a.g1, i, D4);
+        b1[k] = ld4z((const float4 *)a.b1, i, D4);
+        g2[k] = a.Y2 ? ld4z((const float4 *)a.g2, i, D4) : z;
+        b2[k] = a.Y2 ? ld4z((const float4 *)a.b2, i, D4) : z;
     }
     ln_vec(v, g1, b1, D4, a.D, a.eps, red);
     float4 *y1 = (float4 *)(a.Y1 + (u64)row * a.D);
@@ -104,35 +106,61 @@ __device__ __forceinline__ void ln_row64(float4 (&v)[4], const float4 (&g)[4], c
 /* R consecutive rows per wavefront: the rows' loads are issued together and the LayerNorm
  * parameters are loaded once for all R (measured at 3550 rows x 1024: 15.9 / 11.5 / 10.4 us for
  * R = 1 / 2 / 4, and 23.4 / 17.3 / 15.2 us for the pair; at 448 rows R = 1 is fastest).  Each
- * row's arithmetic is ln_row64's, so every R gives the same bits. */
-template <int R>
+ * row's arithmetic is ln_row64's, so every R gives the same bits.
+ * FULL: D = 1024, every lane holds four float4s of the row, so no load or store needs a per-lane
+ * guard (a guarded 16-byte load costs a branch, and a guarded use lets the compiler move the load
+ * behind that branch, after the previous loads have been waited for).
+ * A pending update's first LN_PARTS_AHEAD parts are loaded before any of them is summed (one
+ * memory round trip instead of one per part): part min(b, nparts - 1) is loaded for every b, and
+ * the parts past nparts add +0, which leaves the sum's bits unchanged (the running sum starts at
+ * +0 and, as a sum of at least two terms one of which is +0, is never -0). */
+template <int R, bool FULL>
 __device__ __forceinline__ void layernorm_rows_impl(const NkLnArgs &a) {
-    const u32 lane = threadIdx.x & 63, D4 = a.D >> 2;
+    const u32 lane = threadIdx.x & 63, D4 = FULL ? 256 : a.D >> 2;
     const u32 r0 = (blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6)) * R;
     if (r0 >= a.M) return; /* uniform per wavefront; no barriers */
     float4 v[R][4], g1[4], b1[4], g2[4], b2[4];
     const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+    auto ld = [&](const float4 *p, u32 i) { return FULL ? p[i] : ld4z(p, i, D4); };
+    auto in_row = [&](u32 i) { return FULL || i < D4; };
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         const float4 *x = (const float4 *)(a.X + (u64)min(r0 + r, a.M - 1) * a.D);
 #pragma unroll
-        for (int k = 0; k < 4; ++k) v[r][k] = lane + 64 * k < D4 ? x[lane + 64 * k] : z;
+        for (int k = 0; k < 4; ++k) v[r][k] = ld(x, lane + 64 * k);
     }
     if (a.P) {
         /* pending residual update: x + palpha * (((0 + p0) + p1) + ...), written back to X (this
-         * wavefront owns its rows) */
+         * wavefront owns its rows); the host sets P only with nparts >= 1 */
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             const u32 row = min(r0 + r, a.M - 1);
             float4 t[4] = { z, z, z, z };
-            for (u32 b = 0; b < a.nparts; ++b) {
+            float4 q[LN_PARTS_AHEAD][4];
+#pragma unroll
+            for (u32 b = 0; b < LN_PARTS_AHEAD; ++b) {
+                const float4 *p = (const float4 *)(a.P + ((u64)min(b, a.nparts - 1) * a.M + row) * a.D);
+#pragma unroll
+                for (int k = 0; k < 4; ++k) q[b][k] = ld(p, lane + 64 * k);
+            }
+#pragma unroll
+            for (u32 b = 0; b < LN_PARTS_AHEAD; ++b) {
+                const bool use = b < a.nparts;
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    t[k].x += use ? q[b][k].x : 0.0f;
+                    t[k].y += use ? q[b][k].y : 0.0f;
+                    t[k].z += use ? q[b][k].z : 0.0f;
+                    t[k].w += use ? q[b][k].w : 0.0f;
+                }
+            }
+            for (u32 b = LN_PARTS_AHEAD; b < a.nparts; ++b) {
                 const float4 *p = (const float4 *)(a.P + ((u64)b * a.M + row) * a.D);
 #pragma unroll
-                for (int k = 0; k < 4; ++k)
-                    if (lane + 64 * k < D4) {
-                        const float4 q = p[lane + 64 * k];
-                        t[k].x += q.x; t[k].y += q.y; t[k].z += q.z; t[k].w += q.w;
-                    }
+                for (int k = 0; k < 4; ++k) {
+                    const float4 w = ld(p, lane + 64 * k);
+                    t[k].x += w.x; t[k].y += w.y; t[k].z += w.z; t[k].w += w.w;
+                }
             }
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
@@ -145,18 +173,17 @@ __device__ __forceinline__ void layernorm_rows_impl(const NkLnArgs &a) {
                 float4 *x = (float4 *)(a.X + (u64)row * a.D);
 #pragma unroll
                 for (int k = 0; k < 4; ++k)
-                    if (lane + 64 * k < D4) x[lane + 64 * k] = v[r][k];
+                    if (in_row(lane + 64 * k)) x[lane + 64 * k] = v[r][k];
             }
         }
     }
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
         const u32 i = lane + 64 * k;
-        const bool ok = i < D4;
-        g1[k] = ok ? ((const float4 *)a.g1)[i] : z;
-        b1[k] = ok ? ((const float4 *)a.b1)[i] : z;
-        g2[k] = ok && a.Y2 ? ((const float4 *)a.g2)[i] : z;
-        b2[k] = ok && a.Y2 ? ((const float4 *)a.b2)[i] : z;
+        g1[k] = ld((const float4 *)a.g1, i);
+        b1[k] = ld((const float4 *)a.b1, i);
+        g2[k] = a.Y2 ? ld((const float4 *)a.g2, i) : z;
+        b2[k] = a.Y2 ? ld((const float4 *)a.b2, i) : z;
     }
 #pragma unroll
     for (int r = 0; r < R; ++r) {
@@ -167,30 +194,34 @@ __device__ __forceinline__ void layernorm_rows_impl(const NkLnArgs &a) {
         if (!a.Y2 && ys) {
 #pragma unroll
             for (int k = 0; k < 4; ++k)
-                if (lane + 64 * k < D4) store_split4(ys, a.D, 4 * (lane + 64 * k), v[r][k]);
+                if (in_row(lane + 64 * k)) store_split4(ys, a.D, 4 * (lane + 64 * k), v[r][k]);
             continue;
         }
         float4 *y1 = (float4 *)(a.Y1 + (u64)row * a.D);
 #pragma unroll
         for (int k = 0; k < 4; ++k)
-            if (lane + 64 * k < D4) y1[lane + 64 * k] = v[r][k];
+            if (in_row(lane + 64 * k)) y1[lane + 64 * k] = v[r][k];
         if (!a.Y2) continue;
         ln_row64(v[r], g2, b2, lane, D4, a.D, a.eps);
         if (ys) {
 #pragma unroll
             for (int k = 0; k < 4; ++k)
-                if (lane + 64 * k < D4) store_split4(ys, a.D, 4 * (lane + 64 * k), v[r][k]);
+                if (in_row(lane + 64 * k)) store_split4(ys, a.D, 4 * (lane + 64 * k), v[r][k]);
             continue;
         }
         float4 *y2 = (float4 *)(a.Y2 + (u64)row * a.D);
 #pragma unroll
         for (int k = 0; k < 4; ++k)
-            if (lane + 64 * k < D4) y2[lane + 64 * k] = v[r][k];
+            if (in_row(lane + 64 * k)) y2[lane + 64 * k] = v[r][k];
     }
 }
-extern "C" __global__ __launch_bounds__(256) void layernorm_rows(const NkLnArgs a) { layernorm_rows_impl<1>(a); }
-extern "C" __global__ __launch_bounds__(256) void layernorm_rows_r2(const NkLnArgs a) { layernorm_rows_impl<2>(a); }
-extern "C" __global__ __launch_bounds__(256) void layernorm_rows_r4(const NkLnArgs a) { layernorm_rows_impl<4>(a); }
+template <int R> __device__ __forceinline__ void layernorm_rows_any(const NkLnArgs &a) {
+    if (a.D == 1024) layernorm_rows_impl<R, true>(a);
+    else layernorm_rows_impl<R, false>(a);
+}
+extern "C" __global__ __launch_bounds__(256) void layernorm_rows(const NkLnArgs a) { layernorm_rows_any<1>(a); }
+extern "C" __global__ __launch_bounds__(256) void layernorm_rows_r2(const NkLnArgs a) { layernorm_rows_any<2>(a); }
+extern "C" __global__ __launch_bounds__(256) void layernorm_rows_r4(const NkLnArgs a) { layernorm_rows_any<4>(a); }
 
 /* Relative-position attention of one (head h, query row orow) on a workgroup of 512 threads:
  * reference src/kernels.metal:290-348.

@@ -693,11 +693,12 @@ def test_joint_argmax_tie_lowest_index(gpu, device_loop):
     assert joint_argmax_rows(gpu, enc, pred, W, bias, device_loop)[0][0] == 17
 
 
-def test_compact_rows(gpu):
+@pytest.mark.parametrize("cols", [96, 97])  # 16-byte rows (compact_rows4) and the 4-byte fallback
+def test_compact_rows(gpu, cols):
     import nemoasr
 
     lib = nemoasr.lib()
-    nbuf, rows_total, cols = 3, 40, 96
+    nbuf, rows_total = 3, 40
     rng = np.random.default_rng(3)
     X = rng.standard_normal((nbuf, rows_total, cols)).astype(np.float32)
     d = gpu.put(X)
