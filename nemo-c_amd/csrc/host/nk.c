@@ -524,7 +524,7 @@ static int launch_ln_rows(gpu_t *g, const NkLnArgs *a, uint32_t M) {
 int nk_layernorm2(gpu_t *g, const float *X, const float *g1, const float *b1, const float *g2, const float *b2,
                   float *Y1, float *Y2, uint32_t M, uint32_t D, float eps) {
     if (!M) return 0;
-    if (D > NK_ROW_MAX || D % 4) return bad(g, "layernorm: D must be a multiple of 4, at most 4096");
+    if (!D || D > NK_ROW_MAX || D % 4) return bad(g, "layernorm: D must be a positive multiple of 4, at most 4096");
     NkLnArgs a = { X, g1, b1, g2, b2, Y1, Y2, M, D, eps, 0, NULL, NULL, 0, 0.0f };
     /* many rows: a wavefront per row (D <= 1024), no barriers; 2 or 4 rows per wavefront from
      * 1024 / 2048 rows */
@@ -537,8 +537,8 @@ int nk_layernorm2(gpu_t *g, const float *X, const float *g1, const float *b1, co
 int nk_layernorm2_split(gpu_t *g, float *X, const nk_resid_t *pend, const float *g1, const float *b1, const float *g2,
                         const float *b2, float *Y1, uint16_t *Ys, uint32_t M, uint32_t D, float eps) {
     if (!M) return 0;
-    if (D > 1024 || D % 4 || !Ys || (uintptr_t)Ys % 8 || (g2 && !Y1))
-        return bad(g, "layernorm_split: D a multiple of 4, at most 1024, a split output (and Y1 when paired)");
+    if (!D || D > 1024 || D % 4 || !Ys || (uintptr_t)Ys % 8 || (g2 && !Y1))
+        return bad(g, "layernorm_split: D a positive multiple of 4, at most 1024, a split output (and Y1 when paired)");
     NkLnArgs a = { X, g1, b1, g2, b2, g2 ? Y1 : NULL, NULL, M, D, eps, 0, Ys, NULL, 0, 0.0f };
     if (g2) a.Y2 = Y1; /* any non-NULL Y2 selects the pair; its rows go to Ys */
     if (pend && pend->nparts) {

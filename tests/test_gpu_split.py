@@ -136,6 +136,21 @@ def test_layernorm_split_bits(gpu, M, paired):
     assert rel_err(y, ref) < 1e-5
 
 
+def test_layernorm_zero_width_is_an_error(gpu):
+    """Rows of zero floats are refused before any launch (the row kernels clamp their loads into the
+    row, which needs at least one float4)."""
+    import nemoasr
+
+    L = nemoasr.lib()
+    dX, dg, dYs = gpu.alloc(4096), gpu.alloc(4096), gpu.alloc(4096)
+    for call in (lambda: L.nk_layernorm2_split(gpu.h, dX.ptr, None, dg.ptr, dg.ptr, None, None, None, dYs.ptr, 4, 0, 1e-5),
+                 lambda: L.nk_layernorm2(gpu.h, dX.ptr, dg.ptr, dg.ptr, None, None, dYs.ptr, None, 4, 0, 1e-5)):
+        gpu.begin()
+        assert call() != 0
+        with pytest.raises(RuntimeError, match="layernorm"):
+            gpu.end()
+
+
 def test_attention_chunks_split_bits(gpu):
     import nemoasr
 
@@ -191,9 +206,11 @@ def test_dwconv_rows_split_bits(gpu):
     assert rel_err(y, ref) < 1e-5
 
 
-@pytest.mark.parametrize("M,K,split_in,paired", [(448, 4096, True, True), (448, 1024, True, False), (3584, 4096, False, True),
-                                                 (301, 1024, False, False)])
-def test_resid_pending_folded_by_layernorm(gpu, M, K, split_in, paired):
+@pytest.mark.parametrize("M,K,split_in,paired,D", [(448, 4096, True, True, 1024), (448, 1024, True, False, 1024),
+                                                   (3584, 4096, False, True, 1024), (301, 1024, False, False, 1024),
+                                                   # 8 parts (past the four loaded ahead), and rows narrower than 1024
+                                                   (301, 8192, False, True, 1024), (130, 4096, True, True, 512)])
+def test_resid_pending_folded_by_layernorm(gpu, M, K, split_in, paired, D):
     """A residual update left pending (nk_gemm_resid: the K blocks' partial rows, K split or not) and
     applied by the LayerNorm that follows gives the residual and LayerNorm output of the update done
     by nk_gemm_split then the plain LayerNorm, bit for bit."""
@@ -202,7 +219,6 @@ def test_resid_pending_folded_by_layernorm(gpu, M, K, split_in, paired):
     import nemoasr
 
     L = nemoasr.lib()
-    D = 1024
     rng = np.random.default_rng([M, K, 4])
     A = rng.standard_normal((M, K)).astype(np.float32)
     W = w_bf16(rng, D, K)
