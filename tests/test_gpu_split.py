@@ -179,31 +179,37 @@ def test_attention_chunks_split_bits(gpu):
     assert np.array_equal(dOs.read((m, 2 * D), np.uint16), split_rows(dO.read((m, D))))
 
 
-def test_dwconv_rows_split_bits(gpu):
+@pytest.mark.parametrize("M,D", [(40, 1024), (3585, 1024), (2050, 512)])
+def test_dwconv_rows_split_bits(gpu, M, D):
     import nemoasr
 
     lib = nemoasr.lib()
-    D, taps, M = 1024, 9, 40
+    taps = 9
     rng = np.random.default_rng(12)
-    din = rng.standard_normal((200, D)).astype(np.float32)
+    din = rng.standard_normal((4000, D)).astype(np.float32)
     W = (rng.standard_normal((D, taps)) / 3).astype(np.float32)
     g = (1 + 0.1 * rng.standard_normal(D)).astype(np.float32)
     b = (0.1 * rng.standard_normal(D)).astype(np.float32)
+    pos = [10 + 4 * i for i in range(40)] + list(8 + rng.integers(0, 3990, M - 40))
     rows = []
-    for i in range(M):
-        rows += [10 + 4 * i, 0, 1, 0]
+    for p in pos:
+        rows += [int(p), 0, 1, 0]
     ddin, dW, dg, db = gpu.put(din), gpu.put(W), gpu.put(g), gpu.put(b)
     drows = gpu.put(np.asarray(rows, np.int32))
-    dY, dYs = gpu.alloc(M * D * 4), gpu.alloc(M * D * 4)
+    dY, dYs, dY40 = gpu.alloc(M * D * 4), gpu.alloc(M * D * 4), gpu.alloc(40 * D * 4)
     gpu.begin()
     gpu.check(lib.nk_dwconv_ln_silu_rows(gpu.h, ddin.ptr, drows.ptr, M, dW.ptr, dg.ptr, db.ptr, dY.ptr, D, taps, 1e-5))
     gpu.check(lib.nk_dwconv_ln_silu_rows_split(gpu.h, ddin.ptr, drows.ptr, M, dW.ptr, dg.ptr, db.ptr, None, dYs.ptr, D,
                                                taps, 1e-5))
+    gpu.check(lib.nk_dwconv_ln_silu_rows(gpu.h, ddin.ptr, drows.ptr, 40, dW.ptr, dg.ptr, db.ptr, dY40.ptr, D, taps, 1e-5))
     gpu.end()
     y = dY.read((M, D))
     assert np.array_equal(dYs.read((M, 2 * D), np.uint16), split_rows(y))
-    ref = np.concatenate([oracle.dwconv_ln_silu(din[10 + 4 * i - 8:10 + 4 * i + 1], W, g, b, 1) for i in range(M)])
-    assert rel_err(y, ref) < 1e-5
+    # the same row gives the same bits at any row count
+    assert np.array_equal(bits(y[:40]), bits(dY40.read((40, D))))
+    pick = list(range(40)) + list(range(40, M, max(1, M // 200))) + [M - 1]
+    ref = np.concatenate([oracle.dwconv_ln_silu(din[pos[i] - 8:pos[i] + 1], W, g, b, 1) for i in pick])
+    assert rel_err(y[pick], ref) < 1e-5
 
 
 @pytest.mark.parametrize("M,K,split_in,paired,D", [(448, 4096, True, True, 1024), (448, 1024, True, False, 1024),
