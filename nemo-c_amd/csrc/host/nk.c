@@ -511,14 +511,10 @@ int nk_gemm_ln_pend(gpu_t *g, const float *A, uint32_t lda, const uint16_t *W, u
     return gemm_core(g, A, lda, W, ldw, bias, C, ldc, crow, M, N, K, act, accumulate, alpha, &ln);
 }
 
-/* The many-row LayerNorm: a wavefront per row, or per 2 / 4 consecutive rows from 1024 / 2048 rows;
- * below 1024 rows one wavefront per workgroup, so the rows spread over every CU instead of filling
- * a quarter of them four wavefronts deep.  Every form gives the same bits. */
+/* The many-row LayerNorm: one wavefront per row and per workgroup, so the rows spread over every
+ * CU. */
 static int launch_ln_rows(gpu_t *g, const NkLnArgs *a, uint32_t M) {
-    const uint32_t R = M >= 2048 ? 4 : M >= 1024 ? 2 : 1, W = (M + R - 1) / R;
-    const char *name = R == 4 ? "layernorm_rows_r4" : R == 2 ? "layernorm_rows_r2" : "layernorm_rows";
-    if (R == 1) return gpu_launch(g, name, a, sizeof *a, W, 1, 1, 64, 1, 1);
-    return gpu_launch(g, name, a, sizeof *a, (W + 3) / 4, 1, 1, 256, 1, 1);
+    return gpu_launch(g, "layernorm_rows", a, sizeof *a, M, 1, 1, 64, 1, 1);
 }
 
 int nk_layernorm2(gpu_t *g, const float *X, const float *g1, const float *b1, const float *g2, const float *b2,
@@ -526,8 +522,7 @@ int nk_layernorm2(gpu_t *g, const float *X, const float *g1, const float *b1, co
     if (!M) return 0;
     if (!D || D > NK_ROW_MAX || D % 4) return bad(g, "layernorm: D must be a positive multiple of 4, at most 4096");
     NkLnArgs a = { X, g1, b1, g2, b2, Y1, Y2, M, D, eps, 0, NULL, NULL, 0, 0.0f };
-    /* many rows: a wavefront per row (D <= 1024), no barriers; 2 or 4 rows per wavefront from
-     * 1024 / 2048 rows */
+    /* many rows: a wavefront per row (D <= 1024), no barriers */
     if ((M > 16 || gpu_many_rows(g)) && D <= 1024) {
         return launch_ln_rows(g, &a, M);
     }

@@ -103,10 +103,12 @@ __device__ __forceinline__ void ln_row64(float4 (&v)[4], const float4 (&g)[4], c
     }
 }
 
-/* R consecutive rows per wavefront: the rows' loads are issued together and the LayerNorm
- * parameters are loaded once for all R (measured at 3550 rows x 1024: 15.9 / 11.5 / 10.4 us for
- * R = 1 / 2 / 4, and 23.4 / 17.3 / 15.2 us for the pair; at 448 rows R = 1 is fastest).  Each
- * row's arithmetic is ln_row64's, so every R gives the same bits.
+/* R consecutive rows per wavefront (the rows' loads issued together, the LayerNorm parameters
+ * loaded once for all R); each row's arithmetic is ln_row64's, so every R gives the same bits.
+ * Only R = 1 is launched: with the guarded per-lane loads of an earlier form, 2 and 4 rows per
+ * wavefront paid at thousands of rows, but with the full-width loads below one row per wavefront
+ * is fastest at every size (3584 rows x 1024, graph-replayed: 7.6 / 8.1 / 8.3 us for R = 1 / 2 / 4
+ * with no pending update, 12.6 / 13.5 / 15.6 with one part, 20.5 / 21.6 / 23.1 with four).
  * FULL: D = 1024, every lane holds four float4s of the row, so no load or store needs a per-lane
  * guard (a guarded 16-byte load costs a branch, and a guarded use lets the compiler move the load
  * behind that branch, after the previous loads have been waited for).
@@ -220,8 +222,6 @@ template <int R> __device__ __forceinline__ void layernorm_rows_any(const NkLnAr
     else layernorm_rows_impl<R, false>(a);
 }
 extern "C" __global__ __launch_bounds__(256) void layernorm_rows(const NkLnArgs a) { layernorm_rows_any<1>(a); }
-extern "C" __global__ __launch_bounds__(256) void layernorm_rows_r2(const NkLnArgs a) { layernorm_rows_any<2>(a); }
-extern "C" __global__ __launch_bounds__(256) void layernorm_rows_r4(const NkLnArgs a) { layernorm_rows_any<4>(a); }
 
 /* Relative-position attention of one (head h, query row orow) on a workgroup of 512 threads:
  * reference src/kernels.metal:290-348.
